@@ -1,0 +1,230 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized weight-math hot path on one MI355X.
+
+Headline (BASELINE.json metric): Q4_K decode GEMV, 4096 -> 14336, M = 1,
+f32 activations, GB/s and fraction of the 8 TB/s HBM roofline.  A "step" is
+one GEMV over one weight matrix; the matrix rotates through >= 1 GiB of
+distinct copies so every call streams from HBM rather than the 256 MB MALL.
+The same run reports the Q4_K prefill GEMM (M = 2048, Llama-3-8B FFN up and
+down) in TFLOP/s against the dense FP16 MFMA peak, and the scalar CPU oracle
+timed on this host's cores.  ``--all`` adds the other BASELINE configs.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+INT8_PEAK_TOPS = 5000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--all", action="store_true", help="also run the other BASELINE configs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="", help="comma list: gemv,gemm,head,layer,moe")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP events on the stream the kernels are launched on."""
+
+    def __init__(self, torch, stream):
+        self.t, self.s = torch, stream
+
+    def run(self, fn, iters, warmup):
+        for i in range(warmup):
+            fn(i)
+        self.t.cuda.synchronize()
+        e0 = self.t.cuda.Event(enable_timing=True)
+        e1 = self.t.cuda.Event(enable_timing=True)
+        e0.record(self.s)
+        for i in range(iters):
+            fn(i)
+        e1.record(self.s)
+        self.t.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters  # ms per call
+
+
+def rotation(torch, w_host, min_bytes=1 << 30):
+    base = torch.from_numpy(w_host).cuda()
+    n = max(2, -(-min_bytes // base.numel()))
+    return [base] + [base.clone() for _ in range(n - 1)]
+
+
+def bench_gemv(K, torch, be, timer, args, dt, n_out, n_in, seed, act_f16=False):
+    import numpy as np
+    w = K.quantize(dt, K.synth_normal(n_out * n_in, seed=seed, std=0.02), n_out, n_in, 16)
+    ws = rotation(torch, w)
+    x = K.synth_normal(n_in, seed=seed + 1)
+    xt = torch.from_numpy(x.astype(np.float16) if act_f16 else x).cuda()
+    out = torch.empty((1, n_out), dtype=torch.float16 if act_f16 else torch.float32,
+                      device="cuda")
+    ms = timer.run(lambda i: be.gemm(out, xt, ws[i % len(ws)], dt, n_out, n_in, 1),
+                   args.steps, args.warmup)
+    nbytes = K.row_bytes(dt, n_in) * n_out
+    act_bytes = (n_in + n_out) * (2 if act_f16 else 4)
+    return {"ms": ms, "weight_bytes": nbytes, "bytes": nbytes + act_bytes,
+            "GBps": (nbytes + act_bytes) / ms / 1e6, "copies": len(ws), "w": w, "x": x}
+
+
+def bench_gemm(K, torch, be, timer, dt, M, n_out, n_in, seed, iters=20, warmup=3):
+    import numpy as np
+    w = K.quantize(dt, K.synth_normal(n_out * n_in, seed=seed, std=0.02), n_out, n_in, 16)
+    wt = torch.from_numpy(w).cuda()
+    x = torch.from_numpy(K.synth_normal(M * n_in, seed=seed + 1).astype(np.float16)).cuda()
+    out = torch.empty((M, n_out), dtype=torch.float16, device="cuda")
+    ms = timer.run(lambda i: be.gemm(out, x, wt, dt, n_out, n_in, M), iters, warmup)
+    flops = 2.0 * M * n_out * n_in
+    return {"ms": ms, "TFLOPs": flops / ms / 1e9, "frac": flops / ms / 1e9 / FP16_PEAK_TFLOPS,
+            "M": M, "N": n_out, "K": n_in}
+
+
+def cpu_baseline(O, w, x, n_out, n_in, seconds):
+    """The strict scalar oracle (one f32 chain per output row, parallel over
+    rows) on this host's cores, on a bounded sample of the same GEMV."""
+    cores = min(16, os.cpu_count() or 1)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        O.gemm(O.Q4_K, w, x, n_out, nthreads=cores)
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt_all = (time.perf_counter() - t0) / reps
+    # one core: a 1/16 slice of the rows, scaled
+    rows1 = max(1, n_out // 16)
+    rb = O.row_bytes(O.Q4_K, n_in)
+    t1 = time.perf_counter()
+    O.gemm(O.Q4_K, w[:rows1 * rb], x, rows1, nthreads=1)
+    dt_one = (time.perf_counter() - t1) * n_out / rows1
+    nbytes = rb * n_out + (n_in + n_out) * 4
+    return {"value": nbytes / dt_all / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"Q4_K GEMV {n_in}->{n_out} M=1, {reps} calls over {dt_all * reps:.1f} s",
+            "one_core_GBps": nbytes / dt_one / 1e9}
+
+
+def read_traffic():
+    p = os.path.join(ROOT, "profiles", "q4k_gemv_4096x14336_traffic.txt")
+    if not os.path.exists(p):
+        return None
+    vals = {}
+    for line in open(p):
+        if ":" in line:
+            k, v = line.split(":", 1)
+            vals[k.strip()] = v.strip()
+    try:
+        return float(vals["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (no sharding, no collectives); "
+              "run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import kraken_amd as K
+
+    only = set(filter(None, args.only.split(",")))
+    want = (lambda k: k in only) if only else (lambda k: True)
+    stream = torch.cuda.current_stream()
+    be32 = K.Backend(0, K.ACT_F32, stream)
+    be16 = K.Backend(0, K.ACT_F16, stream)
+    timer = Timer(torch, stream)
+    extras = {}
+
+    # ---- headline: Q4_K GEMV 4096 -> 14336, M = 1 ---------------------------
+    log("gemv q4_k 4096->14336 ...")
+    n_out, n_in = 14336, 4096
+    g = bench_gemv(K, torch, be32, timer, args, K.Q4_K, n_out, n_in, seed=1)
+    log(f"  {g['ms'] * 1e3:.2f} us/call  {g['GBps']:.0f} GB/s  ({g['copies']} copies)")
+    # the same call with f16 activations (the reference GPU's activation type)
+    g16 = bench_gemv(K, torch, be16, timer, args, K.Q4_K, n_out, n_in, seed=1, act_f16=True)
+    extras["gemv_q4k_f16act"] = {"us": g16["ms"] * 1e3, "GBps": g16["GBps"]}
+
+    if want("gemm"):
+        for name, (N_, K_) in (("up", (14336, 4096)), ("down", (4096, 14336))):
+            for M in (512, 2048):
+                log(f"gemm q4_k {name} M={M} ...")
+                r = bench_gemm(K, torch, be16, timer, K.Q4_K, M, N_, K_, seed=10)
+                log(f"  {r['ms'] * 1e3:.1f} us  {r['TFLOPs']:.1f} TFLOP/s  ({100 * r['frac']:.1f}%)")
+                extras[f"prefill_q4k_{name}_m{M}"] = {"us": r["ms"] * 1e3, "TFLOPs": r["TFLOPs"],
+                                                      "frac_fp16_peak": r["frac"]}
+
+    if args.all or want("layer") and only:
+        # config 2: Llama-2-7B Q4_K decode layer, M = 1
+        tot_b, tot_ms = 0, 0.0
+        for nm, (o, i) in (("q", (4096, 4096)), ("k", (4096, 4096)), ("v", (4096, 4096)),
+                           ("o", (4096, 4096)), ("gate", (11008, 4096)), ("up", (11008, 4096)),
+                           ("down", (4096, 11008))):
+            r = bench_gemv(K, torch, be32, timer, args, K.Q4_K, o, i, seed=20)
+            extras[f"layer_{nm}"] = {"us": r["ms"] * 1e3, "GBps": r["GBps"]}
+            tot_b += r["bytes"]
+            tot_ms += r["ms"]
+        extras["layer_total"] = {"us": tot_ms * 1e3, "GBps": tot_b / tot_ms / 1e6}
+        log(f"  layer {tot_ms * 1e3:.1f} us {tot_b / tot_ms / 1e6:.0f} GB/s")
+    if args.all or want("head") and only:
+        for dt, nm in ((K.Q6_K, "q6_k"), (K.Q8_0, "q8_0")):
+            r = bench_gemv(K, torch, be32, timer, args, dt, 128256, 4096, seed=30)
+            extras[f"head_{nm}"] = {"us": r["ms"] * 1e3, "GBps": r["GBps"],
+                                    "frac_hbm": r["GBps"] / HBM_PEAK_GBS}
+            log(f"  head {nm} {r['ms'] * 1e3:.1f} us {r['GBps']:.0f} GB/s")
+
+    # ---- CPU baseline (rank 0, N = 1) ----------------------------------------
+    cpu = None
+    if not args.no_cpu:
+        import oracle as O
+        log("cpu baseline ...")
+        cpu = cpu_baseline(O, g["w"], g["x"], n_out, n_in, args.cpu_seconds)
+        log(f"  {cpu['value']:.2f} GB/s on {cpu['cores']} cores")
+
+    achieved = g["bytes"] / (g["ms"] * 1e-3) / 1e9
+    line = {
+        "metric": "decode GEMV GB/s & %HBM peak (Q4_K 4096x14336); prefill GEMM TFLOPS",
+        "value": round(achieved, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": g["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights quantized to Q4_K, x ~ N(0,1))",
+        "config": {"workload": "q4_k_gemv_4096x14336_m1", "n_in": n_in, "n_out": n_out,
+                   "rows": 1, "activations": "f32", "weight_copies": g["copies"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic(), "kernel": "gemv_seg_kernel<Q4_K,f32,f32,1,8>",
+                     "algorithmic_bytes_per_launch": g["bytes"]},
+        "cpu_baseline": cpu and {k: v for k, v in cpu.items()},
+        "extras": extras,
+    }
+    print(json.dumps(line), flush=True)
+    be32.close()
+    be16.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,237 @@
+"""kraken_amd -- MI355X (gfx950) quantized weight-math backend.
+
+Python mirror of Kraken's ``Backend`` hot-path operators
+(include/krk/backend.hpp:337-1876 in the reference) over the C ABI in
+include/krk_mi355x.h, implemented by the in-tree HIP library
+``kraken_amd/libkrk_mi355x.so``.  Tensors are torch tensors on the GPU; torch
+is only the allocator and stream provider here, every operator runs in the
+library's own kernels.  There is no fallback: if the library or a GPU is
+missing the operators raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkrk_mi355x.so")
+
+# GGUF type ids (include/krk/quant.hpp:16-34) and the ABI's enums.
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+ACT_F32, ACT_F16 = 0, 1
+PATH_AUTO, PATH_EXACT, PATH_MFMA, PATH_INT8 = 0, 1, 2, 3
+DTYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+BLOCK_VALUES = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q6_K: 210}
+
+_vp, _i64, _i32, _f32, _u64 = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_uint64
+_P = C.POINTER
+
+# name -> (restype, argtypes); the complete exported surface of the header.
+SIGNATURES = {
+    "krk_backend_create": (_i32, [_i32, _i32, _P(_vp)]),
+    "krk_backend_destroy": (_i32, [_vp]),
+    "krk_set_stream": (_i32, [_vp, _vp]),
+    "krk_set_gemm_path": (_i32, [_vp, _i32]),
+    "krk_act_type": (_i32, [_vp]),
+    "krk_sync": (_i32, [_vp]),
+    "krk_last_error": (C.c_char_p, [_vp]),
+    "krk_status_string": (C.c_char_p, [_i32]),
+    "krk_dtype_block_size": (_i32, [_i32]),
+    "krk_dtype_block_bytes": (_i32, [_i32]),
+    "krk_dtype_row_bytes": (_i64, [_i32, _i64]),
+    "krk_dtype_row_aligned": (_i32, [_i32, _i64]),
+    "krk_gemm": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64]),
+    "krk_gemm_k_ok": (_i32, [_vp, _i64]),
+    "krk_gemm_accumulate": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp,
+                                   _P(_i32)]),
+    "krk_gemm_group": (_i32, [_vp, _P(_vp), _vp, _P(_vp), _i32, _P(_i64), _i64, _i32,
+                              _i64, _i32, _P(_i32), _i32, _P(_i32), _P(_vp), _P(_i32)]),
+    "krk_router_softmax_supported": (_i32, [_vp]),
+    "krk_router_softmax": (_i32, [_vp, _vp, _vp, _i64, _i32]),
+    "krk_router_topk_supported": (_i32, [_vp]),
+    "krk_router_topk": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp, _vp, _i32, _f32]),
+    "krk_moe_dispatch_supported": (_i32, [_vp]),
+    "krk_moe_dispatch": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64,
+                                _i64, _i32]),
+    "krk_dequant_rows_f32": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64]),
+    "krk_dequant_rows_f16": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64]),
+    "krk_quantize_q8_rows": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "krk_synth_normal": (None, [_vp, _i64, _u64, _f32, _f32, _i32]),
+    "krk_quantize_weights": (_i32, [_i32, _vp, _i64, _i64, _vp, _i32]),
+}
+
+
+class KrkError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib():
+    """The loaded HIP library; raises if it was not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise KrkError(f"{LIB_PATH} is missing: run kraken_amd/build.py "
+                           "(or __graft_entry__.build()) first")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+def row_bytes(wt: int, n: int) -> int:
+    return int(lib().krk_dtype_row_bytes(wt, n))
+
+
+# ------------------------------------------------------------ host helpers --
+def synth_normal(n: int, seed: int, mean: float = 0.0, std: float = 1.0,
+                 nthreads: int = 8):
+    """numpy f32[n] from the library's seeded generator."""
+    import numpy as np
+    v = np.empty(n, np.float32)
+    lib().krk_synth_normal(v.ctypes.data, n, seed, mean, std, nthreads)
+    return v
+
+
+def quantize(wt: int, v, n_rows: int, n_in: int, nthreads: int = 8):
+    """GGUF bytes (numpy uint8) of an f32 [n_rows, n_in] matrix."""
+    import numpy as np
+    v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
+    assert v.size == n_rows * n_in
+    out = np.empty(n_rows * row_bytes(wt, n_in), np.uint8)
+    st = lib().krk_quantize_weights(wt, v.ctypes.data, n_rows, n_in, out.ctypes.data,
+                                    nthreads)
+    if st != 0:
+        raise KrkError(lib().krk_status_string(st).decode())
+    return out
+
+
+# ------------------------------------------------------------------ backend --
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+class Backend:
+    """The MI355X backend: the reference's Backend hot-path surface.
+
+    ``act`` is the activation type (``ACT_F32`` to compare against the f32 CPU
+    oracle, ``ACT_F16`` like the reference's GPU backend).  All tensors are
+    torch CUDA tensors; results are asynchronous on ``stream`` (torch's
+    current stream by default) until :meth:`sync`.
+    """
+
+    def __init__(self, device: int = 0, act: int = ACT_F32, stream=None):
+        import torch
+        if not torch.cuda.is_available():
+            raise KrkError("no GPU visible: the MI355X backend has no CPU fallback")
+        h = _vp()
+        st = lib().krk_backend_create(device, act, C.byref(h))
+        if st != 0:
+            raise KrkError(f"krk_backend_create: {lib().krk_status_string(st).decode()}")
+        self._h = h
+        self.device = device
+        self.act = act
+        self.set_stream(stream if stream is not None else torch.cuda.current_stream(device))
+
+    # context
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().krk_backend_destroy(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def _check(self, st: int, what: str):
+        if st != 0:
+            msg = lib().krk_last_error(self._h).decode()
+            raise KrkError(f"{what}: {lib().krk_status_string(st).decode()}: {msg}")
+
+    def set_stream(self, stream):
+        self.stream = stream
+        self._check(lib().krk_set_stream(self._h, stream.cuda_stream), "set_stream")
+
+    def set_gemm_path(self, path: int):
+        self._check(lib().krk_set_gemm_path(self._h, path), "set_gemm_path")
+
+    def act_type(self) -> int:
+        return int(lib().krk_act_type(self._h))
+
+    def sync(self):
+        self._check(lib().krk_sync(self._h), "sync")
+
+    # hot operators (backend.hpp:859-1054)
+    def gemm(self, out, x, w, wt: int, n_out: int, n_in: int, rows: int):
+        self._check(lib().krk_gemm(self._h, _ptr(out), _ptr(x), _ptr(w), wt, n_out, n_in,
+                                   rows), "gemm")
+
+    def gemm_k_ok(self, k: int) -> bool:
+        return bool(lib().krk_gemm_k_ok(self._h, k))
+
+    def gemm_accumulate(self, dst, x, w, wt: int, n_out: int, n_in: int, rows: int,
+                        rexp=None) -> bool:
+        fused = _i32(0)
+        self._check(lib().krk_gemm_accumulate(self._h, _ptr(dst), _ptr(x), _ptr(w), wt,
+                                              n_out, n_in, rows, _ptr(rexp),
+                                              C.byref(fused)), "gemm_accumulate")
+        return bool(fused.value)
+
+    def gemm_group(self, outs, x, ws, wt: int, n_outs, n_in: int, rows: int,
+                   silu: bool = False, row_parallel_only: bool = False, wts=None,
+                   xs=None):
+        """Returns (fused, silu_fused)."""
+        n = len(ws)
+        arr_o = (_vp * n)(*[_ptr(o) for o in outs])
+        arr_w = (_vp * n)(*[_ptr(w) for w in ws])
+        arr_n = (_i64 * n)(*n_outs)
+        arr_t = (_i32 * n)(*wts) if wts is not None else None
+        arr_x = (_vp * n)(*[_ptr(t) for t in xs]) if xs is not None else None
+        sf, fu = _i32(0), _i32(0)
+        self._check(lib().krk_gemm_group(self._h, arr_o, _ptr(x), arr_w, wt, arr_n, n_in, n,
+                                         rows, int(silu), C.byref(sf),
+                                         int(row_parallel_only), arr_t, arr_x,
+                                         C.byref(fu)), "gemm_group")
+        return bool(fu.value), bool(sf.value)
+
+    def router_softmax(self, probs, logits, n_rows: int, n_expert: int):
+        self._check(lib().krk_router_softmax(self._h, _ptr(probs), _ptr(logits), n_rows,
+                                             n_expert), "router_softmax")
+
+    def router_topk(self, probs, n_rows: int, n_expert: int, k: int, ids, wts,
+                    normalize: bool = True, scale: float = 1.0):
+        self._check(lib().krk_router_topk(self._h, _ptr(probs), n_rows, n_expert, k,
+                                          _ptr(ids), _ptr(wts), int(normalize), scale),
+                    "router_topk")
+
+    def moe_dispatch(self, table, layer: int, n_expert: int, ids, wts, xn, out,
+                     n_tok: int, n_embd: int, n_ff: int, k: int):
+        self._check(lib().krk_moe_dispatch(self._h, _ptr(table), layer, n_expert, _ptr(ids),
+                                           _ptr(wts), _ptr(xn), _ptr(out), n_tok, n_embd,
+                                           n_ff, k), "moe_dispatch")
+
+    # exactness surface
+    def dequant_rows(self, out, w, wt: int, n_rows: int, n_in: int, f16: bool = False):
+        fn = lib().krk_dequant_rows_f16 if f16 else lib().krk_dequant_rows_f32
+        self._check(fn(self._h, _ptr(out), _ptr(w), wt, n_rows, n_in), "dequant_rows")
+
+    def quantize_q8_rows(self, x, rows: int, n: int, xq, dx):
+        self._check(lib().krk_quantize_q8_rows(self._h, _ptr(x), rows, n, _ptr(xq), _ptr(dx)),
+                    "quantize_q8_rows")
+
+
+# MoE device table: krk_moe_entry (include/krk_mi355x.h), the reference's
+# MoeDispatchEntry layout (include/krk/moe_table.hpp:42-50).
+class MoeEntry(C.Structure):
+    _fields_ = [("p", _vp * 3), ("n_out", _i64 * 3), ("n_in", _i64 * 3),
+                ("row_bytes", _i64 * 3), ("type", _i32 * 3), ("present", _i32 * 3),
+                ("_pad", _i32)]
+
+
+def moe_table_bytes(entries) -> bytes:
+    """Pack a list of MoeEntry into the byte image the device table holds."""
+    arr = (MoeEntry * len(entries))(*entries)
+    return bytes(C.string_at(C.addressof(arr), C.sizeof(arr)))

@@ -1,0 +1,416 @@
+// backend.cpp -- the C ABI (include/krk_mi355x.h): argument checks, the
+// dispatch per dtype and row count that HipBackend::gemm does
+// (backend_hip.hip:3175-3490), and the persistent device scratch the backend
+// owns (split/int8/MoE workspaces, backend_hip.hip:3330-3440, 2560-2585).
+// Errors are returned as krk_status codes with a message on the handle,
+// where the reference aborts (backend_hip.hip:78-82).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "krk_kernels.hpp"
+#include "krk_mi355x.h"
+
+struct krk_backend {
+    int device = 0;
+    int act = KRK_ACT_F32;
+    int path = KRK_PATH_AUTO;
+    hipStream_t stream = nullptr;
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+    std::string err;
+};
+
+namespace {
+
+int fail(krk_backend *b, int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    if (b) b->err = buf;
+    return code;
+}
+
+int hip_fail(krk_backend *b, hipError_t e, const char *what) {
+    return fail(b, KRK_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool dtype_on_path(int wt) {
+    return wt == KRK_DT_Q4_0 || wt == KRK_DT_Q8_0 || wt == KRK_DT_Q4_K || wt == KRK_DT_Q6_K;
+}
+
+int make_current(krk_backend *b) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess || cur != b->device) {
+        const hipError_t e = hipSetDevice(b->device);
+        if (e != hipSuccess) return hip_fail(b, e, "hipSetDevice");
+    }
+    return KRK_OK;
+}
+
+int ensure_ws(krk_backend *b, size_t bytes) {
+    if (bytes <= b->ws_bytes) return KRK_OK;
+    if (b->ws) {
+        // the old scratch may still be read by queued work on this stream
+        (void)hipStreamSynchronize(b->stream);
+        (void)hipFree(b->ws);
+        b->ws = nullptr;
+        b->ws_bytes = 0;
+    }
+    const size_t want = (bytes + (1u << 20) - 1) & ~size_t((1u << 20) - 1);
+    const hipError_t e = hipMalloc(&b->ws, want);
+    if (e != hipSuccess) {
+        b->ws = nullptr;
+        return fail(b, KRK_ERR_NOMEM, "scratch of %zu bytes: %s", want, hipGetErrorString(e));
+    }
+    b->ws_bytes = want;
+    return KRK_OK;
+}
+
+// Shape and pointer rules shared by every weight-math entry point.
+int check_mm(krk_backend *b, const void *out, const void *x, const void *w, int wt,
+             int64_t n_out, int64_t n_in, int64_t rows) {
+    if (!b) return KRK_ERR_ARG;
+    if (!out || !x || !w) return fail(b, KRK_ERR_ARG, "null pointer (out=%p x=%p w=%p)", out, x, w);
+    if (n_out <= 0 || n_in <= 0 || rows <= 0)
+        return fail(b, KRK_ERR_ARG, "non-positive size n_out=%lld n_in=%lld rows=%lld",
+                    (long long)n_out, (long long)n_in, (long long)rows);
+    if (!dtype_on_path(wt)) return fail(b, KRK_ERR_DTYPE, "weight type %d is not served", wt);
+    if (n_in % 32 != 0 || !krk_dtype_row_aligned(wt, n_in))
+        return fail(b, KRK_ERR_SHAPE, "n_in=%lld is not a whole number of %d-value blocks",
+                    (long long)n_in, krk_dtype_block_size(wt));
+    if (n_in > (int64_t(1) << 30)) return fail(b, KRK_ERR_SHAPE, "n_in=%lld too large", (long long)n_in);
+    const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
+    if ((wt == KRK_DT_Q4_K && (wa & 15)) || (wa & 1))
+        return fail(b, KRK_ERR_ARG, "weight pointer %p under-aligned for type %d", w, wt);
+    if (reinterpret_cast<uintptr_t>(x) & 15)
+        return fail(b, KRK_ERR_ARG, "activation pointer %p is not 16-byte aligned", x);
+    return KRK_OK;
+}
+
+int run_gemv(krk_backend *b, int wt, krk::SegTable &t) {
+    const hipError_t e = krk::gemv_segments(wt, b->act == KRK_ACT_F16, t, b->stream);
+    if (e != hipSuccess) return hip_fail(b, e, "gemv launch");
+    return KRK_OK;
+}
+
+krk::SegTable one_seg(const void *w, const void *x, void *out, int wt, int64_t n_out,
+                      int64_t n_in, int64_t rows, int kind, const int32_t *rexp) {
+    krk::SegTable t{};
+    t.n = 1;
+    t.n_in = static_cast<int>(n_in);
+    t.row_bytes = krk_dtype_row_bytes(wt, n_in);
+    t.rows = rows;
+    t.x_stride = n_in;
+    t.out_stride = n_out;
+    t.rexp = rexp;
+    t.seg[0] = krk::Seg{w, nullptr, x, out, n_out, 0, kind, 0};
+    return t;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *krk_status_string(int s) {
+    switch (s) {
+        case KRK_OK: return "ok";
+        case KRK_ERR_ARG: return "invalid argument";
+        case KRK_ERR_DTYPE: return "weight type not served";
+        case KRK_ERR_SHAPE: return "shape not addressable";
+        case KRK_ERR_HIP: return "HIP runtime error";
+        case KRK_ERR_NOMEM: return "out of device memory";
+        case KRK_ERR_UNSUPPORTED: return "unsupported";
+        default: return "unknown status";
+    }
+}
+
+int krk_dtype_block_size(int wt) {
+    switch (wt) {
+        case KRK_DT_F32: case KRK_DT_F16: return 1;
+        case KRK_DT_Q4_0: case KRK_DT_Q8_0: return 32;
+        case KRK_DT_Q4_K: case KRK_DT_Q6_K: return 256;
+        default: return 0;
+    }
+}
+
+int krk_dtype_block_bytes(int wt) {
+    switch (wt) {
+        case KRK_DT_F32: return 4;
+        case KRK_DT_F16: return 2;
+        case KRK_DT_Q4_0: return 18;
+        case KRK_DT_Q8_0: return 34;
+        case KRK_DT_Q4_K: return 144;
+        case KRK_DT_Q6_K: return 210;
+        default: return 0;
+    }
+}
+
+int64_t krk_dtype_row_bytes(int wt, int64_t n) {
+    const int bs = krk_dtype_block_size(wt);
+    if (bs <= 0 || n < 0) return 0;
+    return ((n + bs - 1) / bs) * static_cast<int64_t>(krk_dtype_block_bytes(wt));
+}
+
+int krk_dtype_row_aligned(int wt, int64_t n) {
+    const int bs = krk_dtype_block_size(wt);
+    if (bs <= 0) return 0;
+    return bs <= 1 || (n % bs) == 0;
+}
+
+int krk_backend_create(int device, int act, krk_backend **out) {
+    if (!out) return KRK_ERR_ARG;
+    *out = nullptr;
+    if (act != KRK_ACT_F32 && act != KRK_ACT_F16) return KRK_ERR_ARG;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return KRK_ERR_HIP;
+    if (device < 0 || device >= n) return KRK_ERR_ARG;
+    if (hipSetDevice(device) != hipSuccess) return KRK_ERR_HIP;
+    krk_backend *b = new krk_backend();
+    b->device = device;
+    b->act = act;
+    *out = b;
+    return KRK_OK;
+}
+
+int krk_backend_destroy(krk_backend *b) {
+    if (!b) return KRK_ERR_ARG;
+    if (b->ws) {
+        (void)hipSetDevice(b->device);
+        (void)hipStreamSynchronize(b->stream);
+        (void)hipFree(b->ws);
+    }
+    delete b;
+    return KRK_OK;
+}
+
+int krk_set_stream(krk_backend *b, void *stream) {
+    if (!b) return KRK_ERR_ARG;
+    b->stream = static_cast<hipStream_t>(stream);
+    return KRK_OK;
+}
+
+int krk_set_gemm_path(krk_backend *b, int path) {
+    if (!b) return KRK_ERR_ARG;
+    if (path < KRK_PATH_AUTO || path > KRK_PATH_INT8) return fail(b, KRK_ERR_ARG, "gemm path %d", path);
+    b->path = path;
+    return KRK_OK;
+}
+
+int krk_act_type(const krk_backend *b) { return b ? b->act : KRK_ERR_ARG; }
+
+int krk_sync(krk_backend *b) {
+    if (!b) return KRK_ERR_ARG;
+    if (int s = make_current(b)) return s;
+    const hipError_t e = hipStreamSynchronize(b->stream);
+    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "hipStreamSynchronize");
+}
+
+const char *krk_last_error(const krk_backend *b) { return b ? b->err.c_str() : "null handle"; }
+
+int krk_gemm_k_ok(const krk_backend *b, int64_t k) {
+    (void)b;
+    return k > 0 && (k % 32) == 0 && k <= (int64_t(1) << 30);
+}
+
+int krk_gemm(krk_backend *b, void *out, const void *x, const void *w, int wt, int64_t n_out,
+             int64_t n_in, int64_t rows) {
+    if (int s = check_mm(b, out, x, w, wt, n_out, n_in, rows)) return s;
+    if (int s = make_current(b)) return s;
+    const bool f16 = b->act == KRK_ACT_F16;
+    if (rows <= 8 || b->path == KRK_PATH_EXACT) {
+        krk::SegTable t = one_seg(w, x, out, wt, n_out, n_in, rows, krk::SEG_PLAIN, nullptr);
+        return run_gemv(b, wt, t);
+    }
+    const int64_t rb = krk_dtype_row_bytes(wt, n_in);
+    if (b->path == KRK_PATH_INT8) {
+        if (wt != KRK_DT_Q8_0)
+            return fail(b, KRK_ERR_UNSUPPORTED, "the int8 rung serves Q8_0 weights only");
+        if (int s = ensure_ws(b, krk::gemm_int8_workspace(rows, n_in))) return s;
+        const hipError_t e = krk::gemm_int8_q8_0(w, rb, x, f16, out, rows, n_out, n_in, b->ws,
+                                                 b->ws_bytes, b->stream);
+        return e == hipSuccess ? KRK_OK : hip_fail(b, e, "int8 gemm");
+    }
+    if (int s = ensure_ws(b, krk::gemm_mfma_workspace(wt, rows, n_out, n_in))) return s;
+    const hipError_t e = krk::gemm_mfma(wt, w, rb, x, f16, out, rows, n_out, n_in, b->ws,
+                                        b->ws_bytes, b->stream);
+    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "mfma gemm");
+}
+
+int krk_gemm_accumulate(krk_backend *b, void *dst, const void *x, const void *w, int wt,
+                        int64_t n_out, int64_t n_in, int64_t rows, const int32_t *rexp,
+                        int *fused) {
+    if (fused) *fused = 0;
+    if (int s = check_mm(b, dst, x, w, wt, n_out, n_in, rows)) return s;
+    if (dst == x) return fail(b, KRK_ERR_ARG, "gemm_accumulate: x must not alias dst");
+    if (rows != 1) return KRK_OK;  // declined: the caller does gemm + add
+    if (int s = make_current(b)) return s;
+    krk::SegTable t = one_seg(w, x, dst, wt, n_out, n_in, rows, krk::SEG_ACC, rexp);
+    if (int s = run_gemv(b, wt, t)) return s;
+    if (fused) *fused = 1;
+    return KRK_OK;
+}
+
+int krk_gemm_group(krk_backend *b, void *const out[], const void *x, const void *const w[],
+                   int wt, const int64_t n_out[], int64_t n_in, int n_mat, int64_t rows,
+                   int silu, int *silu_fused, int row_parallel_only, const int wts[],
+                   const void *const xs[], int *fused) {
+    (void)row_parallel_only;  // every launch here is row-parallel (no split-K)
+    if (silu_fused) *silu_fused = 0;
+    if (fused) *fused = 0;
+    if (!b) return KRK_ERR_ARG;
+    if (!out || !w || !n_out || n_mat <= 0) return fail(b, KRK_ERR_ARG, "gemm_group: empty group");
+    if (silu && n_mat < 2) return fail(b, KRK_ERR_ARG, "gemm_group: silu needs gate and up");
+    bool uniform = true;
+    for (int m = 0; m < n_mat; m++) {
+        const int t = wts ? wts[m] : wt;
+        const void *xm = xs ? xs[m] : x;
+        if (int s = check_mm(b, out[m], xm, w[m], t, n_out[m], n_in, rows)) return s;
+        if (t != (wts ? wts[0] : wt)) uniform = false;
+    }
+    if (silu && n_out[0] != n_out[1]) return fail(b, KRK_ERR_SHAPE, "gate/up row counts differ");
+    if (int s = make_current(b)) return s;
+    const int t0 = wts ? wts[0] : wt;
+    const int nseg = n_mat - (silu ? 1 : 0);
+    if (rows != 1 || !uniform || nseg > krk::kMaxSegs) {
+        // the default Backend::gemm_group: one gemm per matrix, activation
+        // left to the caller
+        for (int m = 0; m < n_mat; m++)
+            if (int s = krk_gemm(b, out[m], xs ? xs[m] : x, w[m], wts ? wts[m] : wt, n_out[m], n_in,
+                                 rows))
+                return s;
+        return KRK_OK;
+    }
+    krk::SegTable t{};
+    t.n_in = static_cast<int>(n_in);
+    t.row_bytes = krk_dtype_row_bytes(t0, n_in);
+    t.rows = 1;
+    t.x_stride = n_in;
+    t.out_stride = 0;
+    int k = 0;
+    if (silu) {
+        t.seg[k++] = krk::Seg{w[0], w[1], xs ? xs[0] : x, out[0], n_out[0], 0, krk::SEG_SILU, 0};
+    }
+    for (int m = silu ? 2 : 0; m < n_mat; m++)
+        t.seg[k++] = krk::Seg{w[m], nullptr, xs ? xs[m] : x, out[m], n_out[m], 0, krk::SEG_PLAIN, 0};
+    t.n = k;
+    if (int s = run_gemv(b, t0, t)) return s;
+    if (silu_fused) *silu_fused = silu ? 1 : 0;
+    if (fused) *fused = 1;
+    return KRK_OK;
+}
+
+int krk_router_softmax_supported(const krk_backend *b) { return b ? 1 : 0; }
+int krk_router_topk_supported(const krk_backend *b) { return b ? 1 : 0; }
+
+int krk_router_softmax(krk_backend *b, void *probs, const void *logits, int64_t n_rows,
+                       int n_expert) {
+    if (!b) return KRK_ERR_ARG;
+    if (!probs || !logits || n_rows <= 0 || n_expert <= 0 || n_expert > 1024)
+        return fail(b, KRK_ERR_ARG, "router_softmax: bad arguments");
+    if (int s = make_current(b)) return s;
+    const hipError_t e = krk::router_softmax(logits, b->act == KRK_ACT_F16,
+                                             static_cast<float *>(probs), n_rows, n_expert, b->stream);
+    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "router_softmax");
+}
+
+int krk_router_topk(krk_backend *b, const void *probs, int64_t n_rows, int n_expert, int k,
+                    void *ids, void *wts, int normalize, float scale) {
+    if (!b) return KRK_ERR_ARG;
+    if (!probs || !ids || !wts || n_rows <= 0 || n_expert <= 0 || n_expert > 1024 || k <= 0 ||
+        k > n_expert || k > 64)
+        return fail(b, KRK_ERR_ARG, "router_topk: bad arguments");
+    if (int s = make_current(b)) return s;
+    const hipError_t e = krk::router_topk(static_cast<const float *>(probs), n_rows, n_expert, k,
+                                          static_cast<int32_t *>(ids), static_cast<float *>(wts),
+                                          normalize, scale, b->stream);
+    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "router_topk");
+}
+
+int krk_moe_dispatch_supported(const krk_backend *b) { return b ? 1 : 0; }
+
+int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert, const void *ids,
+                     const void *wts, const void *xn, void *out, int64_t n_tok, int64_t n_embd,
+                     int64_t n_ff, int k) {
+    if (!b) return KRK_ERR_ARG;
+    if (!table || !ids || !wts || !xn || !out || n_tok <= 0 || k <= 0 || n_expert <= 0 ||
+        layer < 0 || k > n_expert)
+        return fail(b, KRK_ERR_ARG, "moe_dispatch: bad arguments");
+    if ((n_embd % 256) || (n_ff % 256))
+        return fail(b, KRK_ERR_SHAPE, "moe_dispatch: n_embd=%lld n_ff=%lld must be multiples of 256",
+                    (long long)n_embd, (long long)n_ff);
+    if (reinterpret_cast<uintptr_t>(xn) & 15)
+        return fail(b, KRK_ERR_ARG, "moe_dispatch: xn is not 16-byte aligned");
+    if (int s = make_current(b)) return s;
+    // The table lives on the device; its entries' types and strides are read
+    // there.  The host learns the (uniform) weight type from entry 0 of the
+    // layer so the right kernel instantiation is launched.
+    krk_moe_entry e0;
+    const krk_moe_entry *tab = static_cast<const krk_moe_entry *>(table);
+    hipError_t he = hipMemcpyAsync(&e0, tab + static_cast<int64_t>(layer) * n_expert, sizeof(e0),
+                                   hipMemcpyDeviceToHost, b->stream);
+    if (he == hipSuccess) he = hipStreamSynchronize(b->stream);
+    if (he != hipSuccess) return hip_fail(b, he, "moe_dispatch: reading table entry");
+    for (int m = 0; m < 3; m++) {
+        if (!e0.present[m] || !dtype_on_path(e0.type[m]))
+            return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: matrix %d absent or of type %d", m,
+                        e0.type[m]);
+        if (e0.type[m] != e0.type[0])
+            return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: mixed expert formats");
+    }
+    if (e0.n_in[0] != n_embd || e0.n_out[0] != n_ff || e0.n_in[2] != n_ff || e0.n_out[2] != n_embd)
+        return fail(b, KRK_ERR_SHAPE, "moe_dispatch: table geometry does not match n_embd/n_ff");
+    krk::MoeArgs a{};
+    a.table = table; a.layer = layer; a.n_expert = n_expert; a.k = k;
+    a.ids = static_cast<const int32_t *>(ids);
+    a.wts = static_cast<const float *>(wts);
+    a.xn = xn; a.out = out;
+    a.n_tok = n_tok; a.n_embd = n_embd; a.n_ff = n_ff;
+    a.act_f16 = b->act == KRK_ACT_F16;
+    a.wt = e0.type[0];
+    a.rb_gate = e0.row_bytes[0]; a.rb_up = e0.row_bytes[1]; a.rb_down = e0.row_bytes[2];
+    if (int s = ensure_ws(b, krk::moe_workspace(n_tok, k, n_expert, n_embd, n_ff))) return s;
+    he = krk::moe_dispatch(a, b->ws, b->ws_bytes, b->stream);
+    return he == hipSuccess ? KRK_OK : hip_fail(b, he, "moe_dispatch");
+}
+
+int krk_dequant_rows_f32(krk_backend *b, float *out, const void *w, int wt, int64_t n_rows,
+                         int64_t n_in) {
+    if (!b) return KRK_ERR_ARG;
+    if (!out || !w || n_rows <= 0 || n_in <= 0) return fail(b, KRK_ERR_ARG, "dequant: bad arguments");
+    if (!dtype_on_path(wt)) return fail(b, KRK_ERR_DTYPE, "weight type %d is not served", wt);
+    if (!krk_dtype_row_aligned(wt, n_in)) return fail(b, KRK_ERR_SHAPE, "dequant: ragged row");
+    if (int s = make_current(b)) return s;
+    const hipError_t e = krk::dequant_rows(wt, w, krk_dtype_row_bytes(wt, n_in), n_rows, n_in, out,
+                                           false, b->stream);
+    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "dequant");
+}
+
+int krk_dequant_rows_f16(krk_backend *b, void *out, const void *w, int wt, int64_t n_rows,
+                         int64_t n_in) {
+    if (!b) return KRK_ERR_ARG;
+    if (!out || !w || n_rows <= 0 || n_in <= 0) return fail(b, KRK_ERR_ARG, "dequant: bad arguments");
+    if (!dtype_on_path(wt)) return fail(b, KRK_ERR_DTYPE, "weight type %d is not served", wt);
+    if (!krk_dtype_row_aligned(wt, n_in)) return fail(b, KRK_ERR_SHAPE, "dequant: ragged row");
+    if (int s = make_current(b)) return s;
+    const hipError_t e = krk::dequant_rows(wt, w, krk_dtype_row_bytes(wt, n_in), n_rows, n_in, out,
+                                           true, b->stream);
+    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "dequant");
+}
+
+int krk_quantize_q8_rows(krk_backend *b, const float *x, int64_t rows, int64_t n, int8_t *xq,
+                         float *dx) {
+    if (!b) return KRK_ERR_ARG;
+    if (!x || !xq || !dx || rows <= 0 || n <= 0 || n % 32)
+        return fail(b, KRK_ERR_ARG, "quantize_q8: bad arguments");
+    if (int s = make_current(b)) return s;
+    const hipError_t e = krk::quantize_q8_rows(x, false, rows, n, xq, dx, b->stream);
+    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "quantize_q8");
+}
+
+}  // extern "C"

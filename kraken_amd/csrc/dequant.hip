@@ -1,0 +1,111 @@
+// dequant.hip -- the exactness surface: whole rows through the 32-value chunk
+// contract (bit-identical to the host decoders, src/quant.cpp:331-512 and
+// dequant_row 1911-1960), and the Q8 activation quantizer
+// (quantize_q8_32_d, src/quant.cpp:2167-2197) that the int8 rung feeds on.
+#include "krk_formats.hpp"
+#include "krk_kernels.hpp"
+
+namespace krk {
+
+// One thread per 32-value chunk.  Row r, chunk c -> out[r, 32c .. 32c+31].
+template <int DT, bool F16>
+__global__ void __launch_bounds__(256) dequant_kernel(const uint8_t *__restrict__ w,
+                                                      int64_t row_bytes, int64_t n_rows,
+                                                      int64_t n_in, void *__restrict__ out) {
+    constexpr int BV = blk_vals(DT), BB = blk_bytes(DT), CPB = BV / 32;
+    const int64_t chunks_per_row = n_in / 32;
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= n_rows * chunks_per_row) return;
+    const int64_t r = gid / chunks_per_row, c = gid % chunks_per_row;
+    const uint8_t *blk = w + r * row_bytes + (c / CPB) * BB;
+    float y[32];
+    dequant_chunk<DT>(blk, static_cast<int>(c % CPB), y);
+    const int64_t o = r * n_in + c * 32;
+    if constexpr (F16) {
+        _Float16 *oh = static_cast<_Float16 *>(out) + o;
+#pragma unroll
+        for (int i = 0; i < 32; i++) oh[i] = static_cast<_Float16>(y[i]);
+    } else {
+        float *of = static_cast<float *>(out) + o;
+#pragma unroll
+        for (int i = 0; i < 32; i += 4)
+            *reinterpret_cast<floatx4 *>(of + i) = floatx4{y[i], y[i + 1], y[i + 2], y[i + 3]};
+    }
+}
+
+template <bool F16>
+static hipError_t dq(int dt, const void *w, int64_t rb, int64_t n_rows, int64_t n_in, void *out,
+                     hipStream_t st) {
+    const int64_t total = n_rows * (n_in / 32);
+    const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+    const uint8_t *wb = static_cast<const uint8_t *>(w);
+    switch (dt) {
+        case DT_Q4_0: hipLaunchKernelGGL((dequant_kernel<DT_Q4_0, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
+        case DT_Q8_0: hipLaunchKernelGGL((dequant_kernel<DT_Q8_0, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
+        case DT_Q4_K: hipLaunchKernelGGL((dequant_kernel<DT_Q4_K, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
+        case DT_Q6_K: hipLaunchKernelGGL((dequant_kernel<DT_Q6_K, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t dequant_rows(int dt, const void *w, int64_t row_bytes, int64_t n_rows, int64_t n_in,
+                        void *out, bool to_f16, hipStream_t st) {
+    return to_f16 ? dq<true>(dt, w, row_bytes, n_rows, n_in, out, st)
+                  : dq<false>(dt, w, row_bytes, n_rows, n_in, out, st);
+}
+
+// quantize_q8_32_d: amax over the 32 values, d = amax / 127 (0 for an
+// all-zero block), codes = round-to-nearest-even(x * (1/d)) clamped to
+// [-127, 127]; a NaN product lands on -127 as the host's cvtps + clamp does.
+template <typename XT>
+__global__ void __launch_bounds__(256) quantize_q8_kernel(const XT *__restrict__ x, int64_t nblk,
+                                                          int8_t *__restrict__ xq,
+                                                          float *__restrict__ dx) {
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) v[i] = static_cast<float>(x[b * 32 + i]);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+    dx[b] = d;
+    uint32_t packed[8];
+    if (d == 0.0f) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) packed[k] = 0u;
+    } else {
+        const float inv = 1.0f / d;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float pr = v[4 * k + j] * inv;
+                int q = (pr != pr) ? -127 : static_cast<int>(fminf(fmaxf(__builtin_rintf(pr), -127.0f), 127.0f));
+                word |= (static_cast<uint32_t>(q) & 0xFFu) << (8 * j);
+            }
+            packed[k] = word;
+        }
+    }
+    uint32_t *o = reinterpret_cast<uint32_t *>(xq + b * 32);
+#pragma unroll
+    for (int k = 0; k < 8; k++) o[k] = packed[k];
+}
+
+hipError_t quantize_q8_rows(const void *x, bool x_f16, int64_t rows, int64_t n, int8_t *xq,
+                            float *dx, hipStream_t st) {
+    const int64_t nblk = rows * (n / 32);
+    const dim3 grid(static_cast<unsigned>((nblk + 255) / 256));
+    if (x_f16)
+        hipLaunchKernelGGL((quantize_q8_kernel<_Float16>), grid, dim3(256), 0, st,
+                           static_cast<const _Float16 *>(x), nblk, xq, dx);
+    else
+        hipLaunchKernelGGL((quantize_q8_kernel<float>), grid, dim3(256), 0, st,
+                           static_cast<const float *>(x), nblk, xq, dx);
+    return hipGetLastError();
+}
+
+}  // namespace krk

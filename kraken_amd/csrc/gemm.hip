@@ -1,0 +1,359 @@
+// gemm.hip -- prefill GEMM for rows > 8: out[M, N] = X[M, K] . deq(W)[N, K]^T
+// on gfx950 MFMA.  Replaces the reference's gemm_wmma_kernel / gemm_simt_kernel
+// / gemm_reduce_kernel (src/hip/kernels/gemm.hpp:286-1140) and the int8 rung
+// gemm_dp4a_kernel (src/hip/kernels/gemm_dp4a.hpp:161-610).
+//
+// f16 path (KRK_PATH_MFMA):
+//   * workgroup tile 256 (M) x 256 (N), K consumed 32 values (one GGUF chunk)
+//     per step; 8 waves, each a 128 x 64 sub-tile of 4 x 2
+//     v_mfma_f32_32x32x16_f16 accumulators (128 f32 registers per lane);
+//   * every step the workgroup decodes its 256 weight rows x 32 values with
+//     the host oracle's arithmetic (bit-identical f32), rounds them to f16
+//     into LDS, and stages the activation tile (f16, or f32 rounded to f16)
+//     beside it; rows padded to 80 B so the b128 fragment reads are
+//     bank-conflict free;
+//   * the next step's raw weight bytes and activations are fetched into
+//     registers while the current step's MFMAs run;
+//   * tiles are ordered XCD-first: workgroup g runs on XCD g % 8, so the
+//     launch order is remapped to give each XCD a contiguous run of tiles
+//     sharing one activation row-band in its own L2;
+//   * split-K (z dimension) when the tile count cannot fill 256 CUs, with f32
+//     partials summed in a fixed order by a second kernel.
+//
+// int8 path (KRK_PATH_INT8, Q8_0 weights only): activations quantized per 32
+// with the host rule (quantize_q8_32_d), v_mfma_i32_32x32x32_i8 per 32-value
+// block, and the block fold acc = fma((f32)isum, d_w * d_x, acc) of
+// dot_q8_0_q8_scalar (src/quant.cpp:3261-3279).
+#include "krk_formats.hpp"
+#include "krk_kernels.hpp"
+
+namespace krk {
+
+constexpr int GB_M = 256, GB_N = 256, GB_K = 32;
+constexpr int G_THREADS = 512;
+constexpr int LDS_ROW = 40;  // halves per LDS row: 32 + 8 pad (80 B)
+
+// ------------------------------------------------- weight half-chunk staging
+// Thread view: 16 consecutive values of one weight row, values
+// [32*kt + 16*hf, +16) of the row.  Raw bytes are fetched in fetch() and
+// decoded to f16 in decode(); the f32 intermediate equals the host decoder's.
+template <int DT> struct WStage;
+
+template <> struct WStage<DT_Q4_K> {
+    uint32_t hdr[4], q[4];
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        const int blk = kt >> 3, c = kt & 7;
+        const uint8_t *b = row + blk * 144;
+        const u32x4 h = ld128(b);
+        hdr[0] = h.x; hdr[1] = h.y; hdr[2] = h.z; hdr[3] = h.w;
+        const u32x4 v = ld128(b + 16 + 32 * (c >> 1) + 16 * hf);
+        q[0] = v.x; q[1] = v.y; q[2] = v.z; q[3] = v.w;
+    }
+    __device__ void decode(int kt, _Float16 (&o)[16]) const {
+        const int c = kt & 7;
+        const float d = h2f(hdr[0] & 0xFFFF), dmin = h2f(hdr[0] >> 16);
+        uint32_t sbytes[3] = {hdr[1], hdr[2], hdr[3]};
+        auto sb = [&](int j) { return (sbytes[j >> 2] >> (8 * (j & 3))) & 0xFFu; };
+        int sc, mn;
+        if (c < 4) { sc = sb(c) & 63; mn = sb(c + 4) & 63; }
+        else {
+            sc = (sb(c + 4) & 0xF) | ((sb(c - 4) >> 6) << 4);
+            mn = (sb(c + 4) >> 4) | ((sb(c) >> 6) << 4);
+        }
+        const float d1 = d * static_cast<float>(sc), m1 = dmin * static_cast<float>(mn);
+        const int sh = (c & 1) * 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float qv = static_cast<float>((q[t] >> (8 * k + sh)) & 0xFu);
+                o[4 * t + k] = static_cast<_Float16>(__builtin_fmaf(d1, qv, -m1));
+            }
+    }
+};
+
+template <> struct WStage<DT_Q6_K> {
+    uint32_t ql[4], qh[4], sw, dw;
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        const int blk = kt >> 3, c = kt & 7, h = c >> 2, qd = c & 3;
+        const uint8_t *b = row + blk * 210;
+        load_bytes2<4>(b + 64 * h + 32 * (qd & 1) + 16 * hf, ql);
+        load_bytes2<4>(b + 128 + 32 * h + 16 * hf, qh);
+        // scale byte sc[8h + 2qd + hf] and d (bytes 208..209)
+        const uintptr_t sa = reinterpret_cast<uintptr_t>(b + 192 + 8 * h + 2 * qd + hf);
+        sw = ld32(reinterpret_cast<const uint8_t *>(sa & ~uintptr_t(3))) >> (8 * (sa & 3));
+        const uintptr_t da = reinterpret_cast<uintptr_t>(b + 208);
+        dw = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+    }
+    __device__ void decode(int kt, _Float16 (&o)[16]) const {
+        const int c = kt & 7, qd = c & 3;
+        const float d = h2f(dw & 0xFFFF);
+        const float ds = d * static_cast<float>(static_cast<int8_t>(sw & 0xFF));
+        const int nsh = (qd >> 1) * 4, hsh = 2 * qd;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int qv = ((ql[t] >> (8 * k + nsh)) & 0xF) | (((qh[t] >> (8 * k + hsh)) & 3) << 4);
+                o[4 * t + k] = static_cast<_Float16>(ds * static_cast<float>(qv - 32));
+            }
+    }
+};
+
+template <> struct WStage<DT_Q8_0> {
+    uint32_t q[4], dw;
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        const uint8_t *b = row + kt * 34;
+        load_bytes2<4>(b + 2 + 16 * hf, q);
+        const uintptr_t da = reinterpret_cast<uintptr_t>(b);
+        dw = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+    }
+    __device__ void decode(int, _Float16 (&o)[16]) const {
+        const float d = h2f(dw & 0xFFFF);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                o[4 * t + k] = static_cast<_Float16>(
+                    d * static_cast<float>(static_cast<int8_t>((q[t] >> (8 * k)) & 0xFF)));
+    }
+};
+
+template <> struct WStage<DT_Q4_0> {
+    uint32_t q[4], dw;
+    int hf_;
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        const uint8_t *b = row + kt * 18;
+        load_bytes2<4>(b + 2, q);
+        const uintptr_t da = reinterpret_cast<uintptr_t>(b);
+        dw = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        hf_ = hf;
+    }
+    __device__ void decode(int, _Float16 (&o)[16]) const {
+        const float d = h2f(dw & 0xFFFF);
+        const int sh = hf_ * 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                o[4 * t + k] = static_cast<_Float16>(
+                    d * static_cast<float>(static_cast<int>((q[t] >> (8 * k + sh)) & 0xF) - 8));
+    }
+};
+
+// ------------------------------------------------------- activation staging
+template <typename XT> struct XStage;
+template <> struct XStage<_Float16> {
+    u32x4 v[2];
+    __device__ void fetch(const _Float16 *p, bool ok) {
+        if (ok) {
+            v[0] = *reinterpret_cast<const u32x4 *>(p);
+            v[1] = *reinterpret_cast<const u32x4 *>(p + 8);
+        } else {
+            v[0] = u32x4{0, 0, 0, 0};
+            v[1] = u32x4{0, 0, 0, 0};
+        }
+    }
+    __device__ void store(_Float16 *lds) const {
+        *reinterpret_cast<u32x4 *>(lds) = v[0];
+        *reinterpret_cast<u32x4 *>(lds + 8) = v[1];
+    }
+};
+template <> struct XStage<float> {
+    floatx4 v[4];
+    __device__ void fetch(const float *p, bool ok) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            v[i] = ok ? *reinterpret_cast<const floatx4 *>(p + 4 * i) : floatx4{0, 0, 0, 0};
+    }
+    __device__ void store(_Float16 *lds) const {
+        half8 a, b;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            a[i] = static_cast<_Float16>(v[0][i]);
+            a[4 + i] = static_cast<_Float16>(v[1][i]);
+            b[i] = static_cast<_Float16>(v[2][i]);
+            b[4 + i] = static_cast<_Float16>(v[3][i]);
+        }
+        *reinterpret_cast<half8 *>(lds) = a;
+        *reinterpret_cast<half8 *>(lds + 8) = b;
+    }
+};
+
+// XCD-aware tile order: the hardware hands workgroup g to XCD g % 8.  Give
+// XCD x the contiguous tile range [x*per, (x+1)*per) so its workgroups share
+// activation rows (and weight rows) in that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int g, int G) {
+    const int per = G / 8;
+    if (g >= per * 8) return g;  // tail when G is not a multiple of 8
+    return (g & 7) * per + (g >> 3);
+}
+
+template <int DT, typename XT, typename OT>
+__global__ void __launch_bounds__(G_THREADS, 2)
+    gemm_f16_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const XT *__restrict__ x,
+                    OT *__restrict__ out, float *__restrict__ part, int M, int N, int K,
+                    int k_per_split, int tiles_n) {
+    __shared__ _Float16 Xs[GB_M * LDS_ROW];
+    __shared__ _Float16 Ws[GB_N * LDS_ROW];
+
+    const int G = gridDim.x;
+    const int g = xcd_remap(static_cast<int>(blockIdx.x), G);
+    const int tm = g / tiles_n, tn = g % tiles_n;
+    const int m0 = tm * GB_M, n0 = tn * GB_N;
+    const int kb = static_cast<int>(blockIdx.z) * k_per_split;
+    const int ke = min(K, kb + k_per_split);
+    const int nk = (ke - kb) / GB_K;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves, 128 x 64 each
+
+    // staging roles: row = tid / 2, half = tid & 1
+    const int srow = tid >> 1, shf = tid & 1;
+    const int wr = min(n0 + srow, N - 1);
+    const uint8_t *wrow = w + static_cast<int64_t>(wr) * row_bytes;
+    const bool xok = m0 + srow < M;
+    const XT *xrow = x + static_cast<int64_t>(xok ? m0 + srow : 0) * K + shf * 16;
+
+    floatx16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    WStage<DT> ws;
+    XStage<XT> xs;
+    int kt = kb / GB_K;
+    ws.fetch(wrow, kt, shf);
+    xs.fetch(xrow + kb, xok);
+
+    for (int it = 0; it < nk; it++, kt++) {
+        _Float16 wv[16];
+        ws.decode(kt, wv);
+        __syncthreads();  // the previous step's fragments have been read
+        {
+            half8 a, b;
+#pragma unroll
+            for (int i = 0; i < 8; i++) { a[i] = wv[i]; b[i] = wv[8 + i]; }
+            *reinterpret_cast<half8 *>(&Ws[srow * LDS_ROW + shf * 16]) = a;
+            *reinterpret_cast<half8 *>(&Ws[srow * LDS_ROW + shf * 16 + 8]) = b;
+            xs.store(&Xs[srow * LDS_ROW + shf * 16]);
+        }
+        __syncthreads();
+        if (it + 1 < nk) {  // next step's bytes travel while the MFMAs run
+            ws.fetch(wrow, kt + 1, shf);
+            xs.fetch(xrow + kb + (it + 1) * GB_K, xok);
+        }
+#pragma unroll
+        for (int kk = 0; kk < GB_K; kk += 16) {
+            half8 af[4], bf[2];
+            const int ko = kk + (lane >> 5) * 8;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                af[i] = *reinterpret_cast<const half8 *>(
+                    &Xs[(wm * 128 + i * 32 + (lane & 31)) * LDS_ROW + ko]);
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                bf[j] = *reinterpret_cast<const half8 *>(
+                    &Ws[(wn * 64 + j * 32 + (lane & 31)) * LDS_ROW + ko]);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    // C fragment: lane holds column j = lane % 32, rows 8*(r/4) + 4*(lane/32) + r%4
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+            if (n >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m >= M) continue;
+                const float v = acc[i][j][r];
+                if (part)
+                    part[(static_cast<int64_t>(blockIdx.z) * M + m) * N + n] = v;
+                else
+                    out[static_cast<int64_t>(m) * N + n] = static_cast<OT>(v);
+            }
+        }
+}
+
+// Fixed-order sum of the split-K partials.
+template <typename OT>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float *__restrict__ part,
+                                                            OT *__restrict__ out, int64_t MN,
+                                                            int splits) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= MN) return;
+    float s = 0.0f;
+    for (int z = 0; z < splits; z++) s += part[z * MN + i];
+    out[i] = static_cast<OT>(s);
+}
+
+static int pick_split(int64_t M, int64_t N, int64_t K, int dt) {
+    const int64_t tiles = ((M + GB_M - 1) / GB_M) * ((N + GB_N - 1) / GB_N);
+    const int64_t kblk = blk_vals(dt) < GB_K ? GB_K : blk_vals(dt);
+    int s = 1;
+    // fill at least 256 CUs with one workgroup each, keep >= 2048 K per split
+    while (tiles * s < 256 && K / (s * 2) >= 2048 && (K / (s * 2)) % kblk == 0) s *= 2;
+    return s;
+}
+
+size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K) {
+    const int s = pick_split(M, N, K, dt);
+    return s > 1 ? static_cast<size_t>(s) * M * N * sizeof(float) : 0;
+}
+
+template <int DT, typename XT, typename OT>
+static hipError_t launch_f16(const void *w, int64_t rb, const void *x, void *out, int64_t M,
+                             int64_t N, int64_t K, void *ws, size_t ws_bytes, hipStream_t st) {
+    const int tiles_m = static_cast<int>((M + GB_M - 1) / GB_M);
+    const int tiles_n = static_cast<int>((N + GB_N - 1) / GB_N);
+    const int s = pick_split(M, N, K, DT);
+    const int kps = static_cast<int>(K / s);
+    float *part = nullptr;
+    if (s > 1) {
+        if (ws_bytes < static_cast<size_t>(s) * M * N * sizeof(float)) return hipErrorInvalidValue;
+        part = static_cast<float *>(ws);
+    }
+    dim3 grid(static_cast<unsigned>(tiles_m * tiles_n), 1, static_cast<unsigned>(s));
+    hipLaunchKernelGGL((gemm_f16_kernel<DT, XT, OT>), grid, dim3(G_THREADS), 0, st,
+                       static_cast<const uint8_t *>(w), rb, static_cast<const XT *>(x),
+                       static_cast<OT *>(out), part, static_cast<int>(M), static_cast<int>(N),
+                       static_cast<int>(K), kps, tiles_n);
+    if (s > 1) {
+        const int64_t MN = M * N;
+        hipLaunchKernelGGL((splitk_reduce_kernel<OT>), dim3(static_cast<unsigned>((MN + 255) / 256)),
+                           dim3(256), 0, st, part, static_cast<OT *>(out), MN, s);
+    }
+    return hipGetLastError();
+}
+
+hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bool act_f16,
+                     void *out, int64_t M, int64_t N, int64_t K, void *ws, size_t ws_bytes,
+                     hipStream_t st) {
+#define KRK_GEMM_CASE(D)                                                                       \
+    case D:                                                                                   \
+        return act_f16 ? launch_f16<D, _Float16, _Float16>(w, row_bytes, x, out, M, N, K, ws,  \
+                                                           ws_bytes, st)                       \
+                       : launch_f16<D, float, float>(w, row_bytes, x, out, M, N, K, ws,        \
+                                                     ws_bytes, st);
+    switch (dt) {
+        KRK_GEMM_CASE(DT_Q4_K)
+        KRK_GEMM_CASE(DT_Q6_K)
+        KRK_GEMM_CASE(DT_Q8_0)
+        KRK_GEMM_CASE(DT_Q4_0)
+        default: return hipErrorInvalidValue;
+    }
+#undef KRK_GEMM_CASE
+}
+
+}  // namespace krk

@@ -1,0 +1,124 @@
+// krk_dev.hpp -- device-side building blocks shared by the gfx950 kernels:
+// block geometry, aligned raw loads of 2-byte-aligned GGUF blocks, f16
+// helpers and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace krk {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef int intx4 __attribute__((ext_vector_type(4)));
+typedef int intx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// Q4_K 144 B / 256, Q6_K 210 B / 256, Q4_0 18 B / 32, Q8_0 34 B / 32
+// (include/krk/quant.hpp geometry; src/quant.cpp:1805-1900).
+enum : int { DT_F32 = 0, DT_F16 = 1, DT_Q4_0 = 2, DT_Q8_0 = 8, DT_Q4_K = 12, DT_Q6_K = 14 };
+
+__device__ __forceinline__ float h2f(uint32_t h16) {
+    _Float16 h;
+    uint16_t v = static_cast<uint16_t>(h16);
+    __builtin_memcpy(&h, &v, 2);
+    return static_cast<float>(h);
+}
+
+// One dword from a 4-byte aligned address (global memory, vector load).
+__device__ __forceinline__ uint32_t ld32(const uint8_t *p) {
+    return *reinterpret_cast<const uint32_t *>(p);
+}
+__device__ __forceinline__ u32x4 ld128(const uint8_t *p) {
+    return *reinterpret_cast<const u32x4 *>(p);
+}
+__device__ __forceinline__ u32x2 ld64(const uint8_t *p) {
+    return *reinterpret_cast<const u32x2 *>(p);
+}
+
+// ({hi,lo} >> 8*s)[31:0], s in 0..3 (v_alignbyte_b32).
+__device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
+    return __builtin_amdgcn_alignbyte(hi, lo, s);
+}
+
+// Byte k (0..3) of a dword as f32; the backend selects v_cvt_f32_ubyteN.
+template <int K>
+__device__ __forceinline__ float ubyte_f(uint32_t v) {
+    return static_cast<float>((v >> (8 * K)) & 0xFFu);
+}
+
+// Signed byte k of a dword as f32.
+template <int K>
+__device__ __forceinline__ float sbyte_f(uint32_t v) {
+    return static_cast<float>(static_cast<int32_t>(v << (24 - 8 * K)) >> 24);
+}
+
+__device__ __forceinline__ float shfl_xor(float v, int m) {
+    return __shfl_xor(v, m, kWave);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+    return v;
+}
+
+// Reduce V values per lane (V a power of two, 1..64) across the 64 lanes of a
+// wave.  Afterwards lane l holds the total of value (l >> (6 - log2 V)) in
+// v[0]; a lane whose low 6-log2(V) bits are zero is that value's owner.
+// Each halving step exchanges the half of the array the partner keeps, so the
+// whole reduction costs V-1 + 6-log2(V) shuffles instead of 6*V.
+template <int V>
+__device__ __forceinline__ void wave_reduce_multi(float (&v)[V], int lane) {
+    constexpr int LOGV = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3
+                       : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
+#pragma unroll
+    for (int s = 0; s < LOGV; s++) {
+        const int m = 32 >> s;
+        const int half = V >> (s + 1);
+        const bool upper = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < half; i++) {
+            // keep [half, 2*half) when upper else [0, half)
+            const float keep = upper ? v[i + half] : v[i];
+            const float give = upper ? v[i] : v[i + half];
+            v[i] = keep + shfl_xor(give, m);
+        }
+    }
+#pragma unroll
+    for (int m = (32 >> LOGV); m >= 1; m >>= 1) v[0] += shfl_xor(v[0], m);
+}
+
+// Index of the value a lane owns after wave_reduce_multi<V>.
+template <int V>
+__device__ __forceinline__ int reduce_owner_index(int lane) {
+    constexpr int LOGV = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3
+                       : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
+    // Bit s of the index is the lane bit tested at step s (mask 32 >> s),
+    // with upper halves keeping the high indices: index bit (LOGV-1-s).
+    int idx = 0;
+#pragma unroll
+    for (int s = 0; s < LOGV; s++)
+        if (lane & (32 >> s)) idx |= (V >> (s + 1));
+    return idx;
+}
+
+template <int V>
+__device__ __forceinline__ bool reduce_owner(int lane) {
+    constexpr int LOGV = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3
+                       : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
+    return (lane & ((64 >> LOGV) - 1)) == 0;
+}
+
+__device__ __forceinline__ _Float16 sat_f16(float v) {
+    if (v != v) return static_cast<_Float16>(0.0f);
+    v = fminf(fmaxf(v, -65504.0f), 65504.0f);
+    return static_cast<_Float16>(v);
+}
+
+}  // namespace krk

@@ -1,0 +1,81 @@
+// krk_kernels.hpp -- internal interface between the C-ABI layer (backend.cpp)
+// and the kernel translation units.  Host-side launchers only; no HIP types
+// beyond hipStream_t / hipError_t cross this line.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace krk {
+
+// One projection inside a grouped GEMV launch (the reference's FusedLayer,
+// src/hip/kernels/fused.hpp:48-65).
+enum : int { SEG_PLAIN = 0, SEG_ACC = 1, SEG_SILU = 2 };
+
+struct Seg {
+    const void *w;        // weight rows (gate rows for SEG_SILU)
+    const void *w2;       // up rows for SEG_SILU, else null
+    const void *x;        // activation rows
+    void *out;            // output rows
+    int64_t n_out;
+    int64_t blk_begin;    // first workgroup of this segment (set by the launcher)
+    int kind;
+    int _pad;
+};
+
+constexpr int kMaxSegs = 8;
+
+struct SegTable {
+    Seg seg[kMaxSegs];
+    int n;               // segments in use
+    int n_in;            // shared K
+    int64_t row_bytes;   // shared (one dtype per launch)
+    int64_t rows;        // activation rows
+    int64_t x_stride;    // elements between activation rows
+    int64_t out_stride;  // elements between output rows
+    const int32_t *rexp; // SEG_ACC exponent (nullable)
+};
+
+hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st);
+
+// Bit-exact dequantization (the chunk contract) to f32 / f16 (RNE).
+hipError_t dequant_rows(int dt, const void *w, int64_t row_bytes, int64_t n_rows,
+                        int64_t n_in, void *out, bool to_f16, hipStream_t st);
+
+// Activation quantizer, quant.cpp:2167-2197 semantics.  x in f32 or f16.
+hipError_t quantize_q8_rows(const void *x, bool x_f16, int64_t rows, int64_t n,
+                            int8_t *xq, float *dx, hipStream_t st);
+
+// Prefill GEMM (f16 MFMA, f32 accumulate) and the Q8_0 x Q8 int8 MFMA rung.
+// out[M, N] = X[M, K] . deq(W)[N, K]^T.  `ws` is device scratch of ws_bytes.
+size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K);
+hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bool act_f16,
+                     void *out, int64_t M, int64_t N, int64_t K, void *ws, size_t ws_bytes,
+                     hipStream_t st);
+size_t gemm_int8_workspace(int64_t M, int64_t K);
+hipError_t gemm_int8_q8_0(const void *w, int64_t row_bytes, const void *x, bool act_f16,
+                          void *out, int64_t M, int64_t N, int64_t K, void *ws,
+                          size_t ws_bytes, hipStream_t st);
+
+// Router and MoE dispatch.
+hipError_t router_softmax(const void *logits, bool act_f16, float *probs, int64_t n_rows,
+                          int n_expert, hipStream_t st);
+hipError_t router_topk(const float *probs, int64_t n_rows, int n_expert, int k, int32_t *ids,
+                       float *wts, int normalize, float scale, hipStream_t st);
+
+struct MoeArgs {
+    const void *table;   // krk_moe_entry[n_layer * n_expert]
+    int layer, n_expert, k;
+    const int32_t *ids;
+    const float *wts;
+    const void *xn;
+    void *out;
+    int64_t n_tok, n_embd, n_ff;
+    bool act_f16;
+    int wt;              // the (uniform) weight type of the experts
+    int64_t rb_gate, rb_up, rb_down;
+};
+size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t n_ff);
+hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t st);
+
+}  // namespace krk

@@ -1,0 +1,271 @@
+// moe.hip -- the routed-expert FFN of one layer from device ids, through the
+// device pointer table (Backend::moe_dispatch, backend.hpp:1001-1009; the
+// reference's moe_table_* kernels, src/hip/kernels/moe_table.hpp:38-551).
+//
+// Four launches, none of them per expert and none waiting on the host:
+//   1. plan      one workgroup: expert-major plan of the (token, slot) pairs,
+//                stable (token-then-slot inside an expert), the active-expert
+//                list in ascending id, and each pair's plan position;
+//   2. gate/up   ONE launch over all active experts: workgroup = (expert,
+//                group of ff rows); its pairs' activation rows are gathered
+//                through the plan and share every weight byte read;
+//                mid = silu(gate . x) * (up . x) in f32;
+//   3. down      ONE launch over all active experts, part = down . mid;
+//   4. reduce    out[t] = sum over t's pairs in ascending expert id of
+//                fma(w, part, acc) -- the order and the fused add of the host
+//                loop (engine.cpp:12360-12700, scatter_axpy_rows
+//                backend_cpu.cpp:3193-3217).
+// The weight type is read from the table on the device (no host readback);
+// every expert of a layer must share it.
+#include "gemv_core.hpp"
+#include "krk_mi355x.h"
+
+namespace krk {
+
+struct MoeWs {
+    int32_t *off;       // [n_expert + 1]
+    int32_t *act;       // [n_expert]     active experts, ascending
+    int32_t *n_act;     // [1]
+    int32_t *plan_tok;  // [P]            token of plan position
+    int32_t *plan_pos;  // [P]            plan position of pair t*k+s (-1: dropped)
+    float *mid;         // [P, n_ff]
+    float *part;        // [P, n_embd]
+};
+
+static size_t al(size_t v) { return (v + 255) & ~size_t(255); }
+
+static MoeWs carve(void *ws, int64_t P, int ne, int64_t n_embd, int64_t n_ff) {
+    uint8_t *p = static_cast<uint8_t *>(ws);
+    MoeWs w;
+    w.off = reinterpret_cast<int32_t *>(p); p += al((ne + 1) * 4);
+    w.act = reinterpret_cast<int32_t *>(p); p += al(ne * 4);
+    w.n_act = reinterpret_cast<int32_t *>(p); p += al(4);
+    w.plan_tok = reinterpret_cast<int32_t *>(p); p += al(P * 4);
+    w.plan_pos = reinterpret_cast<int32_t *>(p); p += al(P * 4);
+    w.mid = reinterpret_cast<float *>(p); p += al(P * n_ff * 4);
+    w.part = reinterpret_cast<float *>(p);
+    return w;
+}
+
+size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t n_ff) {
+    const int64_t P = n_tok * k;
+    return al((n_expert + 1) * 4) + al(n_expert * 4) + al(4) + 2 * al(P * 4) +
+           al(P * n_ff * 4) + al(P * n_embd * 4);
+}
+
+// ------------------------------------------------------------------ plan ----
+__global__ void __launch_bounds__(1024) moe_plan_kernel(const int32_t *__restrict__ ids, int64_t P,
+                                                        int k, int ne, MoeWs w) {
+    __shared__ int32_t cnt[1024];
+    __shared__ int32_t offs[1025];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < ne; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int64_t i = tid; i < P; i += blockDim.x) {
+        const int e = ids[i];
+        if (e >= 0 && e < ne) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0, na = 0;
+        for (int e = 0; e < ne; e++) {
+            offs[e] = run;
+            w.off[e] = run;
+            if (cnt[e]) w.act[na++] = e;
+            run += cnt[e];
+        }
+        offs[ne] = run;
+        w.off[ne] = run;
+        w.n_act[0] = na;
+    }
+    __syncthreads();
+    // stable placement: expert e's pairs in ascending pair index (token, slot)
+    for (int e = tid; e < ne; e += blockDim.x) {
+        if (!cnt[e]) continue;
+        int c = offs[e];
+        for (int64_t i = 0; i < P; i++)
+            if (ids[i] == e) {
+                w.plan_tok[c] = static_cast<int32_t>(i / k);
+                w.plan_pos[i] = c;
+                c++;
+            }
+    }
+    for (int64_t i = tid; i < P; i += blockDim.x) {
+        const int e = ids[i];
+        if (e < 0 || e >= ne) w.plan_pos[i] = -1;
+    }
+}
+
+// -------------------------------------------------------------- gate/up ----
+template <typename XT, int MR, int RB>
+__global__ void __launch_bounds__(512) moe_gu_kernel(const krk_moe_entry *__restrict__ tab,
+                                                      const XT *__restrict__ xn, int64_t n_embd,
+                                                      int64_t n_ff, int64_t groups, MoeWs w) {
+    __shared__ float red[8][MR * RB];
+    constexpr int H = RB / 2;
+    const int64_t a = blockIdx.x / groups, g = blockIdx.x % groups;
+    if (a >= w.n_act[0]) return;
+    const int e = w.act[a];
+    const krk_moe_entry &en = tab[e];
+    const int64_t n0 = g * H;
+    const int p0 = w.off[e], np = w.off[e + 1] - p0;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int pass = 0; pass < np; pass += MR) {
+        const XT *xr[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+            xr[m] = pass + m < np ? xn + static_cast<int64_t>(w.plan_tok[p0 + pass + m]) * n_embd
+                                  : nullptr;
+        float acc[MR][RB];
+        const uint8_t *wg = static_cast<const uint8_t *>(en.p[KRK_MOE_GATE]);
+        const uint8_t *wu = static_cast<const uint8_t *>(en.p[KRK_MOE_UP]);
+        switch (en.type[KRK_MOE_GATE]) {
+            case DT_Q4_K: gemv_rows<DT_Q4_K, XT, MR, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
+            case DT_Q6_K: gemv_rows<DT_Q6_K, XT, MR, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
+            case DT_Q4_0: gemv_rows<DT_Q4_0, XT, MR, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
+            default:      gemv_rows<DT_Q8_0, XT, MR, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
+        }
+        float v[MR * RB];
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+#pragma unroll
+            for (int r = 0; r < RB; r++) v[m * RB + r] = acc[m][r];
+        wave_reduce_multi<MR * RB>(v, lane);
+        if (reduce_owner<MR * RB>(lane)) red[wv][reduce_owner_index<MR * RB>(lane)] = v[0];
+        __syncthreads();
+        const int tid = threadIdx.x;
+        if (tid < MR * H) {
+            const int m = tid / H, r = tid % H;
+            float gs = 0.0f, us = 0.0f;
+            for (int kk = 0; kk < nw; kk++) {
+                gs += red[kk][m * RB + r];
+                us += red[kk][m * RB + H + r];
+            }
+            const int64_t n = n0 + r;
+            if (pass + m < np && n < n_ff)
+                w.mid[static_cast<int64_t>(p0 + pass + m) * n_ff + n] = (gs / (1.0f + expf(-gs))) * us;
+        }
+        __syncthreads();
+    }
+}
+
+// ----------------------------------------------------------------- down ----
+template <int MR, int RB>
+__global__ void __launch_bounds__(512) moe_down_kernel(const krk_moe_entry *__restrict__ tab,
+                                                        int64_t n_embd, int64_t n_ff,
+                                                        int64_t groups, MoeWs w) {
+    __shared__ float red[8][MR * RB];
+    const int64_t a = blockIdx.x / groups, g = blockIdx.x % groups;
+    if (a >= w.n_act[0]) return;
+    const int e = w.act[a];
+    const krk_moe_entry &en = tab[e];
+    const int64_t n0 = g * RB;
+    const int p0 = w.off[e], np = w.off[e + 1] - p0;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const uint8_t *wd = static_cast<const uint8_t *>(en.p[KRK_MOE_DOWN]);
+    for (int pass = 0; pass < np; pass += MR) {
+        const float *xr[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+            xr[m] = pass + m < np ? w.mid + static_cast<int64_t>(p0 + pass + m) * n_ff : nullptr;
+        float acc[MR][RB];
+        switch (en.type[KRK_MOE_DOWN]) {
+            case DT_Q4_K: gemv_rows<DT_Q4_K, float, MR, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, acc); break;
+            case DT_Q6_K: gemv_rows<DT_Q6_K, float, MR, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, acc); break;
+            case DT_Q4_0: gemv_rows<DT_Q4_0, float, MR, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, acc); break;
+            default:      gemv_rows<DT_Q8_0, float, MR, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, acc); break;
+        }
+        float v[MR * RB];
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+#pragma unroll
+            for (int r = 0; r < RB; r++) v[m * RB + r] = acc[m][r];
+        wave_reduce_multi<MR * RB>(v, lane);
+        if (reduce_owner<MR * RB>(lane)) red[wv][reduce_owner_index<MR * RB>(lane)] = v[0];
+        __syncthreads();
+        const int tid = threadIdx.x;
+        if (tid < MR * RB) {
+            const int m = tid / RB, r = tid % RB;
+            float sum = 0.0f;
+            for (int kk = 0; kk < nw; kk++) sum += red[kk][tid];
+            const int64_t n = n0 + r;
+            if (pass + m < np && n < n_embd)
+                w.part[static_cast<int64_t>(p0 + pass + m) * n_embd + n] = sum;
+        }
+        __syncthreads();
+    }
+}
+
+// --------------------------------------------------------------- reduce ----
+template <typename OT>
+__global__ void __launch_bounds__(256) moe_reduce_kernel(const int32_t *__restrict__ ids,
+                                                         const float *__restrict__ wts, int k,
+                                                         int64_t n_embd, MoeWs w,
+                                                         OT *__restrict__ out) {
+    const int64_t t = blockIdx.y;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (j >= n_embd) return;
+    // this token's pairs in ascending expert id (insertion sort, k <= 64)
+    int ord[64];
+    int n = 0;
+    for (int s = 0; s < k; s++) {
+        if (w.plan_pos[t * k + s] < 0) continue;
+        const int e = ids[t * k + s];
+        int q = n++;
+        while (q > 0 && ids[t * k + ord[q - 1]] > e) { ord[q] = ord[q - 1]; q--; }
+        ord[q] = s;
+    }
+    float acc = 0.0f;
+    for (int q = 0; q < n; q++) {
+        const int s = ord[q];
+        acc = __builtin_fmaf(wts[t * k + s], w.part[static_cast<int64_t>(w.plan_pos[t * k + s]) * n_embd + j], acc);
+    }
+    out[t * n_embd + j] = static_cast<OT>(acc);
+}
+
+hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t st) {
+    const int64_t P = a.n_tok * a.k;
+    if (ws_bytes < moe_workspace(a.n_tok, a.k, a.n_expert, a.n_embd, a.n_ff)) return hipErrorInvalidValue;
+    if (a.n_expert > 1024 || a.k > 64) return hipErrorInvalidValue;
+    MoeWs w = carve(ws, P, a.n_expert, a.n_embd, a.n_ff);
+    const krk_moe_entry *tab = static_cast<const krk_moe_entry *>(a.table) +
+                               static_cast<int64_t>(a.layer) * a.n_expert;
+    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, st, a.ids, P, a.k, a.n_expert, w);
+    const int64_t amax = P < a.n_expert ? P : a.n_expert;
+    auto waves = [](int64_t K) {
+        int64_t steps = (K / 32 + 63) / 64;  // 2048 values per wave step
+        return static_cast<int>(steps < 1 ? 1 : steps > 8 ? 8 : steps);
+    };
+    const int wgu = waves(a.n_embd), wdn = waves(a.n_ff);
+    if (a.n_tok == 1) {
+        const int64_t ggu = (a.n_ff + 3) / 4, gdn = (a.n_embd + 7) / 8;
+        if (a.act_f16)
+            hipLaunchKernelGGL((moe_gu_kernel<_Float16, 1, 8>), dim3(amax * ggu), dim3(64 * wgu), 0, st,
+                               tab, static_cast<const _Float16 *>(a.xn), a.n_embd, a.n_ff, ggu, w);
+        else
+            hipLaunchKernelGGL((moe_gu_kernel<float, 1, 8>), dim3(amax * ggu), dim3(64 * wgu), 0, st,
+                               tab, static_cast<const float *>(a.xn), a.n_embd, a.n_ff, ggu, w);
+        hipLaunchKernelGGL((moe_down_kernel<1, 8>), dim3(amax * gdn), dim3(64 * wdn), 0, st, tab,
+                           a.n_embd, a.n_ff, gdn, w);
+    } else {
+        const int64_t ggu = (a.n_ff + 1) / 2, gdn = (a.n_embd + 3) / 4;
+        if (a.act_f16)
+            hipLaunchKernelGGL((moe_gu_kernel<_Float16, 2, 4>), dim3(amax * ggu), dim3(64 * wgu), 0, st,
+                               tab, static_cast<const _Float16 *>(a.xn), a.n_embd, a.n_ff, ggu, w);
+        else
+            hipLaunchKernelGGL((moe_gu_kernel<float, 2, 4>), dim3(amax * ggu), dim3(64 * wgu), 0, st,
+                               tab, static_cast<const float *>(a.xn), a.n_embd, a.n_ff, ggu, w);
+        hipLaunchKernelGGL((moe_down_kernel<2, 4>), dim3(amax * gdn), dim3(64 * wdn), 0, st, tab,
+                           a.n_embd, a.n_ff, gdn, w);
+    }
+    const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));
+    if (a.act_f16)
+        hipLaunchKernelGGL((moe_reduce_kernel<_Float16>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
+                           a.n_embd, w, static_cast<_Float16 *>(a.out));
+    else
+        hipLaunchKernelGGL((moe_reduce_kernel<float>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
+                           a.n_embd, w, static_cast<float *>(a.out));
+    return hipGetLastError();
+}
+
+}  // namespace krk

@@ -1,0 +1,245 @@
+// synth.cpp -- seeded synthetic inputs for the benchmark configurations, and
+// the host-side weight quantizers that turn f32 matrices into GGUF blocks.
+//
+// Q8_0 and Q4_0 follow the reference's own fixture generator
+// (tools/make_bench_gguf.py:191-218: f64 arithmetic, Python round() = half to
+// even, struct.pack('<e') = one RNE rounding to f16).  The reference ships no
+// Q4_K or Q6_K quantizer (its K-quant fixtures are random bytes,
+// tools/bench_ops.cpp:96-140), so those two are this library's own min/scale
+// fits; they only generate inputs, and every parity check runs on the bytes
+// they produce.
+#include "krk_mi355x.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+namespace {
+
+// The c-th output of a splitmix64 stream started at `seed`.
+inline uint64_t splitmix_at(uint64_t seed, uint64_t c) {
+    uint64_t z = seed + (c + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+inline double normal_at(uint64_t seed, int64_t i) {
+    const uint64_t p = static_cast<uint64_t>(i) >> 1;
+    const double u1 = static_cast<double>((splitmix_at(seed, 2 * p) >> 11) + 1) *
+                      0x1.0p-53;  // (0, 1]
+    const double u2 = static_cast<double>(splitmix_at(seed, 2 * p + 1) >> 11) *
+                      0x1.0p-53;  // [0, 1)
+    const double r = std::sqrt(-2.0 * std::log(u1));
+    const double th = 6.283185307179586476925286766559 * u2;
+    return (i & 1) ? r * std::sin(th) : r * std::cos(th);
+}
+
+template <class F>
+void par_rows(int64_t n, int nthreads, F &&fn) {
+    if (nthreads <= 1 || n < 2) { fn(int64_t{0}, n); return; }
+    nthreads = static_cast<int>(std::min<int64_t>(std::min(nthreads, 256), n));
+    std::vector<std::thread> th;
+    const int64_t per = (n + nthreads - 1) / nthreads;
+    for (int t = 0; t < nthreads; t++) {
+        const int64_t b = per * t, e = std::min(n, b + per);
+        if (b >= e) break;
+        th.emplace_back([&fn, b, e] { fn(b, e); });
+    }
+    for (auto &t : th) t.join();
+}
+
+// f64 -> IEEE half, one rounding, ties to even (what struct.pack('<e') does).
+uint16_t f64_to_half(double v) {
+    const uint16_t sign = std::signbit(v) ? 0x8000u : 0u;
+    if (std::isnan(v)) return 0x7E00u;
+    const double a = std::fabs(v);
+    if (a >= 65520.0) return static_cast<uint16_t>(sign | 0x7C00u);
+    int e = 0;
+    std::frexp(a, &e);
+    int ue = std::max(e - 1, -14);
+    double q = std::nearbyint(std::ldexp(a, 10 - ue));
+    if (q >= 2048.0) { q *= 0.5; ue++; }
+    const uint32_t qi = static_cast<uint32_t>(q);
+    if (qi < 1024u) return static_cast<uint16_t>(sign | qi);
+    return static_cast<uint16_t>(sign | (static_cast<uint32_t>(ue + 15) << 10) |
+                                 (qi - 1024u));
+}
+
+double half_to_f64(uint16_t h) {
+    const int e = (h >> 10) & 31, m = h & 1023;
+    double v;
+    if (e == 0) v = std::ldexp(static_cast<double>(m), -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = std::ldexp(static_cast<double>(m + 1024), e - 25);
+    return (h & 0x8000u) ? -v : v;
+}
+
+inline void put16(uint8_t *p, uint16_t h) {
+    p[0] = static_cast<uint8_t>(h & 0xFF);
+    p[1] = static_cast<uint8_t>(h >> 8);
+}
+
+inline int clampi(double v, int lo, int hi) {
+    return static_cast<int>(std::min<double>(hi, std::max<double>(lo, v)));
+}
+
+// make_bench_gguf.py:191-202
+void quant_q8_0(const float *v, int64_t n, uint8_t *dst) {
+    for (int64_t b = 0; b < n; b += 32, dst += 34) {
+        double amax = 0.0;
+        for (int i = 0; i < 32; i++) amax = std::max(amax, std::fabs(double(v[b + i])));
+        if (amax == 0.0) amax = 1e-8;
+        const double d = amax / 127.0;
+        put16(dst, f64_to_half(d));
+        for (int i = 0; i < 32; i++)
+            dst[2 + i] = static_cast<uint8_t>(static_cast<int8_t>(
+                clampi(std::nearbyint(double(v[b + i]) / d), -127, 127)));
+    }
+}
+
+// make_bench_gguf.py:205-218: d = (signed extreme) / -8 where the extreme is
+// max(-min, max) -- a magnitude, so d <= 0 -- and q = round(v / d + 8).
+void quant_q4_0(const float *v, int64_t n, uint8_t *dst) {
+    for (int64_t b = 0; b < n; b += 32, dst += 18) {
+        double mn = v[b], mx = v[b];
+        for (int i = 1; i < 32; i++) {
+            mn = std::min(mn, double(v[b + i]));
+            mx = std::max(mx, double(v[b + i]));
+        }
+        const double amax = std::max(-mn, mx);
+        const double d = amax != 0.0 ? amax / -8.0 : 0.0;
+        const double id = d != 0.0 ? 1.0 / d : 0.0;
+        put16(dst, f64_to_half(d));
+        int q[32];
+        for (int i = 0; i < 32; i++)
+            q[i] = clampi(std::nearbyint(double(v[b + i]) * id + 8.0), 0, 15);
+        for (int k = 0; k < 16; k++)
+            dst[2 + k] = static_cast<uint8_t>((q[k] & 15) | ((q[k + 16] & 15) << 4));
+    }
+}
+
+// Q4_K (144 B / 256 values): per 32-value sub-block an affine fit
+// v ~ sc*d * q - m*dmin with q in [0,15]; the eight 6-bit (sc, m) pairs are
+// packed the way get_scale_min_k4 (quant.cpp:427-435) unpacks them.
+void quant_q4_k(const float *v, int64_t n, uint8_t *dst) {
+    for (int64_t b = 0; b < n; b += 256, dst += 144) {
+        double scale[8], minv[8];
+        double smax = 0.0, mmax = 0.0;
+        for (int j = 0; j < 8; j++) {
+            double lo = 0.0, hi = 0.0;
+            for (int l = 0; l < 32; l++) {
+                lo = std::min(lo, double(v[b + 32 * j + l]));
+                hi = std::max(hi, double(v[b + 32 * j + l]));
+            }
+            scale[j] = (hi - lo) / 15.0;
+            minv[j] = -lo;  // >= 0
+            smax = std::max(smax, scale[j]);
+            mmax = std::max(mmax, minv[j]);
+        }
+        const uint16_t hd = f64_to_half(smax / 63.0), hm = f64_to_half(mmax / 63.0);
+        const double d = half_to_f64(hd), dmin = half_to_f64(hm);
+        int sc[8], mq[8];
+        for (int j = 0; j < 8; j++) {
+            sc[j] = d > 0 ? clampi(std::nearbyint(scale[j] / d), 0, 63) : 0;
+            mq[j] = dmin > 0 ? clampi(std::nearbyint(minv[j] / dmin), 0, 63) : 0;
+        }
+        put16(dst, hd);
+        put16(dst + 2, hm);
+        uint8_t *s = dst + 4;
+        for (int j = 0; j < 4; j++) {
+            s[j] = static_cast<uint8_t>((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            s[j + 4] = static_cast<uint8_t>((mq[j] & 63) | ((mq[j + 4] >> 4) << 6));
+            s[j + 8] = static_cast<uint8_t>((sc[j + 4] & 15) | ((mq[j + 4] & 15) << 4));
+        }
+        int q[256];
+        for (int j = 0; j < 8; j++) {
+            const double ds = d * sc[j], dm = dmin * mq[j];
+            for (int l = 0; l < 32; l++) {
+                const double x = double(v[b + 32 * j + l]);
+                q[32 * j + l] = ds > 0 ? clampi(std::nearbyint((x + dm) / ds), 0, 15) : 0;
+            }
+        }
+        uint8_t *qs = dst + 16;
+        for (int g = 0; g < 4; g++)
+            for (int l = 0; l < 32; l++)
+                qs[32 * g + l] = static_cast<uint8_t>(q[64 * g + l] | (q[64 * g + 32 + l] << 4));
+    }
+}
+
+// Q6_K (210 B / 256 values): sixteen int8 scales, one per 16 values, codes in
+// [-32, 31] stored as q+32 split into ql (4 bits) and qh (2 bits) in the
+// plane order deq_q6_k (quant.cpp:491-512) reads them back.
+void quant_q6_k(const float *v, int64_t n, uint8_t *dst) {
+    for (int64_t b = 0; b < n; b += 256, dst += 210) {
+        double scale[16], smax = 0.0;
+        for (int j = 0; j < 16; j++) {
+            double amax = 0.0, sv = 0.0;
+            for (int l = 0; l < 16; l++) {
+                const double x = double(v[b + 16 * j + l]);
+                if (std::fabs(x) > amax) { amax = std::fabs(x); sv = x; }
+            }
+            scale[j] = sv / -32.0;  // the signed extreme lands on code -32
+            smax = std::max(smax, std::fabs(scale[j]));
+        }
+        const uint16_t hd = f64_to_half(smax / 127.0);
+        const double d = half_to_f64(hd);
+        int8_t sc[16];
+        for (int j = 0; j < 16; j++)
+            sc[j] = static_cast<int8_t>(d > 0 ? clampi(std::nearbyint(scale[j] / d), -127, 127) : 0);
+        int q[256];  // q + 32, in [0, 63]
+        for (int j = 0; j < 16; j++) {
+            const double ds = d * sc[j];
+            for (int l = 0; l < 16; l++) {
+                const double x = double(v[b + 16 * j + l]);
+                q[16 * j + l] = (ds != 0 ? clampi(std::nearbyint(x / ds), -32, 31) : 0) + 32;
+            }
+        }
+        uint8_t *ql = dst, *qh = dst + 128;
+        std::memset(dst, 0, 210);
+        for (int h = 0; h < 2; h++)
+            for (int l = 0; l < 32; l++) {
+                const int *qq = q + 128 * h;
+                const int q1 = qq[l], q2 = qq[l + 32], q3 = qq[l + 64], q4 = qq[l + 96];
+                ql[64 * h + l] = static_cast<uint8_t>((q1 & 15) | ((q3 & 15) << 4));
+                ql[64 * h + l + 32] = static_cast<uint8_t>((q2 & 15) | ((q4 & 15) << 4));
+                qh[32 * h + l] = static_cast<uint8_t>((q1 >> 4) | ((q2 >> 4) << 2) |
+                                                      ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+            }
+        std::memcpy(dst + 192, sc, 16);
+        put16(dst + 208, hd);
+    }
+}
+
+}  // namespace
+
+extern "C" void krk_synth_normal(float *v, int64_t n, uint64_t seed, float mean,
+                                 float std_, int nthreads) {
+    if (!v || n <= 0) return;
+    par_rows(n, nthreads, [&](int64_t b, int64_t e) {
+        for (int64_t i = b; i < e; i++)
+            v[i] = static_cast<float>(double(mean) + double(std_) * normal_at(seed, i));
+    });
+}
+
+extern "C" int krk_quantize_weights(int wt, const float *v, int64_t n_rows,
+                                    int64_t n_in, void *dst, int nthreads) {
+    if (!v || !dst || n_rows <= 0 || n_in <= 0) return KRK_ERR_ARG;
+    void (*fn)(const float *, int64_t, uint8_t *) = nullptr;
+    switch (wt) {
+        case KRK_DT_Q8_0: fn = quant_q8_0; break;
+        case KRK_DT_Q4_0: fn = quant_q4_0; break;
+        case KRK_DT_Q4_K: fn = quant_q4_k; break;
+        case KRK_DT_Q6_K: fn = quant_q6_k; break;
+        default: return KRK_ERR_DTYPE;
+    }
+    if (!krk_dtype_row_aligned(wt, n_in)) return KRK_ERR_SHAPE;
+    const int64_t rb = krk_dtype_row_bytes(wt, n_in);
+    uint8_t *out = static_cast<uint8_t *>(dst);
+    par_rows(n_rows, nthreads, [&](int64_t b, int64_t e) {
+        for (int64_t r = b; r < e; r++) fn(v + r * n_in, n_in, out + r * rb);
+    });
+    return KRK_OK;
+}

@@ -1,0 +1,519 @@
+/*
+ * krk_oracle.c -- CPU restatement of Kraken's scalar f32 reference for the
+ * quantized weight-math path (Q4_0 / Q8_0 / Q4_K / Q6_K dequant, the strict
+ * single-chain GEMV dot, the Q8 activation quantizer and integer dot, the
+ * host MoE routing and the routed-expert FFN).
+ *
+ * TEST INFRASTRUCTURE: only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg load this library, and only as the checker.
+ *
+ * Compiled with -ffp-contract=off.  The reference is built with g++ -O3 -mfma
+ * (CMakeLists.txt:35-37), where GCC MAY contract a*b+c into one FMA; each place
+ * where it does (checked against the reference built from its own sources:
+ * Q4_K's d1*q-m1, where it is exact either way, and scatter_axpy_rows'
+ * dst += a*src) is written here as an
+ * explicit fmaf(), and nothing else is fused.
+ *
+ * Pinning (see tests/test_oracle.py): the reference's own known-answer tests
+ * (tests/test_kraken.cpp:396-1042, 2087, 8143), closed forms and brute force
+ * in f64, committed golden vectors (tests/golden/), and, where
+ * oracle/_ref/libkrk_ref.so was built from the reference sources, a bitwise
+ * comparison against the reference itself.
+ */
+#include "krk_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* src/common.cpp:161-187 */
+float orc_fp16_to_fp32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu, bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            uint32_t mm = m;
+            int ee = -1;
+            do { mm <<= 1; ee++; } while (!(mm & 0x400u));
+            mm &= 0x3FFu;
+            bits = sign | ((uint32_t)(127 - 15 - ee) << 23) | (mm << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        bits = sign | ((e - 15 + 127) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* src/common.cpp:189-208.  Restated as written, including its tie rule: the
+ * second rounding clause can never hold (it needs bit 13 both clear and set),
+ * so an exact halfway case in the normal range is truncated rather than
+ * rounded to even.  Only dequant_row_f16 uses this; the device f16 path is
+ * compared against an RNE conversion instead. */
+uint16_t orc_fp32_to_fp16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    int32_t e = (int32_t)((x >> 23) & 0xFFu) - 127 + 15;
+    uint32_t m = x & 0x7FFFFFu;
+    if (((x >> 23) & 0xFFu) == 0xFFu)
+        return (uint16_t)(sign | 0x7C00u | (m ? 0x200u : 0));
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        int sh = 14 - e;
+        uint32_t mm = m | 0x800000u;
+        uint32_t half = mm >> sh;
+        uint32_t rem = mm & ((1u << sh) - 1);
+        uint32_t thresh = 1u << (sh - 1);
+        if (rem > thresh || (rem == thresh && (half & 1))) half++;
+        return (uint16_t)(sign | (half & 0x7FFu));
+    }
+    uint32_t half = ((uint32_t)e << 10) | (m >> 13);
+    if ((m & 0x1FFFu) > 0x1000u || ((m & 0x3FFFu) == 0x1000u && (half & 1))) half++;
+    return (uint16_t)(sign | (half & 0x7FFFu));
+}
+
+static inline float ld_f16(const uint8_t *p) {
+    return orc_fp16_to_fp32((uint16_t)(p[0] | (p[1] << 8)));
+}
+
+/* Geometry: src/quant.cpp:1805-1900 (block size / bytes), 1891-1895 (row). */
+int orc_block_size(int dt) {
+    switch (dt) {
+        case ORC_F32: case ORC_F16: return 1;
+        case ORC_Q4_0: case ORC_Q8_0: return 32;
+        case ORC_Q4_K: case ORC_Q6_K: return 256;
+        default: return 0;
+    }
+}
+int orc_block_bytes(int dt) {
+    switch (dt) {
+        case ORC_F32: return 4;
+        case ORC_F16: return 2;
+        case ORC_Q4_0: return 18;
+        case ORC_Q8_0: return 34;
+        case ORC_Q4_K: return 144;
+        case ORC_Q6_K: return 210;
+        default: return 0;
+    }
+}
+int64_t orc_row_bytes(int dt, int64_t n) {
+    int bs = orc_block_size(dt);
+    if (bs <= 0) return 0;
+    return ((n + bs - 1) / bs) * (int64_t)orc_block_bytes(dt);
+}
+
+/* src/quant.cpp:331-339 */
+static void deq_q4_0(const uint8_t *b, float *y) {
+    float d = ld_f16(b);
+    for (int k = 0; k < 16; k++) {
+        y[k] = d * (float)((int)(b[2 + k] & 0xF) - 8);
+        y[k + 16] = d * (float)((int)(b[2 + k] >> 4) - 8);
+    }
+}
+
+/* src/quant.cpp:381-387 */
+static void deq_q8_0(const uint8_t *b, float *y) {
+    float d = ld_f16(b);
+    for (int k = 0; k < 32; k++) y[k] = d * (float)(int8_t)b[2 + k];
+}
+
+/* src/quant.cpp:427-435 */
+static void scale_min_k4(int j, const uint8_t *q, uint8_t *d, uint8_t *m) {
+    if (j < 4) {
+        *d = (uint8_t)(q[j] & 63);
+        *m = (uint8_t)(q[j + 4] & 63);
+    } else {
+        *d = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+/* src/quant.cpp:437-460.  `d1 * q - m1` is contracted to one FMA by the
+ * reference build (vfmsub in dequant_block), hence fmaf(d1, q, -m1).  The
+ * contraction is immaterial here: d1 = d*sc carries at most 17 significant
+ * bits and d1*q at most 21, so the product is exact and both forms round
+ * only the subtraction (tests/test_oracle.py checks this). */
+static void deq_q4_k(const uint8_t *b, float *y) {
+    float d = ld_f16(b), dmin = ld_f16(b + 2);
+    const uint8_t *sc = b + 4, *q = b + 16;
+    for (int j = 0, is = 0; j < 256; j += 64, is += 2, q += 32) {
+        uint8_t si, mi;
+        scale_min_k4(is, sc, &si, &mi);
+        float d1 = d * (float)si, m1 = dmin * (float)mi;
+        scale_min_k4(is + 1, sc, &si, &mi);
+        float d2 = d * (float)si, m2 = dmin * (float)mi;
+        for (int l = 0; l < 32; l++) {
+            y[j + l] = fmaf(d1, (float)(q[l] & 0xF), -m1);
+            y[j + l + 32] = fmaf(d2, (float)(q[l] >> 4), -m2);
+        }
+    }
+}
+
+/* src/quant.cpp:491-512.  `d * sc * (q - 32)` is (d*sc)*(q-32): two products,
+ * nothing to contract. */
+static void deq_q6_k(const uint8_t *b, float *y) {
+    float d = ld_f16(b + 208);
+    for (int n = 0; n < 256; n += 128) {
+        const uint8_t *ql = b + n / 2, *qh = b + 128 + n / 4;
+        const int8_t *sc = (const int8_t *)(b + 192) + n / 16;
+        float *yy = y + n;
+        for (int l = 0; l < 32; l++) {
+            int is = l / 16;
+            int q1 = (ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4);
+            int q2 = (ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4);
+            int q3 = (ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4);
+            int q4 = (ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4);
+            yy[l] = d * (float)sc[is + 0] * (float)(q1 - 32);
+            yy[l + 32] = d * (float)sc[is + 2] * (float)(q2 - 32);
+            yy[l + 64] = d * (float)sc[is + 4] * (float)(q3 - 32);
+            yy[l + 96] = d * (float)sc[is + 6] * (float)(q4 - 32);
+        }
+    }
+}
+
+/* src/quant.cpp:1553-1601 (the four formats on this path plus F16). */
+static void dequant_block(int dt, const uint8_t *p, float *buf) {
+    switch (dt) {
+        case ORC_F16: buf[0] = ld_f16(p); break;
+        case ORC_F32: memcpy(buf, p, 4); break;
+        case ORC_Q4_0: deq_q4_0(p, buf); break;
+        case ORC_Q8_0: deq_q8_0(p, buf); break;
+        case ORC_Q4_K: deq_q4_k(p, buf); break;
+        case ORC_Q6_K: deq_q6_k(p, buf); break;
+        default: break;
+    }
+}
+
+/* src/quant.cpp:1911-1960 (block formats branch). */
+void orc_dequant_row(int dt, const void *src, float *out, int64_t n) {
+    const uint8_t *p = (const uint8_t *)src;
+    int bs = orc_block_size(dt), bb = orc_block_bytes(dt);
+    float buf[256];
+    for (int64_t i = 0; i < n;) {
+        int cnt = (int)((n - i) < bs ? (n - i) : bs);
+        dequant_block(dt, p, buf);
+        memcpy(out + i, buf, (size_t)cnt * sizeof(float));
+        i += cnt;
+        p += bb;
+    }
+}
+
+/* src/quant.cpp:1962-1979 */
+void orc_dequant_row_f16(int dt, const void *src, uint16_t *out, int64_t n) {
+    float *tmp = (float *)malloc((size_t)n * sizeof(float));
+    orc_dequant_row(dt, src, tmp, n);
+    for (int64_t i = 0; i < n; i++) out[i] = orc_fp32_to_fp16(tmp[i]);
+    free(tmp);
+}
+
+/* src/quant.cpp:5576-5591: the strict scalar branch of vec_dot (fast, avx2
+ * and int8 tiers off): ONE f32 chain over the dequantized blocks.
+ * `sum += buf[k] * x[i + k]` is NOT contracted in the reference build: the
+ * product is rounded, then added.  Measured, not assumed: against
+ * oracle/_ref/libkrk_ref.so (the reference's quant.cpp built with its own
+ * flags) the unfused chain matches bit for bit and the fused one does not. */
+float orc_vec_dot(int dt, const void *src, const float *x, int64_t n) {
+    int bs = orc_block_size(dt), bb = orc_block_bytes(dt);
+    const uint8_t *p = (const uint8_t *)src;
+    float buf[256], sum = 0.0f;
+    for (int64_t i = 0; i < n;) {
+        int cnt = (int)((n - i) < bs ? (n - i) : bs);
+        dequant_block(dt, p, buf);
+        for (int k = 0; k < cnt; k++) sum += buf[k] * x[i + k];
+        i += cnt;
+        p += bb;
+    }
+    return sum;
+}
+
+/* ---- a fixed-size pool over independent outputs (src/backend_cpu.cpp:1-8:
+ * parallel over outputs only, never a split reduction, so the answer does not
+ * depend on the thread count). */
+typedef struct {
+    void (*fn)(void *ctx, int64_t b, int64_t e);
+    void *ctx;
+    int64_t b, e;
+} orc_job;
+
+static void *orc_job_run(void *a) {
+    orc_job *j = (orc_job *)a;
+    j->fn(j->ctx, j->b, j->e);
+    return NULL;
+}
+
+static void par_for(int64_t n, int nthreads,
+                    void (*fn)(void *ctx, int64_t b, int64_t e), void *ctx) {
+    if (nthreads <= 1 || n < 2) { fn(ctx, 0, n); return; }
+    if (nthreads > 256) nthreads = 256;
+    if (nthreads > n) nthreads = (int)n;
+    pthread_t th[256];
+    orc_job jobs[256];
+    int64_t per = (n + nthreads - 1) / nthreads;
+    int started = 0;
+    for (int t = 0; t < nthreads; t++) {
+        int64_t b = per * t, e = b + per < n ? b + per : n;
+        if (b >= e) break;
+        jobs[t].fn = fn; jobs[t].ctx = ctx; jobs[t].b = b; jobs[t].e = e;
+        if (pthread_create(&th[t], NULL, orc_job_run, &jobs[t]) != 0) {
+            fn(ctx, b, e);
+            jobs[t].fn = NULL;
+        }
+        started = t + 1;
+    }
+    for (int t = 0; t < started; t++)
+        if (jobs[t].fn) pthread_join(th[t], NULL);
+}
+
+typedef struct {
+    float *out; const float *x; const uint8_t *w; int dt;
+    int64_t n_out, n_in, rows, rb;
+} gemm_ctx;
+
+static void gemm_body(void *c, int64_t b, int64_t e) {
+    gemm_ctx *g = (gemm_ctx *)c;
+    for (int64_t o = b; o < e; o++)
+        for (int64_t r = 0; r < g->rows; r++)
+            g->out[r * g->n_out + o] =
+                orc_vec_dot(g->dt, g->w + o * g->rb, g->x + r * g->n_in, g->n_in);
+}
+
+/* src/backend_cpu.cpp:914-1320 with the int8/fast/avx2 tiers off: every
+ * output element is vec_dot(row o, x row r) (src/quant.cpp:5420-5428). */
+void orc_gemm(float *out, const float *x, const void *w, int dt,
+              int64_t n_out, int64_t n_in, int64_t rows, int nthreads) {
+    gemm_ctx g = {out, x, (const uint8_t *)w, dt, n_out, n_in, rows,
+                  orc_row_bytes(dt, n_in)};
+    par_for(n_out, nthreads, gemm_body, &g);
+}
+
+/* src/quant.cpp:2167-2197 (quantize_q8_32_d): per 32 values amax, d =
+ * amax/127 (0 for an all-zero block), codes cvtps(x * (1/d)) -- round to
+ * nearest even under the default MXCSR -- clamped to [-127, 127].  A NaN
+ * product converts to INT_MIN there and clamps to -127. */
+void orc_quantize_q8_row(const float *x, int64_t n, int8_t *xq, float *dx) {
+    for (int64_t b = 0; b < n; b += 32) {
+        float amax = 0.0f;
+        for (int i = 0; i < 32; i++) {
+            float a = fabsf(x[b + i]);
+            amax = a > amax ? a : amax;
+        }
+        float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+        dx[b / 32] = d;
+        if (d == 0.0f) { memset(xq + b, 0, 32); continue; }
+        float inv = 1.0f / d;
+        for (int i = 0; i < 32; i++) {
+            float p = x[b + i] * inv;
+            long q = isnan(p) ? -2147483647L - 1 : lrintf(p);
+            if (q < -127) q = -127;
+            if (q > 127) q = 127;
+            xq[b + i] = (int8_t)q;
+        }
+    }
+}
+
+/* src/quant.cpp:3261-3279 (dot_q8_0_q8_scalar): exact integer block sum, then
+ * acc = fma((f32)sum, d * dx[b], acc). */
+float orc_dot_q8_0_q8(const void *w, const int8_t *xq, const float *dx,
+                      int64_t n) {
+    const uint8_t *p = (const uint8_t *)w;
+    float acc = 0.0f;
+    for (int64_t b = 0; b < n / 32; b++, p += 34) {
+        float d = ld_f16(p);
+        int64_t sum = 0;
+        for (int i = 0; i < 32; i++)
+            sum += (int64_t)(int8_t)p[2 + i] * (int64_t)xq[b * 32 + i];
+        acc = fmaf((float)sum, d * dx[b], acc);
+    }
+    return acc;
+}
+
+typedef struct {
+    float *out; const int8_t *xq; const float *dx; const uint8_t *w;
+    int64_t n_out, n_in, rows, rb;
+} gq_ctx;
+
+static void gq_body(void *c, int64_t b, int64_t e) {
+    gq_ctx *g = (gq_ctx *)c;
+    for (int64_t o = b; o < e; o++)
+        for (int64_t r = 0; r < g->rows; r++)
+            g->out[r * g->n_out + o] = orc_dot_q8_0_q8(
+                g->w + o * g->rb, g->xq + r * g->n_in, g->dx + r * (g->n_in / 32),
+                g->n_in);
+}
+
+/* The CPU backend's Q8_0 x int8 rung (src/backend_cpu.cpp:952-1000): each
+ * activation row quantized once, then the scalar integer dot per output. */
+void orc_gemm_q8_0_q8(float *out, const float *x, const void *w,
+                      int64_t n_out, int64_t n_in, int64_t rows, int nthreads) {
+    int8_t *xq = (int8_t *)malloc((size_t)(rows * n_in));
+    float *dx = (float *)malloc((size_t)(rows * (n_in / 32)) * sizeof(float));
+    for (int64_t r = 0; r < rows; r++)
+        orc_quantize_q8_row(x + r * n_in, n_in, xq + r * n_in, dx + r * (n_in / 32));
+    gq_ctx g = {out, xq, dx, (const uint8_t *)w, n_out, n_in, rows,
+                orc_row_bytes(ORC_Q8_0, n_in)};
+    par_for(n_out, nthreads, gq_body, &g);
+    free(xq);
+    free(dx);
+}
+
+/* src/backend_cpu.cpp:2401-2406: o = (g / (1 + exp(-g))) * u, std::exp on a
+ * float argument (expf). */
+void orc_silu_mul(float *out, const float *g, const float *u, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        float x = g[i];
+        out[i] = (x / (1.0f + expf(-x))) * u[i];
+    }
+}
+
+/* src/engine.cpp:11704-11714 (softmax branch): running max, sequential sum of
+ * exp(l - max), multiply by 1/sum. */
+void orc_router_softmax(float *probs, const float *logits, int64_t n_rows,
+                        int ne) {
+    for (int64_t r = 0; r < n_rows; r++) {
+        const float *l = logits + r * ne;
+        float *p = probs + r * ne;
+        float mx = l[0];
+        for (int e = 1; e < ne; e++) mx = l[e] > mx ? l[e] : mx;
+        float sum = 0.0f;
+        for (int e = 0; e < ne; e++) {
+            p[e] = expf(l[e] - mx);
+            sum += p[e];
+        }
+        float inv = sum > 0 ? 1.0f / sum : 0.0f;
+        for (int e = 0; e < ne; e++) p[e] *= inv;
+    }
+}
+
+/* src/engine.cpp:11853-11918 with no residency preference and no bias: k
+ * rounds of argmax over the not-yet-taken experts (strict >, ascending id, so
+ * a tie keeps the lower id); the weight is the probability; then
+ * sum-normalize when asked (wt *= 1/sum) and multiply by scale unless it is
+ * 0 or 1. */
+void orc_router_topk(const float *probs, int64_t n_rows, int ne, int k,
+                     int32_t *ids, float *wts, int normalize, float scale) {
+    for (int64_t r = 0; r < n_rows; r++) {
+        const float *p = probs + r * ne;
+        int32_t *sel = ids + r * k;
+        float *wt = wts + r * k;
+        for (int s = 0; s < k; s++) {
+            int best = -1;
+            float bestp = -1.0f;
+            for (int e = 0; e < ne; e++) {
+                int taken = 0;
+                for (int q = 0; q < s; q++)
+                    if (sel[q] == e) { taken = 1; break; }
+                if (taken) continue;
+                if (p[e] > bestp) { bestp = p[e]; best = e; }
+            }
+            sel[s] = best;
+            wt[s] = best >= 0 ? p[best] : 0.0f;
+        }
+        if (normalize) {
+            float ksum = 0;
+            for (int s = 0; s < k; s++) ksum += wt[s];
+            float kinv = ksum > 0 ? 1.0f / ksum : 0.0f;
+            for (int s = 0; s < k; s++) wt[s] *= kinv;
+        }
+        if (scale != 0.0f && scale != 1.0f)
+            for (int s = 0; s < k; s++) wt[s] *= scale;
+    }
+}
+
+/* The host MoE loop (src/engine.cpp:12360-12700): for each expert in
+ * ascending id, gather the rows that selected it (token-then-slot order),
+ * gate and up gemm, silu_mul (src/backend_cpu.cpp:2369-2410), down gemm, then
+ * scatter_axpy_rows (src/backend_cpu.cpp:3193-3217): dst += a * src, which the
+ * reference build contracts to one FMA per element (a plain add when a==1,
+ * the same value).  The destination starts at zero. */
+void orc_moe_ffn(float *out, const float *x, const void *const *gate,
+                 const void *const *up, const void *const *down, int wt_gate,
+                 int wt_up, int wt_down, const int32_t *ids, const float *wts,
+                 int64_t n_tok, int64_t n_embd, int64_t n_ff, int n_expert,
+                 int k, int nthreads) {
+    memset(out, 0, (size_t)(n_tok * n_embd) * sizeof(float));
+    int64_t cap = n_tok * k;
+    int32_t *rows = (int32_t *)malloc((size_t)cap * sizeof(int32_t));
+    float *alpha = (float *)malloc((size_t)cap * sizeof(float));
+    float *xg = (float *)malloc((size_t)(cap * n_embd) * sizeof(float));
+    float *g = (float *)malloc((size_t)(cap * n_ff) * sizeof(float));
+    float *u = (float *)malloc((size_t)(cap * n_ff) * sizeof(float));
+    float *mid = (float *)malloc((size_t)(cap * n_ff) * sizeof(float));
+    float *dn = (float *)malloc((size_t)(cap * n_embd) * sizeof(float));
+    for (int e = 0; e < n_expert; e++) {
+        int64_t m = 0;
+        for (int64_t t = 0; t < n_tok; t++)
+            for (int s = 0; s < k; s++)
+                if (ids[t * k + s] == e) {
+                    rows[m] = (int32_t)t;
+                    alpha[m] = wts[t * k + s];
+                    m++;
+                }
+        if (m == 0) continue;
+        for (int64_t i = 0; i < m; i++)
+            memcpy(xg + i * n_embd, x + (int64_t)rows[i] * n_embd,
+                   (size_t)n_embd * sizeof(float));
+        orc_gemm(g, xg, gate[e], wt_gate, n_ff, n_embd, m, nthreads);
+        orc_gemm(u, xg, up[e], wt_up, n_ff, n_embd, m, nthreads);
+        orc_silu_mul(mid, g, u, m * n_ff);
+        orc_gemm(dn, mid, down[e], wt_down, n_embd, n_ff, m, nthreads);
+        for (int64_t i = 0; i < m; i++) {
+            float *dr = out + (int64_t)rows[i] * n_embd;
+            const float *sr = dn + i * n_embd;
+            float a = alpha[i];
+            for (int64_t j = 0; j < n_embd; j++) dr[j] = fmaf(a, sr[j], dr[j]);
+        }
+    }
+    free(rows); free(alpha); free(xg); free(g); free(u); free(mid); free(dn);
+}
+
+/* ---- tools/make_bench_gguf.py:191-202 (quantize_q8_0), the repo's own q8_0
+ * fixture generator.  Python floats are f64: amax = max|v| (1e-8 for an all-
+ * zero block), d = amax / 127.0, q = clamp(round_half_even(v / d), +-127),
+ * scale stored with struct.pack('<e', d) -- f64 rounded once to f16, RNE. */
+static uint16_t f64_to_f16_rne(double v) {
+    /* Exact for every finite double: scale into the f16 grid with ldexp and
+     * let nearbyint (round-half-even) pick the neighbour. */
+    uint16_t sign = signbit(v) ? 0x8000u : 0;
+    double a = fabs(v);
+    if (isnan(v)) return 0x7E00u;
+    if (a >= 65520.0) return (uint16_t)(sign | 0x7C00u);
+    int e;
+    frexp(a, &e);           /* a = f * 2^e, f in [0.5, 1) */
+    int ue = e - 1;         /* unbiased exponent */
+    if (ue < -14) ue = -14; /* subnormal grid */
+    double q = nearbyint(ldexp(a, 10 - ue));   /* units of 2^(ue-10) */
+    if (q >= 2048.0) { q /= 2; ue++; }
+    if (ue > 15) return (uint16_t)(sign | 0x7C00u);
+    uint32_t qi = (uint32_t)q;
+    if (qi < 1024) return (uint16_t)(sign | qi);          /* subnormal */
+    return (uint16_t)(sign | ((uint32_t)(ue + 15) << 10) | (qi - 1024));
+}
+
+void orc_quantize_q8_0_weights(const float *v, int64_t n, uint8_t *dst) {
+    for (int64_t b = 0; b < n; b += 32, dst += 34) {
+        double amax = 0.0;
+        for (int i = 0; i < 32; i++) {
+            double a = fabs((double)v[b + i]);
+            amax = a > amax ? a : amax;
+        }
+        if (amax == 0.0) amax = 1e-8;
+        double d = amax / 127.0;
+        uint16_t h = f64_to_f16_rne(d);
+        dst[0] = (uint8_t)(h & 0xFF);
+        dst[1] = (uint8_t)(h >> 8);
+        for (int i = 0; i < 32; i++) {
+            double q = nearbyint((double)v[b + i] / d);
+            if (q < -127) q = -127;
+            if (q > 127) q = 127;
+            dst[2 + i] = (uint8_t)(int8_t)q;
+        }
+    }
+}

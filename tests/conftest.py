@@ -1,0 +1,54 @@
+"""Shared test setup: the `gpu` marker, repo-root imports, seeded inputs."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a real MI355X (runs the HIP library)")
+
+
+@pytest.fixture(scope="session")
+def orc():
+    import oracle
+    oracle.build()
+    return oracle
+
+
+@pytest.fixture(scope="session")
+def krk():
+    import kraken_amd
+    kraken_amd.lib()  # raises if the library was not built
+    return kraken_amd
+
+
+def rand_blocks(rng, dt, n_blocks):
+    """Random block bytes with finite f16 scale fields (every code pattern)."""
+    import oracle
+    bb = {oracle.Q4_0: 18, oracle.Q8_0: 34, oracle.Q4_K: 144, oracle.Q6_K: 210}[dt]
+    w = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
+
+    def setf16(off, scale):
+        v = (rng.standard_normal(n_blocks) * scale).astype(np.float16).view(np.uint16)
+        w[:, off] = v & 0xFF
+        w[:, off + 1] = v >> 8
+
+    if dt in (oracle.Q4_0, oracle.Q8_0):
+        setf16(0, 0.01)
+    elif dt == oracle.Q4_K:
+        setf16(0, 0.01)
+        setf16(2, 0.01)
+    else:
+        setf16(208, 0.01)
+    return w.reshape(-1)
+
+
+@pytest.fixture
+def rng():
+    return np.random.default_rng(20261201)

@@ -1,0 +1,74 @@
+"""Writes tests/golden/quant_golden.npz from the REFERENCE's own host quant
+code (oracle/_ref/libkrk_ref.so, compiled by oracle/Makefile from
+/root/reference/src/quant.cpp + src/common.cpp).
+
+The fixture is data only: seeded block bytes and activations (inputs) and
+the reference's outputs for them (dequant_row f32, dequant_row_f16,
+vec_dot in the strict scalar tier, quantize_q8_row, dot_q8_0_q8_scalar).
+It lets the oracle be checked bit for bit where the reference tree is absent
+(the GPU box).  Run:  python tests/golden/make_golden.py
+"""
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+import oracle  # noqa: E402
+from conftest import rand_blocks  # noqa: E402
+
+OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "quant_golden.npz")
+
+
+def main():
+    oracle.build()
+    ref = oracle.ref()
+    if ref is None:
+        raise SystemExit("oracle/_ref/libkrk_ref.so is not built (needs /root/reference)")
+    p = oracle._p
+    rng = np.random.default_rng(0x5EED)
+    data = {}
+    for dt, name in ((oracle.Q4_0, "q4_0"), (oracle.Q8_0, "q8_0"), (oracle.Q4_K, "q4_k"),
+                     (oracle.Q6_K, "q6_k")):
+        bs = ref.ref_block_size(dt)
+        nb = 2048 // bs
+        n = nb * bs
+        w = rand_blocks(rng, dt, nb)
+        x = rng.standard_normal(n).astype(np.float32)
+        deq = np.empty(n, np.float32)
+        ref.ref_dequant_row(dt, p(w), p(deq), n)
+        h = np.empty(n, np.uint16)
+        ref.ref_dequant_row_f16(dt, p(w), p(h), n)
+        dots = np.empty(8, np.float32)
+        for i in range(8):  # prefixes of growing length pin the chain order
+            m = n * (i + 1) // 8 // bs * bs
+            dots[i] = ref.ref_vec_dot(dt, p(w), p(x), m)
+        data[f"{name}_w"] = w
+        data[f"{name}_x"] = x
+        data[f"{name}_deq"] = deq
+        data[f"{name}_deq_f16"] = h
+        data[f"{name}_dot"] = dots
+    # int8 activation path
+    x = (rng.standard_normal(2048) * 3).astype(np.float32)
+    x[:6] = [1e30, -1e30, 1e-30, 0.0, 3.5, -0.001]
+    x[64:96] = 0.0  # an all-zero block
+    xq = np.empty(2048, np.int8)
+    dx = np.empty(64, np.float32)
+    ref.ref_quantize_q8_row(p(x), 2048, p(xq), p(dx))
+    w = rand_blocks(rng, oracle.Q8_0, 64)
+    x2 = rng.standard_normal(2048).astype(np.float32)
+    xq2 = np.empty(2048, np.int8)
+    dx2 = np.empty(64, np.float32)
+    ref.ref_quantize_q8_row(p(x2), 2048, p(xq2), p(dx2))
+    d8 = np.float32(ref.ref_dot_q8_0_q8_scalar(p(w), p(xq2), p(dx2), 2048))
+    data.update(q8act_x=x, q8act_xq=xq, q8act_dx=dx, q8dot_w=w, q8dot_x=x2,
+                q8dot_out=np.array([d8], np.float32))
+    np.savez_compressed(OUT, **data)
+    print("wrote", OUT, sum(v.nbytes for v in data.values()), "bytes")
+
+
+if __name__ == "__main__":
+    main()

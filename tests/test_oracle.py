@@ -1,0 +1,323 @@
+"""Pins the CPU oracle (oracle/krk_oracle.c) before anything is checked
+against it: the reference's own known-answer tests, closed forms and brute
+force, the committed golden vectors written by the reference's own code, and
+-- where oracle/_ref was built -- the reference itself, bit for bit."""
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import rand_blocks
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz")
+FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K]
+
+
+def f16bytes(v):
+    h = np.float16(v).view(np.uint16)
+    return [int(h) & 0xFF, int(h) >> 8]
+
+
+# ------------------------------------------- reference known-answer tests --
+def test_quant_geometry():  # tests/test_kraken.cpp:396-454
+    L = O.lib()
+    assert L.orc_block_size(O.Q4_0) == 32 and L.orc_block_bytes(O.Q4_0) == 18
+    assert L.orc_block_size(O.Q6_K) == 256 and L.orc_block_bytes(O.Q6_K) == 210
+    assert L.orc_block_size(O.Q4_K) == 256 and L.orc_block_bytes(O.Q4_K) == 144
+    assert L.orc_block_size(O.Q8_0) == 32 and L.orc_block_bytes(O.Q8_0) == 34
+    assert O.row_bytes(O.Q8_0, 64) == 68
+    assert O.row_bytes(O.Q4_K, 4096) == 2304 and O.row_bytes(O.Q4_K, 14336) == 8064
+    assert O.row_bytes(O.Q6_K, 4096) == 3360 and O.row_bytes(O.Q8_0, 4096) == 4352
+
+
+def test_q4_0_layout():  # tests/test_kraken.cpp:456-469
+    blk = np.array(f16bytes(1.0) + [i | (i << 4) for i in range(16)], np.uint8)
+    out = O.dequant(O.Q4_0, blk, 1, 32)[0]
+    assert np.array_equal(out[:16], np.arange(16) - 8.0)
+    assert np.array_equal(out[16:], np.arange(16) - 8.0)
+
+
+def test_q8_0_layout():  # tests/test_kraken.cpp:563-573
+    blk = np.array(f16bytes(0.5) + [(i - 16) & 0xFF for i in range(32)], np.uint8)
+    out = O.dequant(O.Q8_0, blk, 1, 32)[0]
+    assert np.array_equal(out, 0.5 * (np.arange(32) - 16.0))
+
+
+def test_kquant_roundtrip_shape():  # tests/test_kraken.cpp:981-1001, made exact
+    blk = np.array(f16bytes(0.5) + f16bytes(0.25) + [1] * 12 + [0x88] * 128, np.uint8)
+    out = O.dequant(O.Q4_K, blk, 1, 256)[0]
+    # sub-blocks 0..3: sc = m = 1 -> 0.5*8 - 0.25 = 3.75; sub-blocks 4..7 take
+    # sc from the low nibble of bytes 8..11 (1) and m from their high nibble
+    # and byte j's top bits (0) -> 4.0
+    assert np.all(out[:128] == 3.75) and np.all(out[128:] == 4.0)
+    assert abs(out.sum()) < 256 * 8
+
+
+def test_q6_k_group_stride():  # tests/test_kraken.cpp:1026-1042
+    blk = np.zeros(210, np.uint8)
+    blk[208:210] = f16bytes(1.0)
+    blk[192:208] = 1
+    blk[128 + 32] = 0x03
+    out = O.dequant(O.Q6_K, blk, 1, 256)[0]
+    assert out[0] == -32 and out[128] == 16 and out[160] == -32
+
+
+def test_vec_dot_f16_f32():  # tests/test_kraken.cpp:2087-2098
+    w = np.arange(1, 65, dtype=np.float32)
+    x = np.full(64, 0.5, np.float32)
+    assert O.lib().orc_vec_dot(O.F32, O._p(w), O._p(x), 64) == 1040.0
+    h = w.astype(np.float16)
+    assert O.lib().orc_vec_dot(O.F16, O._p(h), O._p(x), 64) == 1040.0
+
+
+def test_q8_activation_domain():  # tests/test_kraken.cpp:8143-8163
+    mag = np.array([1e30, -1e30, 1e-30, 0.0, 3.5, -0.001], np.float32)
+    x = mag[np.arange(512) % 6]
+    xq, dx = O.quantize_q8_row(x)
+    assert xq.max() == 127 and xq.min() == -127
+    assert abs(float(xq[0]) * float(dx[0]) - 1e30) <= 1e30 * 0.02
+
+
+# ------------------------------------------------- closed forms / brute force
+def _pack_q4k(d, dmin, sc, mn, q):
+    """Independent Q4_K packer (the inverse of get_scale_min_k4)."""
+    s = [0] * 12
+    for j in range(4):
+        s[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        s[j + 4] = (mn[j] & 63) | ((mn[j + 4] >> 4) << 6)
+        s[j + 8] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    qs = [q[64 * g + l] | (q[64 * g + 32 + l] << 4) for g in range(4) for l in range(32)]
+    return np.array(f16bytes(d) + f16bytes(dmin) + s + qs, np.uint8)
+
+
+def _fma32(a, b, c):
+    from fractions import Fraction
+    return np.float32(float(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))))
+
+
+def test_q4_k_closed_form_all_scale_slots():
+    rng = np.random.default_rng(7)
+    for trial in range(20):
+        sc = rng.integers(0, 64, 8)
+        mn = rng.integers(0, 64, 8)
+        q = rng.integers(0, 16, 256)
+        d, dmin = np.float16(rng.uniform(0.001, 0.05)), np.float16(rng.uniform(0.001, 0.05))
+        out = O.dequant(O.Q4_K, _pack_q4k(d, dmin, sc, mn, q), 1, 256)[0]
+        for i in range(0, 256, 7):
+            j = i // 32
+            d1 = np.float32(np.float32(d) * np.float32(sc[j]))
+            m1 = np.float32(np.float32(dmin) * np.float32(mn[j]))
+            assert out[i] == _fma32(d1, q[i], -m1), (trial, i)
+
+
+def test_q4_k_contraction_is_immaterial():
+    """d1 = d*sc is exact in f32 (11 + 6 significant bits) and so is d1*q
+    (+4 bits, 21 <= 24): fused and unfused d1*q - m1 round once, identically.
+    So the reference build's vfmsub and a plain multiply-subtract agree on
+    every Q4_K block -- checked here over the whole code space of a scale."""
+    rng = np.random.default_rng(11)
+    for _ in range(3000):
+        d, dmin = np.float16(rng.uniform(1e-4, 0.1)), np.float16(rng.uniform(1e-4, 0.1))
+        s, m, qv = int(rng.integers(0, 64)), int(rng.integers(0, 64)), int(rng.integers(0, 16))
+        d1 = np.float32(np.float32(d) * np.float32(s))
+        m1 = np.float32(np.float32(dmin) * np.float32(m))
+        assert _fma32(d1, qv, -m1) == np.float32(np.float32(d1 * np.float32(qv)) - m1)
+    sc, mn = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+    q = rng.integers(0, 16, 256)
+    d, dmin = np.float16(0.0123), np.float16(0.0456)
+    out = O.dequant(O.Q4_K, _pack_q4k(d, dmin, sc, mn, q), 1, 256)[0]
+    for i in range(256):
+        j = i // 32
+        d1 = np.float32(np.float32(d) * np.float32(sc[j]))
+        m1 = np.float32(np.float32(dmin) * np.float32(mn[j]))
+        assert out[i] == np.float32(np.float32(d1 * np.float32(q[i])) - m1)
+
+
+def test_q6_k_closed_form():
+    rng = np.random.default_rng(3)
+    blk = rand_blocks(rng, O.Q6_K, 1)
+    out = O.dequant(O.Q6_K, blk, 1, 256)[0]
+    ql, qh, sc = blk[:128], blk[128:192], blk[192:208].view(np.int8)
+    d = np.float32(blk[208:210].view(np.float16)[0])
+    for i in range(256):
+        h, r = divmod(i, 128)
+        qd, l = divmod(r, 32)
+        lo = ql[64 * h + l + 32 * (qd & 1)]
+        nib = (lo >> 4) if qd >= 2 else (lo & 15)
+        q = int(nib) | (((int(qh[32 * h + l]) >> (2 * qd)) & 3) << 4)
+        want = np.float32(np.float32(d * np.float32(sc[8 * h + l // 16 + 2 * qd])) * np.float32(q - 32))
+        assert out[i] == want, i
+
+
+def test_vec_dot_is_one_unfused_chain():
+    """The strict tier: sum += round(w*x), in index order (pinned against the
+    reference build, see test_oracle_matches_reference_build)."""
+    rng = np.random.default_rng(5)
+    for dt in FMTS:
+        bs = O.lib().orc_block_size(dt)
+        w = rand_blocks(rng, dt, 1024 // bs)
+        x = rng.standard_normal(1024).astype(np.float32)
+        v = O.dequant(dt, w, 1, 1024)[0]
+        s = np.float32(0)
+        for a, b in zip(v, x):
+            s = np.float32(s + np.float32(a * b))
+        assert O.vec_dot(dt, w, x) == s
+        exact = float(np.dot(v.astype(np.float64), x.astype(np.float64)))
+        assert abs(float(s) - exact) <= 1e-5 * float(np.abs(v.astype(np.float64) * x).sum())
+
+
+def test_quantize_q8_row_closed_form():
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(4096) * 2).astype(np.float32)
+    x[32:64] = 0
+    xq, dx = O.quantize_q8_row(x)
+    for b in range(128):
+        blk = x[32 * b:32 * b + 32]
+        amax = np.float32(np.abs(blk).max())
+        d = np.float32(amax / np.float32(127)) if amax > 0 else np.float32(0)
+        assert dx[b] == d
+        if d == 0:
+            assert not xq[32 * b:32 * b + 32].any()
+            continue
+        inv = np.float32(np.float32(1) / d)
+        q = np.clip(np.rint(blk * inv), -127, 127).astype(np.int8)
+        assert np.array_equal(xq[32 * b:32 * b + 32], q)
+
+
+def test_dot_q8_0_q8_closed_form():
+    rng = np.random.default_rng(13)
+    w = rand_blocks(rng, O.Q8_0, 64)
+    xq, dx = O.quantize_q8_row(rng.standard_normal(2048).astype(np.float32))
+    acc = np.float32(0)
+    wb = w.reshape(64, 34)
+    for b in range(64):
+        d = np.float32(wb[b, :2].view(np.float16)[0])
+        s = int(np.dot(wb[b, 2:].view(np.int8).astype(np.int64),
+                       xq[32 * b:32 * b + 32].astype(np.int64)))
+        acc = _fma32(np.float32(s), np.float32(d * dx[b]), acc)
+    assert O.dot_q8_0_q8(w, xq, dx) == acc
+
+
+def test_router_closed_form():
+    rng = np.random.default_rng(17)
+    logits = rng.standard_normal((6, 128)).astype(np.float32)
+    logits[0, 5] = logits[0, 9] = 9.0  # an exact tie: lower id first
+    p = O.router_softmax(logits)
+    ref = np.exp(logits.astype(np.float64) - logits.max(1, keepdims=True))
+    ref /= ref.sum(1, keepdims=True)
+    assert np.allclose(p, ref, rtol=2e-6, atol=1e-9)
+    ids, wts = O.router_topk(p, 8)
+    assert ids[0, 0] == 5 and ids[0, 1] == 9
+    for r in range(6):
+        order = sorted(range(128), key=lambda e: (-p[r, e], e))[:8]
+        assert list(ids[r]) == order
+        sel = p[r, order].astype(np.float32)
+        ks = np.float32(0)
+        for v in sel:
+            ks = np.float32(ks + v)
+        assert np.array_equal(wts[r], sel * np.float32(np.float32(1) / ks))
+
+
+def test_moe_matches_dense_twin(krk):
+    """One expert at weight 1.0 is the dense FFN (test_kraken.cpp:15328 idea);
+    and the routed sum matches an f64 composition."""
+    rng = np.random.default_rng(19)
+    ne, E, F, T, k = 4, 256, 512, 3, 2
+    mats = {}
+    for e in range(ne):
+        for nm, (o, i) in (("g", (F, E)), ("u", (F, E)), ("d", (E, F))):
+            v = (rng.standard_normal(o * i) * 0.02).astype(np.float32)
+            mats[nm, e] = krk.quantize(O.Q4_K, v, o, i)
+    x = rng.standard_normal((T, E)).astype(np.float32)
+    g = [mats["g", e] for e in range(ne)]
+    u = [mats["u", e] for e in range(ne)]
+    d = [mats["d", e] for e in range(ne)]
+    ids = np.array([[2, 0], [1, 3], [3, 2]], np.int32)
+    one = O.moe_ffn(x, g, u, d, O.Q4_K, ids[:, :1], np.ones((T, 1), np.float32), F)
+    for t in range(T):
+        e = ids[t, 0]
+        mid = O.silu_mul(O.gemm(O.Q4_K, g[e], x[t], F), O.gemm(O.Q4_K, u[e], x[t], F))
+        assert np.array_equal(one[t], O.gemm(O.Q4_K, d[e], mid, E)[0])
+    wts = np.array([[0.7, 0.3], [0.5, 0.5], [0.9, 0.1]], np.float32)
+    out = O.moe_ffn(x, g, u, d, O.Q4_K, ids, wts, F)
+    deq = {key: O.dequant(O.Q4_K, v, *((F, E) if key[0] != "d" else (E, F))).astype(np.float64)
+           for key, v in mats.items()}
+    for t in range(T):
+        acc = np.zeros(E)
+        for s in range(k):
+            e = ids[t, s]
+            gg, uu = deq["g", e] @ x[t], deq["u", e] @ x[t]
+            acc += wts[t, s] * (deq["d", e] @ (gg / (1 + np.exp(-gg)) * uu))
+        assert np.linalg.norm(out[t] - acc) <= 1e-5 * np.linalg.norm(acc)
+
+
+def test_q8_0_fixture_quantizer_matches_python_rule():
+    """tools/make_bench_gguf.py:191-202 restated with Python's own float
+    semantics (f64, round-half-even, struct '<e')."""
+    rng = np.random.default_rng(23)
+    v = (rng.standard_normal(32 * 40) * 0.02).astype(np.float32)
+    v[32:64] = 0.0
+    v[64] = 0.5 * np.float32(1e-3)
+    got = O.quantize_q8_0_weights(v)
+    want = bytearray()
+    for b in range(0, v.size, 32):
+        blk = [float(t) for t in v[b:b + 32]]
+        amax = max(abs(t) for t in blk) or 1e-8
+        d = amax / 127.0
+        want += struct.pack("<e", d)
+        for t in blk:
+            want += struct.pack("<b", max(-127, min(127, int(round(t / d)))))
+    assert bytes(got) == bytes(want)
+
+
+# ------------------------------------------------------------- golden vectors
+def test_oracle_matches_golden_vectors():
+    g = np.load(GOLDEN)
+    for dt, name in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k"), (O.Q6_K, "q6_k")):
+        w, x = g[f"{name}_w"], g[f"{name}_x"]
+        n = x.size
+        deq = O.dequant(dt, w, 1, n)[0]
+        assert np.array_equal(deq.view(np.uint32), g[f"{name}_deq"].view(np.uint32)), name
+        assert np.array_equal(O.dequant_f16(dt, w, 1, n)[0], g[f"{name}_deq_f16"]), name
+        bs = O.lib().orc_block_size(dt)
+        for i in range(8):
+            m = n * (i + 1) // 8 // bs * bs
+            got = np.float32(O.lib().orc_vec_dot(dt, O._p(w), O._p(x), m))
+            assert got == g[f"{name}_dot"][i], (name, i)
+    xq, dx = O.quantize_q8_row(g["q8act_x"])
+    assert np.array_equal(xq, g["q8act_xq"]) and np.array_equal(dx, g["q8act_dx"])
+    xq2, dx2 = O.quantize_q8_row(g["q8dot_x"])
+    assert np.float32(O.dot_q8_0_q8(g["q8dot_w"], xq2, dx2)) == g["q8dot_out"][0]
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (no reference tree)")
+def test_oracle_matches_reference_build():
+    ref = O.ref()
+    rng = np.random.default_rng(29)
+    for dt in FMTS:
+        bs = O.lib().orc_block_size(dt)
+        for trial in range(4):
+            nb = 4096 // bs
+            w = rand_blocks(rng, dt, nb)
+            x = rng.standard_normal(nb * bs).astype(np.float32)
+            a = O.dequant(dt, w, 1, nb * bs)[0]
+            b = np.empty_like(a)
+            ref.ref_dequant_row(dt, O._p(w), O._p(b), nb * bs)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+            assert np.float32(O.vec_dot(dt, w, x)) == np.float32(
+                ref.ref_vec_dot(dt, O._p(w), O._p(x), nb * bs))
+            h = np.empty(nb * bs, np.uint16)
+            ref.ref_dequant_row_f16(dt, O._p(w), O._p(h), nb * bs)
+            assert np.array_equal(O.dequant_f16(dt, w, 1, nb * bs)[0], h)
+    x = (rng.standard_normal(8192) * 5).astype(np.float32)
+    xq, dx = O.quantize_q8_row(x)
+    xq2, dx2 = np.empty_like(xq), np.empty_like(dx)
+    ref.ref_quantize_q8_row(O._p(x), 8192, O._p(xq2), O._p(dx2))
+    assert np.array_equal(xq, xq2) and np.array_equal(dx, dx2)
+    w = rand_blocks(rng, O.Q8_0, 256)
+    assert np.float32(O.dot_q8_0_q8(w, xq, dx)) == np.float32(
+        ref.ref_dot_q8_0_q8_scalar(O._p(w), O._p(xq), O._p(dx), 8192))
+    for f in (0.5, 1.0 + 2.0 ** -11, 65504.0, 1e-7, 3.0e-5, -2.5):
+        assert O.lib().orc_fp32_to_fp16(f) == ref.ref_fp32_to_fp16(f)
