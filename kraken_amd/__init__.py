@@ -76,6 +76,12 @@ def lib():
         if not os.path.exists(LIB_PATH):
             raise KrkError(f"{LIB_PATH} is missing: run kraken_amd/build.py "
                            "(or __graft_entry__.build()) first")
+        # torch ships its own copy of the HIP runtime (soname libamdhip64.so.7,
+        # file name libamdhip64.so).  Loading torch first makes this library
+        # bind to that same copy, so the process holds ONE runtime and torch's
+        # streams and allocations are valid here; the other order would load
+        # two runtimes side by side.
+        import torch  # noqa: F401
         L = C.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)

@@ -22,9 +22,17 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t *__restrict_
     dequant_chunk<DT>(blk, static_cast<int>(c % CPB), y);
     const int64_t o = r * n_in + c * 32;
     if constexpr (F16) {
-        _Float16 *oh = static_cast<_Float16 *>(out) + o;
+        // IEEE RNE to f16, with the sign of a zero kept: gfx950's packed
+        // f32->f16 conversion returns +0 for -0, and the f32 values here are
+        // the host decoder's bits, signed zeros included.
+        uint16_t *oh = static_cast<uint16_t *>(out) + o;
 #pragma unroll
-        for (int i = 0; i < 32; i++) oh[i] = static_cast<_Float16>(y[i]);
+        for (int i = 0; i < 32; i++) {
+            const _Float16 h = static_cast<_Float16>(y[i]);
+            uint16_t hb;
+            __builtin_memcpy(&hb, &h, 2);
+            oh[i] = static_cast<uint16_t>(hb | ((__float_as_uint(y[i]) >> 16) & 0x8000u));
+        }
     } else {
         float *of = static_cast<float *>(out) + o;
 #pragma unroll

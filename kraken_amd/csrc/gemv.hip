@@ -22,6 +22,8 @@
 //     in one transposed butterfly (wave_reduce_multi), and the waves' partials
 //     are added in wave order through LDS.  No atomics: the result is
 //     deterministic for a given shape.
+#include <cstdlib>
+
 #include "gemv_core.hpp"
 
 namespace krk {
@@ -98,7 +100,1211 @@ __global__ void __launch_bounds__(512) gemv_seg_kernel(SegTable t) {
     }
 }
 
+// Rows per group of the decode GEMV (KRK_GEMV_RB = 2 | 4 | 8, default 4).
+static int gemv_rb_knob() {
+    static const int v = [] {
+        const char *e = std::getenv("KRK_GEMV_RB");
+        return e ? std::atoi(e) : 4;
+    }();
+    return v;
+}
+
+static int gemv_mfma_knob() {
+    static const int v = [] {
+        const char *e = std::getenv("KRK_GEMV_MFMA");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v;
+}
+static int gemv_stream_knob() {
+    static const int v = [] {
+        const char *e = std::getenv("KRK_GEMV_STREAM");
+        return e ? std::atoi(e) : 1;
+    }();
+    return v;
+}
+static int gemv_lds_knob() {
+    static const int v = [] {
+        const char *e = std::getenv("KRK_GEMV_LDS");
+        return e ? std::atoi(e) : 1;
+    }();
+    return v;
+}
+static int gemv_wave_knob() {
+    static const int v = [] {
+        const char *e = std::getenv("KRK_GEMV_WAVE");
+        return e ? std::atoi(e) : 1;
+    }();
+    return v;
+}
+static int gemv_spw_knob() {
+    static const int v = [] {
+        const char *e = std::getenv("KRK_GEMV_SPW");
+        return e ? std::atoi(e) : 2;
+    }();
+    return v;
+}
+
+// --------------------------------------------------- persistent decode GEMV --
+// rows == 1: a fixed grid of workgroups (as many as the chip keeps resident)
+// walks all row groups of all segments.  Each wave loads its 2048-value step
+// of x ONCE into registers for the whole kernel (the non-persistent form
+// re-read x -- 16 KB at K = 4096 -- for every 4..8 weight rows, more bytes
+// than the weights themselves), and the next group's weight pieces are in
+// flight while the current group is decoded and reduced.
+template <int DT, typename XT, typename OT, int RB>
+__global__ void __launch_bounds__(512) gemv_persist_kernel(SegTable t, int64_t total) {
+    using F = LaneFmt<DT>;
+    constexpr int BV = blk_vals(DT), BB = blk_bytes(DT);
+    constexpr int BPS = kWave / F::LPB;
+    constexpr int H = RB / 2;
+    __shared__ float red[2][8][RB];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int p = lane % F::LPB;
+    const int b = wv * BPS + lane / F::LPB;  // this lane's block (one step per wave)
+    const int nb = t.n_in / BV;
+    const bool active = b < nb;
+
+    // (segment, first row) of a global group index
+    auto locate = [&](int64_t g, int &si, int64_t &n0) {
+        si = 0;
+        while (si + 1 < t.n && g >= t.seg[si + 1].blk_begin) si++;
+        n0 = (g - t.seg[si].blk_begin) * (t.seg[si].kind == SEG_SILU ? H : RB);
+    };
+    auto fetch = [&](uint32_t (&raw)[RB][F::NRAW], int si, int64_t n0) {
+        const Seg &s = t.seg[si];
+        const bool pair = s.kind == SEG_SILU;
+        const uint8_t *w = static_cast<const uint8_t *>(s.w);
+        const uint8_t *w2 = static_cast<const uint8_t *>(s.w2);
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            int64_t n = n0 + (pair ? (r % H) : r);
+            if (n >= s.n_out) n = s.n_out - 1;
+            const uint8_t *wb = (pair && r >= H) ? w2 : w;
+            F::load(raw[r], wb + n * t.row_bytes + static_cast<int64_t>(b) * BB, p);
+        }
+    };
+
+    float xv[32], xs[F::NG];
+    const void *xcur = nullptr;
+    uint32_t rawA[RB][F::NRAW], rawB[RB][F::NRAW];
+    int64_t g = blockIdx.x;
+    int si;
+    int64_t n0;
+    if (g < total) {
+        locate(g, si, n0);
+        if (active) fetch(rawA, si, n0);
+    }
+    int par = 0;
+    for (; g < total; g += gridDim.x, par ^= 1) {
+        const Seg &s = t.seg[si];
+        // next group's bytes travel while this one is decoded
+        const int64_t gn = g + gridDim.x;
+        int sn = si;
+        int64_t nn = 0;
+        if (gn < total) {
+            locate(gn, sn, nn);
+            if (active) fetch(rawB, sn, nn);
+        }
+        if (s.x != xcur) {  // once per workgroup unless segments read different x
+            xcur = s.x;
+            if (active) {
+                const XT *xb = static_cast<const XT *>(s.x) + static_cast<int64_t>(b) * BV;
+#pragma unroll
+                for (int r = 0; r < F::NRUN; r++) load_run<F::RUN>(xb + F::run_start(p, r), &xv[r * F::RUN]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 32; i++) xv[i] = 0.0f;
+            }
+#pragma unroll
+            for (int q = 0; q < F::NG; q++) xs[q] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; i++) xs[F::group_of(i)] += xv[i];
+        }
+        float v[RB];
+#pragma unroll
+        for (int r = 0; r < RB; r++) v[r] = active ? F::dot(rawA[r], p, xv, xs) : 0.0f;
+        wave_reduce_multi<RB>(v, lane);
+        if (reduce_owner<RB>(lane)) red[par][wv][reduce_owner_index<RB>(lane)] = v[0];
+        __syncthreads();
+        const int tid = threadIdx.x;
+        const int kind = s.kind;
+        OT *out = static_cast<OT *>(s.out);
+        if (kind != SEG_SILU) {
+            if (tid < RB) {
+                float sum = 0.0f;
+                for (int k = 0; k < nw; k++) sum += red[par][k][tid];
+                const int64_t n = n0 + tid;
+                const float inv = (kind == SEG_ACC && t.rexp) ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
+                if (n < s.n_out) store_out<OT>(out + n, sum, kind, inv);
+            }
+        } else if (tid < H) {
+            float gs = 0.0f, us = 0.0f;
+            for (int k = 0; k < nw; k++) {
+                gs += red[par][k][tid];
+                us += red[par][k][H + tid];
+            }
+            const int64_t n = n0 + tid;
+            if (n < s.n_out) {
+                if constexpr (sizeof(OT) == 2) {
+                    const float hg = static_cast<float>(static_cast<_Float16>(gs));
+                    const float hu = static_cast<float>(static_cast<_Float16>(us));
+                    out[n] = sat_f16(silu_f(hg) * hu);
+                } else {
+                    out[n] = (gs / (1.0f + expf(-gs))) * us;
+                }
+            }
+        }
+        // red[par] is rewritten two groups later; the barrier of the next
+        // group orders those writes after these reads.
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int k = 0; k < F::NRAW; k++) rawA[r][k] = rawB[r][k];
+        si = sn;
+        n0 = nn;
+    }
+}
+
+// ------------------------------------------------------ MFMA decode GEMV ----
+// Q4_K, rows == 1, K <= 8192: the multiply-adds run on the matrix cores.
+//
+// v_mfma_f32_16x16x32_f16 computes C[16][16] += A[16][32] . B[32][16] with
+//   A lane l: row l%16, k = 8*(l/16) + 0..7     (verified on gfx950)
+//   B lane l: col l%16, k = 8*(l/16) + 0..7
+//   C lane l: col l%16, rows 4*(l/16) + 0..3
+// One MFMA covers one 32-value sub-block s of 16 weight rows:
+//   B[k][j]  = nibble code of row j (the code c placed at bits 4..7 of a
+//              16-bit lane is the exact f16 subnormal c * 2^-20),
+//   A[i][k]  = x_h[k] if i/2 == s else 0, h = i%2, x = x_0 + x_1 split into
+//              two f16 (x_0 = f16(x), x_1 = f16(x - x_0): ~22 bits of x),
+// so the eight MFMAs of a super-block all accumulate into ONE C whose row
+// i = (s, h) holds sum_k c_jk * x_h,k for sub-block s: lane (j, g) ends up
+// with exactly the two sub-blocks 2g, 2g+1 of row j whose scales it decodes.
+// A is block-diagonal and the same for every row, so each wave builds it
+// once (32 VGPRs per super-block it owns) and then streams weight rows.
+// VALU per weight: ~7 ops per 8 codes for the masks plus ~0.3 for the scale
+// fold -- a third of the fma_mix path.
+__device__ __forceinline__ void q4k_pair_scales(const uint32_t (&h)[4], int g, float &sc0,
+                                                float &mn0, float &sc1, float &mn1) {
+    // sub-blocks 2g, 2g+1 (get_scale_min_k4, quant.cpp:427-435), branch-free
+    const float d = h2f(h[0] & 0xFFFF), dmin = h2f(h[0] >> 16);
+    const uint32_t sh = 16u * static_cast<uint32_t>(g & 1);
+    const uint32_t Y = h[1] >> sh, Z = h[2] >> sh, W = h[3] >> sh;
+    const bool hi = g >= 2;
+    const uint32_t A = hi ? W : Y, Am = hi ? (W >> 4) : Z;
+    const uint32_t s2 = hi ? 2u : 0u;
+    const uint32_t sa = (A & 15u) | ((Y >> s2) & 0x30u);
+    const uint32_t sb = ((A >> 8) & 15u) | ((Y >> (8u + s2)) & 0x30u);
+    const uint32_t ma = (Am & 15u) | ((Z >> s2) & 0x30u);
+    const uint32_t mb = ((Am >> 8) & 15u) | ((Z >> (8u + s2)) & 0x30u);
+    sc0 = d * static_cast<float>(sa);
+    sc1 = d * static_cast<float>(sb);
+    mn0 = dmin * static_cast<float>(ma);
+    mn1 = dmin * static_cast<float>(mb);
+}
+
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+template <typename XT, typename OT, int SPW>
+__global__ void __launch_bounds__(SPW == 1 ? 1024 : 512) gemv_mfma_q4k_kernel(SegTable t, int64_t total) {
+    constexpr int RG = 16;
+    constexpr float kTwo20 = 1048576.0f;
+    __shared__ float red[2][16][RG];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int j = lane & 15, g = lane >> 4;
+    const int nb = t.n_in / 256;
+    constexpr uint32_t M = 0x00F000F0u;
+
+    auto locate = [&](int64_t gi, int &si, int64_t &n0) {
+        si = 0;
+        while (si + 1 < t.n && gi >= t.seg[si + 1].blk_begin) si++;
+        n0 = (gi - t.seg[si].blk_begin) * (t.seg[si].kind == SEG_SILU ? RG / 2 : RG);
+    };
+    // lane's raw bytes of its row j: 4 x 8 B of nibbles + the 16 B header
+    auto fetch = [&](u32x2 (&q)[SPW][4], uint32_t (&h)[SPW][4], int si, int64_t n0) {
+        const Seg &sg = t.seg[si];
+        const bool pair = sg.kind == SEG_SILU;
+        int64_t n = n0 + (pair ? (j & 7) : j);
+        if (n >= sg.n_out) n = sg.n_out - 1;
+        const uint8_t *w = static_cast<const uint8_t *>((pair && j >= 8) ? sg.w2 : sg.w) + n * t.row_bytes;
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            int sb = wv * SPW + u;
+            if (sb >= nb) sb = nb - 1;
+            const uint8_t *blk = w + static_cast<int64_t>(sb) * 144;
+            const u32x4 hv = ld128(blk);
+            h[u][0] = hv.x; h[u][1] = hv.y; h[u][2] = hv.z; h[u][3] = hv.w;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) q[u][jj] = ld64(blk + 16 + 32 * jj + 8 * g);
+        }
+    };
+
+    half8 A[SPW][8];
+    float xs[SPW][2];
+    const void *xcur = nullptr;
+    u32x2 qA[SPW][4], qB[SPW][4];
+    uint32_t hA[SPW][4], hB[SPW][4];
+    int64_t gi = blockIdx.x;
+    int si = 0;
+    int64_t n0 = 0;
+    if (gi < total) {
+        locate(gi, si, n0);
+        fetch(qA, hA, si, n0);
+    }
+    int par = 0;
+    for (; gi < total; gi += gridDim.x, par ^= 1) {
+        const Seg &sg = t.seg[si];
+        const int64_t gn = gi + gridDim.x;
+        int sn = si;
+        int64_t nn = 0;
+        if (gn < total) {
+            locate(gn, sn, nn);
+            fetch(qB, hB, sn, nn);
+        }
+        if (sg.x != xcur) {
+            xcur = sg.x;
+            // A operands: row i = (s = i/2, h = i%2); k order matches the
+            // B halves (bytes 0,2,1,3,4,6,5,7 of the lane's 8-byte run)
+            const XT *x = static_cast<const XT *>(sg.x);
+            const int i = lane & 15, s_i = i >> 1, h_i = i & 1;
+            constexpr int kperm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+#pragma unroll
+            for (int u = 0; u < SPW; u++) {
+                const int sb = wv * SPW + u;
+                const bool ok = sb < nb;
+                const int64_t base = static_cast<int64_t>(ok ? sb : 0) * 256 +
+                                     64 * (s_i >> 1) + 32 * (s_i & 1) + 8 * g;
+                float xf[8];
+                load_run<8>(x + base, xf);
+                float psum = 0.0f;
+                half8 xd;
+#pragma unroll
+                for (int tt = 0; tt < 8; tt++) {
+                    const float v = ok ? xf[kperm[tt]] : 0.0f;
+                    psum += v;
+                    const _Float16 x0 = static_cast<_Float16>(v);
+                    xd[tt] = h_i == 0 ? x0 : static_cast<_Float16>(v - static_cast<float>(x0));
+                }
+#pragma unroll
+                for (int s = 0; s < 8; s++) {
+                    half8 a;
+#pragma unroll
+                    for (int tt = 0; tt < 8; tt++) a[tt] = s == s_i ? xd[tt] : static_cast<_Float16>(0.0f);
+                    A[u][s] = a;
+                }
+                // sub-block sums: lanes (i, g') cover sub-block s_i in 4 runs of 8
+                psum += __shfl_xor(psum, 16, 64);
+                psum += __shfl_xor(psum, 32, 64);
+                // lane (j, g) needs the sums of sub-blocks 2g and 2g+1, held by
+                // lanes i = 4g (s = 2g) and i = 4g + 2 (s = 2g + 1)
+                xs[u][0] = __shfl(psum, 4 * g, 64);
+                xs[u][1] = __shfl(psum, 4 * g + 2, 64);
+            }
+        }
+        float part = 0.0f;
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            floatx4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const uint32_t D0 = qA[u][jj].x, D1 = qA[u][jj].y;
+                const u32x4v blo = {(D0 << 4) & M, (D0 >> 4) & M, (D1 << 4) & M, (D1 >> 4) & M};
+                const u32x4v bhi = {D0 & M, (D0 >> 8) & M, D1 & M, (D1 >> 8) & M};
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u][2 * jj], __builtin_bit_cast(half8, blo), c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u][2 * jj + 1], __builtin_bit_cast(half8, bhi), c, 0, 0, 0);
+            }
+            float sc0, mn0, sc1, mn1;
+            q4k_pair_scales(hA[u], g, sc0, mn0, sc1, mn1);
+            const bool ok = wv * SPW + u < nb;
+            float v = (sc0 * kTwo20) * (c[0] + c[1]);
+            v = __builtin_fmaf(sc1 * kTwo20, c[2] + c[3], v);
+            v = __builtin_fmaf(-mn0, xs[u][0], v);
+            v = __builtin_fmaf(-mn1, xs[u][1], v);
+            part += ok ? v : 0.0f;
+        }
+        part += __shfl_xor(part, 16, 64);
+        part += __shfl_xor(part, 32, 64);
+        if (lane < 16) red[par][wv][lane] = part;
+        __syncthreads();
+        const int tid = threadIdx.x;
+        const int kind = sg.kind;
+        OT *out = static_cast<OT *>(sg.out);
+        if (kind != SEG_SILU) {
+            if (tid < RG) {
+                float sum = 0.0f;
+                for (int k = 0; k < nw; k++) sum += red[par][k][tid];
+                const int64_t n = n0 + tid;
+                const float inv = (kind == SEG_ACC && t.rexp) ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
+                if (n < sg.n_out) store_out<OT>(out + n, sum, kind, inv);
+            }
+        } else if (tid < RG / 2) {
+            float gs = 0.0f, us = 0.0f;
+            for (int k = 0; k < nw; k++) {
+                gs += red[par][k][tid];
+                us += red[par][k][RG / 2 + tid];
+            }
+            const int64_t n = n0 + tid;
+            if (n < sg.n_out) {
+                if constexpr (sizeof(OT) == 2) {
+                    const float hg = static_cast<float>(static_cast<_Float16>(gs));
+                    const float hu = static_cast<float>(static_cast<_Float16>(us));
+                    out[n] = sat_f16(silu_f(hg) * hu);
+                } else {
+                    out[n] = (gs / (1.0f + expf(-gs))) * us;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) qA[u][jj] = qB[u][jj];
+#pragma unroll
+            for (int k = 0; k < 4; k++) hA[u][k] = hB[u][k];
+        }
+        si = sn;
+        n0 = nn;
+    }
+}
+
+template <typename XT, typename OT, int SPW>
+static hipError_t launch_mfma_q4k(SegTable t, hipStream_t st) {
+    constexpr int RG = 16;
+    int64_t total = 0;
+    for (int i = 0; i < t.n; i++) {
+        t.seg[i].blk_begin = total;
+        const int64_t per = t.seg[i].kind == SEG_SILU ? RG / 2 : RG;
+        total += (t.seg[i].n_out + per - 1) / per;
+    }
+    const int nb = t.n_in / 256;
+    const int nw = (nb + SPW - 1) / SPW;
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_mfma_q4k_kernel<XT, OT, SPW>,
+                                                     64 * nw, 0) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    int64_t grid = static_cast<int64_t>(cus) * per_cu;
+    if (grid > total) grid = total;
+    hipLaunchKernelGGL((gemv_mfma_q4k_kernel<XT, OT, SPW>), dim3(static_cast<unsigned>(grid)),
+                       dim3(64 * nw), 0, st, t, total);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------- independent-wave GEMV ----
+// rows == 1.  Every wave is its own unit of work: a lane owns 64 weights of a
+// row (WaveFmt), so one wave covers 4096 values of K with no other wave --
+// no LDS, no barrier, no cross-wave reduction.  Waves are persistent: each
+// loads its activations once (K <= 4096; longer rows re-read x per 4096-value
+// step from L1/L2) and walks groups of RB rows, with the next group's weight
+// bytes in flight while the current group is decoded.  A group's RB partial
+// sums are reduced across the wave by one transposed butterfly and written
+// by their owner lanes.
+template <int DT, typename XT, typename OT, int RB, int ABL = 0>
+__global__ void __launch_bounds__(256) gemv_wave_kernel(SegTable t, int64_t total) {
+    using F = WaveFmt<DT>;
+    constexpr int BV = blk_vals(DT), BB = blk_bytes(DT);
+    constexpr int H = RB / 2;
+    const int lane = threadIdx.x & 63;
+    const int64_t W = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int64_t NW = static_cast<int64_t>(gridDim.x) * (blockDim.x >> 6);
+    const int slot = F::slot_of(lane);
+    const int nb = t.n_in / BV;
+    const int nsteps = (nb + F::BPS - 1) / F::BPS;
+
+    auto locate = [&](int64_t g, int &si, int64_t &n0) {
+        si = 0;
+        while (si + 1 < t.n && g >= t.seg[si + 1].blk_begin) si++;
+        n0 = (g - t.seg[si].blk_begin) * (t.seg[si].kind == SEG_SILU ? H : RB);
+    };
+    auto fetch = [&](uint32_t (&raw)[RB][F::NRAW], int si, int64_t n0, int st) {
+        const Seg &s = t.seg[si];
+        const bool pair = s.kind == SEG_SILU;
+        // a lane past the row end re-reads the last block(s) and is masked
+        // out of the sum (Q4_0 / Q8_0 lanes own two blocks; K % 64 == 0 there)
+        int b = st * F::BPS + F::blk_of(lane);
+        constexpr int per_lane = (DT == DT_Q4_0 || DT == DT_Q8_0) ? 2 : 1;
+        if (b > nb - per_lane) b = nb - per_lane;
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            int64_t n = n0 + (pair ? (r % H) : r);
+            if (n >= s.n_out) n = s.n_out - 1;
+            const uint8_t *wb = static_cast<const uint8_t *>((pair && r >= H) ? s.w2 : s.w);
+            if constexpr (ABL == 2) {
+#pragma unroll
+                for (int k = 0; k < F::NRAW; k++) raw[r][k] = static_cast<uint32_t>(n * 2654435761u + k + b);
+            } else {
+                F::load(raw[r], wb + n * t.row_bytes + static_cast<int64_t>(b) * BB, slot);
+            }
+        }
+    };
+    auto load_x = [&](const void *xp, int st, float (&xv)[64], float (&xs)[F::NG]) {
+        const int b = st * F::BPS + F::blk_of(lane);
+        const bool ok = b < nb;
+        const XT *xb = static_cast<const XT *>(xp) + static_cast<int64_t>(ok ? b : 0) * BV;
+#pragma unroll
+        for (int r = 0; r < F::NRUN; r++) load_run<F::RUN>(xb + F::run_start(slot, r), &xv[r * F::RUN]);
+#pragma unroll
+        for (int q = 0; q < F::NG; q++) xs[q] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 64; i++) {
+            if (!ok) xv[i] = 0.0f;
+            xs[F::group_of(i)] += xv[i];
+        }
+    };
+
+    float xv[64], xs[F::NG];
+    const void *xcur = nullptr;
+    uint32_t rawA[RB][F::NRAW], rawB[RB][F::NRAW];
+    int64_t g = W;
+    int si = 0;
+    int64_t n0 = 0;
+    if (g < total) {
+        locate(g, si, n0);
+        fetch(rawA, si, n0, 0);
+    }
+    for (; g < total; g += NW) {
+        const Seg &s = t.seg[si];
+        float v[RB];
+#pragma unroll
+        for (int r = 0; r < RB; r++) v[r] = 0.0f;
+        const int64_t gn = g + NW;
+        int sn = si;
+        int64_t nn = 0;
+        for (int st = 0; st < nsteps; st++) {
+            if (st + 1 < nsteps) {
+                fetch(rawB, si, n0, st + 1);
+            } else if (gn < total) {  // the next group's first step
+                locate(gn, sn, nn);
+                fetch(rawB, sn, nn, 0);
+            }
+            if (nsteps > 1 || s.x != xcur) {
+                xcur = s.x;
+                load_x(s.x, st, xv, xs);
+            }
+            const bool ok = st * F::BPS + F::blk_of(lane) < nb;
+            if constexpr (DT == DT_Q4_K && ABL == 0) {
+                // code dword outer, row inner: RB x 4 independent chains
+                float acc[RB][F::NACC];
+#pragma unroll
+                for (int r = 0; r < RB; r++)
+#pragma unroll
+                    for (int q = 0; q < F::NACC; q++) acc[r][q] = 0.0f;
+#pragma unroll
+                for (int tt = 0; tt < F::NDW; tt++)
+#pragma unroll
+                    for (int r = 0; r < RB; r++) F::accum(rawA[r], tt, xv, acc[r]);
+#pragma unroll
+                for (int r = 0; r < RB; r++) {
+                    const float d = F::finish(rawA[r], slot, acc[r], xs);
+                    v[r] += ok ? d : 0.0f;
+                }
+            } else
+#pragma unroll
+            for (int r = 0; r < RB; r++) {
+                float d;
+                if constexpr (ABL == 1) {
+                    uint32_t h = 0;
+#pragma unroll
+                    for (int k = 0; k < F::NRAW; k++) h ^= rawA[r][k];
+                    d = static_cast<float>(h & 1) * xv[0];
+                } else {
+                    d = F::dot(rawA[r], slot, xv, xs);
+                }
+                v[r] += ok ? d : 0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < RB; r++)
+#pragma unroll
+                for (int k = 0; k < F::NRAW; k++) rawA[r][k] = rawB[r][k];
+        }
+        wave_reduce_multi<RB>(v, lane);
+        const int idx = reduce_owner_index<RB>(lane);
+        const int kind = s.kind;
+        OT *out = static_cast<OT *>(s.out);
+        if (kind != SEG_SILU) {
+            if (reduce_owner<RB>(lane)) {
+                const int64_t n = n0 + idx;
+                const float inv = (kind == SEG_ACC && t.rexp) ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
+                if (n < s.n_out) store_out<OT>(out + n, v[0], kind, inv);
+            }
+        } else {
+            // up row r sits with the owner of index H + r
+            constexpr int SH = 64 / RB;  // lanes per owned index
+            const float u = __shfl(v[0], (lane + H * SH) & 63, 64);
+            if (reduce_owner<RB>(lane) && idx < H) {
+                const int64_t n = n0 + idx;
+                if (n < s.n_out) {
+                    const float gs = v[0];
+                    if constexpr (sizeof(OT) == 2) {
+                        const float hg = static_cast<float>(static_cast<_Float16>(gs));
+                        const float hu = static_cast<float>(static_cast<_Float16>(u));
+                        out[n] = sat_f16(silu_f(hg) * hu);
+                    } else {
+                        out[n] = (gs / (1.0f + expf(-gs))) * u;
+                    }
+                }
+            }
+        }
+        si = sn;
+        n0 = nn;
+    }
+}
+
+template <int DT, typename XT, typename OT, int RB, int ABL = 0>
+static hipError_t launch_wave(SegTable t, hipStream_t st) {
+    int64_t total = 0;
+    for (int i = 0; i < t.n; i++) {
+        t.seg[i].blk_begin = total;
+        const int64_t per = t.seg[i].kind == SEG_SILU ? RB / 2 : RB;
+        total += (t.seg[i].n_out + per - 1) / per;
+    }
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    static int per_cu = 0;
+    if (!per_cu &&
+        (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_wave_kernel<DT, XT, OT, RB, ABL>, 256, 0) !=
+             hipSuccess || per_cu < 1))
+        per_cu = 1;
+    const int64_t waves = total;  // one wave per group at most
+    int64_t grid = static_cast<int64_t>(cus) * per_cu;
+    if (grid * 4 > waves) grid = (waves + 3) / 4;
+    hipLaunchKernelGGL((gemv_wave_kernel<DT, XT, OT, RB, ABL>), dim3(static_cast<unsigned>(grid)), dim3(256),
+                       0, st, t, total);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------- LDS-staged GEMV ----
+// rows == 1, the decode shape.  Measured on MI355X: with x held in registers,
+// every wave must pull its whole 16 KB slice of x through L2/L1 once, and
+// with the few rows per wave that latency hiding needs, that is as many
+// bytes as the weights (7x at one row per wave).  So x is staged ONCE per
+// workgroup into LDS (f32, padded 4 floats per 64 so the b128 reads of the
+// 64 lanes spread over the banks), and waves read it back in 4-value runs,
+// each run applied to RB rows.  A lane owns 64 weights of a row (WaveFmt
+// layout), a wave covers 4096 values of K with no other wave, waves are
+// persistent and independent (no barrier after the staging), and the next
+// group's weight bytes are in flight while the current group is decoded.
+__device__ __forceinline__ int xpad(int k) { return k + 4 * (k >> 6); }
+
+template <int DT> struct XRuns;  // where dword t of a lane's codes finds its x
+template <> struct XRuns<DT_Q4_K> {
+    // lane base 64*jp within the block; dword t: low run 4t, high run 32 + 4t
+    __device__ static int base(int lane) { return 256 * (lane >> 2) + 64 * (lane & 3); }
+};
+template <> struct XRuns<DT_Q6_K> {
+    __device__ static int base(int lane) {
+        const int jp = lane & 3;
+        return 256 * (lane >> 2) + 128 * (jp >> 1) + 16 * (jp & 1);
+    }
+};
+template <> struct XRuns<DT_Q4_0> {
+    __device__ static int base(int lane) { return 64 * lane; }
+};
+template <> struct XRuns<DT_Q8_0> {
+    __device__ static int base(int lane) { return 64 * lane; }
+};
+
+template <int DT, int RB> struct LdsDot;
+
+template <int RB> struct LdsDot<DT_Q4_K, RB> {
+    using F = WaveFmt<DT_Q4_K>;
+    static constexpr int NS = 2;  // x sums per lane
+    __device__ static void sums(const float *xl, int b0, float (&xs)[NS]) {
+        float a = 0.0f, c = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            const floatx4 u = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + i));
+            const floatx4 w = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 + i));
+            a += (u.x + u.y) + (u.z + u.w);
+            c += (w.x + w.y) + (w.z + w.w);
+        }
+        xs[0] = a; xs[1] = c;
+    }
+    __device__ static void run(const uint32_t (&raw)[RB][F::NRAW], int jp, const float *xl, int b0,
+                               const float (&xs)[NS], float (&v)[RB]) {
+        float acc[RB][4];
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) acc[r][q] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 4 * t));
+            const floatx4 hi = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 + 4 * t));
+            const float xl4[4] = {lo.x, lo.y, lo.z, lo.w}, xh4[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+            for (int r = 0; r < RB; r++) nib8(raw[r][4 + t], xl4, xh4, acc[r][t & 1], acc[r][2 + (t & 1)]);
+        }
+#pragma unroll
+        for (int r = 0; r < RB; r++) v[r] = F::finish(raw[r], jp, acc[r], xs);
+    }
+};
+
+template <int RB> struct LdsDot<DT_Q6_K, RB> {
+    using F = WaveFmt<DT_Q6_K>;
+    static constexpr int NS = 4;
+    __device__ static void sums(const float *xl, int b0, float (&xs)[NS]) {
+#pragma unroll
+        for (int qd = 0; qd < 4; qd++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const floatx4 u = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * qd + i));
+                a += (u.x + u.y) + (u.z + u.w);
+            }
+            xs[qd] = a;
+        }
+    }
+    __device__ static void run(const uint32_t (&raw)[RB][F::NRAW], int jp, const float *xl, int b0,
+                               const float (&xs)[NS], float (&v)[RB]) {
+        float sq[RB][4];
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) sq[r][q] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            float xq[4][4];
+#pragma unroll
+            for (int qd = 0; qd < 4; qd++) {
+                const floatx4 u = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * qd + 4 * t));
+                xq[qd][0] = u.x; xq[qd][1] = u.y; xq[qd][2] = u.z; xq[qd][3] = u.w;
+            }
+#pragma unroll
+            for (int r = 0; r < RB; r++) {
+                const uint32_t A = raw[r][t], B = raw[r][4 + t], H = raw[r][8 + t];
+                const uint32_t q[4] = {(A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u),
+                                       (B & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u),
+                                       ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u),
+                                       ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u)};
+#pragma unroll
+                for (int qd = 0; qd < 4; qd++) {
+                    sq[r][qd] = mix2(q[qd] & 0x003F003Fu, xq[qd][0], xq[qd][2], sq[r][qd]);
+                    sq[r][qd] = mix2((q[qd] >> 8) & 0x003F003Fu, xq[qd][1], xq[qd][3], sq[r][qd]);
+                }
+            }
+        }
+        const uint32_t sel = 8u * static_cast<uint32_t>(jp & 1);
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            const float d = h2f(raw[r][14] & 0xFFFF);
+            const uint32_t w0 = raw[r][12] >> sel, w1 = raw[r][13] >> sel;
+            const int sc[4] = {static_cast<int8_t>(w0 & 0xFF), static_cast<int8_t>((w0 >> 16) & 0xFF),
+                               static_cast<int8_t>(w1 & 0xFF), static_cast<int8_t>((w1 >> 16) & 0xFF)};
+            float a = 0.0f;
+#pragma unroll
+            for (int qd = 0; qd < 4; qd++) {
+                const float ds = d * static_cast<float>(sc[qd]);
+                a = __builtin_fmaf(ds * kTwo24, sq[r][qd], a);
+                a = __builtin_fmaf(-32.0f * ds, xs[qd], a);
+            }
+            v[r] = a;
+        }
+    }
+};
+
+template <int RB> struct LdsDot<DT_Q4_0, RB> {
+    using F = WaveFmt<DT_Q4_0>;
+    static constexpr int NS = 2;
+    __device__ static void sums(const float *xl, int b0, float (&xs)[NS]) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                const floatx4 w = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * u + i));
+                a += (w.x + w.y) + (w.z + w.w);
+            }
+            xs[u] = a;
+        }
+    }
+    __device__ static void run(const uint32_t (&raw)[RB][F::NRAW], int, const float *xl, int b0,
+                               const float (&xs)[NS], float (&v)[RB]) {
+        float acc[RB][2][2];
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) acc[r][u][0] = acc[r][u][1] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const floatx4 lo = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * u + 4 * t));
+                const floatx4 hi = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * u + 16 + 4 * t));
+                const float xl4[4] = {lo.x, lo.y, lo.z, lo.w}, xh4[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+                for (int r = 0; r < RB; r++) nib8(raw[r][5 * u + t], xl4, xh4, acc[r][u][0], acc[r][u][1]);
+            }
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const float d = h2f(raw[r][5 * u + 4] & 0xFFFF);
+                a = __builtin_fmaf(d * kTwo24, acc[r][u][0], a);
+                a = __builtin_fmaf(d * kTwo20, acc[r][u][1], a);
+                a = __builtin_fmaf(-8.0f * d, xs[u], a);
+            }
+            v[r] = a;
+        }
+    }
+};
+
+template <int RB> struct LdsDot<DT_Q8_0, RB> {
+    using F = WaveFmt<DT_Q8_0>;
+    static constexpr int NS = 2;
+    __device__ static void sums(const float *xl, int b0, float (&xs)[NS]) {
+        LdsDot<DT_Q4_0, RB>::sums(xl, b0, xs);
+    }
+    __device__ static void run(const uint32_t (&raw)[RB][F::NRAW], int, const float *xl, int b0,
+                               const float (&xs)[NS], float (&v)[RB]) {
+        float acc[RB][2][2];
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) acc[r][u][0] = acc[r][u][1] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const floatx4 xv = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * u + 4 * t));
+#pragma unroll
+                for (int r = 0; r < RB; r++) {
+                    const uint32_t q = raw[r][9 * u + t] ^ 0x80808080u;
+                    acc[r][u][0] = mix2(q & 0x00FF00FFu, xv.x, xv.z, acc[r][u][0]);
+                    acc[r][u][1] = mix2((q >> 8) & 0x00FF00FFu, xv.y, xv.w, acc[r][u][1]);
+                }
+            }
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const float d = h2f(raw[r][9 * u + 8] & 0xFFFF);
+                a = __builtin_fmaf(d * kTwo24, acc[r][u][0] + acc[r][u][1], a);
+                a = __builtin_fmaf(-128.0f * d, xs[u], a);
+            }
+            v[r] = a;
+        }
+    }
+};
+
+template <int DT, typename XT, typename OT, int RB>
+__global__ void __launch_bounds__(256) gemv_lds_kernel(SegTable t, int64_t total) {
+    using F = WaveFmt<DT>;
+    using D = LdsDot<DT, RB>;
+    constexpr int BV = blk_vals(DT), BB = blk_bytes(DT);
+    constexpr int H = RB / 2;
+    extern __shared__ float xl[];
+    const int lane = threadIdx.x & 63;
+    const int64_t W = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int64_t NW = static_cast<int64_t>(gridDim.x) * (blockDim.x >> 6);
+    const int slot = F::slot_of(lane);
+    const int nb = t.n_in / BV;
+    const int nsteps = (nb + F::BPS - 1) / F::BPS;
+
+    auto locate = [&](int64_t g, int &si, int64_t &n0) {
+        si = 0;
+        while (si + 1 < t.n && g >= t.seg[si + 1].blk_begin) si++;
+        n0 = (g - t.seg[si].blk_begin) * (t.seg[si].kind == SEG_SILU ? H : RB);
+    };
+    auto fetch = [&](uint32_t (&raw)[RB][F::NRAW], int si, int64_t n0, int st) {
+        const Seg &s = t.seg[si];
+        const bool pair = s.kind == SEG_SILU;
+        constexpr int per_lane = (DT == DT_Q4_0 || DT == DT_Q8_0) ? 2 : 1;
+        int b = st * F::BPS + F::blk_of(lane);
+        if (b > nb - per_lane) b = nb - per_lane;
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            int64_t n = n0 + (pair ? (r % H) : r);
+            if (n >= s.n_out) n = s.n_out - 1;
+            const uint8_t *wb = static_cast<const uint8_t *>((pair && r >= H) ? s.w2 : s.w);
+            F::load(raw[r], wb + n * t.row_bytes + static_cast<int64_t>(b) * BB, slot);
+        }
+    };
+
+    float xs[D::NS];
+    int xs_step = -1;
+    uint32_t rawA[RB][F::NRAW], rawB[RB][F::NRAW];
+    int64_t g = W;
+    int si = 0;
+    int64_t n0 = 0;
+    // the first group's weight bytes are requested before x is staged, so
+    // the two HBM round trips overlap instead of following each other
+    if (g < total) {
+        locate(g, si, n0);
+        fetch(rawA, si, n0, 0);
+    }
+    // stage x (all segments of a launch read the same x)
+    {
+        const XT *x = static_cast<const XT *>(t.seg[0].x);
+        for (int k = threadIdx.x * 4; k < t.n_in; k += blockDim.x * 4) {
+            floatx4 v;
+            if constexpr (sizeof(XT) == 4) {
+                v = *reinterpret_cast<const floatx4 *>(x + k);
+            } else {
+                v = floatx4{static_cast<float>(x[k]), static_cast<float>(x[k + 1]),
+                             static_cast<float>(x[k + 2]), static_cast<float>(x[k + 3])};
+            }
+            *reinterpret_cast<floatx4 *>(xl + xpad(k)) = v;
+        }
+    }
+    __syncthreads();
+
+    for (; g < total; g += NW) {
+        const Seg &s = t.seg[si];
+        float v[RB];
+#pragma unroll
+        for (int r = 0; r < RB; r++) v[r] = 0.0f;
+        const int64_t gn = g + NW;
+        int sn = si;
+        int64_t nn = 0;
+        for (int st = 0; st < nsteps; st++) {
+            if (st + 1 < nsteps) {
+                fetch(rawB, si, n0, st + 1);
+            } else if (gn < total) {
+                locate(gn, sn, nn);
+                fetch(rawB, sn, nn, 0);
+            }
+            const bool ok = st * F::BPS + F::blk_of(lane) < nb;
+            const int b0 = ok ? st * F::BPS * BV + XRuns<DT>::base(lane) : 0;
+            if (xs_step != st) {
+                D::sums(xl, b0, xs);
+                xs_step = nsteps > 1 ? -1 : st;
+            }
+            float d[RB];
+            D::run(rawA, slot, xl, b0, xs, d);
+#pragma unroll
+            for (int r = 0; r < RB; r++) v[r] += ok ? d[r] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < RB; r++)
+#pragma unroll
+                for (int k = 0; k < F::NRAW; k++) rawA[r][k] = rawB[r][k];
+        }
+        wave_reduce_multi<RB>(v, lane);
+        const int idx = reduce_owner_index<RB>(lane);
+        const int kind = s.kind;
+        OT *out = static_cast<OT *>(s.out);
+        if (kind != SEG_SILU) {
+            if (reduce_owner<RB>(lane)) {
+                const int64_t n = n0 + idx;
+                const float inv = (kind == SEG_ACC && t.rexp) ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
+                if (n < s.n_out) store_out<OT>(out + n, v[0], kind, inv);
+            }
+        } else {
+            constexpr int SH = 64 / RB;
+            const float u = __shfl(v[0], (lane + H * SH) & 63, 64);
+            if (reduce_owner<RB>(lane) && idx < H) {
+                const int64_t n = n0 + idx;
+                if (n < s.n_out) {
+                    const float gs = v[0];
+                    if constexpr (sizeof(OT) == 2) {
+                        const float hg = static_cast<float>(static_cast<_Float16>(gs));
+                        const float hu = static_cast<float>(static_cast<_Float16>(u));
+                        out[n] = sat_f16(silu_f(hg) * hu);
+                    } else {
+                        out[n] = (gs / (1.0f + expf(-gs))) * u;
+                    }
+                }
+            }
+        }
+        si = sn;
+        n0 = nn;
+    }
+}
+
+// --------------------------------------------- LDS-DMA streamed decode GEMV --
+// Measured on MI355X: the vector-memory path delivers ~5.2 TB/s of LANE
+// bytes whether they come from HBM or L2, so a decode GEMV is bound by the
+// bytes its lanes receive, not by the bytes HBM sends.  Per-lane loads of a
+// block's header (8 or 4 lanes re-reading the same 16 B) and per-wave x
+// reloads cost as much as the weights themselves.  This kernel therefore
+// receives every weight byte exactly once: a wave copies its group of RB
+// consecutive rows (one contiguous region) into a private LDS slot with
+// global_load_lds_dwordx4 -- 64 lanes x 16 B = 1 KB per instruction, fully
+// coalesced, no VGPR round trip -- and lanes then read their pieces from
+// LDS.  Three slots per wave keep two groups in flight while one is decoded;
+// x is staged once per workgroup.  The compiler does not track the LDS-DMA
+// dependency, so the waits are explicit (vmcnt counts this wave's
+// outstanding loads in issue order).
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    // s_waitcnt simm16: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Rows per group of the streamed kernel.  A unit of work is RB rows x one
+// wave step (4096 values of K); its bytes are RB pieces of P = BPS * BB
+// contiguous bytes, which the DMA gathers into one slot back to back.
+template <int DT> struct StreamCfg { static constexpr int RB = (DT == DT_Q4_K || DT == DT_Q4_0) ? 4 : 2; };
+
+template <int DT, typename XT, typename OT, int RB, int NSLOT>
+__global__ void __launch_bounds__(1024) gemv_stream_kernel(SegTable t, int64_t total, int xfloats) {
+    using F = WaveFmt<DT>;
+    using D = LdsDot<DT, RB>;
+    constexpr int BV = blk_vals(DT), BB = blk_bytes(DT);
+    constexpr int P = F::BPS * BB;               // one row's bytes of one step
+    constexpr int U = RB * P;                    // one unit's bytes
+    constexpr int CH = (U + 1023) / 1024;        // DMA instructions per unit
+    constexpr int SLOT = CH * 1024;
+    constexpr int per_lane = (DT == DT_Q4_0 || DT == DT_Q8_0) ? 2 : 1;
+    static_assert(P % 16 == 0, "pieces must be whole 16-byte chunks");
+    extern __shared__ float smem[];
+    float *xl = smem;
+    __shared__ Seg segl[kMaxSegs];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint8_t *slots = reinterpret_cast<uint8_t *>(smem + xfloats) + wv * (NSLOT * SLOT);
+    const int64_t W = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wv;
+    const int64_t NW = static_cast<int64_t>(gridDim.x) * (blockDim.x >> 6);
+    const int slot_lane = F::slot_of(lane);
+    const int nb = t.n_in / BV;
+    const int nsteps = (nb + F::BPS - 1) / F::BPS;
+    const int64_t rb = t.row_bytes;
+    // this wave's units: groups W, W + NW, ... each split into nsteps steps
+    const int64_t my_groups = W < total ? (total - 1 - W) / NW + 1 : 0;
+    const int64_t my_units = my_groups * nsteps;
+
+    // group g -> segment fields.  The table is copied to LDS first: indexed
+    // in the kernel arguments it would be read through vector memory, and
+    // the waits for those reads would also drain the weight DMA.
+    const int nseg = t.n;
+    if (threadIdx.x < nseg) segl[threadIdx.x] = t.seg[threadIdx.x];
+    const float inv_acc = t.rexp ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
+    __syncthreads();
+    auto locate = [&](int64_t g, const uint8_t *&w, int64_t &n_out, int64_t &n0, void *&out,
+                      int &kind) {
+        int i = 0;
+        while (i + 1 < nseg && g >= segl[i + 1].blk_begin) i++;
+        w = static_cast<const uint8_t *>(segl[i].w);
+        n_out = segl[i].n_out;
+        n0 = (g - segl[i].blk_begin) * RB;
+        out = segl[i].out;
+        kind = segl[i].kind;
+    };
+    auto issue = [&](int64_t j) {
+        const int64_t g = W + (j / nsteps) * NW;
+        const int st = static_cast<int>(j % nsteps);
+        const uint8_t *w;
+        int64_t n_out, n0;
+        void *out;
+        int kind;
+        locate(g, w, n_out, n0, out, kind);
+        const int64_t lim = rb - 16;             // last whole chunk of a row
+        uint8_t *dst = slots + static_cast<int>(j % NSLOT) * SLOT;
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int o = c * 1024 + 16 * lane;
+            if (c + 1 < CH || o < U) {
+                const int r = o / P;
+                int64_t n = n0 + r;
+                if (n >= n_out) n = n_out - 1;
+                int64_t off = static_cast<int64_t>(st) * P + (o - r * P);
+                if (off > lim) off = lim;        // past the row end: masked lanes read this
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(w + n * rb + off),
+                                                 (lds_void_t *)(dst + c * 1024), 16, 0, 0);
+            }
+        }
+    };
+
+    // NSLOT - 1 units in flight before anything else
+#pragma unroll
+    for (int k = 0; k < NSLOT - 1; k++)
+        if (k < my_units) issue(k);
+
+    // stage x once per workgroup (the DMA above overlaps with it)
+    {
+        const XT *x = static_cast<const XT *>(t.seg[0].x);
+        for (int k = threadIdx.x * 4; k < t.n_in; k += blockDim.x * 4) {
+            floatx4 v;
+            if constexpr (sizeof(XT) == 4) {
+                v = *reinterpret_cast<const floatx4 *>(x + k);
+            } else {
+                v = floatx4{static_cast<float>(x[k]), static_cast<float>(x[k + 1]),
+                             static_cast<float>(x[k + 2]), static_cast<float>(x[k + 3])};
+            }
+            *reinterpret_cast<floatx4 *>(xl + xpad(k)) = v;
+        }
+    }
+    __syncthreads();
+
+    float xs[D::NS];
+    int xs_step = -1;
+    float v[RB];
+#pragma unroll
+    for (int r = 0; r < RB; r++) v[r] = 0.0f;
+    for (int64_t j = 0; j < my_units; j++) {
+        // slot (j + NSLOT - 1) % NSLOT held unit j - 1, whose bytes are consumed
+        if (j + NSLOT - 1 < my_units) issue(j + NSLOT - 1);
+        const int64_t ahead = my_units - 1 - j;
+        if (ahead >= NSLOT - 1) wait_vmcnt<(NSLOT - 1) * CH>();
+        else if (NSLOT > 2 && ahead == 1) wait_vmcnt<CH>();
+        else wait_vmcnt<0>();
+        const int st = static_cast<int>(j % nsteps);
+        const uint8_t *slot = slots + static_cast<int>(j % NSLOT) * SLOT;
+        int b = st * F::BPS + F::blk_of(lane);
+        const bool ok = b < nb;
+        if (b > nb - per_lane) b = nb - per_lane;
+        const int lb = b - st * F::BPS;
+        uint32_t raw[RB][F::NRAW];
+#pragma unroll
+        for (int r = 0; r < RB; r++) F::load(raw[r], slot + r * P + lb * BB, slot_lane);
+        const int b0 = ok ? st * F::BPS * BV + XRuns<DT>::base(lane) : 0;
+        if (xs_step != st) {
+            D::sums(xl, b0, xs);
+            xs_step = nsteps > 1 ? -1 : st;
+        }
+        float d[RB];
+        D::run(raw, slot_lane, xl, b0, xs, d);
+#pragma unroll
+        for (int r = 0; r < RB; r++) v[r] += ok ? d[r] : 0.0f;
+        if (st == nsteps - 1) {
+            const int64_t g = W + (j / nsteps) * NW;
+            const uint8_t *w;
+            int64_t n_out, n0;
+            void *out;
+            int kind;
+            locate(g, w, n_out, n0, out, kind);
+            wave_reduce_multi<RB>(v, lane);
+            if (reduce_owner<RB>(lane)) {
+                const int64_t n = n0 + reduce_owner_index<RB>(lane);
+                if (n < n_out) store_out<OT>(static_cast<OT *>(out) + n, v[0], kind, kind == SEG_ACC ? inv_acc : 1.0f);
+            }
+#pragma unroll
+            for (int r = 0; r < RB; r++) v[r] = 0.0f;
+        }
+    }
+}
+
+template <int DT, typename XT, typename OT, int RB, int NSLOT>
+static hipError_t launch_stream(SegTable t, hipStream_t st) {
+    constexpr int SLOT = ((RB * WaveFmt<DT>::BPS * blk_bytes(DT) + 1023) / 1024) * 1024;
+    int64_t total = 0;
+    for (int i = 0; i < t.n; i++) {
+        t.seg[i].blk_begin = total;
+        total += (t.seg[i].n_out + RB - 1) / RB;
+    }
+    const int xfloats = (t.n_in + 4 * (t.n_in / 64) + 4 + 3) & ~3;
+    const size_t xbytes = static_cast<size_t>(xfloats) * sizeof(float) + sizeof(Seg) * kMaxSegs;
+    const size_t per_wave = static_cast<size_t>(NSLOT) * SLOT;
+    constexpr size_t kLds = 160u * 1024u;
+    // waves per workgroup: the most resident waves per CU (at most 4 per
+    // SIMD), ties to the larger workgroup (x is staged once per workgroup)
+    int best_nw = 0, best_waves = 0;
+    for (int nw = 1; nw <= 16; nw++) {
+        const size_t l = xbytes + nw * per_wave;
+        if (l > kLds) break;
+        int per_cu = static_cast<int>(kLds / l);
+        if (per_cu * nw > 16) per_cu = 16 / nw;
+        if (per_cu * nw >= best_waves) { best_waves = per_cu * nw; best_nw = nw; }
+    }
+    if (!best_nw) return hipErrorInvalidValue;
+    const int nw = best_nw;
+    const size_t lds = xbytes - sizeof(Seg) * kMaxSegs + nw * per_wave;  // dynamic part
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    int64_t grid = static_cast<int64_t>(cus) * (best_waves / nw);
+    if (grid * nw > total) grid = (total + nw - 1) / nw;
+    hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, RB, NSLOT>), dim3(static_cast<unsigned>(grid)),
+                       dim3(64 * nw), lds, st, t, total, xfloats);
+    return hipGetLastError();
+}
+
+static int gemv_stream_cfg_knob() {  // experiment: RB * 10 + NSLOT, 0 = default
+    static const int v = [] {
+        const char *e = std::getenv("KRK_STREAM_CFG");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v;
+}
+
+template <int DT, typename XT, typename OT>
+static hipError_t launch_stream(const SegTable &t, hipStream_t st) {
+    if constexpr (sizeof(XT) == 4 && sizeof(OT) == 4 && (DT == DT_Q4_K || DT == DT_Q6_K)) {
+        switch (gemv_stream_cfg_knob()) {
+            case 43: return launch_stream<DT, XT, OT, 4, 3>(t, st);
+            case 42: return launch_stream<DT, XT, OT, 4, 2>(t, st);
+            case 23: return launch_stream<DT, XT, OT, 2, 3>(t, st);
+            case 22: return launch_stream<DT, XT, OT, 2, 2>(t, st);
+            case 13: return launch_stream<DT, XT, OT, 1, 3>(t, st);
+            case 12: return launch_stream<DT, XT, OT, 1, 2>(t, st);
+            default: break;
+        }
+    }
+    return launch_stream<DT, XT, OT, StreamCfg<DT>::RB, 2>(t, st);
+}
+
+template <int DT, typename XT, typename OT>
+static bool try_stream(const SegTable &t, hipStream_t st, hipError_t &err) {
+    if (t.rows != 1 || !gemv_stream_knob() || t.n_in > 16384) return false;
+    for (int i = 0; i < t.n; i++) {
+        if (t.seg[i].kind == SEG_SILU || t.seg[i].x != t.seg[0].x) return false;
+        if (reinterpret_cast<uintptr_t>(t.seg[i].w) & 15) return false;
+    }
+    if ((DT == DT_Q4_0 || DT == DT_Q8_0) && t.n_in % 64) return false;
+    if (t.row_bytes % 16) return false;
+    err = launch_stream<DT, XT, OT>(t, st);
+    return true;
+}
+
+constexpr int kLdsGemvMaxK = 16384;  // f32 x plus padding must fit in LDS
+
+template <int DT, typename XT, typename OT, int RB>
+static hipError_t launch_lds(SegTable t, hipStream_t st) {
+    int64_t total = 0;
+    for (int i = 0; i < t.n; i++) {
+        t.seg[i].blk_begin = total;
+        const int64_t per = t.seg[i].kind == SEG_SILU ? RB / 2 : RB;
+        total += (t.seg[i].n_out + per - 1) / per;
+    }
+    const size_t lds = static_cast<size_t>(t.n_in + 4 * (t.n_in / 64) + 4) * sizeof(float);
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    // resident workgroups per CU, queried once per distinct LDS size
+    static size_t cached_lds[8] = {};
+    static int cached_occ[8] = {};
+    int per_cu = 0;
+    for (int i = 0; i < 8 && cached_lds[i]; i++)
+        if (cached_lds[i] == lds) { per_cu = cached_occ[i]; break; }
+    if (!per_cu) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_lds_kernel<DT, XT, OT, RB>, 256,
+                                                         lds) != hipSuccess || per_cu < 1)
+            per_cu = 1;
+        for (int i = 0; i < 8; i++)
+            if (!cached_lds[i]) { cached_lds[i] = lds; cached_occ[i] = per_cu; break; }
+    }
+    int64_t grid = static_cast<int64_t>(cus) * per_cu;
+    if (grid * 4 > total) grid = (total + 3) / 4;
+    hipLaunchKernelGGL((gemv_lds_kernel<DT, XT, OT, RB>), dim3(static_cast<unsigned>(grid)), dim3(256),
+                       lds, st, t, total);
+    return hipGetLastError();
+}
+
 // ------------------------------------------------------------- launcher ----
+
 template <int DT, typename XT, typename OT, int MR, int RB>
 static hipError_t launch_seg(const SegTable &t, int64_t total_blocks, hipStream_t st) {
     const int nb = t.n_in / blk_vals(DT);
@@ -111,8 +1317,80 @@ static hipError_t launch_seg(const SegTable &t, int64_t total_blocks, hipStream_
     return hipGetLastError();
 }
 
+template <int DT, typename XT, typename OT, int RB>
+static hipError_t launch_persist(SegTable t, hipStream_t st) {
+    int64_t total = 0;
+    for (int i = 0; i < t.n; i++) {
+        t.seg[i].blk_begin = total;
+        const int64_t per = t.seg[i].kind == SEG_SILU ? RB / 2 : RB;
+        total += (t.seg[i].n_out + per - 1) / per;
+    }
+    const int nsteps = (t.n_in / blk_vals(DT) + kWave / LaneFmt<DT>::LPB - 1) / (kWave / LaneFmt<DT>::LPB);
+    const int threads = 64 * nsteps;
+    // resident workgroups per CU for this instantiation and block size
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    static int per_cu = 0;
+    if (!per_cu && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_persist_kernel<DT, XT, OT, RB>,
+                                                                 threads, 0) != hipSuccess || per_cu < 1))
+        per_cu = 1;
+    int64_t grid = static_cast<int64_t>(cus) * per_cu;
+    if (grid > total) grid = total;
+    hipLaunchKernelGGL((gemv_persist_kernel<DT, XT, OT, RB>), dim3(static_cast<unsigned>(grid)),
+                       dim3(threads), 0, st, t, total);
+    return hipGetLastError();
+}
+
 template <int DT, typename XT, typename OT>
 static hipError_t dispatch_mr(SegTable t, hipStream_t st) {
+    {
+        const int nsteps = (t.n_in / blk_vals(DT) + kWave / LaneFmt<DT>::LPB - 1) /
+                           (kWave / LaneFmt<DT>::LPB);
+        if constexpr (DT == DT_Q4_K) {
+            // matrix-core decode GEMV (KRK_GEMV_MFMA=0 keeps the VALU form)
+            const int nb = t.n_in / 256;
+            if (t.rows == 1 && gemv_mfma_knob() && nb <= 16) {
+                if (gemv_spw_knob() == 1) return launch_mfma_q4k<XT, OT, 1>(t, st);
+                return launch_mfma_q4k<XT, OT, 2>(t, st);
+            }
+        }
+        const bool two_blocks = DT == DT_Q4_0 || DT == DT_Q8_0;
+        {
+            hipError_t err = hipSuccess;
+            if (try_stream<DT, XT, OT>(t, st, err)) return err;
+        }
+        bool same_x = true;
+        for (int i = 1; i < t.n; i++) same_x = same_x && t.seg[i].x == t.seg[0].x;
+        if (t.rows == 1 && gemv_lds_knob() && same_x && t.n_in <= kLdsGemvMaxK &&
+            (!two_blocks || t.n_in % 64 == 0)) {
+            switch (gemv_rb_knob()) {
+                case 2: return launch_lds<DT, XT, OT, 2>(t, st);
+                case 8: return launch_lds<DT, XT, OT, 8>(t, st);
+                default: return launch_lds<DT, XT, OT, 4>(t, st);
+            }
+        }
+        if (t.rows == 1 && gemv_wave_knob() && (!two_blocks || t.n_in % 64 == 0)) {
+            switch (gemv_rb_knob()) {
+                case 2: return launch_wave<DT, XT, OT, 2>(t, st);
+                case 41: return launch_wave<DT, XT, OT, 4, 1>(t, st);
+                case 42: return launch_wave<DT, XT, OT, 4, 2>(t, st);
+                case 8: return launch_wave<DT, XT, OT, 8>(t, st);
+                default: return launch_wave<DT, XT, OT, 4>(t, st);
+            }
+        }
+        if (t.rows == 1 && nsteps <= 8) {
+            switch (gemv_rb_knob()) {
+                case 2: return launch_persist<DT, XT, OT, 2>(t, st);
+                case 8: return launch_persist<DT, XT, OT, 8>(t, st);
+                default: return launch_persist<DT, XT, OT, 4>(t, st);
+            }
+        }
+    }
     // rows per x pass and weight rows per block, MR*RB = 8 values per lane
     int mr = t.rows <= 1 ? 1 : t.rows == 2 ? 2 : 4;
     const int rb = 8 / mr;

@@ -102,24 +102,9 @@ __device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, int64_t
             F::load(raw[r], wb + n * row_bytes + static_cast<int64_t>(b) * BB, p);
         }
 #pragma unroll
-        for (int r = 0; r < RB; r++) {
-            float wq[32], sc[F::NG], off[F::NG];
-            F::decode(raw[r], p, wq, sc, off);
+        for (int r = 0; r < RB; r++)
 #pragma unroll
-            for (int m = 0; m < MR; m++) {
-                float s[F::NG];
-#pragma unroll
-                for (int g = 0; g < F::NG; g++) s[g] = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 32; i++)
-                    s[F::group_of(i)] = __builtin_fmaf(wq[i], xv[m][i], s[F::group_of(i)]);
-                float a = acc[m][r];
-#pragma unroll
-                for (int g = 0; g < F::NG; g++)
-                    a = __builtin_fmaf(sc[g], s[g], __builtin_fmaf(-off[g], xs[m][g], a));
-                acc[m][r] = a;
-            }
-        }
+            for (int m = 0; m < MR; m++) acc[m][r] += F::dot(raw[r], p, xv[m], xs[m]);
     }
 }
 

@@ -114,10 +114,42 @@ __device__ __forceinline__ void load_bytes2(const uint8_t *p, uint32_t (&o)[NW])
 }
 
 // --------------------------------------------------------------- LaneFmt ----
-// The lane view: LPB lanes per block, each owning 32 values ("a piece"), NG
-// groups sharing one (scale, off) pair.  pos(p, i) is the position inside the
-// block of the piece's i-th value; runs(p, r) the start of its r-th run of
-// RUN consecutive values (the x loads).
+// The lane view: LPB lanes per block, each owning 32 values ("a piece").
+// run_start(p, r) is where, inside the block, the r-th run of RUN consecutive
+// values of piece p starts; the lane's activations arrive in that order as
+// xv[0..31].  dot() returns the piece's contribution sum_i w_i * xv_i.
+//
+// Codes are never converted with v_cvt: a code c < 1024 placed in the low 10
+// bits of a 16-bit lane IS the f16 subnormal c * 2^-24, which v_fma_mix_f32
+// widens exactly inside the FMA.  So sum_i c_i * x_i costs one FMA per value
+// plus ~0.6 ops of masking, and the 2^24 goes back into the block scale
+// (a power of two: exact).  Per group g of values sharing a scale:
+//     contribution = scale_g * 2^24 * sum(c_i * x_i) - off_g * sum(x_i)
+// where off_g folds the format's zero point (Q4_K's min, Q6_K's 32, ...).
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+
+// acc += c(v.lo) * x0 + c(v.hi) * x1 for a dword holding two codes
+__device__ __forceinline__ float mix2(uint32_t v, float x0, float x1, float acc) {
+    const half2v h = as_h2(v);
+    acc = __builtin_fmaf(static_cast<float>(h.x), x0, acc);
+    return __builtin_fmaf(static_cast<float>(h.y), x1, acc);
+}
+
+// Eight 4-bit codes of a dword: bytes k = 0..3 hold (lo nibble, hi nibble).
+// Low nibbles go to xl[k], high nibbles (as 16*c) to xh[k].
+__device__ __forceinline__ void nib8(uint32_t v, const float *xl, const float *xh, float &sl,
+                                     float &sh) {
+    const uint32_t s8 = v >> 8;
+    sl = mix2(v & 0x000F000Fu, xl[0], xl[2], sl);
+    sl = mix2(s8 & 0x000F000Fu, xl[1], xl[3], sl);
+    sh = mix2(v & 0x00F000F0u, xh[0], xh[2], sh);
+    sh = mix2(s8 & 0x00F000F0u, xh[1], xh[3], sh);
+}
+
+constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
+
 template <int DT> struct LaneFmt;
 
 // Q4_K: piece p covers qs bytes [16p, 16p+16): sub-block 2j low nibbles
@@ -125,41 +157,37 @@ template <int DT> struct LaneFmt;
 template <> struct LaneFmt<DT_Q4_K> {
     static constexpr int LPB = 8, NG = 2, RUN = 16, NRUN = 2, NRAW = 8;
     __device__ static int run_start(int p, int r) { return 64 * (p >> 1) + 32 * r + 16 * (p & 1); }
+    __device__ static int group_of(int i) { return i >> 4; }
     __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int p) {
         const u32x4 h = ld128(blk);
         const u32x4 q = ld128(blk + 16 + 16 * p);
         raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
         raw[4] = q.x; raw[5] = q.y; raw[6] = q.z; raw[7] = q.w;
     }
-    // wq[i]: i < 16 -> q (low nibble), i >= 16 -> 16*q (high nibble, masked in place)
-    __device__ static void decode(const uint32_t (&raw)[NRAW], int p, float (&wq)[32],
-                                  float (&sc)[NG], float (&off)[NG]) {
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int p, const float (&xv)[32],
+                                const float (&xs)[NG]) {
         const float d = h2f(raw[0] & 0xFFFF), dmin = h2f(raw[0] >> 16);
-        const uint32_t sh = 16u * static_cast<uint32_t>((p >> 1) & 1);  // j & 1
+        // this lane's two sub-blocks 2j, 2j+1 (get_scale_min_k4, quant.cpp:427)
+        const uint32_t sh = 16u * static_cast<uint32_t>((p >> 1) & 1);
         const uint32_t Y = raw[1] >> sh, Z = raw[2] >> sh, W = raw[3] >> sh;
-        int sa, sb, ma, mb;
-        if (p < 4) {  // sub-blocks 0..3: 6-bit fields stored directly
+        uint32_t sa, sb, ma, mb;
+        if (p < 4) {
             sa = Y & 63; sb = (Y >> 8) & 63; ma = Z & 63; mb = (Z >> 8) & 63;
-        } else {      // sub-blocks 4..7: low 4 bits in scales[8..11], top 2 in the high bits
+        } else {
             sa = (W & 0xF) | (((Y >> 6) & 3) << 4);
             sb = ((W >> 8) & 0xF) | (((Y >> 14) & 3) << 4);
             ma = ((W >> 4) & 0xF) | (((Z >> 6) & 3) << 4);
             mb = ((W >> 12) & 0xF) | (((Z >> 14) & 3) << 4);
         }
-        sc[0] = d * static_cast<float>(sa);
-        off[0] = dmin * static_cast<float>(ma);
-        sc[1] = d * static_cast<float>(sb) * 0.0625f;
-        off[1] = dmin * static_cast<float>(mb);
+        float sl = 0.0f, shi = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const uint32_t lo = raw[4 + t] & 0x0F0F0F0Fu, hi = raw[4 + t] & 0xF0F0F0F0u;
-            wq[4 * t + 0] = ubyte_f<0>(lo); wq[4 * t + 1] = ubyte_f<1>(lo);
-            wq[4 * t + 2] = ubyte_f<2>(lo); wq[4 * t + 3] = ubyte_f<3>(lo);
-            wq[16 + 4 * t + 0] = ubyte_f<0>(hi); wq[16 + 4 * t + 1] = ubyte_f<1>(hi);
-            wq[16 + 4 * t + 2] = ubyte_f<2>(hi); wq[16 + 4 * t + 3] = ubyte_f<3>(hi);
-        }
+        for (int t = 0; t < 4; t++) nib8(raw[4 + t], &xv[4 * t], &xv[16 + 4 * t], sl, shi);
+        const float dl = d * static_cast<float>(sa), dh = d * static_cast<float>(sb);
+        float a = (dl * kTwo24) * sl;
+        a = __builtin_fmaf(dh * kTwo20, shi, a);
+        a = __builtin_fmaf(-dmin * static_cast<float>(ma), xs[0], a);
+        return __builtin_fmaf(-dmin * static_cast<float>(mb), xs[1], a);
     }
-    __device__ static int group_of(int i) { return i >> 4; }
 };
 
 // Q6_K: piece p = (half h = p/4, sub = p%4): values 128h + 32qd + 8sub + t for
@@ -168,9 +196,10 @@ template <> struct LaneFmt<DT_Q4_K> {
 template <> struct LaneFmt<DT_Q6_K> {
     static constexpr int LPB = 8, NG = 4, RUN = 8, NRUN = 4, NRAW = 9;
     __device__ static int run_start(int p, int r) { return 128 * (p >> 2) + 32 * r + 8 * (p & 3); }
+    __device__ static int group_of(int i) { return i >> 3; }
     __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int p) {
         const int h = p >> 2, o = 8 * (p & 3);
-        uint32_t a[2], b[2], q[2], s[2], dd[1];
+        uint32_t a[2], b[2], q[2], s[2];
         load_bytes2<2>(blk + 64 * h + o, a);
         load_bytes2<2>(blk + 64 * h + 32 + o, b);
         load_bytes2<2>(blk + 128 + 32 * h + o, q);
@@ -178,42 +207,42 @@ template <> struct LaneFmt<DT_Q6_K> {
         // d is the last two bytes of the block; read the dword that holds them
         // without touching anything past the block.
         const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
-        dd[0] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        raw[8] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
         raw[0] = a[0]; raw[1] = a[1]; raw[2] = b[0]; raw[3] = b[1];
-        raw[4] = q[0]; raw[5] = q[1]; raw[6] = s[0]; raw[7] = s[1]; raw[8] = dd[0];
+        raw[4] = q[0]; raw[5] = q[1]; raw[6] = s[0]; raw[7] = s[1];
     }
-    // wq = q6 code in [0, 63]; value = (d*sc) * (q - 32).
-    __device__ static void decode(const uint32_t (&raw)[NRAW], int p, float (&wq)[32],
-                                  float (&sc)[NG], float (&off)[NG]) {
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int p, const float (&xv)[32],
+                                const float (&xs)[NG]) {
         const float d = h2f(raw[8] & 0xFFFF);
-        const uint32_t sub2 = static_cast<uint32_t>((p & 3) >> 1);
-#pragma unroll
-        for (int qd = 0; qd < 4; qd++) {
-            const int idx = static_cast<int>(sub2) + 2 * qd;  // byte in the 8 scale bytes
-            const uint32_t sw = idx < 4 ? raw[6] : raw[7];
-            const int s8 = static_cast<int32_t>(sw << (24 - 8 * (idx & 3))) >> 24;
-            const float ds = d * static_cast<float>(s8);
-            sc[qd] = ds;
-            off[qd] = 32.0f * ds;
-        }
+        const int sub2 = (p & 3) >> 1;
+        float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             const uint32_t A = raw[t], B = raw[2 + t], H = raw[4 + t];
-            const uint32_t q0 = (A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u);
-            const uint32_t q1 = (B & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u);
-            const uint32_t q2 = ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
-            const uint32_t q3 = ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
-            const uint32_t qq[4] = {q0, q1, q2, q3};
+            // byte-parallel 6-bit codes of the four quadrants
+            const uint32_t q[4] = {(A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u),
+                                   (B & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u),
+                                   ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u),
+                                   ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u)};
 #pragma unroll
             for (int qd = 0; qd < 4; qd++) {
-                wq[8 * qd + 4 * t + 0] = ubyte_f<0>(qq[qd]);
-                wq[8 * qd + 4 * t + 1] = ubyte_f<1>(qq[qd]);
-                wq[8 * qd + 4 * t + 2] = ubyte_f<2>(qq[qd]);
-                wq[8 * qd + 4 * t + 3] = ubyte_f<3>(qq[qd]);
+                const float *x = &xv[8 * qd + 4 * t];
+                s[qd] = mix2(q[qd] & 0x003F003Fu, x[0], x[2], s[qd]);
+                s[qd] = mix2((q[qd] >> 8) & 0x003F003Fu, x[1], x[3], s[qd]);
             }
         }
+        float a = 0.0f;
+#pragma unroll
+        for (int qd = 0; qd < 4; qd++) {
+            const int idx = sub2 + 2 * qd;  // byte in the 8 scale bytes
+            const uint32_t sw = idx < 4 ? raw[6] : raw[7];
+            const int s8 = static_cast<int32_t>(sw << (24 - 8 * (idx & 3))) >> 24;
+            const float ds = d * static_cast<float>(s8);
+            a = __builtin_fmaf(ds * kTwo24, s[qd], a);
+            a = __builtin_fmaf(-32.0f * ds, xs[qd], a);
+        }
+        return a;
     }
-    __device__ static int group_of(int i) { return i >> 3; }
 };
 
 // Q4_0: one lane per 32-value block.  Low nibbles are values 0..15, high
@@ -221,6 +250,7 @@ template <> struct LaneFmt<DT_Q6_K> {
 template <> struct LaneFmt<DT_Q4_0> {
     static constexpr int LPB = 1, NG = 2, RUN = 32, NRUN = 1, NRAW = 5;
     __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int i) { return i >> 4; }
     __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
         uint32_t q[4];
         load_bytes2<4>(blk + 2, q);
@@ -228,27 +258,24 @@ template <> struct LaneFmt<DT_Q4_0> {
         raw[4] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
         raw[0] = q[0]; raw[1] = q[1]; raw[2] = q[2]; raw[3] = q[3];
     }
-    __device__ static void decode(const uint32_t (&raw)[NRAW], int, float (&wq)[32],
-                                  float (&sc)[NG], float (&off)[NG]) {
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[32],
+                                const float (&xs)[NG]) {
         const float d = h2f(raw[4] & 0xFFFF);
-        sc[0] = d; off[0] = 8.0f * d;
-        sc[1] = d * 0.0625f; off[1] = 8.0f * d;
+        float sl = 0.0f, shi = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const uint32_t lo = raw[t] & 0x0F0F0F0Fu, hi = raw[t] & 0xF0F0F0F0u;
-            wq[4 * t + 0] = ubyte_f<0>(lo); wq[4 * t + 1] = ubyte_f<1>(lo);
-            wq[4 * t + 2] = ubyte_f<2>(lo); wq[4 * t + 3] = ubyte_f<3>(lo);
-            wq[16 + 4 * t + 0] = ubyte_f<0>(hi); wq[16 + 4 * t + 1] = ubyte_f<1>(hi);
-            wq[16 + 4 * t + 2] = ubyte_f<2>(hi); wq[16 + 4 * t + 3] = ubyte_f<3>(hi);
-        }
+        for (int t = 0; t < 4; t++) nib8(raw[t], &xv[4 * t], &xv[16 + 4 * t], sl, shi);
+        float a = (d * kTwo24) * sl;
+        a = __builtin_fmaf(d * kTwo20, shi, a);
+        return __builtin_fmaf(-8.0f * d, xs[0] + xs[1], a);
     }
-    __device__ static int group_of(int i) { return i >> 4; }
 };
 
-// Q8_0: one lane per 32-value block; value = d * (int8)q.
+// Q8_0: one lane per 32-value block; value = d * (int8)q.  Codes are biased
+// to q + 128 (xor 0x80) so they are non-negative subnormals.
 template <> struct LaneFmt<DT_Q8_0> {
     static constexpr int LPB = 1, NG = 1, RUN = 32, NRUN = 1, NRAW = 9;
     __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int) { return 0; }
     __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
         uint32_t q[8];
         load_bytes2<8>(blk + 2, q);
@@ -257,17 +284,212 @@ template <> struct LaneFmt<DT_Q8_0> {
 #pragma unroll
         for (int k = 0; k < 8; k++) raw[k] = q[k];
     }
-    __device__ static void decode(const uint32_t (&raw)[NRAW], int, float (&wq)[32],
-                                  float (&sc)[NG], float (&off)[NG]) {
-        sc[0] = h2f(raw[8] & 0xFFFF);
-        off[0] = 0.0f;
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[32],
+                                const float (&xs)[NG]) {
+        const float d = h2f(raw[8] & 0xFFFF);
+        float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            wq[4 * t + 0] = sbyte_f<0>(raw[t]); wq[4 * t + 1] = sbyte_f<1>(raw[t]);
-            wq[4 * t + 2] = sbyte_f<2>(raw[t]); wq[4 * t + 3] = sbyte_f<3>(raw[t]);
+            const uint32_t u = raw[t] ^ 0x80808080u;
+            const float *x = &xv[4 * t];
+            s0 = mix2(u & 0x00FF00FFu, x[0], x[2], s0);
+            s1 = mix2((u >> 8) & 0x00FF00FFu, x[1], x[3], s1);
+        }
+        const float a = (d * kTwo24) * (s0 + s1);
+        return __builtin_fmaf(-128.0f * d, xs[0], a);
+    }
+};
+
+
+// --------------------------------------------------------------- WaveFmt ----
+// The independent-wave view used by the decode GEMV: one lane owns 64
+// consecutive-in-block weights of a row (two LaneFmt pieces that share their
+// scales), so a wave covers a whole "step" of 4096 values (Q4_K / Q6_K: 16
+// blocks; Q4_0 / Q8_0: 128 blocks) and a row of K <= 4096 needs no other
+// wave.  xv[0..63] are the lane's activations in run order.
+template <int DT> struct WaveFmt;
+
+template <> struct WaveFmt<DT_Q4_K> {
+    // lane slot jp = lane % 4 of block lane / 4: qs bytes [32jp, 32jp+32) =
+    // sub-block 2jp (low nibbles, values 64jp + 0..31) and 2jp+1 (high
+    // nibbles, values 64jp + 32..63)
+    static constexpr int LPB = 4, BPS = 16, NG = 2, RUN = 64, NRUN = 1, NRAW = 12;
+    __device__ static int blk_of(int lane) { return lane >> 2; }
+    __device__ static int slot_of(int lane) { return lane & 3; }
+    __device__ static int run_start(int jp, int) { return 64 * jp; }
+    __device__ static int group_of(int i) { return i >> 5; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int jp) {
+        const u32x4 h = ld128(blk);
+        const u32x4 a = ld128(blk + 16 + 32 * jp);
+        const u32x4 b = ld128(blk + 32 + 32 * jp);
+        raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+        raw[4] = a.x; raw[5] = a.y; raw[6] = a.z; raw[7] = a.w;
+        raw[8] = b.x; raw[9] = b.y; raw[10] = b.z; raw[11] = b.w;
+    }
+    // Partial sums: acc[0..1] low nibbles (even / odd dwords), acc[2..3]
+    // high nibbles -- four independent chains per row.
+    static constexpr int NACC = 4;
+    __device__ static void accum(const uint32_t (&raw)[NRAW], int t, const float (&xv)[64],
+                                 float (&acc)[NACC]) {
+        const int e = t & 1;
+        nib8(raw[4 + t], &xv[4 * t], &xv[32 + 4 * t], acc[e], acc[2 + e]);
+    }
+    static constexpr int NDW = 8;  // dwords of codes per lane
+    __device__ static float finish(const uint32_t (&raw)[NRAW], int jp, const float (&acc)[NACC],
+                                   const float (&xs)[NG]) {
+        const float d = h2f(raw[0] & 0xFFFF), dmin = h2f(raw[0] >> 16);
+        // sub-blocks 2jp, 2jp+1 (get_scale_min_k4, quant.cpp:427-435), no branches
+        const uint32_t sh = 16u * static_cast<uint32_t>(jp & 1);
+        const uint32_t Y = raw[1] >> sh, Z = raw[2] >> sh, W = raw[3] >> sh;
+        const bool hi = jp >= 2;
+        const uint32_t A = hi ? W : Y, Am = hi ? (W >> 4) : Z, s2 = hi ? 2u : 0u;
+        const uint32_t sa = (A & 15u) | ((Y >> s2) & 0x30u);
+        const uint32_t sb = ((A >> 8) & 15u) | ((Y >> (8u + s2)) & 0x30u);
+        const uint32_t ma = (Am & 15u) | ((Z >> s2) & 0x30u);
+        const uint32_t mb = ((Am >> 8) & 15u) | ((Z >> (8u + s2)) & 0x30u);
+        float a = (d * static_cast<float>(sa) * kTwo24) * (acc[0] + acc[1]);
+        a = __builtin_fmaf(d * static_cast<float>(sb) * kTwo20, acc[2] + acc[3], a);
+        a = __builtin_fmaf(-dmin * static_cast<float>(ma), xs[0], a);
+        return __builtin_fmaf(-dmin * static_cast<float>(mb), xs[1], a);
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int jp, const float (&xv)[64],
+                                const float (&xs)[NG]) {
+        float acc[NACC] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < NDW; t++) accum(raw, t, xv, acc);
+        return finish(raw, jp, acc, xs);
+    }
+};
+
+template <> struct WaveFmt<DT_Q6_K> {
+    // lane slot jp: half h = jp/2, l0 = 16 (jp & 1): values 128h + 32qd + l0 + t,
+    // qd = 0..3, t = 0..15 (four runs of 16); scales sc[8h + (jp&1) + 2qd]
+    static constexpr int LPB = 4, BPS = 16, NG = 4, RUN = 16, NRUN = 4, NRAW = 15;
+    __device__ static int blk_of(int lane) { return lane >> 2; }
+    __device__ static int slot_of(int lane) { return lane & 3; }
+    __device__ static int run_start(int jp, int r) { return 128 * (jp >> 1) + 32 * r + 16 * (jp & 1); }
+    __device__ static int group_of(int i) { return i >> 4; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int jp) {
+        const int h = jp >> 1, l0 = 16 * (jp & 1);
+        uint32_t a[4], b[4], q[4], s[2];
+        load_bytes2<4>(blk + 64 * h + l0, a);
+        load_bytes2<4>(blk + 64 * h + 32 + l0, b);
+        load_bytes2<4>(blk + 128 + 32 * h + l0, q);
+        load_bytes2<2>(blk + 192 + 8 * h, s);
+        const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
+        raw[14] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+#pragma unroll
+        for (int k = 0; k < 4; k++) { raw[k] = a[k]; raw[4 + k] = b[k]; raw[8 + k] = q[k]; }
+        raw[12] = s[0]; raw[13] = s[1];
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int jp, const float (&xv)[64],
+                                const float (&xs)[NG]) {
+        const float d = h2f(raw[14] & 0xFFFF);
+        float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t A = raw[t], B = raw[4 + t], H = raw[8 + t];
+            const uint32_t q[4] = {(A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u),
+                                   (B & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u),
+                                   ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u),
+                                   ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u)};
+#pragma unroll
+            for (int qd = 0; qd < 4; qd++) {
+                const float *x = &xv[16 * qd + 4 * t];
+                sq[qd] = mix2(q[qd] & 0x003F003Fu, x[0], x[2], sq[qd]);
+                sq[qd] = mix2((q[qd] >> 8) & 0x003F003Fu, x[1], x[3], sq[qd]);
+            }
+        }
+        // scale bytes (jp&1) + {0,2} in raw[12], (jp&1) + {4,6} in raw[13]
+        const uint32_t sel = 8u * static_cast<uint32_t>(jp & 1);
+        const uint32_t w0 = raw[12] >> sel, w1 = raw[13] >> sel;
+        const int sc[4] = {static_cast<int8_t>(w0 & 0xFF), static_cast<int8_t>((w0 >> 16) & 0xFF),
+                           static_cast<int8_t>(w1 & 0xFF), static_cast<int8_t>((w1 >> 16) & 0xFF)};
+        float a = 0.0f;
+#pragma unroll
+        for (int qd = 0; qd < 4; qd++) {
+            const float ds = d * static_cast<float>(sc[qd]);
+            a = __builtin_fmaf(ds * kTwo24, sq[qd], a);
+            a = __builtin_fmaf(-32.0f * ds, xs[qd], a);
+        }
+        return a;
+    }
+};
+
+template <> struct WaveFmt<DT_Q4_0> {
+    // lane owns blocks 2*lane, 2*lane+1 of the step: 64 contiguous values
+    static constexpr int LPB = 1, BPS = 128, NG = 2, RUN = 64, NRUN = 1, NRAW = 10;
+    __device__ static int blk_of(int lane) { return 2 * lane; }
+    __device__ static int slot_of(int) { return 0; }
+    __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int i) { return i >> 5; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const uint8_t *b = blk + 18 * u;
+            uint32_t q[4];
+            load_bytes2<4>(b + 2, q);
+            const uintptr_t da = reinterpret_cast<uintptr_t>(b);
+            raw[5 * u + 4] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+#pragma unroll
+            for (int k = 0; k < 4; k++) raw[5 * u + k] = q[k];
         }
     }
-    __device__ static int group_of(int) { return 0; }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[64],
+                                const float (&xs)[NG]) {
+        float a = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const float d = h2f(raw[5 * u + 4] & 0xFFFF);
+            float sl = 0.0f, shi = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                nib8(raw[5 * u + t], &xv[32 * u + 4 * t], &xv[32 * u + 16 + 4 * t], sl, shi);
+            a = __builtin_fmaf(d * kTwo24, sl, a);
+            a = __builtin_fmaf(d * kTwo20, shi, a);
+            a = __builtin_fmaf(-8.0f * d, xs[u], a);
+        }
+        return a;
+    }
+};
+
+template <> struct WaveFmt<DT_Q8_0> {
+    static constexpr int LPB = 1, BPS = 128, NG = 2, RUN = 64, NRUN = 1, NRAW = 18;
+    __device__ static int blk_of(int lane) { return 2 * lane; }
+    __device__ static int slot_of(int) { return 0; }
+    __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int i) { return i >> 5; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const uint8_t *b = blk + 34 * u;
+            uint32_t q[8];
+            load_bytes2<8>(b + 2, q);
+            const uintptr_t da = reinterpret_cast<uintptr_t>(b);
+            raw[9 * u + 8] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+#pragma unroll
+            for (int k = 0; k < 8; k++) raw[9 * u + k] = q[k];
+        }
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[64],
+                                const float (&xs)[NG]) {
+        float a = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const float d = h2f(raw[9 * u + 8] & 0xFFFF);
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const uint32_t v = raw[9 * u + t] ^ 0x80808080u;
+                const float *x = &xv[32 * u + 4 * t];
+                s0 = mix2(v & 0x00FF00FFu, x[0], x[2], s0);
+                s1 = mix2((v >> 8) & 0x00FF00FFu, x[1], x[3], s1);
+            }
+            a = __builtin_fmaf(d * kTwo24, s0 + s1, a);
+            a = __builtin_fmaf(-128.0f * d, xs[u], a);
+        }
+        return a;
+    }
 };
 
 }  // namespace krk
