@@ -42,23 +42,48 @@ def parse():
 
 
 class Timer:
-    """HIP events on the stream the kernels are launched on."""
+    """HIP events on the stream the kernels are launched on.
 
-    def __init__(self, torch, stream):
-        self.t, self.s = torch, stream
+    A Python call through ctypes costs ~13 us of host time, longer than a
+    decode GEMV kernel, so timing a loop of eager calls measures the host.
+    ``run`` therefore captures the calls into a HIP graph (on a side stream,
+    with the backends switched to it) and times graph replays: the kernels
+    then run back to back exactly as a serving loop's graph would run them.
+    """
 
-    def run(self, fn, iters, warmup):
+    def __init__(self, torch, stream, backends):
+        self.t, self.s, self.backends = torch, stream, backends
+
+    def run(self, fn, iters, warmup, graph=True):
+        torch = self.t
         for i in range(warmup):
             fn(i)
-        self.t.cuda.synchronize()
-        e0 = self.t.cuda.Event(enable_timing=True)
-        e1 = self.t.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        if not graph:
+            e0.record(self.s)
+            for i in range(iters):
+                fn(i)
+            e1.record(self.s)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / iters  # ms per call
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        with torch.cuda.graph(g, stream=side):
+            for be in self.backends:
+                be.set_stream(side)
+            for i in range(iters):
+                fn(i)
+        for be in self.backends:
+            be.set_stream(self.s)
+        g.replay()  # warm replay
+        torch.cuda.synchronize()
         e0.record(self.s)
-        for i in range(iters):
-            fn(i)
+        g.replay()
         e1.record(self.s)
-        self.t.cuda.synchronize()
-        return e0.elapsed_time(e1) / iters  # ms per call
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters
 
 
 def rotation(torch, w_host, min_bytes=1 << 30):
@@ -150,7 +175,7 @@ def main():
     stream = torch.cuda.current_stream()
     be32 = K.Backend(0, K.ACT_F32, stream)
     be16 = K.Backend(0, K.ACT_F16, stream)
-    timer = Timer(torch, stream)
+    timer = Timer(torch, stream, (be32, be16))
     extras = {}
 
     # ---- headline: Q4_K GEMV 4096 -> 14336, M = 1 ---------------------------

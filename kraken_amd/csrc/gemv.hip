@@ -116,6 +116,13 @@ static int gemv_mfma_knob() {
     }();
     return v;
 }
+static int gemv_stream_mode_knob() {  // experiment: 1 = no compute, 2 = no DMA
+    static const int v = [] {
+        const char *e = std::getenv("KRK_STREAM_MODE");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v;
+}
 static int gemv_stream_knob() {
     static const int v = [] {
         const char *e = std::getenv("KRK_GEMV_STREAM");
@@ -1046,13 +1053,13 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Rows per group of the streamed kernel.  A unit of work is RB rows x one
-// wave step (4096 values of K); its bytes are RB pieces of P = BPS * BB
-// contiguous bytes, which the DMA gathers into one slot back to back.
-template <int DT> struct StreamCfg { static constexpr int RB = (DT == DT_Q4_K || DT == DT_Q4_0) ? 4 : 2; };
-
-template <int DT, typename XT, typename OT, int RB, int NSLOT>
-__global__ void __launch_bounds__(1024) gemv_stream_kernel(SegTable t, int64_t total, int xfloats) {
+// A unit of work is RB rows x one wave step (4096 values of K); its bytes
+// are RB pieces of P = BPS * BB contiguous bytes that the DMA gathers into a
+// slot back to back.  XREG: the whole row is one step (K <= 4096), so each
+// lane keeps its 64 activations and their group sums in registers for the
+// kernel's lifetime; otherwise x is staged in LDS and read per unit.
+template <int DT, typename XT, typename OT, int RB, int NSLOT, bool XREG>
+__global__ void __launch_bounds__(512) gemv_stream_kernel(SegTable t, int64_t total, int xfloats, int mode) {
     using F = WaveFmt<DT>;
     using D = LdsDot<DT, RB>;
     constexpr int BV = blk_vals(DT), BB = blk_bytes(DT);
@@ -1062,84 +1069,110 @@ __global__ void __launch_bounds__(1024) gemv_stream_kernel(SegTable t, int64_t t
     constexpr int SLOT = CH * 1024;
     constexpr int per_lane = (DT == DT_Q4_0 || DT == DT_Q8_0) ? 2 : 1;
     static_assert(P % 16 == 0, "pieces must be whole 16-byte chunks");
+    static_assert((NSLOT - 1) * CH < 64, "vmcnt is 6 bits");
     extern __shared__ float smem[];
-    float *xl = smem;
     __shared__ Seg segl[kMaxSegs];
+    float *xl = smem;
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    uint8_t *slots = reinterpret_cast<uint8_t *>(smem + xfloats) + wv * (NSLOT * SLOT);
+    uint8_t *slots = reinterpret_cast<uint8_t *>(smem + (XREG ? 0 : xfloats)) + wv * (NSLOT * SLOT);
     const int64_t W = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wv;
     const int64_t NW = static_cast<int64_t>(gridDim.x) * (blockDim.x >> 6);
     const int slot_lane = F::slot_of(lane);
     const int nb = t.n_in / BV;
-    const int nsteps = (nb + F::BPS - 1) / F::BPS;
+    const int nsteps = XREG ? 1 : (nb + F::BPS - 1) / F::BPS;
     const int64_t rb = t.row_bytes;
-    // this wave's units: groups W, W + NW, ... each split into nsteps steps
     const int64_t my_groups = W < total ? (total - 1 - W) / NW + 1 : 0;
     const int64_t my_units = my_groups * nsteps;
 
-    // group g -> segment fields.  The table is copied to LDS first: indexed
-    // in the kernel arguments it would be read through vector memory, and
-    // the waits for those reads would also drain the weight DMA.
+    // The segment table is copied to LDS: indexed in the kernel arguments it
+    // would be read through vector memory, and the waits for those reads
+    // would also drain the weight DMA.
     const int nseg = t.n;
     if (threadIdx.x < nseg) segl[threadIdx.x] = t.seg[threadIdx.x];
     const float inv_acc = t.rexp ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
     __syncthreads();
-    auto locate = [&](int64_t g, const uint8_t *&w, int64_t &n_out, int64_t &n0, void *&out,
-                      int &kind) {
+    auto seg_of = [&](int64_t g) {
         int i = 0;
         while (i + 1 < nseg && g >= segl[i + 1].blk_begin) i++;
-        w = static_cast<const uint8_t *>(segl[i].w);
-        n_out = segl[i].n_out;
-        n0 = (g - segl[i].blk_begin) * RB;
-        out = segl[i].out;
-        kind = segl[i].kind;
+        return i;
     };
+
+    // Chunk c of a unit: lane bytes [1024c + 16 lane, +16) of the RB pieces,
+    // i.e. row r = o / P at offset o % P of the step.  Lanes past U re-read
+    // the unit's first chunk into the slot's unused tail.
+    int32_t dl[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int o = c * 1024 + 16 * lane;
+        const int r = o / P;
+        dl[c] = o < U ? static_cast<int32_t>(r * rb + (o - r * P)) : 16 * lane;
+    }
     auto issue = [&](int64_t j) {
+        if (mode == 2) return;
         const int64_t g = W + (j / nsteps) * NW;
         const int st = static_cast<int>(j % nsteps);
-        const uint8_t *w;
-        int64_t n_out, n0;
-        void *out;
-        int kind;
-        locate(g, w, n_out, n0, out, kind);
-        const int64_t lim = rb - 16;             // last whole chunk of a row
+        const int si = seg_of(g);
+        const uint8_t *w = static_cast<const uint8_t *>(segl[si].w);
+        const int64_t n_out = segl[si].n_out;
+        const int64_t n0 = (g - segl[si].blk_begin) * RB;
+        const uint8_t *base = w + n0 * rb + static_cast<int64_t>(st) * P;
         uint8_t *dst = slots + static_cast<int>(j % NSLOT) * SLOT;
+        if ((n0 + RB - 1) * rb + static_cast<int64_t>(st) * P + P <= n_out * rb) {
 #pragma unroll
-        for (int c = 0; c < CH; c++) {
-            const int o = c * 1024 + 16 * lane;
-            if (c + 1 < CH || o < U) {
-                const int r = o / P;
+            for (int c = 0; c < CH; c++)
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(base + dl[c]),
+                                                 (lds_void_t *)(dst + c * 1024), 16, 0, 0);
+        } else {
+            // the matrix's last rows: clamp rows and row ends to stay inside
+            const int64_t lim = rb - 16;
+#pragma unroll
+            for (int c = 0; c < CH; c++) {
+                const int o = c * 1024 + 16 * lane;
+                const int r = o < U ? o / P : 0;
                 int64_t n = n0 + r;
                 if (n >= n_out) n = n_out - 1;
-                int64_t off = static_cast<int64_t>(st) * P + (o - r * P);
-                if (off > lim) off = lim;        // past the row end: masked lanes read this
+                int64_t off = static_cast<int64_t>(st) * P + (o < U ? o - r * P : 0);
+                if (off > lim) off = lim;
                 __builtin_amdgcn_global_load_lds(static_cast<const void *>(w + n * rb + off),
                                                  (lds_void_t *)(dst + c * 1024), 16, 0, 0);
             }
         }
     };
 
-    // NSLOT - 1 units in flight before anything else
 #pragma unroll
     for (int k = 0; k < NSLOT - 1; k++)
         if (k < my_units) issue(k);
 
-    // stage x once per workgroup (the DMA above overlaps with it)
-    {
-        const XT *x = static_cast<const XT *>(t.seg[0].x);
+    // activations: registers (XREG) or LDS, fetched while the DMA is in flight
+    float xv[XREG ? 64 : 1], xg[XREG ? F::NG : 1];
+    const XT *xsrc = static_cast<const XT *>(t.seg[0].x);
+    if constexpr (XREG) {
+        const int b = F::blk_of(lane);
+        const bool okx = b < nb;
+        const XT *xb = xsrc + static_cast<int64_t>(okx ? b : 0) * BV;
+#pragma unroll
+        for (int r = 0; r < F::NRUN; r++) load_run<F::RUN>(xb + F::run_start(slot_lane, r), &xv[r * F::RUN]);
+#pragma unroll
+        for (int q = 0; q < F::NG; q++) xg[q] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 64; i++) {
+            if (!okx) xv[i] = 0.0f;
+            xg[F::group_of(i)] += xv[i];
+        }
+    } else {
         for (int k = threadIdx.x * 4; k < t.n_in; k += blockDim.x * 4) {
             floatx4 v;
             if constexpr (sizeof(XT) == 4) {
-                v = *reinterpret_cast<const floatx4 *>(x + k);
+                v = *reinterpret_cast<const floatx4 *>(xsrc + k);
             } else {
-                v = floatx4{static_cast<float>(x[k]), static_cast<float>(x[k + 1]),
-                             static_cast<float>(x[k + 2]), static_cast<float>(x[k + 3])};
+                v = floatx4{static_cast<float>(xsrc[k]), static_cast<float>(xsrc[k + 1]),
+                             static_cast<float>(xsrc[k + 2]), static_cast<float>(xsrc[k + 3])};
             }
             *reinterpret_cast<floatx4 *>(xl + xpad(k)) = v;
         }
+        __syncthreads();
     }
-    __syncthreads();
 
     float xs[D::NS];
     int xs_step = -1;
@@ -1153,7 +1186,7 @@ __global__ void __launch_bounds__(1024) gemv_stream_kernel(SegTable t, int64_t t
         if (ahead >= NSLOT - 1) wait_vmcnt<(NSLOT - 1) * CH>();
         else if (NSLOT > 2 && ahead == 1) wait_vmcnt<CH>();
         else wait_vmcnt<0>();
-        const int st = static_cast<int>(j % nsteps);
+        const int st = XREG ? 0 : static_cast<int>(j % nsteps);
         const uint8_t *slot = slots + static_cast<int>(j % NSLOT) * SLOT;
         int b = st * F::BPS + F::blk_of(lane);
         const bool ok = b < nb;
@@ -1162,26 +1195,34 @@ __global__ void __launch_bounds__(1024) gemv_stream_kernel(SegTable t, int64_t t
         uint32_t raw[RB][F::NRAW];
 #pragma unroll
         for (int r = 0; r < RB; r++) F::load(raw[r], slot + r * P + lb * BB, slot_lane);
-        const int b0 = ok ? st * F::BPS * BV + XRuns<DT>::base(lane) : 0;
-        if (xs_step != st) {
-            D::sums(xl, b0, xs);
-            xs_step = nsteps > 1 ? -1 : st;
-        }
         float d[RB];
-        D::run(raw, slot_lane, xl, b0, xs, d);
+        if (mode == 1) {
+#pragma unroll
+            for (int r = 0; r < RB; r++) d[r] = __uint_as_float(raw[r][0] ^ raw[r][F::NRAW - 1]);
+        } else if constexpr (XREG) {
+#pragma unroll
+            for (int r = 0; r < RB; r++) d[r] = F::dot(raw[r], slot_lane, xv, xg);
+        } else {
+            const int b0 = ok ? st * F::BPS * BV + XRuns<DT>::base(lane) : 0;
+            if (xs_step != st) {
+                D::sums(xl, b0, xs);
+                xs_step = nsteps > 1 ? -1 : st;
+            }
+            D::run(raw, slot_lane, xl, b0, xs, d);
+        }
 #pragma unroll
         for (int r = 0; r < RB; r++) v[r] += ok ? d[r] : 0.0f;
-        if (st == nsteps - 1) {
+        if (XREG || st == nsteps - 1) {
             const int64_t g = W + (j / nsteps) * NW;
-            const uint8_t *w;
-            int64_t n_out, n0;
-            void *out;
-            int kind;
-            locate(g, w, n_out, n0, out, kind);
+            const int si = seg_of(g);
+            const int64_t n0 = (g - segl[si].blk_begin) * RB;
             wave_reduce_multi<RB>(v, lane);
             if (reduce_owner<RB>(lane)) {
                 const int64_t n = n0 + reduce_owner_index<RB>(lane);
-                if (n < n_out) store_out<OT>(static_cast<OT *>(out) + n, v[0], kind, kind == SEG_ACC ? inv_acc : 1.0f);
+                const int kind = segl[si].kind;
+                if (n < segl[si].n_out)
+                    store_out<OT>(static_cast<OT *>(segl[si].out) + n, v[0], kind,
+                                  kind == SEG_ACC ? inv_acc : 1.0f);
             }
 #pragma unroll
             for (int r = 0; r < RB; r++) v[r] = 0.0f;
@@ -1189,7 +1230,7 @@ __global__ void __launch_bounds__(1024) gemv_stream_kernel(SegTable t, int64_t t
     }
 }
 
-template <int DT, typename XT, typename OT, int RB, int NSLOT>
+template <int DT, typename XT, typename OT, int RB, int NSLOT, bool XREG>
 static hipError_t launch_stream(SegTable t, hipStream_t st) {
     constexpr int SLOT = ((RB * WaveFmt<DT>::BPS * blk_bytes(DT) + 1023) / 1024) * 1024;
     int64_t total = 0;
@@ -1197,23 +1238,31 @@ static hipError_t launch_stream(SegTable t, hipStream_t st) {
         t.seg[i].blk_begin = total;
         total += (t.seg[i].n_out + RB - 1) / RB;
     }
-    const int xfloats = (t.n_in + 4 * (t.n_in / 64) + 4 + 3) & ~3;
-    const size_t xbytes = static_cast<size_t>(xfloats) * sizeof(float) + sizeof(Seg) * kMaxSegs;
+    const int xfloats = XREG ? 0 : (t.n_in + 4 * (t.n_in / 64) + 4 + 3) & ~3;
+    const size_t xbytes = static_cast<size_t>(xfloats) * sizeof(float);
     const size_t per_wave = static_cast<size_t>(NSLOT) * SLOT;
-    constexpr size_t kLds = 160u * 1024u;
-    // waves per workgroup: the most resident waves per CU (at most 4 per
-    // SIMD), ties to the larger workgroup (x is staged once per workgroup)
-    int best_nw = 0, best_waves = 0;
-    for (int nw = 1; nw <= 16; nw++) {
-        const size_t l = xbytes + nw * per_wave;
-        if (l > kLds) break;
-        int per_cu = static_cast<int>(kLds / l);
-        if (per_cu * nw > 16) per_cu = 16 / nw;
-        if (per_cu * nw >= best_waves) { best_waves = per_cu * nw; best_nw = nw; }
+    // waves per workgroup: the most resident waves per CU, ties to the
+    // larger workgroup (fewer x stagings); occupancy per shape is cached
+    struct Pick { int n_in, nw, per_cu; };
+    static Pick cache[8] = {};
+    int nw = 0, per_cu = 0;
+    for (const Pick &c : cache)
+        if (c.nw && c.n_in == (XREG ? 0 : t.n_in)) { nw = c.nw; per_cu = c.per_cu; break; }
+    if (!nw) {
+        int best = 0;
+        for (int cand = 1; cand <= 8; cand++) {
+            const size_t lds = xbytes + cand * per_wave;
+            if (lds + sizeof(Seg) * kMaxSegs > 160u * 1024u) break;
+            int blocks = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                    &blocks, gemv_stream_kernel<DT, XT, OT, RB, NSLOT, XREG>, 64 * cand, lds) != hipSuccess)
+                blocks = 0;
+            if (blocks * cand >= best && blocks > 0) { best = blocks * cand; nw = cand; per_cu = blocks; }
+        }
+        if (!nw) return hipErrorInvalidValue;
+        for (Pick &c : cache)
+            if (!c.nw) { c = Pick{XREG ? 0 : t.n_in, nw, per_cu}; break; }
     }
-    if (!best_nw) return hipErrorInvalidValue;
-    const int nw = best_nw;
-    const size_t lds = xbytes - sizeof(Seg) * kMaxSegs + nw * per_wave;  // dynamic part
     static int cus = 0;
     if (!cus) {
         int dev = 0;
@@ -1221,10 +1270,10 @@ static hipError_t launch_stream(SegTable t, hipStream_t st) {
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             cus = 256;
     }
-    int64_t grid = static_cast<int64_t>(cus) * (best_waves / nw);
+    int64_t grid = static_cast<int64_t>(cus) * per_cu;
     if (grid * nw > total) grid = (total + nw - 1) / nw;
-    hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, RB, NSLOT>), dim3(static_cast<unsigned>(grid)),
-                       dim3(64 * nw), lds, st, t, total, xfloats);
+    hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, RB, NSLOT, XREG>), dim3(static_cast<unsigned>(grid)),
+                       dim3(64 * nw), xbytes + nw * per_wave, st, t, total, xfloats, gemv_stream_mode_knob());
     return hipGetLastError();
 }
 
@@ -1236,20 +1285,25 @@ static int gemv_stream_cfg_knob() {  // experiment: RB * 10 + NSLOT, 0 = default
     return v;
 }
 
-template <int DT, typename XT, typename OT>
-static hipError_t launch_stream(const SegTable &t, hipStream_t st) {
+template <int DT, typename XT, typename OT, bool XREG>
+static hipError_t launch_stream_x(const SegTable &t, hipStream_t st) {
     if constexpr (sizeof(XT) == 4 && sizeof(OT) == 4 && (DT == DT_Q4_K || DT == DT_Q6_K)) {
         switch (gemv_stream_cfg_knob()) {
-            case 43: return launch_stream<DT, XT, OT, 4, 3>(t, st);
-            case 42: return launch_stream<DT, XT, OT, 4, 2>(t, st);
-            case 23: return launch_stream<DT, XT, OT, 2, 3>(t, st);
-            case 22: return launch_stream<DT, XT, OT, 2, 2>(t, st);
-            case 13: return launch_stream<DT, XT, OT, 1, 3>(t, st);
-            case 12: return launch_stream<DT, XT, OT, 1, 2>(t, st);
+            case 43: return launch_stream<DT, XT, OT, 4, 3, XREG>(t, st);
+            case 42: return launch_stream<DT, XT, OT, 4, 2, XREG>(t, st);
+            case 23: return launch_stream<DT, XT, OT, 2, 3, XREG>(t, st);
+            case 22: return launch_stream<DT, XT, OT, 2, 2, XREG>(t, st);
+            case 12: return launch_stream<DT, XT, OT, 1, 2, XREG>(t, st);
             default: break;
         }
     }
-    return launch_stream<DT, XT, OT, StreamCfg<DT>::RB, 2>(t, st);
+    return launch_stream<DT, XT, OT, 2, 2, XREG>(t, st);
+}
+
+template <int DT, typename XT, typename OT>
+static hipError_t launch_stream(const SegTable &t, hipStream_t st) {
+    return t.n_in <= WaveFmt<DT>::BPS * blk_vals(DT) ? launch_stream_x<DT, XT, OT, true>(t, st)
+                                                     : launch_stream_x<DT, XT, OT, false>(t, st);
 }
 
 template <int DT, typename XT, typename OT>
@@ -1419,6 +1473,7 @@ static hipError_t dispatch_dt(int dt, const SegTable &t, hipStream_t st) {
 }
 
 hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st) {
+    if (gemv_digits_ok(dt, t)) return gemv_digits(act_f16, t, st);
     if (act_f16) return dispatch_dt<_Float16, _Float16>(dt, t, st);
     return dispatch_dt<float, float>(dt, t, st);
 }

@@ -1,0 +1,469 @@
+// gemv_digits.hip -- Q4_K decode GEMV on the int8 matrix cores.
+//
+// Decode GEMV (rows == 1) is bound by HBM, but with a 4-bit format the VALU
+// work of a dequantize-and-FMA loop (one v_fma_mix per weight plus the
+// nibble unpacking, scales and reductions: ~2.8 VALU ops per weight) costs
+// as much time as the bytes.  Here the products run on the int8 MFMA:
+//
+//   * B operand: the weight codes themselves.  Sixteen low (or high)
+//     nibbles of a lane's four code dwords are sixteen int8 values after a
+//     single AND (and a shift for the high ones): 0.375 VALU ops per weight.
+//   * A operand: the activations as exact integers.  Each 32-value
+//     sub-block of x is scaled by a power of two so that its largest value
+//     has 22 bits, rounded to an integer X (error <= 2^-23 of the sub-block
+//     maximum) and split into three balanced int8 digits,
+//     X = d0 + 2^8 d1 + 2^16 d2.  Rows 4s'+p of A hold digit plane p of
+//     sub-block s', zero elsewhere, so one 16x16x64 MFMA yields for every
+//     weight row (column) and sub-block the three exact int32 plane sums.
+//   * The Q4_K block formula (src/quant.cpp:427-447, dequant_q4_K with
+//     get_scale_min_k4) is applied to the plane sums once per (row,
+//     sub-block):  y += d*sc * 2^-e * (C0 + 2^8 C1 + 2^16 C2) - dmin*m * sum(x).
+//
+// The products are exact; the result differs from the f32 reference chain
+// only by the 2^-23 activation rounding and f32 accumulation order, far
+// inside the 1e-5 relative budget.
+//
+// Data movement: each wave streams units of 16*RGN rows x 256*KB values
+// (RGN*16 row pieces of KB*144 contiguous bytes) into a private LDS slot
+// with global_load_lds_dwordx4 -- every weight byte is delivered once and
+// coalesced -- while the digit table of x is built once per workgroup.
+// NSLOT slots keep NSLOT-1 units in flight during the decode.
+#include <cstdlib>
+
+#include "gemv_core.hpp"
+#include "krk_formats.hpp"
+#include "krk_kernels.hpp"
+
+namespace krk {
+
+namespace {
+
+#ifdef KRK_TRACE
+__device__ uint64_t g_trace[4096 * 16];
+#define TRACE(k) do { if (lane == 0 && W_ < 4096) g_trace[W_ * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define TRACE(k) do { } while (0)
+#endif
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+template <int N> __device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    // s_waitcnt simm16: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+constexpr int kTabBlk = 768;   // digit bytes per 256-value block: 8 sub-blocks x 3 planes x 32
+constexpr int kZero = 512;     // zero bytes read by lanes whose A row is empty
+constexpr int kMaxK = 16384;
+constexpr int kXPasses = 8;  // x sub-blocks staged per thread (4 threads per sub-block)
+
+__device__ __forceinline__ v4i ld_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
+
+template <typename XT, typename OT, int RGN, int KB, int NSLOT>
+__global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_t total, int nks, int nwc,
+                                                               int mode, int late_knob) {
+    constexpr int BB = 144;
+    constexpr int P = KB * BB;                   // row piece of one unit
+    constexpr int ROWS = 16 * RGN;
+    constexpr int U = ROWS * P;
+    constexpr int CH = (U + 1023) / 1024;
+    constexpr int SLOT = CH * 1024;
+    static_assert((NSLOT - 1) * CH < 64, "vmcnt is 6 bits");
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ Seg segl[kMaxSegs];
+    const int nb = t.n_in / 256;
+    uint8_t *tab = lds;                               // [nb][8][3][32] int8 digits
+    uint8_t *zero = tab + nb * kTabBlk;               // kZero zero bytes
+    float2 *ex = reinterpret_cast<float2 *>(zero + kZero);  // [nb * 8] {2^-e, sum x}
+    uint8_t *slots0 = reinterpret_cast<uint8_t *>(ex + nb * 8);
+    float *red = reinterpret_cast<float *>(slots0 + nwc * (NSLOT * SLOT));  // [2][nwc][ROWS]
+
+    // Every wave streams, multiplies and builds a share of the digit table.
+    // The vector-memory counter of a wave is in order, so each wave issues
+    // its x loads FIRST, then its weight DMA, and waits only until the DMA
+    // instructions remain outstanding: x has then arrived, the weights keep
+    // streaming while the table is built.
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t W_ = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wv;
+    (void)W_;
+    TRACE(0);
+    uint8_t *slots = slots0 + wv * (NSLOT * SLOT);
+    const int64_t rb = t.row_bytes;
+    // A workgroup owns tiles of ROWS rows (tiles blockIdx.x, + gridDim.x, ...);
+    // its waves split K: wave wv takes the units ks = wv, wv + nwc, ...
+    const int64_t my_tiles = blockIdx.x < total ? (total - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+    const int cnt = wv < nks ? (nks - 1 - wv) / nwc + 1 : 0;
+    const int64_t my_units = my_tiles * cnt;
+
+    const int nseg = t.n;
+    auto seg_w = [&](int64_t g, const Seg *tab_) {
+        int i = 0;
+        while (i + 1 < nseg && g >= tab_[i + 1].blk_begin) i++;
+        return i;
+    };
+
+    // chunk c, lane l: slot bytes [1024c + 16l, +16) = row o / P, offset o % P
+    int32_t dl[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int o = c * 1024 + 16 * lane;
+        const int r = o / P;
+        dl[c] = o < U ? static_cast<int32_t>(r * rb + (o - r * P)) : 0;
+    }
+    // the first units read the segment table from the kernel arguments (the
+    // LDS copy is not ready yet); later ones from LDS
+    auto issue = [&](int64_t j, const Seg *tab_) {
+        if (mode == 2) return;
+        const int64_t g = blockIdx.x + (j / cnt) * gridDim.x;
+        const int ks = wv + static_cast<int>(j % cnt) * nwc;
+        const int si = seg_w(g, tab_);
+        const uint8_t *w = static_cast<const uint8_t *>(tab_[si].w);
+        const int64_t n_out = tab_[si].n_out;
+        const int64_t n0 = (g - tab_[si].blk_begin) * ROWS;
+        const int64_t k0 = static_cast<int64_t>(ks) * P;
+        uint8_t *dst = slots + static_cast<int>(j % NSLOT) * SLOT;
+        if ((n0 + ROWS - 1) * rb + k0 + P <= n_out * rb) {
+            const uint8_t *base = w + n0 * rb + k0;
+#pragma unroll
+            for (int c = 0; c < CH; c++)
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(base + dl[c]),
+                                                 (lds_void_t *)(dst + c * 1024), 16, 0, 0);
+        } else {
+            // the matrix's last rows: clamp rows and row ends to stay inside
+            const int64_t lim = rb - 16;
+#pragma unroll
+            for (int c = 0; c < CH; c++) {
+                const int o = c * 1024 + 16 * lane;
+                const int r = o < U ? o / P : 0;
+                int64_t n = n0 + r;
+                if (n >= n_out) n = n_out - 1;
+                int64_t off = k0 + (o < U ? o - r * P : 0);
+                if (off > lim) off = lim;
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(w + n * rb + off),
+                                                 (lds_void_t *)(dst + c * 1024), 16, 0, 0);
+            }
+        }
+    };
+
+    // ---- x loads (four threads per 32-value sub-block, kXPasses passes)
+    const XT *x = static_cast<const XT *>(t.seg[0].x);
+    const int q = threadIdx.x & 3;
+    const int nsb = mode == 3 ? 0 : nb * 8;
+    float xv[kXPasses][8];
+#pragma unroll
+    for (int u = 0; u < kXPasses; u++) {
+        const int sb = (threadIdx.x >> 2) + u * (blockDim.x >> 2);
+        const XT *xp = x + (sb < nsb ? sb : 0) * 32 + 8 * q;
+        if (u * (blockDim.x >> 2) >= nsb) break;   // uniform
+        if constexpr (sizeof(XT) == 4) {
+            const floatx4 u0 = *reinterpret_cast<const floatx4 *>(xp);
+            const floatx4 u1 = *reinterpret_cast<const floatx4 *>(xp + 4);
+            xv[u][0] = u0.x; xv[u][1] = u0.y; xv[u][2] = u0.z; xv[u][3] = u0.w;
+            xv[u][4] = u1.x; xv[u][5] = u1.y; xv[u][6] = u1.z; xv[u][7] = u1.w;
+        } else {
+            const half8 h = *reinterpret_cast<const half8 *>(xp);
+#pragma unroll
+            for (int k = 0; k < 8; k++) xv[u][k] = static_cast<float>(h[k]);
+        }
+    }
+    // ---- weight DMA of the first NSLOT units, then wait for x only.  The
+    // last `late` waves issue theirs after the table: a wave stalls while
+    // the memory pipeline cannot take its DMA, and those waves build the
+    // table meanwhile.
+    const int late = late_knob < nwc / 2 ? late_knob : nwc / 2;
+    const bool early = wv < nwc - late;
+    const int first = my_units < NSLOT ? static_cast<int>(my_units) : NSLOT;
+    if (early) {
+#pragma unroll
+        for (int k = 0; k < NSLOT; k++)
+            if (k < first) issue(k, t.seg);
+        TRACE(14);
+        if (first >= 2) wait_vm<2 * CH>();
+        else if (first == 1) wait_vm<CH>();
+        else wait_vm<0>();
+    } else {
+        wait_vm<0>();
+    }
+    TRACE(13);
+
+    // ---- digit table of x
+    for (int i = threadIdx.x; i < kZero / 4; i += blockDim.x) reinterpret_cast<uint32_t *>(zero)[i] = 0u;
+#pragma unroll
+    for (int u = 0; u < kXPasses; u++) {
+        const int sb = (threadIdx.x >> 2) + u * (blockDim.x >> 2);
+        if (u * (blockDim.x >> 2) >= nsb) break;   // uniform
+        const float *v = xv[u];
+        float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            amax = fmaxf(amax, fabsf(v[k]));
+            sum += v[k];
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        sum += __shfl_xor(sum, 1, 64);
+        sum += __shfl_xor(sum, 2, 64);
+        if (sb >= nsb) continue;
+        // 2^e with |x| * 2^e < 2^22: from amax's exponent field E (amax in
+        // [2^(E-127), 2^(E-126))), e = 149 - E, kept where 2^e and 2^-e
+        // are normal floats; zero and non-finite sub-blocks get no digits
+        const uint32_t Eb = (__float_as_uint(amax) >> 23) & 255u;
+        const bool live = amax > 0.0f && Eb < 255u;
+        int e = live ? 149 - static_cast<int>(Eb) : 0;
+        e = e > 126 ? 126 : e;
+        const float up = __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
+        const float dn = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+        uint32_t p0[2] = {0u, 0u}, p1[2] = {0u, 0u}, p2[2] = {0u, 0u};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int X = live ? static_cast<int>(__builtin_rintf(v[k] * up)) : 0;
+            const int d0 = ((X + 128) & 255) - 128;
+            const int X1 = (X - d0) >> 8;
+            const int d1 = ((X1 + 128) & 255) - 128;
+            const int d2 = (X1 - d1) >> 8;    // |d2| <= 64
+            const int sh = 8 * (k & 3);
+            p0[k >> 2] |= (static_cast<uint32_t>(d0) & 255u) << sh;
+            p1[k >> 2] |= (static_cast<uint32_t>(d1) & 255u) << sh;
+            p2[k >> 2] |= (static_cast<uint32_t>(d2) & 255u) << sh;
+        }
+        uint8_t *o = tab + (sb >> 3) * kTabBlk + (sb & 7) * 96 + 8 * q;
+        *reinterpret_cast<u32x2 *>(o) = u32x2{p0[0], p0[1]};
+        *reinterpret_cast<u32x2 *>(o + 32) = u32x2{p1[0], p1[1]};
+        *reinterpret_cast<u32x2 *>(o + 64) = u32x2{p2[0], p2[1]};
+        if (q == 0) ex[sb] = float2{live ? dn : 1.0f, sum};
+    }
+    if (threadIdx.x < nseg) segl[threadIdx.x] = t.seg[threadIdx.x];
+    if (!early) {
+#pragma unroll
+        for (int k = 0; k < NSLOT; k++)
+            if (k < first) issue(k, t.seg);
+    }
+    const float inv_acc = t.rexp ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
+    __syncthreads();
+    TRACE(1);
+
+    // ---- per-lane roles
+    const int c16 = lane & 15;      // B column = row within a row group; A row
+    const int gq = lane >> 4;       // k group of the lane (bytes 16 gq .. +15 of a 64-byte half)
+    const int ap = c16 & 3, as = c16 >> 2;  // A row = 4 * sub-block' + digit plane
+    const int sl = 2 * (gq >> 1);           // sub-block' of this lane's low-nibble MFMA
+    const bool a_lo = ap < 3 && as == sl, a_hi = ap < 3 && as == sl + 1;
+    const int a_off = as * 96 + ap * 32 + 16 * (gq & 1);
+    // A addresses advance by one table block per 256 values; empty lanes stay
+    // on the zero area (the h = 1 half is reached by an immediate offset)
+    const uint8_t *a_lo_p = a_lo ? tab + a_off : zero;
+    const uint8_t *a_hi_p = a_hi ? tab + a_off : zero;
+    const int a_lo_inc = a_lo ? kTabBlk : 0, a_hi_inc = a_hi ? kTabBlk : 0;
+    const uint32_t M = 0x0F0F0F0Fu;
+    const uint32_t bsh = 8u * static_cast<uint32_t>(gq);
+
+    int64_t j = 0;
+    for (int64_t ti = 0; ti < my_tiles; ti++) {
+        float acc[RGN];
+#pragma unroll
+        for (int r = 0; r < RGN; r++) acc[r] = 0.0f;
+        for (int kk = 0; kk < cnt; kk++, j++) {
+            // units j + 1 .. j + NSLOT - 1 may still be in flight
+            const int64_t ahead = my_units - 1 - j;
+            if (ahead >= NSLOT - 1) wait_vm<(NSLOT - 1) * CH>();
+            else if (NSLOT > 2 && ahead == 1) wait_vm<CH>();
+            else wait_vm<0>();
+            const int ks = wv + kk * nwc;
+            const uint8_t *slot = slots + static_cast<int>(j % NSLOT) * SLOT;
+            // the unit's bytes -> registers, then its slot takes unit j + NSLOT
+            u32x4 hdr[KB][RGN], qa[KB][RGN], qb[KB][RGN];
+#pragma unroll
+            for (int b = 0; b < KB; b++)
+#pragma unroll
+                for (int rg = 0; rg < RGN; rg++) {
+                    const uint8_t *rp = slot + (rg * 16 + c16) * P + b * BB;
+                    hdr[b][rg] = *reinterpret_cast<const u32x4 *>(rp);
+                    qa[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 16 + 16 * gq);
+                    qb[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 80 + 16 * gq);
+                }
+            __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+            if (j + NSLOT < my_units) issue(j + NSLOT, segl);
+            if (j < 4) TRACE(2 + 3 * j);
+            if (mode == 1) continue;
+#pragma unroll
+            for (int b = 0; b < KB; b++) {
+                const int blk = ks * KB + b;
+                if (KB > 1 && blk >= nb) break;
+                const uint8_t *alp = a_lo_p + blk * a_lo_inc;
+                const uint8_t *ahp = a_hi_p + blk * a_hi_inc;
+                const v4i A0l = ld_v4i(alp), A1l = ld_v4i(alp + 384);
+                const v4i A0h = ld_v4i(ahp), A1h = ld_v4i(ahp + 384);
+                // this lane's sub-blocks gq (h = 0) and 4 + gq (h = 1) of block blk
+                const float2 ex0 = ex[blk * 8 + gq], ex1 = ex[blk * 8 + 4 + gq];
+#pragma unroll
+                for (int rg = 0; rg < RGN; rg++) {
+                    const u32x4 hd = hdr[b][rg], q0 = qa[b][rg], q1 = qb[b][rg];
+                    const v4i B0l = {static_cast<int>(q0.x & M), static_cast<int>(q0.y & M),
+                                     static_cast<int>(q0.z & M), static_cast<int>(q0.w & M)};
+                    const v4i B0h = {static_cast<int>((q0.x >> 4) & M), static_cast<int>((q0.y >> 4) & M),
+                                     static_cast<int>((q0.z >> 4) & M), static_cast<int>((q0.w >> 4) & M)};
+                    const v4i B1l = {static_cast<int>(q1.x & M), static_cast<int>(q1.y & M),
+                                     static_cast<int>(q1.z & M), static_cast<int>(q1.w & M)};
+                    const v4i B1h = {static_cast<int>((q1.x >> 4) & M), static_cast<int>((q1.y >> 4) & M),
+                                     static_cast<int>((q1.z >> 4) & M), static_cast<int>((q1.w >> 4) & M)};
+                    const v4i z = {0, 0, 0, 0};
+                    v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0l, B0l, z, 0, 0, 0);
+                    C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0h, B0h, C0, 0, 0, 0);
+                    v4i C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1l, B1l, z, 0, 0, 0);
+                    C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1h, B1h, C1, 0, 0, 0);
+                    // scales of sub-blocks gq and 4 + gq (get_scale_min_k4,
+                    // src/quant.cpp:427-435): bytes gq of scales[0..3], [4..7], [8..11]
+                    const uint32_t s1 = hd.y >> bsh, s2 = hd.z >> bsh, s3 = hd.w >> bsh;
+                    const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
+                    const float sc0 = static_cast<float>(s1 & 63u), m0 = static_cast<float>(s2 & 63u);
+                    const float sc1 = static_cast<float>((s3 & 15u) | ((s1 >> 2) & 0x30u));
+                    const float m1 = static_cast<float>(((s3 >> 4) & 15u) | ((s2 >> 2) & 0x30u));
+                    const int S0 = C0[0] + (C0[1] << 8) + (C0[2] << 16);
+                    const int S1 = C1[0] + (C1[1] << 8) + (C1[2] << 16);
+                    float a = acc[rg];
+                    a = __builtin_fmaf(d * sc0, ex0.x * static_cast<float>(S0), a);
+                    a = __builtin_fmaf(-dmin * m0, ex0.y, a);
+                    a = __builtin_fmaf(d * sc1, ex1.x * static_cast<float>(S1), a);
+                    a = __builtin_fmaf(-dmin * m1, ex1.y, a);
+                    acc[rg] = a;
+                }
+            }
+        }
+        if (j >= 1 && j - 1 < 4) TRACE(3 + 3 * (j - 1));
+        // partial sums of the compute waves -> LDS, then one thread per row
+        // adds them in wave order and stores the row
+        float *rbuf = red + (ti & 1) * nwc * ROWS;
+#pragma unroll
+        for (int rg = 0; rg < RGN; rg++) {
+            float v = acc[rg];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            if (gq == 0) rbuf[wv * ROWS + rg * 16 + c16] = v;
+        }
+        __syncthreads();
+        if (ti < 4) TRACE(4 + 3 * ti);
+        if (threadIdx.x < ROWS) {
+            float v = 0.0f;
+            for (int k = 0; k < nwc; k++) v += rbuf[k * ROWS + threadIdx.x];
+            const int64_t g = blockIdx.x + ti * gridDim.x;
+            const int si = seg_w(g, segl);
+            const int64_t n = (g - segl[si].blk_begin) * ROWS + threadIdx.x;
+            if (n < segl[si].n_out) {
+                const int kind = segl[si].kind;
+                store_out<OT>(static_cast<OT *>(segl[si].out) + n, v, kind,
+                              kind == SEG_ACC ? inv_acc : 1.0f);
+            }
+        }
+    }
+    TRACE(15);
+}
+
+int mode_knob() {  // experiment: 1 = no compute, 2 = no DMA, 3 = no x table
+    static const int v = [] {
+        const char *e = std::getenv("KRK_DIGITS_MODE");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v;
+}
+
+int late_knob() {
+    static const int v = [] {
+        const char *e = std::getenv("KRK_DIGITS_LATE");
+        return e ? std::atoi(e) : 4;
+    }();
+    return v;
+}
+
+int cfg_knob() {  // experiment: RGN * 100 + KB * 10 + NSLOT, 0 = default
+    static const int v = [] {
+        const char *e = std::getenv("KRK_DIGITS_CFG");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v;
+}
+
+template <typename XT, typename OT, int RGN, int KB, int NSLOT>
+hipError_t launch(SegTable t, hipStream_t st) {
+    constexpr int ROWS = 16 * RGN;
+    constexpr int SLOT = ((ROWS * KB * 144 + 1023) / 1024) * 1024;
+    int64_t total = 0;
+    for (int i = 0; i < t.n; i++) {
+        t.seg[i].blk_begin = total;
+        total += (t.seg[i].n_out + ROWS - 1) / ROWS;
+    }
+    const int nb = t.n_in / 256;
+    const int nks = (nb + KB - 1) / KB;
+    const size_t fixed = static_cast<size_t>(nb) * kTabBlk + kZero + static_cast<size_t>(nb) * 8 * sizeof(float2);
+    const size_t per_wave = static_cast<size_t>(NSLOT) * SLOT + 2 * ROWS * sizeof(float);
+    // kXPasses sub-blocks per thread (4 threads each) must cover nb * 8
+    const int min_nw = (nb * 8 * 4 + 64 * kXPasses - 1) / (64 * kXPasses);
+    struct Pick { int nb, nw, per_cu; };
+    static Pick cache[16] = {};
+    int nw = 0, per_cu = 0;
+    for (const Pick &c : cache)
+        if (c.nw && c.nb == nb) { nw = c.nw; per_cu = c.per_cu; break; }
+    if (!nw) {
+        int best = 0;
+        for (int cand = min_nw; cand <= 8; cand++) {
+            const size_t l = fixed + cand * per_wave;
+            if (l + sizeof(Seg) * kMaxSegs > 160u * 1024u) break;
+            int blocks = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                    &blocks, gemv_q4k_digits_kernel<XT, OT, RGN, KB, NSLOT>, 64 * cand, l) != hipSuccess)
+                blocks = 0;
+            if (blocks > 0 && blocks * cand >= best) { best = blocks * cand; nw = cand; per_cu = blocks; }
+        }
+        if (!nw) return hipErrorNotSupported;
+        for (Pick &c : cache)
+            if (!c.nw) { c = Pick{nb, nw, per_cu}; break; }
+    }
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    int64_t grid = static_cast<int64_t>(cus) * per_cu;
+    if (grid > total) grid = total;
+    hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, RGN, KB, NSLOT>), dim3(static_cast<unsigned>(grid)),
+                       dim3(64 * nw), fixed + nw * per_wave, st, t, total, nks, nw, mode_knob(), late_knob());
+    return hipGetLastError();
+}
+
+template <typename XT, typename OT>
+hipError_t dispatch(const SegTable &t, hipStream_t st) {
+    switch (cfg_knob()) {
+        case 222: return launch<XT, OT, 2, 2, 2>(t, st);
+        case 223: return launch<XT, OT, 2, 2, 3>(t, st);
+        case 212: return launch<XT, OT, 2, 1, 2>(t, st);
+        case 213: return launch<XT, OT, 2, 1, 3>(t, st);
+        case 122: return launch<XT, OT, 1, 2, 2>(t, st);
+        case 113: return launch<XT, OT, 1, 1, 3>(t, st);
+        default:
+            // K <= 8192: 32-row tiles of two blocks per unit; longer rows:
+            // 16-row tiles (more tiles for the K-split to spread over)
+            return t.n_in <= 8192 ? launch<XT, OT, 2, 2, 2>(t, st) : launch<XT, OT, 1, 2, 2>(t, st);
+    }
+}
+
+}  // namespace
+
+bool gemv_digits_ok(int dt, const SegTable &t) {
+    if (dt != DT_Q4_K || t.rows != 1 || t.n_in % 256 || t.n_in > kMaxK || t.row_bytes % 16) return false;
+    if (std::getenv("KRK_DIGITS") && std::atoi(std::getenv("KRK_DIGITS")) == 0) return false;
+    for (int i = 0; i < t.n; i++) {
+        if (t.seg[i].kind == SEG_SILU || t.seg[i].x != t.seg[0].x) return false;
+        if (reinterpret_cast<uintptr_t>(t.seg[i].w) & 15) return false;
+    }
+    return true;
+}
+
+hipError_t gemv_digits(bool act_f16, const SegTable &t, hipStream_t st) {
+    return act_f16 ? dispatch<_Float16, _Float16>(t, st) : dispatch<float, float>(t, st);
+}
+
+}  // namespace krk
