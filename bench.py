@@ -38,6 +38,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="", help="comma list: gemv,gemm,head,layer,moe")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="counter run: 5 plain copies of 256 MiB, then 20 headline GEMVs")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="turn two rocprofv3 --pmc counter_collection.csv files of a "
+                         "--pmc-pass run into the traffic summary (printed)")
     return ap.parse_args()
 
 
@@ -144,6 +149,66 @@ def cpu_baseline(O, w, x, n_out, n_in, seconds):
             "one_core_GBps": nbytes / dt_one / 1e9}
 
 
+COPY_BYTES = 256 << 20
+
+
+def pmc_pass():
+    """The program the HBM-traffic counters are read on: a plain copy of known
+    size (the calibration) and the headline GEMV, eagerly, on one stream."""
+    import torch
+
+    import kraken_amd as K
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    be = K.Backend(0, K.ACT_F32)
+    n_out, n_in = 14336, 4096
+    w = K.quantize(K.Q4_K, K.synth_normal(n_out * n_in, seed=1, std=0.02), n_out, n_in, 16)
+    ws = rotation(torch, w)
+    x = torch.from_numpy(K.synth_normal(n_in, seed=2)).cuda()
+    out = torch.empty((1, n_out), dtype=torch.float32, device="cuda")
+    for i in range(20):
+        be.gemm(out, x, ws[i % len(ws)], K.Q4_K, n_out, n_in, 1)
+    torch.cuda.synchronize()
+    be.close()
+
+
+def summarize_pmc(fetch_csv, write_csv):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the copy and the GEMV,
+    the copy's counter/true-bytes factor, and the GEMV's HBM bytes."""
+    import csv
+    import statistics
+
+    def per_kernel(path, counter):
+        # per dispatch: the calibration copies are the largest copy dispatches
+        # (the 256 MiB ones; the weight clones are smaller), the GEMV is ours
+        copies, gemv = [], []
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            v = float(r["Counter_Value"])
+            if "krk::" in r["Kernel_Name"]:
+                gemv.append(v)
+            elif "copyBuffer" in r["Kernel_Name"]:
+                copies.append(v)
+        top = max(copies)
+        cal = [v for v in copies if v > 0.9 * top]
+        return {"copy": statistics.median(cal), "gemv": statistics.median(gemv),
+                "n_copy": len(cal), "n_gemv": len(gemv)}
+
+    f, w = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
+    kib = COPY_BYTES / 1024.0
+    rf, rw = f["copy"] / kib, w["copy"] / kib
+    gf, gw = f["gemv"] / rf * 1024.0, w["gemv"] / rw * 1024.0
+    return {"copy_dispatches": f["n_copy"], "gemv_dispatches": f["n_gemv"],
+            "copy_fetch_kib": f["copy"], "copy_write_kib": w["copy"], "copy_true_kib": kib,
+            "fetch_factor": rf, "write_factor": rw, "gemv_fetch_kib": f["gemv"],
+            "gemv_write_kib": w["gemv"], "gemv_fetch_bytes": gf, "gemv_write_bytes": gw,
+            "hbm_bytes_per_launch": gf + gw}
+
+
 def read_traffic():
     p = os.path.join(ROOT, "profiles", "q4k_gemv_4096x14336_traffic.txt")
     if not os.path.exists(p):
@@ -161,10 +226,17 @@ def read_traffic():
 
 def main():
     args = parse()
+    if args.summarize_pmc:
+        for k, v in summarize_pmc(*args.summarize_pmc).items():
+            print(f"{k}: {v:.1f}" if isinstance(v, float) else f"{k}: {v}")
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (no sharding, no collectives); "
               "run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_pass:
+        pmc_pass()
+        return
     import numpy as np
     import torch
 
@@ -241,7 +313,7 @@ def main():
                    "rows": 1, "activations": "f32", "weight_copies": g["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(), "kernel": "gemv_seg_kernel<Q4_K,f32,f32,1,8>",
+                     "traffic": read_traffic(), "kernel": "gemv_q4k_digits_kernel<float,float,2,2,2>",
                      "algorithmic_bytes_per_launch": g["bytes"]},
         "cpu_baseline": cpu and {k: v for k, v in cpu.items()},
         "extras": extras,
