@@ -106,7 +106,10 @@ int krk_dtype_row_aligned(int wt, int64_t n);
 
 /* Backend::gemm -- backend.hpp:859-860; HipBackend::gemm backend_hip.hip:3175.
  * out[rows, n_out] = x[rows, n_in] . W[n_out, n_in]^T.
- * rows == 1..8: fused dequant+dot GEMV (f32 products, f32 accumulate).
+ * rows == 1..8: fused dequant+dot GEMV with exact products and f32
+ *               accumulation; Q4_K at rows == 1 forms the products on the
+ *               int8 matrix cores from exact digit planes of x (rounded at
+ *               2^-23 of each 32-value sub-block's maximum).
  * rows  > 8   : per krk_set_gemm_path. */
 int krk_gemm(krk_backend *b, void *out, const void *x, const void *w, int wt,
              int64_t n_out, int64_t n_in, int64_t rows);
