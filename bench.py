@@ -268,6 +268,17 @@ def main():
                 extras[f"prefill_q4k_{name}_m{M}"] = {"us": r["ms"] * 1e3, "TFLOPs": r["TFLOPs"],
                                                       "frac_fp16_peak": r["frac"]}
 
+    if want("int8"):
+        # the Q8_0 x Q8 int8 rung at the C3 up shape (KRK_PATH_INT8)
+        be16.set_gemm_path(K.PATH_INT8)
+        for M in (512, 2048):
+            log(f"gemm q8_0 int8 rung up M={M} ...")
+            r = bench_gemm(K, torch, be16, timer, K.Q8_0, M, 14336, 4096, seed=12)
+            extras[f"prefill_q8_0_int8_up_m{M}"] = {
+                "us": r["ms"] * 1e3, "TOPs": r["TFLOPs"], "frac_int8_peak": r["TFLOPs"] / INT8_PEAK_TOPS}
+            log(f"  {r['ms'] * 1e3:.1f} us  {r['TFLOPs']:.1f} TOP/s  ({100 * r['TFLOPs'] / INT8_PEAK_TOPS:.1f}% of int8 peak)")
+        be16.set_gemm_path(K.PATH_AUTO)
+
     if args.all or want("layer") and only:
         # config 2: Llama-2-7B Q4_K decode layer, M = 1
         tot_b, tot_ms = 0, 0.0

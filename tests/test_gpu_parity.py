@@ -314,3 +314,50 @@ def test_q8_0_config1_gemv(krk, torch_cuda, be32):
     be32.gemm(out, dev(torch, x), dev(torch, w), O.Q8_0, 2048, 2048, 1)
     be32.sync()
     assert rel(host(out), O.gemm(O.Q8_0, w, x, 2048)) <= GEMV_TOL
+
+
+# ------------------------------------------------------------- int8 rung --
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", [(17, 96, 256), (130, 200, 2048), (256, 384, 4096)])
+def test_int8_rung_q8_0_bit_exact(krk, torch_cuda, be16, be32, shape):
+    """KRK_PATH_INT8: Q8_0 weights x activations quantized per 32
+    (quantize_q8_32_d), integer block dots folded as fma(isum, dw*dx, acc) in
+    block order -- bit-identical to dot_q8_0_q8_scalar (quant.cpp:3261-3279)."""
+    torch = torch_cuda
+    M, N, K = shape
+    w = make_weights(krk, krk.Q8_0, N, K, seed=70)
+    x = krk.synth_normal(M * K, seed=71).reshape(M, K)
+    x[0, :32] = 0.0                      # an all-zero block: d = 0, codes 0
+    x[1, 5] = 6.0e4                      # one large value: the rest of its block rounds to 0
+    say("int8 rung", M, N, K)
+    ref = O.gemm_q8_0_q8(w, x, N)
+    for be in (be32, be16):
+        be.set_gemm_path(krk.PATH_INT8)
+    try:
+        out32 = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        be32.gemm(out32, dev(torch, x), dev(torch, w), krk.Q8_0, N, K, M)
+        be32.sync()
+        assert np.array_equal(host(out32).view(np.uint32), ref.view(np.uint32))
+        xh = x.astype(np.float16)
+        ref16 = O.gemm_q8_0_q8(w, xh.astype(np.float32), N).astype(np.float16)
+        out16 = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        be16.gemm(out16, dev(torch, xh), dev(torch, w), krk.Q8_0, N, K, M)
+        be16.sync()
+        assert np.array_equal(host(out16).view(np.uint16), ref16.view(np.uint16))
+    finally:
+        for be in (be32, be16):
+            be.set_gemm_path(krk.PATH_AUTO)
+
+
+@pytest.mark.gpu
+def test_int8_rung_refuses_other_formats(krk, torch_cuda, be32):
+    torch = torch_cuda
+    be32.set_gemm_path(krk.PATH_INT8)
+    try:
+        w = make_weights(krk, krk.Q4_K, 32, 256, seed=72)
+        x = dev(torch, krk.synth_normal(16 * 256, seed=73).reshape(16, 256))
+        out = torch.empty((16, 32), dtype=torch.float32, device="cuda")
+        with pytest.raises(krk.KrkError, match="UNSUPPORTED|Q8_0"):
+            be32.gemm(out, x, dev(torch, w), krk.Q4_K, 32, 256, 16)
+    finally:
+        be32.set_gemm_path(krk.PATH_AUTO)
