@@ -29,9 +29,9 @@
 
 namespace krk {
 
-constexpr int GB_M = 256, GB_N = 256, GB_K = 32;
+constexpr int GB_M = 256, GB_N = 256, GB_K = 64;
 constexpr int G_THREADS = 512;
-constexpr int LDS_ROW = 40;  // halves per LDS row: 32 + 8 pad (80 B)
+constexpr int LDS_ROW = 72;  // halves per LDS row: 64 + 8 pad (144 B)
 
 // ------------------------------------------------- weight half-chunk staging
 // Thread view: 16 consecutive values of one weight row, values
@@ -189,13 +189,21 @@ __device__ __forceinline__ int xcd_remap(int g, int G) {
     return (g & 7) * per + (g >> 3);
 }
 
+// Raw operand bytes of one thread for one K step (64 values): the two
+// 16-value halves of its weight chunk and its 32 activations.
+template <int DT, typename XT> struct StepRegs {
+    WStage<DT> w0, w1;
+    XStage<XT> x0, x1;
+};
+
 template <int DT, typename XT, typename OT>
-__global__ void __launch_bounds__(G_THREADS, 2)
+__global__ void __launch_bounds__(G_THREADS, 1)
     gemm_f16_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const XT *__restrict__ x,
                     OT *__restrict__ out, float *__restrict__ part, int M, int N, int K,
                     int k_per_split, int tiles_n) {
-    __shared__ _Float16 Xs[GB_M * LDS_ROW];
-    __shared__ _Float16 Ws[GB_N * LDS_ROW];
+    // two LDS stages of a 256 x 64 activation tile and a 256 x 64 weight tile
+    __shared__ _Float16 Xs[2][GB_M * LDS_ROW];
+    __shared__ _Float16 Ws[2][GB_N * LDS_ROW];
 
     const int G = gridDim.x;
     const int g = xcd_remap(static_cast<int>(blockIdx.x), G);
@@ -203,17 +211,57 @@ __global__ void __launch_bounds__(G_THREADS, 2)
     const int m0 = tm * GB_M, n0 = tn * GB_N;
     const int kb = static_cast<int>(blockIdx.z) * k_per_split;
     const int ke = min(K, kb + k_per_split);
-    const int nk = (ke - kb) / GB_K;
+    const int nk = (ke - kb + GB_K - 1) / GB_K;   // a K of 32 mod 64 ends in a half step
+    const int cend = ke / 32;                      // first chunk past this split
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves, 128 x 64 each
 
-    // staging roles: row = tid / 2, half = tid & 1
+    // staging roles: row = tid / 2, values [64 kt + 32 shf, +32) of the row
+    // (one 32-value GGUF chunk)
     const int srow = tid >> 1, shf = tid & 1;
     const int wr = min(n0 + srow, N - 1);
     const uint8_t *wrow = w + static_cast<int64_t>(wr) * row_bytes;
     const bool xok = m0 + srow < M;
-    const XT *xrow = x + static_cast<int64_t>(xok ? m0 + srow : 0) * K + shf * 16;
+    const XT *xrow = x + static_cast<int64_t>(xok ? m0 + srow : 0) * K + shf * 32;
+    const int c0 = kb / 32 + shf;  // chunk index of step 0
+
+    auto fetch = [&](StepRegs<DT, XT> &r, int it) {
+        const int c = c0 + 2 * it;
+        const bool ok = c < cend;
+        const int cc = ok ? c : cend - 1;          // stay inside the row
+        r.w0.fetch(wrow, cc, 0);
+        r.w1.fetch(wrow, cc, 1);
+        const XT *xp = xrow + kb + (ok ? it * GB_K : 0);
+        r.x0.fetch(xp, xok && ok);
+        r.x1.fetch(xp + 16, xok && ok);
+    };
+    auto stage = [&](const StepRegs<DT, XT> &r, int it, int s) {
+        const int c = c0 + 2 * it;
+        _Float16 a[16], b[16];
+        r.w0.decode(c, a);
+        r.w1.decode(c, b);
+        if (c >= cend) {   // the half step past K: zero weights (the activations are zero too)
+#pragma unroll
+            for (int i = 0; i < 16; i++) { a[i] = static_cast<_Float16>(0.0f); b[i] = a[i]; }
+        }
+        _Float16 *wd = &Ws[s][srow * LDS_ROW + shf * 32];
+        half8 h;
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = a[i];
+        *reinterpret_cast<half8 *>(wd) = h;
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = a[8 + i];
+        *reinterpret_cast<half8 *>(wd + 8) = h;
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = b[i];
+        *reinterpret_cast<half8 *>(wd + 16) = h;
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = b[8 + i];
+        *reinterpret_cast<half8 *>(wd + 24) = h;
+        r.x0.store(&Xs[s][srow * LDS_ROW + shf * 32]);
+        r.x1.store(&Xs[s][srow * LDS_ROW + shf * 32 + 16]);
+    };
 
     floatx16 acc[4][2];
 #pragma unroll
@@ -223,48 +271,49 @@ __global__ void __launch_bounds__(G_THREADS, 2)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    WStage<DT> ws;
-    XStage<XT> xs;
-    int kt = kb / GB_K;
-    ws.fetch(wrow, kt, shf);
-    xs.fetch(xrow + kb, xok);
-
-    for (int it = 0; it < nk; it++, kt++) {
-        _Float16 wv[16];
-        ws.decode(kt, wv);
-        __syncthreads();  // the previous step's fragments have been read
-        {
-            half8 a, b;
-#pragma unroll
-            for (int i = 0; i < 8; i++) { a[i] = wv[i]; b[i] = wv[8 + i]; }
-            *reinterpret_cast<half8 *>(&Ws[srow * LDS_ROW + shf * 16]) = a;
-            *reinterpret_cast<half8 *>(&Ws[srow * LDS_ROW + shf * 16 + 8]) = b;
-            xs.store(&Xs[srow * LDS_ROW + shf * 16]);
-        }
-        __syncthreads();
-        if (it + 1 < nk) {  // next step's bytes travel while the MFMAs run
-            ws.fetch(wrow, kt + 1, shf);
-            xs.fetch(xrow + kb + (it + 1) * GB_K, xok);
-        }
+    auto mfma_step = [&](int s) {
 #pragma unroll
         for (int kk = 0; kk < GB_K; kk += 16) {
             half8 af[4], bf[2];
             const int ko = kk + (lane >> 5) * 8;
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                af[i] = *reinterpret_cast<const half8 *>(
-                    &Xs[(wm * 128 + i * 32 + (lane & 31)) * LDS_ROW + ko]);
+                af[i] = *reinterpret_cast<const half8 *>(&Xs[s][(wm * 128 + i * 32 + (lane & 31)) * LDS_ROW + ko]);
 #pragma unroll
             for (int j = 0; j < 2; j++)
-                bf[j] = *reinterpret_cast<const half8 *>(
-                    &Ws[(wn * 64 + j * 32 + (lane & 31)) * LDS_ROW + ko]);
+                bf[j] = *reinterpret_cast<const half8 *>(&Ws[s][(wn * 64 + j * 32 + (lane & 31)) * LDS_ROW + ko]);
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
                 for (int j = 0; j < 2; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
+    };
+
+    // Pipeline: the raw bytes of step it + 2 are in flight while step it + 1
+    // is decoded into the free LDS stage and step it's MFMAs run; one
+    // barrier per step.  Two register sets alternate (the loop is unrolled
+    // by two so they stay in registers).
+    StepRegs<DT, XT> ra, rb;
+    if (nk > 0) fetch(ra, 0);
+    if (nk > 1) fetch(rb, 1);
+    if (nk > 0) stage(ra, 0, 0);
+    if (nk > 2) fetch(ra, 2);
+    __syncthreads();
+    int it = 0;
+    for (; it + 1 < nk; it += 2) {
+        // even step: MFMA stage 0, decode rb (step it + 1) -> stage 1, refill rb
+        mfma_step(0);
+        stage(rb, it + 1, 1);
+        if (it + 3 < nk) fetch(rb, it + 3);
+        __syncthreads();
+        // odd step: MFMA stage 1, decode ra (step it + 2) -> stage 0, refill ra
+        mfma_step(1);
+        if (it + 2 < nk) stage(ra, it + 2, 0);
+        if (it + 4 < nk) fetch(ra, it + 4);
+        __syncthreads();
     }
+    if (it < nk) mfma_step(0);   // odd step count: the last step sits in stage 0
 
     // C fragment: lane holds column j = lane % 32, rows 8*(r/4) + 4*(lane/32) + r%4
 #pragma unroll

@@ -208,10 +208,14 @@ def test_gemm_group_qkv_and_silu(krk, torch_cuda, be32):
 
 # --------------------------------------------------------------- MFMA GEMM --
 @pytest.mark.parametrize("dt", FMTS)
-@pytest.mark.parametrize("shape", [(300, 520, 1024), (64, 256, 4096)])
+@pytest.mark.parametrize("shape", [(300, 520, 1024), (64, 256, 4096), (40, 96, 288)])
 def test_gemm_mfma_parity(krk, torch_cuda, be16, be32, dt, shape):
+    """f16 MFMA GEMM: whole 64-value K steps, a trailing half step (K = 288
+    for the 32-value formats) and edge tiles in M and N."""
     torch = torch_cuda
     M, N, K = shape
+    if K % krk.BLOCK_VALUES[dt]:
+        pytest.skip("K is not a whole number of this format's blocks")
     w = make_weights(krk, dt, N, K, seed=60 + dt)
     x = krk.synth_normal(M * K, seed=61).reshape(M, K).astype(np.float16)
     say("gemm", dt, M, N, K)
