@@ -125,6 +125,66 @@ def bench_gemm(K, torch, be, timer, dt, M, n_out, n_in, seed, iters=20, warmup=3
             "M": M, "N": n_out, "K": n_in}
 
 
+def q4k_random_rows(torch, n_rows, n_in, gen):
+    """Q4_K rows of random codes and scales with fixed d = dmin = 2^-10 (f16
+    0x1400): valid blocks, made on the device (the MoE bank is 1.36 GB)."""
+    nb = n_in // 256
+    w = torch.randint(0, 256, (n_rows, nb, 144), dtype=torch.uint8, device="cuda", generator=gen)
+    w[:, :, 0] = 0x00
+    w[:, :, 1] = 0x14
+    w[:, :, 2] = 0x00
+    w[:, :, 3] = 0x14
+    return w.reshape(n_rows, nb * 144)
+
+
+def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, k=8, calls=64):
+    """qwen3moe-shaped experts (Q4_K gate/up [1536, 4096],
+    down [4096, 1536]), router softmax -> top-8 -> normalize -> dispatch.
+    Each timed call routes a different seeded logits block, so the experts
+    read vary and the 1.36 GB bank streams from HBM."""
+    import numpy as np
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    mats, entries = [], []
+    for e in range(n_expert):
+        ent = K.MoeEntry()
+        for m, (o, i) in enumerate(((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff))):
+            t = q4k_random_rows(torch, o, i, gen)
+            mats.append(t)
+            ent.p[m] = t.data_ptr()
+            ent.n_out[m], ent.n_in[m] = o, i
+            ent.row_bytes[m] = K.row_bytes(K.Q4_K, i)
+            ent.type[m] = K.Q4_K
+            ent.present[m] = 1
+        entries.append(ent)
+    table = torch.from_numpy(np.frombuffer(K.moe_table_bytes(entries), np.uint8).copy()).cuda()
+    logits = torch.from_numpy(K.synth_normal(calls * n_tok * n_expert, seed=31)).cuda()
+    logits = logits.reshape(calls, n_tok, n_expert)
+    x = torch.from_numpy(K.synth_normal(n_tok * n_embd, seed=32)).cuda().reshape(n_tok, n_embd)
+    probs = torch.empty((n_tok, n_expert), dtype=torch.float32, device="cuda")
+    ids = torch.empty((n_tok, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((n_tok, k), dtype=torch.float32, device="cuda")
+    out = torch.empty((n_tok, n_embd), dtype=torch.float32, device="cuda")
+
+    def step(i):
+        be.router_softmax(probs, logits[i % calls], n_tok, n_expert)
+        be.router_topk(probs, n_tok, n_expert, k, ids, wts, True, 1.0)
+        be.moe_dispatch(table, 0, n_expert, ids, wts, x, out, n_tok, n_embd, n_ff, k)
+
+    ms = timer.run(step, calls, 4)
+    # distinct experts per call, from the same routing on the host
+    import oracle as O
+    distinct = []
+    lg = logits.cpu().numpy()
+    for i in range(calls):
+        rid, _ = O.router_topk(O.router_softmax(lg[i]), k)
+        distinct.append(len(set(rid.reshape(-1).tolist())))
+    per_expert = 2 * n_ff * K.row_bytes(K.Q4_K, n_embd) + n_embd * K.row_bytes(K.Q4_K, n_ff)
+    nbytes = float(np.mean(distinct)) * per_expert + 4 * (2 * n_tok * n_embd + n_tok * n_expert)
+    return {"us": ms * 1e3, "GBps": nbytes / ms / 1e6, "distinct_experts": float(np.mean(distinct)),
+            "bytes_per_call": nbytes}
+
+
 def cpu_baseline(O, w, x, n_out, n_in, seconds):
     """The strict scalar oracle (one f32 chain per output row, parallel over
     rows) on this host's cores, on a bounded sample of the same GEMV."""
@@ -297,6 +357,13 @@ def main():
             extras[f"head_{nm}"] = {"us": r["ms"] * 1e3, "GBps": r["GBps"],
                                     "frac_hbm": r["GBps"] / HBM_PEAK_GBS}
             log(f"  head {nm} {r['ms'] * 1e3:.1f} us {r['GBps']:.0f} GB/s")
+
+    if args.all or want("moe") and only:
+        for T in (1, 16):
+            log(f"moe C5 n_tok={T} ...")
+            r = bench_moe(K, torch, be32, timer, T)
+            extras[f"moe_c5_t{T}"] = r
+            log(f"  {r['us']:.1f} us  {r['GBps']:.0f} GB/s  ({r['distinct_experts']:.1f} experts)")
 
     # ---- CPU baseline (rank 0, N = 1) ----------------------------------------
     cpu = None

@@ -14,6 +14,17 @@
 #include "krk_kernels.hpp"
 #include "krk_mi355x.h"
 
+// (table, layer, geometry) of an MoE dispatch whose table entry was checked
+struct MoeKey {
+    const void *table;
+    int layer, n_expert;
+    int64_t n_embd, n_ff;
+    bool operator==(const MoeKey &o) const {
+        return table == o.table && layer == o.layer && n_expert == o.n_expert && n_embd == o.n_embd &&
+               n_ff == o.n_ff;
+    }
+};
+
 struct krk_backend {
     int device = 0;
     int act = KRK_ACT_F32;
@@ -22,6 +33,10 @@ struct krk_backend {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     std::string err;
+    static constexpr int kMoeCache = 256;  // layers of MoE tables checked once
+    struct MoeOk { MoeKey key; krk_moe_entry e0; };
+    MoeOk moe_ok[kMoeCache];
+    int n_moe_ok = 0;
 };
 
 namespace {
@@ -347,24 +362,36 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
     if (reinterpret_cast<uintptr_t>(xn) & 15)
         return fail(b, KRK_ERR_ARG, "moe_dispatch: xn is not 16-byte aligned");
     if (int s = make_current(b)) return s;
-    // The table lives on the device; its entries' types and strides are read
-    // there.  The host learns the (uniform) weight type from entry 0 of the
-    // layer so the right kernel instantiation is launched.
-    krk_moe_entry e0;
+    // The table lives on the device and the kernels read every entry's type
+    // and strides there.  The host checks the layer's geometry once per
+    // (table, layer): the first call reads entry 0 back (one synchronous
+    // copy), later calls find it in the cache and stay asynchronous, so a
+    // steady-state dispatch can be captured in a graph.  A table rewritten
+    // in place with another geometry after its first use is not re-checked.
+    krk_moe_entry e0{};
     const krk_moe_entry *tab = static_cast<const krk_moe_entry *>(table);
-    hipError_t he = hipMemcpyAsync(&e0, tab + static_cast<int64_t>(layer) * n_expert, sizeof(e0),
-                                   hipMemcpyDeviceToHost, b->stream);
-    if (he == hipSuccess) he = hipStreamSynchronize(b->stream);
-    if (he != hipSuccess) return hip_fail(b, he, "moe_dispatch: reading table entry");
-    for (int m = 0; m < 3; m++) {
-        if (!e0.present[m] || !dtype_on_path(e0.type[m]))
-            return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: matrix %d absent or of type %d", m,
-                        e0.type[m]);
-        if (e0.type[m] != e0.type[0])
-            return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: mixed expert formats");
+    const MoeKey key{table, layer, n_expert, n_embd, n_ff};
+    int hit = -1;
+    for (int i = 0; i < b->n_moe_ok; i++)
+        if (b->moe_ok[i].key == key) { hit = i; break; }
+    if (hit >= 0) {
+        e0 = b->moe_ok[hit].e0;
+    } else {
+        hipError_t he = hipMemcpyAsync(&e0, tab + static_cast<int64_t>(layer) * n_expert, sizeof(e0),
+                                       hipMemcpyDeviceToHost, b->stream);
+        if (he == hipSuccess) he = hipStreamSynchronize(b->stream);
+        if (he != hipSuccess) return hip_fail(b, he, "moe_dispatch: reading table entry");
+        for (int m = 0; m < 3; m++) {
+            if (!e0.present[m] || !dtype_on_path(e0.type[m]))
+                return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: matrix %d absent or of type %d", m,
+                            e0.type[m]);
+            if (e0.type[m] != e0.type[0])
+                return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: mixed expert formats");
+        }
+        if (e0.n_in[0] != n_embd || e0.n_out[0] != n_ff || e0.n_in[2] != n_ff || e0.n_out[2] != n_embd)
+            return fail(b, KRK_ERR_SHAPE, "moe_dispatch: table geometry does not match n_embd/n_ff");
+        if (b->n_moe_ok < krk_backend::kMoeCache) b->moe_ok[b->n_moe_ok++] = {key, e0};
     }
-    if (e0.n_in[0] != n_embd || e0.n_out[0] != n_ff || e0.n_in[2] != n_ff || e0.n_out[2] != n_embd)
-        return fail(b, KRK_ERR_SHAPE, "moe_dispatch: table geometry does not match n_embd/n_ff");
     krk::MoeArgs a{};
     a.table = table; a.layer = layer; a.n_expert = n_expert; a.k = k;
     a.ids = static_cast<const int32_t *>(ids);
@@ -375,7 +402,7 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
     a.wt = e0.type[0];
     a.rb_gate = e0.row_bytes[0]; a.rb_up = e0.row_bytes[1]; a.rb_down = e0.row_bytes[2];
     if (int s = ensure_ws(b, krk::moe_workspace(n_tok, k, n_expert, n_embd, n_ff))) return s;
-    he = krk::moe_dispatch(a, b->ws, b->ws_bytes, b->stream);
+    const hipError_t he = krk::moe_dispatch(a, b->ws, b->ws_bytes, b->stream);
     return he == hipSuccess ? KRK_OK : hip_fail(b, he, "moe_dispatch");
 }
 

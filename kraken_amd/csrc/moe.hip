@@ -15,8 +15,8 @@
 //                fma(w, part, acc) -- the order and the fused add of the host
 //                loop (engine.cpp:12360-12700, scatter_axpy_rows
 //                backend_cpu.cpp:3193-3217).
-// The weight type is read from the table on the device (no host readback);
-// every expert of a layer must share it.
+// The weight types and strides are read from the table on the device; every
+// expert of a layer must share one type.
 #include "gemv_core.hpp"
 #include "krk_mi355x.h"
 

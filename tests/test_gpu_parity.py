@@ -365,3 +365,33 @@ def test_int8_rung_refuses_other_formats(krk, torch_cuda, be32):
             be32.gemm(out, x, dev(torch, w), krk.Q4_K, 32, 256, 16)
     finally:
         be32.set_gemm_path(krk.PATH_AUTO)
+
+
+def test_moe_dispatch_graph_replay(krk, torch_cuda, be32):
+    """After the first (checking) call a dispatch is asynchronous: it can be
+    captured in a HIP graph, and every replay equals the eager result."""
+    torch = torch_cuda
+    dt, ne, n_embd, n_ff, k, n_tok = O.Q4_K, 8, 512, 512, 2, 3
+    mats, table, keep = build_moe(krk, torch, dt, ne, n_embd, n_ff, seed=950)
+    logits = krk.synth_normal(n_tok * ne, seed=79).reshape(n_tok, ne)
+    ids, wts = O.router_topk(O.router_softmax(logits), k)
+    x = dev(torch, krk.synth_normal(n_tok * n_embd, seed=80).reshape(n_tok, n_embd))
+    dids, dwts = dev(torch, ids), dev(torch, wts)
+    eager = torch.empty((n_tok, n_embd), dtype=torch.float32, device="cuda")
+    be32.moe_dispatch(table, 0, ne, dids, dwts, x, eager, n_tok, n_embd, n_ff, k)
+    be32.sync()
+    out = torch.zeros((n_tok, n_embd), dtype=torch.float32, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    main = be32.stream
+    with torch.cuda.graph(g, stream=side):
+        be32.set_stream(side)
+        be32.moe_dispatch(table, 0, ne, dids, dwts, x, out, n_tok, n_embd, n_ff, k)
+    be32.set_stream(main)
+    want = host(eager)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out).view(np.uint32), want.view(np.uint32)), rep
