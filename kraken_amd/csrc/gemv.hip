@@ -22,8 +22,6 @@
 //     in one transposed butterfly (wave_reduce_multi), and the waves' partials
 //     are added in wave order through LDS.  No atomics: the result is
 //     deterministic for a given shape.
-#include <cstdlib>
-
 #include "gemv_core.hpp"
 
 namespace krk {
@@ -98,58 +96,6 @@ __global__ void __launch_bounds__(512) gemv_seg_kernel(SegTable t) {
             }
         }
     }
-}
-
-// Rows per group of the decode GEMV (KRK_GEMV_RB = 2 | 4 | 8, default 4).
-static int gemv_rb_knob() {
-    static const int v = [] {
-        const char *e = std::getenv("KRK_GEMV_RB");
-        return e ? std::atoi(e) : 4;
-    }();
-    return v;
-}
-
-static int gemv_mfma_knob() {
-    static const int v = [] {
-        const char *e = std::getenv("KRK_GEMV_MFMA");
-        return e ? std::atoi(e) : 0;
-    }();
-    return v;
-}
-static int gemv_stream_mode_knob() {  // experiment: 1 = no compute, 2 = no DMA
-    static const int v = [] {
-        const char *e = std::getenv("KRK_STREAM_MODE");
-        return e ? std::atoi(e) : 0;
-    }();
-    return v;
-}
-static int gemv_stream_knob() {
-    static const int v = [] {
-        const char *e = std::getenv("KRK_GEMV_STREAM");
-        return e ? std::atoi(e) : 1;
-    }();
-    return v;
-}
-static int gemv_lds_knob() {
-    static const int v = [] {
-        const char *e = std::getenv("KRK_GEMV_LDS");
-        return e ? std::atoi(e) : 1;
-    }();
-    return v;
-}
-static int gemv_wave_knob() {
-    static const int v = [] {
-        const char *e = std::getenv("KRK_GEMV_WAVE");
-        return e ? std::atoi(e) : 1;
-    }();
-    return v;
-}
-static int gemv_spw_knob() {
-    static const int v = [] {
-        const char *e = std::getenv("KRK_GEMV_SPW");
-        return e ? std::atoi(e) : 2;
-    }();
-    return v;
 }
 
 // --------------------------------------------------- persistent decode GEMV --
@@ -273,236 +219,6 @@ __global__ void __launch_bounds__(512) gemv_persist_kernel(SegTable t, int64_t t
     }
 }
 
-// ------------------------------------------------------ MFMA decode GEMV ----
-// Q4_K, rows == 1, K <= 8192: the multiply-adds run on the matrix cores.
-//
-// v_mfma_f32_16x16x32_f16 computes C[16][16] += A[16][32] . B[32][16] with
-//   A lane l: row l%16, k = 8*(l/16) + 0..7     (verified on gfx950)
-//   B lane l: col l%16, k = 8*(l/16) + 0..7
-//   C lane l: col l%16, rows 4*(l/16) + 0..3
-// One MFMA covers one 32-value sub-block s of 16 weight rows:
-//   B[k][j]  = nibble code of row j (the code c placed at bits 4..7 of a
-//              16-bit lane is the exact f16 subnormal c * 2^-20),
-//   A[i][k]  = x_h[k] if i/2 == s else 0, h = i%2, x = x_0 + x_1 split into
-//              two f16 (x_0 = f16(x), x_1 = f16(x - x_0): ~22 bits of x),
-// so the eight MFMAs of a super-block all accumulate into ONE C whose row
-// i = (s, h) holds sum_k c_jk * x_h,k for sub-block s: lane (j, g) ends up
-// with exactly the two sub-blocks 2g, 2g+1 of row j whose scales it decodes.
-// A is block-diagonal and the same for every row, so each wave builds it
-// once (32 VGPRs per super-block it owns) and then streams weight rows.
-// VALU per weight: ~7 ops per 8 codes for the masks plus ~0.3 for the scale
-// fold -- a third of the fma_mix path.
-__device__ __forceinline__ void q4k_pair_scales(const uint32_t (&h)[4], int g, float &sc0,
-                                                float &mn0, float &sc1, float &mn1) {
-    // sub-blocks 2g, 2g+1 (get_scale_min_k4, quant.cpp:427-435), branch-free
-    const float d = h2f(h[0] & 0xFFFF), dmin = h2f(h[0] >> 16);
-    const uint32_t sh = 16u * static_cast<uint32_t>(g & 1);
-    const uint32_t Y = h[1] >> sh, Z = h[2] >> sh, W = h[3] >> sh;
-    const bool hi = g >= 2;
-    const uint32_t A = hi ? W : Y, Am = hi ? (W >> 4) : Z;
-    const uint32_t s2 = hi ? 2u : 0u;
-    const uint32_t sa = (A & 15u) | ((Y >> s2) & 0x30u);
-    const uint32_t sb = ((A >> 8) & 15u) | ((Y >> (8u + s2)) & 0x30u);
-    const uint32_t ma = (Am & 15u) | ((Z >> s2) & 0x30u);
-    const uint32_t mb = ((Am >> 8) & 15u) | ((Z >> (8u + s2)) & 0x30u);
-    sc0 = d * static_cast<float>(sa);
-    sc1 = d * static_cast<float>(sb);
-    mn0 = dmin * static_cast<float>(ma);
-    mn1 = dmin * static_cast<float>(mb);
-}
-
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-
-template <typename XT, typename OT, int SPW>
-__global__ void __launch_bounds__(SPW == 1 ? 1024 : 512) gemv_mfma_q4k_kernel(SegTable t, int64_t total) {
-    constexpr int RG = 16;
-    constexpr float kTwo20 = 1048576.0f;
-    __shared__ float red[2][16][RG];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int j = lane & 15, g = lane >> 4;
-    const int nb = t.n_in / 256;
-    constexpr uint32_t M = 0x00F000F0u;
-
-    auto locate = [&](int64_t gi, int &si, int64_t &n0) {
-        si = 0;
-        while (si + 1 < t.n && gi >= t.seg[si + 1].blk_begin) si++;
-        n0 = (gi - t.seg[si].blk_begin) * (t.seg[si].kind == SEG_SILU ? RG / 2 : RG);
-    };
-    // lane's raw bytes of its row j: 4 x 8 B of nibbles + the 16 B header
-    auto fetch = [&](u32x2 (&q)[SPW][4], uint32_t (&h)[SPW][4], int si, int64_t n0) {
-        const Seg &sg = t.seg[si];
-        const bool pair = sg.kind == SEG_SILU;
-        int64_t n = n0 + (pair ? (j & 7) : j);
-        if (n >= sg.n_out) n = sg.n_out - 1;
-        const uint8_t *w = static_cast<const uint8_t *>((pair && j >= 8) ? sg.w2 : sg.w) + n * t.row_bytes;
-#pragma unroll
-        for (int u = 0; u < SPW; u++) {
-            int sb = wv * SPW + u;
-            if (sb >= nb) sb = nb - 1;
-            const uint8_t *blk = w + static_cast<int64_t>(sb) * 144;
-            const u32x4 hv = ld128(blk);
-            h[u][0] = hv.x; h[u][1] = hv.y; h[u][2] = hv.z; h[u][3] = hv.w;
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) q[u][jj] = ld64(blk + 16 + 32 * jj + 8 * g);
-        }
-    };
-
-    half8 A[SPW][8];
-    float xs[SPW][2];
-    const void *xcur = nullptr;
-    u32x2 qA[SPW][4], qB[SPW][4];
-    uint32_t hA[SPW][4], hB[SPW][4];
-    int64_t gi = blockIdx.x;
-    int si = 0;
-    int64_t n0 = 0;
-    if (gi < total) {
-        locate(gi, si, n0);
-        fetch(qA, hA, si, n0);
-    }
-    int par = 0;
-    for (; gi < total; gi += gridDim.x, par ^= 1) {
-        const Seg &sg = t.seg[si];
-        const int64_t gn = gi + gridDim.x;
-        int sn = si;
-        int64_t nn = 0;
-        if (gn < total) {
-            locate(gn, sn, nn);
-            fetch(qB, hB, sn, nn);
-        }
-        if (sg.x != xcur) {
-            xcur = sg.x;
-            // A operands: row i = (s = i/2, h = i%2); k order matches the
-            // B halves (bytes 0,2,1,3,4,6,5,7 of the lane's 8-byte run)
-            const XT *x = static_cast<const XT *>(sg.x);
-            const int i = lane & 15, s_i = i >> 1, h_i = i & 1;
-            constexpr int kperm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-#pragma unroll
-            for (int u = 0; u < SPW; u++) {
-                const int sb = wv * SPW + u;
-                const bool ok = sb < nb;
-                const int64_t base = static_cast<int64_t>(ok ? sb : 0) * 256 +
-                                     64 * (s_i >> 1) + 32 * (s_i & 1) + 8 * g;
-                float xf[8];
-                load_run<8>(x + base, xf);
-                float psum = 0.0f;
-                half8 xd;
-#pragma unroll
-                for (int tt = 0; tt < 8; tt++) {
-                    const float v = ok ? xf[kperm[tt]] : 0.0f;
-                    psum += v;
-                    const _Float16 x0 = static_cast<_Float16>(v);
-                    xd[tt] = h_i == 0 ? x0 : static_cast<_Float16>(v - static_cast<float>(x0));
-                }
-#pragma unroll
-                for (int s = 0; s < 8; s++) {
-                    half8 a;
-#pragma unroll
-                    for (int tt = 0; tt < 8; tt++) a[tt] = s == s_i ? xd[tt] : static_cast<_Float16>(0.0f);
-                    A[u][s] = a;
-                }
-                // sub-block sums: lanes (i, g') cover sub-block s_i in 4 runs of 8
-                psum += __shfl_xor(psum, 16, 64);
-                psum += __shfl_xor(psum, 32, 64);
-                // lane (j, g) needs the sums of sub-blocks 2g and 2g+1, held by
-                // lanes i = 4g (s = 2g) and i = 4g + 2 (s = 2g + 1)
-                xs[u][0] = __shfl(psum, 4 * g, 64);
-                xs[u][1] = __shfl(psum, 4 * g + 2, 64);
-            }
-        }
-        float part = 0.0f;
-#pragma unroll
-        for (int u = 0; u < SPW; u++) {
-            floatx4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const uint32_t D0 = qA[u][jj].x, D1 = qA[u][jj].y;
-                const u32x4v blo = {(D0 << 4) & M, (D0 >> 4) & M, (D1 << 4) & M, (D1 >> 4) & M};
-                const u32x4v bhi = {D0 & M, (D0 >> 8) & M, D1 & M, (D1 >> 8) & M};
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u][2 * jj], __builtin_bit_cast(half8, blo), c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[u][2 * jj + 1], __builtin_bit_cast(half8, bhi), c, 0, 0, 0);
-            }
-            float sc0, mn0, sc1, mn1;
-            q4k_pair_scales(hA[u], g, sc0, mn0, sc1, mn1);
-            const bool ok = wv * SPW + u < nb;
-            float v = (sc0 * kTwo20) * (c[0] + c[1]);
-            v = __builtin_fmaf(sc1 * kTwo20, c[2] + c[3], v);
-            v = __builtin_fmaf(-mn0, xs[u][0], v);
-            v = __builtin_fmaf(-mn1, xs[u][1], v);
-            part += ok ? v : 0.0f;
-        }
-        part += __shfl_xor(part, 16, 64);
-        part += __shfl_xor(part, 32, 64);
-        if (lane < 16) red[par][wv][lane] = part;
-        __syncthreads();
-        const int tid = threadIdx.x;
-        const int kind = sg.kind;
-        OT *out = static_cast<OT *>(sg.out);
-        if (kind != SEG_SILU) {
-            if (tid < RG) {
-                float sum = 0.0f;
-                for (int k = 0; k < nw; k++) sum += red[par][k][tid];
-                const int64_t n = n0 + tid;
-                const float inv = (kind == SEG_ACC && t.rexp) ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
-                if (n < sg.n_out) store_out<OT>(out + n, sum, kind, inv);
-            }
-        } else if (tid < RG / 2) {
-            float gs = 0.0f, us = 0.0f;
-            for (int k = 0; k < nw; k++) {
-                gs += red[par][k][tid];
-                us += red[par][k][RG / 2 + tid];
-            }
-            const int64_t n = n0 + tid;
-            if (n < sg.n_out) {
-                if constexpr (sizeof(OT) == 2) {
-                    const float hg = static_cast<float>(static_cast<_Float16>(gs));
-                    const float hu = static_cast<float>(static_cast<_Float16>(us));
-                    out[n] = sat_f16(silu_f(hg) * hu);
-                } else {
-                    out[n] = (gs / (1.0f + expf(-gs))) * us;
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < SPW; u++) {
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) qA[u][jj] = qB[u][jj];
-#pragma unroll
-            for (int k = 0; k < 4; k++) hA[u][k] = hB[u][k];
-        }
-        si = sn;
-        n0 = nn;
-    }
-}
-
-template <typename XT, typename OT, int SPW>
-static hipError_t launch_mfma_q4k(SegTable t, hipStream_t st) {
-    constexpr int RG = 16;
-    int64_t total = 0;
-    for (int i = 0; i < t.n; i++) {
-        t.seg[i].blk_begin = total;
-        const int64_t per = t.seg[i].kind == SEG_SILU ? RG / 2 : RG;
-        total += (t.seg[i].n_out + per - 1) / per;
-    }
-    const int nb = t.n_in / 256;
-    const int nw = (nb + SPW - 1) / SPW;
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            cus = 256;
-    }
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_mfma_q4k_kernel<XT, OT, SPW>,
-                                                     64 * nw, 0) != hipSuccess || per_cu < 1)
-        per_cu = 1;
-    int64_t grid = static_cast<int64_t>(cus) * per_cu;
-    if (grid > total) grid = total;
-    hipLaunchKernelGGL((gemv_mfma_q4k_kernel<XT, OT, SPW>), dim3(static_cast<unsigned>(grid)),
-                       dim3(64 * nw), 0, st, t, total);
-    return hipGetLastError();
-}
-
 // ------------------------------------------------- independent-wave GEMV ----
 // rows == 1.  Every wave is its own unit of work: a lane owns 64 weights of a
 // row (WaveFmt), so one wave covers 4096 values of K with no other wave --
@@ -512,7 +228,7 @@ static hipError_t launch_mfma_q4k(SegTable t, hipStream_t st) {
 // bytes in flight while the current group is decoded.  A group's RB partial
 // sums are reduced across the wave by one transposed butterfly and written
 // by their owner lanes.
-template <int DT, typename XT, typename OT, int RB, int ABL = 0>
+template <int DT, typename XT, typename OT, int RB>
 __global__ void __launch_bounds__(256) gemv_wave_kernel(SegTable t, int64_t total) {
     using F = WaveFmt<DT>;
     constexpr int BV = blk_vals(DT), BB = blk_bytes(DT);
@@ -542,12 +258,7 @@ __global__ void __launch_bounds__(256) gemv_wave_kernel(SegTable t, int64_t tota
             int64_t n = n0 + (pair ? (r % H) : r);
             if (n >= s.n_out) n = s.n_out - 1;
             const uint8_t *wb = static_cast<const uint8_t *>((pair && r >= H) ? s.w2 : s.w);
-            if constexpr (ABL == 2) {
-#pragma unroll
-                for (int k = 0; k < F::NRAW; k++) raw[r][k] = static_cast<uint32_t>(n * 2654435761u + k + b);
-            } else {
-                F::load(raw[r], wb + n * t.row_bytes + static_cast<int64_t>(b) * BB, slot);
-            }
+            F::load(raw[r], wb + n * t.row_bytes + static_cast<int64_t>(b) * BB, slot);
         }
     };
     auto load_x = [&](const void *xp, int st, float (&xv)[64], float (&xs)[F::NG]) {
@@ -595,7 +306,7 @@ __global__ void __launch_bounds__(256) gemv_wave_kernel(SegTable t, int64_t tota
                 load_x(s.x, st, xv, xs);
             }
             const bool ok = st * F::BPS + F::blk_of(lane) < nb;
-            if constexpr (DT == DT_Q4_K && ABL == 0) {
+            if constexpr (DT == DT_Q4_K) {
                 // code dword outer, row inner: RB x 4 independent chains
                 float acc[RB][F::NACC];
 #pragma unroll
@@ -614,15 +325,7 @@ __global__ void __launch_bounds__(256) gemv_wave_kernel(SegTable t, int64_t tota
             } else
 #pragma unroll
             for (int r = 0; r < RB; r++) {
-                float d;
-                if constexpr (ABL == 1) {
-                    uint32_t h = 0;
-#pragma unroll
-                    for (int k = 0; k < F::NRAW; k++) h ^= rawA[r][k];
-                    d = static_cast<float>(h & 1) * xv[0];
-                } else {
-                    d = F::dot(rawA[r], slot, xv, xs);
-                }
+                const float d = F::dot(rawA[r], slot, xv, xs);
                 v[r] += ok ? d : 0.0f;
             }
 #pragma unroll
@@ -663,7 +366,7 @@ __global__ void __launch_bounds__(256) gemv_wave_kernel(SegTable t, int64_t tota
     }
 }
 
-template <int DT, typename XT, typename OT, int RB, int ABL = 0>
+template <int DT, typename XT, typename OT, int RB>
 static hipError_t launch_wave(SegTable t, hipStream_t st) {
     int64_t total = 0;
     for (int i = 0; i < t.n; i++) {
@@ -680,13 +383,13 @@ static hipError_t launch_wave(SegTable t, hipStream_t st) {
     }
     static int per_cu = 0;
     if (!per_cu &&
-        (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_wave_kernel<DT, XT, OT, RB, ABL>, 256, 0) !=
+        (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_wave_kernel<DT, XT, OT, RB>, 256, 0) !=
              hipSuccess || per_cu < 1))
         per_cu = 1;
     const int64_t waves = total;  // one wave per group at most
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
     if (grid * 4 > waves) grid = (waves + 3) / 4;
-    hipLaunchKernelGGL((gemv_wave_kernel<DT, XT, OT, RB, ABL>), dim3(static_cast<unsigned>(grid)), dim3(256),
+    hipLaunchKernelGGL((gemv_wave_kernel<DT, XT, OT, RB>), dim3(static_cast<unsigned>(grid)), dim3(256),
                        0, st, t, total);
     return hipGetLastError();
 }
@@ -1059,7 +762,7 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 // lane keeps its 64 activations and their group sums in registers for the
 // kernel's lifetime; otherwise x is staged in LDS and read per unit.
 template <int DT, typename XT, typename OT, int RB, int NSLOT, bool XREG>
-__global__ void __launch_bounds__(512) gemv_stream_kernel(SegTable t, int64_t total, int xfloats, int mode) {
+__global__ void __launch_bounds__(512) gemv_stream_kernel(SegTable t, int64_t total, int xfloats) {
     using F = WaveFmt<DT>;
     using D = LdsDot<DT, RB>;
     constexpr int BV = blk_vals(DT), BB = blk_bytes(DT);
@@ -1109,7 +812,6 @@ __global__ void __launch_bounds__(512) gemv_stream_kernel(SegTable t, int64_t to
         dl[c] = o < U ? static_cast<int32_t>(r * rb + (o - r * P)) : 16 * lane;
     }
     auto issue = [&](int64_t j) {
-        if (mode == 2) return;
         const int64_t g = W + (j / nsteps) * NW;
         const int st = static_cast<int>(j % nsteps);
         const int si = seg_of(g);
@@ -1196,10 +898,7 @@ __global__ void __launch_bounds__(512) gemv_stream_kernel(SegTable t, int64_t to
 #pragma unroll
         for (int r = 0; r < RB; r++) F::load(raw[r], slot + r * P + lb * BB, slot_lane);
         float d[RB];
-        if (mode == 1) {
-#pragma unroll
-            for (int r = 0; r < RB; r++) d[r] = __uint_as_float(raw[r][0] ^ raw[r][F::NRAW - 1]);
-        } else if constexpr (XREG) {
+        if constexpr (XREG) {
 #pragma unroll
             for (int r = 0; r < RB; r++) d[r] = F::dot(raw[r], slot_lane, xv, xg);
         } else {
@@ -1273,30 +972,14 @@ static hipError_t launch_stream(SegTable t, hipStream_t st) {
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
     if (grid * nw > total) grid = (total + nw - 1) / nw;
     hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, RB, NSLOT, XREG>), dim3(static_cast<unsigned>(grid)),
-                       dim3(64 * nw), xbytes + nw * per_wave, st, t, total, xfloats, gemv_stream_mode_knob());
+                       dim3(64 * nw), xbytes + nw * per_wave, st, t, total, xfloats);
     return hipGetLastError();
 }
 
-static int gemv_stream_cfg_knob() {  // experiment: RB * 10 + NSLOT, 0 = default
-    static const int v = [] {
-        const char *e = std::getenv("KRK_STREAM_CFG");
-        return e ? std::atoi(e) : 0;
-    }();
-    return v;
-}
-
+// two rows per unit, two slots: measured best over RB in {1, 2, 4} and
+// two or three slots on MI355X for Q4_K / Q6_K / Q8_0 at K = 4096
 template <int DT, typename XT, typename OT, bool XREG>
 static hipError_t launch_stream_x(const SegTable &t, hipStream_t st) {
-    if constexpr (sizeof(XT) == 4 && sizeof(OT) == 4 && (DT == DT_Q4_K || DT == DT_Q6_K)) {
-        switch (gemv_stream_cfg_knob()) {
-            case 43: return launch_stream<DT, XT, OT, 4, 3, XREG>(t, st);
-            case 42: return launch_stream<DT, XT, OT, 4, 2, XREG>(t, st);
-            case 23: return launch_stream<DT, XT, OT, 2, 3, XREG>(t, st);
-            case 22: return launch_stream<DT, XT, OT, 2, 2, XREG>(t, st);
-            case 12: return launch_stream<DT, XT, OT, 1, 2, XREG>(t, st);
-            default: break;
-        }
-    }
     return launch_stream<DT, XT, OT, 2, 2, XREG>(t, st);
 }
 
@@ -1308,7 +991,7 @@ static hipError_t launch_stream(const SegTable &t, hipStream_t st) {
 
 template <int DT, typename XT, typename OT>
 static bool try_stream(const SegTable &t, hipStream_t st, hipError_t &err) {
-    if (t.rows != 1 || !gemv_stream_knob() || t.n_in > 16384) return false;
+    if (t.rows != 1 || t.n_in > 16384) return false;
     for (int i = 0; i < t.n; i++) {
         if (t.seg[i].kind == SEG_SILU || t.seg[i].x != t.seg[0].x) return false;
         if (reinterpret_cast<uintptr_t>(t.seg[i].w) & 15) return false;
@@ -1400,50 +1083,24 @@ static hipError_t launch_persist(SegTable t, hipStream_t st) {
     return hipGetLastError();
 }
 
+// rows == 1 picks, in order: the LDS-DMA streamed kernel (one x for all
+// segments, aligned rows); the x-in-LDS kernel (one x, e.g. fused gate+up
+// with SiLU); the independent-wave kernel (one x per segment); the
+// persistent kernel.  rows > 1 takes the multi-row segment kernel.
 template <int DT, typename XT, typename OT>
 static hipError_t dispatch_mr(SegTable t, hipStream_t st) {
-    {
-        const int nsteps = (t.n_in / blk_vals(DT) + kWave / LaneFmt<DT>::LPB - 1) /
-                           (kWave / LaneFmt<DT>::LPB);
-        if constexpr (DT == DT_Q4_K) {
-            // matrix-core decode GEMV (KRK_GEMV_MFMA=0 keeps the VALU form)
-            const int nb = t.n_in / 256;
-            if (t.rows == 1 && gemv_mfma_knob() && nb <= 16) {
-                if (gemv_spw_knob() == 1) return launch_mfma_q4k<XT, OT, 1>(t, st);
-                return launch_mfma_q4k<XT, OT, 2>(t, st);
-            }
-        }
+    if (t.rows == 1) {
         const bool two_blocks = DT == DT_Q4_0 || DT == DT_Q8_0;
-        {
-            hipError_t err = hipSuccess;
-            if (try_stream<DT, XT, OT>(t, st, err)) return err;
-        }
+        hipError_t err = hipSuccess;
+        if (try_stream<DT, XT, OT>(t, st, err)) return err;
         bool same_x = true;
         for (int i = 1; i < t.n; i++) same_x = same_x && t.seg[i].x == t.seg[0].x;
-        if (t.rows == 1 && gemv_lds_knob() && same_x && t.n_in <= kLdsGemvMaxK &&
-            (!two_blocks || t.n_in % 64 == 0)) {
-            switch (gemv_rb_knob()) {
-                case 2: return launch_lds<DT, XT, OT, 2>(t, st);
-                case 8: return launch_lds<DT, XT, OT, 8>(t, st);
-                default: return launch_lds<DT, XT, OT, 4>(t, st);
-            }
-        }
-        if (t.rows == 1 && gemv_wave_knob() && (!two_blocks || t.n_in % 64 == 0)) {
-            switch (gemv_rb_knob()) {
-                case 2: return launch_wave<DT, XT, OT, 2>(t, st);
-                case 41: return launch_wave<DT, XT, OT, 4, 1>(t, st);
-                case 42: return launch_wave<DT, XT, OT, 4, 2>(t, st);
-                case 8: return launch_wave<DT, XT, OT, 8>(t, st);
-                default: return launch_wave<DT, XT, OT, 4>(t, st);
-            }
-        }
-        if (t.rows == 1 && nsteps <= 8) {
-            switch (gemv_rb_knob()) {
-                case 2: return launch_persist<DT, XT, OT, 2>(t, st);
-                case 8: return launch_persist<DT, XT, OT, 8>(t, st);
-                default: return launch_persist<DT, XT, OT, 4>(t, st);
-            }
-        }
+        if (same_x && t.n_in <= kLdsGemvMaxK && (!two_blocks || t.n_in % 64 == 0))
+            return launch_lds<DT, XT, OT, 4>(t, st);
+        if (!two_blocks || t.n_in % 64 == 0) return launch_wave<DT, XT, OT, 4>(t, st);
+        const int nsteps = (t.n_in / blk_vals(DT) + kWave / LaneFmt<DT>::LPB - 1) /
+                           (kWave / LaneFmt<DT>::LPB);
+        if (nsteps <= 8) return launch_persist<DT, XT, OT, 4>(t, st);
     }
     // rows per x pass and weight rows per block, MR*RB = 8 values per lane
     int mr = t.rows <= 1 ? 1 : t.rows == 2 ? 2 : 4;

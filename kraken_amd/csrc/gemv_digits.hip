@@ -28,8 +28,6 @@
 // with global_load_lds_dwordx4 -- every weight byte is delivered once and
 // coalesced -- while the digit table of x is built once per workgroup.
 // NSLOT slots keep NSLOT-1 units in flight during the decode.
-#include <cstdlib>
-
 #include "gemv_core.hpp"
 #include "krk_formats.hpp"
 #include "krk_kernels.hpp"
@@ -38,12 +36,6 @@ namespace krk {
 
 namespace {
 
-#ifdef KRK_TRACE
-__device__ uint64_t g_trace[4096 * 16];
-#define TRACE(k) do { if (lane == 0 && W_ < 4096) g_trace[W_ * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define TRACE(k) do { } while (0)
-#endif
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -58,12 +50,15 @@ constexpr int kTabBlk = 768;   // digit bytes per 256-value block: 8 sub-blocks 
 constexpr int kZero = 512;     // zero bytes read by lanes whose A row is empty
 constexpr int kMaxK = 16384;
 constexpr int kXPasses = 8;  // x sub-blocks staged per thread (4 threads per sub-block)
+// Waves that issue their first weight DMA only after building the digit
+// table: a wave stalls while the memory pipeline cannot accept its DMA, and
+// these keep the table build moving meanwhile (measured: 4 of 8 best).
+constexpr int kLateWaves = 4;
 
 __device__ __forceinline__ v4i ld_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
 template <typename XT, typename OT, int RGN, int KB, int NSLOT>
-__global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_t total, int nks, int nwc,
-                                                               int mode, int late_knob) {
+__global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_t total, int nks, int nwc) {
     constexpr int BB = 144;
     constexpr int P = KB * BB;                   // row piece of one unit
     constexpr int ROWS = 16 * RGN;
@@ -87,9 +82,6 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     // streaming while the table is built.
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t W_ = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + wv;
-    (void)W_;
-    TRACE(0);
     uint8_t *slots = slots0 + wv * (NSLOT * SLOT);
     const int64_t rb = t.row_bytes;
     // A workgroup owns tiles of ROWS rows (tiles blockIdx.x, + gridDim.x, ...);
@@ -116,7 +108,6 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     // the first units read the segment table from the kernel arguments (the
     // LDS copy is not ready yet); later ones from LDS
     auto issue = [&](int64_t j, const Seg *tab_) {
-        if (mode == 2) return;
         const int64_t g = blockIdx.x + (j / cnt) * gridDim.x;
         const int ks = wv + static_cast<int>(j % cnt) * nwc;
         const int si = seg_w(g, tab_);
@@ -151,7 +142,7 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     // ---- x loads (four threads per 32-value sub-block, kXPasses passes)
     const XT *x = static_cast<const XT *>(t.seg[0].x);
     const int q = threadIdx.x & 3;
-    const int nsb = mode == 3 ? 0 : nb * 8;
+    const int nsb = nb * 8;
     float xv[kXPasses][8];
 #pragma unroll
     for (int u = 0; u < kXPasses; u++) {
@@ -173,21 +164,19 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     // last `late` waves issue theirs after the table: a wave stalls while
     // the memory pipeline cannot take its DMA, and those waves build the
     // table meanwhile.
-    const int late = late_knob < nwc / 2 ? late_knob : nwc / 2;
+    const int late = kLateWaves < nwc / 2 ? kLateWaves : nwc / 2;
     const bool early = wv < nwc - late;
     const int first = my_units < NSLOT ? static_cast<int>(my_units) : NSLOT;
     if (early) {
 #pragma unroll
         for (int k = 0; k < NSLOT; k++)
             if (k < first) issue(k, t.seg);
-        TRACE(14);
         if (first >= 2) wait_vm<2 * CH>();
         else if (first == 1) wait_vm<CH>();
         else wait_vm<0>();
     } else {
         wait_vm<0>();
     }
-    TRACE(13);
 
     // ---- digit table of x
     for (int i = threadIdx.x; i < kZero / 4; i += blockDim.x) reinterpret_cast<uint32_t *>(zero)[i] = 0u;
@@ -243,7 +232,6 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     }
     const float inv_acc = t.rexp ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
     __syncthreads();
-    TRACE(1);
 
     // ---- per-lane roles
     const int c16 = lane & 15;      // B column = row within a row group; A row
@@ -286,8 +274,6 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
                 }
             __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
             if (j + NSLOT < my_units) issue(j + NSLOT, segl);
-            if (j < 4) TRACE(2 + 3 * j);
-            if (mode == 1) continue;
 #pragma unroll
             for (int b = 0; b < KB; b++) {
                 const int blk = ks * KB + b;
@@ -332,7 +318,6 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
                 }
             }
         }
-        if (j >= 1 && j - 1 < 4) TRACE(3 + 3 * (j - 1));
         // partial sums of the compute waves -> LDS, then one thread per row
         // adds them in wave order and stores the row
         float *rbuf = red + (ti & 1) * nwc * ROWS;
@@ -344,7 +329,6 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
             if (gq == 0) rbuf[wv * ROWS + rg * 16 + c16] = v;
         }
         __syncthreads();
-        if (ti < 4) TRACE(4 + 3 * ti);
         if (threadIdx.x < ROWS) {
             float v = 0.0f;
             for (int k = 0; k < nwc; k++) v += rbuf[k * ROWS + threadIdx.x];
@@ -358,31 +342,6 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
             }
         }
     }
-    TRACE(15);
-}
-
-int mode_knob() {  // experiment: 1 = no compute, 2 = no DMA, 3 = no x table
-    static const int v = [] {
-        const char *e = std::getenv("KRK_DIGITS_MODE");
-        return e ? std::atoi(e) : 0;
-    }();
-    return v;
-}
-
-int late_knob() {
-    static const int v = [] {
-        const char *e = std::getenv("KRK_DIGITS_LATE");
-        return e ? std::atoi(e) : 4;
-    }();
-    return v;
-}
-
-int cfg_knob() {  // experiment: RGN * 100 + KB * 10 + NSLOT, 0 = default
-    static const int v = [] {
-        const char *e = std::getenv("KRK_DIGITS_CFG");
-        return e ? std::atoi(e) : 0;
-    }();
-    return v;
 }
 
 template <typename XT, typename OT, int RGN, int KB, int NSLOT>
@@ -430,31 +389,22 @@ hipError_t launch(SegTable t, hipStream_t st) {
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
     if (grid > total) grid = total;
     hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, RGN, KB, NSLOT>), dim3(static_cast<unsigned>(grid)),
-                       dim3(64 * nw), fixed + nw * per_wave, st, t, total, nks, nw, mode_knob(), late_knob());
+                       dim3(64 * nw), fixed + nw * per_wave, st, t, total, nks, nw);
     return hipGetLastError();
 }
 
+// K <= 8192: 32-row tiles of two blocks per unit; longer rows: 16-row
+// tiles, so the K-split has more tiles to spread over (both measured best of
+// 16/32-row tiles x 1/2 blocks x 2/3 slots at 4096 and 14336)
 template <typename XT, typename OT>
 hipError_t dispatch(const SegTable &t, hipStream_t st) {
-    switch (cfg_knob()) {
-        case 222: return launch<XT, OT, 2, 2, 2>(t, st);
-        case 223: return launch<XT, OT, 2, 2, 3>(t, st);
-        case 212: return launch<XT, OT, 2, 1, 2>(t, st);
-        case 213: return launch<XT, OT, 2, 1, 3>(t, st);
-        case 122: return launch<XT, OT, 1, 2, 2>(t, st);
-        case 113: return launch<XT, OT, 1, 1, 3>(t, st);
-        default:
-            // K <= 8192: 32-row tiles of two blocks per unit; longer rows:
-            // 16-row tiles (more tiles for the K-split to spread over)
-            return t.n_in <= 8192 ? launch<XT, OT, 2, 2, 2>(t, st) : launch<XT, OT, 1, 2, 2>(t, st);
-    }
+    return t.n_in <= 8192 ? launch<XT, OT, 2, 2, 2>(t, st) : launch<XT, OT, 1, 2, 2>(t, st);
 }
 
 }  // namespace
 
 bool gemv_digits_ok(int dt, const SegTable &t) {
     if (dt != DT_Q4_K || t.rows != 1 || t.n_in % 256 || t.n_in > kMaxK || t.row_bytes % 16) return false;
-    if (std::getenv("KRK_DIGITS") && std::atoi(std::getenv("KRK_DIGITS")) == 0) return false;
     for (int i = 0; i < t.n; i++) {
         if (t.seg[i].kind == SEG_SILU || t.seg[i].x != t.seg[0].x) return false;
         if (reinterpret_cast<uintptr_t>(t.seg[i].w) & 15) return false;
