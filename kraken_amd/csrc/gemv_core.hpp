@@ -58,11 +58,13 @@ template <int DT, typename XT, int MR, int RB>
 __device__ __forceinline__ void gemv_rows(const uint8_t *__restrict__ w, int64_t row_bytes,
                                           int64_t n_out, int n_in, const XT *const (&xr)[MR],
                                           int64_t n0, const uint8_t *__restrict__ w2,
-                                          float (&acc)[MR][RB]) {
+                                          float (&acc)[MR][RB], int wv = -1, int nw = 0) {
+    // wv / nw: this wave's share of K (default: the workgroup's waves split it)
     using F = LaneFmt<DT>;
     constexpr int BV = blk_vals(DT), BB = blk_bytes(DT);
     constexpr int BPS = kWave / F::LPB;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    if (wv < 0) { wv = threadIdx.x >> 6; nw = blockDim.x >> 6; }
     const int p = lane % F::LPB, bl = lane / F::LPB;
     const int nb = n_in / BV;
     const int nsteps = (nb + BPS - 1) / BPS;

@@ -2,7 +2,9 @@
 // device pointer table (Backend::moe_dispatch, backend.hpp:1001-1009; the
 // reference's moe_table_* kernels, src/hip/kernels/moe_table.hpp:38-551).
 //
-// Four launches, none of them per expert and none waiting on the host:
+// Decode (one token) takes the two-launch path below the plan kernel; more
+// tokens take four launches, none of them per expert and none waiting on
+// the host:
 //   1. plan      one workgroup: expert-major plan of the (token, slot) pairs,
 //                stable (token-then-slot inside an expert), the active-expert
 //                list in ascending id, and each pair's plan position;
@@ -54,15 +56,21 @@ size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t
 }
 
 // ------------------------------------------------------------------ plan ----
-__global__ void __launch_bounds__(1024) moe_plan_kernel(const int32_t *__restrict__ ids, int64_t P,
+constexpr int kPlanLds = 4096;  // (token, slot) pairs whose ids the plan keeps in LDS
+__global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict__ ids, int64_t P,
                                                         int k, int ne, MoeWs w) {
     __shared__ int32_t cnt[1024];
     __shared__ int32_t offs[1025];
+    __shared__ int32_t sid[kPlanLds];   // the ids, when they fit
     const int tid = threadIdx.x;
+    const bool in_lds = P <= kPlanLds;
     for (int e = tid; e < ne; e += blockDim.x) cnt[e] = 0;
+    if (in_lds)
+        for (int64_t i = tid; i < P; i += blockDim.x) sid[i] = ids[i];
     __syncthreads();
+    auto id_at = [&](int64_t i) { return in_lds ? sid[i] : ids[i]; };
     for (int64_t i = tid; i < P; i += blockDim.x) {
-        const int e = ids[i];
+        const int e = id_at(i);
         if (e >= 0 && e < ne) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
@@ -70,28 +78,27 @@ __global__ void __launch_bounds__(1024) moe_plan_kernel(const int32_t *__restric
         int run = 0, na = 0;
         for (int e = 0; e < ne; e++) {
             offs[e] = run;
-            w.off[e] = run;
             if (cnt[e]) w.act[na++] = e;
             run += cnt[e];
         }
         offs[ne] = run;
-        w.off[ne] = run;
         w.n_act[0] = na;
     }
     __syncthreads();
+    for (int e = tid; e <= ne; e += blockDim.x) w.off[e] = offs[e];
     // stable placement: expert e's pairs in ascending pair index (token, slot)
     for (int e = tid; e < ne; e += blockDim.x) {
         if (!cnt[e]) continue;
         int c = offs[e];
         for (int64_t i = 0; i < P; i++)
-            if (ids[i] == e) {
+            if (id_at(i) == e) {
                 w.plan_tok[c] = static_cast<int32_t>(i / k);
                 w.plan_pos[i] = c;
                 c++;
             }
     }
     for (int64_t i = tid; i < P; i += blockDim.x) {
-        const int e = ids[i];
+        const int e = id_at(i);
         if (e < 0 || e >= ne) w.plan_pos[i] = -1;
     }
 }
@@ -103,8 +110,11 @@ __global__ void __launch_bounds__(512) moe_gu_kernel(const krk_moe_entry *__rest
                                                       int64_t n_ff, int64_t groups, MoeWs w) {
     __shared__ float red[8][MR * RB];
     constexpr int H = RB / 2;
-    const int64_t a = blockIdx.x / groups, g = blockIdx.x % groups;
-    if (a >= w.n_act[0]) return;
+    // persistent: items (active expert, row group) in expert-major order; the
+    // first item past the active experts ends the walk
+    const int64_t items = static_cast<int64_t>(w.n_act[0]) * groups;
+    for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+    const int64_t a = item / groups, g = item % groups;
     const int e = w.act[a];
     const krk_moe_entry &en = tab[e];
     const int64_t n0 = g * H;
@@ -147,6 +157,7 @@ __global__ void __launch_bounds__(512) moe_gu_kernel(const krk_moe_entry *__rest
         }
         __syncthreads();
     }
+    }
 }
 
 // ----------------------------------------------------------------- down ----
@@ -155,8 +166,9 @@ __global__ void __launch_bounds__(512) moe_down_kernel(const krk_moe_entry *__re
                                                         int64_t n_embd, int64_t n_ff,
                                                         int64_t groups, MoeWs w) {
     __shared__ float red[8][MR * RB];
-    const int64_t a = blockIdx.x / groups, g = blockIdx.x % groups;
-    if (a >= w.n_act[0]) return;
+    const int64_t items = static_cast<int64_t>(w.n_act[0]) * groups;
+    for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+    const int64_t a = item / groups, g = item % groups;
     const int e = w.act[a];
     const krk_moe_entry &en = tab[e];
     const int64_t n0 = g * RB;
@@ -194,6 +206,7 @@ __global__ void __launch_bounds__(512) moe_down_kernel(const krk_moe_entry *__re
         }
         __syncthreads();
     }
+    }
 }
 
 // --------------------------------------------------------------- reduce ----
@@ -223,6 +236,114 @@ __global__ void __launch_bounds__(256) moe_reduce_kernel(const int32_t *__restri
     out[t * n_embd + j] = static_cast<OT>(acc);
 }
 
+// ------------------------------------------------------- one token ----
+// Decode (n_tok == 1) needs no plan: the token's experts are ids[0..k-1].
+// Two launches: gate/up per (slot, row group) into mid[slot], then the down
+// projections fused with the reduction -- a workgroup owns RB output rows
+// and walks the token's experts in ascending id, adding fma(w, part, acc)
+// in that order (the host loop's order), so no per-slot partials are stored
+// and no reduce launch follows.
+template <typename XT, int RB>
+__global__ void __launch_bounds__(512) moe_gu1_kernel(const krk_moe_entry *__restrict__ tab,
+                                                       const int32_t *__restrict__ ids, int k, int ne,
+                                                       const XT *__restrict__ xn, int64_t n_embd,
+                                                       int64_t n_ff, int64_t groups, float *__restrict__ mid) {
+    __shared__ float red[8][RB];
+    constexpr int H = RB / 2;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int64_t items = static_cast<int64_t>(k) * groups;
+    for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+        const int s = static_cast<int>(item / groups);
+        const int64_t n0 = (item % groups) * H;
+        const int e = ids[s];
+        if (e < 0 || e >= ne) continue;   // a dropped slot (uniform per workgroup)
+        const krk_moe_entry &en = tab[e];
+        const XT *xr[1] = {xn};
+        float acc[1][RB];
+        const uint8_t *wg = static_cast<const uint8_t *>(en.p[KRK_MOE_GATE]);
+        const uint8_t *wu = static_cast<const uint8_t *>(en.p[KRK_MOE_UP]);
+        switch (en.type[KRK_MOE_GATE]) {
+            case DT_Q4_K: gemv_rows<DT_Q4_K, XT, 1, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
+            case DT_Q6_K: gemv_rows<DT_Q6_K, XT, 1, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
+            case DT_Q4_0: gemv_rows<DT_Q4_0, XT, 1, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
+            default:      gemv_rows<DT_Q8_0, XT, 1, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
+        }
+        float v[RB];
+#pragma unroll
+        for (int r = 0; r < RB; r++) v[r] = acc[0][r];
+        wave_reduce_multi<RB>(v, lane);
+        if (reduce_owner<RB>(lane)) red[wv][reduce_owner_index<RB>(lane)] = v[0];
+        __syncthreads();
+        if (threadIdx.x < H) {
+            const int r = threadIdx.x;
+            float gs = 0.0f, us = 0.0f;
+            for (int kk = 0; kk < nw; kk++) {
+                gs += red[kk][r];
+                us += red[kk][H + r];
+            }
+            const int64_t n = n0 + r;
+            if (n < n_ff) mid[static_cast<int64_t>(s) * n_ff + n] = (gs / (1.0f + expf(-gs))) * us;
+        }
+        __syncthreads();
+    }
+}
+
+template <typename OT, int RB>
+__global__ void __launch_bounds__(512) moe_down1_kernel(const krk_moe_entry *__restrict__ tab,
+                                                         const int32_t *__restrict__ ids,
+                                                         const float *__restrict__ wts, int k, int ne,
+                                                         int64_t n_embd, int64_t n_ff, int64_t groups,
+                                                         const float *__restrict__ mid, OT *__restrict__ out) {
+    // wave q computes the RB rows for the token's q-th expert in ascending
+    // id; the partials meet in LDS and one thread per row adds them in q order
+    __shared__ float part[64][RB];
+    __shared__ int ord[64];
+    __shared__ int nlive;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if (threadIdx.x == 0) {
+        // the token's live slots in ascending expert id (insertion sort, k <= 64)
+        int n = 0;
+        for (int s = 0; s < k; s++) {
+            const int e = ids[s];
+            if (e < 0 || e >= ne) continue;
+            int q = n++;
+            while (q > 0 && ids[ord[q - 1]] > e) { ord[q] = ord[q - 1]; q--; }
+            ord[q] = s;
+        }
+        nlive = n;
+    }
+    __syncthreads();
+    const int nq = nlive;
+    for (int64_t g = blockIdx.x; g < groups; g += gridDim.x) {
+        const int64_t n0 = g * RB;
+        for (int q = wv; q < nq; q += nw) {
+            const int s = ord[q];
+            const krk_moe_entry &en = tab[ids[s]];
+            const float *xr[1] = {mid + static_cast<int64_t>(s) * n_ff};
+            float a2[1][RB];
+            const uint8_t *wd = static_cast<const uint8_t *>(en.p[KRK_MOE_DOWN]);
+            switch (en.type[KRK_MOE_DOWN]) {
+                case DT_Q4_K: gemv_rows<DT_Q4_K, float, 1, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, a2, 0, 1); break;
+                case DT_Q6_K: gemv_rows<DT_Q6_K, float, 1, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, a2, 0, 1); break;
+                case DT_Q4_0: gemv_rows<DT_Q4_0, float, 1, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, a2, 0, 1); break;
+                default:      gemv_rows<DT_Q8_0, float, 1, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, a2, 0, 1); break;
+            }
+            float v[RB];
+#pragma unroll
+            for (int r = 0; r < RB; r++) v[r] = a2[0][r];
+            wave_reduce_multi<RB>(v, lane);
+            if (reduce_owner<RB>(lane)) part[q][reduce_owner_index<RB>(lane)] = v[0];
+        }
+        __syncthreads();
+        if (threadIdx.x < RB && n0 + threadIdx.x < n_embd) {
+            float acc = 0.0f;
+            for (int q = 0; q < nq; q++) acc = __builtin_fmaf(wts[ord[q]], part[q][threadIdx.x], acc);
+            out[n0 + threadIdx.x] = static_cast<OT>(acc);
+        }
+        __syncthreads();
+    }
+}
+
 hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t st) {
     const int64_t P = a.n_tok * a.k;
     if (ws_bytes < moe_workspace(a.n_tok, a.k, a.n_expert, a.n_embd, a.n_ff)) return hipErrorInvalidValue;
@@ -230,34 +351,47 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     MoeWs w = carve(ws, P, a.n_expert, a.n_embd, a.n_ff);
     const krk_moe_entry *tab = static_cast<const krk_moe_entry *>(a.table) +
                                static_cast<int64_t>(a.layer) * a.n_expert;
-    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(1024), 0, st, a.ids, P, a.k, a.n_expert, w);
-    const int64_t amax = P < a.n_expert ? P : a.n_expert;
     auto waves = [](int64_t K) {
         int64_t steps = (K / 32 + 63) / 64;  // 2048 values per wave step
         return static_cast<int>(steps < 1 ? 1 : steps > 8 ? 8 : steps);
     };
     const int wgu = waves(a.n_embd), wdn = waves(a.n_ff);
+    // the active-expert count is known on the device only: launch a grid
+    // the chip keeps resident and let the workgroups walk the items
+    auto cap = [](int64_t want, int waves_per_wg) {
+        const int64_t resident = 256LL * (32 / waves_per_wg);
+        return dim3(static_cast<unsigned>(want < resident ? want : resident));
+    };
     if (a.n_tok == 1) {
         const int64_t ggu = (a.n_ff + 3) / 4, gdn = (a.n_embd + 7) / 8;
         if (a.act_f16)
-            hipLaunchKernelGGL((moe_gu_kernel<_Float16, 1, 8>), dim3(amax * ggu), dim3(64 * wgu), 0, st,
-                               tab, static_cast<const _Float16 *>(a.xn), a.n_embd, a.n_ff, ggu, w);
+            hipLaunchKernelGGL((moe_gu1_kernel<_Float16, 8>), cap(a.k * ggu, wgu), dim3(64 * wgu), 0, st, tab,
+                               a.ids, a.k, a.n_expert, static_cast<const _Float16 *>(a.xn), a.n_embd, a.n_ff,
+                               ggu, w.mid);
         else
-            hipLaunchKernelGGL((moe_gu_kernel<float, 1, 8>), dim3(amax * ggu), dim3(64 * wgu), 0, st,
-                               tab, static_cast<const float *>(a.xn), a.n_embd, a.n_ff, ggu, w);
-        hipLaunchKernelGGL((moe_down_kernel<1, 8>), dim3(amax * gdn), dim3(64 * wdn), 0, st, tab,
-                           a.n_embd, a.n_ff, gdn, w);
-    } else {
-        const int64_t ggu = (a.n_ff + 1) / 2, gdn = (a.n_embd + 3) / 4;
+            hipLaunchKernelGGL((moe_gu1_kernel<float, 8>), cap(a.k * ggu, wgu), dim3(64 * wgu), 0, st, tab,
+                               a.ids, a.k, a.n_expert, static_cast<const float *>(a.xn), a.n_embd, a.n_ff,
+                               ggu, w.mid);
         if (a.act_f16)
-            hipLaunchKernelGGL((moe_gu_kernel<_Float16, 2, 4>), dim3(amax * ggu), dim3(64 * wgu), 0, st,
-                               tab, static_cast<const _Float16 *>(a.xn), a.n_embd, a.n_ff, ggu, w);
+            hipLaunchKernelGGL((moe_down1_kernel<_Float16, 8>), cap(gdn, 8), dim3(64 * 8), 0, st, tab, a.ids,
+                               a.wts, a.k, a.n_expert, a.n_embd, a.n_ff, gdn, w.mid,
+                               static_cast<_Float16 *>(a.out));
         else
-            hipLaunchKernelGGL((moe_gu_kernel<float, 2, 4>), dim3(amax * ggu), dim3(64 * wgu), 0, st,
-                               tab, static_cast<const float *>(a.xn), a.n_embd, a.n_ff, ggu, w);
-        hipLaunchKernelGGL((moe_down_kernel<2, 4>), dim3(amax * gdn), dim3(64 * wdn), 0, st, tab,
-                           a.n_embd, a.n_ff, gdn, w);
+            hipLaunchKernelGGL((moe_down1_kernel<float, 8>), cap(gdn, 8), dim3(64 * 8), 0, st, tab, a.ids,
+                               a.wts, a.k, a.n_expert, a.n_embd, a.n_ff, gdn, w.mid, static_cast<float *>(a.out));
+        return hipGetLastError();
     }
+    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w);
+    const int64_t amax = P < a.n_expert ? P : a.n_expert;
+    const int64_t ggu = (a.n_ff + 1) / 2, gdn = (a.n_embd + 3) / 4;
+    if (a.act_f16)
+        hipLaunchKernelGGL((moe_gu_kernel<_Float16, 2, 4>), cap(amax * ggu, wgu), dim3(64 * wgu), 0, st,
+                           tab, static_cast<const _Float16 *>(a.xn), a.n_embd, a.n_ff, ggu, w);
+    else
+        hipLaunchKernelGGL((moe_gu_kernel<float, 2, 4>), cap(amax * ggu, wgu), dim3(64 * wgu), 0, st,
+                           tab, static_cast<const float *>(a.xn), a.n_embd, a.n_ff, ggu, w);
+    hipLaunchKernelGGL((moe_down_kernel<2, 4>), cap(amax * gdn, wdn), dim3(64 * wdn), 0, st, tab,
+                       a.n_embd, a.n_ff, gdn, w);
     const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));
     if (a.act_f16)
         hipLaunchKernelGGL((moe_reduce_kernel<_Float16>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
