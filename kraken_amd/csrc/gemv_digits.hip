@@ -97,13 +97,18 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         return i;
     };
 
-    // chunk c, lane l: slot bytes [1024c + 16l, +16) = row o / P, offset o % P
+    // chunk c, lane l: slot bytes [1024c + 16l, +16) = tile row r = o / P at
+    // offset o % P.  Rows 0..15 come from base 0, rows 16..31 from base 1:
+    // the next 16 rows of the same matrix, or for a gate/up (SiLU) segment
+    // the same 16 rows of the up matrix.
     int32_t dl[CH];
+    uint32_t hi_rows = 0;   // bit c: this lane's chunk c lies in rows 16..31
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int o = c * 1024 + 16 * lane;
-        const int r = o / P;
-        dl[c] = o < U ? static_cast<int32_t>(r * rb + (o - r * P)) : 0;
+        const int r = o < U ? o / P : 0;
+        dl[c] = o < U ? static_cast<int32_t>((r & 15) * rb + (o - r * P)) : 0;
+        if (r >= 16) hi_rows |= 1u << c;
     }
     // the first units read the segment table from the kernel arguments (the
     // LDS copy is not ready yet); later ones from LDS
@@ -111,16 +116,19 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         const int64_t g = blockIdx.x + (j / cnt) * gridDim.x;
         const int ks = wv + static_cast<int>(j % cnt) * nwc;
         const int si = seg_w(g, tab_);
+        const bool pair = tab_[si].kind == SEG_SILU;
+        const int tr = pair ? 16 : ROWS;               // output rows per tile
         const uint8_t *w = static_cast<const uint8_t *>(tab_[si].w);
+        const uint8_t *w1 = pair ? static_cast<const uint8_t *>(tab_[si].w2) : w + 16 * rb;
         const int64_t n_out = tab_[si].n_out;
-        const int64_t n0 = (g - tab_[si].blk_begin) * ROWS;
+        const int64_t n0 = (g - tab_[si].blk_begin) * tr;
         const int64_t k0 = static_cast<int64_t>(ks) * P;
         uint8_t *dst = slots + static_cast<int>(j % NSLOT) * SLOT;
-        if ((n0 + ROWS - 1) * rb + k0 + P <= n_out * rb) {
-            const uint8_t *base = w + n0 * rb + k0;
+        if ((n0 + tr - 1) * rb + k0 + P <= n_out * rb) {
+            const uint8_t *b0 = w + n0 * rb + k0, *b1 = w1 + n0 * rb + k0;
 #pragma unroll
             for (int c = 0; c < CH; c++)
-                __builtin_amdgcn_global_load_lds(static_cast<const void *>(base + dl[c]),
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>(((hi_rows >> c) & 1 ? b1 : b0) + dl[c]),
                                                  (lds_void_t *)(dst + c * 1024), 16, 0, 0);
         } else {
             // the matrix's last rows: clamp rows and row ends to stay inside
@@ -129,11 +137,12 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
             for (int c = 0; c < CH; c++) {
                 const int o = c * 1024 + 16 * lane;
                 const int r = o < U ? o / P : 0;
-                int64_t n = n0 + r;
+                const bool up = pair && r >= 16;
+                int64_t n = n0 + (pair ? (r & 15) : r);
                 if (n >= n_out) n = n_out - 1;
                 int64_t off = k0 + (o < U ? o - r * P : 0);
                 if (off > lim) off = lim;
-                __builtin_amdgcn_global_load_lds(static_cast<const void *>(w + n * rb + off),
+                __builtin_amdgcn_global_load_lds(static_cast<const void *>((up ? w1 : w) + n * rb + off),
                                                  (lds_void_t *)(dst + c * 1024), 16, 0, 0);
             }
         }
@@ -330,15 +339,38 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         }
         __syncthreads();
         if (threadIdx.x < ROWS) {
-            float v = 0.0f;
-            for (int k = 0; k < nwc; k++) v += rbuf[k * ROWS + threadIdx.x];
             const int64_t g = blockIdx.x + ti * gridDim.x;
             const int si = seg_w(g, segl);
-            const int64_t n = (g - segl[si].blk_begin) * ROWS + threadIdx.x;
-            if (n < segl[si].n_out) {
-                const int kind = segl[si].kind;
-                store_out<OT>(static_cast<OT *>(segl[si].out) + n, v, kind,
-                              kind == SEG_ACC ? inv_acc : 1.0f);
+            const int kind = segl[si].kind;
+            if (kind == SEG_SILU) {
+                // rows t and 16 + t of the tile are gate and up of output n0 + t
+                if (threadIdx.x < 16) {
+                    float gs = 0.0f, us = 0.0f;
+                    for (int k = 0; k < nwc; k++) {
+                        gs += rbuf[k * ROWS + threadIdx.x];
+                        us += rbuf[k * ROWS + 16 + threadIdx.x];
+                    }
+                    const int64_t n = (g - segl[si].blk_begin) * 16 + threadIdx.x;
+                    if (n < segl[si].n_out) {
+                        OT *o = static_cast<OT *>(segl[si].out) + n;
+                        if constexpr (sizeof(OT) == 2) {
+                            // fused_gate_silu_kernel (fused.hpp:161-166): both
+                            // dots rounded to f16, activation in f32, saturated
+                            const float hg = static_cast<float>(static_cast<_Float16>(gs));
+                            const float hu = static_cast<float>(static_cast<_Float16>(us));
+                            *o = sat_f16(silu_f(hg) * hu);
+                        } else {
+                            *o = (gs / (1.0f + expf(-gs))) * us;   // silu_mul, backend_cpu.cpp:2401-2406
+                        }
+                    }
+                }
+            } else {
+                float v = 0.0f;
+                for (int k = 0; k < nwc; k++) v += rbuf[k * ROWS + threadIdx.x];
+                const int64_t n = (g - segl[si].blk_begin) * ROWS + threadIdx.x;
+                if (n < segl[si].n_out)
+                    store_out<OT>(static_cast<OT *>(segl[si].out) + n, v, kind,
+                                  kind == SEG_ACC ? inv_acc : 1.0f);
             }
         }
     }
@@ -351,7 +383,8 @@ hipError_t launch(SegTable t, hipStream_t st) {
     int64_t total = 0;
     for (int i = 0; i < t.n; i++) {
         t.seg[i].blk_begin = total;
-        total += (t.seg[i].n_out + ROWS - 1) / ROWS;
+        const int64_t tr = t.seg[i].kind == SEG_SILU ? 16 : ROWS;   // gate/up: 16 + 16 rows
+        total += (t.seg[i].n_out + tr - 1) / tr;
     }
     const int nb = t.n_in / 256;
     const int nks = (nb + KB - 1) / KB;
@@ -406,7 +439,9 @@ hipError_t dispatch(const SegTable &t, hipStream_t st) {
 bool gemv_digits_ok(int dt, const SegTable &t) {
     if (dt != DT_Q4_K || t.rows != 1 || t.n_in % 256 || t.n_in > kMaxK || t.row_bytes % 16) return false;
     for (int i = 0; i < t.n; i++) {
-        if (t.seg[i].kind == SEG_SILU || t.seg[i].x != t.seg[0].x) return false;
+        if (t.seg[i].x != t.seg[0].x) return false;
+        if (t.seg[i].kind == SEG_SILU && (t.n_in > 8192 || (reinterpret_cast<uintptr_t>(t.seg[i].w2) & 15)))
+            return false;   // gate/up pairs use the 32-row tiles
         if (reinterpret_cast<uintptr_t>(t.seg[i].w) & 15) return false;
     }
     return true;
