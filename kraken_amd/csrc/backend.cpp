@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "krk_kernels.hpp"
 #include "krk_mi355x.h"
@@ -34,7 +35,7 @@ struct krk_backend {
     size_t ws_bytes = 0;
     std::string err;
     static constexpr int kMoeCache = 256;  // layers of MoE tables checked once
-    struct MoeOk { MoeKey key; krk_moe_entry e0; };
+    struct MoeOk { MoeKey key; krk_moe_entry e0; bool aligned; };
     MoeOk moe_ok[kMoeCache];
     int n_moe_ok = 0;
 };
@@ -362,13 +363,14 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
     if (reinterpret_cast<uintptr_t>(xn) & 15)
         return fail(b, KRK_ERR_ARG, "moe_dispatch: xn is not 16-byte aligned");
     if (int s = make_current(b)) return s;
-    // The table lives on the device and the kernels read every entry's type
-    // and strides there.  The host checks the layer's geometry once per
-    // (table, layer): the first call reads entry 0 back (one synchronous
-    // copy), later calls find it in the cache and stay asynchronous, so a
-    // steady-state dispatch can be captured in a graph.  A table rewritten
-    // in place with another geometry after its first use is not re-checked.
+    // The table lives on the device and the kernels read the routed entries
+    // there.  The host checks the layer once per (table, layer): the first
+    // call reads the layer's entries back (one synchronous copy), later calls
+    // find the result in the cache and stay asynchronous, so a steady-state
+    // dispatch can be captured in a graph.  A table rewritten in place after
+    // its first use is not re-checked.
     krk_moe_entry e0{};
+    bool aligned = false;
     const krk_moe_entry *tab = static_cast<const krk_moe_entry *>(table);
     const MoeKey key{table, layer, n_expert, n_embd, n_ff};
     int hit = -1;
@@ -376,21 +378,32 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
         if (b->moe_ok[i].key == key) { hit = i; break; }
     if (hit >= 0) {
         e0 = b->moe_ok[hit].e0;
+        aligned = b->moe_ok[hit].aligned;
     } else {
-        hipError_t he = hipMemcpyAsync(&e0, tab + static_cast<int64_t>(layer) * n_expert, sizeof(e0),
-                                       hipMemcpyDeviceToHost, b->stream);
+        // every bank of the layer: present, on this path, one weight type,
+        // the layer's geometry; and whether all rows start 16-byte aligned
+        std::vector<krk_moe_entry> ents(static_cast<size_t>(n_expert));
+        hipError_t he = hipMemcpyAsync(ents.data(), tab + static_cast<int64_t>(layer) * n_expert,
+                                       sizeof(krk_moe_entry) * ents.size(), hipMemcpyDeviceToHost, b->stream);
         if (he == hipSuccess) he = hipStreamSynchronize(b->stream);
-        if (he != hipSuccess) return hip_fail(b, he, "moe_dispatch: reading table entry");
-        for (int m = 0; m < 3; m++) {
-            if (!e0.present[m] || !dtype_on_path(e0.type[m]))
-                return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: matrix %d absent or of type %d", m,
-                            e0.type[m]);
-            if (e0.type[m] != e0.type[0])
-                return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: mixed expert formats");
+        if (he != hipSuccess) return hip_fail(b, he, "moe_dispatch: reading the table");
+        e0 = ents[0];
+        aligned = true;
+        for (int e = 0; e < n_expert; e++) {
+            const krk_moe_entry &en = ents[static_cast<size_t>(e)];
+            for (int m = 0; m < 3; m++) {
+                if (!en.present[m] || !dtype_on_path(en.type[m]))
+                    return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: expert %d matrix %d absent or of type %d",
+                                e, m, en.type[m]);
+                if (en.type[m] != e0.type[0])
+                    return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: mixed expert formats");
+                if (reinterpret_cast<uintptr_t>(en.p[m]) & 15) aligned = false;
+            }
+            if (en.n_in[0] != n_embd || en.n_out[0] != n_ff || en.n_in[1] != n_embd || en.n_out[1] != n_ff ||
+                en.n_in[2] != n_ff || en.n_out[2] != n_embd)
+                return fail(b, KRK_ERR_SHAPE, "moe_dispatch: expert %d geometry does not match n_embd/n_ff", e);
         }
-        if (e0.n_in[0] != n_embd || e0.n_out[0] != n_ff || e0.n_in[2] != n_ff || e0.n_out[2] != n_embd)
-            return fail(b, KRK_ERR_SHAPE, "moe_dispatch: table geometry does not match n_embd/n_ff");
-        if (b->n_moe_ok < krk_backend::kMoeCache) b->moe_ok[b->n_moe_ok++] = {key, e0};
+        if (b->n_moe_ok < krk_backend::kMoeCache) b->moe_ok[b->n_moe_ok++] = {key, e0, aligned};
     }
     krk::MoeArgs a{};
     a.table = table; a.layer = layer; a.n_expert = n_expert; a.k = k;
@@ -401,6 +414,7 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
     a.act_f16 = b->act == KRK_ACT_F16;
     a.wt = e0.type[0];
     a.rb_gate = e0.row_bytes[0]; a.rb_up = e0.row_bytes[1]; a.rb_down = e0.row_bytes[2];
+    a.aligned16 = aligned;
     if (int s = ensure_ws(b, krk::moe_workspace(n_tok, k, n_expert, n_embd, n_ff))) return s;
     const hipError_t he = krk::moe_dispatch(a, b->ws, b->ws_bytes, b->stream);
     return he == hipSuccess ? KRK_OK : hip_fail(b, he, "moe_dispatch");

@@ -10,7 +10,7 @@
 //     single AND (and a shift for the high ones): 0.375 VALU ops per weight.
 //   * A operand: the activations as exact integers.  Each 32-value
 //     sub-block of x is scaled by a power of two so that its largest value
-//     has 22 bits, rounded to an integer X (error <= 2^-23 of the sub-block
+//     has 22 bits, rounded to an integer X (error <= 2^-22 of the sub-block
 //     maximum) and split into three balanced int8 digits,
 //     X = d0 + 2^8 d1 + 2^16 d2.  Rows 4s'+p of A hold digit plane p of
 //     sub-block s', zero elsewhere, so one 16x16x64 MFMA yields for every
@@ -31,6 +31,7 @@
 #include "gemv_core.hpp"
 #include "krk_formats.hpp"
 #include "krk_kernels.hpp"
+#include "krk_mi355x.h"
 
 namespace krk {
 
@@ -169,6 +170,24 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
             for (int k = 0; k < 8; k++) xv[u][k] = static_cast<float>(h[k]);
         }
     }
+    // ---- routed experts: resolve the segments on the device first (one
+    // dependent read of the ids and the table entries per workgroup)
+    const bool moe = t.moe_tab != nullptr;
+    if (moe) {
+        if (threadIdx.x < nseg) {
+            const int32_t *ids = t.moe_ids;
+            const krk_moe_entry *mt = static_cast<const krk_moe_entry *>(t.moe_tab);
+            int e = ids[threadIdx.x];
+            if (e < 0 || e >= t.moe_ne) e = 0;   // a dropped slot: any bank, its row is never read
+            Seg sg = t.seg[threadIdx.x];
+            sg.w = mt[e].p[KRK_MOE_GATE];
+            sg.w2 = mt[e].p[KRK_MOE_UP];
+            sg.out = static_cast<float *>(t.seg[0].out) + static_cast<int64_t>(threadIdx.x) * t.seg[0].n_out;
+            segl[threadIdx.x] = sg;
+        }
+        __syncthreads();
+    }
+
     // ---- weight DMA of the first NSLOT units, then wait for x only.  The
     // last `late` waves issue theirs after the table: a wave stalls while
     // the memory pipeline cannot take its DMA, and those waves build the
@@ -177,9 +196,15 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     const bool early = wv < nwc - late;
     const int first = my_units < NSLOT ? static_cast<int>(my_units) : NSLOT;
     if (early) {
+        if (moe) {
 #pragma unroll
-        for (int k = 0; k < NSLOT; k++)
-            if (k < first) issue(k, t.seg);
+            for (int k = 0; k < NSLOT; k++)
+                if (k < first) issue(k, segl);
+        } else {
+#pragma unroll
+            for (int k = 0; k < NSLOT; k++)
+                if (k < first) issue(k, t.seg);
+        }
         if (first >= 2) wait_vm<2 * CH>();
         else if (first == 1) wait_vm<CH>();
         else wait_vm<0>();
@@ -206,11 +231,13 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         sum += __shfl_xor(sum, 2, 64);
         if (sb >= nsb) continue;
         // 2^e with |x| * 2^e < 2^22: from amax's exponent field E (amax in
-        // [2^(E-127), 2^(E-126))), e = 149 - E, kept where 2^e and 2^-e
-        // are normal floats; zero and non-finite sub-blocks get no digits
+        // [2^(E-127), 2^(E-126))), e = 148 - E puts amax * 2^e in
+        // [2^21, 2^22), so the top digit stays within [-64, 64]; kept where
+        // 2^e and 2^-e are normal floats; zero and non-finite sub-blocks get
+        // no digits
         const uint32_t Eb = (__float_as_uint(amax) >> 23) & 255u;
         const bool live = amax > 0.0f && Eb < 255u;
-        int e = live ? 149 - static_cast<int>(Eb) : 0;
+        int e = live ? 148 - static_cast<int>(Eb) : 0;
         e = e > 126 ? 126 : e;
         const float up = __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
         const float dn = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
@@ -233,11 +260,17 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         *reinterpret_cast<u32x2 *>(o + 64) = u32x2{p2[0], p2[1]};
         if (q == 0) ex[sb] = float2{live ? dn : 1.0f, sum};
     }
-    if (threadIdx.x < nseg) segl[threadIdx.x] = t.seg[threadIdx.x];
+    if (!moe && threadIdx.x < nseg) segl[threadIdx.x] = t.seg[threadIdx.x];
     if (!early) {
+        if (moe) {
 #pragma unroll
-        for (int k = 0; k < NSLOT; k++)
-            if (k < first) issue(k, t.seg);
+            for (int k = 0; k < NSLOT; k++)
+                if (k < first) issue(k, segl);
+        } else {
+#pragma unroll
+            for (int k = 0; k < NSLOT; k++)
+                if (k < first) issue(k, t.seg);
+        }
     }
     const float inv_acc = t.rexp ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
     __syncthreads();

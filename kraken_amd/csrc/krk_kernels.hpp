@@ -34,6 +34,12 @@ struct SegTable {
     int64_t x_stride;    // elements between activation rows
     int64_t out_stride;  // elements between output rows
     const int32_t *rexp; // SEG_ACC exponent (nullable)
+    // Routed experts (nullable): segment i's gate / up pointers are read on
+    // the device from moe_tab[moe_ids[i]] (krk_moe_entry) instead of seg[i].w /
+    // w2; seg[i].out is then seg[0].out + i * seg[0].n_out.
+    const void *moe_tab;
+    const int32_t *moe_ids;
+    int moe_ne;
 };
 
 hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st);
@@ -77,6 +83,7 @@ struct MoeArgs {
     bool act_f16;
     int wt;              // the (uniform) weight type of the experts
     int64_t rb_gate, rb_up, rb_down;
+    bool aligned16;      // every bank's rows start 16-byte aligned
 };
 size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t n_ff);
 hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t st);

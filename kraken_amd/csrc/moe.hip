@@ -364,7 +364,29 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     };
     if (a.n_tok == 1) {
         const int64_t ggu = (a.n_ff + 3) / 4, gdn = (a.n_embd + 7) / 8;
-        if (a.act_f16)
+        // Q4_K banks with f32 activations: gate/up on the int8 matrix cores
+        // (the digits GEMV), the routed banks resolved on the device
+        SegTable t{};
+        t.n = a.k;
+        t.n_in = static_cast<int>(a.n_embd);
+        t.row_bytes = a.rb_gate;
+        t.rows = 1;
+        t.x_stride = a.n_embd;
+        t.out_stride = a.n_ff;
+        t.moe_tab = tab;
+        t.moe_ids = a.ids;
+        t.moe_ne = a.n_expert;
+        for (int i = 0; i < a.k && i < kMaxSegs; i++) {
+            t.seg[i].x = a.xn;
+            t.seg[i].out = w.mid;
+            t.seg[i].n_out = a.n_ff;
+            t.seg[i].kind = SEG_SILU;
+        }
+        if (!a.act_f16 && a.wt == DT_Q4_K && a.aligned16 && a.k <= kMaxSegs && a.rb_gate == a.rb_up &&
+            gemv_digits_ok(DT_Q4_K, t)) {
+            const hipError_t e = gemv_digits(false, t, st);
+            if (e != hipSuccess) return e;
+        } else if (a.act_f16)
             hipLaunchKernelGGL((moe_gu1_kernel<_Float16, 8>), cap(a.k * ggu, wgu), dim3(64 * wgu), 0, st, tab,
                                a.ids, a.k, a.n_expert, static_cast<const _Float16 *>(a.xn), a.n_embd, a.n_ff,
                                ggu, w.mid);

@@ -296,6 +296,45 @@ def test_moe_dispatch_parity(krk, torch_cuda, be32, n_tok):
     assert e <= GEMV_TOL
 
 
+# ------------------------------------------------- digit-plane edge cases --
+def digit_edge_x(n_in, seed):
+    """Activations whose 32-value sub-blocks put the digit split at its
+    limits: a largest magnitude just under a power of two (the top int8 digit
+    at its bound), constant sub-blocks, zero, subnormal and wide-range ones."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal(n_in).astype(np.float32)
+    top = np.float32(np.nextafter(np.float32(2.0), np.float32(0.0)))   # 2 - 2^-23
+    for sb in range(n_in // 32):
+        v = x[32 * sb:32 * sb + 32]
+        kind, scale = sb % 6, np.float32(2.0) ** int(rng.integers(-8, 8))
+        if kind == 0:
+            np.clip(v, -1.9, 1.9, out=v)
+            v[int(rng.integers(32))] = top * (1 if sb % 2 else -1)
+        elif kind == 1:
+            v[:] = top
+        elif kind == 2:
+            v[:] = -top * rng.uniform(0.999, 1.0, 32).astype(np.float32)
+        elif kind == 3:
+            v[:] = 0.0
+        elif kind == 4:
+            v[:] = v * np.float32(1e-41)
+        v *= scale
+    return x
+
+
+@pytest.mark.parametrize("n_in", [512, 4096, 14336])
+def test_q4_k_digits_extreme_sub_blocks(krk, torch_cuda, be32, n_in):
+    torch = torch_cuda
+    n_out = 96
+    w = make_weights(krk, O.Q4_K, n_out, n_in, seed=700 + n_in)
+    x = digit_edge_x(n_in, seed=n_in)
+    say("digits edge", n_out, n_in)
+    out = torch.empty((1, n_out), dtype=torch.float32, device="cuda")
+    be32.gemm(out, dev(torch, x), dev(torch, w), O.Q4_K, n_out, n_in, 1)
+    be32.sync()
+    assert rel(host(out)[0], O.gemm(O.Q4_K, w, x, n_out)[0]) <= GEMV_TOL
+
+
 # ------------------------------------------------- full-size configurations --
 def test_headline_q4_k_gemv_full_size(krk, torch_cuda, be32):
     """BASELINE config 2 headline shape: Q4_K 4096 -> 14336, M = 1."""
