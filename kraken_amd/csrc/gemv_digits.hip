@@ -20,7 +20,7 @@
 //     sub-block):  y += d*sc * 2^-e * (C0 + 2^8 C1 + 2^16 C2) - dmin*m * sum(x).
 //
 // The products are exact; the result differs from the f32 reference chain
-// only by the 2^-23 activation rounding and f32 accumulation order, far
+// only by the 2^-22 activation rounding and f32 accumulation order, far
 // inside the 1e-5 relative budget.
 //
 // Data movement: each wave streams units of 16*RGN rows x 256*KB values
@@ -50,6 +50,9 @@ template <int N> __device__ __forceinline__ void wait_vm() {
 constexpr int kTabBlk = 768;   // digit bytes per 256-value block: 8 sub-blocks x 3 planes x 32
 constexpr int kZero = 512;     // zero bytes read by lanes whose A row is empty
 constexpr int kMaxK = 16384;
+constexpr int kMaxDownSlots = 16;
+static_assert(sizeof(Seg) * (kMaxSegs - 1) >= kMaxDownSlots * (sizeof(void *) + sizeof(float)),
+              "down-mode slot table fits in the segment table");
 constexpr int kXPasses = 8;  // x sub-blocks staged per thread (4 threads per sub-block)
 // Waves that issue their first weight DMA only after building the digit
 // table: a wave stalls while the memory pipeline cannot accept its DMA, and
@@ -58,7 +61,7 @@ constexpr int kLateWaves = 4;
 
 __device__ __forceinline__ v4i ld_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
-template <typename XT, typename OT, int RGN, int KB, int NSLOT>
+template <typename XT, typename OT, int RGN, int KB, int NSLOT, bool DOWN>
 __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_t total, int nks, int nwc) {
     constexpr int BB = 144;
     constexpr int P = KB * BB;                   // row piece of one unit
@@ -69,6 +72,10 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     static_assert((NSLOT - 1) * CH < 64, "vmcnt is 6 bits");
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ Seg segl[kMaxSegs];
+    // down mode uses segl[0] only; the bank and the weight of each slot live
+    // in segl[1..] (the LDS budget is full: 8 waves take all but this table)
+    const uint8_t **bankl = reinterpret_cast<const uint8_t **>(&segl[1]);
+    float *wl = reinterpret_cast<float *>(bankl + kMaxDownSlots);
     const int nb = t.n_in / 256;
     uint8_t *tab = lds;                               // [nb][8][3][32] int8 digits
     uint8_t *zero = tab + nb * kTabBlk;               // kZero zero bytes
@@ -92,6 +99,7 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     const int64_t my_units = my_tiles * cnt;
 
     const int nseg = t.n;
+    const int upk = DOWN ? static_cast<int>(t.moe_kslot / (KB * 256)) : 1;   // units per slot
     auto seg_w = [&](int64_t g, const Seg *tab_) {
         int i = 0;
         while (i + 1 < nseg && g >= tab_[i + 1].blk_begin) i++;
@@ -119,11 +127,20 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         const int si = seg_w(g, tab_);
         const bool pair = tab_[si].kind == SEG_SILU;
         const int tr = pair ? 16 : ROWS;               // output rows per tile
-        const uint8_t *w = static_cast<const uint8_t *>(tab_[si].w);
+        const uint8_t *w;
+        int64_t k0;
+        if constexpr (DOWN) {
+            // the unit's slot and its offset inside that slot's bank row
+            const int sl = ks / upk;
+            w = bankl[sl];
+            k0 = static_cast<int64_t>(ks - sl * upk) * P;
+        } else {
+            w = static_cast<const uint8_t *>(tab_[si].w);
+            k0 = static_cast<int64_t>(ks) * P;
+        }
         const uint8_t *w1 = pair ? static_cast<const uint8_t *>(tab_[si].w2) : w + 16 * rb;
         const int64_t n_out = tab_[si].n_out;
         const int64_t n0 = (g - tab_[si].blk_begin) * tr;
-        const int64_t k0 = static_cast<int64_t>(ks) * P;
         uint8_t *dst = slots + static_cast<int>(j % NSLOT) * SLOT;
         if ((n0 + tr - 1) * rb + k0 + P <= n_out * rb) {
             const uint8_t *b0 = w + n0 * rb + k0, *b1 = w1 + n0 * rb + k0;
@@ -173,7 +190,17 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     // ---- routed experts: resolve the segments on the device first (one
     // dependent read of the ids and the table entries per workgroup)
     const bool moe = t.moe_tab != nullptr;
-    if (moe) {
+    if (DOWN) {
+        if (threadIdx.x < t.moe_k) {
+            const krk_moe_entry *mt = static_cast<const krk_moe_entry *>(t.moe_tab);
+            const int e = t.moe_ids[threadIdx.x];
+            const bool live = e >= 0 && e < t.moe_ne;
+            bankl[threadIdx.x] = static_cast<const uint8_t *>(mt[live ? e : 0].p[KRK_MOE_DOWN]);
+            wl[threadIdx.x] = live ? t.moe_wts[threadIdx.x] : 0.0f;
+        }
+        if (threadIdx.x == 0) segl[0] = t.seg[0];
+        __syncthreads();
+    } else if (moe) {
         if (threadIdx.x < nseg) {
             const int32_t *ids = t.moe_ids;
             const krk_moe_entry *mt = static_cast<const krk_moe_entry *>(t.moe_tab);
@@ -258,7 +285,11 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         *reinterpret_cast<u32x2 *>(o) = u32x2{p0[0], p0[1]};
         *reinterpret_cast<u32x2 *>(o + 32) = u32x2{p1[0], p1[1]};
         *reinterpret_cast<u32x2 *>(o + 64) = u32x2{p2[0], p2[1]};
-        if (q == 0) ex[sb] = float2{live ? dn : 1.0f, sum};
+        if (q == 0) {
+            // down mode: the slot weight scales the sub-block's activations
+            const float ws = DOWN ? wl[sb / static_cast<int>(t.moe_kslot / 32)] : 1.0f;
+            ex[sb] = float2{(live ? dn : 1.0f) * ws, sum * ws};
+        }
     }
     if (!moe && threadIdx.x < nseg) segl[threadIdx.x] = t.seg[threadIdx.x];
     if (!early) {
@@ -409,7 +440,7 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     }
 }
 
-template <typename XT, typename OT, int RGN, int KB, int NSLOT>
+template <typename XT, typename OT, int RGN, int KB, int NSLOT, bool DOWN>
 hipError_t launch(SegTable t, hipStream_t st) {
     constexpr int ROWS = 16 * RGN;
     constexpr int SLOT = ((ROWS * KB * 144 + 1023) / 1024) * 1024;
@@ -437,7 +468,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
             if (l + sizeof(Seg) * kMaxSegs > 160u * 1024u) break;
             int blocks = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &blocks, gemv_q4k_digits_kernel<XT, OT, RGN, KB, NSLOT>, 64 * cand, l) != hipSuccess)
+                    &blocks, gemv_q4k_digits_kernel<XT, OT, RGN, KB, NSLOT, DOWN>, 64 * cand, l) != hipSuccess)
                 blocks = 0;
             if (blocks > 0 && blocks * cand >= best) { best = blocks * cand; nw = cand; per_cu = blocks; }
         }
@@ -454,7 +485,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
     }
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
     if (grid > total) grid = total;
-    hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, RGN, KB, NSLOT>), dim3(static_cast<unsigned>(grid)),
+    hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, RGN, KB, NSLOT, DOWN>), dim3(static_cast<unsigned>(grid)),
                        dim3(64 * nw), fixed + nw * per_wave, st, t, total, nks, nw);
     return hipGetLastError();
 }
@@ -464,13 +495,23 @@ hipError_t launch(SegTable t, hipStream_t st) {
 // 16/32-row tiles x 1/2 blocks x 2/3 slots at 4096 and 14336)
 template <typename XT, typename OT>
 hipError_t dispatch(const SegTable &t, hipStream_t st) {
-    return t.n_in <= 8192 ? launch<XT, OT, 2, 2, 2>(t, st) : launch<XT, OT, 1, 2, 2>(t, st);
+    if constexpr (sizeof(XT) == 4) {
+        if (t.moe_tab && t.moe_down)
+            return t.n_in <= 8192 ? launch<XT, OT, 2, 2, 2, true>(t, st) : launch<XT, OT, 1, 2, 2, true>(t, st);
+    } else {
+        if (t.moe_tab && t.moe_down) return hipErrorNotSupported;   // down mode takes f32 activations
+    }
+    return t.n_in <= 8192 ? launch<XT, OT, 2, 2, 2, false>(t, st) : launch<XT, OT, 1, 2, 2, false>(t, st);
 }
 
 }  // namespace
 
 bool gemv_digits_ok(int dt, const SegTable &t) {
     if (dt != DT_Q4_K || t.rows != 1 || t.n_in % 256 || t.n_in > kMaxK || t.row_bytes % 16) return false;
+    if (t.moe_tab && t.moe_down &&
+        (t.n != 1 || t.moe_k < 1 || t.moe_k > kMaxDownSlots || t.moe_kslot % 512 ||
+         t.n_in != t.moe_k * t.moe_kslot || t.seg[0].kind != SEG_PLAIN))
+        return false;   // down mode: whole units (2 blocks) per slot
     for (int i = 0; i < t.n; i++) {
         if (t.seg[i].x != t.seg[0].x) return false;
         if (t.seg[i].kind == SEG_SILU && (t.n_in > 8192 || (reinterpret_cast<uintptr_t>(t.seg[i].w2) & 15)))

@@ -34,12 +34,21 @@ struct SegTable {
     int64_t x_stride;    // elements between activation rows
     int64_t out_stride;  // elements between output rows
     const int32_t *rexp; // SEG_ACC exponent (nullable)
-    // Routed experts (nullable): segment i's gate / up pointers are read on
-    // the device from moe_tab[moe_ids[i]] (krk_moe_entry) instead of seg[i].w /
-    // w2; seg[i].out is then seg[0].out + i * seg[0].n_out.
+    // Routed experts (moe_tab nullable).  Gate/up mode (moe_down == 0):
+    // segment i's gate / up pointers are read on the device from
+    // moe_tab[moe_ids[i]] (krk_moe_entry) instead of seg[i].w / w2, and
+    // seg[i].out is seg[0].out + i * seg[0].n_out.  Down mode (moe_down == 1):
+    // one segment whose K is moe_k slots of moe_kslot values; slot s's part of
+    // every row lies in the down bank of expert moe_ids[s] (row stride
+    // row_bytes) and its activations are scaled by moe_wts[s]; a dropped slot
+    // (id outside [0, moe_ne)) contributes zero.
     const void *moe_tab;
     const int32_t *moe_ids;
+    const float *moe_wts;
     int moe_ne;
+    int moe_down;
+    int moe_k;
+    int64_t moe_kslot;
 };
 
 hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st);

@@ -394,6 +394,29 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
             hipLaunchKernelGGL((moe_gu1_kernel<float, 8>), cap(a.k * ggu, wgu), dim3(64 * wgu), 0, st, tab,
                                a.ids, a.k, a.n_expert, static_cast<const float *>(a.xn), a.n_embd, a.n_ff,
                                ggu, w.mid);
+        // down projections as one GEMV over the concatenated slots, the
+        // routing weights folded into the activation scales
+        SegTable d{};
+        d.n = 1;
+        d.n_in = static_cast<int>(a.k * a.n_ff);
+        d.row_bytes = a.rb_down;
+        d.rows = 1;
+        d.x_stride = d.n_in;
+        d.out_stride = a.n_embd;
+        d.seg[0].x = w.mid;
+        d.seg[0].out = a.out;
+        d.seg[0].n_out = a.n_embd;
+        d.seg[0].kind = SEG_PLAIN;
+        d.moe_tab = tab;
+        d.moe_ids = a.ids;
+        d.moe_wts = a.wts;
+        d.moe_ne = a.n_expert;
+        d.moe_down = 1;
+        d.moe_k = a.k;
+        d.moe_kslot = a.n_ff;
+        if (!a.act_f16 && a.wt == DT_Q4_K && a.aligned16 && a.k * a.n_ff <= (1 << 30) &&
+            gemv_digits_ok(DT_Q4_K, d))
+            return gemv_digits(false, d, st);
         if (a.act_f16)
             hipLaunchKernelGGL((moe_down1_kernel<_Float16, 8>), cap(gdn, 8), dim3(64 * 8), 0, st, tab, a.ids,
                                a.wts, a.k, a.n_expert, a.n_embd, a.n_ff, gdn, w.mid,
