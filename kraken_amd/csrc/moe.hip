@@ -6,8 +6,8 @@
 // tokens take four launches, none of them per expert and none waiting on
 // the host:
 //   1. plan      one workgroup: expert-major plan of the (token, slot) pairs,
-//                stable (token-then-slot inside an expert), the active-expert
-//                list in ascending id, and each pair's plan position;
+//                the active-expert list in ascending id, and each pair's
+//                plan position;
 //   2. gate/up   ONE launch over all active experts: workgroup = (expert,
 //                group of ff rows); its pairs' activation rows are gathered
 //                through the plan and share every weight byte read;
@@ -56,13 +56,18 @@ size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t
 }
 
 // ------------------------------------------------------------------ plan ----
+// Pairs of one expert are computed independently of one another, so their
+// order inside the expert's range does not change any result; placement
+// takes a per-expert atomic cursor.  The expert offsets and the active list
+// come from a block-wide exclusive scan (4 experts per thread).
 constexpr int kPlanLds = 4096;  // (token, slot) pairs whose ids the plan keeps in LDS
 __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict__ ids, int64_t P,
                                                         int k, int ne, MoeWs w) {
     __shared__ int32_t cnt[1024];
-    __shared__ int32_t offs[1025];
+    __shared__ int32_t cur[1024];
     __shared__ int32_t sid[kPlanLds];   // the ids, when they fit
-    const int tid = threadIdx.x;
+    __shared__ int32_t wsum[2][4];      // per-wave totals: pairs, active experts
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const bool in_lds = P <= kPlanLds;
     for (int e = tid; e < ne; e += blockDim.x) cnt[e] = 0;
     if (in_lds)
@@ -74,32 +79,48 @@ __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict
         if (e >= 0 && e < ne) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    if (tid == 0) {
-        int run = 0, na = 0;
-        for (int e = 0; e < ne; e++) {
-            offs[e] = run;
-            if (cnt[e]) w.act[na++] = e;
-            run += cnt[e];
+    // exclusive scan over experts 4 tid .. 4 tid + 3 (ne <= 1024)
+    int c[4], run = 0, act = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = 4 * tid + j;
+        c[j] = e < ne ? cnt[e] : 0;
+        run += c[j];
+        act += c[j] > 0;
+    }
+    int ir = run, ia = act;   // inclusive wave scans
+    for (int d = 1; d < 64; d <<= 1) {
+        const int orr = __shfl_up(ir, d, 64), oa = __shfl_up(ia, d, 64);
+        if (lane >= d) { ir += orr; ia += oa; }
+    }
+    if (lane == 63) { wsum[0][wv] = ir; wsum[1][wv] = ia; }
+    __syncthreads();
+    int base = ir - run, abase = ia - act;
+    for (int v = 0; v < wv; v++) { base += wsum[0][v]; abase += wsum[1][v]; }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = 4 * tid + j;
+        if (e < ne) {
+            w.off[e] = base;
+            cur[e] = base;
+            if (c[j]) w.act[abase++] = e;
         }
-        offs[ne] = run;
-        w.n_act[0] = na;
+        base += c[j];
+    }
+    if (tid == blockDim.x - 1) {
+        w.off[ne] = base;   // the last thread's running total is the grand total
+        w.n_act[0] = abase;
     }
     __syncthreads();
-    for (int e = tid; e <= ne; e += blockDim.x) w.off[e] = offs[e];
-    // stable placement: expert e's pairs in ascending pair index (token, slot)
-    for (int e = tid; e < ne; e += blockDim.x) {
-        if (!cnt[e]) continue;
-        int c = offs[e];
-        for (int64_t i = 0; i < P; i++)
-            if (id_at(i) == e) {
-                w.plan_tok[c] = static_cast<int32_t>(i / k);
-                w.plan_pos[i] = c;
-                c++;
-            }
-    }
     for (int64_t i = tid; i < P; i += blockDim.x) {
         const int e = id_at(i);
-        if (e < 0 || e >= ne) w.plan_pos[i] = -1;
+        if (e < 0 || e >= ne) {
+            w.plan_pos[i] = -1;
+            continue;
+        }
+        const int pos = atomicAdd(&cur[e], 1);
+        w.plan_tok[pos] = static_cast<int32_t>(i / k);
+        w.plan_pos[i] = pos;
     }
 }
 

@@ -7,6 +7,10 @@
 #include "krk_dev.hpp"
 #include "krk_kernels.hpp"
 
+// wave-wide reductions of the device library (DPP/permlane based)
+extern "C" __device__ __attribute__((const)) float __ockl_wfred_max_f32(float);
+extern "C" __device__ __attribute__((const)) int __ockl_wfred_min_i32(int);
+
 namespace krk {
 
 constexpr int kMaxExpertsPerLane = 16;   // n_expert <= 1024 over 64 lanes
@@ -19,7 +23,7 @@ template <typename T>
 __global__ void __launch_bounds__(64) router_softmax_kernel(const T *__restrict__ logits,
                                                            float *__restrict__ probs,
                                                            int64_t n_rows, int ne) {
-    __shared__ float ex[kMaxExpertsPerLane * 64];
+    __shared__ __align__(16) float ex[kMaxExpertsPerLane * 64];
     __shared__ float inv_s;
     const int64_t r = blockIdx.x;
     const int lane = threadIdx.x;
@@ -29,21 +33,40 @@ __global__ void __launch_bounds__(64) router_softmax_kernel(const T *__restrict_
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < kMaxExpertsPerLane; i++) {
+        v[i] = -INFINITY;
+        if (64 * i >= ne) break;   // uniform
         const int e = lane + 64 * i;
         v[i] = e < ne ? static_cast<float>(l[e]) : -INFINITY;
         mx = fmaxf(mx, v[i]);
     }
-    // the host's running max keeps l[0] first; max is order-free except for NaN
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    // the host's running max keeps l[0] first; max is order-free except for
+    // NaN, which fmax (and the wave reduction) skip as the host's > does
+    mx = __ockl_wfred_max_f32(mx);
 #pragma unroll
     for (int i = 0; i < kMaxExpertsPerLane; i++) {
+        if (64 * i >= ne) break;
         const int e = lane + 64 * i;
         if (e < ne) ex[e] = expf(v[i] - mx);
     }
     __syncthreads();
     if (lane == 0) {
+        // ascending id; the reads are batched 16 at a time so only the adds
+        // form the serial chain
         float sum = 0.0f;
-        for (int e = 0; e < ne; e++) sum += ex[e];
+        int e = 0;
+        for (; e + 16 <= ne; e += 16) {
+            floatx4 q[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) q[j] = *reinterpret_cast<const floatx4 *>(&ex[e + 4 * j]);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sum += q[j].x;
+                sum += q[j].y;
+                sum += q[j].z;
+                sum += q[j].w;
+            }
+        }
+        for (; e < ne; e++) sum += ex[e];
         inv_s = sum > 0.0f ? 1.0f / sum : 0.0f;
     }
     __syncthreads();
@@ -81,6 +104,8 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float *__restrict
     float v[kMaxExpertsPerLane];
 #pragma unroll
     for (int i = 0; i < kMaxExpertsPerLane; i++) {
+        v[i] = -INFINITY;
+        if (64 * i >= ne) break;   // uniform
         const int e = lane + 64 * i;
         v[i] = e < ne ? p[e] : -INFINITY;
     }
@@ -91,21 +116,20 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float *__restrict
         int be = -1;
 #pragma unroll
         for (int i = 0; i < kMaxExpertsPerLane; i++) {
+            if (64 * i >= ne) break;
             const int e = lane + 64 * i;
             if (e < ne && !(taken & (1u << i)) && v[i] > bp) { bp = v[i]; be = e; }
         }
-        // wave argmax: larger p wins, equal p -> lower id (an invalid -1 loses)
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float op = __shfl_xor(bp, m, 64);
-            const int oe = __shfl_xor(be, m, 64);
-            const bool take = (oe >= 0) && (be < 0 || op > bp || (op == bp && oe < be));
-            bp = take ? op : bp;
-            be = take ? oe : be;
-        }
+        // wave argmax: the largest p, and among lanes holding it the lowest id
+        // (a lane without a candidate keeps -1 and id -1, which never win)
+        const float gp = __ockl_wfred_max_f32(bp);
+        be = __ockl_wfred_min_i32(be >= 0 && bp == gp ? be : 0x7fffffff);
+        if (be == 0x7fffffff) be = -1;
+        bp = gp;
         if (be >= 0 && (be & 63) == lane) taken |= 1u << (be >> 6);
         if (lane == 0) {
             isel[s] = be;
-            wsel[s] = be >= 0 ? p[be] : 0.0f;
+            wsel[s] = be >= 0 ? bp : 0.0f;   // bp is p[be] itself
         }
     }
     __syncthreads();
