@@ -12,8 +12,9 @@
 //     into LDS, and stages the activation tile (f16, or f32 rounded to f16)
 //     beside it; rows padded to 80 B so the b128 fragment reads are
 //     bank-conflict free;
-//   * the next step's raw weight bytes and activations are fetched into
-//     registers while the current step's MFMAs run;
+//   * the two wave groups run out of phase (ping-pong): one group's MFMAs
+//     overlap the other group's decode and LDS stores, and each thread
+//     fetches the raw bytes of its next step while the other group computes;
 //   * tiles are ordered XCD-first: workgroup g runs on XCD g % 8, so the
 //     launch order is remapped to give each XCD a contiguous run of tiles
 //     sharing one activation row-band in its own L2;
@@ -69,6 +70,49 @@ template <> struct WStage<DT_Q4_K> {
                 const float qv = static_cast<float>((q[t] >> (8 * k + sh)) & 0xFu);
                 o[4 * t + k] = static_cast<_Float16>(__builtin_fmaf(d1, qv, -m1));
             }
+    }
+};
+
+// Q4_K by chunk pair: step p (64 values) is sub-blocks 2(p%4), 2(p%4)+1 of
+// block p/4, which share the 32 code bytes (low nibbles: the even chunk,
+// high nibbles: the odd one).  The thread with slice h takes code bytes
+// [16h, 16h+16): values 16h .. 16h+15 of both chunks.  All lanes extract
+// the same nibbles, so one mask serves four values.
+struct Q4KPair {
+    uint32_t hdr[4], q[4];
+    __device__ void fetch(const uint8_t *row, int p, int h) {
+        const uint8_t *b = row + (p >> 2) * 144;
+        const u32x4 hv = ld128(b);
+        hdr[0] = hv.x; hdr[1] = hv.y; hdr[2] = hv.z; hdr[3] = hv.w;
+        const u32x4 v = ld128(b + 16 + 32 * (p & 3) + 16 * h);
+        q[0] = v.x; q[1] = v.y; q[2] = v.z; q[3] = v.w;
+    }
+    // lo / hi: the slice of the even / odd chunk, f16 of the host decoder's f32
+    __device__ void decode(int p, _Float16 (&lo)[16], _Float16 (&hi)[16]) const {
+        const float d = h2f(hdr[0] & 0xFFFF), dmin = h2f(hdr[0] >> 16);
+        // sub-blocks 2jp, 2jp+1 (get_scale_min_k4, quant.cpp:427-435), no branches
+        const int jp = p & 3;
+        const uint32_t sh = 16u * static_cast<uint32_t>(jp & 1);
+        const uint32_t Y = hdr[1] >> sh, Z = hdr[2] >> sh, W = hdr[3] >> sh;
+        const bool up = jp >= 2;
+        const uint32_t A = up ? W : Y, Am = up ? (W >> 4) : Z, s2 = up ? 2u : 0u;
+        const uint32_t sa = (A & 15u) | ((Y >> s2) & 0x30u);
+        const uint32_t sb = ((A >> 8) & 15u) | ((Y >> (8u + s2)) & 0x30u);
+        const uint32_t ma = (Am & 15u) | ((Z >> s2) & 0x30u);
+        const uint32_t mb = ((Am >> 8) & 15u) | ((Z >> (8u + s2)) & 0x30u);
+        const float d1a = d * static_cast<float>(sa), m1a = dmin * static_cast<float>(ma);
+        const float d1b = d * static_cast<float>(sb), m1b = dmin * static_cast<float>(mb);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t l = q[t] & 0x0F0F0F0Fu, u = (q[t] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                lo[4 * t + k] = static_cast<_Float16>(
+                    __builtin_fmaf(d1a, static_cast<float>((l >> (8 * k)) & 0xFFu), -m1a));
+                hi[4 * t + k] = static_cast<_Float16>(
+                    __builtin_fmaf(d1b, static_cast<float>((u >> (8 * k)) & 0xFFu), -m1b));
+            }
+        }
     }
 };
 
@@ -195,6 +239,10 @@ template <int DT, typename XT> struct StepRegs {
     WStage<DT> w0, w1;
     XStage<XT> x0, x1;
 };
+template <typename XT> struct StepRegs<DT_Q4_K, XT> {
+    Q4KPair w;
+    XStage<XT> x0, x1;
+};
 
 template <int DT, typename XT, typename OT>
 __global__ void __launch_bounds__(G_THREADS, 1)
@@ -215,11 +263,16 @@ __global__ void __launch_bounds__(G_THREADS, 1)
     const int cend = ke / 32;                      // first chunk past this split
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves, 128 x 64 each
+    const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves, 128 x 64 each (wm = group)
 
-    // staging roles: row = tid / 2, values [64 kt + 32 shf, +32) of the row
-    // (one 32-value GGUF chunk)
-    const int srow = tid >> 1, shf = tid & 1;
+    // Two wave groups (waves 0-3 and 4-7; each SIMD holds one wave of each)
+    // run out of phase: while one group's MFMAs consume a stage, the other
+    // decodes and stores its half of the next stage.  Group gp computes
+    // output rows 128 gp .. +127 and stages activation rows and weight rows
+    // 128 gp .. +127: thread role row = 128 gp + (tid % 256) / 2, values
+    // [64 kt + 32 shf, +32) of the row (one 32-value GGUF chunk).
+    const int gp = wave >> 2;
+    const int srow = gp * 128 + ((tid & 255) >> 1), shf = tid & 1;
     const int wr = min(n0 + srow, N - 1);
     const uint8_t *wrow = w + static_cast<int64_t>(wr) * row_bytes;
     const bool xok = m0 + srow < M;
@@ -230,8 +283,13 @@ __global__ void __launch_bounds__(G_THREADS, 1)
         const int c = c0 + 2 * it;
         const bool ok = c < cend;
         const int cc = ok ? c : cend - 1;          // stay inside the row
-        r.w0.fetch(wrow, cc, 0);
-        r.w1.fetch(wrow, cc, 1);
+        if constexpr (DT == DT_Q4_K) {
+            const int pp = c >> 1;                  // chunk pair of this step
+            r.w.fetch(wrow, 2 * pp < cend ? pp : (cend - 1) >> 1, shf);
+        } else {
+            r.w0.fetch(wrow, cc, 0);
+            r.w1.fetch(wrow, cc, 1);
+        }
         const XT *xp = xrow + kb + (ok ? it * GB_K : 0);
         r.x0.fetch(xp, xok && ok);
         r.x1.fetch(xp + 16, xok && ok);
@@ -239,13 +297,28 @@ __global__ void __launch_bounds__(G_THREADS, 1)
     auto stage = [&](const StepRegs<DT, XT> &r, int it, int s) {
         const int c = c0 + 2 * it;
         _Float16 a[16], b[16];
-        r.w0.decode(c, a);
-        r.w1.decode(c, b);
-        if (c >= cend) {   // the half step past K: zero weights (the activations are zero too)
+        // a, b: the two 16-value runs this thread stores, at wo and wo + 16
+        // (Q4_K: slice shf of the even chunk at 16 shf, of the odd at 32 + 16 shf)
+        int wo = shf * 32, bo = shf * 32 + 16;
+        if constexpr (DT == DT_Q4_K) {
+            const int pp = c >> 1;
+            r.w.decode(pp, a, b);
+            if (2 * pp + 1 >= cend) {   // the half step past K: zero the odd chunk
 #pragma unroll
-            for (int i = 0; i < 16; i++) { a[i] = static_cast<_Float16>(0.0f); b[i] = a[i]; }
+                for (int i = 0; i < 16; i++) b[i] = static_cast<_Float16>(0.0f);
+            }
+            wo = 16 * shf;
+            bo = 32 + 16 * shf;
+        } else {
+            r.w0.decode(c, a);
+            r.w1.decode(c, b);
+            if (c >= cend) {   // the half step past K: zero weights (the activations are zero too)
+#pragma unroll
+                for (int i = 0; i < 16; i++) { a[i] = static_cast<_Float16>(0.0f); b[i] = a[i]; }
+            }
         }
-        _Float16 *wd = &Ws[s][srow * LDS_ROW + shf * 32];
+        _Float16 *wd = &Ws[s][srow * LDS_ROW + wo];
+        _Float16 *wb = &Ws[s][srow * LDS_ROW + bo];
         half8 h;
 #pragma unroll
         for (int i = 0; i < 8; i++) h[i] = a[i];
@@ -255,10 +328,10 @@ __global__ void __launch_bounds__(G_THREADS, 1)
         *reinterpret_cast<half8 *>(wd + 8) = h;
 #pragma unroll
         for (int i = 0; i < 8; i++) h[i] = b[i];
-        *reinterpret_cast<half8 *>(wd + 16) = h;
+        *reinterpret_cast<half8 *>(wb) = h;
 #pragma unroll
         for (int i = 0; i < 8; i++) h[i] = b[8 + i];
-        *reinterpret_cast<half8 *>(wd + 24) = h;
+        *reinterpret_cast<half8 *>(wb + 8) = h;
         r.x0.store(&Xs[s][srow * LDS_ROW + shf * 32]);
         r.x1.store(&Xs[s][srow * LDS_ROW + shf * 32 + 16]);
     };
@@ -290,30 +363,39 @@ __global__ void __launch_bounds__(G_THREADS, 1)
         }
     };
 
-    // Pipeline: the raw bytes of step it + 2 are in flight while step it + 1
-    // is decoded into the free LDS stage and step it's MFMAs run; one
-    // barrier per step.  Two register sets alternate (the loop is unrolled
-    // by two so they stay in registers).
-    StepRegs<DT, XT> ra, rb;
-    if (nk > 0) fetch(ra, 0);
-    if (nk > 1) fetch(rb, 1);
-    if (nk > 0) stage(ra, 0, 0);
-    if (nk > 2) fetch(ra, 2);
+    // Pipeline (phases separated by workgroup barriers):
+    //   group 0:  C0 | M1 | C1 | M2 | C2 | ...
+    //   group 1:  M1 | C0 | M2 | C1 | M3 | ...
+    // Ct = MFMAs over stage t % 2, Mt = decode and store this group's half
+    // of step t into stage t % 2, then fetch step t + 1's raw bytes.  A stage
+    // is complete one phase before either group reads it, and rewritten only
+    // after both groups have read it.  Both groups pass 2 nk barriers.
+    StepRegs<DT, XT> r;
+    if (nk > 0) {
+        fetch(r, 0);
+        stage(r, 0, 0);
+        if (nk > 1) fetch(r, 1);
+    }
     __syncthreads();
-    int it = 0;
-    for (; it + 1 < nk; it += 2) {
-        // even step: MFMA stage 0, decode rb (step it + 1) -> stage 1, refill rb
-        mfma_step(0);
-        stage(rb, it + 1, 1);
-        if (it + 3 < nk) fetch(rb, it + 3);
-        __syncthreads();
-        // odd step: MFMA stage 1, decode ra (step it + 2) -> stage 0, refill ra
-        mfma_step(1);
-        if (it + 2 < nk) stage(ra, it + 2, 0);
-        if (it + 4 < nk) fetch(ra, it + 4);
+    if (gp == 1) {
+        if (1 < nk) {
+            stage(r, 1, 1);
+            if (2 < nk) fetch(r, 2);
+        }
         __syncthreads();
     }
-    if (it < nk) mfma_step(0);   // odd step count: the last step sits in stage 0
+    for (int t = 0; t < nk; t++) {
+        __builtin_amdgcn_s_setprio(1);
+        mfma_step(t & 1);
+        __builtin_amdgcn_s_setprio(0);
+        __syncthreads();
+        const int ms = t + 1 + gp;
+        if (ms < nk) {
+            stage(r, ms, ms & 1);
+            if (ms + 1 < nk) fetch(r, ms + 1);
+        }
+        if (t + 1 < nk || gp == 0) __syncthreads();
+    }
 
     // C fragment: lane holds column j = lane % 32, rows 8*(r/4) + 4*(lane/32) + r%4
 #pragma unroll
