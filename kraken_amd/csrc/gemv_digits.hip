@@ -23,11 +23,13 @@
 // only by the 2^-22 activation rounding and f32 accumulation order, far
 // inside the 1e-5 relative budget.
 //
-// Data movement: each wave streams units of 16*RGN rows x 256*KB values
-// (RGN*16 row pieces of KB*144 contiguous bytes) into a private LDS slot
+// Data movement: each wave streams units of ROWS rows x 256*KB values
+// (ROWS row pieces of KB*144 contiguous bytes) into a private LDS slot
 // with global_load_lds_dwordx4 -- every weight byte is delivered once and
 // coalesced -- while the digit table of x is built once per workgroup.
 // NSLOT slots keep NSLOT-1 units in flight during the decode.
+#include <cstdint>
+
 #include "gemv_core.hpp"
 #include "krk_formats.hpp"
 #include "krk_kernels.hpp"
@@ -53,7 +55,8 @@ constexpr int kMaxK = 16384;
 constexpr int kMaxDownSlots = 16;
 static_assert(sizeof(Seg) * (kMaxSegs - 1) >= kMaxDownSlots * (sizeof(void *) + sizeof(float)),
               "down-mode slot table fits in the segment table");
-constexpr int kXPasses = 8;  // x sub-blocks staged per thread (4 threads per sub-block)
+constexpr int kXPasses = 8;
+constexpr int kRedWaves = 8;   // reduction slots per row (waves per workgroup <= 8)  // x sub-blocks staged per thread (4 threads per sub-block)
 // Waves that issue their first weight DMA only after building the digit
 // table: a wave stalls while the memory pipeline cannot accept its DMA, and
 // these keep the table build moving meanwhile (measured: 4 of 8 best).
@@ -61,11 +64,12 @@ constexpr int kLateWaves = 4;
 
 __device__ __forceinline__ v4i ld_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
-template <typename XT, typename OT, int RGN, int KB, int NSLOT, bool DOWN>
+template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN>
 __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_t total, int nks, int nwc) {
     constexpr int BB = 144;
     constexpr int P = KB * BB;                   // row piece of one unit
-    constexpr int ROWS = 16 * RGN;
+    constexpr int RGN = (ROWS + 15) / 16;        // 16-row MFMA groups (the last may be partial)
+    constexpr int RS = 16 * RGN;                 // reduction stride
     constexpr int U = ROWS * P;
     constexpr int CH = (U + 1023) / 1024;
     constexpr int SLOT = CH * 1024;
@@ -81,7 +85,7 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     uint8_t *zero = tab + nb * kTabBlk;               // kZero zero bytes
     float2 *ex = reinterpret_cast<float2 *>(zero + kZero);  // [nb * 8] {2^-e, sum x}
     uint8_t *slots0 = reinterpret_cast<uint8_t *>(ex + nb * 8);
-    float *red = reinterpret_cast<float *>(slots0 + nwc * (NSLOT * SLOT));  // [2][nwc][ROWS]
+    float *red = reinterpret_cast<float *>(slots0 + nwc * (NSLOT * SLOT));  // [2][RS][kRedWaves]
 
     // Every wave streams, multiplies and builds a share of the digit table.
     // The vector-memory counter of a wave is in order, so each wave issues
@@ -340,7 +344,9 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
             for (int b = 0; b < KB; b++)
 #pragma unroll
                 for (int rg = 0; rg < RGN; rg++) {
-                    const uint8_t *rp = slot + (rg * 16 + c16) * P + b * BB;
+                    // rows past ROWS (a partial last group) read row ROWS - 1; discarded
+                    const int rr = rg * 16 + c16 < ROWS ? rg * 16 + c16 : ROWS - 1;
+                    const uint8_t *rp = slot + rr * P + b * BB;
                     hdr[b][rg] = *reinterpret_cast<const u32x4 *>(rp);
                     qa[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 16 + 16 * gq);
                     qb[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 80 + 16 * gq);
@@ -391,17 +397,28 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
                 }
             }
         }
-        // partial sums of the compute waves -> LDS, then one thread per row
-        // adds them in wave order and stores the row
-        float *rbuf = red + (ti & 1) * nwc * ROWS;
+        // partial sums of the compute waves -> LDS as [row][wave], then one
+        // thread per row reads its eight partials at once (two b128 reads)
+        // and adds them in wave order
+        float *rbuf = red + (ti & 1) * RS * kRedWaves;
 #pragma unroll
         for (int rg = 0; rg < RGN; rg++) {
             float v = acc[rg];
             v += __shfl_xor(v, 16, 64);
             v += __shfl_xor(v, 32, 64);
-            if (gq == 0) rbuf[wv * ROWS + rg * 16 + c16] = v;
+            if (gq == 0) rbuf[(rg * 16 + c16) * kRedWaves + wv] = v;
         }
         __syncthreads();
+        auto row_sum = [&](int r) {
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(rbuf + r * kRedWaves);
+            const floatx4 b = *reinterpret_cast<const floatx4 *>(rbuf + r * kRedWaves + 4);
+            const float p[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            float v = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kRedWaves; k++)
+                if (k < nwc) v += p[k];
+            return v;
+        };
         if (threadIdx.x < ROWS) {
             const int64_t g = blockIdx.x + ti * gridDim.x;
             const int si = seg_w(g, segl);
@@ -409,11 +426,7 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
             if (kind == SEG_SILU) {
                 // rows t and 16 + t of the tile are gate and up of output n0 + t
                 if (threadIdx.x < 16) {
-                    float gs = 0.0f, us = 0.0f;
-                    for (int k = 0; k < nwc; k++) {
-                        gs += rbuf[k * ROWS + threadIdx.x];
-                        us += rbuf[k * ROWS + 16 + threadIdx.x];
-                    }
+                    const float gs = row_sum(threadIdx.x), us = row_sum(16 + threadIdx.x);
                     const int64_t n = (g - segl[si].blk_begin) * 16 + threadIdx.x;
                     if (n < segl[si].n_out) {
                         OT *o = static_cast<OT *>(segl[si].out) + n;
@@ -429,8 +442,7 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
                     }
                 }
             } else {
-                float v = 0.0f;
-                for (int k = 0; k < nwc; k++) v += rbuf[k * ROWS + threadIdx.x];
+                const float v = row_sum(threadIdx.x);
                 const int64_t n = (g - segl[si].blk_begin) * ROWS + threadIdx.x;
                 if (n < segl[si].n_out)
                     store_out<OT>(static_cast<OT *>(segl[si].out) + n, v, kind,
@@ -440,9 +452,9 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     }
 }
 
-template <typename XT, typename OT, int RGN, int KB, int NSLOT, bool DOWN>
+template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN>
 hipError_t launch(SegTable t, hipStream_t st) {
-    constexpr int ROWS = 16 * RGN;
+    constexpr int RS = 16 * ((ROWS + 15) / 16);
     constexpr int SLOT = ((ROWS * KB * 144 + 1023) / 1024) * 1024;
     int64_t total = 0;
     for (int i = 0; i < t.n; i++) {
@@ -452,8 +464,9 @@ hipError_t launch(SegTable t, hipStream_t st) {
     }
     const int nb = t.n_in / 256;
     const int nks = (nb + KB - 1) / KB;
-    const size_t fixed = static_cast<size_t>(nb) * kTabBlk + kZero + static_cast<size_t>(nb) * 8 * sizeof(float2);
-    const size_t per_wave = static_cast<size_t>(NSLOT) * SLOT + 2 * ROWS * sizeof(float);
+    const size_t fixed = static_cast<size_t>(nb) * kTabBlk + kZero + static_cast<size_t>(nb) * 8 * sizeof(float2) +
+                         2 * RS * kRedWaves * sizeof(float);
+    const size_t per_wave = static_cast<size_t>(NSLOT) * SLOT;
     // kXPasses sub-blocks per thread (4 threads each) must cover nb * 8
     const int min_nw = (nb * 8 * 4 + 64 * kXPasses - 1) / (64 * kXPasses);
     struct Pick { int nb, nw, per_cu; };
@@ -468,7 +481,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
             if (l + sizeof(Seg) * kMaxSegs > 160u * 1024u) break;
             int blocks = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &blocks, gemv_q4k_digits_kernel<XT, OT, RGN, KB, NSLOT, DOWN>, 64 * cand, l) != hipSuccess)
+                    &blocks, gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN>, 64 * cand, l) != hipSuccess)
                 blocks = 0;
             if (blocks > 0 && blocks * cand >= best) { best = blocks * cand; nw = cand; per_cu = blocks; }
         }
@@ -485,23 +498,59 @@ hipError_t launch(SegTable t, hipStream_t st) {
     }
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
     if (grid > total) grid = total;
-    hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, RGN, KB, NSLOT, DOWN>), dim3(static_cast<unsigned>(grid)),
+    hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN>), dim3(static_cast<unsigned>(grid)),
                        dim3(64 * nw), fixed + nw * per_wave, st, t, total, nks, nw);
     return hipGetLastError();
 }
 
-// K <= 8192: 32-row tiles of two blocks per unit; longer rows: 16-row
-// tiles, so the K-split has more tiles to spread over (both measured best of
-// 16/32-row tiles x 1/2 blocks x 2/3 slots at 4096 and 14336)
+template <typename XT, typename OT, bool DOWN>
+hipError_t launch_rows(int rows, const SegTable &t, hipStream_t st) {
+    switch (rows) {
+        case 32: return launch<XT, OT, 32, 2, 2, DOWN>(t, st);
+        case 28: return launch<XT, OT, 28, 2, 2, DOWN>(t, st);
+        case 24: return launch<XT, OT, 24, 2, 2, DOWN>(t, st);
+        case 20: return launch<XT, OT, 20, 2, 2, DOWN>(t, st);
+        default: return launch<XT, OT, 16, 2, 2, DOWN>(t, st);
+    }
+}
+
+// Tile height: gate/up pairs take 32 rows (16 + 16); rows longer than 8192
+// values take 16 (the digit table leaves LDS for 16-row slots only).
+// Otherwise the height among 16..32 that minimises rounds x height, the
+// time of the workgroup with the most tiles when one workgroup runs per CU
+// (e.g. 14336 rows: 28-row tiles, 512 = 2 per CU, instead of 448 32-row
+// tiles of which 192 CUs run two and 64 run one).
+int pick_rows(const SegTable &t) {
+    for (int i = 0; i < t.n; i++)
+        if (t.seg[i].kind == SEG_SILU) return 32;
+    if (t.n_in > 8192) return 16;
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    int best = 32;
+    int64_t best_cost = INT64_MAX;
+    for (int r = 32; r >= 16; r -= 4) {
+        int64_t tiles = 0;
+        for (int i = 0; i < t.n; i++) tiles += (t.seg[i].n_out + r - 1) / r;
+        const int64_t cost = (tiles + cus - 1) / cus * r;
+        if (cost < best_cost) { best_cost = cost; best = r; }
+    }
+    return best;
+}
+
 template <typename XT, typename OT>
 hipError_t dispatch(const SegTable &t, hipStream_t st) {
+    const int rows = pick_rows(t);
     if constexpr (sizeof(XT) == 4) {
-        if (t.moe_tab && t.moe_down)
-            return t.n_in <= 8192 ? launch<XT, OT, 2, 2, 2, true>(t, st) : launch<XT, OT, 1, 2, 2, true>(t, st);
+        if (t.moe_tab && t.moe_down) return launch_rows<XT, OT, true>(rows, t, st);
     } else {
         if (t.moe_tab && t.moe_down) return hipErrorNotSupported;   // down mode takes f32 activations
     }
-    return t.n_in <= 8192 ? launch<XT, OT, 2, 2, 2, false>(t, st) : launch<XT, OT, 1, 2, 2, false>(t, st);
+    return launch_rows<XT, OT, false>(rows, t, st);
 }
 
 }  // namespace
