@@ -64,7 +64,7 @@ constexpr int kLateWaves = 4;
 
 __device__ __forceinline__ v4i ld_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
-template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN>
+template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX>
 __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_t total, int nks, int nwc) {
     constexpr int BB = 144;
     constexpr int P = KB * BB;                   // row piece of one unit
@@ -81,11 +81,13 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     const uint8_t **bankl = reinterpret_cast<const uint8_t **>(&segl[1]);
     float *wl = reinterpret_cast<float *>(bankl + kMaxDownSlots);
     const int nb = t.n_in / 256;
-    uint8_t *tab = lds;                               // [nb][8][3][32] int8 digits
-    uint8_t *zero = tab + nb * kTabBlk;               // kZero zero bytes
-    float2 *ex = reinterpret_cast<float2 *>(zero + kZero);  // [nb * 8] {2^-e, sum x}
-    uint8_t *slots0 = reinterpret_cast<uint8_t *>(ex + nb * 8);
-    float *red = reinterpret_cast<float *>(slots0 + nwc * (NSLOT * SLOT));  // [2][RS][kRedWaves]
+    // NX activation rows share every weight unit: one digit table per row
+    const int tstride = nb * kTabBlk;                 // bytes of one row's table
+    uint8_t *tab = lds;                               // [NX][nb][8][3][32] int8 digits
+    uint8_t *zero = tab + NX * tstride;               // kZero zero bytes
+    float2 *ex = reinterpret_cast<float2 *>(zero + kZero);  // [NX][nb * 8] {2^-e, sum x}
+    uint8_t *slots0 = reinterpret_cast<uint8_t *>(ex + NX * nb * 8);
+    float *red = reinterpret_cast<float *>(slots0 + nwc * (NSLOT * SLOT));  // [2][NX][RS][kRedWaves]
 
     // Every wave streams, multiplies and builds a share of the digit table.
     // The vector-memory counter of a wave is in order, so each wave issues
@@ -170,17 +172,24 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         }
     };
 
-    // ---- x loads (four threads per 32-value sub-block, kXPasses passes)
+    // ---- x loads (four threads per 32-value sub-block, kXPasses passes over
+    // the NX rows' sub-blocks; rows past t.rows read as zero)
     const XT *x = static_cast<const XT *>(t.seg[0].x);
     const int q = threadIdx.x & 3;
     const int nsb = nb * 8;
+    const int nxs = NX * nsb;
     float xv[kXPasses][8];
 #pragma unroll
     for (int u = 0; u < kXPasses; u++) {
-        const int sb = (threadIdx.x >> 2) + u * (blockDim.x >> 2);
-        const XT *xp = x + (sb < nsb ? sb : 0) * 32 + 8 * q;
-        if (u * (blockDim.x >> 2) >= nsb) break;   // uniform
-        if constexpr (sizeof(XT) == 4) {
+        const int f = (threadIdx.x >> 2) + u * (blockDim.x >> 2);
+        const int xr = NX > 1 ? f / nsb : 0, sb = NX > 1 ? f - xr * nsb : f;
+        const bool xin = f < nxs && xr < t.rows;
+        const XT *xp = x + (xin ? static_cast<int64_t>(xr) * t.x_stride + sb * 32 : 0) + 8 * q;
+        if (u * (blockDim.x >> 2) >= nxs) break;   // uniform
+        if (NX > 1 && !xin) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) xv[u][k] = 0.0f;
+        } else if constexpr (sizeof(XT) == 4) {
             const floatx4 u0 = *reinterpret_cast<const floatx4 *>(xp);
             const floatx4 u1 = *reinterpret_cast<const floatx4 *>(xp + 4);
             xv[u][0] = u0.x; xv[u][1] = u0.y; xv[u][2] = u0.z; xv[u][3] = u0.w;
@@ -247,8 +256,9 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     for (int i = threadIdx.x; i < kZero / 4; i += blockDim.x) reinterpret_cast<uint32_t *>(zero)[i] = 0u;
 #pragma unroll
     for (int u = 0; u < kXPasses; u++) {
-        const int sb = (threadIdx.x >> 2) + u * (blockDim.x >> 2);
-        if (u * (blockDim.x >> 2) >= nsb) break;   // uniform
+        const int f = (threadIdx.x >> 2) + u * (blockDim.x >> 2);
+        const int xr = NX > 1 ? f / nsb : 0, sb = NX > 1 ? f - xr * nsb : f;
+        if (u * (blockDim.x >> 2) >= nxs) break;   // uniform
         const float *v = xv[u];
         float amax = 0.0f, sum = 0.0f;
 #pragma unroll
@@ -260,7 +270,7 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
         sum += __shfl_xor(sum, 1, 64);
         sum += __shfl_xor(sum, 2, 64);
-        if (sb >= nsb) continue;
+        if (f >= nxs) continue;
         // 2^e with |x| * 2^e < 2^22: from amax's exponent field E (amax in
         // [2^(E-127), 2^(E-126))), e = 148 - E puts amax * 2^e in
         // [2^21, 2^22), so the top digit stays within [-64, 64]; kept where
@@ -285,14 +295,14 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
             p1[k >> 2] |= (static_cast<uint32_t>(d1) & 255u) << sh;
             p2[k >> 2] |= (static_cast<uint32_t>(d2) & 255u) << sh;
         }
-        uint8_t *o = tab + (sb >> 3) * kTabBlk + (sb & 7) * 96 + 8 * q;
+        uint8_t *o = tab + xr * tstride + (sb >> 3) * kTabBlk + (sb & 7) * 96 + 8 * q;
         *reinterpret_cast<u32x2 *>(o) = u32x2{p0[0], p0[1]};
         *reinterpret_cast<u32x2 *>(o + 32) = u32x2{p1[0], p1[1]};
         *reinterpret_cast<u32x2 *>(o + 64) = u32x2{p2[0], p2[1]};
         if (q == 0) {
             // down mode: the slot weight scales the sub-block's activations
             const float ws = DOWN ? wl[sb / static_cast<int>(t.moe_kslot / 32)] : 1.0f;
-            ex[sb] = float2{(live ? dn : 1.0f) * ws, sum * ws};
+            ex[xr * nsb + sb] = float2{(live ? dn : 1.0f) * ws, sum * ws};
         }
     }
     if (!moe && threadIdx.x < nseg) segl[threadIdx.x] = t.seg[threadIdx.x];
@@ -327,9 +337,11 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
 
     int64_t j = 0;
     for (int64_t ti = 0; ti < my_tiles; ti++) {
-        float acc[RGN];
+        float acc[NX][RGN];
 #pragma unroll
-        for (int r = 0; r < RGN; r++) acc[r] = 0.0f;
+        for (int xr = 0; xr < NX; xr++)
+#pragma unroll
+            for (int r = 0; r < RGN; r++) acc[xr][r] = 0.0f;
         for (int kk = 0; kk < cnt; kk++, j++) {
             // units j + 1 .. j + NSLOT - 1 may still be in flight
             const int64_t ahead = my_units - 1 - j;
@@ -357,12 +369,6 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
             for (int b = 0; b < KB; b++) {
                 const int blk = ks * KB + b;
                 if (KB > 1 && blk >= nb) break;
-                const uint8_t *alp = a_lo_p + blk * a_lo_inc;
-                const uint8_t *ahp = a_hi_p + blk * a_hi_inc;
-                const v4i A0l = ld_v4i(alp), A1l = ld_v4i(alp + 384);
-                const v4i A0h = ld_v4i(ahp), A1h = ld_v4i(ahp + 384);
-                // this lane's sub-blocks gq (h = 0) and 4 + gq (h = 1) of block blk
-                const float2 ex0 = ex[blk * 8 + gq], ex1 = ex[blk * 8 + 4 + gq];
 #pragma unroll
                 for (int rg = 0; rg < RGN; rg++) {
                     const u32x4 hd = hdr[b][rg], q0 = qa[b][rg], q1 = qb[b][rg];
@@ -374,11 +380,6 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
                                      static_cast<int>(q1.z & M), static_cast<int>(q1.w & M)};
                     const v4i B1h = {static_cast<int>((q1.x >> 4) & M), static_cast<int>((q1.y >> 4) & M),
                                      static_cast<int>((q1.z >> 4) & M), static_cast<int>((q1.w >> 4) & M)};
-                    const v4i z = {0, 0, 0, 0};
-                    v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0l, B0l, z, 0, 0, 0);
-                    C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0h, B0h, C0, 0, 0, 0);
-                    v4i C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1l, B1l, z, 0, 0, 0);
-                    C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1h, B1h, C1, 0, 0, 0);
                     // scales of sub-blocks gq and 4 + gq (get_scale_min_k4,
                     // src/quant.cpp:427-435): bytes gq of scales[0..3], [4..7], [8..11]
                     const uint32_t s1 = hd.y >> bsh, s2 = hd.z >> bsh, s3 = hd.w >> bsh;
@@ -386,28 +387,46 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
                     const float sc0 = static_cast<float>(s1 & 63u), m0 = static_cast<float>(s2 & 63u);
                     const float sc1 = static_cast<float>((s3 & 15u) | ((s1 >> 2) & 0x30u));
                     const float m1 = static_cast<float>(((s3 >> 4) & 15u) | ((s2 >> 2) & 0x30u));
-                    const int S0 = C0[0] + (C0[1] << 8) + (C0[2] << 16);
-                    const int S1 = C1[0] + (C1[1] << 8) + (C1[2] << 16);
-                    float a = acc[rg];
-                    a = __builtin_fmaf(d * sc0, ex0.x * static_cast<float>(S0), a);
-                    a = __builtin_fmaf(-dmin * m0, ex0.y, a);
-                    a = __builtin_fmaf(d * sc1, ex1.x * static_cast<float>(S1), a);
-                    a = __builtin_fmaf(-dmin * m1, ex1.y, a);
-                    acc[rg] = a;
+                    const float ds0 = d * sc0, ds1 = d * sc1, dm0 = -dmin * m0, dm1 = -dmin * m1;
+                    const v4i z = {0, 0, 0, 0};
+#pragma unroll
+                    for (int xr = 0; xr < NX; xr++) {
+                        // this activation row's digit table
+                        const uint8_t *alp = a_lo_p + (a_lo ? xr * tstride : 0) + blk * a_lo_inc;
+                        const uint8_t *ahp = a_hi_p + (a_hi ? xr * tstride : 0) + blk * a_hi_inc;
+                        const v4i A0l = ld_v4i(alp), A1l = ld_v4i(alp + 384);
+                        const v4i A0h = ld_v4i(ahp), A1h = ld_v4i(ahp + 384);
+                        // this lane's sub-blocks gq (h = 0) and 4 + gq (h = 1) of block blk
+                        const float2 ex0 = ex[xr * nsb + blk * 8 + gq], ex1 = ex[xr * nsb + blk * 8 + 4 + gq];
+                        v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0l, B0l, z, 0, 0, 0);
+                        C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0h, B0h, C0, 0, 0, 0);
+                        v4i C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1l, B1l, z, 0, 0, 0);
+                        C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1h, B1h, C1, 0, 0, 0);
+                        const int S0 = C0[0] + (C0[1] << 8) + (C0[2] << 16);
+                        const int S1 = C1[0] + (C1[1] << 8) + (C1[2] << 16);
+                        float a = acc[xr][rg];
+                        a = __builtin_fmaf(ds0, ex0.x * static_cast<float>(S0), a);
+                        a = __builtin_fmaf(dm0, ex0.y, a);
+                        a = __builtin_fmaf(ds1, ex1.x * static_cast<float>(S1), a);
+                        a = __builtin_fmaf(dm1, ex1.y, a);
+                        acc[xr][rg] = a;
+                    }
                 }
             }
         }
-        // partial sums of the compute waves -> LDS as [row][wave], then one
-        // thread per row reads its eight partials at once (two b128 reads)
-        // and adds them in wave order
-        float *rbuf = red + (ti & 1) * RS * kRedWaves;
+        // partial sums of the compute waves -> LDS as [x row][row][wave], then
+        // one thread per (x row, row) reads its eight partials at once (two
+        // b128 reads) and adds them in wave order
+        float *rbuf = red + (ti & 1) * NX * RS * kRedWaves;
 #pragma unroll
-        for (int rg = 0; rg < RGN; rg++) {
-            float v = acc[rg];
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            if (gq == 0) rbuf[(rg * 16 + c16) * kRedWaves + wv] = v;
-        }
+        for (int xr = 0; xr < NX; xr++)
+#pragma unroll
+            for (int rg = 0; rg < RGN; rg++) {
+                float v = acc[xr][rg];
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                if (gq == 0) rbuf[((xr * RS) + rg * 16 + c16) * kRedWaves + wv] = v;
+            }
         __syncthreads();
         auto row_sum = [&](int r) {
             const floatx4 a = *reinterpret_cast<const floatx4 *>(rbuf + r * kRedWaves);
@@ -419,17 +438,20 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
                 if (k < nwc) v += p[k];
             return v;
         };
-        if (threadIdx.x < ROWS) {
+        if (threadIdx.x < NX * ROWS) {
+            const int xr = NX > 1 ? static_cast<int>(threadIdx.x) / ROWS : 0;
+            const int tr = static_cast<int>(threadIdx.x) - xr * ROWS;   // row within the tile
             const int64_t g = blockIdx.x + ti * gridDim.x;
             const int si = seg_w(g, segl);
             const int kind = segl[si].kind;
-            if (kind == SEG_SILU) {
+            const int64_t ooff = static_cast<int64_t>(xr) * t.out_stride;
+            if (xr < t.rows && kind == SEG_SILU) {
                 // rows t and 16 + t of the tile are gate and up of output n0 + t
-                if (threadIdx.x < 16) {
-                    const float gs = row_sum(threadIdx.x), us = row_sum(16 + threadIdx.x);
-                    const int64_t n = (g - segl[si].blk_begin) * 16 + threadIdx.x;
+                if (tr < 16) {
+                    const float gs = row_sum(xr * RS + tr), us = row_sum(xr * RS + 16 + tr);
+                    const int64_t n = (g - segl[si].blk_begin) * 16 + tr;
                     if (n < segl[si].n_out) {
-                        OT *o = static_cast<OT *>(segl[si].out) + n;
+                        OT *o = static_cast<OT *>(segl[si].out) + ooff + n;
                         if constexpr (sizeof(OT) == 2) {
                             // fused_gate_silu_kernel (fused.hpp:161-166): both
                             // dots rounded to f16, activation in f32, saturated
@@ -441,18 +463,28 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
                         }
                     }
                 }
-            } else {
-                const float v = row_sum(threadIdx.x);
-                const int64_t n = (g - segl[si].blk_begin) * ROWS + threadIdx.x;
+            } else if (xr < t.rows) {
+                const float v = row_sum(xr * RS + tr);
+                const int64_t n = (g - segl[si].blk_begin) * ROWS + tr;
                 if (n < segl[si].n_out)
-                    store_out<OT>(static_cast<OT *>(segl[si].out) + n, v, kind,
+                    store_out<OT>(static_cast<OT *>(segl[si].out) + ooff + n, v, kind,
                                   kind == SEG_ACC ? inv_acc : 1.0f);
             }
         }
     }
 }
 
-template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN>
+constexpr size_t kLdsBudget = 160u * 1024u - sizeof(Seg) * kMaxSegs;   // dynamic LDS per workgroup
+
+// LDS shared by the waves of a workgroup: NX digit tables with their scale
+// pairs, the zero area and the double-buffered reduction
+size_t fixed_lds(int nb, int rs, int nx) {
+    return static_cast<size_t>(nx) * nb * (kTabBlk + 8 * sizeof(float2)) + kZero +
+           2 * static_cast<size_t>(nx) * rs * kRedWaves * sizeof(float);
+}
+constexpr size_t slot_bytes(int rows) { return ((rows * 2 * 144 + 1023) / 1024) * 1024; }
+
+template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX>
 hipError_t launch(SegTable t, hipStream_t st) {
     constexpr int RS = 16 * ((ROWS + 15) / 16);
     constexpr int SLOT = ((ROWS * KB * 144 + 1023) / 1024) * 1024;
@@ -464,11 +496,10 @@ hipError_t launch(SegTable t, hipStream_t st) {
     }
     const int nb = t.n_in / 256;
     const int nks = (nb + KB - 1) / KB;
-    const size_t fixed = static_cast<size_t>(nb) * kTabBlk + kZero + static_cast<size_t>(nb) * 8 * sizeof(float2) +
-                         2 * RS * kRedWaves * sizeof(float);
+    const size_t fixed = fixed_lds(nb, RS, NX);
     const size_t per_wave = static_cast<size_t>(NSLOT) * SLOT;
-    // kXPasses sub-blocks per thread (4 threads each) must cover nb * 8
-    const int min_nw = (nb * 8 * 4 + 64 * kXPasses - 1) / (64 * kXPasses);
+    // kXPasses sub-blocks per thread (4 threads each) must cover NX * nb * 8
+    const int min_nw = (NX * nb * 8 * 4 + 64 * kXPasses - 1) / (64 * kXPasses);
     struct Pick { int nb, nw, per_cu; };
     static Pick cache[16] = {};
     int nw = 0, per_cu = 0;
@@ -478,10 +509,11 @@ hipError_t launch(SegTable t, hipStream_t st) {
         int best = 0;
         for (int cand = min_nw; cand <= 8; cand++) {
             const size_t l = fixed + cand * per_wave;
-            if (l + sizeof(Seg) * kMaxSegs > 160u * 1024u) break;
+            if (l > kLdsBudget) break;
             int blocks = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &blocks, gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN>, 64 * cand, l) != hipSuccess)
+                    &blocks, gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN, NX>, 64 * cand, l) !=
+                hipSuccess)
                 blocks = 0;
             if (blocks > 0 && blocks * cand >= best) { best = blocks * cand; nw = cand; per_cu = blocks; }
         }
@@ -498,32 +530,32 @@ hipError_t launch(SegTable t, hipStream_t st) {
     }
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
     if (grid > total) grid = total;
-    hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN>), dim3(static_cast<unsigned>(grid)),
-                       dim3(64 * nw), fixed + nw * per_wave, st, t, total, nks, nw);
+    hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN, NX>),
+                       dim3(static_cast<unsigned>(grid)), dim3(64 * nw), fixed + nw * per_wave, st, t, total,
+                       nks, nw);
     return hipGetLastError();
 }
 
-template <typename XT, typename OT, bool DOWN>
+template <typename XT, typename OT, bool DOWN, int NX>
 hipError_t launch_rows(int rows, const SegTable &t, hipStream_t st) {
-    switch (rows) {
-        case 32: return launch<XT, OT, 32, 2, 2, DOWN>(t, st);
-        case 28: return launch<XT, OT, 28, 2, 2, DOWN>(t, st);
-        case 24: return launch<XT, OT, 24, 2, 2, DOWN>(t, st);
-        case 20: return launch<XT, OT, 20, 2, 2, DOWN>(t, st);
-        default: return launch<XT, OT, 16, 2, 2, DOWN>(t, st);
+    if constexpr (NX == 1) {
+        switch (rows) {
+            case 32: return launch<XT, OT, 32, 2, 2, DOWN, NX>(t, st);
+            case 28: return launch<XT, OT, 28, 2, 2, DOWN, NX>(t, st);
+            case 24: return launch<XT, OT, 24, 2, 2, DOWN, NX>(t, st);
+            case 20: return launch<XT, OT, 20, 2, 2, DOWN, NX>(t, st);
+            default: return launch<XT, OT, 16, 2, 2, DOWN, NX>(t, st);
+        }
+    } else {
+        switch (rows) {
+            case 32: return launch<XT, OT, 32, 2, 2, DOWN, NX>(t, st);
+            case 24: return launch<XT, OT, 24, 2, 2, DOWN, NX>(t, st);
+            default: return launch<XT, OT, 16, 2, 2, DOWN, NX>(t, st);
+        }
     }
 }
 
-// Tile height: gate/up pairs take 32 rows (16 + 16); rows longer than 8192
-// values take 16 (the digit table leaves LDS for 16-row slots only).
-// Otherwise the height among 16..32 that minimises rounds x height, the
-// time of the workgroup with the most tiles when one workgroup runs per CU
-// (e.g. 14336 rows: 28-row tiles, 512 = 2 per CU, instead of 448 32-row
-// tiles of which 192 CUs run two and 64 run one).
-int pick_rows(const SegTable &t) {
-    for (int i = 0; i < t.n; i++)
-        if (t.seg[i].kind == SEG_SILU) return 32;
-    if (t.n_in > 8192) return 16;
+int device_cus() {
     static int cus = 0;
     if (!cus) {
         int dev = 0;
@@ -531,9 +563,24 @@ int pick_rows(const SegTable &t) {
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             cus = 256;
     }
-    int best = 32;
+    return cus;
+}
+
+// Tile height: gate/up pairs take 32 rows (16 + 16).  Otherwise, among the
+// heights whose slots leave room for 8 waves next to the NX digit tables
+// (16 if none does), the one that minimises rounds x height: the time of the
+// workgroup with the most tiles when one workgroup runs per CU (e.g. 14336
+// rows at NX = 1: 28-row tiles, 512 = 2 per CU, instead of 448 32-row tiles
+// of which 192 CUs run two and 64 run one).
+int pick_rows(const SegTable &t, int nx) {
+    for (int i = 0; i < t.n; i++)
+        if (t.seg[i].kind == SEG_SILU) return 32;
+    const int nb = t.n_in / 256;
+    const int cus = device_cus();
+    int best = 16;
     int64_t best_cost = INT64_MAX;
-    for (int r = 32; r >= 16; r -= 4) {
+    for (int r = 32; r >= 16; r -= (nx == 1 ? 4 : 8)) {
+        if (fixed_lds(nb, 16 * ((r + 15) / 16), nx) + 8 * 2 * slot_bytes(r) > kLdsBudget) continue;
         int64_t tiles = 0;
         for (int i = 0; i < t.n; i++) tiles += (t.seg[i].n_out + r - 1) / r;
         const int64_t cost = (tiles + cus - 1) / cus * r;
@@ -542,21 +589,57 @@ int pick_rows(const SegTable &t) {
     return best;
 }
 
+// Activation rows per pass: the largest of 4, 2, 1 whose sub-blocks the x
+// staging covers (kXPasses sub-blocks per 4 threads, at most 8 waves) with
+// LDS left for the waves that staging needs (at least four) at 16-row slots
+int nx_cap(int n_in) {
+    const int nb = n_in / 256;
+    for (int nx = 4; nx > 1; nx >>= 1) {
+        const int min_nw = (nx * nb * 8 * 4 + 64 * kXPasses - 1) / (64 * kXPasses);
+        const int nw = min_nw < 4 ? 4 : min_nw;
+        if (nw <= 8 && fixed_lds(nb, 16, nx) + nw * 2 * slot_bytes(16) <= kLdsBudget) return nx;
+    }
+    return 1;
+}
+
+template <typename XT, typename OT, int NX>
+hipError_t dispatch_nx(const SegTable &t, hipStream_t st) {
+    const int rows = pick_rows(t, NX);
+    if constexpr (sizeof(XT) == 4 && NX == 1) {
+        if (t.moe_tab && t.moe_down) return launch_rows<XT, OT, true, 1>(rows, t, st);
+    } else {
+        if (t.moe_tab && t.moe_down) return hipErrorNotSupported;   // down mode: f32 activations, one row
+    }
+    return launch_rows<XT, OT, false, NX>(rows, t, st);
+}
+
+// rows 2..8: passes of up to nx_cap activation rows, each reading W once
 template <typename XT, typename OT>
 hipError_t dispatch(const SegTable &t, hipStream_t st) {
-    const int rows = pick_rows(t);
-    if constexpr (sizeof(XT) == 4) {
-        if (t.moe_tab && t.moe_down) return launch_rows<XT, OT, true>(rows, t, st);
-    } else {
-        if (t.moe_tab && t.moe_down) return hipErrorNotSupported;   // down mode takes f32 activations
+    if (t.rows == 1) return dispatch_nx<XT, OT, 1>(t, st);
+    const int cap = nx_cap(t.n_in);
+    for (int64_t r0 = 0; r0 < t.rows; r0 += cap) {
+        SegTable p = t;
+        const int64_t c = t.rows - r0 < cap ? t.rows - r0 : cap;
+        p.rows = c;
+        for (int i = 0; i < p.n; i++) {
+            p.seg[i].x = static_cast<const XT *>(t.seg[i].x) + r0 * t.x_stride;
+            p.seg[i].out = static_cast<OT *>(t.seg[i].out) + r0 * t.out_stride;
+        }
+        const hipError_t e = c == 1 ? dispatch_nx<XT, OT, 1>(p, st)
+                           : c == 2 ? dispatch_nx<XT, OT, 2>(p, st)
+                                    : dispatch_nx<XT, OT, 4>(p, st);
+        if (e != hipSuccess) return e;
     }
-    return launch_rows<XT, OT, false>(rows, t, st);
+    return hipSuccess;
 }
 
 }  // namespace
 
 bool gemv_digits_ok(int dt, const SegTable &t) {
-    if (dt != DT_Q4_K || t.rows != 1 || t.n_in % 256 || t.n_in > kMaxK || t.row_bytes % 16) return false;
+    if (dt != DT_Q4_K || t.rows < 1 || t.rows > 8 || t.n_in % 256 || t.n_in > kMaxK || t.row_bytes % 16)
+        return false;
+    if (t.moe_tab && t.rows != 1) return false;
     if (t.moe_tab && t.moe_down &&
         (t.n != 1 || t.moe_k < 1 || t.moe_k > kMaxDownSlots || t.moe_kslot % 512 ||
          t.n_in != t.moe_k * t.moe_kslot || t.seg[0].kind != SEG_PLAIN))

@@ -321,6 +321,35 @@ def test_moe_dispatch_one_token_whole_units(krk, torch_cuda, be32, k, drop):
     assert e <= GEMV_TOL
 
 
+@pytest.mark.parametrize("rows,n_out,n_in", [(2, 520, 4096), (4, 300, 4096), (7, 200, 4096),
+                                          (3, 96, 14336), (8, 64, 11008), (5, 40, 256)])
+def test_q4_k_digits_rows(krk, torch_cuda, be32, rows, n_out, n_in):
+    """Rows 2..8 on the digit-plane kernel: passes of up to 4 activation rows
+    (2 for rows longer than 8192 values) share each weight unit."""
+    torch = torch_cuda
+    w = make_weights(krk, O.Q4_K, n_out, n_in, seed=800 + rows)
+    x = krk.synth_normal(rows * n_in, seed=801 + rows).reshape(rows, n_in)
+    say("digits rows", rows, n_out, n_in)
+    out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    be32.gemm(out, dev(torch, x), dev(torch, w), O.Q4_K, n_out, n_in, rows)
+    be32.sync()
+    ref = O.gemm(O.Q4_K, w, x, n_out)
+    for r in range(rows):
+        assert rel(host(out)[r], ref[r]) <= GEMV_TOL, r
+
+
+def test_q4_k_digits_rows_f16(krk, torch_cuda, be16):
+    torch = torch_cuda
+    rows, n_out, n_in = 3, 260, 4096
+    w = make_weights(krk, O.Q4_K, n_out, n_in, seed=820)
+    x = krk.synth_normal(rows * n_in, seed=821).reshape(rows, n_in).astype(np.float16)
+    out = torch.empty((rows, n_out), dtype=torch.float16, device="cuda")
+    be16.gemm(out, dev(torch, x), dev(torch, w), O.Q4_K, n_out, n_in, rows)
+    be16.sync()
+    ref = O.gemm(O.Q4_K, w, x.astype(np.float32), n_out)
+    assert rel(host(out).astype(np.float32), ref) <= 6e-4
+
+
 # ------------------------------------------------- digit-plane edge cases --
 def digit_edge_x(n_in, seed):
     """Activations whose 32-value sub-blocks put the digit split at its
