@@ -98,9 +98,14 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     uint8_t *slots = slots0 + wv * (NSLOT * SLOT);
     const int64_t rb = t.row_bytes;
-    // A workgroup owns tiles of ROWS rows (tiles blockIdx.x, + gridDim.x, ...);
-    // its waves split K: wave wv takes the units ks = wv, wv + nwc, ...
-    const int64_t my_tiles = blockIdx.x < total ? (total - 1 - blockIdx.x) / gridDim.x + 1 : 0;
+    // A workgroup owns tiles of ROWS rows (tiles lb, lb + nlb, ...); its
+    // waves split K: wave wv takes the units ks = wv, wv + nwc, ...  With
+    // several routed tokens, workgroup group tok serves token tok.
+    const bool multi = t.moe_tokens > 1;
+    const int nlb = multi ? t.moe_wpt : static_cast<int>(gridDim.x);
+    const int tok = multi ? static_cast<int>(blockIdx.x) / nlb : 0;
+    const int lb = multi ? static_cast<int>(blockIdx.x) - tok * nlb : static_cast<int>(blockIdx.x);
+    const int64_t my_tiles = lb < total ? (total - 1 - lb) / nlb + 1 : 0;
     const int cnt = wv < nks ? (nks - 1 - wv) / nwc + 1 : 0;
     const int64_t my_units = my_tiles * cnt;
 
@@ -128,7 +133,7 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     // the first units read the segment table from the kernel arguments (the
     // LDS copy is not ready yet); later ones from LDS
     auto issue = [&](int64_t j, const Seg *tab_) {
-        const int64_t g = blockIdx.x + (j / cnt) * gridDim.x;
+        const int64_t g = lb + (j / cnt) * nlb;
         const int ks = wv + static_cast<int>(j % cnt) * nwc;
         const int si = seg_w(g, tab_);
         const bool pair = tab_[si].kind == SEG_SILU;
@@ -174,7 +179,7 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
 
     // ---- x loads (four threads per 32-value sub-block, kXPasses passes over
     // the NX rows' sub-blocks; rows past t.rows read as zero)
-    const XT *x = static_cast<const XT *>(t.seg[0].x);
+    const XT *x = static_cast<const XT *>(t.seg[0].x) + (multi ? tok * t.moe_xtok : 0);
     const int q = threadIdx.x & 3;
     const int nsb = nb * 8;
     const int nxs = NX * nsb;
@@ -206,23 +211,29 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     if (DOWN) {
         if (threadIdx.x < t.moe_k) {
             const krk_moe_entry *mt = static_cast<const krk_moe_entry *>(t.moe_tab);
-            const int e = t.moe_ids[threadIdx.x];
+            const int64_t pi = static_cast<int64_t>(tok) * t.moe_k + threadIdx.x;
+            const int e = t.moe_ids[pi];
             const bool live = e >= 0 && e < t.moe_ne;
             bankl[threadIdx.x] = static_cast<const uint8_t *>(mt[live ? e : 0].p[KRK_MOE_DOWN]);
-            wl[threadIdx.x] = live ? t.moe_wts[threadIdx.x] : 0.0f;
+            wl[threadIdx.x] = live ? t.moe_wts[pi] : 0.0f;
         }
-        if (threadIdx.x == 0) segl[0] = t.seg[0];
+        if (threadIdx.x == 0) {
+            Seg sg = t.seg[0];
+            if (multi) sg.out = static_cast<float *>(sg.out) + tok * t.moe_otok;
+            segl[0] = sg;
+        }
         __syncthreads();
     } else if (moe) {
         if (threadIdx.x < nseg) {
-            const int32_t *ids = t.moe_ids;
+            const int32_t *ids = t.moe_ids + static_cast<int64_t>(tok) * nseg;
             const krk_moe_entry *mt = static_cast<const krk_moe_entry *>(t.moe_tab);
             int e = ids[threadIdx.x];
             if (e < 0 || e >= t.moe_ne) e = 0;   // a dropped slot: any bank, its row is never read
             Seg sg = t.seg[threadIdx.x];
             sg.w = mt[e].p[KRK_MOE_GATE];
             sg.w2 = mt[e].p[KRK_MOE_UP];
-            sg.out = static_cast<float *>(t.seg[0].out) + static_cast<int64_t>(threadIdx.x) * t.seg[0].n_out;
+            sg.out = static_cast<float *>(t.seg[0].out) + (multi ? tok * t.moe_otok : 0) +
+                     static_cast<int64_t>(threadIdx.x) * t.seg[0].n_out;
             segl[threadIdx.x] = sg;
         }
         __syncthreads();
@@ -441,7 +452,7 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         if (threadIdx.x < NX * ROWS) {
             const int xr = NX > 1 ? static_cast<int>(threadIdx.x) / ROWS : 0;
             const int tr = static_cast<int>(threadIdx.x) - xr * ROWS;   // row within the tile
-            const int64_t g = blockIdx.x + ti * gridDim.x;
+            const int64_t g = lb + ti * nlb;
             const int si = seg_w(g, segl);
             const int kind = segl[si].kind;
             const int64_t ooff = static_cast<int64_t>(xr) * t.out_stride;
@@ -529,7 +540,16 @@ hipError_t launch(SegTable t, hipStream_t st) {
             cus = 256;
     }
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
-    if (grid > total) grid = total;
+    if (t.moe_tokens > 1) {
+        // a group of workgroups per token, the groups filling the chip together
+        int64_t wpt = grid / t.moe_tokens;
+        if (wpt > total) wpt = total;
+        if (wpt < 1) wpt = 1;
+        t.moe_wpt = static_cast<int>(wpt);
+        grid = wpt * t.moe_tokens;
+    } else if (grid > total) {
+        grid = total;
+    }
     hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN, NX>),
                        dim3(static_cast<unsigned>(grid)), dim3(64 * nw), fixed + nw * per_wave, st, t, total,
                        nks, nw);
@@ -583,6 +603,7 @@ int pick_rows(const SegTable &t, int nx) {
         if (fixed_lds(nb, 16 * ((r + 15) / 16), nx) + 8 * 2 * slot_bytes(r) > kLdsBudget) continue;
         int64_t tiles = 0;
         for (int i = 0; i < t.n; i++) tiles += (t.seg[i].n_out + r - 1) / r;
+        if (t.moe_tokens > 1) tiles *= t.moe_tokens;
         const int64_t cost = (tiles + cus - 1) / cus * r;
         if (cost < best_cost) { best_cost = cost; best = r; }
     }

@@ -49,6 +49,13 @@ struct SegTable {
     int moe_down;
     int moe_k;
     int64_t moe_kslot;
+    // Several tokens (moe_tokens > 1): the grid is moe_tokens groups of
+    // moe_wpt workgroups; group tk handles token tk: its ids and weights at
+    // moe_ids / moe_wts + tk * k, its activations at seg[0].x + tk * moe_xtok
+    // elements and its outputs at seg[0].out + tk * moe_otok elements.
+    int moe_tokens;
+    int moe_wpt;
+    int64_t moe_xtok, moe_otok;
 };
 
 hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st);

@@ -2,8 +2,9 @@
 // device pointer table (Backend::moe_dispatch, backend.hpp:1001-1009; the
 // reference's moe_table_* kernels, src/hip/kernels/moe_table.hpp:38-551).
 //
-// Decode (one token) takes the two-launch path below the plan kernel; more
-// tokens take four launches, none of them per expert and none waiting on
+// Q4_K banks with f32 activations take two launches of the digit-plane GEMV
+// for any token count (below).  Otherwise one token takes two VALU launches,
+// and more tokens take four, none of them per expert and none waiting on
 // the host:
 //   1. plan      one workgroup: expert-major plan of the (token, slot) pairs,
 //                the active-expert list in ascending id, and each pair's
@@ -383,61 +384,74 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
         const int64_t resident = 256LL * (32 / waves_per_wg);
         return dim3(static_cast<unsigned>(want < resident ? want : resident));
     };
+    // Q4_K banks with f32 activations, any token count: both stages on the
+    // digit-plane kernel (int8 matrix cores), the routed banks resolved on
+    // the device, one group of workgroups per token.
+    //   gate/up: one segment per slot, mid[t * k + s] = silu(g) * u;
+    //   down:    one GEMV per token over its k slots concatenated, the
+    //            routing weights folded into the activation scales, written
+    //            straight to out[t].
+    SegTable gu{};
+    gu.n = a.k;
+    gu.n_in = static_cast<int>(a.n_embd);
+    gu.row_bytes = a.rb_gate;
+    gu.rows = 1;
+    gu.x_stride = a.n_embd;
+    gu.out_stride = a.n_ff;
+    gu.moe_tab = tab;
+    gu.moe_ids = a.ids;
+    gu.moe_ne = a.n_expert;
+    gu.moe_tokens = static_cast<int>(a.n_tok);
+    gu.moe_xtok = a.n_embd;
+    gu.moe_otok = a.k * a.n_ff;
+    for (int i = 0; i < a.k && i < kMaxSegs; i++) {
+        gu.seg[i].x = a.xn;
+        gu.seg[i].out = w.mid;
+        gu.seg[i].n_out = a.n_ff;
+        gu.seg[i].kind = SEG_SILU;
+    }
+    SegTable d{};
+    d.n = 1;
+    d.n_in = static_cast<int>(a.k * a.n_ff);
+    d.row_bytes = a.rb_down;
+    d.rows = 1;
+    d.x_stride = d.n_in;
+    d.out_stride = a.n_embd;
+    d.seg[0].x = w.mid;
+    d.seg[0].out = a.out;
+    d.seg[0].n_out = a.n_embd;
+    d.seg[0].kind = SEG_PLAIN;
+    d.moe_tab = tab;
+    d.moe_ids = a.ids;
+    d.moe_wts = a.wts;
+    d.moe_ne = a.n_expert;
+    d.moe_down = 1;
+    d.moe_k = a.k;
+    d.moe_kslot = a.n_ff;
+    d.moe_tokens = static_cast<int>(a.n_tok);
+    d.moe_xtok = a.k * a.n_ff;
+    d.moe_otok = a.n_embd;
+    const bool on_digits = !a.act_f16 && a.wt == DT_Q4_K && a.aligned16 && a.rb_gate == a.rb_up &&
+                           a.k <= kMaxSegs && a.n_tok <= (1 << 20) && a.k * a.n_ff <= (1 << 30);
+    const bool gu_ok = on_digits && gemv_digits_ok(DT_Q4_K, gu);
+    const bool dn_ok = on_digits && gemv_digits_ok(DT_Q4_K, d);
+    if (gu_ok && (dn_ok || a.n_tok == 1)) {
+        const hipError_t e = gemv_digits(false, gu, st);
+        if (e != hipSuccess) return e;
+        if (dn_ok) return gemv_digits(false, d, st);
+    }
     if (a.n_tok == 1) {
         const int64_t ggu = (a.n_ff + 3) / 4, gdn = (a.n_embd + 7) / 8;
-        // Q4_K banks with f32 activations: gate/up on the int8 matrix cores
-        // (the digits GEMV), the routed banks resolved on the device
-        SegTable t{};
-        t.n = a.k;
-        t.n_in = static_cast<int>(a.n_embd);
-        t.row_bytes = a.rb_gate;
-        t.rows = 1;
-        t.x_stride = a.n_embd;
-        t.out_stride = a.n_ff;
-        t.moe_tab = tab;
-        t.moe_ids = a.ids;
-        t.moe_ne = a.n_expert;
-        for (int i = 0; i < a.k && i < kMaxSegs; i++) {
-            t.seg[i].x = a.xn;
-            t.seg[i].out = w.mid;
-            t.seg[i].n_out = a.n_ff;
-            t.seg[i].kind = SEG_SILU;
+        if (!gu_ok) {
+            if (a.act_f16)
+                hipLaunchKernelGGL((moe_gu1_kernel<_Float16, 8>), cap(a.k * ggu, wgu), dim3(64 * wgu), 0, st,
+                                   tab, a.ids, a.k, a.n_expert, static_cast<const _Float16 *>(a.xn), a.n_embd,
+                                   a.n_ff, ggu, w.mid);
+            else
+                hipLaunchKernelGGL((moe_gu1_kernel<float, 8>), cap(a.k * ggu, wgu), dim3(64 * wgu), 0, st, tab,
+                                   a.ids, a.k, a.n_expert, static_cast<const float *>(a.xn), a.n_embd, a.n_ff,
+                                   ggu, w.mid);
         }
-        if (!a.act_f16 && a.wt == DT_Q4_K && a.aligned16 && a.k <= kMaxSegs && a.rb_gate == a.rb_up &&
-            gemv_digits_ok(DT_Q4_K, t)) {
-            const hipError_t e = gemv_digits(false, t, st);
-            if (e != hipSuccess) return e;
-        } else if (a.act_f16)
-            hipLaunchKernelGGL((moe_gu1_kernel<_Float16, 8>), cap(a.k * ggu, wgu), dim3(64 * wgu), 0, st, tab,
-                               a.ids, a.k, a.n_expert, static_cast<const _Float16 *>(a.xn), a.n_embd, a.n_ff,
-                               ggu, w.mid);
-        else
-            hipLaunchKernelGGL((moe_gu1_kernel<float, 8>), cap(a.k * ggu, wgu), dim3(64 * wgu), 0, st, tab,
-                               a.ids, a.k, a.n_expert, static_cast<const float *>(a.xn), a.n_embd, a.n_ff,
-                               ggu, w.mid);
-        // down projections as one GEMV over the concatenated slots, the
-        // routing weights folded into the activation scales
-        SegTable d{};
-        d.n = 1;
-        d.n_in = static_cast<int>(a.k * a.n_ff);
-        d.row_bytes = a.rb_down;
-        d.rows = 1;
-        d.x_stride = d.n_in;
-        d.out_stride = a.n_embd;
-        d.seg[0].x = w.mid;
-        d.seg[0].out = a.out;
-        d.seg[0].n_out = a.n_embd;
-        d.seg[0].kind = SEG_PLAIN;
-        d.moe_tab = tab;
-        d.moe_ids = a.ids;
-        d.moe_wts = a.wts;
-        d.moe_ne = a.n_expert;
-        d.moe_down = 1;
-        d.moe_k = a.k;
-        d.moe_kslot = a.n_ff;
-        if (!a.act_f16 && a.wt == DT_Q4_K && a.aligned16 && a.k * a.n_ff <= (1 << 30) &&
-            gemv_digits_ok(DT_Q4_K, d))
-            return gemv_digits(false, d, st);
         if (a.act_f16)
             hipLaunchKernelGGL((moe_down1_kernel<_Float16, 8>), cap(gdn, 8), dim3(64 * 8), 0, st, tab, a.ids,
                                a.wts, a.k, a.n_expert, a.n_embd, a.n_ff, gdn, w.mid,

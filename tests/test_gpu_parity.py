@@ -296,22 +296,25 @@ def test_moe_dispatch_parity(krk, torch_cuda, be32, n_tok):
     assert e <= GEMV_TOL
 
 
-@pytest.mark.parametrize("k,drop", [(2, False), (8, False), (4, True)])
-def test_moe_dispatch_one_token_whole_units(krk, torch_cuda, be32, k, drop):
-    """n_ff a multiple of 512: the one-token path runs gate/up and down on the
-    digit-plane kernel (down over the concatenated slots).  drop: a slot with
-    id -1 contributes nothing, as in the host loop."""
+@pytest.mark.parametrize("n_tok,k,drop", [(1, 2, False), (1, 8, False), (1, 4, True), (3, 4, True),
+                                          (16, 8, False)])
+def test_moe_dispatch_whole_units(krk, torch_cuda, be32, n_tok, k, drop):
+    """n_ff a multiple of 512: gate/up and down run on the digit-plane kernel
+    (down over each token's concatenated slots), one workgroup group per
+    token.  drop: a slot with id -1 contributes nothing, as in the host
+    loop."""
     torch = torch_cuda
     dt, ne, n_embd, n_ff = O.Q4_K, 8, 1024, 1024
     mats, table, keep = build_moe(krk, torch, dt, ne, n_embd, n_ff, seed=950)
-    logits = krk.synth_normal(ne, seed=81 + k).reshape(1, ne)
+    logits = krk.synth_normal(n_tok * ne, seed=81 + k).reshape(n_tok, ne)
     ids, wts = O.router_topk(O.router_softmax(logits), k)
     if drop:
         ids[0, 1] = -1
-    x = krk.synth_normal(n_embd, seed=82).reshape(1, n_embd)
-    say("moe one token", k, ids.tolist())
-    out = torch.empty((1, n_embd), dtype=torch.float32, device="cuda")
-    be32.moe_dispatch(table, 0, ne, dev(torch, ids), dev(torch, wts), dev(torch, x), out, 1,
+        ids[n_tok - 1, k - 1] = -1
+    x = krk.synth_normal(n_tok * n_embd, seed=82).reshape(n_tok, n_embd)
+    say("moe whole units", n_tok, k, ids.tolist())
+    out = torch.empty((n_tok, n_embd), dtype=torch.float32, device="cuda")
+    be32.moe_dispatch(table, 0, ne, dev(torch, ids), dev(torch, wts), dev(torch, x), out, n_tok,
                       n_embd, n_ff, k)
     be32.sync()
     ref = O.moe_ffn(x, [mats[0, e] for e in range(ne)], [mats[1, e] for e in range(ne)],
