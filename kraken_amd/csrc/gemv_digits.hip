@@ -64,7 +64,7 @@ constexpr int kLateWaves = 4;
 
 __device__ __forceinline__ v4i ld_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
-template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX>
+template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT>
 __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_t total, int nks, int nwc) {
     constexpr int BB = 144;
     constexpr int P = KB * BB;                   // row piece of one unit
@@ -101,7 +101,7 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     // A workgroup owns tiles of ROWS rows (tiles lb, lb + nlb, ...); its
     // waves split K: wave wv takes the units ks = wv, wv + nwc, ...  With
     // several routed tokens, workgroup group tok serves token tok.
-    const bool multi = t.moe_tokens > 1;
+    constexpr bool multi = MT;   // several routed tokens
     const int nlb = multi ? t.moe_wpt : static_cast<int>(gridDim.x);
     const int tok = multi ? static_cast<int>(blockIdx.x) / nlb : 0;
     const int lb = multi ? static_cast<int>(blockIdx.x) - tok * nlb : static_cast<int>(blockIdx.x);
@@ -228,13 +228,25 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
             const int32_t *ids = t.moe_ids + static_cast<int64_t>(tok) * nseg;
             const krk_moe_entry *mt = static_cast<const krk_moe_entry *>(t.moe_tab);
             int e = ids[threadIdx.x];
-            if (e < 0 || e >= t.moe_ne) e = 0;   // a dropped slot: any bank, its row is never read
+            const bool live = e >= 0 && e < t.moe_ne;
+            // segments in ascending expert id (dropped slots last): tokens
+            // sharing an expert then stream it at about the same time
+            int rank = 0;
+            for (int i = 0; i < nseg; i++) {
+                const int o = ids[i];
+                const bool ol = o >= 0 && o < t.moe_ne;
+                const bool before = live ? (ol && (o < e || (o == e && i < static_cast<int>(threadIdx.x))))
+                                         : (ol || i < static_cast<int>(threadIdx.x));
+                rank += before ? 1 : 0;
+            }
+            if (!live) e = 0;   // a dropped slot: any bank, its row is never read
             Seg sg = t.seg[threadIdx.x];
             sg.w = mt[e].p[KRK_MOE_GATE];
             sg.w2 = mt[e].p[KRK_MOE_UP];
             sg.out = static_cast<float *>(t.seg[0].out) + (multi ? tok * t.moe_otok : 0) +
                      static_cast<int64_t>(threadIdx.x) * t.seg[0].n_out;
-            segl[threadIdx.x] = sg;
+            sg.blk_begin = t.seg[rank].blk_begin;   // equal segments: the tile ranges are the same
+            segl[rank] = sg;
         }
         __syncthreads();
     }
@@ -495,7 +507,7 @@ size_t fixed_lds(int nb, int rs, int nx) {
 }
 constexpr size_t slot_bytes(int rows) { return ((rows * 2 * 144 + 1023) / 1024) * 1024; }
 
-template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX>
+template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT>
 hipError_t launch(SegTable t, hipStream_t st) {
     constexpr int RS = 16 * ((ROWS + 15) / 16);
     constexpr int SLOT = ((ROWS * KB * 144 + 1023) / 1024) * 1024;
@@ -523,7 +535,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
             if (l > kLdsBudget) break;
             int blocks = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &blocks, gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN, NX>, 64 * cand, l) !=
+                    &blocks, gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT>, 64 * cand, l) !=
                 hipSuccess)
                 blocks = 0;
             if (blocks > 0 && blocks * cand >= best) { best = blocks * cand; nw = cand; per_cu = blocks; }
@@ -540,7 +552,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
             cus = 256;
     }
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
-    if (t.moe_tokens > 1) {
+    if (MT) {
         // a group of workgroups per token, the groups filling the chip together
         int64_t wpt = grid / t.moe_tokens;
         if (wpt > total) wpt = total;
@@ -550,27 +562,27 @@ hipError_t launch(SegTable t, hipStream_t st) {
     } else if (grid > total) {
         grid = total;
     }
-    hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN, NX>),
+    hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT>),
                        dim3(static_cast<unsigned>(grid)), dim3(64 * nw), fixed + nw * per_wave, st, t, total,
                        nks, nw);
     return hipGetLastError();
 }
 
-template <typename XT, typename OT, bool DOWN, int NX>
+template <typename XT, typename OT, bool DOWN, int NX, bool MT = false>
 hipError_t launch_rows(int rows, const SegTable &t, hipStream_t st) {
     if constexpr (NX == 1) {
         switch (rows) {
-            case 32: return launch<XT, OT, 32, 2, 2, DOWN, NX>(t, st);
-            case 28: return launch<XT, OT, 28, 2, 2, DOWN, NX>(t, st);
-            case 24: return launch<XT, OT, 24, 2, 2, DOWN, NX>(t, st);
-            case 20: return launch<XT, OT, 20, 2, 2, DOWN, NX>(t, st);
-            default: return launch<XT, OT, 16, 2, 2, DOWN, NX>(t, st);
+            case 32: return launch<XT, OT, 32, 2, 2, DOWN, NX, MT>(t, st);
+            case 28: return launch<XT, OT, 28, 2, 2, DOWN, NX, MT>(t, st);
+            case 24: return launch<XT, OT, 24, 2, 2, DOWN, NX, MT>(t, st);
+            case 20: return launch<XT, OT, 20, 2, 2, DOWN, NX, MT>(t, st);
+            default: return launch<XT, OT, 16, 2, 2, DOWN, NX, MT>(t, st);
         }
     } else {
         switch (rows) {
-            case 32: return launch<XT, OT, 32, 2, 2, DOWN, NX>(t, st);
-            case 24: return launch<XT, OT, 24, 2, 2, DOWN, NX>(t, st);
-            default: return launch<XT, OT, 16, 2, 2, DOWN, NX>(t, st);
+            case 32: return launch<XT, OT, 32, 2, 2, DOWN, NX, MT>(t, st);
+            case 24: return launch<XT, OT, 24, 2, 2, DOWN, NX, MT>(t, st);
+            default: return launch<XT, OT, 16, 2, 2, DOWN, NX, MT>(t, st);
         }
     }
 }
@@ -627,9 +639,14 @@ template <typename XT, typename OT, int NX>
 hipError_t dispatch_nx(const SegTable &t, hipStream_t st) {
     const int rows = pick_rows(t, NX);
     if constexpr (sizeof(XT) == 4 && NX == 1) {
-        if (t.moe_tab && t.moe_down) return launch_rows<XT, OT, true, 1>(rows, t, st);
+        if (t.moe_tab && t.moe_down)
+            return t.moe_tokens > 1 ? launch_rows<XT, OT, true, 1, true>(rows, t, st)
+                                    : launch_rows<XT, OT, true, 1, false>(rows, t, st);
+        if (t.moe_tab && t.moe_tokens > 1)   // gate/up pairs: 32-row tiles
+            return launch<XT, OT, 32, 2, 2, false, 1, true>(t, st);
     } else {
-        if (t.moe_tab && t.moe_down) return hipErrorNotSupported;   // down mode: f32 activations, one row
+        // down mode and several tokens: f32 activations, one row
+        if (t.moe_tab && (t.moe_down || t.moe_tokens > 1)) return hipErrorNotSupported;
     }
     return launch_rows<XT, OT, false, NX>(rows, t, st);
 }
