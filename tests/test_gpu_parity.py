@@ -232,6 +232,21 @@ def test_gemm_mfma_parity(krk, torch_cuda, be16, be32, dt, shape):
     assert e16 <= GEMM_TOL and e32 <= GEMM_TOL
 
 
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K])
+def test_gemm_mfma_parity_many_tiles(krk, torch_cuda, be16, dt):
+    """384 tiles (no split-K) with an M edge tile of 8 rows."""
+    torch = torch_cuda
+    M, N, K = 520, 32768, 256
+    w = make_weights(krk, dt, N, K, seed=70 + dt)
+    x = krk.synth_normal(M * K, seed=71).reshape(M, K).astype(np.float16)
+    say("gemm many tiles", dt, M, N, K)
+    out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    be16.gemm(out, dev(torch, x), dev(torch, w), dt, N, K, M)
+    be16.sync()
+    ref = O.gemm(dt, w, x.astype(np.float32), N)
+    assert rel(host(out).astype(np.float32), ref) <= GEMM_TOL
+
+
 # ------------------------------------------------------------------ router --
 def test_router_softmax_topk(krk, torch_cuda, be32, rng):
     torch = torch_cuda
