@@ -1,4 +1,4 @@
-// gemv_digits.hip -- Q4_K decode GEMV on the int8 matrix cores.
+// gemv_digits.hip -- Q4_K and Q6_K decode GEMV on the int8 matrix cores.
 //
 // Decode GEMV (rows == 1) is bound by HBM, but with a 4-bit format the VALU
 // work of a dequantize-and-FMA loop (one v_fma_mix per weight plus the
@@ -55,8 +55,8 @@ constexpr int kMaxK = 16384;
 constexpr int kMaxDownSlots = 16;
 static_assert(sizeof(Seg) * (kMaxSegs - 1) >= kMaxDownSlots * (sizeof(void *) + sizeof(float)),
               "down-mode slot table fits in the segment table");
-constexpr int kXPasses = 8;
-constexpr int kRedWaves = 8;   // reduction slots per row (waves per workgroup <= 8)  // x sub-blocks staged per thread (4 threads per sub-block)
+constexpr int kXPasses = 8;    // x sub-blocks staged per thread (4 threads per sub-block)
+constexpr int kRedWaves = 8;   // reduction slots per row (waves per workgroup <= 8)
 // Waves that issue their first weight DMA only after building the digit
 // table: a wave stalls while the memory pipeline cannot accept its DMA, and
 // these keep the table build moving meanwhile (measured: 4 of 8 best).
@@ -64,16 +64,36 @@ constexpr int kLateWaves = 4;
 
 __device__ __forceinline__ v4i ld_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
-template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT>
-__global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_t total, int nks, int nwc) {
-    constexpr int BB = 144;
+// LDS-DMA of N bytes per lane (the builtin needs a literal size)
+template <int N> __device__ __forceinline__ void dma_lds(const void *src, uint8_t *dst);
+template <> __device__ __forceinline__ void dma_lds<4>(const void *src, uint8_t *dst) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)dst, 4, 0, 0);
+}
+template <> __device__ __forceinline__ void dma_lds<16>(const void *src, uint8_t *dst) {
+    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)dst, 16, 0, 0);
+}
+
+template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT>
+__global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t total, int nks, int nwc) {
+    constexpr bool Q6 = DT == DT_Q6_K;
+    constexpr int BB = Q6 ? 210 : 144;           // block bytes
     constexpr int P = KB * BB;                   // row piece of one unit
     constexpr int RGN = (ROWS + 15) / 16;        // 16-row MFMA groups (the last may be partial)
     constexpr int RS = 16 * RGN;                 // reduction stride
-    constexpr int U = ROWS * P;
-    constexpr int CH = (U + 1023) / 1024;
-    constexpr int SLOT = CH * 1024;
-    static_assert((NSLOT - 1) * CH < 64, "vmcnt is 6 bits");
+    // LDS unit layout: row r at r * PL.  Q4_K pieces are 16-byte multiples
+    // (dwordx4 LDS-DMA).  Q6_K blocks (210 bytes) go to a 224-byte stride so
+    // every LDS read is 16-byte aligned; with dword LDS-DMA each lane picks
+    // its own 4-byte source window inside its block, so no byte outside the
+    // matrix is ever read.
+    constexpr int BL = Q6 ? 224 : BB;            // LDS block stride
+    constexpr int PL = KB * BL;                  // LDS row stride
+    constexpr int U = ROWS * PL;
+    constexpr int DMA = Q6 ? 4 : 16;             // bytes per lane per LDS-DMA instruction
+    constexpr int CHB = 64 * DMA;                // bytes per instruction
+    constexpr int CH = (U + CHB - 1) / CHB;
+    constexpr int SLOT = ((U + 1023) / 1024) * 1024;
+    static_assert(NSLOT * CH < 64, "vmcnt is 6 bits");
+    static_assert(!Q6 || (ROWS <= 16 && !DOWN && !MT), "Q6_K: 16-row tiles, plain segments");
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ Seg segl[kMaxSegs];
     // down mode uses segl[0] only; the bank and the weight of each slot live
@@ -86,7 +106,10 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     uint8_t *tab = lds;                               // [NX][nb][8][3][32] int8 digits
     uint8_t *zero = tab + NX * tstride;               // kZero zero bytes
     float2 *ex = reinterpret_cast<float2 *>(zero + kZero);  // [NX][nb * 8] {2^-e, sum x}
-    uint8_t *slots0 = reinterpret_cast<uint8_t *>(ex + NX * nb * 8);
+    // Q6_K: exact integer sums of X over each 16-value half of a sub-block
+    // (for the code offset 32), stored as int bits
+    float2 *ex16 = ex + NX * nb * 8;                  // [NX][nb * 8] (Q6_K only)
+    uint8_t *slots0 = reinterpret_cast<uint8_t *>(ex + (Q6 ? 2 : 1) * NX * nb * 8);
     float *red = reinterpret_cast<float *>(slots0 + nwc * (NSLOT * SLOT));  // [2][NX][RS][kRedWaves]
 
     // Every wave streams, multiplies and builds a share of the digit table.
@@ -121,13 +144,25 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     // offset o % P.  Rows 0..15 come from base 0, rows 16..31 from base 1:
     // the next 16 rows of the same matrix, or for a gate/up (SiLU) segment
     // the same 16 rows of the up matrix.
+    // source offset, inside the row piece, of LDS offset rem of a row.
+    // Q6_K: a block's last 4-byte window (LDS 208) takes bytes 206..209, so
+    // no lane reads past its block (d then sits at LDS 210); windows past it
+    // are padding and read the piece start
+    auto src_off = [](int rem) {
+        if constexpr (Q6) {
+            const int b = rem / BL, off = rem - b * BL;
+            return off <= BB - 2 ? b * BB + (off == BB - 2 ? off - 2 : off) : 0;
+        } else {
+            return rem;
+        }
+    };
     int32_t dl[CH];
     uint32_t hi_rows = 0;   // bit c: this lane's chunk c lies in rows 16..31
 #pragma unroll
     for (int c = 0; c < CH; c++) {
-        const int o = c * 1024 + 16 * lane;
-        const int r = o < U ? o / P : 0;
-        dl[c] = o < U ? static_cast<int32_t>((r & 15) * rb + (o - r * P)) : 0;
+        const int o = c * CHB + DMA * lane;
+        const int r = o < U ? o / PL : 0;
+        dl[c] = o < U ? static_cast<int32_t>((r & 15) * rb + src_off(o - r * PL)) : 0;
         if (r >= 16) hi_rows |= 1u << c;
     }
     // the first units read the segment table from the kernel arguments (the
@@ -157,22 +192,20 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
             const uint8_t *b0 = w + n0 * rb + k0, *b1 = w1 + n0 * rb + k0;
 #pragma unroll
             for (int c = 0; c < CH; c++)
-                __builtin_amdgcn_global_load_lds(static_cast<const void *>(((hi_rows >> c) & 1 ? b1 : b0) + dl[c]),
-                                                 (lds_void_t *)(dst + c * 1024), 16, 0, 0);
+                dma_lds<DMA>(static_cast<const void *>(((hi_rows >> c) & 1 ? b1 : b0) + dl[c]), dst + c * CHB);
         } else {
             // the matrix's last rows: clamp rows and row ends to stay inside
-            const int64_t lim = rb - 16;
+            const int64_t lim = rb - DMA;
 #pragma unroll
             for (int c = 0; c < CH; c++) {
-                const int o = c * 1024 + 16 * lane;
-                const int r = o < U ? o / P : 0;
+                const int o = c * CHB + DMA * lane;
+                const int r = o < U ? o / PL : 0;
                 const bool up = pair && r >= 16;
                 int64_t n = n0 + (pair ? (r & 15) : r);
                 if (n >= n_out) n = n_out - 1;
-                int64_t off = k0 + (o < U ? o - r * P : 0);
+                int64_t off = k0 + (o < U ? src_off(o - r * PL) : 0);
                 if (off > lim) off = lim;
-                __builtin_amdgcn_global_load_lds(static_cast<const void *>((up ? w1 : w) + n * rb + off),
-                                                 (lds_void_t *)(dst + c * 1024), 16, 0, 0);
+                dma_lds<DMA>(static_cast<const void *>((up ? w1 : w) + n * rb + off), dst + c * CHB);
             }
         }
     };
@@ -306,9 +339,11 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         const float up = __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
         const float dn = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
         uint32_t p0[2] = {0u, 0u}, p1[2] = {0u, 0u}, p2[2] = {0u, 0u};
+        int xsum = 0;   // Q6_K: exact integer sum of this thread's 8 X
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const int X = live ? static_cast<int>(__builtin_rintf(v[k] * up)) : 0;
+            xsum += X;
             const int d0 = ((X + 128) & 255) - 128;
             const int X1 = (X - d0) >> 8;
             const int d1 = ((X1 + 128) & 255) - 128;
@@ -322,10 +357,14 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
         *reinterpret_cast<u32x2 *>(o) = u32x2{p0[0], p0[1]};
         *reinterpret_cast<u32x2 *>(o + 32) = u32x2{p1[0], p1[1]};
         *reinterpret_cast<u32x2 *>(o + 64) = u32x2{p2[0], p2[1]};
+        // Q6_K: sum of X over each 16-value half (threads q, q ^ 1)
+        xsum += __shfl_xor(xsum, 1, 64);
+        const int xsum_hi = __shfl_xor(xsum, 2, 64);
         if (q == 0) {
             // down mode: the slot weight scales the sub-block's activations
             const float ws = DOWN ? wl[sb / static_cast<int>(t.moe_kslot / 32)] : 1.0f;
             ex[xr * nsb + sb] = float2{(live ? dn : 1.0f) * ws, sum * ws};
+            if (Q6) ex16[xr * nsb + sb] = float2{__int_as_float(xsum), __int_as_float(xsum_hi)};
         }
     }
     if (!moe && threadIdx.x < nseg) segl[threadIdx.x] = t.seg[threadIdx.x];
@@ -355,6 +394,13 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
     const uint8_t *a_lo_p = a_lo ? tab + a_off : zero;
     const uint8_t *a_hi_p = a_hi ? tab + a_off : zero;
     const int a_lo_inc = a_lo ? kTabBlk : 0, a_hi_inc = a_hi ? kTabBlk : 0;
+    // Q6_K: MFMA chunk qd of a block takes, in lane group gq = 2h + lh, the
+    // 16 values 128h + 32qd + 16lh + i -- one scale sub-block; the A row
+    // 4gq + p holds their digit plane p (sub-block 4h + qd of the table)
+    const int h6 = gq >> 1, lh6 = gq & 1;
+    const bool a6 = ap < 3 && as == gq;
+    const uint8_t *a6_p = a6 ? tab + 4 * h6 * 96 + ap * 32 + 16 * lh6 : zero;
+    const int a6_inc = a6 ? kTabBlk : 0, a6_qd = a6 ? 96 : 0;
     const uint32_t M = 0x0F0F0F0Fu;
     const uint32_t bsh = 8u * static_cast<uint32_t>(gq);
 
@@ -374,17 +420,29 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
             const int ks = wv + kk * nwc;
             const uint8_t *slot = slots + static_cast<int>(j % NSLOT) * SLOT;
             // the unit's bytes -> registers, then its slot takes unit j + NSLOT
+            // (Q4_K: header, low and high code halves; Q6_K: both ql halves,
+            // qh, this lane's 8 scale bytes and d)
             u32x4 hdr[KB][RGN], qa[KB][RGN], qb[KB][RGN];
+            uint2 sc6[KB][RGN];
+            uint32_t d6[KB][RGN];
 #pragma unroll
             for (int b = 0; b < KB; b++)
 #pragma unroll
                 for (int rg = 0; rg < RGN; rg++) {
                     // rows past ROWS (a partial last group) read row ROWS - 1; discarded
                     const int rr = rg * 16 + c16 < ROWS ? rg * 16 + c16 : ROWS - 1;
-                    const uint8_t *rp = slot + rr * P + b * BB;
-                    hdr[b][rg] = *reinterpret_cast<const u32x4 *>(rp);
-                    qa[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 16 + 16 * gq);
-                    qb[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 80 + 16 * gq);
+                    const uint8_t *rp = slot + rr * PL + b * BL;
+                    if constexpr (Q6) {
+                        hdr[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 64 * h6 + 16 * lh6);        // ql, qd even
+                        qa[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 64 * h6 + 32 + 16 * lh6);    // ql, qd odd
+                        qb[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 128 + 32 * h6 + 16 * lh6);   // qh
+                        sc6[b][rg] = *reinterpret_cast<const uint2 *>(rp + 192 + 8 * h6);
+                        d6[b][rg] = *reinterpret_cast<const uint32_t *>(rp + 208);   // d in the high half
+                    } else {
+                        hdr[b][rg] = *reinterpret_cast<const u32x4 *>(rp);
+                        qa[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 16 + 16 * gq);
+                        qb[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 80 + 16 * gq);
+                    }
                 }
             __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
             if (j + NSLOT < my_units) issue(j + NSLOT, segl);
@@ -394,45 +452,80 @@ __global__ void __launch_bounds__(512) gemv_q4k_digits_kernel(SegTable t, int64_
                 if (KB > 1 && blk >= nb) break;
 #pragma unroll
                 for (int rg = 0; rg < RGN; rg++) {
-                    const u32x4 hd = hdr[b][rg], q0 = qa[b][rg], q1 = qb[b][rg];
-                    const v4i B0l = {static_cast<int>(q0.x & M), static_cast<int>(q0.y & M),
-                                     static_cast<int>(q0.z & M), static_cast<int>(q0.w & M)};
-                    const v4i B0h = {static_cast<int>((q0.x >> 4) & M), static_cast<int>((q0.y >> 4) & M),
-                                     static_cast<int>((q0.z >> 4) & M), static_cast<int>((q0.w >> 4) & M)};
-                    const v4i B1l = {static_cast<int>(q1.x & M), static_cast<int>(q1.y & M),
-                                     static_cast<int>(q1.z & M), static_cast<int>(q1.w & M)};
-                    const v4i B1h = {static_cast<int>((q1.x >> 4) & M), static_cast<int>((q1.y >> 4) & M),
-                                     static_cast<int>((q1.z >> 4) & M), static_cast<int>((q1.w >> 4) & M)};
-                    // scales of sub-blocks gq and 4 + gq (get_scale_min_k4,
-                    // src/quant.cpp:427-435): bytes gq of scales[0..3], [4..7], [8..11]
-                    const uint32_t s1 = hd.y >> bsh, s2 = hd.z >> bsh, s3 = hd.w >> bsh;
-                    const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
-                    const float sc0 = static_cast<float>(s1 & 63u), m0 = static_cast<float>(s2 & 63u);
-                    const float sc1 = static_cast<float>((s3 & 15u) | ((s1 >> 2) & 0x30u));
-                    const float m1 = static_cast<float>(((s3 >> 4) & 15u) | ((s2 >> 2) & 0x30u));
-                    const float ds0 = d * sc0, ds1 = d * sc1, dm0 = -dmin * m0, dm1 = -dmin * m1;
                     const v4i z = {0, 0, 0, 0};
+                    if constexpr (Q6) {
+                        // q = low 4 bits from ql | 2 high bits from qh (dequant_q6_K,
+                        // src/quant.cpp:462-512), codes 0..63 as int8; the code
+                        // offset 32 is applied through the 16-value sums of x
+                        const u32x4 l0 = hdr[b][rg], l1 = qa[b][rg], qh = qb[b][rg];
+                        const float d = h2f(d6[b][rg] >> 16);
 #pragma unroll
-                    for (int xr = 0; xr < NX; xr++) {
-                        // this activation row's digit table
-                        const uint8_t *alp = a_lo_p + (a_lo ? xr * tstride : 0) + blk * a_lo_inc;
-                        const uint8_t *ahp = a_hi_p + (a_hi ? xr * tstride : 0) + blk * a_hi_inc;
-                        const v4i A0l = ld_v4i(alp), A1l = ld_v4i(alp + 384);
-                        const v4i A0h = ld_v4i(ahp), A1h = ld_v4i(ahp + 384);
-                        // this lane's sub-blocks gq (h = 0) and 4 + gq (h = 1) of block blk
-                        const float2 ex0 = ex[xr * nsb + blk * 8 + gq], ex1 = ex[xr * nsb + blk * 8 + 4 + gq];
-                        v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0l, B0l, z, 0, 0, 0);
-                        C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0h, B0h, C0, 0, 0, 0);
-                        v4i C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1l, B1l, z, 0, 0, 0);
-                        C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1h, B1h, C1, 0, 0, 0);
-                        const int S0 = C0[0] + (C0[1] << 8) + (C0[2] << 16);
-                        const int S1 = C1[0] + (C1[1] << 8) + (C1[2] << 16);
-                        float a = acc[xr][rg];
-                        a = __builtin_fmaf(ds0, ex0.x * static_cast<float>(S0), a);
-                        a = __builtin_fmaf(dm0, ex0.y, a);
-                        a = __builtin_fmaf(ds1, ex1.x * static_cast<float>(S1), a);
-                        a = __builtin_fmaf(dm1, ex1.y, a);
-                        acc[xr][rg] = a;
+                        for (int qd = 0; qd < 4; qd++) {
+                            const u32x4 ql = (qd & 1) ? l1 : l0;
+                            const uint32_t ns = (qd >> 1) * 4u, hs = 2u * qd;
+                            const v4i B = {static_cast<int>(((ql.x >> ns) & M) | (((qh.x >> hs) & 0x03030303u) << 4)),
+                                           static_cast<int>(((ql.y >> ns) & M) | (((qh.y >> hs) & 0x03030303u) << 4)),
+                                           static_cast<int>(((ql.z >> ns) & M) | (((qh.z >> hs) & 0x03030303u) << 4)),
+                                           static_cast<int>(((ql.w >> ns) & M) | (((qh.w >> hs) & 0x03030303u) << 4))};
+                            // scale of sub-block 16 (8h + 2qd + lh): byte 2qd + lh of this lane's 8
+                            const int jj = 2 * qd + lh6;
+                            const uint32_t sw = jj < 4 ? sc6[b][rg].x : sc6[b][rg].y;
+                            const float ds = d * static_cast<float>(static_cast<int8_t>(sw >> (8 * (jj & 3))));
+#pragma unroll
+                            for (int xr = 0; xr < NX; xr++) {
+                                const uint8_t *ap6 = a6_p + (a6 ? xr * tstride : 0) + blk * a6_inc + qd * a6_qd;
+                                const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(ld_v4i(ap6), B, z, 0, 0, 0);
+                                const int sbi = xr * nsb + blk * 8 + 4 * h6 + qd;
+                                const float2 e2 = ex[sbi], h2 = ex16[sbi];
+                                // S = sum (q - 32) X over the 16 values: |S| <= 16 * 32 * 2^22
+                                // fits int32, so wrapping unsigned arithmetic gives it exactly
+                                const uint32_t xs = static_cast<uint32_t>(__float_as_int(lh6 ? h2.y : h2.x));
+                                const int S = static_cast<int>(static_cast<uint32_t>(C[0]) +
+                                                               (static_cast<uint32_t>(C[1]) << 8) +
+                                                               (static_cast<uint32_t>(C[2]) << 16) - 32u * xs);
+                                acc[xr][rg] = __builtin_fmaf(ds, e2.x * static_cast<float>(S), acc[xr][rg]);
+                            }
+                        }
+                    } else {
+                        const u32x4 hd = hdr[b][rg], q0 = qa[b][rg], q1 = qb[b][rg];
+                        const v4i B0l = {static_cast<int>(q0.x & M), static_cast<int>(q0.y & M),
+                                         static_cast<int>(q0.z & M), static_cast<int>(q0.w & M)};
+                        const v4i B0h = {static_cast<int>((q0.x >> 4) & M), static_cast<int>((q0.y >> 4) & M),
+                                         static_cast<int>((q0.z >> 4) & M), static_cast<int>((q0.w >> 4) & M)};
+                        const v4i B1l = {static_cast<int>(q1.x & M), static_cast<int>(q1.y & M),
+                                         static_cast<int>(q1.z & M), static_cast<int>(q1.w & M)};
+                        const v4i B1h = {static_cast<int>((q1.x >> 4) & M), static_cast<int>((q1.y >> 4) & M),
+                                         static_cast<int>((q1.z >> 4) & M), static_cast<int>((q1.w >> 4) & M)};
+                        // scales of sub-blocks gq and 4 + gq (get_scale_min_k4,
+                        // src/quant.cpp:427-435): bytes gq of scales[0..3], [4..7], [8..11]
+                        const uint32_t s1 = hd.y >> bsh, s2 = hd.z >> bsh, s3 = hd.w >> bsh;
+                        const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
+                        const float sc0 = static_cast<float>(s1 & 63u), m0 = static_cast<float>(s2 & 63u);
+                        const float sc1 = static_cast<float>((s3 & 15u) | ((s1 >> 2) & 0x30u));
+                        const float m1 = static_cast<float>(((s3 >> 4) & 15u) | ((s2 >> 2) & 0x30u));
+                        const float ds0 = d * sc0, ds1 = d * sc1, dm0 = -dmin * m0, dm1 = -dmin * m1;
+#pragma unroll
+                        for (int xr = 0; xr < NX; xr++) {
+                            // this activation row's digit table
+                            const uint8_t *alp = a_lo_p + (a_lo ? xr * tstride : 0) + blk * a_lo_inc;
+                            const uint8_t *ahp = a_hi_p + (a_hi ? xr * tstride : 0) + blk * a_hi_inc;
+                            const v4i A0l = ld_v4i(alp), A1l = ld_v4i(alp + 384);
+                            const v4i A0h = ld_v4i(ahp), A1h = ld_v4i(ahp + 384);
+                            // this lane's sub-blocks gq (h = 0) and 4 + gq (h = 1) of block blk
+                            const float2 ex0 = ex[xr * nsb + blk * 8 + gq], ex1 = ex[xr * nsb + blk * 8 + 4 + gq];
+                            v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0l, B0l, z, 0, 0, 0);
+                            C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0h, B0h, C0, 0, 0, 0);
+                            v4i C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1l, B1l, z, 0, 0, 0);
+                            C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1h, B1h, C1, 0, 0, 0);
+                            const int S0 = C0[0] + (C0[1] << 8) + (C0[2] << 16);
+                            const int S1 = C1[0] + (C1[1] << 8) + (C1[2] << 16);
+                            float a = acc[xr][rg];
+                            a = __builtin_fmaf(ds0, ex0.x * static_cast<float>(S0), a);
+                            a = __builtin_fmaf(dm0, ex0.y, a);
+                            a = __builtin_fmaf(ds1, ex1.x * static_cast<float>(S1), a);
+                            a = __builtin_fmaf(dm1, ex1.y, a);
+                            acc[xr][rg] = a;
+                        }
                     }
                 }
             }
@@ -501,16 +594,19 @@ constexpr size_t kLdsBudget = 160u * 1024u - sizeof(Seg) * kMaxSegs;   // dynami
 
 // LDS shared by the waves of a workgroup: NX digit tables with their scale
 // pairs, the zero area and the double-buffered reduction
-size_t fixed_lds(int nb, int rs, int nx) {
-    return static_cast<size_t>(nx) * nb * (kTabBlk + 8 * sizeof(float2)) + kZero +
+size_t fixed_lds(int nb, int rs, int nx, bool q6) {
+    return static_cast<size_t>(nx) * nb * (kTabBlk + (q6 ? 2 : 1) * 8 * sizeof(float2)) + kZero +
            2 * static_cast<size_t>(nx) * rs * kRedWaves * sizeof(float);
 }
-constexpr size_t slot_bytes(int rows) { return ((rows * 2 * 144 + 1023) / 1024) * 1024; }
+constexpr size_t slot_bytes(int rows, bool q6 = false) {
+    return ((rows * 2 * (q6 ? 224 : 144) + 1023) / 1024) * 1024;
+}
 
-template <typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT>
+template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT>
 hipError_t launch(SegTable t, hipStream_t st) {
+    constexpr bool Q6 = DT == DT_Q6_K;
     constexpr int RS = 16 * ((ROWS + 15) / 16);
-    constexpr int SLOT = ((ROWS * KB * 144 + 1023) / 1024) * 1024;
+    constexpr int SLOT = ((ROWS * KB * (Q6 ? 224 : 144) + 1023) / 1024) * 1024;
     int64_t total = 0;
     for (int i = 0; i < t.n; i++) {
         t.seg[i].blk_begin = total;
@@ -519,7 +615,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
     }
     const int nb = t.n_in / 256;
     const int nks = (nb + KB - 1) / KB;
-    const size_t fixed = fixed_lds(nb, RS, NX);
+    const size_t fixed = fixed_lds(nb, RS, NX, Q6);
     const size_t per_wave = static_cast<size_t>(NSLOT) * SLOT;
     // kXPasses sub-blocks per thread (4 threads each) must cover NX * nb * 8
     const int min_nw = (NX * nb * 8 * 4 + 64 * kXPasses - 1) / (64 * kXPasses);
@@ -535,7 +631,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
             if (l > kLdsBudget) break;
             int blocks = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &blocks, gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT>, 64 * cand, l) !=
+                    &blocks, gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT>, 64 * cand, l) !=
                 hipSuccess)
                 blocks = 0;
             if (blocks > 0 && blocks * cand >= best) { best = blocks * cand; nw = cand; per_cu = blocks; }
@@ -562,7 +658,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
     } else if (grid > total) {
         grid = total;
     }
-    hipLaunchKernelGGL((gemv_q4k_digits_kernel<XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT>),
+    hipLaunchKernelGGL((gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT>),
                        dim3(static_cast<unsigned>(grid)), dim3(64 * nw), fixed + nw * per_wave, st, t, total,
                        nks, nw);
     return hipGetLastError();
@@ -570,19 +666,20 @@ hipError_t launch(SegTable t, hipStream_t st) {
 
 template <typename XT, typename OT, bool DOWN, int NX, bool MT = false>
 hipError_t launch_rows(int rows, const SegTable &t, hipStream_t st) {
+    constexpr int DT = DT_Q4_K;
     if constexpr (NX == 1) {
         switch (rows) {
-            case 32: return launch<XT, OT, 32, 2, 2, DOWN, NX, MT>(t, st);
-            case 28: return launch<XT, OT, 28, 2, 2, DOWN, NX, MT>(t, st);
-            case 24: return launch<XT, OT, 24, 2, 2, DOWN, NX, MT>(t, st);
-            case 20: return launch<XT, OT, 20, 2, 2, DOWN, NX, MT>(t, st);
-            default: return launch<XT, OT, 16, 2, 2, DOWN, NX, MT>(t, st);
+            case 32: return launch<DT, XT, OT, 32, 2, 2, DOWN, NX, MT>(t, st);
+            case 28: return launch<DT, XT, OT, 28, 2, 2, DOWN, NX, MT>(t, st);
+            case 24: return launch<DT, XT, OT, 24, 2, 2, DOWN, NX, MT>(t, st);
+            case 20: return launch<DT, XT, OT, 20, 2, 2, DOWN, NX, MT>(t, st);
+            default: return launch<DT, XT, OT, 16, 2, 2, DOWN, NX, MT>(t, st);
         }
     } else {
         switch (rows) {
-            case 32: return launch<XT, OT, 32, 2, 2, DOWN, NX, MT>(t, st);
-            case 24: return launch<XT, OT, 24, 2, 2, DOWN, NX, MT>(t, st);
-            default: return launch<XT, OT, 16, 2, 2, DOWN, NX, MT>(t, st);
+            case 32: return launch<DT, XT, OT, 32, 2, 2, DOWN, NX, MT>(t, st);
+            case 24: return launch<DT, XT, OT, 24, 2, 2, DOWN, NX, MT>(t, st);
+            default: return launch<DT, XT, OT, 16, 2, 2, DOWN, NX, MT>(t, st);
         }
     }
 }
@@ -612,7 +709,7 @@ int pick_rows(const SegTable &t, int nx) {
     int best = 16;
     int64_t best_cost = INT64_MAX;
     for (int r = 32; r >= 16; r -= (nx == 1 ? 4 : 8)) {
-        if (fixed_lds(nb, 16 * ((r + 15) / 16), nx) + 8 * 2 * slot_bytes(r) > kLdsBudget) continue;
+        if (fixed_lds(nb, 16 * ((r + 15) / 16), nx, false) + 8 * 2 * slot_bytes(r) > kLdsBudget) continue;
         int64_t tiles = 0;
         for (int i = 0; i < t.n; i++) tiles += (t.seg[i].n_out + r - 1) / r;
         if (t.moe_tokens > 1) tiles *= t.moe_tokens;
@@ -625,25 +722,27 @@ int pick_rows(const SegTable &t, int nx) {
 // Activation rows per pass: the largest of 4, 2, 1 whose sub-blocks the x
 // staging covers (kXPasses sub-blocks per 4 threads, at most 8 waves) with
 // LDS left for the waves that staging needs (at least four) at 16-row slots
-int nx_cap(int n_in) {
+int nx_cap(int n_in, bool q6) {
     const int nb = n_in / 256;
     for (int nx = 4; nx > 1; nx >>= 1) {
         const int min_nw = (nx * nb * 8 * 4 + 64 * kXPasses - 1) / (64 * kXPasses);
         const int nw = min_nw < 4 ? 4 : min_nw;
-        if (nw <= 8 && fixed_lds(nb, 16, nx) + nw * 2 * slot_bytes(16) <= kLdsBudget) return nx;
+        if (nw <= 8 && fixed_lds(nb, 16, nx, q6) + nw * 2 * slot_bytes(16, q6) <= kLdsBudget) return nx;
     }
     return 1;
 }
 
 template <typename XT, typename OT, int NX>
-hipError_t dispatch_nx(const SegTable &t, hipStream_t st) {
+hipError_t dispatch_nx(int dt, const SegTable &t, hipStream_t st) {
+    // Q6_K: 16-row tiles (a 27-instruction unit of dword DMA), plain segments
+    if (dt == DT_Q6_K) return launch<DT_Q6_K, XT, OT, 16, 2, 2, false, NX, false>(t, st);
     const int rows = pick_rows(t, NX);
     if constexpr (sizeof(XT) == 4 && NX == 1) {
         if (t.moe_tab && t.moe_down)
             return t.moe_tokens > 1 ? launch_rows<XT, OT, true, 1, true>(rows, t, st)
                                     : launch_rows<XT, OT, true, 1, false>(rows, t, st);
         if (t.moe_tab && t.moe_tokens > 1)   // gate/up pairs: 32-row tiles
-            return launch<XT, OT, 32, 2, 2, false, 1, true>(t, st);
+            return launch<DT_Q4_K, XT, OT, 32, 2, 2, false, 1, true>(t, st);
     } else {
         // down mode and several tokens: f32 activations, one row
         if (t.moe_tab && (t.moe_down || t.moe_tokens > 1)) return hipErrorNotSupported;
@@ -653,9 +752,9 @@ hipError_t dispatch_nx(const SegTable &t, hipStream_t st) {
 
 // rows 2..8: passes of up to nx_cap activation rows, each reading W once
 template <typename XT, typename OT>
-hipError_t dispatch(const SegTable &t, hipStream_t st) {
-    if (t.rows == 1) return dispatch_nx<XT, OT, 1>(t, st);
-    const int cap = nx_cap(t.n_in);
+hipError_t dispatch(int dt, const SegTable &t, hipStream_t st) {
+    if (t.rows == 1) return dispatch_nx<XT, OT, 1>(dt, t, st);
+    const int cap = nx_cap(t.n_in, dt == DT_Q6_K);
     for (int64_t r0 = 0; r0 < t.rows; r0 += cap) {
         SegTable p = t;
         const int64_t c = t.rows - r0 < cap ? t.rows - r0 : cap;
@@ -664,9 +763,9 @@ hipError_t dispatch(const SegTable &t, hipStream_t st) {
             p.seg[i].x = static_cast<const XT *>(t.seg[i].x) + r0 * t.x_stride;
             p.seg[i].out = static_cast<OT *>(t.seg[i].out) + r0 * t.out_stride;
         }
-        const hipError_t e = c == 1 ? dispatch_nx<XT, OT, 1>(p, st)
-                           : c == 2 ? dispatch_nx<XT, OT, 2>(p, st)
-                                    : dispatch_nx<XT, OT, 4>(p, st);
+        const hipError_t e = c == 1 ? dispatch_nx<XT, OT, 1>(dt, p, st)
+                           : c == 2 ? dispatch_nx<XT, OT, 2>(dt, p, st)
+                                    : dispatch_nx<XT, OT, 4>(dt, p, st);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -675,8 +774,18 @@ hipError_t dispatch(const SegTable &t, hipStream_t st) {
 }  // namespace
 
 bool gemv_digits_ok(int dt, const SegTable &t) {
-    if (dt != DT_Q4_K || t.rows < 1 || t.rows > 8 || t.n_in % 256 || t.n_in > kMaxK || t.row_bytes % 16)
-        return false;
+    if (t.rows < 1 || t.rows > 8 || t.n_in > kMaxK) return false;
+    if (dt == DT_Q6_K) {
+        // two-block units (even block count), 4-byte aligned rows for the
+        // dword DMA, plain segments only
+        if (t.n_in % 512 || t.row_bytes % 4 || t.moe_tab) return false;
+        for (int i = 0; i < t.n; i++)
+            if (t.seg[i].x != t.seg[0].x || t.seg[i].kind == SEG_SILU ||
+                (reinterpret_cast<uintptr_t>(t.seg[i].w) & 3))
+                return false;
+        return true;
+    }
+    if (dt != DT_Q4_K || t.n_in % 256 || t.row_bytes % 16) return false;
     if (t.moe_tab && t.rows != 1) return false;
     if (t.moe_tab && t.moe_down &&
         (t.n != 1 || t.moe_k < 1 || t.moe_k > kMaxDownSlots || t.moe_kslot % 512 ||
@@ -691,8 +800,8 @@ bool gemv_digits_ok(int dt, const SegTable &t) {
     return true;
 }
 
-hipError_t gemv_digits(bool act_f16, const SegTable &t, hipStream_t st) {
-    return act_f16 ? dispatch<_Float16, _Float16>(t, st) : dispatch<float, float>(t, st);
+hipError_t gemv_digits(int dt, bool act_f16, const SegTable &t, hipStream_t st) {
+    return act_f16 ? dispatch<_Float16, _Float16>(dt, t, st) : dispatch<float, float>(dt, t, st);
 }
 
 }  // namespace krk

@@ -59,9 +59,9 @@ struct SegTable {
 };
 
 hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st);
-// Q4_K rows == 1 on the int8 MFMA (activations as exact int8 digit planes)
+// Q4_K / Q6_K rows 1..8 on the int8 MFMA (activations as exact int8 digit planes)
 bool gemv_digits_ok(int dt, const SegTable &t);
-hipError_t gemv_digits(bool act_f16, const SegTable &t, hipStream_t st);
+hipError_t gemv_digits(int dt, bool act_f16, const SegTable &t, hipStream_t st);
 
 // Bit-exact dequantization (the chunk contract) to f32 / f16 (RNE).
 hipError_t dequant_rows(int dt, const void *w, int64_t row_bytes, int64_t n_rows,

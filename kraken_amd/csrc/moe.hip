@@ -436,9 +436,9 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     const bool gu_ok = on_digits && gemv_digits_ok(DT_Q4_K, gu);
     const bool dn_ok = on_digits && gemv_digits_ok(DT_Q4_K, d);
     if (gu_ok && (dn_ok || a.n_tok == 1)) {
-        const hipError_t e = gemv_digits(false, gu, st);
+        const hipError_t e = gemv_digits(DT_Q4_K, false, gu, st);
         if (e != hipSuccess) return e;
-        if (dn_ok) return gemv_digits(false, d, st);
+        if (dn_ok) return gemv_digits(DT_Q4_K, false, d, st);
     }
     if (a.n_tok == 1) {
         const int64_t ggu = (a.n_ff + 3) / 4, gdn = (a.n_embd + 7) / 8;

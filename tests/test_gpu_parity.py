@@ -407,6 +407,40 @@ def test_q4_k_digits_extreme_sub_blocks(krk, torch_cuda, be32, n_in):
     assert rel(host(out)[0], O.gemm(O.Q4_K, w, x, n_out)[0]) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("rows,n_out,n_in", [(1, 300, 4096), (3, 520, 2048), (1, 64, 16384),
+                                          (8, 40, 512), (2, 130, 14336)])
+def test_q6_k_digits(krk, torch_cuda, be32, rows, n_out, n_in):
+    """Q6_K on the digit-plane kernel: two-block units packed by dword
+    LDS-DMA, one MFMA per 16-value scale group, the code offset 32 applied
+    through exact integer sums of the activation digits."""
+    torch = torch_cuda
+    w = make_weights(krk, O.Q6_K, n_out, n_in, seed=840 + rows)
+    x = krk.synth_normal(rows * n_in, seed=841 + rows).reshape(rows, n_in)
+    say("q6_k digits", rows, n_out, n_in)
+    out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    be32.gemm(out, dev(torch, x), dev(torch, w), O.Q6_K, n_out, n_in, rows)
+    be32.sync()
+    ref = O.gemm(O.Q6_K, w, x, n_out)
+    for r in range(rows):
+        assert rel(host(out)[r], ref[r]) <= GEMV_TOL, r
+
+
+def test_q6_k_digits_extreme_sub_blocks(krk, torch_cuda, be32, be16):
+    torch = torch_cuda
+    n_out, n_in = 96, 4096
+    w = make_weights(krk, O.Q6_K, n_out, n_in, seed=850)
+    x = digit_edge_x(n_in, seed=851)
+    out = torch.empty((1, n_out), dtype=torch.float32, device="cuda")
+    be32.gemm(out, dev(torch, x), dev(torch, w), O.Q6_K, n_out, n_in, 1)
+    be32.sync()
+    assert rel(host(out)[0], O.gemm(O.Q6_K, w, x, n_out)[0]) <= GEMV_TOL
+    xh = krk.synth_normal(n_in, seed=852).astype(np.float16)
+    out16 = torch.empty((1, n_out), dtype=torch.float16, device="cuda")
+    be16.gemm(out16, dev(torch, xh), dev(torch, w), O.Q6_K, n_out, n_in, 1)
+    be16.sync()
+    assert rel(host(out16).astype(np.float32), O.gemm(O.Q6_K, w, xh.astype(np.float32), n_out)) <= 6e-4
+
+
 # ------------------------------------------------- full-size configurations --
 def test_headline_q4_k_gemv_full_size(krk, torch_cuda, be32):
     """BASELINE config 2 headline shape: Q4_K 4096 -> 14336, M = 1."""
