@@ -73,22 +73,22 @@ template <> __device__ __forceinline__ void dma_lds<16>(const void *src, uint8_t
     __builtin_amdgcn_global_load_lds(src, (lds_void_t *)dst, 16, 0, 0);
 }
 
-template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT>
+template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT, bool RSPLIT>
 __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t total, int nks, int nwc) {
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr int BB = Q6 ? 210 : 144;           // block bytes
     constexpr int P = KB * BB;                   // row piece of one unit
     constexpr int RGN = (ROWS + 15) / 16;        // 16-row MFMA groups (the last may be partial)
     constexpr int RS = 16 * RGN;                 // reduction stride
-    // LDS unit layout: row r at r * PL.  Q4_K pieces are 16-byte multiples
-    // (dwordx4 LDS-DMA).  Q6_K blocks (210 bytes) go to a 224-byte stride so
-    // every LDS read is 16-byte aligned; with dword LDS-DMA each lane picks
-    // its own 4-byte source window inside its block, so no byte outside the
-    // matrix is ever read.
+    // LDS unit layout: row r at r * PL, delivered by dwordx4 LDS-DMA.  Q4_K
+    // pieces are 16-byte multiples.  Q6_K blocks (210 bytes) go to a 224-byte
+    // stride so every LDS read is 16-byte aligned: each lane picks its own
+    // 16-byte source window inside its block (sources are 2-byte aligned),
+    // so no byte outside the matrix is ever read.
     constexpr int BL = Q6 ? 224 : BB;            // LDS block stride
     constexpr int PL = KB * BL;                  // LDS row stride
     constexpr int U = ROWS * PL;
-    constexpr int DMA = Q6 ? 4 : 16;             // bytes per lane per LDS-DMA instruction
+    constexpr int DMA = 16;                      // bytes per lane per LDS-DMA instruction
     constexpr int CHB = 64 * DMA;                // bytes per instruction
     constexpr int CH = (U + CHB - 1) / CHB;
     constexpr int SLOT = ((U + 1023) / 1024) * 1024;
@@ -128,8 +128,13 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     const int nlb = multi ? t.moe_wpt : static_cast<int>(gridDim.x);
     const int tok = multi ? static_cast<int>(blockIdx.x) / nlb : 0;
     const int lb = multi ? static_cast<int>(blockIdx.x) - tok * nlb : static_cast<int>(blockIdx.x);
-    const int64_t my_tiles = lb < total ? (total - 1 - lb) / nlb + 1 : 0;
-    const int cnt = wv < nks ? (nks - 1 - wv) / nwc + 1 : 0;
+    // Row split (chosen when there are many tiles): each wave owns whole
+    // tiles (all K units), so no cross-wave reduction is needed.
+    constexpr bool rsplit = RSPLIT;
+    const int64_t wid = rsplit ? static_cast<int64_t>(lb) * nwc + wv : lb;
+    const int64_t wstride = rsplit ? static_cast<int64_t>(nlb) * nwc : nlb;
+    const int64_t my_tiles = wid < total ? (total - 1 - wid) / wstride + 1 : 0;
+    const int cnt = rsplit ? nks : (wv < nks ? (nks - 1 - wv) / nwc + 1 : 0);
     const int64_t my_units = my_tiles * cnt;
 
     const int nseg = t.n;
@@ -145,13 +150,12 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     // the next 16 rows of the same matrix, or for a gate/up (SiLU) segment
     // the same 16 rows of the up matrix.
     // source offset, inside the row piece, of LDS offset rem of a row.
-    // Q6_K: a block's last 4-byte window (LDS 208) takes bytes 206..209, so
-    // no lane reads past its block (d then sits at LDS 210); windows past it
-    // are padding and read the piece start
+    // Q6_K: windows 0..12 of a block are its bytes 0..207; window 13 (LDS
+    // 208..223) takes bytes 194..209, so d sits at LDS 222
     auto src_off = [](int rem) {
         if constexpr (Q6) {
             const int b = rem / BL, off = rem - b * BL;
-            return off <= BB - 2 ? b * BB + (off == BB - 2 ? off - 2 : off) : 0;
+            return b * BB + (off < BB - 2 ? off : BB - 16);
         } else {
             return rem;
         }
@@ -168,8 +172,8 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     // the first units read the segment table from the kernel arguments (the
     // LDS copy is not ready yet); later ones from LDS
     auto issue = [&](int64_t j, const Seg *tab_) {
-        const int64_t g = lb + (j / cnt) * nlb;
-        const int ks = wv + static_cast<int>(j % cnt) * nwc;
+        const int64_t g = wid + (j / cnt) * wstride;
+        const int ks = rsplit ? static_cast<int>(j % cnt) : wv + static_cast<int>(j % cnt) * nwc;
         const int si = seg_w(g, tab_);
         const bool pair = tab_[si].kind == SEG_SILU;
         const int tr = pair ? 16 : ROWS;               // output rows per tile
@@ -417,7 +421,7 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
             if (ahead >= NSLOT - 1) wait_vm<(NSLOT - 1) * CH>();
             else if (NSLOT > 2 && ahead == 1) wait_vm<CH>();
             else wait_vm<0>();
-            const int ks = wv + kk * nwc;
+            const int ks = rsplit ? kk : wv + kk * nwc;
             const uint8_t *slot = slots + static_cast<int>(j % NSLOT) * SLOT;
             // the unit's bytes -> registers, then its slot takes unit j + NSLOT
             // (Q4_K: header, low and high code halves; Q6_K: both ql halves,
@@ -437,7 +441,7 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
                         qa[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 64 * h6 + 32 + 16 * lh6);    // ql, qd odd
                         qb[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 128 + 32 * h6 + 16 * lh6);   // qh
                         sc6[b][rg] = *reinterpret_cast<const uint2 *>(rp + 192 + 8 * h6);
-                        d6[b][rg] = *reinterpret_cast<const uint32_t *>(rp + 208);   // d in the high half
+                        d6[b][rg] = *reinterpret_cast<const uint32_t *>(rp + 220);   // d in the high half
                     } else {
                         hdr[b][rg] = *reinterpret_cast<const u32x4 *>(rp);
                         qa[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 16 + 16 * gq);
@@ -530,9 +534,61 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
                 }
             }
         }
-        // partial sums of the compute waves -> LDS as [x row][row][wave], then
-        // one thread per (x row, row) reads its eight partials at once (two
-        // b128 reads) and adds them in wave order
+        // one output row: a gate/up pair (gs, us) or a plain dot (gs)
+        auto emit = [&](int si, int xr, int64_t n, float gs, float us) {
+            const int kind = segl[si].kind;
+            OT *o = static_cast<OT *>(segl[si].out) + static_cast<int64_t>(xr) * t.out_stride + n;
+            if (kind == SEG_SILU) {
+                if constexpr (sizeof(OT) == 2) {
+                    // fused_gate_silu_kernel (fused.hpp:161-166): both dots
+                    // rounded to f16, activation in f32, saturated
+                    const float hg = static_cast<float>(static_cast<_Float16>(gs));
+                    const float hu = static_cast<float>(static_cast<_Float16>(us));
+                    *o = sat_f16(silu_f(hg) * hu);
+                } else {
+                    *o = (gs / (1.0f + expf(-gs))) * us;   // silu_mul, backend_cpu.cpp:2401-2406
+                }
+            } else {
+                store_out<OT>(o, gs, kind, kind == SEG_ACC ? inv_acc : 1.0f);
+            }
+        };
+        const int64_t g = wid + ti * wstride;
+        if constexpr (RSPLIT) {
+            // the wave's own rows: sum over the four k groups, lanes of group
+            // 0 hold rows rg * 16 + c16 (gate/up pairs: rg 0 gate, rg 1 up)
+            float v[NX][RGN];
+#pragma unroll
+            for (int xr = 0; xr < NX; xr++)
+#pragma unroll
+                for (int rg = 0; rg < RGN; rg++) {
+                    v[xr][rg] = acc[xr][rg];
+                    v[xr][rg] += __shfl_xor(v[xr][rg], 16, 64);
+                    v[xr][rg] += __shfl_xor(v[xr][rg], 32, 64);
+                }
+            if (gq == 0) {
+                const int si = seg_w(g, segl);
+                const bool pair = segl[si].kind == SEG_SILU;
+#pragma unroll
+                for (int xr = 0; xr < NX; xr++) {
+                    if (xr >= t.rows) break;
+                    if (pair) {
+                        const int64_t n = (g - segl[si].blk_begin) * 16 + c16;
+                        if (n < segl[si].n_out) emit(si, xr, n, v[xr][0], RGN > 1 ? v[xr][RGN - 1] : 0.0f);
+                    } else {
+#pragma unroll
+                        for (int rg = 0; rg < RGN; rg++) {
+                            const int tr = rg * 16 + c16;
+                            const int64_t n = (g - segl[si].blk_begin) * ROWS + tr;
+                            if (tr < ROWS && n < segl[si].n_out) emit(si, xr, n, v[xr][rg], 0.0f);
+                        }
+                    }
+                }
+            }
+            continue;
+        }
+        // K split: partial sums of the waves -> LDS as [x row][row][wave],
+        // then one thread per (x row, row) reads its eight partials at once
+        // (two b128 reads) and adds them in wave order
         float *rbuf = red + (ti & 1) * NX * RS * kRedWaves;
 #pragma unroll
         for (int xr = 0; xr < NX; xr++)
@@ -557,34 +613,15 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
         if (threadIdx.x < NX * ROWS) {
             const int xr = NX > 1 ? static_cast<int>(threadIdx.x) / ROWS : 0;
             const int tr = static_cast<int>(threadIdx.x) - xr * ROWS;   // row within the tile
-            const int64_t g = lb + ti * nlb;
             const int si = seg_w(g, segl);
-            const int kind = segl[si].kind;
-            const int64_t ooff = static_cast<int64_t>(xr) * t.out_stride;
-            if (xr < t.rows && kind == SEG_SILU) {
+            if (xr < t.rows && segl[si].kind == SEG_SILU) {
                 // rows t and 16 + t of the tile are gate and up of output n0 + t
-                if (tr < 16) {
-                    const float gs = row_sum(xr * RS + tr), us = row_sum(xr * RS + 16 + tr);
-                    const int64_t n = (g - segl[si].blk_begin) * 16 + tr;
-                    if (n < segl[si].n_out) {
-                        OT *o = static_cast<OT *>(segl[si].out) + ooff + n;
-                        if constexpr (sizeof(OT) == 2) {
-                            // fused_gate_silu_kernel (fused.hpp:161-166): both
-                            // dots rounded to f16, activation in f32, saturated
-                            const float hg = static_cast<float>(static_cast<_Float16>(gs));
-                            const float hu = static_cast<float>(static_cast<_Float16>(us));
-                            *o = sat_f16(silu_f(hg) * hu);
-                        } else {
-                            *o = (gs / (1.0f + expf(-gs))) * us;   // silu_mul, backend_cpu.cpp:2401-2406
-                        }
-                    }
-                }
+                const int64_t n = (g - segl[si].blk_begin) * 16 + tr;
+                if (tr < 16 && n < segl[si].n_out)
+                    emit(si, xr, n, row_sum(xr * RS + tr), row_sum(xr * RS + 16 + tr));
             } else if (xr < t.rows) {
-                const float v = row_sum(xr * RS + tr);
                 const int64_t n = (g - segl[si].blk_begin) * ROWS + tr;
-                if (n < segl[si].n_out)
-                    store_out<OT>(static_cast<OT *>(segl[si].out) + ooff + n, v, kind,
-                                  kind == SEG_ACC ? inv_acc : 1.0f);
+                if (n < segl[si].n_out) emit(si, xr, n, row_sum(xr * RS + tr), 0.0f);
             }
         }
     }
@@ -602,7 +639,8 @@ constexpr size_t slot_bytes(int rows, bool q6 = false) {
     return ((rows * 2 * (q6 ? 224 : 144) + 1023) / 1024) * 1024;
 }
 
-template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT>
+template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT,
+          bool RSPLIT = false>
 hipError_t launch(SegTable t, hipStream_t st) {
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr int RS = 16 * ((ROWS + 15) / 16);
@@ -631,7 +669,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
             if (l > kLdsBudget) break;
             int blocks = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &blocks, gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT>, 64 * cand, l) !=
+                    &blocks, gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, RSPLIT>, 64 * cand, l) !=
                 hipSuccess)
                 blocks = 0;
             if (blocks > 0 && blocks * cand >= best) { best = blocks * cand; nw = cand; per_cu = blocks; }
@@ -648,6 +686,10 @@ hipError_t launch(SegTable t, hipStream_t st) {
             cus = 256;
     }
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
+    // row split when every wave of a full grid gets at least two tiles
+    if constexpr (!RSPLIT && NX == 1 && !DOWN && !MT) {
+        if (total >= 2 * grid * nw) return launch<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, true>(t, st);
+    }
     if (MT) {
         // a group of workgroups per token, the groups filling the chip together
         int64_t wpt = grid / t.moe_tokens;
@@ -658,7 +700,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
     } else if (grid > total) {
         grid = total;
     }
-    hipLaunchKernelGGL((gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT>),
+    hipLaunchKernelGGL((gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, RSPLIT>),
                        dim3(static_cast<unsigned>(grid)), dim3(64 * nw), fixed + nw * per_wave, st, t, total,
                        nks, nw);
     return hipGetLastError();

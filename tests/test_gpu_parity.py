@@ -441,6 +441,24 @@ def test_q6_k_digits_extreme_sub_blocks(krk, torch_cuda, be32, be16):
     assert rel(host(out16).astype(np.float32), O.gemm(O.Q6_K, w, xh.astype(np.float32), n_out)) <= 6e-4
 
 
+@pytest.mark.parametrize("dt,rows,n_out", [(O.Q4_K, 1, 70001), (O.Q4_K, 2, 70000), (O.Q6_K, 1, 66001),
+                                          (O.Q6_K, 3, 66000)])
+def test_digits_row_split(krk, torch_cuda, be32, dt, rows, n_out):
+    """Enough tiles that each wave owns whole tiles (no cross-wave
+    reduction), with a partial last tile."""
+    torch = torch_cuda
+    n_in = 512
+    w = make_weights(krk, dt, n_out, n_in, seed=860 + rows)
+    x = krk.synth_normal(rows * n_in, seed=861 + rows).reshape(rows, n_in)
+    say("row split", dt, rows, n_out, n_in)
+    out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    be32.gemm(out, dev(torch, x), dev(torch, w), dt, n_out, n_in, rows)
+    be32.sync()
+    ref = O.gemm(dt, w, x, n_out)
+    for r in range(rows):
+        assert rel(host(out)[r], ref[r]) <= GEMV_TOL, r
+
+
 # ------------------------------------------------- full-size configurations --
 def test_headline_q4_k_gemv_full_size(krk, torch_cuda, be32):
     """BASELINE config 2 headline shape: Q4_K 4096 -> 14336, M = 1."""
