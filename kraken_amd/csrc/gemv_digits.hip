@@ -76,7 +76,13 @@ template <> __device__ __forceinline__ void dma_lds<16>(const void *src, uint8_t
 template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT, bool RSPLIT>
 __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t total, int nks, int nwc) {
     constexpr bool Q6 = DT == DT_Q6_K;
-    constexpr int BB = Q6 ? 210 : 144;           // block bytes
+    // 32-value formats: 8 blocks per 256 values, each in an LDS slot of
+    // 16-byte windows taken inside the block (Q8_0: 34 -> 48 bytes, Q4_0:
+    // 18 -> 32), so the codes sit 16-byte aligned at slot offset 16
+    constexpr bool QS = DT == DT_Q8_0 || DT == DT_Q4_0;
+    constexpr bool Q8 = DT == DT_Q8_0;
+    constexpr int bb = Q8 ? 34 : 18, sbl = Q8 ? 48 : 32;   // QS block bytes, LDS slot
+    constexpr int BB = Q6 ? 210 : QS ? 8 * bb : 144;       // source bytes per 256 values
     constexpr int P = KB * BB;                   // row piece of one unit
     constexpr int RGN = (ROWS + 15) / 16;        // 16-row MFMA groups (the last may be partial)
     constexpr int RS = 16 * RGN;                 // reduction stride
@@ -85,7 +91,7 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     // stride so every LDS read is 16-byte aligned: each lane picks its own
     // 16-byte source window inside its block (sources are 2-byte aligned),
     // so no byte outside the matrix is ever read.
-    constexpr int BL = Q6 ? 224 : BB;            // LDS block stride
+    constexpr int BL = Q6 ? 224 : QS ? 8 * sbl : BB;   // LDS bytes per 256 values
     constexpr int PL = KB * BL;                  // LDS row stride
     constexpr int U = ROWS * PL;
     constexpr int DMA = 16;                      // bytes per lane per LDS-DMA instruction
@@ -93,7 +99,7 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     constexpr int CH = (U + CHB - 1) / CHB;
     constexpr int SLOT = ((U + 1023) / 1024) * 1024;
     static_assert(NSLOT * CH < 64, "vmcnt is 6 bits");
-    static_assert(!Q6 || (ROWS <= 16 && !DOWN && !MT), "Q6_K: 16-row tiles, plain segments");
+    static_assert(!(Q6 || QS) || (!DOWN && !MT), "Q6_K, Q8_0, Q4_0: plain segments");
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ Seg segl[kMaxSegs];
     // down mode uses segl[0] only; the bank and the weight of each slot live
@@ -109,7 +115,7 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     // Q6_K: exact integer sums of X over each 16-value half of a sub-block
     // (for the code offset 32), stored as int bits
     float2 *ex16 = ex + NX * nb * 8;                  // [NX][nb * 8] (Q6_K only)
-    uint8_t *slots0 = reinterpret_cast<uint8_t *>(ex + (Q6 ? 2 : 1) * NX * nb * 8);
+    uint8_t *slots0 = reinterpret_cast<uint8_t *>(ex + (Q6 || DT == DT_Q4_0 ? 2 : 1) * NX * nb * 8);
     float *red = reinterpret_cast<float *>(slots0 + nwc * (NSLOT * SLOT));  // [2][NX][RS][kRedWaves]
 
     // Every wave streams, multiplies and builds a share of the digit table.
@@ -152,10 +158,15 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     // source offset, inside the row piece, of LDS offset rem of a row.
     // Q6_K: windows 0..12 of a block are its bytes 0..207; window 13 (LDS
     // 208..223) takes bytes 194..209, so d sits at LDS 222
+    // QS: window 0 of a block is bytes 0..15 (d first), window 1 bytes
+    // 2..17 (codes 0..15), Q8_0's window 2 bytes 18..33 (codes 16..31)
     auto src_off = [](int rem) {
         if constexpr (Q6) {
             const int b = rem / BL, off = rem - b * BL;
             return b * BB + (off < BB - 2 ? off : BB - 16);
+        } else if constexpr (QS) {
+            const int b = rem / sbl, w = (rem - b * sbl) >> 4;
+            return b * bb + (w == 0 ? 0 : w == 1 ? 2 : 18);
         } else {
             return rem;
         }
@@ -368,7 +379,7 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
             // down mode: the slot weight scales the sub-block's activations
             const float ws = DOWN ? wl[sb / static_cast<int>(t.moe_kslot / 32)] : 1.0f;
             ex[xr * nsb + sb] = float2{(live ? dn : 1.0f) * ws, sum * ws};
-            if (Q6) ex16[xr * nsb + sb] = float2{__int_as_float(xsum), __int_as_float(xsum_hi)};
+            if (Q6 || DT == DT_Q4_0) ex16[xr * nsb + sb] = float2{__int_as_float(xsum), __int_as_float(xsum_hi)};
         }
     }
     if (!moe && threadIdx.x < nseg) segl[threadIdx.x] = t.seg[threadIdx.x];
@@ -405,6 +416,13 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     const bool a6 = ap < 3 && as == gq;
     const uint8_t *a6_p = a6 ? tab + 4 * h6 * 96 + ap * 32 + 16 * lh6 : zero;
     const int a6_inc = a6 ? kTabBlk : 0, a6_qd = a6 ? 96 : 0;
+    // QS: MFMA chunk m of 256 values takes blocks 2m, 2m + 1; lane group gq
+    // holds 16 codes of block 2m + (gq >> 1), half gq & 1; A row 4s' + p
+    // (s' = 0, 1) holds plane p of block 2m + s'; C rows 4gq + j of lanes
+    // gq < 2 are block 2m + gq's plane sums
+    const bool aq = ap < 3 && as == (gq >> 1);
+    const uint8_t *aq_p = aq ? tab + (gq >> 1) * 96 + ap * 32 + 16 * (gq & 1) : zero;
+    const int aq_inc = aq ? kTabBlk : 0, aq_m = aq ? 2 * 96 : 0;
     const uint32_t M = 0x0F0F0F0Fu;
     const uint32_t bsh = 8u * static_cast<uint32_t>(gq);
 
@@ -426,9 +444,10 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
             // the unit's bytes -> registers, then its slot takes unit j + NSLOT
             // (Q4_K: header, low and high code halves; Q6_K: both ql halves,
             // qh, this lane's 8 scale bytes and d)
-            u32x4 hdr[KB][RGN], qa[KB][RGN], qb[KB][RGN];
+            u32x4 hdr[KB][RGN], qa[KB][RGN], qb[KB][RGN], qc[KB][RGN];
             uint2 sc6[KB][RGN];
             uint32_t d6[KB][RGN];
+            u32x4 dq[KB][RGN];   // QS: d of block 2m + (gq & 1), m = 0..3
 #pragma unroll
             for (int b = 0; b < KB; b++)
 #pragma unroll
@@ -436,7 +455,19 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
                     // rows past ROWS (a partial last group) read row ROWS - 1; discarded
                     const int rr = rg * 16 + c16 < ROWS ? rg * 16 + c16 : ROWS - 1;
                     const uint8_t *rp = slot + rr * PL + b * BL;
-                    if constexpr (Q6) {
+                    if constexpr (QS) {
+                        // codes of block 2m + (gq >> 1): Q8_0 half gq & 1, Q4_0 all 16 bytes
+                        const int co = 16 + (Q8 ? 16 * (gq & 1) : 0);
+                        const uint8_t *bq = rp + (gq >> 1) * sbl + co, *bd = rp + (gq & 1) * sbl;
+                        hdr[b][rg] = *reinterpret_cast<const u32x4 *>(bq);
+                        qa[b][rg] = *reinterpret_cast<const u32x4 *>(bq + 2 * sbl);
+                        qb[b][rg] = *reinterpret_cast<const u32x4 *>(bq + 4 * sbl);
+                        qc[b][rg] = *reinterpret_cast<const u32x4 *>(bq + 6 * sbl);
+                        dq[b][rg] = u32x4{*reinterpret_cast<const uint32_t *>(bd),
+                                          *reinterpret_cast<const uint32_t *>(bd + 2 * sbl),
+                                          *reinterpret_cast<const uint32_t *>(bd + 4 * sbl),
+                                          *reinterpret_cast<const uint32_t *>(bd + 6 * sbl)};
+                    } else if constexpr (Q6) {
                         hdr[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 64 * h6 + 16 * lh6);        // ql, qd even
                         qa[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 64 * h6 + 32 + 16 * lh6);    // ql, qd odd
                         qb[b][rg] = *reinterpret_cast<const u32x4 *>(rp + 128 + 32 * h6 + 16 * lh6);   // qh
@@ -457,7 +488,51 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
 #pragma unroll
                 for (int rg = 0; rg < RGN; rg++) {
                     const v4i z = {0, 0, 0, 0};
-                    if constexpr (Q6) {
+                    if constexpr (QS) {
+                        // Q8_0: y = d * sum q x (dequant_q8_0, src/quant.cpp:381-387);
+                        // Q4_0: y = d * sum (q - 8) x (dequant_q4_0, quant.cpp:331-339),
+                        // the offset 8 applied through exact integer digit sums
+                        const uint32_t hsh = (gq & 1) ? 4u : 0u;
+#pragma unroll
+                        for (int m = 0; m < 4; m++) {
+                            const u32x4 qv = m == 0 ? hdr[b][rg] : m == 1 ? qa[b][rg] : m == 2 ? qb[b][rg] : qc[b][rg];
+                            v4i B;
+                            if constexpr (Q8) {
+                                B = v4i{static_cast<int>(qv.x), static_cast<int>(qv.y), static_cast<int>(qv.z),
+                                        static_cast<int>(qv.w)};
+                            } else {
+                                B = v4i{static_cast<int>((qv.x >> hsh) & M), static_cast<int>((qv.y >> hsh) & M),
+                                        static_cast<int>((qv.z >> hsh) & M), static_cast<int>((qv.w >> hsh) & M)};
+                            }
+                            const uint32_t dw = m == 0 ? dq[b][rg].x : m == 1 ? dq[b][rg].y : m == 2 ? dq[b][rg].z
+                                                                                                 : dq[b][rg].w;
+                            const float d = h2f(dw & 0xFFFFu);
+#pragma unroll
+                            for (int xr = 0; xr < NX; xr++) {
+                                const uint8_t *apq = aq_p + (aq ? xr * tstride : 0) + blk * aq_inc + m * aq_m;
+                                const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(ld_v4i(apq), B, z, 0, 0, 0);
+                                // lanes gq >= 2 hold empty C rows; they add nothing
+                                const int sbi = xr * nsb + blk * 8 + 2 * m + (gq & 1);
+                                float sv;
+                                if constexpr (Q8) {
+                                    // |sum q X| < 2^34: combine the exact plane sums in f32
+                                    sv = __builtin_fmaf(65536.0f, static_cast<float>(C[2]),
+                                                        __builtin_fmaf(256.0f, static_cast<float>(C[1]),
+                                                                       static_cast<float>(C[0])));
+                                } else {
+                                    // sum (q - 8) X over 32 values: |S| <= 2^30, exact in int32
+                                    const float2 h2 = ex16[sbi];
+                                    const uint32_t xs = static_cast<uint32_t>(__float_as_int(h2.x)) +
+                                                        static_cast<uint32_t>(__float_as_int(h2.y));
+                                    const int S = static_cast<int>(static_cast<uint32_t>(C[0]) +
+                                                                   (static_cast<uint32_t>(C[1]) << 8) +
+                                                                   (static_cast<uint32_t>(C[2]) << 16) - 8u * xs);
+                                    sv = static_cast<float>(S);
+                                }
+                                if (gq < 2) acc[xr][rg] = __builtin_fmaf(d, ex[sbi].x * sv, acc[xr][rg]);
+                            }
+                        }
+                    } else if constexpr (Q6) {
                         // q = low 4 bits from ql | 2 high bits from qh (dequant_q6_K,
                         // src/quant.cpp:462-512), codes 0..63 as int8; the code
                         // offset 32 is applied through the 16-value sums of x
@@ -635,8 +710,12 @@ size_t fixed_lds(int nb, int rs, int nx, bool q6) {
     return static_cast<size_t>(nx) * nb * (kTabBlk + (q6 ? 2 : 1) * 8 * sizeof(float2)) + kZero +
            2 * static_cast<size_t>(nx) * rs * kRedWaves * sizeof(float);
 }
-constexpr size_t slot_bytes(int rows, bool q6 = false) {
-    return ((rows * 2 * (q6 ? 224 : 144) + 1023) / 1024) * 1024;
+// LDS bytes of one 256-value row piece of a unit (see the kernel's layout)
+constexpr int lds_per_256(int dt) {
+    return dt == DT_Q6_K ? 224 : dt == DT_Q8_0 ? 384 : dt == DT_Q4_0 ? 256 : 144;
+}
+constexpr size_t slot_bytes(int rows, int dt = DT_Q4_K) {
+    return ((rows * 2 * lds_per_256(dt) + 1023) / 1024) * 1024;
 }
 
 template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT,
@@ -644,7 +723,7 @@ template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DO
 hipError_t launch(SegTable t, hipStream_t st) {
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr int RS = 16 * ((ROWS + 15) / 16);
-    constexpr int SLOT = ((ROWS * KB * (Q6 ? 224 : 144) + 1023) / 1024) * 1024;
+    constexpr int SLOT = ((ROWS * KB * lds_per_256(DT) + 1023) / 1024) * 1024;
     int64_t total = 0;
     for (int i = 0; i < t.n; i++) {
         t.seg[i].blk_begin = total;
@@ -653,7 +732,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
     }
     const int nb = t.n_in / 256;
     const int nks = (nb + KB - 1) / KB;
-    const size_t fixed = fixed_lds(nb, RS, NX, Q6);
+    const size_t fixed = fixed_lds(nb, RS, NX, Q6 || DT == DT_Q4_0);
     const size_t per_wave = static_cast<size_t>(NSLOT) * SLOT;
     // kXPasses sub-blocks per thread (4 threads each) must cover NX * nb * 8
     const int min_nw = (NX * nb * 8 * 4 + 64 * kXPasses - 1) / (64 * kXPasses);
@@ -764,20 +843,25 @@ int pick_rows(const SegTable &t, int nx) {
 // Activation rows per pass: the largest of 4, 2, 1 whose sub-blocks the x
 // staging covers (kXPasses sub-blocks per 4 threads, at most 8 waves) with
 // LDS left for the waves that staging needs (at least four) at 16-row slots
-int nx_cap(int n_in, bool q6) {
+int nx_cap(int n_in, int dt) {
     const int nb = n_in / 256;
     for (int nx = 4; nx > 1; nx >>= 1) {
         const int min_nw = (nx * nb * 8 * 4 + 64 * kXPasses - 1) / (64 * kXPasses);
         const int nw = min_nw < 4 ? 4 : min_nw;
-        if (nw <= 8 && fixed_lds(nb, 16, nx, q6) + nw * 2 * slot_bytes(16, q6) <= kLdsBudget) return nx;
+        if (nw <= 8 &&
+            fixed_lds(nb, 16, nx, dt == DT_Q6_K || dt == DT_Q4_0) + nw * 2 * slot_bytes(16, dt) <= kLdsBudget)
+            return nx;
     }
     return 1;
 }
 
 template <typename XT, typename OT, int NX>
 hipError_t dispatch_nx(int dt, const SegTable &t, hipStream_t st) {
-    // Q6_K: 16-row tiles (a 27-instruction unit of dword DMA), plain segments
+    // Q6_K, Q8_0, Q4_0: 16-row tiles (Q8_0's 384-byte LDS pieces one per
+    // unit, the others two), plain segments
     if (dt == DT_Q6_K) return launch<DT_Q6_K, XT, OT, 16, 2, 2, false, NX, false>(t, st);
+    if (dt == DT_Q8_0) return launch<DT_Q8_0, XT, OT, 16, 1, 2, false, NX, false>(t, st);
+    if (dt == DT_Q4_0) return launch<DT_Q4_0, XT, OT, 16, 2, 2, false, NX, false>(t, st);
     const int rows = pick_rows(t, NX);
     if constexpr (sizeof(XT) == 4 && NX == 1) {
         if (t.moe_tab && t.moe_down)
@@ -796,7 +880,7 @@ hipError_t dispatch_nx(int dt, const SegTable &t, hipStream_t st) {
 template <typename XT, typename OT>
 hipError_t dispatch(int dt, const SegTable &t, hipStream_t st) {
     if (t.rows == 1) return dispatch_nx<XT, OT, 1>(dt, t, st);
-    const int cap = nx_cap(t.n_in, dt == DT_Q6_K);
+    const int cap = nx_cap(t.n_in, dt);
     for (int64_t r0 = 0; r0 < t.rows; r0 += cap) {
         SegTable p = t;
         const int64_t c = t.rows - r0 < cap ? t.rows - r0 : cap;
@@ -817,10 +901,14 @@ hipError_t dispatch(int dt, const SegTable &t, hipStream_t st) {
 
 bool gemv_digits_ok(int dt, const SegTable &t) {
     if (t.rows < 1 || t.rows > 8 || t.n_in > kMaxK) return false;
-    if (dt == DT_Q6_K) {
-        // two-block units (even block count), 4-byte aligned rows for the
-        // dword DMA, plain segments only
-        if (t.n_in % 512 || t.row_bytes % 4 || t.moe_tab) return false;
+    if (dt == DT_Q6_K || dt == DT_Q8_0 || dt == DT_Q4_0) {
+        // whole units (Q8_0: 256 values, the others 512), plain segments only.
+        // Q8_0 and Q4_0 at one row stay on the VALU stream kernel, which
+        // measured faster there (their decode is cheap); from two rows on the
+        // digit planes share each weight unit and win
+        if ((dt != DT_Q6_K && t.rows < 2) || t.n_in % (dt == DT_Q8_0 ? 256 : 512) || t.row_bytes % 4 ||
+            t.moe_tab)
+            return false;
         for (int i = 0; i < t.n; i++)
             if (t.seg[i].x != t.seg[0].x || t.seg[i].kind == SEG_SILU ||
                 (reinterpret_cast<uintptr_t>(t.seg[i].w) & 3))

@@ -442,7 +442,7 @@ def test_q6_k_digits_extreme_sub_blocks(krk, torch_cuda, be32, be16):
 
 
 @pytest.mark.parametrize("dt,rows,n_out", [(O.Q4_K, 1, 70001), (O.Q4_K, 2, 70000), (O.Q6_K, 1, 66001),
-                                          (O.Q6_K, 3, 66000)])
+                                          (O.Q6_K, 3, 66000), (O.Q8_0, 2, 70003), (O.Q4_0, 2, 66002)])
 def test_digits_row_split(krk, torch_cuda, be32, dt, rows, n_out):
     """Enough tiles that each wave owns whole tiles (no cross-wave
     reduction), with a partial last tile."""
@@ -451,6 +451,26 @@ def test_digits_row_split(krk, torch_cuda, be32, dt, rows, n_out):
     w = make_weights(krk, dt, n_out, n_in, seed=860 + rows)
     x = krk.synth_normal(rows * n_in, seed=861 + rows).reshape(rows, n_in)
     say("row split", dt, rows, n_out, n_in)
+    out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    be32.gemm(out, dev(torch, x), dev(torch, w), dt, n_out, n_in, rows)
+    be32.sync()
+    ref = O.gemm(dt, w, x, n_out)
+    for r in range(rows):
+        assert rel(host(out)[r], ref[r]) <= GEMV_TOL, r
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("rows,n_out,n_in", [(2, 300, 4096), (4, 96, 1024), (3, 50, 16384)])
+def test_small_block_digits(krk, torch_cuda, be32, dt, rows, n_out, n_in):
+    """Q8_0 and Q4_0 with 2..8 rows on the digit-plane kernel: 32-value
+    blocks placed in 16-byte-aligned LDS slots, Q8_0 codes as the int8
+    operand, Q4_0 nibbles with the offset 8 applied through exact integer
+    digit sums; row 0 carries the extreme sub-blocks."""
+    torch = torch_cuda
+    w = make_weights(krk, dt, n_out, n_in, seed=870 + rows)
+    x = krk.synth_normal(rows * n_in, seed=871 + rows).reshape(rows, n_in)
+    x[0] = digit_edge_x(n_in, seed=872)
+    say("small-block digits", dt, rows, n_out, n_in)
     out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
     be32.gemm(out, dev(torch, x), dev(torch, w), dt, n_out, n_in, rows)
     be32.sync()
