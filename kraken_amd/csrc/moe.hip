@@ -366,6 +366,8 @@ __global__ void __launch_bounds__(512) moe_down1_kernel(const krk_moe_entry *__r
     }
 }
 
+constexpr int64_t kMoeTokenGroups = 64;
+
 hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t st) {
     const int64_t P = a.n_tok * a.k;
     if (ws_bytes < moe_workspace(a.n_tok, a.k, a.n_expert, a.n_embd, a.n_ff)) return hipErrorInvalidValue;
@@ -431,8 +433,12 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     d.moe_tokens = static_cast<int>(a.n_tok);
     d.moe_xtok = a.k * a.n_ff;
     d.moe_otok = a.n_embd;
+    // A token group reads its experts for itself, so an expert routed to
+    // several tokens is read several times: the path serves decode-sized
+    // batches (up to kMoeTokenGroups tokens); larger ones take the plan path,
+    // which reads each active expert once per pass of two tokens.
     const bool on_digits = !a.act_f16 && a.wt == DT_Q4_K && a.aligned16 && a.rb_gate == a.rb_up &&
-                           a.k <= kMaxSegs && a.n_tok <= (1 << 20) && a.k * a.n_ff <= (1 << 30);
+                           a.k <= kMaxSegs && a.n_tok <= kMoeTokenGroups && a.k * a.n_ff <= (1 << 30);
     const bool gu_ok = on_digits && gemv_digits_ok(DT_Q4_K, gu);
     const bool dn_ok = on_digits && gemv_digits_ok(DT_Q4_K, d);
     if (gu_ok && (dn_ok || a.n_tok == 1)) {
