@@ -426,7 +426,7 @@ def main():
                    "rows": 1, "activations": "f32", "weight_copies": g["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(), "kernel": "gemv_q4k_digits_kernel<float,float,28,2,2,false>",
+                     "traffic": read_traffic(), "kernel": "gemv_digits_kernel<Q4_K, float, float, 28, 2, 2, false, 1, false, false>",
                      "algorithmic_bytes_per_launch": g["bytes"]},
         "cpu_baseline": cpu and {k: v for k, v in cpu.items()},
         "extras": extras,
