@@ -140,6 +140,8 @@ class Backend:
         if st != 0:
             raise KrkError(f"krk_backend_create: {lib().krk_status_string(st).decode()}")
         self._h = h
+        # bound now: module globals may already be gone when __del__ runs at exit
+        self._destroy = lib().krk_backend_destroy
         self.device = device
         self.act = act
         self.set_stream(stream if stream is not None else torch.cuda.current_stream(device))
@@ -147,7 +149,7 @@ class Backend:
     # context
     def close(self):
         if getattr(self, "_h", None):
-            lib().krk_backend_destroy(self._h)
+            self._destroy(self._h)
             self._h = None
 
     __del__ = close

@@ -66,14 +66,12 @@ __device__ __forceinline__ v4i ld_v4i(const uint8_t *p) { return *reinterpret_ca
 
 // LDS-DMA of N bytes per lane (the builtin needs a literal size)
 template <int N> __device__ __forceinline__ void dma_lds(const void *src, uint8_t *dst);
-template <> __device__ __forceinline__ void dma_lds<4>(const void *src, uint8_t *dst) {
-    __builtin_amdgcn_global_load_lds(src, (lds_void_t *)dst, 4, 0, 0);
-}
 template <> __device__ __forceinline__ void dma_lds<16>(const void *src, uint8_t *dst) {
     __builtin_amdgcn_global_load_lds(src, (lds_void_t *)dst, 16, 0, 0);
 }
 
-template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT, bool RSPLIT>
+template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT, bool RSPLIT,
+          bool EM>
 __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t total, int nks, int nwc) {
     constexpr bool Q6 = DT == DT_Q6_K;
     // 32-value formats: 8 blocks per 256 values, each in an LDS slot of
@@ -99,7 +97,20 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     constexpr int CH = (U + CHB - 1) / CHB;
     constexpr int SLOT = ((U + 1023) / 1024) * 1024;
     static_assert(NSLOT * CH < 64, "vmcnt is 6 bits");
-    static_assert(!(Q6 || QS) || (!DOWN && !MT), "Q6_K, Q8_0, Q4_0: plain segments");
+    static_assert(!(Q6 || QS) || (!DOWN && !MT && !EM), "Q6_K, Q8_0, Q4_0: plain segments");
+    static_assert(!EM || (!DOWN && !MT && !RSPLIT), "expert items: one mode");
+    // expert-major item of this workgroup group; groups past the last item
+    // leave at once (before any barrier or LDS use)
+    int em_e = 0, em_rows = 0;
+    int64_t em_first = 0;
+    if constexpr (EM) {
+        const int item = static_cast<int>(blockIdx.x) / t.em_wpe;
+        if (item >= *t.em_n_items) return;
+        em_e = t.em_items[4 * item];
+        em_first = t.em_items[4 * item + 1];
+        em_rows = t.em_items[4 * item + 2];
+    }
+    const int64_t nrows = EM ? em_rows : t.rows;   // activation rows of this launch
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ Seg segl[kMaxSegs];
     // down mode uses segl[0] only; the bank and the weight of each slot live
@@ -130,18 +141,23 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     // A workgroup owns tiles of ROWS rows (tiles lb, lb + nlb, ...); its
     // waves split K: wave wv takes the units ks = wv, wv + nwc, ...  With
     // several routed tokens, workgroup group tok serves token tok.
-    constexpr bool multi = MT;   // several routed tokens
-    const int nlb = multi ? t.moe_wpt : static_cast<int>(gridDim.x);
+    constexpr bool multi = MT || EM;   // several routed tokens / expert items
+    const int nlb = MT ? t.moe_wpt : EM ? t.em_wpe : static_cast<int>(gridDim.x);
     const int tok = multi ? static_cast<int>(blockIdx.x) / nlb : 0;
     const int lb = multi ? static_cast<int>(blockIdx.x) - tok * nlb : static_cast<int>(blockIdx.x);
     // Row split (chosen when there are many tiles): each wave owns whole
     // tiles (all K units), so no cross-wave reduction is needed.
     constexpr bool rsplit = RSPLIT;
-    const int64_t wid = rsplit ? static_cast<int64_t>(lb) * nwc + wv : lb;
-    const int64_t wstride = rsplit ? static_cast<int64_t>(nlb) * nwc : nlb;
-    const int64_t my_tiles = wid < total ? (total - 1 - wid) / wstride + 1 : 0;
+    // tile and unit counts fit 31 bits (the launch checks total * nks), so
+    // the per-unit index arithmetic stays in 32-bit scalar registers
+    const int wid = rsplit ? lb * nwc + wv : lb;
+    const int wstride = rsplit ? nlb * nwc : nlb;
+    const int ntiles = static_cast<int>(total);
+    const int my_tiles =
+        wid < ntiles ? static_cast<int>(static_cast<uint32_t>(ntiles - 1 - wid) / static_cast<uint32_t>(wstride)) + 1
+                     : 0;
     const int cnt = rsplit ? nks : (wv < nks ? (nks - 1 - wv) / nwc + 1 : 0);
-    const int64_t my_units = my_tiles * cnt;
+    const int my_units = my_tiles * cnt;
 
     const int nseg = t.n;
     const int upk = DOWN ? static_cast<int>(t.moe_kslot / (KB * 256)) : 1;   // units per slot
@@ -182,9 +198,10 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     }
     // the first units read the segment table from the kernel arguments (the
     // LDS copy is not ready yet); later ones from LDS
-    auto issue = [&](int64_t j, const Seg *tab_) {
-        const int64_t g = wid + (j / cnt) * wstride;
-        const int ks = rsplit ? static_cast<int>(j % cnt) : wv + static_cast<int>(j % cnt) * nwc;
+    auto issue = [&](int j, const Seg *tab_) {
+        const int jt = static_cast<int>(static_cast<uint32_t>(j) / static_cast<uint32_t>(cnt)), jk = j - jt * cnt;
+        const int64_t g = wid + static_cast<int64_t>(jt) * wstride;
+        const int ks = rsplit ? jk : wv + jk * nwc;
         const int si = seg_w(g, tab_);
         const bool pair = tab_[si].kind == SEG_SILU;
         const int tr = pair ? 16 : ROWS;               // output rows per tile
@@ -226,8 +243,17 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     };
 
     // ---- x loads (four threads per 32-value sub-block, kXPasses passes over
-    // the NX rows' sub-blocks; rows past t.rows read as zero)
-    const XT *x = static_cast<const XT *>(t.seg[0].x) + (multi ? tok * t.moe_xtok : 0);
+    // the NX rows' sub-blocks; rows past nrows read as zero)
+    const XT *x = static_cast<const XT *>(t.seg[0].x) + (MT ? tok * t.moe_xtok : 0);
+    // activation row r of this launch (expert items gather their rows)
+    auto xrow_off = [&](int r) -> int64_t {
+        if constexpr (EM) {
+            const int64_t p = em_first + r;
+            return (t.em_tok ? static_cast<int64_t>(t.em_tok[p]) : p) * t.em_xrow;
+        } else {
+            return static_cast<int64_t>(r) * t.x_stride;
+        }
+    };
     const int q = threadIdx.x & 3;
     const int nsb = nb * 8;
     const int nxs = NX * nsb;
@@ -236,8 +262,8 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     for (int u = 0; u < kXPasses; u++) {
         const int f = (threadIdx.x >> 2) + u * (blockDim.x >> 2);
         const int xr = NX > 1 ? f / nsb : 0, sb = NX > 1 ? f - xr * nsb : f;
-        const bool xin = f < nxs && xr < t.rows;
-        const XT *xp = x + (xin ? static_cast<int64_t>(xr) * t.x_stride + sb * 32 : 0) + 8 * q;
+        const bool xin = f < nxs && xr < nrows;
+        const XT *xp = x + (xin ? xrow_off(xr) + sb * 32 : 0) + 8 * q;
         if (u * (blockDim.x >> 2) >= nxs) break;   // uniform
         if (NX > 1 && !xin) {
 #pragma unroll
@@ -256,7 +282,18 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     // ---- routed experts: resolve the segments on the device first (one
     // dependent read of the ids and the table entries per workgroup)
     const bool moe = t.moe_tab != nullptr;
-    if (DOWN) {
+    if (EM) {
+        if (threadIdx.x == 0) {
+            const krk_moe_entry &en = static_cast<const krk_moe_entry *>(t.moe_tab)[em_e];
+            Seg sg = t.seg[0];
+            const bool pair = sg.kind == SEG_SILU;
+            sg.w = en.p[pair ? KRK_MOE_GATE : KRK_MOE_DOWN];
+            sg.w2 = pair ? en.p[KRK_MOE_UP] : nullptr;
+            sg.out = static_cast<float *>(sg.out) + em_first * t.em_orow;
+            segl[0] = sg;
+        }
+        __syncthreads();
+    } else if (DOWN) {
         if (threadIdx.x < t.moe_k) {
             const krk_moe_entry *mt = static_cast<const krk_moe_entry *>(t.moe_tab);
             const int64_t pi = static_cast<int64_t>(tok) * t.moe_k + threadIdx.x;
@@ -305,7 +342,7 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     // table meanwhile.
     const int late = kLateWaves < nwc / 2 ? kLateWaves : nwc / 2;
     const bool early = wv < nwc - late;
-    const int first = my_units < NSLOT ? static_cast<int>(my_units) : NSLOT;
+    const int first = my_units < NSLOT ? my_units : NSLOT;
     if (early) {
         if (moe) {
 #pragma unroll
@@ -426,8 +463,8 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     const uint32_t M = 0x0F0F0F0Fu;
     const uint32_t bsh = 8u * static_cast<uint32_t>(gq);
 
-    int64_t j = 0;
-    for (int64_t ti = 0; ti < my_tiles; ti++) {
+    int j = 0;
+    for (int ti = 0; ti < my_tiles; ti++) {
         float acc[NX][RGN];
 #pragma unroll
         for (int xr = 0; xr < NX; xr++)
@@ -435,7 +472,7 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
             for (int r = 0; r < RGN; r++) acc[xr][r] = 0.0f;
         for (int kk = 0; kk < cnt; kk++, j++) {
             // units j + 1 .. j + NSLOT - 1 may still be in flight
-            const int64_t ahead = my_units - 1 - j;
+            const int ahead = my_units - 1 - j;
             if (ahead >= NSLOT - 1) wait_vm<(NSLOT - 1) * CH>();
             else if (NSLOT > 2 && ahead == 1) wait_vm<CH>();
             else wait_vm<0>();
@@ -627,7 +664,7 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
                 store_out<OT>(o, gs, kind, kind == SEG_ACC ? inv_acc : 1.0f);
             }
         };
-        const int64_t g = wid + ti * wstride;
+        const int64_t g = wid + static_cast<int64_t>(ti) * wstride;
         if constexpr (RSPLIT) {
             // the wave's own rows: sum over the four k groups, lanes of group
             // 0 hold rows rg * 16 + c16 (gate/up pairs: rg 0 gate, rg 1 up)
@@ -645,7 +682,7 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
                 const bool pair = segl[si].kind == SEG_SILU;
 #pragma unroll
                 for (int xr = 0; xr < NX; xr++) {
-                    if (xr >= t.rows) break;
+                    if (xr >= nrows) break;
                     if (pair) {
                         const int64_t n = (g - segl[si].blk_begin) * 16 + c16;
                         if (n < segl[si].n_out) emit(si, xr, n, v[xr][0], RGN > 1 ? v[xr][RGN - 1] : 0.0f);
@@ -689,12 +726,12 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
             const int xr = NX > 1 ? static_cast<int>(threadIdx.x) / ROWS : 0;
             const int tr = static_cast<int>(threadIdx.x) - xr * ROWS;   // row within the tile
             const int si = seg_w(g, segl);
-            if (xr < t.rows && segl[si].kind == SEG_SILU) {
+            if (xr < nrows && segl[si].kind == SEG_SILU) {
                 // rows t and 16 + t of the tile are gate and up of output n0 + t
                 const int64_t n = (g - segl[si].blk_begin) * 16 + tr;
                 if (tr < 16 && n < segl[si].n_out)
                     emit(si, xr, n, row_sum(xr * RS + tr), row_sum(xr * RS + 16 + tr));
-            } else if (xr < t.rows) {
+            } else if (xr < nrows) {
                 const int64_t n = (g - segl[si].blk_begin) * ROWS + tr;
                 if (n < segl[si].n_out) emit(si, xr, n, row_sum(xr * RS + tr), 0.0f);
             }
@@ -719,7 +756,7 @@ constexpr size_t slot_bytes(int rows, int dt = DT_Q4_K) {
 }
 
 template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT,
-          bool RSPLIT = false>
+          bool RSPLIT = false, bool EM = false>
 hipError_t launch(SegTable t, hipStream_t st) {
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr int RS = 16 * ((ROWS + 15) / 16);
@@ -732,6 +769,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
     }
     const int nb = t.n_in / 256;
     const int nks = (nb + KB - 1) / KB;
+    if (total * nks >= (int64_t{1} << 31)) return hipErrorNotSupported;   // 32-bit unit indices
     const size_t fixed = fixed_lds(nb, RS, NX, Q6 || DT == DT_Q4_0);
     const size_t per_wave = static_cast<size_t>(NSLOT) * SLOT;
     // kXPasses sub-blocks per thread (4 threads each) must cover NX * nb * 8
@@ -748,7 +786,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
             if (l > kLdsBudget) break;
             int blocks = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &blocks, gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, RSPLIT>, 64 * cand, l) !=
+                    &blocks, gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, RSPLIT, EM>, 64 * cand, l) !=
                 hipSuccess)
                 blocks = 0;
             if (blocks > 0 && blocks * cand >= best) { best = blocks * cand; nw = cand; per_cu = blocks; }
@@ -766,10 +804,19 @@ hipError_t launch(SegTable t, hipStream_t st) {
     }
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
     // row split when every wave of a full grid gets at least two tiles
-    if constexpr (!RSPLIT && NX == 1 && !DOWN && !MT) {
+    if constexpr (!RSPLIT && NX == 1 && !DOWN && !MT && !EM) {
         if (total >= 2 * grid * nw) return launch<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, true>(t, st);
     }
-    if (MT) {
+    if (EM) {
+        // a group of workgroups per expert item; about three workgroups per
+        // CU over the items a call can have, so the groups of the items that
+        // exist fill the chip (the others leave at once)
+        int64_t wpe = (grid * 3 + t.em_max_items - 1) / t.em_max_items;
+        if (wpe > total) wpe = total;
+        if (wpe < 1) wpe = 1;
+        t.em_wpe = static_cast<int>(wpe);
+        grid = wpe * t.em_max_items;
+    } else if (MT) {
         // a group of workgroups per token, the groups filling the chip together
         int64_t wpt = grid / t.moe_tokens;
         if (wpt > total) wpt = total;
@@ -779,7 +826,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
     } else if (grid > total) {
         grid = total;
     }
-    hipLaunchKernelGGL((gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, RSPLIT>),
+    hipLaunchKernelGGL((gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, RSPLIT, EM>),
                        dim3(static_cast<unsigned>(grid)), dim3(64 * nw), fixed + nw * per_wave, st, t, total,
                        nks, nw);
     return hipGetLastError();
@@ -879,6 +926,16 @@ hipError_t dispatch_nx(int dt, const SegTable &t, hipStream_t st) {
 // rows 2..8: passes of up to nx_cap activation rows, each reading W once
 template <typename XT, typename OT>
 hipError_t dispatch(int dt, const SegTable &t, hipStream_t st) {
+    if (t.em_items) {
+        // expert items of up to t.rows (2) activation rows: gate/up pairs or down
+        if constexpr (sizeof(XT) == 4) {
+            if (t.rows != 2) return hipErrorNotSupported;
+            return t.seg[0].kind == SEG_SILU ? launch<DT_Q4_K, XT, OT, 32, 2, 2, false, 2, false, false, true>(t, st)
+                                             : launch<DT_Q4_K, XT, OT, 16, 2, 2, false, 2, false, false, true>(t, st);
+        } else {
+            return hipErrorNotSupported;   // f32 activations
+        }
+    }
     if (t.rows == 1) return dispatch_nx<XT, OT, 1>(dt, t, st);
     const int cap = nx_cap(t.n_in, dt);
     for (int64_t r0 = 0; r0 < t.rows; r0 += cap) {
@@ -916,6 +973,11 @@ bool gemv_digits_ok(int dt, const SegTable &t) {
         return true;
     }
     if (dt != DT_Q4_K || t.n_in % 256 || t.row_bytes % 16) return false;
+    if (t.em_items) {
+        // expert items: one segment, f32 rows of up to 2, Q4_K banks
+        return t.n == 1 && t.rows == 2 && !t.moe_down && t.em_max_items > 0 && t.em_xrow % 4 == 0 &&
+               (t.seg[0].kind == SEG_PLAIN || (t.seg[0].kind == SEG_SILU && t.n_in <= 8192));
+    }
     if (t.moe_tab && t.rows != 1) return false;
     if (t.moe_tab && t.moe_down &&
         (t.n != 1 || t.moe_k < 1 || t.moe_k > kMaxDownSlots || t.moe_kslot % 512 ||

@@ -33,6 +33,8 @@ struct MoeWs {
     int32_t *plan_pos;  // [P]            plan position of pair t*k+s (-1: dropped)
     float *mid;         // [P, n_ff]
     float *part;        // [P, n_embd]
+    int32_t *items;     // [P][4]         {expert, first plan position, rows <= kItemRows, 0}
+    int32_t *n_items;   // [1]
 };
 
 static size_t al(size_t v) { return (v + 255) & ~size_t(255); }
@@ -46,14 +48,16 @@ static MoeWs carve(void *ws, int64_t P, int ne, int64_t n_embd, int64_t n_ff) {
     w.plan_tok = reinterpret_cast<int32_t *>(p); p += al(P * 4);
     w.plan_pos = reinterpret_cast<int32_t *>(p); p += al(P * 4);
     w.mid = reinterpret_cast<float *>(p); p += al(P * n_ff * 4);
-    w.part = reinterpret_cast<float *>(p);
+    w.part = reinterpret_cast<float *>(p); p += al(P * n_embd * 4);
+    w.items = reinterpret_cast<int32_t *>(p); p += al(P * 16);
+    w.n_items = reinterpret_cast<int32_t *>(p);
     return w;
 }
 
 size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t n_ff) {
     const int64_t P = n_tok * k;
     return al((n_expert + 1) * 4) + al(n_expert * 4) + al(4) + 2 * al(P * 4) +
-           al(P * n_ff * 4) + al(P * n_embd * 4);
+           al(P * n_ff * 4) + al(P * n_embd * 4) + al(P * 16) + al(4);
 }
 
 // ------------------------------------------------------------------ plan ----
@@ -62,12 +66,13 @@ size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t
 // takes a per-expert atomic cursor.  The expert offsets and the active list
 // come from a block-wide exclusive scan (4 experts per thread).
 constexpr int kPlanLds = 4096;  // (token, slot) pairs whose ids the plan keeps in LDS
+constexpr int kItemRows = 2;    // activation rows of an expert item (the digit kernel's NX)
 __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict__ ids, int64_t P,
                                                         int k, int ne, MoeWs w) {
     __shared__ int32_t cnt[1024];
     __shared__ int32_t cur[1024];
     __shared__ int32_t sid[kPlanLds];   // the ids, when they fit
-    __shared__ int32_t wsum[2][4];      // per-wave totals: pairs, active experts
+    __shared__ int32_t wsum[3][4];      // per-wave totals: pairs, active experts, items
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const bool in_lds = P <= kPlanLds;
     for (int e = tid; e < ne; e += blockDim.x) cnt[e] = 0;
@@ -81,23 +86,26 @@ __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict
     }
     __syncthreads();
     // exclusive scan over experts 4 tid .. 4 tid + 3 (ne <= 1024)
-    int c[4], run = 0, act = 0;
+    // items: each active expert's pairs in runs of up to kItemRows (the rows
+    // one digit-plane pass multiplies against the expert's weights)
+    int c[4], run = 0, act = 0, its = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int e = 4 * tid + j;
         c[j] = e < ne ? cnt[e] : 0;
         run += c[j];
         act += c[j] > 0;
+        its += (c[j] + kItemRows - 1) / kItemRows;
     }
-    int ir = run, ia = act;   // inclusive wave scans
+    int ir = run, ia = act, ii = its;   // inclusive wave scans
     for (int d = 1; d < 64; d <<= 1) {
-        const int orr = __shfl_up(ir, d, 64), oa = __shfl_up(ia, d, 64);
-        if (lane >= d) { ir += orr; ia += oa; }
+        const int orr = __shfl_up(ir, d, 64), oa = __shfl_up(ia, d, 64), oi = __shfl_up(ii, d, 64);
+        if (lane >= d) { ir += orr; ia += oa; ii += oi; }
     }
-    if (lane == 63) { wsum[0][wv] = ir; wsum[1][wv] = ia; }
+    if (lane == 63) { wsum[0][wv] = ir; wsum[1][wv] = ia; wsum[2][wv] = ii; }
     __syncthreads();
-    int base = ir - run, abase = ia - act;
-    for (int v = 0; v < wv; v++) { base += wsum[0][v]; abase += wsum[1][v]; }
+    int base = ir - run, abase = ia - act, ibase = ii - its;
+    for (int v = 0; v < wv; v++) { base += wsum[0][v]; abase += wsum[1][v]; ibase += wsum[2][v]; }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int e = 4 * tid + j;
@@ -105,12 +113,20 @@ __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict
             w.off[e] = base;
             cur[e] = base;
             if (c[j]) w.act[abase++] = e;
+            for (int r = 0; r < c[j]; r += kItemRows) {
+                int32_t *it = w.items + 4 * ibase++;
+                it[0] = e;
+                it[1] = base + r;
+                it[2] = c[j] - r < kItemRows ? c[j] - r : kItemRows;
+                it[3] = 0;
+            }
         }
         base += c[j];
     }
     if (tid == blockDim.x - 1) {
         w.off[ne] = base;   // the last thread's running total is the grand total
         w.n_act[0] = abase;
+        w.n_items[0] = ibase;
     }
     __syncthreads();
     for (int64_t i = tid; i < P; i += blockDim.x) {
@@ -237,24 +253,35 @@ __global__ void __launch_bounds__(256) moe_reduce_kernel(const int32_t *__restri
                                                          const float *__restrict__ wts, int k,
                                                          int64_t n_embd, MoeWs w,
                                                          OT *__restrict__ out) {
+    // this token's live pairs in ascending expert id (insertion sort by one
+    // thread, k <= 64), then every thread adds its column in that order
+    __shared__ int32_t ord_pos[64];
+    __shared__ float ord_w[64];
+    __shared__ int nlive;
     const int64_t t = blockIdx.y;
+    if (threadIdx.x == 0) {
+        int ord[64];
+        int n = 0;
+        for (int s = 0; s < k; s++) {
+            if (w.plan_pos[t * k + s] < 0) continue;
+            const int e = ids[t * k + s];
+            int q = n++;
+            while (q > 0 && ids[t * k + ord[q - 1]] > e) { ord[q] = ord[q - 1]; q--; }
+            ord[q] = s;
+        }
+        for (int q = 0; q < n; q++) {
+            ord_pos[q] = w.plan_pos[t * k + ord[q]];
+            ord_w[q] = wts[t * k + ord[q]];
+        }
+        nlive = n;
+    }
+    __syncthreads();
     const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (j >= n_embd) return;
-    // this token's pairs in ascending expert id (insertion sort, k <= 64)
-    int ord[64];
-    int n = 0;
-    for (int s = 0; s < k; s++) {
-        if (w.plan_pos[t * k + s] < 0) continue;
-        const int e = ids[t * k + s];
-        int q = n++;
-        while (q > 0 && ids[t * k + ord[q - 1]] > e) { ord[q] = ord[q - 1]; q--; }
-        ord[q] = s;
-    }
+    const int n = nlive;
     float acc = 0.0f;
-    for (int q = 0; q < n; q++) {
-        const int s = ord[q];
-        acc = __builtin_fmaf(wts[t * k + s], w.part[static_cast<int64_t>(w.plan_pos[t * k + s]) * n_embd + j], acc);
-    }
+    for (int q = 0; q < n; q++)
+        acc = __builtin_fmaf(ord_w[q], w.part[static_cast<int64_t>(ord_pos[q]) * n_embd + j], acc);
     out[t * n_embd + j] = static_cast<OT>(acc);
 }
 
@@ -434,13 +461,58 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     d.moe_xtok = a.k * a.n_ff;
     d.moe_otok = a.n_embd;
     // A token group reads its experts for itself, so an expert routed to
-    // several tokens is read several times: the path serves decode-sized
-    // batches (up to kMoeTokenGroups tokens); larger ones take the plan path,
-    // which reads each active expert once per pass of two tokens.
+    // several tokens is read several times: token groups serve decode-sized
+    // batches (up to kMoeTokenGroups tokens). Larger Q4_K batches take
+    // expert-major items, which read each active expert once per item of
+    // kItemRows tokens; what the digit kernel cannot take goes to the plan path.
     const bool on_digits = !a.act_f16 && a.wt == DT_Q4_K && a.aligned16 && a.rb_gate == a.rb_up &&
-                           a.k <= kMaxSegs && a.n_tok <= kMoeTokenGroups && a.k * a.n_ff <= (1 << 30);
-    const bool gu_ok = on_digits && gemv_digits_ok(DT_Q4_K, gu);
-    const bool dn_ok = on_digits && gemv_digits_ok(DT_Q4_K, d);
+                           a.k <= kMaxSegs && a.k * a.n_ff <= (1 << 30);
+    const bool groups = on_digits && a.n_tok <= kMoeTokenGroups;
+    const bool gu_ok = groups && gemv_digits_ok(DT_Q4_K, gu);
+    const bool dn_ok = groups && gemv_digits_ok(DT_Q4_K, d);
+    if (on_digits && a.n_tok > kMoeTokenGroups) {
+        // expert-major items, each expert's weights read once per run of up
+        // to kItemRows of its tokens; then the ordered per-token reduce
+        SegTable eg{};
+        eg.n = 1;
+        eg.n_in = static_cast<int>(a.n_embd);
+        eg.row_bytes = a.rb_gate;
+        eg.rows = kItemRows;
+        eg.out_stride = a.n_ff;
+        eg.seg[0].x = a.xn;
+        eg.seg[0].out = w.mid;
+        eg.seg[0].n_out = a.n_ff;
+        eg.seg[0].kind = SEG_SILU;
+        eg.moe_tab = tab;
+        eg.moe_ne = a.n_expert;
+        eg.em_items = w.items;
+        eg.em_n_items = w.n_items;
+        eg.em_tok = w.plan_tok;
+        eg.em_max_items = static_cast<int>(P);
+        eg.em_xrow = a.n_embd;
+        eg.em_orow = a.n_ff;
+        SegTable ed = eg;
+        ed.n_in = static_cast<int>(a.n_ff);
+        ed.row_bytes = a.rb_down;
+        ed.out_stride = a.n_embd;
+        ed.seg[0].x = w.mid;
+        ed.seg[0].out = w.part;
+        ed.seg[0].n_out = a.n_embd;
+        ed.seg[0].kind = SEG_PLAIN;
+        ed.em_tok = nullptr;
+        ed.em_xrow = a.n_ff;
+        ed.em_orow = a.n_embd;
+        if (P <= (1 << 20) && gemv_digits_ok(DT_Q4_K, eg) && gemv_digits_ok(DT_Q4_K, ed)) {
+            hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w);
+            hipError_t e = gemv_digits(DT_Q4_K, false, eg, st);
+            if (e == hipSuccess) e = gemv_digits(DT_Q4_K, false, ed, st);
+            if (e != hipSuccess) return e;
+            const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));
+            hipLaunchKernelGGL((moe_reduce_kernel<float>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
+                               a.n_embd, w, static_cast<float *>(a.out));
+            return hipGetLastError();
+        }
+    }
     if (gu_ok && (dn_ok || a.n_tok == 1)) {
         const hipError_t e = gemv_digits(DT_Q4_K, false, gu, st);
         if (e != hipSuccess) return e;
