@@ -789,7 +789,11 @@ hipError_t launch(SegTable t, hipStream_t st) {
                     &blocks, gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, RSPLIT, EM>, 64 * cand, l) !=
                 hipSuccess)
                 blocks = 0;
-            if (blocks > 0 && blocks * cand >= best) { best = blocks * cand; nw = cand; per_cu = blocks; }
+            // waves doing useful work per CU: with K split over the waves a
+            // tile lasts ceil(nks / waves) units (seven waves over eight
+            // units run at 8/14); with the row split every wave owns tiles
+            const int score = RSPLIT ? 64 * blocks * cand : 64 * blocks * nks / ((nks + cand - 1) / cand);
+            if (blocks > 0 && score >= best) { best = score; nw = cand; per_cu = blocks; }
         }
         if (!nw) return hipErrorNotSupported;
         for (Pick &c : cache)
