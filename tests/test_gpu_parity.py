@@ -579,3 +579,34 @@ def test_moe_dispatch_graph_replay(krk, torch_cuda, be32):
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(host(out).view(np.uint32), want.view(np.uint32)), rep
+
+
+def test_error_paths_write_nothing(krk, torch_cuda, be32):
+    """Arguments the reference aborts on (a K that is not whole blocks,
+    backend_hip.hip:3186-3191; geometry moe_dispatch cannot express,
+    2500-2524) come back here as status codes, before any launch: the output
+    keeps its sentinel and the backend stays usable for the next call."""
+    torch = torch_cuda
+    n_out, n_in = 64, 4096
+    w = dev(torch, make_weights(krk, O.Q4_K, n_out, n_in, seed=990))
+    x = dev(torch, krk.synth_normal(2 * n_in, seed=991))
+    out = torch.full((2, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    cases = [
+        ("not whole blocks", lambda: be32.gemm(out, x, w, O.Q4_0, n_out, 100, 1), "shape"),
+        ("type not served", lambda: be32.gemm(out, x, w, 3, n_out, n_in, 1), "type"),
+        ("zero rows", lambda: be32.gemm(out, x, w, O.Q4_K, n_out, n_in, 0), "argument"),
+        ("zero outputs", lambda: be32.gemm(out, x, w, O.Q4_K, 0, n_in, 1), "argument"),
+        ("x under-aligned", lambda: be32.gemm(out, x[1:], w, O.Q4_K, n_out, n_in, 1), "argument"),
+        ("w under-aligned", lambda: be32.gemm(out, x, w[1:], O.Q4_K, n_out, n_in, 1), "argument"),
+        ("k above n_expert", lambda: be32.router_topk(out, 1, 4, 8, out, out), "argument"),
+    ]
+    for name, call, word in cases:
+        say("error path", name)
+        with pytest.raises(krk.KrkError, match=f"(?i){word}"):
+            call()
+    be32.sync()
+    assert torch.isnan(out).all()
+    be32.gemm(out, x, w, O.Q4_K, n_out, n_in, 2)
+    be32.sync()
+    ref = O.gemm(O.Q4_K, host(w), host(x).reshape(2, n_in), n_out)
+    assert rel(host(out), ref) <= GEMV_TOL
