@@ -27,14 +27,17 @@
 extern "C" {
 #endif
 
-/* GGUF type ids; only these four block formats (plus F16/F32 activations)
- * are on this path.  include/krk/quant.hpp:16-34. */
+/* GGUF type ids; these block formats (plus F16/F32 activations) are on
+ * this path.  include/krk/quant.hpp:16-34.  Q5_K is served by the dequant,
+ * GEMV (rows 1..8, exact prefill) and MFMA GEMM paths; moe_dispatch banks
+ * and the int8 rung take the other four (and Q8_0) only. */
 enum krk_dtype {
     KRK_DT_F32 = 0,
     KRK_DT_F16 = 1,
     KRK_DT_Q4_0 = 2,
     KRK_DT_Q8_0 = 8,
     KRK_DT_Q4_K = 12,
+    KRK_DT_Q5_K = 13,
     KRK_DT_Q6_K = 14
 };
 

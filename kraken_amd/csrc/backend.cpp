@@ -57,7 +57,8 @@ int hip_fail(krk_backend *b, hipError_t e, const char *what) {
 }
 
 bool dtype_on_path(int wt) {
-    return wt == KRK_DT_Q4_0 || wt == KRK_DT_Q8_0 || wt == KRK_DT_Q4_K || wt == KRK_DT_Q6_K;
+    return wt == KRK_DT_Q4_0 || wt == KRK_DT_Q8_0 || wt == KRK_DT_Q4_K || wt == KRK_DT_Q5_K ||
+           wt == KRK_DT_Q6_K;
 }
 
 int make_current(krk_backend *b) {
@@ -102,7 +103,7 @@ int check_mm(krk_backend *b, const void *out, const void *x, const void *w, int 
                     (long long)n_in, krk_dtype_block_size(wt));
     if (n_in > (int64_t(1) << 30)) return fail(b, KRK_ERR_SHAPE, "n_in=%lld too large", (long long)n_in);
     const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
-    if ((wt == KRK_DT_Q4_K && (wa & 15)) || (wa & 1))
+    if (((wt == KRK_DT_Q4_K || wt == KRK_DT_Q5_K) && (wa & 15)) || (wa & 1))
         return fail(b, KRK_ERR_ARG, "weight pointer %p under-aligned for type %d", w, wt);
     if (reinterpret_cast<uintptr_t>(x) & 15)
         return fail(b, KRK_ERR_ARG, "activation pointer %p is not 16-byte aligned", x);
@@ -150,7 +151,7 @@ int krk_dtype_block_size(int wt) {
     switch (wt) {
         case KRK_DT_F32: case KRK_DT_F16: return 1;
         case KRK_DT_Q4_0: case KRK_DT_Q8_0: return 32;
-        case KRK_DT_Q4_K: case KRK_DT_Q6_K: return 256;
+        case KRK_DT_Q4_K: case KRK_DT_Q5_K: case KRK_DT_Q6_K: return 256;
         default: return 0;
     }
 }
@@ -162,6 +163,7 @@ int krk_dtype_block_bytes(int wt) {
         case KRK_DT_Q4_0: return 18;
         case KRK_DT_Q8_0: return 34;
         case KRK_DT_Q4_K: return 144;
+        case KRK_DT_Q5_K: return 176;
         case KRK_DT_Q6_K: return 210;
         default: return 0;
     }
@@ -380,7 +382,8 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
         e0 = b->moe_ok[hit].e0;
         aligned = b->moe_ok[hit].aligned;
     } else {
-        // every bank of the layer: present, on this path, one weight type,
+        // every bank of the layer: present, of a type the expert kernels
+        // take (the path's formats but Q5_K), one weight type,
         // the layer's geometry; and whether all rows start 16-byte aligned
         std::vector<krk_moe_entry> ents(static_cast<size_t>(n_expert));
         hipError_t he = hipMemcpyAsync(ents.data(), tab + static_cast<int64_t>(layer) * n_expert,
@@ -392,7 +395,7 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
         for (int e = 0; e < n_expert; e++) {
             const krk_moe_entry &en = ents[static_cast<size_t>(e)];
             for (int m = 0; m < 3; m++) {
-                if (!en.present[m] || !dtype_on_path(en.type[m]))
+                if (!en.present[m] || !dtype_on_path(en.type[m]) || en.type[m] == KRK_DT_Q5_K)
                     return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: expert %d matrix %d absent or of type %d",
                                 e, m, en.type[m]);
                 if (en.type[m] != e0.type[0])

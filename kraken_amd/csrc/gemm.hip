@@ -144,6 +144,39 @@ template <> struct WStage<DT_Q6_K> {
     }
 };
 
+// Q5_K: Q4_K's staging plus the 16 high-bit bytes qh[16 hf .. +16) of the
+// same positions; chunk c takes bit c of each as bit 4 of its code
+// (quant.cpp:462-489).
+template <> struct WStage<DT_Q5_K> {
+    uint32_t hdr[4], q[4], h[4];
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        const int blk = kt >> 3, c = kt & 7;
+        const uint8_t *b = row + blk * 176;
+        const u32x4 hv = ld128(b);
+        hdr[0] = hv.x; hdr[1] = hv.y; hdr[2] = hv.z; hdr[3] = hv.w;
+        const u32x4 qv = ld128(b + 48 + 32 * (c >> 1) + 16 * hf);
+        q[0] = qv.x; q[1] = qv.y; q[2] = qv.z; q[3] = qv.w;
+        const u32x4 bv = ld128(b + 16 + 16 * hf);
+        h[0] = bv.x; h[1] = bv.y; h[2] = bv.z; h[3] = bv.w;
+    }
+    __device__ void decode(int kt, _Float16 (&o)[16]) const {
+        const int c = kt & 7;
+        const float d = h2f(hdr[0] & 0xFFFF), dmin = h2f(hdr[0] >> 16);
+        uint32_t sa, sb, ma, mb;
+        q4k_pair_scale_bytes(hdr, c >> 1, sa, sb, ma, mb);
+        const bool odd = c & 1;
+        const float d1 = d * static_cast<float>(odd ? sb : sa), m1 = dmin * static_cast<float>(odd ? mb : ma);
+        const int sh = odd ? 4 : 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t qv = ((q[t] >> (8 * k + sh)) & 0xFu) | (((h[t] >> (8 * k + c)) & 1u) << 4);
+                o[4 * t + k] = static_cast<_Float16>(__builtin_fmaf(d1, static_cast<float>(qv), -m1));
+            }
+    }
+};
+
 template <> struct WStage<DT_Q8_0> {
     uint32_t q[4], dw;
     __device__ void fetch(const uint8_t *row, int kt, int hf) {
@@ -479,6 +512,7 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
                                                      ws_bytes, st);
     switch (dt) {
         KRK_GEMM_CASE(DT_Q4_K)
+        KRK_GEMM_CASE(DT_Q5_K)
         KRK_GEMM_CASE(DT_Q6_K)
         KRK_GEMM_CASE(DT_Q8_0)
         KRK_GEMM_CASE(DT_Q4_0)

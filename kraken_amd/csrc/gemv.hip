@@ -412,6 +412,10 @@ template <> struct XRuns<DT_Q4_K> {
     // lane base 64*jp within the block; dword t: low run 4t, high run 32 + 4t
     __device__ static int base(int lane) { return 256 * (lane >> 2) + 64 * (lane & 3); }
 };
+template <> struct XRuns<DT_Q5_K> {
+    // Q4_K's value order: lane base 64*jp; dword t: low run 4t, high run 32 + 4t
+    __device__ static int base(int lane) { return 256 * (lane >> 2) + 64 * (lane & 3); }
+};
 template <> struct XRuns<DT_Q6_K> {
     __device__ static int base(int lane) {
         const int jp = lane & 3;
@@ -455,6 +459,32 @@ template <int RB> struct LdsDot<DT_Q4_K, RB> {
             const float xl4[4] = {lo.x, lo.y, lo.z, lo.w}, xh4[4] = {hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
             for (int r = 0; r < RB; r++) nib8(raw[r][4 + t], xl4, xh4, acc[r][t & 1], acc[r][2 + (t & 1)]);
+        }
+#pragma unroll
+        for (int r = 0; r < RB; r++) v[r] = F::finish(raw[r], jp, acc[r], xs);
+    }
+};
+
+template <int RB> struct LdsDot<DT_Q5_K, RB> {
+    using F = WaveFmt<DT_Q5_K>;
+    static constexpr int NS = 2;  // x sums per lane
+    __device__ static void sums(const float *xl, int b0, float (&xs)[NS]) {
+        LdsDot<DT_Q4_K, RB>::sums(xl, b0, xs);
+    }
+    __device__ static void run(const uint32_t (&raw)[RB][F::NRAW], int jp, const float *xl, int b0,
+                               const float (&xs)[NS], float (&v)[RB]) {
+        float acc[RB][4];
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) acc[r][q] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const floatx4 lo = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 4 * t));
+            const floatx4 hi = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 + 4 * t));
+            const float xl4[4] = {lo.x, lo.y, lo.z, lo.w}, xh4[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+            for (int r = 0; r < RB; r++) F::accum(raw[r], t, jp, xl4, xh4, acc[r]);
         }
 #pragma unroll
         for (int r = 0; r < RB; r++) v[r] = F::finish(raw[r], jp, acc[r], xs);
@@ -1122,6 +1152,7 @@ template <typename XT, typename OT>
 static hipError_t dispatch_dt(int dt, const SegTable &t, hipStream_t st) {
     switch (dt) {
         case DT_Q4_K: return dispatch_mr<DT_Q4_K, XT, OT>(t, st);
+        case DT_Q5_K: return dispatch_mr<DT_Q5_K, XT, OT>(t, st);
         case DT_Q6_K: return dispatch_mr<DT_Q6_K, XT, OT>(t, st);
         case DT_Q4_0: return dispatch_mr<DT_Q4_0, XT, OT>(t, st);
         case DT_Q8_0: return dispatch_mr<DT_Q8_0, XT, OT>(t, st);

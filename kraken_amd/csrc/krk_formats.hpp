@@ -20,10 +20,10 @@ namespace krk {
 
 // ---------------------------------------------------------------- geometry --
 __host__ __device__ constexpr int blk_vals(int dt) {
-    return dt == DT_Q4_K || dt == DT_Q6_K ? 256 : (dt == DT_Q4_0 || dt == DT_Q8_0) ? 32 : 1;
+    return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K ? 256 : (dt == DT_Q4_0 || dt == DT_Q8_0) ? 32 : 1;
 }
 __host__ __device__ constexpr int blk_bytes(int dt) {
-    return dt == DT_Q4_K ? 144 : dt == DT_Q6_K ? 210 : dt == DT_Q4_0 ? 18
+    return dt == DT_Q4_K ? 144 : dt == DT_Q5_K ? 176 : dt == DT_Q6_K ? 210 : dt == DT_Q4_0 ? 18
          : dt == DT_Q8_0 ? 34 : dt == DT_F16 ? 2 : 4;
 }
 
@@ -77,6 +77,23 @@ __device__ __forceinline__ void dequant_chunk<DT_Q4_K>(const uint8_t *b, int c, 
     const int sh = (c & 1) * 4;
     for (int l = 0; l < 32; l++)
         y[l] = __builtin_fmaf(d1, static_cast<float>((q[l] >> sh) & 0xF), -m1);
+}
+
+// src/quant.cpp:462-489: Q4_K's layout with 32 high-bit bytes at 16 and the
+// codes at 48; chunk c takes bit c of qh[l] as bit 4 of its code.  d1*q is
+// exact (17 + 5 significant bits), so the FMA matches either host form.
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_Q5_K>(const uint8_t *b, int c, float *y) {
+    const float d = ldh(b), dmin = ldh(b + 2);
+    int si, mi;
+    scale_min_k4(c, b + 4, si, mi);
+    const float d1 = d * static_cast<float>(si), m1 = dmin * static_cast<float>(mi);
+    const uint8_t *qh = b + 16, *q = b + 48 + 32 * (c >> 1);
+    const int sh = (c & 1) * 4;
+    for (int l = 0; l < 32; l++) {
+        const int code = ((q[l] >> sh) & 0xF) | (((qh[l] >> c) & 1) << 4);
+        y[l] = __builtin_fmaf(d1, static_cast<float>(code), -m1);
+    }
 }
 
 // src/quant.cpp:491-512: chunk c = quadrant (c & 3) of half (c >> 2).
@@ -150,6 +167,20 @@ __device__ __forceinline__ void nib8(uint32_t v, const float *xl, const float *x
 
 constexpr float kTwo24 = 16777216.0f, kTwo20 = 1048576.0f;
 
+// The 6-bit (scale, min) bytes of sub-blocks 2j and 2j+1 from a K-quant
+// header held as dwords raw[1..3] (get_scale_min_k4, quant.cpp:427-435).
+__device__ __forceinline__ void q4k_pair_scale_bytes(const uint32_t *raw, int j, uint32_t &sa, uint32_t &sb,
+                                                     uint32_t &ma, uint32_t &mb) {
+    const uint32_t sh = 16u * static_cast<uint32_t>(j & 1);
+    const uint32_t Y = raw[1] >> sh, Z = raw[2] >> sh, W = raw[3] >> sh;
+    const bool hi = j >= 2;
+    const uint32_t A = hi ? W : Y, Am = hi ? (W >> 4) : Z, s2 = hi ? 2u : 0u;
+    sa = (A & 15u) | ((Y >> s2) & 0x30u);
+    sb = ((A >> 8) & 15u) | ((Y >> (8u + s2)) & 0x30u);
+    ma = (Am & 15u) | ((Z >> s2) & 0x30u);
+    mb = ((Am >> 8) & 15u) | ((Z >> (8u + s2)) & 0x30u);
+}
+
 template <int DT> struct LaneFmt;
 
 // Q4_K: piece p covers qs bytes [16p, 16p+16): sub-block 2j low nibbles
@@ -185,6 +216,49 @@ template <> struct LaneFmt<DT_Q4_K> {
         const float dl = d * static_cast<float>(sa), dh = d * static_cast<float>(sb);
         float a = (dl * kTwo24) * sl;
         a = __builtin_fmaf(dh * kTwo20, shi, a);
+        a = __builtin_fmaf(-dmin * static_cast<float>(ma), xs[0], a);
+        return __builtin_fmaf(-dmin * static_cast<float>(mb), xs[1], a);
+    }
+};
+
+// Five-bit codes of a dword of code bytes A and high-bit bytes H: the nibble
+// at bit NS of each byte of A, plus bit HB of each byte of H as bit 4,
+// summed against x as f16 subnormals (c * 2^-24) like nib8.
+__device__ __forceinline__ float q5x4(uint32_t A, uint32_t H, int ns, int hb, const float *x, float acc) {
+    const uint32_t q = ((A >> ns) & 0x0F0F0F0Fu) | (((H >> hb) << 4) & 0x10101010u);
+    acc = mix2(q & 0x001F001Fu, x[0], x[2], acc);
+    return mix2((q >> 8) & 0x001F001Fu, x[1], x[3], acc);
+}
+
+// Q5_K: piece p covers qs bytes [16p, 16p+16) (at block offset 48) and the
+// same 16 positions l of qh: sub-block 2j low nibbles + qh bit 2j (values
+// 64j + 16(p&1) + i), sub-block 2j+1 high nibbles + qh bit 2j+1, j = p/2.
+template <> struct LaneFmt<DT_Q5_K> {
+    static constexpr int LPB = 8, NG = 2, RUN = 16, NRUN = 2, NRAW = 12;
+    __device__ static int run_start(int p, int r) { return 64 * (p >> 1) + 32 * r + 16 * (p & 1); }
+    __device__ static int group_of(int i) { return i >> 4; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int p) {
+        const u32x4 h = ld128(blk);
+        const u32x4 hb = ld128(blk + 16 + 16 * (p & 1));
+        const u32x4 q = ld128(blk + 48 + 16 * p);
+        raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+        raw[4] = q.x; raw[5] = q.y; raw[6] = q.z; raw[7] = q.w;
+        raw[8] = hb.x; raw[9] = hb.y; raw[10] = hb.z; raw[11] = hb.w;
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int p, const float (&xv)[32],
+                                const float (&xs)[NG]) {
+        const float d = h2f(raw[0] & 0xFFFF), dmin = h2f(raw[0] >> 16);
+        const int j = p >> 1;
+        uint32_t sa, sb, ma, mb;
+        q4k_pair_scale_bytes(raw, j, sa, sb, ma, mb);
+        float sl = 0.0f, shi = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            sl = q5x4(raw[4 + t], raw[8 + t], 0, 2 * j, &xv[4 * t], sl);
+            shi = q5x4(raw[4 + t], raw[8 + t], 4, 2 * j + 1, &xv[16 + 4 * t], shi);
+        }
+        float a = (d * static_cast<float>(sa) * kTwo24) * sl;
+        a = __builtin_fmaf(d * static_cast<float>(sb) * kTwo24, shi, a);
         a = __builtin_fmaf(-dmin * static_cast<float>(ma), xs[0], a);
         return __builtin_fmaf(-dmin * static_cast<float>(mb), xs[1], a);
     }
@@ -357,6 +431,55 @@ template <> struct WaveFmt<DT_Q4_K> {
         float acc[NACC] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < NDW; t++) accum(raw, t, xv, acc);
+        return finish(raw, jp, acc, xs);
+    }
+};
+
+template <> struct WaveFmt<DT_Q5_K> {
+    // lane slot jp = lane % 4 of block lane / 4: qs bytes [32jp, 32jp+32)
+    // (block offset 48) and all 32 qh bytes, bits 2jp (low nibbles,
+    // sub-block 2jp, values 64jp + 0..31) and 2jp+1 (high nibbles, values
+    // 64jp + 32..63)
+    static constexpr int LPB = 4, BPS = 16, NG = 2, RUN = 64, NRUN = 1, NRAW = 20;
+    __device__ static int blk_of(int lane) { return lane >> 2; }
+    __device__ static int slot_of(int lane) { return lane & 3; }
+    __device__ static int run_start(int jp, int) { return 64 * jp; }
+    __device__ static int group_of(int i) { return i >> 5; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int jp) {
+        const u32x4 h = ld128(blk);
+        const u32x4 h0 = ld128(blk + 16), h1 = ld128(blk + 32);
+        const u32x4 a = ld128(blk + 48 + 32 * jp);
+        const u32x4 b = ld128(blk + 64 + 32 * jp);
+        raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
+        raw[4] = a.x; raw[5] = a.y; raw[6] = a.z; raw[7] = a.w;
+        raw[8] = b.x; raw[9] = b.y; raw[10] = b.z; raw[11] = b.w;
+        raw[12] = h0.x; raw[13] = h0.y; raw[14] = h0.z; raw[15] = h0.w;
+        raw[16] = h1.x; raw[17] = h1.y; raw[18] = h1.z; raw[19] = h1.w;
+    }
+    // acc[0..1] low-nibble codes (even / odd dwords), acc[2..3] high
+    static constexpr int NACC = 4;
+    __device__ static void accum(const uint32_t (&raw)[NRAW], int t, int jp, const float *xl, const float *xh,
+                                 float (&acc)[NACC]) {
+        const int e = t & 1;
+        acc[e] = q5x4(raw[4 + t], raw[12 + t], 0, 2 * jp, xl, acc[e]);
+        acc[2 + e] = q5x4(raw[4 + t], raw[12 + t], 4, 2 * jp + 1, xh, acc[2 + e]);
+    }
+    static constexpr int NDW = 8;  // dwords of codes per lane
+    __device__ static float finish(const uint32_t (&raw)[NRAW], int jp, const float (&acc)[NACC],
+                                   const float (&xs)[NG]) {
+        const float d = h2f(raw[0] & 0xFFFF), dmin = h2f(raw[0] >> 16);
+        uint32_t sa, sb, ma, mb;
+        q4k_pair_scale_bytes(raw, jp, sa, sb, ma, mb);
+        float a = (d * static_cast<float>(sa) * kTwo24) * (acc[0] + acc[1]);
+        a = __builtin_fmaf(d * static_cast<float>(sb) * kTwo24, acc[2] + acc[3], a);
+        a = __builtin_fmaf(-dmin * static_cast<float>(ma), xs[0], a);
+        return __builtin_fmaf(-dmin * static_cast<float>(mb), xs[1], a);
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int jp, const float (&xv)[64],
+                                const float (&xs)[NG]) {
+        float acc[NACC] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < NDW; t++) accum(raw, t, jp, &xv[4 * t], &xv[32 + 4 * t], acc);
         return finish(raw, jp, acc, xs);
     }
 };

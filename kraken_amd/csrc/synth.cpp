@@ -169,6 +169,59 @@ void quant_q4_k(const float *v, int64_t n, uint8_t *dst) {
     }
 }
 
+// Q5_K (176 B / 256 values): Q4_K's header and packed (sc, m) pairs, codes
+// in [0, 31] whose bit 4 goes to qh[l] bit 2g (low-nibble sub-block of chunk
+// pair g) or 2g+1 (high-nibble sub-block), as deq_q5_k (quant.cpp:462-489)
+// reads them back.
+void quant_q5_k(const float *v, int64_t n, uint8_t *dst) {
+    for (int64_t b = 0; b < n; b += 256, dst += 176) {
+        double scale[8], minv[8];
+        double smax = 0.0, mmax = 0.0;
+        for (int j = 0; j < 8; j++) {
+            double lo = 0.0, hi = 0.0;
+            for (int l = 0; l < 32; l++) {
+                lo = std::min(lo, double(v[b + 32 * j + l]));
+                hi = std::max(hi, double(v[b + 32 * j + l]));
+            }
+            scale[j] = (hi - lo) / 31.0;
+            minv[j] = -lo;
+            smax = std::max(smax, scale[j]);
+            mmax = std::max(mmax, minv[j]);
+        }
+        const uint16_t hd = f64_to_half(smax / 63.0), hm = f64_to_half(mmax / 63.0);
+        const double d = half_to_f64(hd), dmin = half_to_f64(hm);
+        int sc[8], mq[8];
+        for (int j = 0; j < 8; j++) {
+            sc[j] = d > 0 ? clampi(std::nearbyint(scale[j] / d), 0, 63) : 0;
+            mq[j] = dmin > 0 ? clampi(std::nearbyint(minv[j] / dmin), 0, 63) : 0;
+        }
+        put16(dst, hd);
+        put16(dst + 2, hm);
+        uint8_t *s = dst + 4;
+        for (int j = 0; j < 4; j++) {
+            s[j] = static_cast<uint8_t>((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+            s[j + 4] = static_cast<uint8_t>((mq[j] & 63) | ((mq[j + 4] >> 4) << 6));
+            s[j + 8] = static_cast<uint8_t>((sc[j + 4] & 15) | ((mq[j + 4] & 15) << 4));
+        }
+        int q[256];
+        for (int j = 0; j < 8; j++) {
+            const double ds = d * sc[j], dm = dmin * mq[j];
+            for (int l = 0; l < 32; l++) {
+                const double x = double(v[b + 32 * j + l]);
+                q[32 * j + l] = ds > 0 ? clampi(std::nearbyint((x + dm) / ds), 0, 31) : 0;
+            }
+        }
+        uint8_t *qh = dst + 16, *qs = dst + 48;
+        for (int l = 0; l < 32; l++) qh[l] = 0;
+        for (int g = 0; g < 4; g++)
+            for (int l = 0; l < 32; l++) {
+                const int a = q[64 * g + l], c = q[64 * g + 32 + l];
+                qs[32 * g + l] = static_cast<uint8_t>((a & 15) | ((c & 15) << 4));
+                qh[l] = static_cast<uint8_t>(qh[l] | ((a >> 4) << (2 * g)) | ((c >> 4) << (2 * g + 1)));
+            }
+    }
+}
+
 // Q6_K (210 B / 256 values): sixteen int8 scales, one per 16 values, codes in
 // [-32, 31] stored as q+32 split into ql (4 bits) and qh (2 bits) in the
 // plane order deq_q6_k (quant.cpp:491-512) reads them back.
@@ -232,6 +285,7 @@ extern "C" int krk_quantize_weights(int wt, const float *v, int64_t n_rows,
         case KRK_DT_Q8_0: fn = quant_q8_0; break;
         case KRK_DT_Q4_0: fn = quant_q4_0; break;
         case KRK_DT_Q4_K: fn = quant_q4_k; break;
+        case KRK_DT_Q5_K: fn = quant_q5_k; break;
         case KRK_DT_Q6_K: fn = quant_q6_k; break;
         default: return KRK_ERR_DTYPE;
     }

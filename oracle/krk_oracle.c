@@ -1,6 +1,6 @@
 /*
  * krk_oracle.c -- CPU restatement of Kraken's scalar f32 reference for the
- * quantized weight-math path (Q4_0 / Q8_0 / Q4_K / Q6_K dequant, the strict
+ * quantized weight-math path (Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K dequant, the strict
  * single-chain GEMV dot, the Q8 activation quantizer and integer dot, the
  * host MoE routing and the routed-expert FFN).
  *
@@ -89,7 +89,7 @@ int orc_block_size(int dt) {
     switch (dt) {
         case ORC_F32: case ORC_F16: return 1;
         case ORC_Q4_0: case ORC_Q8_0: return 32;
-        case ORC_Q4_K: case ORC_Q6_K: return 256;
+        case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: return 256;
         default: return 0;
     }
 }
@@ -100,6 +100,7 @@ int orc_block_bytes(int dt) {
         case ORC_Q4_0: return 18;
         case ORC_Q8_0: return 34;
         case ORC_Q4_K: return 144;
+        case ORC_Q5_K: return 176;
         case ORC_Q6_K: return 210;
         default: return 0;
     }
@@ -157,6 +158,29 @@ static void deq_q4_k(const uint8_t *b, float *y) {
     }
 }
 
+/* src/quant.cpp:462-489.  Q4_K's header and scales, then 32 high-bit bytes
+ * qh and 128 code bytes: chunk pair j takes bit 2j of qh[l] as bit 4 of its
+ * low-nibble code and bit 2j+1 for its high-nibble code.  As in Q4_K the
+ * product d1*q is exact (at most 17 + 5 significant bits), so the FMA the
+ * reference build forms and a separate multiply agree. */
+static void deq_q5_k(const uint8_t *b, float *y) {
+    float d = ld_f16(b), dmin = ld_f16(b + 2);
+    const uint8_t *sc = b + 4, *qh = b + 16, *q = b + 48;
+    for (int j = 0, is = 0; j < 256; j += 64, is += 2, q += 32) {
+        uint8_t si, mi;
+        scale_min_k4(is, sc, &si, &mi);
+        float d1 = d * (float)si, m1 = dmin * (float)mi;
+        scale_min_k4(is + 1, sc, &si, &mi);
+        float d2 = d * (float)si, m2 = dmin * (float)mi;
+        for (int l = 0; l < 32; l++) {
+            int lo = (q[l] & 0xF) | (((qh[l] >> is) & 1) << 4);
+            int hi = (q[l] >> 4) | (((qh[l] >> (is + 1)) & 1) << 4);
+            y[j + l] = fmaf(d1, (float)lo, -m1);
+            y[j + l + 32] = fmaf(d2, (float)hi, -m2);
+        }
+    }
+}
+
 /* src/quant.cpp:491-512.  `d * sc * (q - 32)` is (d*sc)*(q-32): two products,
  * nothing to contract. */
 static void deq_q6_k(const uint8_t *b, float *y) {
@@ -179,7 +203,7 @@ static void deq_q6_k(const uint8_t *b, float *y) {
     }
 }
 
-/* src/quant.cpp:1553-1601 (the four formats on this path plus F16). */
+/* src/quant.cpp:1553-1601 (the formats on this path plus F16). */
 static void dequant_block(int dt, const uint8_t *p, float *buf) {
     switch (dt) {
         case ORC_F16: buf[0] = ld_f16(p); break;
@@ -187,6 +211,7 @@ static void dequant_block(int dt, const uint8_t *p, float *buf) {
         case ORC_Q4_0: deq_q4_0(p, buf); break;
         case ORC_Q8_0: deq_q8_0(p, buf); break;
         case ORC_Q4_K: deq_q4_k(p, buf); break;
+        case ORC_Q5_K: deq_q5_k(p, buf); break;
         case ORC_Q6_K: deq_q6_k(p, buf); break;
         default: break;
     }

@@ -16,7 +16,7 @@ from conftest import rand_blocks
 
 pytestmark = pytest.mark.gpu
 
-FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K]
+FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K]
 GEMV_TOL = 1e-5
 GEMM_TOL = 2e-3
 
@@ -134,9 +134,10 @@ def test_gemv_f16_activations(krk, torch_cuda, be16, dt):
     assert rel(host(out).astype(np.float32), ref) <= 6e-4
 
 
-def test_gemv_exact_path_many_rows(krk, torch_cuda, be32):
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q5_K])
+def test_gemv_exact_path_many_rows(krk, torch_cuda, be32, dt):
     torch = torch_cuda
-    dt, rows, n_out, n_in = O.Q4_K, 13, 136, 1024
+    rows, n_out, n_in = 13, 136, 1024
     w = make_weights(krk, dt, n_out, n_in, seed=11)
     x = krk.synth_normal(rows * n_in, seed=12).reshape(rows, n_in)
     be32.set_gemm_path(krk.PATH_EXACT)

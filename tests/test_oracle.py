@@ -12,7 +12,7 @@ import oracle as O
 from conftest import rand_blocks
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz")
-FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K]
+FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K]
 
 
 def f16bytes(v):
@@ -321,3 +321,38 @@ def test_oracle_matches_reference_build():
         ref.ref_dot_q8_0_q8_scalar(O._p(w), O._p(xq), O._p(dx), 8192))
     for f in (0.5, 1.0 + 2.0 ** -11, 65504.0, 1e-7, 3.0e-5, -2.5):
         assert O.lib().orc_fp32_to_fp16(f) == ref.ref_fp32_to_fp16(f)
+
+
+def test_q5_k_closed_form():
+    """Q5_K (quant.cpp:462-489) by construction: d = 1, dmin = 0.5, every
+    scale slot 1..8 and min slot 2 * j, codes and high bits from known
+    patterns, so each value is sc_j * (nibble + 16 * bit) - 0.5 * m_j; then
+    the high-bit order (bit 2j low nibble, bit 2j+1 high nibble) with all
+    qh bytes a single bit."""
+    blk = np.zeros(176, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    sc = list(range(1, 9))
+    mn = [2 * j for j in range(8)]
+    # get_scale_min_k4 packing: j < 4 in the low 6 bits of bytes j and j + 4;
+    # j >= 4 in byte j + 4 (low nibble scale, high nibble min) plus the top
+    # two bits of bytes j - 4 and j
+    for j in range(4):
+        blk[4 + j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        blk[8 + j] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        blk[12 + j] = (sc[j + 4] & 15) | ((mn[j + 4] & 15) << 4)
+    codes = np.arange(128, dtype=np.uint8)
+    blk[48:] = (codes * 7) & 0xFF
+    for bit in range(8):
+        qh = np.zeros(32, np.uint8)
+        qh[:] = 1 << bit
+        blk[16:48] = qh
+        y = O.dequant(O.Q5_K, blk, 1, 256)[0]
+        want = np.empty(256, np.float64)
+        for j in range(4):
+            q = blk[48 + 32 * j: 48 + 32 * j + 32].astype(np.int64)
+            lo = (q & 15) + (16 if bit == 2 * j else 0)
+            hi = (q >> 4) + (16 if bit == 2 * j + 1 else 0)
+            want[64 * j: 64 * j + 32] = sc[2 * j] * lo - 0.5 * mn[2 * j]
+            want[64 * j + 32: 64 * j + 64] = sc[2 * j + 1] * hi - 0.5 * mn[2 * j + 1]
+        assert np.array_equal(y, want.astype(np.float32)), bit
