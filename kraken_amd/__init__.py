@@ -59,7 +59,35 @@ SIGNATURES = {
     "krk_quantize_q8_rows": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "krk_synth_normal": (None, [_vp, _i64, _u64, _f32, _f32, _i32]),
     "krk_quantize_weights": (_i32, [_i32, _vp, _i64, _i64, _vp, _i32]),
+    # include/krk_gguf.h
+    "krk_gguf_open": (_i32, [C.c_char_p, _P(_vp), C.c_char_p, C.c_size_t]),
+    "krk_gguf_close": (None, [_vp]),
+    "krk_gguf_version": (C.c_uint32, [_vp]),
+    "krk_gguf_alignment": (_u64, [_vp]),
+    "krk_gguf_data_offset": (_u64, [_vp]),
+    "krk_gguf_tensor_count": (_i64, [_vp]),
+    "krk_gguf_tensor": (_i32, [_vp, _i64, _vp]),
+    "krk_gguf_find_tensor": (_i64, [_vp, C.c_char_p]),
+    "krk_gguf_kv_count": (_i64, [_vp]),
+    "krk_gguf_kv_key": (C.c_char_p, [_vp, _i64]),
+    "krk_gguf_kv_type": (_i32, [_vp, _i64, _P(C.c_uint32), _P(C.c_uint32), _P(_u64)]),
+    "krk_gguf_find_kv": (_i64, [_vp, C.c_char_p]),
+    "krk_gguf_get_i64": (_i32, [_vp, C.c_char_p, _P(_i64)]),
+    "krk_gguf_get_f64": (_i32, [_vp, C.c_char_p, _P(C.c_double)]),
+    "krk_gguf_get_bool": (_i32, [_vp, C.c_char_p, _P(_i32)]),
+    "krk_gguf_get_str": (_i32, [_vp, C.c_char_p, _P(C.c_char_p)]),
+    "krk_gguf_array_i64": (_i32, [_vp, C.c_char_p, _u64, _P(_i64)]),
+    "krk_gguf_array_f64": (_i32, [_vp, C.c_char_p, _u64, _P(C.c_double)]),
+    "krk_gguf_array_str": (_i32, [_vp, C.c_char_p, _u64, _P(C.c_char_p)]),
+    "krk_gguf_upload": (_i32, [_vp, _vp, _i64, _vp]),
 }
+
+
+class GgufTensorInfo(C.Structure):
+    """krk_gguf_tensor_info (include/krk_gguf.h)."""
+    _fields_ = [("name", C.c_char_p), ("type_id", C.c_uint32), ("dtype_known", C.c_int),
+                ("n_dims", C.c_int), ("ne", C.c_uint64 * 4), ("offset", C.c_uint64),
+                ("n_elements", C.c_int64), ("n_bytes", C.c_uint64), ("data", C.c_void_p)]
 
 
 class KrkError(RuntimeError):
@@ -243,3 +271,105 @@ def moe_table_bytes(entries) -> bytes:
     """Pack a list of MoeEntry into the byte image the device table holds."""
     arr = (MoeEntry * len(entries))(*entries)
     return bytes(C.string_at(C.addressof(arr), C.sizeof(arr)))
+
+
+# ------------------------------------------------------------------ GGUF --
+class Gguf:
+    """A memory-mapped GGUF file: krk::Gguf (include/krk/gguf.hpp:86-160) over
+    include/krk_gguf.h.  ``tensors()`` gives the descriptors in file order,
+    ``data(name)`` a zero-copy numpy view of a tensor's bytes (valid while the
+    object lives), ``upload(backend, name, dst)`` copies them verbatim into a
+    device tensor."""
+
+    def __init__(self, path: str):
+        h = _vp()
+        err = C.create_string_buffer(512)
+        st = lib().krk_gguf_open(os.fsencode(path), C.byref(h), err, 512)
+        if st != 0:
+            raise KrkError(f"gguf_open: {lib().krk_status_string(st).decode()}: "
+                           f"{err.value.decode(errors='replace')}")
+        self._h = h
+        self._close = lib().krk_gguf_close
+
+    def close(self):
+        if getattr(self, "_h", None):
+            self._close(self._h)
+            self._h = None
+
+    __del__ = close
+
+    @property
+    def version(self) -> int:
+        return int(lib().krk_gguf_version(self._h))
+
+    @property
+    def alignment(self) -> int:
+        return int(lib().krk_gguf_alignment(self._h))
+
+    @property
+    def data_offset(self) -> int:
+        return int(lib().krk_gguf_data_offset(self._h))
+
+    def tensor_count(self) -> int:
+        return int(lib().krk_gguf_tensor_count(self._h))
+
+    def tensor(self, i) -> GgufTensorInfo:
+        if isinstance(i, str):
+            j = int(lib().krk_gguf_find_tensor(self._h, i.encode()))
+            if j < 0:
+                raise KeyError(i)
+            i = j
+        t = GgufTensorInfo()
+        if lib().krk_gguf_tensor(self._h, i, C.byref(t)) != 0:
+            raise IndexError(i)
+        return t
+
+    def tensors(self):
+        return [self.tensor(i) for i in range(self.tensor_count())]
+
+    def data(self, name):
+        """Zero-copy numpy uint8 view of a served-type tensor's bytes."""
+        import numpy as np
+        t = self.tensor(name)
+        if not t.dtype_known:
+            raise KrkError(f"tensor {t.name.decode()} has type {t.type_id}, not served")
+        buf = (C.c_uint8 * t.n_bytes).from_address(t.data)
+        return np.ctypeslib.as_array(buf)
+
+    def keys(self):
+        return [lib().krk_gguf_kv_key(self._h, i).decode(errors="replace")
+                for i in range(int(lib().krk_gguf_kv_count(self._h)))]
+
+    def kv_type(self, i: int):
+        t, e, n = C.c_uint32(), C.c_uint32(), _u64()
+        lib().krk_gguf_kv_type(self._h, i, C.byref(t), C.byref(e), C.byref(n))
+        return t.value, e.value, n.value
+
+    def get_i64(self, key: str, default: int = 0) -> int:
+        v = _i64(default)
+        lib().krk_gguf_get_i64(self._h, key.encode(), C.byref(v))
+        return v.value
+
+    def get_f64(self, key: str, default: float = 0.0) -> float:
+        v = C.c_double(default)
+        lib().krk_gguf_get_f64(self._h, key.encode(), C.byref(v))
+        return v.value
+
+    def get_bool(self, key: str, default: bool = False) -> bool:
+        v = _i32(int(default))
+        lib().krk_gguf_get_bool(self._h, key.encode(), C.byref(v))
+        return bool(v.value)
+
+    def get_str(self, key: str, default: str = "") -> str:
+        v = C.c_char_p()
+        if lib().krk_gguf_get_str(self._h, key.encode(), C.byref(v)) != 0:
+            return default
+        return v.value.decode(errors="replace")
+
+    def upload(self, backend: "Backend", name, dst) -> None:
+        """Copy tensor ``name`` verbatim into device tensor ``dst``."""
+        t = self.tensor(name)
+        if dst.numel() * dst.element_size() < t.n_bytes:
+            raise KrkError("gguf upload: destination smaller than the tensor")
+        j = int(lib().krk_gguf_find_tensor(self._h, t.name))
+        backend._check(lib().krk_gguf_upload(backend._h, self._h, j, _ptr(dst)), "gguf_upload")

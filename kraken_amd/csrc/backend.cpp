@@ -12,6 +12,7 @@
 #include <string>
 #include <vector>
 
+#include "krk_gguf.h"
 #include "krk_kernels.hpp"
 #include "krk_mi355x.h"
 
@@ -458,3 +459,17 @@ int krk_quantize_q8_rows(krk_backend *b, const float *x, int64_t rows, int64_t n
 }
 
 }  // extern "C"
+
+// Verbatim upload of a GGUF tensor (the model loader's upload of raw block
+// bytes): the mapping is pageable, so the copy is staged and the call waits
+// for it before the source may be unmapped.
+extern "C" int krk_gguf_upload(krk_backend *b, const krk_gguf *g, int64_t i, void *dst) {
+    if (!b) return KRK_ERR_ARG;
+    krk_gguf_tensor_info t{};
+    if (!g || !dst || krk_gguf_tensor(g, i, &t) != KRK_OK) return fail(b, KRK_ERR_ARG, "gguf_upload: bad arguments");
+    if (!t.dtype_known) return fail(b, KRK_ERR_DTYPE, "gguf_upload: tensor '%s' has type %u", t.name, t.type_id);
+    if (int s = make_current(b)) return s;
+    hipError_t e = hipMemcpyAsync(dst, t.data, t.n_bytes, hipMemcpyHostToDevice, b->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(b->stream);
+    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "gguf_upload");
+}

@@ -52,3 +52,25 @@ def rand_blocks(rng, dt, n_blocks):
 @pytest.fixture
 def rng():
     return np.random.default_rng(20261201)
+
+
+# GPU fixtures: one backend per activation type per test module
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need the MI355X"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def be32(krk, torch_cuda):
+    b = krk.Backend(0, krk.ACT_F32)
+    yield b
+    b.close()
+
+
+@pytest.fixture(scope="module")
+def be16(krk, torch_cuda):
+    b = krk.Backend(0, krk.ACT_F16)
+    yield b
+    b.close()

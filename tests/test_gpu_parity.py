@@ -26,27 +26,6 @@ def say(*a):
     sys.stdout.flush()
 
 
-@pytest.fixture(scope="module")
-def torch_cuda():
-    import torch
-    assert torch.cuda.is_available(), "GPU tests need the MI355X"
-    return torch
-
-
-@pytest.fixture(scope="module")
-def be32(krk, torch_cuda):
-    b = krk.Backend(0, krk.ACT_F32)
-    yield b
-    b.close()
-
-
-@pytest.fixture(scope="module")
-def be16(krk, torch_cuda):
-    b = krk.Backend(0, krk.ACT_F16)
-    yield b
-    b.close()
-
-
 def dev(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 

@@ -275,7 +275,8 @@ def test_q8_0_fixture_quantizer_matches_python_rule():
 # ------------------------------------------------------------- golden vectors
 def test_oracle_matches_golden_vectors():
     g = np.load(GOLDEN)
-    for dt, name in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k"), (O.Q6_K, "q6_k")):
+    for dt, name in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k"), (O.Q5_K, "q5_k"),
+                     (O.Q6_K, "q6_k")):
         w, x = g[f"{name}_w"], g[f"{name}_x"]
         n = x.size
         deq = O.dequant(dt, w, 1, n)[0]
