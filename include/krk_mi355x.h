@@ -28,9 +28,9 @@ extern "C" {
 #endif
 
 /* GGUF type ids; these block formats (plus F16/F32 activations) are on
- * this path.  include/krk/quant.hpp:16-34.  Q5_K is served by the dequant,
- * GEMV (rows 1..8, exact prefill) and MFMA GEMM paths; moe_dispatch banks
- * and the int8 rung take the other four (and Q8_0) only. */
+ * this path.  include/krk/quant.hpp:16-47.  Q5_K and IQ4_NL are served by
+ * the dequant, GEMV (rows 1..8, exact prefill) and MFMA GEMM paths;
+ * moe_dispatch banks take Q4_0 / Q8_0 / Q4_K / Q6_K, the int8 rung Q8_0. */
 enum krk_dtype {
     KRK_DT_F32 = 0,
     KRK_DT_F16 = 1,
@@ -38,7 +38,8 @@ enum krk_dtype {
     KRK_DT_Q8_0 = 8,
     KRK_DT_Q4_K = 12,
     KRK_DT_Q5_K = 13,
-    KRK_DT_Q6_K = 14
+    KRK_DT_Q6_K = 14,
+    KRK_DT_IQ4_NL = 20
 };
 
 /* Activation type of a handle: backend.hpp `act_type()` (F16 on the

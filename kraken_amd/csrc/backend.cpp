@@ -59,7 +59,7 @@ int hip_fail(krk_backend *b, hipError_t e, const char *what) {
 
 bool dtype_on_path(int wt) {
     return wt == KRK_DT_Q4_0 || wt == KRK_DT_Q8_0 || wt == KRK_DT_Q4_K || wt == KRK_DT_Q5_K ||
-           wt == KRK_DT_Q6_K;
+           wt == KRK_DT_Q6_K || wt == KRK_DT_IQ4_NL;
 }
 
 int make_current(krk_backend *b) {
@@ -151,7 +151,7 @@ const char *krk_status_string(int s) {
 int krk_dtype_block_size(int wt) {
     switch (wt) {
         case KRK_DT_F32: case KRK_DT_F16: return 1;
-        case KRK_DT_Q4_0: case KRK_DT_Q8_0: return 32;
+        case KRK_DT_Q4_0: case KRK_DT_Q8_0: case KRK_DT_IQ4_NL: return 32;
         case KRK_DT_Q4_K: case KRK_DT_Q5_K: case KRK_DT_Q6_K: return 256;
         default: return 0;
     }
@@ -161,7 +161,7 @@ int krk_dtype_block_bytes(int wt) {
     switch (wt) {
         case KRK_DT_F32: return 4;
         case KRK_DT_F16: return 2;
-        case KRK_DT_Q4_0: return 18;
+        case KRK_DT_Q4_0: case KRK_DT_IQ4_NL: return 18;
         case KRK_DT_Q8_0: return 34;
         case KRK_DT_Q4_K: return 144;
         case KRK_DT_Q5_K: return 176;
@@ -384,7 +384,7 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
         aligned = b->moe_ok[hit].aligned;
     } else {
         // every bank of the layer: present, of a type the expert kernels
-        // take (the path's formats but Q5_K), one weight type,
+        // take (the path's formats but Q5_K and IQ4_NL), one weight type,
         // the layer's geometry; and whether all rows start 16-byte aligned
         std::vector<krk_moe_entry> ents(static_cast<size_t>(n_expert));
         hipError_t he = hipMemcpyAsync(ents.data(), tab + static_cast<int64_t>(layer) * n_expert,
@@ -396,7 +396,8 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
         for (int e = 0; e < n_expert; e++) {
             const krk_moe_entry &en = ents[static_cast<size_t>(e)];
             for (int m = 0; m < 3; m++) {
-                if (!en.present[m] || !dtype_on_path(en.type[m]) || en.type[m] == KRK_DT_Q5_K)
+                if (!en.present[m] || !dtype_on_path(en.type[m]) || en.type[m] == KRK_DT_Q5_K ||
+                    en.type[m] == KRK_DT_IQ4_NL)
                     return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: expert %d matrix %d absent or of type %d",
                                 e, m, en.type[m]);
                 if (en.type[m] != e0.type[0])

@@ -218,6 +218,32 @@ template <> struct WStage<DT_Q4_0> {
     }
 };
 
+// IQ4_NL: Q4_0's staging, each nibble an index into the grid (value d * grid[q],
+// quant.cpp:566-574), looked up four at a time
+template <> struct WStage<DT_IQ4_NL> {
+    uint32_t q[4], dw;
+    int hf_;
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        const uint8_t *b = row + kt * 18;
+        load_bytes2<4>(b + 2, q);
+        const uintptr_t da = reinterpret_cast<uintptr_t>(b);
+        dw = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        hf_ = hf;
+    }
+    __device__ void decode(int, _Float16 (&o)[16]) const {
+        const float d = h2f(dw & 0xFFFF);
+        const int sh = hf_ * 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t g = iq4_lookup((q[t] >> sh) & 0x0F0F0F0Fu);   // grid + 128 per byte
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                o[4 * t + k] = static_cast<_Float16>(
+                    d * static_cast<float>(static_cast<int>((g >> (8 * k)) & 0xFF) - 128));
+        }
+    }
+};
+
 // ------------------------------------------------------- activation staging
 template <typename XT> struct XStage;
 template <> struct XStage<_Float16> {
@@ -516,6 +542,7 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
         KRK_GEMM_CASE(DT_Q6_K)
         KRK_GEMM_CASE(DT_Q8_0)
         KRK_GEMM_CASE(DT_Q4_0)
+        KRK_GEMM_CASE(DT_IQ4_NL)
         default: return hipErrorInvalidValue;
     }
 #undef KRK_GEMM_CASE

@@ -251,7 +251,7 @@ __global__ void __launch_bounds__(256) gemv_wave_kernel(SegTable t, int64_t tota
         // a lane past the row end re-reads the last block(s) and is masked
         // out of the sum (Q4_0 / Q8_0 lanes own two blocks; K % 64 == 0 there)
         int b = st * F::BPS + F::blk_of(lane);
-        constexpr int per_lane = (DT == DT_Q4_0 || DT == DT_Q8_0) ? 2 : 1;
+        constexpr int per_lane = (blk_vals(DT) == 32) ? 2 : 1;
         if (b > nb - per_lane) b = nb - per_lane;
 #pragma unroll
         for (int r = 0; r < RB; r++) {
@@ -423,6 +423,9 @@ template <> struct XRuns<DT_Q6_K> {
     }
 };
 template <> struct XRuns<DT_Q4_0> {
+    __device__ static int base(int lane) { return 64 * lane; }
+};
+template <> struct XRuns<DT_IQ4_NL> {
     __device__ static int base(int lane) { return 64 * lane; }
 };
 template <> struct XRuns<DT_Q8_0> {
@@ -601,6 +604,41 @@ template <int RB> struct LdsDot<DT_Q4_0, RB> {
     }
 };
 
+template <int RB> struct LdsDot<DT_IQ4_NL, RB> {
+    using F = WaveFmt<DT_IQ4_NL>;
+    static constexpr int NS = 2;
+    __device__ static void sums(const float *xl, int b0, float (&xs)[NS]) {
+        LdsDot<DT_Q4_0, RB>::sums(xl, b0, xs);
+    }
+    __device__ static void run(const uint32_t (&raw)[RB][F::NRAW], int, const float *xl, int b0,
+                               const float (&xs)[NS], float (&v)[RB]) {
+        float acc[RB][2];
+#pragma unroll
+        for (int r = 0; r < RB; r++) acc[r][0] = acc[r][1] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const floatx4 lo = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * u + 4 * t));
+                const floatx4 hi = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * u + 16 + 4 * t));
+                const float xl4[4] = {lo.x, lo.y, lo.z, lo.w}, xh4[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+                for (int r = 0; r < RB; r++) acc[r][u] = iq4x8(raw[r][5 * u + t], xl4, xh4, acc[r][u]);
+            }
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const float d = h2f(raw[r][5 * u + 4] & 0xFFFF);
+                a = __builtin_fmaf(d * kTwo24, acc[r][u], a);
+                a = __builtin_fmaf(-128.0f * d, xs[u], a);
+            }
+            v[r] = a;
+        }
+    }
+};
+
 template <int RB> struct LdsDot<DT_Q8_0, RB> {
     using F = WaveFmt<DT_Q8_0>;
     static constexpr int NS = 2;
@@ -662,7 +700,7 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(SegTable t, int64_t total
     auto fetch = [&](uint32_t (&raw)[RB][F::NRAW], int si, int64_t n0, int st) {
         const Seg &s = t.seg[si];
         const bool pair = s.kind == SEG_SILU;
-        constexpr int per_lane = (DT == DT_Q4_0 || DT == DT_Q8_0) ? 2 : 1;
+        constexpr int per_lane = (blk_vals(DT) == 32) ? 2 : 1;
         int b = st * F::BPS + F::blk_of(lane);
         if (b > nb - per_lane) b = nb - per_lane;
 #pragma unroll
@@ -800,7 +838,7 @@ __global__ void __launch_bounds__(512) gemv_stream_kernel(SegTable t, int64_t to
     constexpr int U = RB * P;                    // one unit's bytes
     constexpr int CH = (U + 1023) / 1024;        // DMA instructions per unit
     constexpr int SLOT = CH * 1024;
-    constexpr int per_lane = (DT == DT_Q4_0 || DT == DT_Q8_0) ? 2 : 1;
+    constexpr int per_lane = (blk_vals(DT) == 32) ? 2 : 1;
     static_assert(P % 16 == 0, "pieces must be whole 16-byte chunks");
     static_assert((NSLOT - 1) * CH < 64, "vmcnt is 6 bits");
     extern __shared__ float smem[];
@@ -1026,7 +1064,7 @@ static bool try_stream(const SegTable &t, hipStream_t st, hipError_t &err) {
         if (t.seg[i].kind == SEG_SILU || t.seg[i].x != t.seg[0].x) return false;
         if (reinterpret_cast<uintptr_t>(t.seg[i].w) & 15) return false;
     }
-    if ((DT == DT_Q4_0 || DT == DT_Q8_0) && t.n_in % 64) return false;
+    if ((blk_vals(DT) == 32) && t.n_in % 64) return false;
     if (t.row_bytes % 16) return false;
     err = launch_stream<DT, XT, OT>(t, st);
     return true;
@@ -1120,7 +1158,7 @@ static hipError_t launch_persist(SegTable t, hipStream_t st) {
 template <int DT, typename XT, typename OT>
 static hipError_t dispatch_mr(SegTable t, hipStream_t st) {
     if (t.rows == 1) {
-        const bool two_blocks = DT == DT_Q4_0 || DT == DT_Q8_0;
+        const bool two_blocks = blk_vals(DT) == 32;
         hipError_t err = hipSuccess;
         if (try_stream<DT, XT, OT>(t, st, err)) return err;
         bool same_x = true;
@@ -1155,6 +1193,7 @@ static hipError_t dispatch_dt(int dt, const SegTable &t, hipStream_t st) {
         case DT_Q5_K: return dispatch_mr<DT_Q5_K, XT, OT>(t, st);
         case DT_Q6_K: return dispatch_mr<DT_Q6_K, XT, OT>(t, st);
         case DT_Q4_0: return dispatch_mr<DT_Q4_0, XT, OT>(t, st);
+        case DT_IQ4_NL: return dispatch_mr<DT_IQ4_NL, XT, OT>(t, st);
         case DT_Q8_0: return dispatch_mr<DT_Q8_0, XT, OT>(t, st);
         default: return hipErrorInvalidValue;
     }

@@ -20,10 +20,12 @@ namespace krk {
 
 // ---------------------------------------------------------------- geometry --
 __host__ __device__ constexpr int blk_vals(int dt) {
-    return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K ? 256 : (dt == DT_Q4_0 || dt == DT_Q8_0) ? 32 : 1;
+    return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K             ? 256
+           : (dt == DT_Q4_0 || dt == DT_Q8_0 || dt == DT_IQ4_NL) ? 32
+                                                                  : 1;
 }
 __host__ __device__ constexpr int blk_bytes(int dt) {
-    return dt == DT_Q4_K ? 144 : dt == DT_Q5_K ? 176 : dt == DT_Q6_K ? 210 : dt == DT_Q4_0 ? 18
+    return dt == DT_Q4_K ? 144 : dt == DT_Q5_K ? 176 : dt == DT_Q6_K ? 210 : dt == DT_Q4_0 || dt == DT_IQ4_NL ? 18
          : dt == DT_Q8_0 ? 34 : dt == DT_F16 ? 2 : 4;
 }
 
@@ -44,6 +46,20 @@ __device__ __forceinline__ void dequant_chunk<DT_Q4_0>(const uint8_t *b, int, fl
     for (int k = 0; k < 16; k++) {
         y[k] = d * static_cast<float>(static_cast<int>(b[2 + k] & 0xF) - 8);
         y[k + 16] = d * static_cast<float>(static_cast<int>(b[2 + k] >> 4) - 8);
+    }
+}
+
+// IQ4_NL's grid (ggml's kvalues_iq4nl, src/quant.cpp:88-91), a format constant
+__device__ __constant__ const int8_t kIq4nlGrid[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                                       1,    13,   25,  38,  53,  69,  89,  113};
+
+// src/quant.cpp:566-574: value d * grid[q], one product
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_IQ4_NL>(const uint8_t *b, int, float *y) {
+    const float d = ldh(b);
+    for (int k = 0; k < 16; k++) {
+        y[k] = d * static_cast<float>(kIq4nlGrid[b[2 + k] & 0xF]);
+        y[k + 16] = d * static_cast<float>(kIq4nlGrid[b[2 + k] >> 4]);
     }
 }
 
@@ -344,6 +360,46 @@ template <> struct LaneFmt<DT_Q4_0> {
     }
 };
 
+// IQ4_NL grid values biased by 128 (1..241), as bytes: grid lookups of four
+// indices at a time with v_perm (a selector byte 0..7 picks a byte of the
+// 8-byte table in its two dword operands), two halves joined on index bit 3
+constexpr uint32_t kIq4B0 = 0x3F2D1801u, kIq4B1 = 0x766A5D4Fu, kIq4B2 = 0xA6998D81u, kIq4B3 = 0xF1D9C5B5u;
+__device__ __forceinline__ uint32_t iq4_lookup(uint32_t idx) {   // idx: four indices 0..15 as bytes
+    const uint32_t sel = idx & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kIq4B1, kIq4B0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(kIq4B3, kIq4B2, sel);
+    const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & m) | (lo & ~m);
+}
+// acc += sum over the 8 indices of a dword (low nibbles with xl[0..3], high
+// nibbles with xh[0..3]) of (grid + 128) * 2^-24 * x, as f16 subnormals
+__device__ __forceinline__ float iq4x8(uint32_t v, const float *xl, const float *xh, float acc) {
+    const uint32_t a = iq4_lookup(v & 0x0F0F0F0Fu), b = iq4_lookup((v >> 4) & 0x0F0F0F0Fu);
+    acc = mix2(a & 0x00FF00FFu, xl[0], xl[2], acc);
+    acc = mix2((a >> 8) & 0x00FF00FFu, xl[1], xl[3], acc);
+    acc = mix2(b & 0x00FF00FFu, xh[0], xh[2], acc);
+    return mix2((b >> 8) & 0x00FF00FFu, xh[1], xh[3], acc);
+}
+
+// IQ4_NL: Q4_0's block (one lane per block), value d * grid[q]; the 128 bias
+// comes off through the x sums
+template <> struct LaneFmt<DT_IQ4_NL> {
+    static constexpr int LPB = 1, NG = 2, RUN = 32, NRUN = 1, NRAW = 5;
+    __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int i) { return i >> 4; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int p) {
+        LaneFmt<DT_Q4_0>::load(raw, blk, p);
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[32],
+                                const float (&xs)[NG]) {
+        const float d = h2f(raw[4] & 0xFFFF);
+        float s = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) s = iq4x8(raw[t], &xv[4 * t], &xv[16 + 4 * t], s);
+        return __builtin_fmaf(-128.0f * d, xs[0] + xs[1], (d * kTwo24) * s);
+    }
+};
+
 // Q8_0: one lane per 32-value block; value = d * (int8)q.  Codes are biased
 // to q + 128 (xor 0x80) so they are non-negative subnormals.
 template <> struct LaneFmt<DT_Q8_0> {
@@ -571,6 +627,32 @@ template <> struct WaveFmt<DT_Q4_0> {
             a = __builtin_fmaf(d * kTwo24, sl, a);
             a = __builtin_fmaf(d * kTwo20, shi, a);
             a = __builtin_fmaf(-8.0f * d, xs[u], a);
+        }
+        return a;
+    }
+};
+
+template <> struct WaveFmt<DT_IQ4_NL> {
+    // lane owns blocks 2*lane, 2*lane+1 of the step: 64 contiguous values
+    static constexpr int LPB = 1, BPS = 128, NG = 2, RUN = 64, NRUN = 1, NRAW = 10;
+    __device__ static int blk_of(int lane) { return 2 * lane; }
+    __device__ static int slot_of(int) { return 0; }
+    __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int i) { return i >> 5; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int p) {
+        WaveFmt<DT_Q4_0>::load(raw, blk, p);
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[64],
+                                const float (&xs)[NG]) {
+        float a = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const float d = h2f(raw[5 * u + 4] & 0xFFFF);
+            float s = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) s = iq4x8(raw[5 * u + t], &xv[32 * u + 4 * t], &xv[32 * u + 16 + 4 * t], s);
+            a = __builtin_fmaf(d * kTwo24, s, a);
+            a = __builtin_fmaf(-128.0f * d, xs[u], a);
         }
         return a;
     }

@@ -169,6 +169,28 @@ void quant_q4_k(const float *v, int64_t n, uint8_t *dst) {
     }
 }
 
+// IQ4_NL (18 B / 32 values): d = amax / 127 rounded to f16 (the grid spans
+// -127..113), each value to the nearest grid point of v / d.
+void quant_iq4_nl(const float *v, int64_t n, uint8_t *dst) {
+    static const int grid[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+    for (int64_t b = 0; b < n; b += 32, dst += 18) {
+        double amax = 0.0;
+        for (int l = 0; l < 32; l++) amax = std::max(amax, std::fabs(double(v[b + l])));
+        const uint16_t hd = f64_to_half(amax / 127.0);
+        const double d = half_to_f64(hd);
+        int q[32];
+        for (int l = 0; l < 32; l++) {
+            const double t = d > 0 ? double(v[b + l]) / d : 0.0;
+            int best = 0;
+            for (int k = 1; k < 16; k++)
+                if (std::fabs(t - grid[k]) < std::fabs(t - grid[best])) best = k;
+            q[l] = best;
+        }
+        put16(dst, hd);
+        for (int l = 0; l < 16; l++) dst[2 + l] = static_cast<uint8_t>(q[l] | (q[l + 16] << 4));
+    }
+}
+
 // Q5_K (176 B / 256 values): Q4_K's header and packed (sc, m) pairs, codes
 // in [0, 31] whose bit 4 goes to qh[l] bit 2g (low-nibble sub-block of chunk
 // pair g) or 2g+1 (high-nibble sub-block), as deq_q5_k (quant.cpp:462-489)
@@ -284,6 +306,7 @@ extern "C" int krk_quantize_weights(int wt, const float *v, int64_t n_rows,
     switch (wt) {
         case KRK_DT_Q8_0: fn = quant_q8_0; break;
         case KRK_DT_Q4_0: fn = quant_q4_0; break;
+        case KRK_DT_IQ4_NL: fn = quant_iq4_nl; break;
         case KRK_DT_Q4_K: fn = quant_q4_k; break;
         case KRK_DT_Q5_K: fn = quant_q5_k; break;
         case KRK_DT_Q6_K: fn = quant_q6_k; break;

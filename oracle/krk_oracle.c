@@ -1,6 +1,6 @@
 /*
  * krk_oracle.c -- CPU restatement of Kraken's scalar f32 reference for the
- * quantized weight-math path (Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K dequant, the strict
+ * quantized weight-math path (Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K / IQ4_NL dequant, the strict
  * single-chain GEMV dot, the Q8 activation quantizer and integer dot, the
  * host MoE routing and the routed-expert FFN).
  *
@@ -88,7 +88,7 @@ static inline float ld_f16(const uint8_t *p) {
 int orc_block_size(int dt) {
     switch (dt) {
         case ORC_F32: case ORC_F16: return 1;
-        case ORC_Q4_0: case ORC_Q8_0: return 32;
+        case ORC_Q4_0: case ORC_Q8_0: case ORC_IQ4_NL: return 32;
         case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: return 256;
         default: return 0;
     }
@@ -97,7 +97,7 @@ int orc_block_bytes(int dt) {
     switch (dt) {
         case ORC_F32: return 4;
         case ORC_F16: return 2;
-        case ORC_Q4_0: return 18;
+        case ORC_Q4_0: case ORC_IQ4_NL: return 18;
         case ORC_Q8_0: return 34;
         case ORC_Q4_K: return 144;
         case ORC_Q5_K: return 176;
@@ -117,6 +117,21 @@ static void deq_q4_0(const uint8_t *b, float *y) {
     for (int k = 0; k < 16; k++) {
         y[k] = d * (float)((int)(b[2 + k] & 0xF) - 8);
         y[k + 16] = d * (float)((int)(b[2 + k] >> 4) - 8);
+    }
+}
+
+/* IQ4_NL's non-linear grid: ggml's kvalues_iq4nl, a constant of the format
+ * (src/quant.cpp:88-91). */
+static const int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                  1, 13, 25, 38, 53, 69, 89, 113};
+
+/* src/quant.cpp:566-574: Q4_0's layout, each nibble an index into the grid,
+ * value d * grid[q] (one product). */
+static void deq_iq4_nl(const uint8_t *b, float *y) {
+    float d = ld_f16(b);
+    for (int k = 0; k < 16; k++) {
+        y[k] = d * (float)kIq4nl[b[2 + k] & 0xF];
+        y[k + 16] = d * (float)kIq4nl[b[2 + k] >> 4];
     }
 }
 
@@ -210,6 +225,7 @@ static void dequant_block(int dt, const uint8_t *p, float *buf) {
         case ORC_F32: memcpy(buf, p, 4); break;
         case ORC_Q4_0: deq_q4_0(p, buf); break;
         case ORC_Q8_0: deq_q8_0(p, buf); break;
+        case ORC_IQ4_NL: deq_iq4_nl(p, buf); break;
         case ORC_Q4_K: deq_q4_k(p, buf); break;
         case ORC_Q5_K: deq_q5_k(p, buf); break;
         case ORC_Q6_K: deq_q6_k(p, buf); break;

@@ -4,7 +4,7 @@ CPU: against the reference's own reader (krk::Gguf, src/gguf.cpp, built in
 place into oracle/_ref) on the reference's three GGUF checkpoints; on files
 written here from the specification (every metadata type, a non-default
 alignment, a type id the library does not serve); and its refusals.
-GPU: real Q8_0 blocks of the reference checkpoint (tests/golden fixture),
+GPU: real Q8_0 and IQ4_NL blocks of the reference checkpoints (tests/golden fixture),
 written into a GGUF, read, uploaded verbatim and decoded on the device
 bit-for-bit against the oracle."""
 import ctypes as C
@@ -22,7 +22,7 @@ REF_DIR = "/root/reference"
 REF_FILES = ["TinyLLama-v0.Q8_0.gguf", "tinystories-gpt-0.1-3m.Q2_K.gguf",
              "tiny-llama3-test-Q3_K_M.gguf"]
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "gguf_q8_0_blocks.npz")
-SERVED = {0, 1, 2, 8, 12, 13, 14}
+SERVED = {0, 1, 2, 8, 12, 13, 14, 20}
 
 
 def _ref_reader():
@@ -101,7 +101,7 @@ def test_reader_reads_every_metadata_type(krk, tmp_path):
     q8 = bytes(rng.integers(0, 256, 2 * 34 * 3, dtype=np.uint8))
     q4k = bytes(rng.integers(0, 256, 144 * 2, dtype=np.uint8))
     f32 = np.arange(5, dtype=np.float32).tobytes()
-    unknown = bytes(range(50))
+    unknown = bytes(range(50))   # type 11 (Q3_K), not served
     kvs = [("general.architecture", STRING, "llama"), ("general.alignment", U32, 64),
            ("a.u8", U8, 250), ("a.i8", I8, -5), ("a.u16", U16, 65000), ("a.i16", I16, -300),
            ("a.i32", I32, -70000), ("a.f32", F32, 1.5), ("a.bool", BOOL, 1), ("a.u64", U64, 2 ** 40),
@@ -109,7 +109,7 @@ def test_reader_reads_every_metadata_type(krk, tmp_path):
            ("a.arr_i32", ARRAY, [1, -2, 3], I32), ("a.arr_f32", ARRAY, [0.5, 0.25], F32),
            ("a.arr_str", ARRAY, ["x", "yz"], STRING), ("a.arr_u64", ARRAY, [7, 2 ** 33], U64)]
     tensors = [("w.q8", 8, [64, 3], q8), ("w.q4k", 12, [256, 2], q4k), ("v.f32", 0, [5], f32),
-               ("u.iq4", 20, [32, 3], unknown)]
+               ("u.q3k", 11, [256, 3], unknown)]
     path = str(tmp_path / "m.gguf")
     data_off = write_gguf(path, kvs, tensors, alignment=64)
     g = krk.Gguf(path)
@@ -133,7 +133,7 @@ def test_reader_reads_every_metadata_type(krk, tmp_path):
     for name, tid, ne, data in tensors:
         t = g.tensor(name)
         assert t.type_id == tid and list(t.ne)[: len(ne)] == ne
-        if tid == 20:
+        if tid == 11:
             assert not t.dtype_known and t.n_bytes == 0
             with pytest.raises(krk.KrkError):
                 g.data(name)
@@ -170,31 +170,32 @@ def test_reader_refuses_bad_files(krk, tmp_path):
 
 
 @pytest.mark.gpu
-def test_gguf_upload_real_q8_0_blocks(krk, torch_cuda, be32, tmp_path):
-    """Real ggml Q8_0 blocks (three tensors of the reference's TinyLlama
-    checkpoint) through a GGUF file, the reader, the verbatim upload and the
-    device decoder, bit for bit against the oracle; and one GEMV on them."""
+def test_gguf_upload_real_blocks(krk, torch_cuda, be32, tmp_path):
+    """Real ggml blocks (Q8_0 and IQ4_NL tensors of the reference's
+    checkpoints) through a GGUF file, the reader, the verbatim upload and the
+    device decoder, bit for bit against the oracle; and one GEMV on each."""
     torch = torch_cuda
     f = np.load(GOLD)
     n = len([k for k in f.files if k.startswith("name")])
-    tensors = [(f[f"name{i}"].tobytes().decode(), 8, [int(x) for x in f[f"ne{i}"]], f[f"bytes{i}"].tobytes())
-               for i in range(n)]
+    # names are unique per source file; two files share "blk.0.attn_q.weight"
+    tensors = [(f"t{i}." + f[f"name{i}"].tobytes().decode(), int(f[f"type{i}"][0]),
+                [int(x) for x in f[f"ne{i}"]], f[f"bytes{i}"].tobytes()) for i in range(n)]
     path = str(tmp_path / "real.gguf")
     write_gguf(path, [("general.architecture", STRING, "llama")], tensors)
     g = krk.Gguf(path)
-    for name, _, ne, data in tensors:
+    for name, dt, ne, data in tensors:
         n_in, n_rows = ne[0], ne[1]
         dev = torch.empty(len(data), dtype=torch.uint8, device="cuda")
         g.upload(be32, name, dev)
         assert bytes(dev.cpu().numpy()) == data
         out = torch.empty((n_rows, n_in), dtype=torch.float32, device="cuda")
-        be32.dequant_rows(out, dev, O.Q8_0, n_rows, n_in)
+        be32.dequant_rows(out, dev, dt, n_rows, n_in)
         be32.sync()
-        want = O.dequant(O.Q8_0, np.frombuffer(data, np.uint8), n_rows, n_in)
+        want = O.dequant(dt, np.frombuffer(data, np.uint8), n_rows, n_in)
         assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32)), name
         x = krk.synth_normal(n_in, seed=3)
         y = torch.empty((1, n_rows), dtype=torch.float32, device="cuda")
-        be32.gemm(y, torch.from_numpy(x).cuda(), dev, O.Q8_0, n_rows, n_in, 1)
+        be32.gemm(y, torch.from_numpy(x).cuda(), dev, dt, n_rows, n_in, 1)
         be32.sync()
-        ref = O.gemm(O.Q8_0, np.frombuffer(data, np.uint8), x.reshape(1, n_in), n_rows)
+        ref = O.gemm(dt, np.frombuffer(data, np.uint8), x.reshape(1, n_in), n_rows)
         assert np.linalg.norm(y.cpu().numpy() - ref) <= 1e-5 * np.linalg.norm(ref), name

@@ -12,7 +12,7 @@ import oracle as O
 from conftest import rand_blocks
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz")
-FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K]
+FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL]
 
 
 def f16bytes(v):
@@ -276,7 +276,7 @@ def test_q8_0_fixture_quantizer_matches_python_rule():
 def test_oracle_matches_golden_vectors():
     g = np.load(GOLDEN)
     for dt, name in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k"), (O.Q5_K, "q5_k"),
-                     (O.Q6_K, "q6_k")):
+                     (O.Q6_K, "q6_k"), (O.IQ4_NL, "iq4_nl")):
         w, x = g[f"{name}_w"], g[f"{name}_x"]
         n = x.size
         deq = O.dequant(dt, w, 1, n)[0]
@@ -357,3 +357,14 @@ def test_q5_k_closed_form():
             want[64 * j: 64 * j + 32] = sc[2 * j] * lo - 0.5 * mn[2 * j]
             want[64 * j + 32: 64 * j + 64] = sc[2 * j + 1] * hi - 0.5 * mn[2 * j + 1]
         assert np.array_equal(y, want.astype(np.float32)), bit
+
+
+def test_iq4_nl_closed_form():
+    """IQ4_NL (quant.cpp:566-574): with d = 1 every index 0..15 in both
+    nibbles decodes to the grid value itself, low nibbles first."""
+    grid = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[2:] = [(k & 15) | ((15 - k) << 4) for k in range(16)]
+    y = O.dequant(O.IQ4_NL, blk, 1, 32)[0]
+    assert y[:16].tolist() == grid and y[16:].tolist() == grid[::-1]
