@@ -244,6 +244,34 @@ template <> struct WStage<DT_IQ4_NL> {
     }
 };
 
+// IQ4_XS: chunk kt is sub-block kt % 8 of block kt / 8: the 8-byte header and
+// the sub-block's 16 index bytes; half hf takes the low (0) or high nibbles
+template <> struct WStage<DT_IQ4_XS> {
+    uint32_t q[4], h0, h1;
+    int hf_;
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        const uint8_t *b = row + (kt >> 3) * 136;
+        const u32x2 h = ld64(b);
+        h0 = h.x;
+        h1 = h.y;
+        const u32x4 v = ld128(b + 8 + 16 * (kt & 7));
+        q[0] = v.x; q[1] = v.y; q[2] = v.z; q[3] = v.w;
+        hf_ = hf;
+    }
+    __device__ void decode(int kt, _Float16 (&o)[16]) const {
+        const float dl = iq4xs_scale(h0, h1, kt & 7);
+        const int sh = hf_ * 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t g = iq4_lookup((q[t] >> sh) & 0x0F0F0F0Fu);
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                o[4 * t + k] = static_cast<_Float16>(
+                    dl * static_cast<float>(static_cast<int>((g >> (8 * k)) & 0xFF) - 128));
+        }
+    }
+};
+
 // ------------------------------------------------------- activation staging
 template <typename XT> struct XStage;
 template <> struct XStage<_Float16> {
@@ -543,6 +571,7 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
         KRK_GEMM_CASE(DT_Q8_0)
         KRK_GEMM_CASE(DT_Q4_0)
         KRK_GEMM_CASE(DT_IQ4_NL)
+        KRK_GEMM_CASE(DT_IQ4_XS)
         default: return hipErrorInvalidValue;
     }
 #undef KRK_GEMM_CASE

@@ -20,10 +20,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kWave = 64;
 
 // Q4_K 144 B / 256, Q5_K 176 B / 256, Q6_K 210 B / 256, Q4_0 and IQ4_NL 18 B / 32,
-// Q8_0 34 B / 32
+// Q8_0 34 B / 32, IQ4_XS 136 B / 256
 // (include/krk/quant.hpp geometry; src/quant.cpp:1805-1900).
 enum : int { DT_F32 = 0, DT_F16 = 1, DT_Q4_0 = 2, DT_Q8_0 = 8, DT_Q4_K = 12, DT_Q5_K = 13, DT_Q6_K = 14,
-             DT_IQ4_NL = 20 };
+             DT_IQ4_NL = 20, DT_IQ4_XS = 23 };
 
 __device__ __forceinline__ float h2f(uint32_t h16) {
     _Float16 h;

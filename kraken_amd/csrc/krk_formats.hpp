@@ -20,12 +20,13 @@ namespace krk {
 
 // ---------------------------------------------------------------- geometry --
 __host__ __device__ constexpr int blk_vals(int dt) {
-    return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K             ? 256
+    return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K || dt == DT_IQ4_XS ? 256
            : (dt == DT_Q4_0 || dt == DT_Q8_0 || dt == DT_IQ4_NL) ? 32
                                                                   : 1;
 }
 __host__ __device__ constexpr int blk_bytes(int dt) {
-    return dt == DT_Q4_K ? 144 : dt == DT_Q5_K ? 176 : dt == DT_Q6_K ? 210 : dt == DT_Q4_0 || dt == DT_IQ4_NL ? 18
+    return dt == DT_Q4_K ? 144 : dt == DT_Q5_K ? 176 : dt == DT_Q6_K ? 210 : dt == DT_IQ4_XS ? 136
+         : dt == DT_Q4_0 || dt == DT_IQ4_NL ? 18
          : dt == DT_Q8_0 ? 34 : dt == DT_F16 ? 2 : 4;
 }
 
@@ -60,6 +61,20 @@ __device__ __forceinline__ void dequant_chunk<DT_IQ4_NL>(const uint8_t *b, int, 
     for (int k = 0; k < 16; k++) {
         y[k] = d * static_cast<float>(kIq4nlGrid[b[2 + k] & 0xF]);
         y[k + 16] = d * static_cast<float>(kIq4nlGrid[b[2 + k] >> 4]);
+    }
+}
+
+// src/quant.cpp:641-659: chunk c = sub-block c, value (d * (ls - 32)) * grid[q]
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_IQ4_XS>(const uint8_t *b, int c, float *y) {
+    const float d = ldh(b);
+    const uint32_t sh = static_cast<uint32_t>(b[2]) | (static_cast<uint32_t>(b[3]) << 8);
+    const int ls = ((b[4 + c / 2] >> (4 * (c % 2))) & 0xF) | (((sh >> (2 * c)) & 3) << 4);
+    const float dl = d * static_cast<float>(ls - 32);
+    const uint8_t *qs = b + 8 + 16 * c;
+    for (int j = 0; j < 16; j++) {
+        y[j] = dl * static_cast<float>(kIq4nlGrid[qs[j] & 0xF]);
+        y[j + 16] = dl * static_cast<float>(kIq4nlGrid[qs[j] >> 4]);
     }
 }
 
@@ -400,6 +415,35 @@ template <> struct LaneFmt<DT_IQ4_NL> {
     }
 };
 
+// IQ4_XS scale of sub-block ib from the header dwords h0 = d | scales_h << 16
+// and h1 = scales_l[0..3]: d * (ls - 32) (quant.cpp:646-650)
+__device__ __forceinline__ float iq4xs_scale(uint32_t h0, uint32_t h1, int ib) {
+    const uint32_t ls = ((h1 >> (4 * ib)) & 0xFu) | (((h0 >> (16 + 2 * ib)) & 3u) << 4);
+    return h2f(h0 & 0xFFFF) * static_cast<float>(static_cast<int>(ls) - 32);
+}
+
+// IQ4_XS: piece p = sub-block p (32 values: 16 index bytes at 8 + 16p, low
+// nibbles first), eight lanes per 256-value block
+template <> struct LaneFmt<DT_IQ4_XS> {
+    static constexpr int LPB = 8, NG = 2, RUN = 32, NRUN = 1, NRAW = 6;
+    __device__ static int run_start(int p, int) { return 32 * p; }
+    __device__ static int group_of(int i) { return i >> 4; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int p) {
+        const u32x2 h = ld64(blk);
+        const u32x4 q = ld128(blk + 8 + 16 * p);
+        raw[0] = q.x; raw[1] = q.y; raw[2] = q.z; raw[3] = q.w;
+        raw[4] = h.x; raw[5] = h.y;
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int p, const float (&xv)[32],
+                                const float (&xs)[NG]) {
+        const float dl = iq4xs_scale(raw[4], raw[5], p);
+        float s = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) s = iq4x8(raw[t], &xv[4 * t], &xv[16 + 4 * t], s);
+        return __builtin_fmaf(-128.0f * dl, xs[0] + xs[1], (dl * kTwo24) * s);
+    }
+};
+
 // Q8_0: one lane per 32-value block; value = d * (int8)q.  Codes are biased
 // to q + 128 (xor 0x80) so they are non-negative subnormals.
 template <> struct LaneFmt<DT_Q8_0> {
@@ -653,6 +697,37 @@ template <> struct WaveFmt<DT_IQ4_NL> {
             for (int t = 0; t < 4; t++) s = iq4x8(raw[5 * u + t], &xv[32 * u + 4 * t], &xv[32 * u + 16 + 4 * t], s);
             a = __builtin_fmaf(d * kTwo24, s, a);
             a = __builtin_fmaf(-128.0f * d, xs[u], a);
+        }
+        return a;
+    }
+};
+
+template <> struct WaveFmt<DT_IQ4_XS> {
+    // lane slot jp = lane % 4 of block lane / 4: sub-blocks 2jp, 2jp+1 (index
+    // bytes 8 + 32jp .. +32), 64 contiguous values
+    static constexpr int LPB = 4, BPS = 16, NG = 2, RUN = 64, NRUN = 1, NRAW = 10;
+    __device__ static int blk_of(int lane) { return lane >> 2; }
+    __device__ static int slot_of(int lane) { return lane & 3; }
+    __device__ static int run_start(int jp, int) { return 64 * jp; }
+    __device__ static int group_of(int i) { return i >> 5; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int jp) {
+        const u32x2 h = ld64(blk);
+        const u32x4 a = ld128(blk + 8 + 32 * jp), b = ld128(blk + 24 + 32 * jp);
+        raw[0] = a.x; raw[1] = a.y; raw[2] = a.z; raw[3] = a.w;
+        raw[4] = b.x; raw[5] = b.y; raw[6] = b.z; raw[7] = b.w;
+        raw[8] = h.x; raw[9] = h.y;
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int jp, const float (&xv)[64],
+                                const float (&xs)[NG]) {
+        float a = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const float dl = iq4xs_scale(raw[8], raw[9], 2 * jp + u);
+            float s = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) s = iq4x8(raw[4 * u + t], &xv[32 * u + 4 * t], &xv[32 * u + 16 + 4 * t], s);
+            a = __builtin_fmaf(dl * kTwo24, s, a);
+            a = __builtin_fmaf(-128.0f * dl, xs[u], a);
         }
         return a;
     }

@@ -191,6 +191,44 @@ void quant_iq4_nl(const float *v, int64_t n, uint8_t *dst) {
     }
 }
 
+// IQ4_XS (136 B / 256 values): per 32-value sub-block a positive scale
+// s = amax / 127 on a 6-bit grid ls - 32 in 1..31 of d = max s / 31, then
+// IQ4_NL's nearest grid index of v / (d (ls - 32)).
+void quant_iq4_xs(const float *v, int64_t n, uint8_t *dst) {
+    static const int grid[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+    for (int64_t b = 0; b < n; b += 256, dst += 136) {
+        double s[8], smax = 0.0;
+        for (int ib = 0; ib < 8; ib++) {
+            double amax = 0.0;
+            for (int l = 0; l < 32; l++) amax = std::max(amax, std::fabs(double(v[b + 32 * ib + l])));
+            s[ib] = amax / 127.0;
+            smax = std::max(smax, s[ib]);
+        }
+        const uint16_t hd = f64_to_half(smax / 31.0);
+        const double d = half_to_f64(hd);
+        put16(dst, hd);
+        uint16_t sh = 0;
+        uint8_t *sl = dst + 4, *qs = dst + 8;
+        for (int k = 0; k < 4; k++) sl[k] = 0;
+        for (int ib = 0; ib < 8; ib++) {
+            const int ls = 32 + (d > 0 ? clampi(std::nearbyint(s[ib] / d), 1, 31) : 1);
+            sl[ib / 2] = static_cast<uint8_t>(sl[ib / 2] | ((ls & 15) << (4 * (ib % 2))));
+            sh = static_cast<uint16_t>(sh | (((ls >> 4) & 3) << (2 * ib)));
+            const double dl = d * (ls - 32);
+            int q[32];
+            for (int l = 0; l < 32; l++) {
+                const double t = dl > 0 ? double(v[b + 32 * ib + l]) / dl : 0.0;
+                int best = 0;
+                for (int k = 1; k < 16; k++)
+                    if (std::fabs(t - grid[k]) < std::fabs(t - grid[best])) best = k;
+                q[l] = best;
+            }
+            for (int l = 0; l < 16; l++) qs[16 * ib + l] = static_cast<uint8_t>(q[l] | (q[l + 16] << 4));
+        }
+        put16(dst + 2, sh);
+    }
+}
+
 // Q5_K (176 B / 256 values): Q4_K's header and packed (sc, m) pairs, codes
 // in [0, 31] whose bit 4 goes to qh[l] bit 2g (low-nibble sub-block of chunk
 // pair g) or 2g+1 (high-nibble sub-block), as deq_q5_k (quant.cpp:462-489)
@@ -307,6 +345,7 @@ extern "C" int krk_quantize_weights(int wt, const float *v, int64_t n_rows,
         case KRK_DT_Q8_0: fn = quant_q8_0; break;
         case KRK_DT_Q4_0: fn = quant_q4_0; break;
         case KRK_DT_IQ4_NL: fn = quant_iq4_nl; break;
+        case KRK_DT_IQ4_XS: fn = quant_iq4_xs; break;
         case KRK_DT_Q4_K: fn = quant_q4_k; break;
         case KRK_DT_Q5_K: fn = quant_q5_k; break;
         case KRK_DT_Q6_K: fn = quant_q6_k; break;

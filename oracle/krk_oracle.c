@@ -1,6 +1,6 @@
 /*
  * krk_oracle.c -- CPU restatement of Kraken's scalar f32 reference for the
- * quantized weight-math path (Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K / IQ4_NL dequant, the strict
+ * quantized weight-math path (Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K / IQ4_NL / IQ4_XS dequant, the strict
  * single-chain GEMV dot, the Q8 activation quantizer and integer dot, the
  * host MoE routing and the routed-expert FFN).
  *
@@ -89,7 +89,7 @@ int orc_block_size(int dt) {
     switch (dt) {
         case ORC_F32: case ORC_F16: return 1;
         case ORC_Q4_0: case ORC_Q8_0: case ORC_IQ4_NL: return 32;
-        case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: return 256;
+        case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_IQ4_XS: return 256;
         default: return 0;
     }
 }
@@ -101,6 +101,7 @@ int orc_block_bytes(int dt) {
         case ORC_Q8_0: return 34;
         case ORC_Q4_K: return 144;
         case ORC_Q5_K: return 176;
+        case ORC_IQ4_XS: return 136;
         case ORC_Q6_K: return 210;
         default: return 0;
     }
@@ -132,6 +133,24 @@ static void deq_iq4_nl(const uint8_t *b, float *y) {
     for (int k = 0; k < 16; k++) {
         y[k] = d * (float)kIq4nl[b[2 + k] & 0xF];
         y[k + 16] = d * (float)kIq4nl[b[2 + k] >> 4];
+    }
+}
+
+/* src/quant.cpp:641-659: 256 values in eight sub-blocks of 32, each with a
+ * 6-bit scale ls (low 4 bits in scales_l, high 2 in scales_h) and IQ4_NL
+ * grid indices; value (d * (ls - 32)) * grid[q]: the first product is exact
+ * (11 + 6 bits), the second rounds. */
+static void deq_iq4_xs(const uint8_t *b, float *y) {
+    float d = ld_f16(b);
+    uint16_t sh = (uint16_t)(b[2] | (b[3] << 8));
+    const uint8_t *sl = b + 4, *qs = b + 8;
+    for (int ib = 0; ib < 8; ib++, y += 32, qs += 16) {
+        int ls = ((sl[ib / 2] >> (4 * (ib % 2))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4);
+        float dl = d * (float)(ls - 32);
+        for (int j = 0; j < 16; j++) {
+            y[j] = dl * (float)kIq4nl[qs[j] & 0xF];
+            y[j + 16] = dl * (float)kIq4nl[qs[j] >> 4];
+        }
     }
 }
 
@@ -226,6 +245,7 @@ static void dequant_block(int dt, const uint8_t *p, float *buf) {
         case ORC_Q4_0: deq_q4_0(p, buf); break;
         case ORC_Q8_0: deq_q8_0(p, buf); break;
         case ORC_IQ4_NL: deq_iq4_nl(p, buf); break;
+        case ORC_IQ4_XS: deq_iq4_xs(p, buf); break;
         case ORC_Q4_K: deq_q4_k(p, buf); break;
         case ORC_Q5_K: deq_q5_k(p, buf); break;
         case ORC_Q6_K: deq_q6_k(p, buf); break;

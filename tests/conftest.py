@@ -32,7 +32,7 @@ def rand_blocks(rng, dt, n_blocks):
     """Random block bytes with finite f16 scale fields (every code pattern)."""
     import oracle
     bb = {oracle.Q4_0: 18, oracle.Q8_0: 34, oracle.Q4_K: 144, oracle.Q5_K: 176, oracle.Q6_K: 210,
-          oracle.IQ4_NL: 18}[dt]
+          oracle.IQ4_NL: 18, oracle.IQ4_XS: 136}[dt]
     w = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
 
     def setf16(off, scale):
@@ -40,7 +40,7 @@ def rand_blocks(rng, dt, n_blocks):
         w[:, off] = v & 0xFF
         w[:, off + 1] = v >> 8
 
-    if dt in (oracle.Q4_0, oracle.Q8_0, oracle.IQ4_NL):
+    if dt in (oracle.Q4_0, oracle.Q8_0, oracle.IQ4_NL, oracle.IQ4_XS):
         setf16(0, 0.01)
     elif dt in (oracle.Q4_K, oracle.Q5_K):
         setf16(0, 0.01)

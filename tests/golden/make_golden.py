@@ -3,7 +3,7 @@ code (oracle/_ref/libkrk_ref.so, compiled by oracle/Makefile from
 /root/reference/src/quant.cpp + src/common.cpp).
 
 The fixture is data only: seeded block bytes and activations (inputs) and
-the reference's outputs for them (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL: dequant_row f32, dequant_row_f16,
+the reference's outputs for them (Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS: dequant_row f32, dequant_row_f16,
 vec_dot in the strict scalar tier, quantize_q8_row, dot_q8_0_q8_scalar).
 It lets the oracle be checked bit for bit where the reference tree is absent
 (the GPU box).  Run:  python tests/golden/make_golden.py
@@ -95,6 +95,20 @@ def main():
         m = n * (i + 1) // 8 // bs * bs
         dots[i] = ref.ref_vec_dot(dt, p(w), p(x), m)
     data.update(iq4_nl_w=w, iq4_nl_x=x, iq4_nl_deq=deq, iq4_nl_deq_f16=h, iq4_nl_dot=dots)
+    # IQ4_XS, also from a stream of its own
+    rngx = np.random.default_rng(0x5EEDB)
+    dt, bs = oracle.IQ4_XS, 256
+    w = rand_blocks(rngx, dt, n // bs)
+    x = rngx.standard_normal(n).astype(np.float32)
+    deq = np.empty(n, np.float32)
+    ref.ref_dequant_row(dt, p(w), p(deq), n)
+    h = np.empty(n, np.uint16)
+    ref.ref_dequant_row_f16(dt, p(w), p(h), n)
+    dots = np.empty(8, np.float32)
+    for i in range(8):
+        m = n * (i + 1) // 8 // bs * bs
+        dots[i] = ref.ref_vec_dot(dt, p(w), p(x), m)
+    data.update(iq4_xs_w=w, iq4_xs_x=x, iq4_xs_deq=deq, iq4_xs_deq_f16=h, iq4_xs_dot=dots)
     np.savez_compressed(OUT, **data)
     print("wrote", OUT, sum(v.nbytes for v in data.values()), "bytes")
 

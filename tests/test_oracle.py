@@ -12,7 +12,7 @@ import oracle as O
 from conftest import rand_blocks
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz")
-FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL]
+FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS]
 
 
 def f16bytes(v):
@@ -276,7 +276,7 @@ def test_q8_0_fixture_quantizer_matches_python_rule():
 def test_oracle_matches_golden_vectors():
     g = np.load(GOLDEN)
     for dt, name in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k"), (O.Q5_K, "q5_k"),
-                     (O.Q6_K, "q6_k"), (O.IQ4_NL, "iq4_nl")):
+                     (O.Q6_K, "q6_k"), (O.IQ4_NL, "iq4_nl"), (O.IQ4_XS, "iq4_xs")):
         w, x = g[f"{name}_w"], g[f"{name}_x"]
         n = x.size
         deq = O.dequant(dt, w, 1, n)[0]
@@ -368,3 +368,23 @@ def test_iq4_nl_closed_form():
     blk[2:] = [(k & 15) | ((15 - k) << 4) for k in range(16)]
     y = O.dequant(O.IQ4_NL, blk, 1, 32)[0]
     assert y[:16].tolist() == grid and y[16:].tolist() == grid[::-1]
+
+
+def test_iq4_xs_closed_form():
+    """IQ4_XS (quant.cpp:641-659): d = 0.5, sub-block ib's 6-bit scale
+    ls = 17 + 5 ib split over scales_l (low nibble) and scales_h (2 bits),
+    indices k and 15 - k: value 0.5 (ls - 32) grid[q]."""
+    grid = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+    blk = np.zeros(136, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    ls = [17 + 5 * ib for ib in range(8)]
+    sh = sum(((l >> 4) & 3) << (2 * ib) for ib, l in enumerate(ls))
+    blk[2], blk[3] = sh & 0xFF, sh >> 8
+    for ib in range(8):
+        blk[4 + ib // 2] |= (ls[ib] & 15) << (4 * (ib % 2))
+        blk[8 + 16 * ib: 24 + 16 * ib] = [(k & 15) | ((15 - k) << 4) for k in range(16)]
+    y = O.dequant(O.IQ4_XS, blk, 1, 256)[0]
+    for ib in range(8):
+        dl = np.float32(0.5) * np.float32(ls[ib] - 32)
+        want = [dl * np.float32(g) for g in grid] + [dl * np.float32(g) for g in grid[::-1]]
+        assert y[32 * ib: 32 * ib + 32].tolist() == [float(np.float32(w)) for w in want], ib
