@@ -69,9 +69,11 @@ hipError_t dequant_rows(int dt, const void *w, int64_t row_bytes, int64_t n_rows
 // quantize_q8_32_d: amax over the 32 values, d = amax / 127 (0 for an
 // all-zero block), codes = round-to-nearest-even(x * (1/d)) clamped to
 // [-127, 127]; a NaN product lands on -127 as the host's cvtps + clamp does.
-template <typename XT>
+// CT int8_t writes the packed codes; CT _Float16 writes the same codes as
+// exact f16 values (the int8 rung's MFMA operand).
+template <typename XT, typename CT>
 __global__ void __launch_bounds__(256) quantize_q8_kernel(const XT *__restrict__ x, int64_t nblk,
-                                                          int8_t *__restrict__ xq,
+                                                          CT *__restrict__ xq,
                                                           float *__restrict__ dx) {
     const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= nblk) return;
@@ -101,9 +103,21 @@ __global__ void __launch_bounds__(256) quantize_q8_kernel(const XT *__restrict__
             packed[k] = word;
         }
     }
-    uint32_t *o = reinterpret_cast<uint32_t *>(xq + b * 32);
+    if constexpr (sizeof(CT) == 1) {
+        uint32_t *o = reinterpret_cast<uint32_t *>(xq + b * 32);
 #pragma unroll
-    for (int k = 0; k < 8; k++) o[k] = packed[k];
+        for (int k = 0; k < 8; k++) o[k] = packed[k];
+    } else {
+        half8 *o = reinterpret_cast<half8 *>(xq + b * 32);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            half8 h;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                h[j] = static_cast<_Float16>(static_cast<int8_t>(packed[2 * k + j / 4] >> (8 * (j % 4))));
+            o[k] = h;
+        }
+    }
 }
 
 hipError_t quantize_q8_rows(const void *x, bool x_f16, int64_t rows, int64_t n, int8_t *xq,
@@ -111,10 +125,23 @@ hipError_t quantize_q8_rows(const void *x, bool x_f16, int64_t rows, int64_t n, 
     const int64_t nblk = rows * (n / 32);
     const dim3 grid(static_cast<unsigned>((nblk + 255) / 256));
     if (x_f16)
-        hipLaunchKernelGGL((quantize_q8_kernel<_Float16>), grid, dim3(256), 0, st,
+        hipLaunchKernelGGL((quantize_q8_kernel<_Float16, int8_t>), grid, dim3(256), 0, st,
                            static_cast<const _Float16 *>(x), nblk, xq, dx);
     else
-        hipLaunchKernelGGL((quantize_q8_kernel<float>), grid, dim3(256), 0, st,
+        hipLaunchKernelGGL((quantize_q8_kernel<float, int8_t>), grid, dim3(256), 0, st,
+                           static_cast<const float *>(x), nblk, xq, dx);
+    return hipGetLastError();
+}
+
+hipError_t quantize_q8_rows_f16codes(const void *x, bool x_f16, int64_t rows, int64_t n,
+                                     _Float16 *xq, float *dx, hipStream_t st) {
+    const int64_t nblk = rows * (n / 32);
+    const dim3 grid(static_cast<unsigned>((nblk + 255) / 256));
+    if (x_f16)
+        hipLaunchKernelGGL((quantize_q8_kernel<_Float16, _Float16>), grid, dim3(256), 0, st,
+                           static_cast<const _Float16 *>(x), nblk, xq, dx);
+    else
+        hipLaunchKernelGGL((quantize_q8_kernel<float, _Float16>), grid, dim3(256), 0, st,
                            static_cast<const float *>(x), nblk, xq, dx);
     return hipGetLastError();
 }

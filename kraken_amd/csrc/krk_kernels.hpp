@@ -83,6 +83,8 @@ hipError_t dequant_rows(int dt, const void *w, int64_t row_bytes, int64_t n_rows
 // Activation quantizer, quant.cpp:2167-2197 semantics.  x in f32 or f16.
 hipError_t quantize_q8_rows(const void *x, bool x_f16, int64_t rows, int64_t n,
                             int8_t *xq, float *dx, hipStream_t st);
+hipError_t quantize_q8_rows_f16codes(const void *x, bool x_f16, int64_t rows, int64_t n,
+                                     _Float16 *xq, float *dx, hipStream_t st);
 
 // Prefill GEMM (f16 MFMA, f32 accumulate) and the Q8_0 x Q8 int8 MFMA rung.
 // out[M, N] = X[M, K] . deq(W)[N, K]^T.  `ws` is device scratch of ws_bytes.
