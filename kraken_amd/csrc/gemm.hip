@@ -272,6 +272,67 @@ template <> struct WStage<DT_IQ4_XS> {
     }
 };
 
+// the byte at p, from the 4-aligned dword that holds it
+__device__ __forceinline__ uint32_t byte_at(const uint8_t *p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    return (ld32(reinterpret_cast<const uint8_t *>(a & ~uintptr_t(3))) >> (8 * (a & 3))) & 0xFF;
+}
+
+// Q2_K: chunk kt = plane j of half h of block kt / 8 (c = 4h + j); half hf
+// takes code bytes 32h + 16hf .. +16 and scale byte 8h + 2j + hf
+template <> struct WStage<DT_Q2_K> {
+    uint32_t q[4], sw, dw;
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        const int c = kt & 7, h = c >> 2, j = c & 3;
+        const uint8_t *b = row + (kt >> 3) * 84;
+        const u32x4 v = ld128(b + 16 + 32 * h + 16 * hf);
+        q[0] = v.x; q[1] = v.y; q[2] = v.z; q[3] = v.w;
+        sw = byte_at(b + 8 * h + 2 * j + hf);
+        dw = ld32(b + 80);
+    }
+    __device__ void decode(int kt, _Float16 (&o)[16]) const {
+        const int j = kt & 3;
+        const float dl = h2f(dw & 0xFFFF) * static_cast<float>(sw & 0xF);
+        const float ml = h2f(dw >> 16) * static_cast<float>(sw >> 4);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                o[4 * t + k] = static_cast<_Float16>(
+                    __builtin_fmaf(dl, static_cast<float>((q[t] >> (8 * k + 2 * j)) & 3), -ml));
+    }
+};
+
+// Q3_K: as Q2_K, plus the hmask bytes 16hf .. +16 (bit 4h + j) and the
+// packed 6-bit scale 8h + 2j + hf
+template <> struct WStage<DT_Q3_K> {
+    uint32_t q[4], m[4], lo, hi, dw;
+    int hf_;
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        const int c = kt & 7, h = c >> 2, j = c & 3;
+        const uint8_t *b = row + (kt >> 3) * 110;
+        load_bytes2<4>(b + 32 + 32 * h + 16 * hf, q);
+        load_bytes2<4>(b + 16 * hf, m);
+        lo = byte_at(b + 96 + 2 * j + hf);
+        hi = byte_at(b + 104 + ((2 * j + hf) & 3));
+        dw = q3k_d_word(b);
+        hf_ = hf;
+    }
+    __device__ void decode(int kt, _Float16 (&o)[16]) const {
+        const int c = kt & 7, h = c >> 2, j = c & 3, i = 8 * h + 2 * j + hf_;
+        const int sc = static_cast<int>(((lo >> (4 * h)) & 0xF) | (((hi >> (2 * (i >> 2))) & 3) << 4));
+        const float dl = h2f(dw & 0xFFFF) * static_cast<float>(sc - 32);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int code = static_cast<int>((q[t] >> (8 * k + 2 * j)) & 3) -
+                                 (((m[t] >> (8 * k + 4 * h + j)) & 1) ? 0 : 4);
+                o[4 * t + k] = static_cast<_Float16>(dl * static_cast<float>(code));
+            }
+    }
+};
+
 // ------------------------------------------------------- activation staging
 template <typename XT> struct XStage;
 template <> struct XStage<_Float16> {
@@ -572,6 +633,8 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
         KRK_GEMM_CASE(DT_Q4_0)
         KRK_GEMM_CASE(DT_IQ4_NL)
         KRK_GEMM_CASE(DT_IQ4_XS)
+        KRK_GEMM_CASE(DT_Q2_K)
+        KRK_GEMM_CASE(DT_Q3_K)
         default: return hipErrorInvalidValue;
     }
 #undef KRK_GEMM_CASE

@@ -422,6 +422,8 @@ template <> struct XRuns<DT_Q6_K> {
         return 256 * (lane >> 2) + 128 * (jp >> 1) + 16 * (jp & 1);
     }
 };
+template <> struct XRuns<DT_Q2_K> : XRuns<DT_Q6_K> {};
+template <> struct XRuns<DT_Q3_K> : XRuns<DT_Q6_K> {};
 template <> struct XRuns<DT_Q4_0> {
     __device__ static int base(int lane) { return 64 * lane; }
 };
@@ -559,6 +561,52 @@ template <int RB> struct LdsDot<DT_Q6_K, RB> {
         }
     }
 };
+
+// Q2_K / Q3_K: Q6_K's x runs and plane sums, their own codes and fold
+template <int DT, int RB> struct LdsDotPlanes {
+    using F = WaveFmt<DT>;
+    static constexpr int NS = 4;
+    __device__ static void sums(const float *xl, int b0, float (&xs)[NS]) {
+        LdsDot<DT_Q6_K, RB>::sums(xl, b0, xs);
+    }
+    __device__ static void run(const uint32_t (&raw)[RB][F::NRAW], int jp, const float *xl, int b0,
+                               const float (&xs)[NS], float (&v)[RB]) {
+        float sq[RB][4];
+#pragma unroll
+        for (int r = 0; r < RB; r++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) sq[r][q] = 0.0f;
+        const int h = jp >> 1;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            float xq[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const floatx4 u = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * j + 4 * t));
+                xq[j][0] = u.x; xq[j][1] = u.y; xq[j][2] = u.z; xq[j][3] = u.w;
+            }
+#pragma unroll
+            for (int r = 0; r < RB; r++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    uint32_t q, m;
+                    if constexpr (DT == DT_Q2_K) {
+                        q = plane2(raw[r][t], j);
+                        m = 0x00030003u;
+                    } else {
+                        q = plane3(raw[r][t] >> (2 * j), raw[r][4 + t], 4 * h + j);
+                        m = 0x00070007u;
+                    }
+                    sq[r][j] = mix2(q & m, xq[j][0], xq[j][2], sq[r][j]);
+                    sq[r][j] = mix2((q >> 8) & m, xq[j][1], xq[j][3], sq[r][j]);
+                }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; r++) v[r] = F::fold(raw[r], jp, sq[r], xs);
+    }
+};
+template <int RB> struct LdsDot<DT_Q2_K, RB> : LdsDotPlanes<DT_Q2_K, RB> {};
+template <int RB> struct LdsDot<DT_Q3_K, RB> : LdsDotPlanes<DT_Q3_K, RB> {};
 
 template <int RB> struct LdsDot<DT_Q4_0, RB> {
     using F = WaveFmt<DT_Q4_0>;
@@ -1233,6 +1281,8 @@ static hipError_t dispatch_dt(int dt, const SegTable &t, hipStream_t st) {
         case DT_Q4_0: return dispatch_mr<DT_Q4_0, XT, OT>(t, st);
         case DT_IQ4_NL: return dispatch_mr<DT_IQ4_NL, XT, OT>(t, st);
         case DT_IQ4_XS: return dispatch_mr<DT_IQ4_XS, XT, OT>(t, st);
+        case DT_Q2_K: return dispatch_mr<DT_Q2_K, XT, OT>(t, st);
+        case DT_Q3_K: return dispatch_mr<DT_Q3_K, XT, OT>(t, st);
         case DT_Q8_0: return dispatch_mr<DT_Q8_0, XT, OT>(t, st);
         default: return hipErrorInvalidValue;
     }

@@ -20,12 +20,15 @@ namespace krk {
 
 // ---------------------------------------------------------------- geometry --
 __host__ __device__ constexpr int blk_vals(int dt) {
-    return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K || dt == DT_IQ4_XS ? 256
+    return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K || dt == DT_IQ4_XS || dt == DT_Q2_K ||
+                   dt == DT_Q3_K
+               ? 256
            : (dt == DT_Q4_0 || dt == DT_Q8_0 || dt == DT_IQ4_NL) ? 32
                                                                   : 1;
 }
 __host__ __device__ constexpr int blk_bytes(int dt) {
     return dt == DT_Q4_K ? 144 : dt == DT_Q5_K ? 176 : dt == DT_Q6_K ? 210 : dt == DT_IQ4_XS ? 136
+         : dt == DT_Q2_K ? 84 : dt == DT_Q3_K ? 110
          : dt == DT_Q4_0 || dt == DT_IQ4_NL ? 18
          : dt == DT_Q8_0 ? 34 : dt == DT_F16 ? 2 : 4;
 }
@@ -141,6 +144,42 @@ __device__ __forceinline__ void dequant_chunk<DT_Q6_K>(const uint8_t *b, int c, 
         // (d * sc) * (q - 32), left to right as the host writes it
         const float ds = d * static_cast<float>(sc[l / 16]);
         y[l] = ds * static_cast<float>(q - 32);
+    }
+}
+
+// Q2_K and Q3_K share Q6_K's four planes: chunk c = 4h + j holds values
+// 128h + 32j + l whose code is bit pair j of byte 32h + l of the 64 code
+// bytes, with scale 8h + 2j + l / 16.
+// src/quant.cpp:398-423: value (d * (sc & 15)) * q - dmin * (sc >> 4); both
+// products are exact, so the FMA rounds as the host's multiply-subtract does.
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_Q2_K>(const uint8_t *b, int c, float *y) {
+    const float d = ldh(b + 80), dmin = ldh(b + 82);
+    const int h = c >> 2, j = c & 3;
+    const uint8_t *q = b + 16 + 32 * h;
+    for (int l = 0; l < 32; l++) {
+        const int sc = b[8 * h + 2 * j + l / 16];
+        y[l] = __builtin_fmaf(d * static_cast<float>(sc & 0xF), static_cast<float>((q[l] >> (2 * j)) & 3),
+                              -(dmin * static_cast<float>(sc >> 4)));
+    }
+}
+
+// Q3_K 6-bit scale i from the 12 packed bytes r (quant.cpp:520-528)
+__device__ __forceinline__ int q3k_scale(const uint8_t *r, int i) {
+    return ((r[i & 7] >> (4 * (i >> 3))) & 0xF) | (((r[8 + (i & 3)] >> (2 * (i >> 2))) & 3) << 4);
+}
+
+// src/quant.cpp:514-554: code (q >> 2j & 3) - (hmask[l] bit 4h + j ? 0 : 4),
+// value (d * (sc - 32)) * code
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_Q3_K>(const uint8_t *b, int c, float *y) {
+    const float d = ldh(b + 108);
+    const int h = c >> 2, j = c & 3;
+    const uint8_t *q = b + 32 + 32 * h;
+    for (int l = 0; l < 32; l++) {
+        const float dl = d * static_cast<float>(q3k_scale(b + 96, 8 * h + 2 * j + l / 16) - 32);
+        const int code = ((q[l] >> (2 * j)) & 3) - (((b[l] >> (4 * h + j)) & 1) ? 0 : 4);
+        y[l] = dl * static_cast<float>(code);
     }
 }
 
@@ -345,6 +384,106 @@ template <> struct LaneFmt<DT_Q6_K> {
             const float ds = d * static_cast<float>(s8);
             a = __builtin_fmaf(ds * kTwo24, s[qd], a);
             a = __builtin_fmaf(-32.0f * ds, xs[qd], a);
+        }
+        return a;
+    }
+};
+
+// Two-bit planes (Q2_K, Q3_K).  Plane j of four code bytes q as byte-parallel
+// codes; Q3_K adds 4 where the hmask bit is set (non-negative codes 0..7,
+// the -4 going into the x-sum term).
+__device__ __forceinline__ uint32_t plane2(uint32_t q, int j) { return (q >> (2 * j)) & 0x03030303u; }
+__device__ __forceinline__ uint32_t plane3(uint32_t q, uint32_t hm, int bit) {
+    return ((q >> 0) & 0x03030303u) | (((hm >> bit) & 0x01010101u) << 2);
+}
+// Q2_K (scale, min) of scale byte idx (0..7) held in two dwords
+__device__ __forceinline__ uint32_t byte_of(uint32_t w0, uint32_t w1, int idx) {
+    return ((idx < 4 ? w0 : w1) >> (8 * (idx & 3))) & 0xFF;
+}
+// Q3_K scale 8h + b (b = 2j + s, 0..7) from the packed dwords R0, R1, R2 of
+// bytes 96..107: low nibble of byte b at 4h, two high bits from byte 8 + b % 4
+// at 4h + 2 (j / 2)
+__device__ __forceinline__ int q3k_scale_w(uint32_t R0, uint32_t R1, uint32_t R2, int h, int b) {
+    const uint32_t lo = (byte_of(R0, R1, b) >> (4 * h)) & 0xF;
+    const uint32_t hi = (R2 >> (8 * (b & 3) + 4 * h + 2 * (b >> 2))) & 3;
+    return static_cast<int>(lo | (hi << 4));
+}
+
+// Q3_K's d (bytes 108..109) in the low half of a dword, read from the
+// 4-aligned dword that holds them, which never leaves the block's page
+__device__ __forceinline__ uint32_t q3k_d_word(const uint8_t *blk) {
+    const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 108);
+    return ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+}
+
+// Q2_K lane view: piece p, half h = p / 4, bytes o = 8 (p % 4) .. +7 of the
+// half's 32 code bytes; run r = plane j (values 128h + 32j + o + t).
+template <> struct LaneFmt<DT_Q2_K> {
+    static constexpr int LPB = 8, NG = 4, RUN = 8, NRUN = 4, NRAW = 5;
+    __device__ static int run_start(int p, int r) { return 128 * (p >> 2) + 32 * r + 8 * (p & 3); }
+    __device__ static int group_of(int i) { return i >> 3; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int p) {
+        const int h = p >> 2, o = 8 * (p & 3);
+        const u32x2 q = ld64(blk + 16 + 32 * h + o), sc = ld64(blk + 8 * h);
+        raw[0] = q.x; raw[1] = q.y; raw[2] = sc.x; raw[3] = sc.y;
+        raw[4] = ld32(blk + 80);
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int p, const float (&xv)[32],
+                                const float (&xs)[NG]) {
+        const float d = h2f(raw[4] & 0xFFFF), dmin = h2f(raw[4] >> 16);
+        const int s = (p & 3) >> 1;
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float sj = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint32_t q = plane2(raw[t], j);
+                const float *x = &xv[8 * j + 4 * t];
+                sj = mix2(q & 0x00030003u, x[0], x[2], sj);
+                sj = mix2((q >> 8) & 0x00030003u, x[1], x[3], sj);
+            }
+            const uint32_t sc = byte_of(raw[2], raw[3], 2 * j + s);
+            a = __builtin_fmaf(d * static_cast<float>(sc & 0xF) * kTwo24, sj, a);
+            a = __builtin_fmaf(-(dmin * static_cast<float>(sc >> 4)), xs[j], a);
+        }
+        return a;
+    }
+};
+
+// Q3_K lane view: as Q2_K's, with the hmask bytes o .. +7 (bit 4h + j)
+template <> struct LaneFmt<DT_Q3_K> {
+    static constexpr int LPB = 8, NG = 4, RUN = 8, NRUN = 4, NRAW = 8;
+    __device__ static int run_start(int p, int r) { return 128 * (p >> 2) + 32 * r + 8 * (p & 3); }
+    __device__ static int group_of(int i) { return i >> 3; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int p) {
+        const int h = p >> 2, o = 8 * (p & 3);
+        uint32_t q[2], m[2], sc[3];
+        load_bytes2<2>(blk + 32 + 32 * h + o, q);
+        load_bytes2<2>(blk + o, m);
+        load_bytes2<3>(blk + 96, sc);
+        raw[0] = q[0]; raw[1] = q[1]; raw[2] = m[0]; raw[3] = m[1];
+        raw[4] = sc[0]; raw[5] = sc[1]; raw[6] = sc[2];
+        raw[7] = q3k_d_word(blk);
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int p, const float (&xv)[32],
+                                const float (&xs)[NG]) {
+        const float d = h2f(raw[7] & 0xFFFF);
+        const int h = p >> 2, s = (p & 3) >> 1;
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float sj = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint32_t q = plane3(raw[t] >> (2 * j), raw[2 + t], 4 * h + j);
+                const float *x = &xv[8 * j + 4 * t];
+                sj = mix2(q & 0x00070007u, x[0], x[2], sj);
+                sj = mix2((q >> 8) & 0x00070007u, x[1], x[3], sj);
+            }
+            const float dl = d * static_cast<float>(q3k_scale_w(raw[4], raw[5], raw[6], h, 2 * j + s) - 32);
+            a = __builtin_fmaf(dl * kTwo24, sj, a);
+            a = __builtin_fmaf(-4.0f * dl, xs[j], a);
         }
         return a;
     }
@@ -636,6 +775,107 @@ template <> struct WaveFmt<DT_Q6_K> {
             a = __builtin_fmaf(-32.0f * ds, xs[qd], a);
         }
         return a;
+    }
+};
+
+// Q2_K / Q3_K wave view, as Q6_K's: slot jp, half h = jp / 2, s = jp % 2,
+// values 128h + 32j + 16s + t (plane j = run, t = 0..15), code bytes
+// 32h + 16s .. +16
+template <> struct WaveFmt<DT_Q2_K> {
+    static constexpr int LPB = 4, BPS = 16, NG = 4, RUN = 16, NRUN = 4, NRAW = 7;
+    __device__ static int blk_of(int lane) { return lane >> 2; }
+    __device__ static int slot_of(int lane) { return lane & 3; }
+    __device__ static int run_start(int jp, int r) { return 128 * (jp >> 1) + 32 * r + 16 * (jp & 1); }
+    __device__ static int group_of(int i) { return i >> 4; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int jp) {
+        const int h = jp >> 1, s = jp & 1;
+        const u32x4 q = ld128(blk + 16 + 32 * h + 16 * s);
+        const u32x2 sc = ld64(blk + 8 * h);
+        raw[0] = q.x; raw[1] = q.y; raw[2] = q.z; raw[3] = q.w;
+        raw[4] = sc.x; raw[5] = sc.y; raw[6] = ld32(blk + 80);
+    }
+    __device__ static void plane_sums(const uint32_t (&raw)[NRAW], const float (&xv)[64], float (&sq)[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const uint32_t q = plane2(raw[t], j);
+                const float *x = &xv[16 * j + 4 * t];
+                a = mix2(q & 0x00030003u, x[0], x[2], a);
+                a = mix2((q >> 8) & 0x00030003u, x[1], x[3], a);
+            }
+            sq[j] = a;
+        }
+    }
+    __device__ static float fold(const uint32_t (&raw)[NRAW], int jp, const float (&sq)[4], const float (&xs)[NG]) {
+        const float d = h2f(raw[6] & 0xFFFF), dmin = h2f(raw[6] >> 16);
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t sc = byte_of(raw[4], raw[5], 2 * j + (jp & 1));
+            a = __builtin_fmaf(d * static_cast<float>(sc & 0xF) * kTwo24, sq[j], a);
+            a = __builtin_fmaf(-(dmin * static_cast<float>(sc >> 4)), xs[j], a);
+        }
+        return a;
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int jp, const float (&xv)[64],
+                                const float (&xs)[NG]) {
+        float sq[4];
+        plane_sums(raw, xv, sq);
+        return fold(raw, jp, sq, xs);
+    }
+};
+
+template <> struct WaveFmt<DT_Q3_K> {
+    static constexpr int LPB = 4, BPS = 16, NG = 4, RUN = 16, NRUN = 4, NRAW = 12;
+    __device__ static int blk_of(int lane) { return lane >> 2; }
+    __device__ static int slot_of(int lane) { return lane & 3; }
+    __device__ static int run_start(int jp, int r) { return 128 * (jp >> 1) + 32 * r + 16 * (jp & 1); }
+    __device__ static int group_of(int i) { return i >> 4; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int jp) {
+        const int h = jp >> 1, s = jp & 1;
+        uint32_t q[4], m[4], sc[3];
+        load_bytes2<4>(blk + 32 + 32 * h + 16 * s, q);
+        load_bytes2<4>(blk + 16 * s, m);
+        load_bytes2<3>(blk + 96, sc);
+#pragma unroll
+        for (int k = 0; k < 4; k++) { raw[k] = q[k]; raw[4 + k] = m[k]; }
+        raw[8] = sc[0]; raw[9] = sc[1]; raw[10] = sc[2];
+        raw[11] = q3k_d_word(blk);
+    }
+    __device__ static void plane_sums(const uint32_t (&raw)[NRAW], int jp, const float (&xv)[64], float (&sq)[4]) {
+        const int h = jp >> 1;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const uint32_t q = plane3(raw[t] >> (2 * j), raw[4 + t], 4 * h + j);
+                const float *x = &xv[16 * j + 4 * t];
+                a = mix2(q & 0x00070007u, x[0], x[2], a);
+                a = mix2((q >> 8) & 0x00070007u, x[1], x[3], a);
+            }
+            sq[j] = a;
+        }
+    }
+    __device__ static float fold(const uint32_t (&raw)[NRAW], int jp, const float (&sq)[4], const float (&xs)[NG]) {
+        const float d = h2f(raw[11] & 0xFFFF);
+        const int h = jp >> 1;
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float dl = d * static_cast<float>(q3k_scale_w(raw[8], raw[9], raw[10], h, 2 * j + (jp & 1)) - 32);
+            a = __builtin_fmaf(dl * kTwo24, sq[j], a);
+            a = __builtin_fmaf(-4.0f * dl, xs[j], a);
+        }
+        return a;
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int jp, const float (&xv)[64],
+                                const float (&xs)[NG]) {
+        float sq[4];
+        plane_sums(raw, jp, xv, sq);
+        return fold(raw, jp, sq, xs);
     }
 };
 

@@ -191,6 +191,79 @@ void quant_iq4_nl(const float *v, int64_t n, uint8_t *dst) {
     }
 }
 
+// Q2_K (84 B / 256 values): per 16-value group a 4-bit scale of
+// (max - min) / 3 and a 4-bit min of -min (min clamped to <= 0) on grids of
+// d = max scale / 15 and dmin = max min / 15; codes round((v + m) / s) in 0..3.
+void quant_q2_k(const float *v, int64_t n, uint8_t *dst) {
+    for (int64_t b = 0; b < n; b += 256, dst += 84) {
+        double sc[16], mn[16], smax = 0.0, mmax = 0.0;
+        for (int g = 0; g < 16; g++) {
+            double lo = 0.0, hi = 0.0;
+            for (int l = 0; l < 16; l++) {
+                lo = std::min(lo, double(v[b + 16 * g + l]));
+                hi = std::max(hi, double(v[b + 16 * g + l]));
+            }
+            sc[g] = (hi - lo) / 3.0;
+            mn[g] = -lo;
+            smax = std::max(smax, sc[g]);
+            mmax = std::max(mmax, mn[g]);
+        }
+        const uint16_t hd = f64_to_half(smax / 15.0), hm = f64_to_half(mmax / 15.0);
+        const double d = half_to_f64(hd), dmin = half_to_f64(hm);
+        put16(dst + 80, hd);
+        put16(dst + 82, hm);
+        for (int k = 0; k < 64; k++) dst[16 + k] = 0;
+        // group g = value index / 16 = 8h + 2j + s
+        for (int g = 0; g < 16; g++) {
+            const int is = d > 0 ? clampi(std::nearbyint(sc[g] / d), 0, 15) : 0;
+            const int im = dmin > 0 ? clampi(std::nearbyint(mn[g] / dmin), 0, 15) : 0;
+            dst[g] = static_cast<uint8_t>(is | (im << 4));
+            const double dl = d * is, ml = dmin * im;
+            const int h = g >> 3, j = (g >> 1) & 3, s = g & 1;
+            for (int l = 0; l < 16; l++) {
+                const int q = dl > 0 ? clampi(std::nearbyint((double(v[b + 16 * g + l]) + ml) / dl), 0, 3) : 0;
+                dst[16 + 32 * h + 16 * s + l] = static_cast<uint8_t>(dst[16 + 32 * h + 16 * s + l] | (q << (2 * j)));
+            }
+        }
+    }
+}
+
+// Q3_K (110 B / 256 values): per 16-value group a positive scale amax / 4
+// on a 6-bit grid (stored sc - 32 in 1..31 of d = max scale / 31); codes
+// round(v / s) in -4..3, stored as 2 bits plus an hmask bit set for codes >= 0.
+void quant_q3_k(const float *v, int64_t n, uint8_t *dst) {
+    for (int64_t b = 0; b < n; b += 256, dst += 110) {
+        double sc[16], smax = 0.0;
+        for (int g = 0; g < 16; g++) {
+            double amax = 0.0;
+            for (int l = 0; l < 16; l++) amax = std::max(amax, std::fabs(double(v[b + 16 * g + l])));
+            sc[g] = amax / 4.0;
+            smax = std::max(smax, sc[g]);
+        }
+        const uint16_t hd = f64_to_half(smax / 31.0);
+        const double d = half_to_f64(hd);
+        for (int k = 0; k < 108; k++) dst[k] = 0;
+        put16(dst + 108, hd);
+        for (int g = 0; g < 16; g++) {
+            const int is = d > 0 ? clampi(std::nearbyint(sc[g] / d), 1, 31) : 1;
+            const int s6 = is + 32;
+            if (g < 8)
+                dst[96 + g] = static_cast<uint8_t>(dst[96 + g] | (s6 & 15));
+            else
+                dst[96 + g - 8] = static_cast<uint8_t>(dst[96 + g - 8] | ((s6 & 15) << 4));
+            dst[104 + (g & 3)] = static_cast<uint8_t>(dst[104 + (g & 3)] | (((s6 >> 4) & 3) << (2 * (g >> 2))));
+            const double dl = d * is;
+            const int h = g >> 3, j = (g >> 1) & 3, s = g & 1;
+            for (int l = 0; l < 16; l++) {
+                const int c = dl > 0 ? clampi(std::nearbyint(double(v[b + 16 * g + l]) / dl), -4, 3) : 0;
+                const int q = c >= 0 ? c : c + 4;
+                dst[32 + 32 * h + 16 * s + l] = static_cast<uint8_t>(dst[32 + 32 * h + 16 * s + l] | (q << (2 * j)));
+                if (c >= 0) dst[16 * s + l] = static_cast<uint8_t>(dst[16 * s + l] | (1 << (4 * h + j)));
+            }
+        }
+    }
+}
+
 // IQ4_XS (136 B / 256 values): per 32-value sub-block a positive scale
 // s = amax / 127 on a 6-bit grid ls - 32 in 1..31 of d = max s / 31, then
 // IQ4_NL's nearest grid index of v / (d (ls - 32)).
@@ -346,6 +419,8 @@ extern "C" int krk_quantize_weights(int wt, const float *v, int64_t n_rows,
         case KRK_DT_Q4_0: fn = quant_q4_0; break;
         case KRK_DT_IQ4_NL: fn = quant_iq4_nl; break;
         case KRK_DT_IQ4_XS: fn = quant_iq4_xs; break;
+        case KRK_DT_Q2_K: fn = quant_q2_k; break;
+        case KRK_DT_Q3_K: fn = quant_q3_k; break;
         case KRK_DT_Q4_K: fn = quant_q4_k; break;
         case KRK_DT_Q5_K: fn = quant_q5_k; break;
         case KRK_DT_Q6_K: fn = quant_q6_k; break;

@@ -89,7 +89,7 @@ int orc_block_size(int dt) {
     switch (dt) {
         case ORC_F32: case ORC_F16: return 1;
         case ORC_Q4_0: case ORC_Q8_0: case ORC_IQ4_NL: return 32;
-        case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_IQ4_XS: return 256;
+        case ORC_Q2_K: case ORC_Q3_K: case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_IQ4_XS: return 256;
         default: return 0;
     }
 }
@@ -99,6 +99,8 @@ int orc_block_bytes(int dt) {
         case ORC_F16: return 2;
         case ORC_Q4_0: case ORC_IQ4_NL: return 18;
         case ORC_Q8_0: return 34;
+        case ORC_Q2_K: return 84;
+        case ORC_Q3_K: return 110;
         case ORC_Q4_K: return 144;
         case ORC_Q5_K: return 176;
         case ORC_IQ4_XS: return 136;
@@ -152,6 +154,55 @@ static void deq_iq4_xs(const uint8_t *b, float *y) {
             y[j + 16] = dl * (float)kIq4nl[qs[j] >> 4];
         }
     }
+}
+
+/* src/quant.cpp:398-423.  84 B / 256: 16 scale bytes (low nibble scale,
+ * high nibble min), 64 bytes of 2-bit codes, f16 d at 80 and dmin at 82.
+ * Value index 128g + 32j + 16s + l takes bits 2j of qs[32g + 16s + l] and
+ * scale byte 8g + 2j + s; value (d*sc)*q - dmin*m, where d*sc (<= 15 bits)
+ * and its product with q (<= 17) are exact, so only the subtraction rounds
+ * and an FMA gives the same bits. */
+static void deq_q2_k(const uint8_t *b, float *y) {
+    float d = ld_f16(b + 80), dmin = ld_f16(b + 82);
+    for (int g = 0; g < 2; g++)
+        for (int j = 0; j < 4; j++)
+            for (int s = 0; s < 2; s++) {
+                uint8_t sc = b[8 * g + 2 * j + s];
+                float dl = d * (float)(sc & 0xF), ml = dmin * (float)(sc >> 4);
+                const uint8_t *q = b + 16 + 32 * g + 16 * s;
+                float *yy = y + 128 * g + 32 * j + 16 * s;
+                for (int l = 0; l < 16; l++) yy[l] = fmaf(dl, (float)((q[l] >> (2 * j)) & 3), -ml);
+            }
+}
+
+/* Q3_K 6-bit scale i (0..15) from the 12 packed bytes (quant.cpp:520-528):
+ * low 4 bits from byte i (i < 8) or the high nibble of byte i - 8, high 2
+ * bits from byte 8 + i % 4 at bit 2 (i / 4). */
+static int q3k_scale(const uint8_t *r, int i) {
+    int lo = i < 8 ? (r[i] & 0xF) : (r[i - 8] >> 4);
+    int hi = (r[8 + (i & 3)] >> (2 * (i >> 2))) & 3;
+    return lo | (hi << 4);
+}
+
+/* src/quant.cpp:514-554.  110 B / 256: hmask[32], 2-bit qs[64], 12 bytes of
+ * 6-bit scales, f16 d at 108.  Value index 128n + 32j + 16s + l: code
+ * (qs[32n + 16s + l] >> 2j) & 3, minus 4 unless bit 4n + j of
+ * hmask[16s + l] is set; scale 8n + 2j + s; value (d*(sc - 32))*code, the
+ * first product exact (11 + 6 bits), the second rounding once. */
+static void deq_q3_k(const uint8_t *b, float *y) {
+    float d = ld_f16(b + 108);
+    const uint8_t *hm = b, *qs = b + 32, *sr = b + 96;
+    for (int n = 0; n < 2; n++)
+        for (int j = 0; j < 4; j++)
+            for (int s = 0; s < 2; s++) {
+                float dl = d * (float)(q3k_scale(sr, 8 * n + 2 * j + s) - 32);
+                const uint8_t *q = qs + 32 * n + 16 * s;
+                float *yy = y + 128 * n + 32 * j + 16 * s;
+                for (int l = 0; l < 16; l++) {
+                    int c = ((q[l] >> (2 * j)) & 3) - ((hm[16 * s + l] >> (4 * n + j)) & 1 ? 0 : 4);
+                    yy[l] = dl * (float)c;
+                }
+            }
 }
 
 /* src/quant.cpp:381-387 */
@@ -246,6 +297,8 @@ static void dequant_block(int dt, const uint8_t *p, float *buf) {
         case ORC_Q8_0: deq_q8_0(p, buf); break;
         case ORC_IQ4_NL: deq_iq4_nl(p, buf); break;
         case ORC_IQ4_XS: deq_iq4_xs(p, buf); break;
+        case ORC_Q2_K: deq_q2_k(p, buf); break;
+        case ORC_Q3_K: deq_q3_k(p, buf); break;
         case ORC_Q4_K: deq_q4_k(p, buf); break;
         case ORC_Q5_K: deq_q5_k(p, buf); break;
         case ORC_Q6_K: deq_q6_k(p, buf); break;

@@ -1,5 +1,5 @@
-"""Writes tests/golden/gguf_q8_0_blocks.npz: the raw bytes of real Q8_0 and
-IQ4_NL tensors from the reference's own test checkpoints (TinyLLama-v0
+"""Writes tests/golden/gguf_q8_0_blocks.npz: the raw bytes of real Q8_0,
+IQ4_NL and Q3_K tensors from the reference's own test checkpoints (TinyLLama-v0
 Q8_0, tinystories-gpt Q2_K mix, tiny-llama3 Q3_K_M: data the reference's
 tests read), taken with this library's GGUF reader,
 which tests/test_gguf.py checks against the reference's reader.  The GPU
@@ -23,7 +23,9 @@ PICK = [("TinyLLama-v0.Q8_0.gguf", "blk.0.attn_q.weight", K.Q8_0),
         ("TinyLLama-v0.Q8_0.gguf", "blk.7.ffn_gate.weight", K.Q8_0),
         ("tinystories-gpt-0.1-3m.Q2_K.gguf", "blk.0.attn_qkv.weight", K.IQ4_NL),
         ("tinystories-gpt-0.1-3m.Q2_K.gguf", "blk.0.ffn_up.weight", K.IQ4_NL),
-        ("tiny-llama3-test-Q3_K_M.gguf", "blk.0.attn_q.weight", K.IQ4_NL)]
+        ("tiny-llama3-test-Q3_K_M.gguf", "blk.0.attn_q.weight", K.IQ4_NL),
+        ("tinystories-gpt-0.1-3m.Q2_K.gguf", "blk.0.ffn_down.weight", K.Q3_K),
+        ("tinystories-gpt-0.1-3m.Q2_K.gguf", "blk.7.ffn_down.weight", K.Q3_K)]
 
 
 def main():

@@ -12,7 +12,7 @@ import oracle as O
 from conftest import rand_blocks
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz")
-FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS]
+FMTS = [O.Q4_0, O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS]
 
 
 def f16bytes(v):
@@ -276,7 +276,8 @@ def test_q8_0_fixture_quantizer_matches_python_rule():
 def test_oracle_matches_golden_vectors():
     g = np.load(GOLDEN)
     for dt, name in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k"), (O.Q5_K, "q5_k"),
-                     (O.Q6_K, "q6_k"), (O.IQ4_NL, "iq4_nl"), (O.IQ4_XS, "iq4_xs")):
+                     (O.Q6_K, "q6_k"), (O.IQ4_NL, "iq4_nl"), (O.IQ4_XS, "iq4_xs"), (O.Q2_K, "q2_k"),
+                     (O.Q3_K, "q3_k")):
         w, x = g[f"{name}_w"], g[f"{name}_x"]
         n = x.size
         deq = O.dequant(dt, w, 1, n)[0]
@@ -388,3 +389,59 @@ def test_iq4_xs_closed_form():
         dl = np.float32(0.5) * np.float32(ls[ib] - 32)
         want = [dl * np.float32(g) for g in grid] + [dl * np.float32(g) for g in grid[::-1]]
         assert y[32 * ib: 32 * ib + 32].tolist() == [float(np.float32(w)) for w in want], ib
+
+
+def test_q2_k_closed_form():
+    """Q2_K (quant.cpp:398-423): d = 0.25, dmin = 0.5; scale byte i holds
+    scale i % 16 and min 15 - i % 16; qs byte l holds codes (l + k) % 4 in
+    its four bit pairs k.  Value index 128g + 32j + 16s + l: code bit pair
+    j of qs[32g + 16s + l], scale byte 8g + 2j + s; value d sc q - dmin m."""
+    blk = np.zeros(84, np.uint8)
+    for i in range(16):
+        blk[i] = (i & 15) | ((15 - i) << 4)
+    for l in range(64):
+        blk[16 + l] = sum(((l + k) % 4) << (2 * k) for k in range(4))
+    blk[80:82] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    blk[82:84] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    y = O.dequant(O.Q2_K, blk, 1, 256)[0]
+    for g in range(2):
+        for j in range(4):
+            for s in range(2):
+                i = 8 * g + 2 * j + s
+                for l in range(16):
+                    q = (16 * s + l + j) % 4
+                    want = 0.25 * i * q - 0.5 * (15 - i)
+                    assert y[128 * g + 32 * j + 16 * s + l] == np.float32(want), (g, j, s, l)
+
+
+def test_q3_k_closed_form():
+    """Q3_K (quant.cpp:514-554): d = 0.5, the sixteen 6-bit scales
+    sc_i = 7 + 3i (so sc - 32 crosses zero) packed as the reference packs
+    them (low nibbles in bytes 0..7, high 2-bit pairs in bytes 8..11);
+    qs byte l holds codes (l + k) % 4; hmask bit 4n + j of byte m is set when
+    (m + n + j) is even.  Value (d (sc - 32)) (code - (hbit ? 0 : 4))."""
+    sc = [7 + 3 * i for i in range(16)]
+    blk = np.zeros(110, np.uint8)
+    for m in range(32):
+        blk[m] = sum(1 << (4 * n + j) for n in range(2) for j in range(4) if (m + n + j) % 2 == 0)
+    for l in range(64):
+        blk[32 + l] = sum(((l + k) % 4) << (2 * k) for k in range(4))
+    r = [0] * 12
+    for i in range(16):
+        if i < 8:
+            r[i] |= sc[i] & 15
+        else:
+            r[i - 8] |= (sc[i] & 15) << 4
+        r[8 + i % 4] |= ((sc[i] >> 4) & 3) << (2 * (i // 4))
+    blk[96:108] = r
+    blk[108:110] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    y = O.dequant(O.Q3_K, blk, 1, 256)[0]
+    for n in range(2):
+        for j in range(4):
+            for s in range(2):
+                i = 8 * n + 2 * j + s
+                for l in range(16):
+                    m = 16 * s + l
+                    code = (32 * n + m + j) % 4 - (0 if (m + n + j) % 2 == 0 else 4)
+                    want = np.float32(0.5 * (sc[i] - 32)) * np.float32(code)
+                    assert y[128 * n + 32 * j + 16 * s + l] == want, (n, j, s, l)
