@@ -28,7 +28,7 @@ extern "C" {
 #endif
 
 /* GGUF type ids; these block formats (plus F16/F32 activations) are on
- * this path.  include/krk/quant.hpp:16-47.  Q2_K, Q3_K, Q5_K, IQ4_NL and IQ4_XS are served by
+ * this path.  include/krk/quant.hpp:16-47.  Q2_K, Q3_K, Q5_K, IQ4_NL, IQ4_XS and MXFP4 are served by
  * the dequant, GEMV (rows 1..8, exact prefill) and MFMA GEMM paths;
  * moe_dispatch banks take Q4_0 / Q8_0 / Q4_K / Q6_K, the int8 rung Q8_0. */
 enum krk_dtype {
@@ -42,7 +42,8 @@ enum krk_dtype {
     KRK_DT_Q5_K = 13,
     KRK_DT_Q6_K = 14,
     KRK_DT_IQ4_NL = 20,
-    KRK_DT_IQ4_XS = 23
+    KRK_DT_IQ4_XS = 23,
+    KRK_DT_MXFP4 = 39
 };
 
 /* Activation type of a handle: backend.hpp `act_type()` (F16 on the

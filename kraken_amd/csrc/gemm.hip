@@ -272,11 +272,30 @@ template <> struct WStage<DT_IQ4_XS> {
     }
 };
 
-// the byte at p, from the 4-aligned dword that holds it
-__device__ __forceinline__ uint32_t byte_at(const uint8_t *p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    return (ld32(reinterpret_cast<const uint8_t *>(a & ~uintptr_t(3))) >> (8 * (a & 3))) & 0xFF;
-}
+// MXFP4: chunk kt is block kt (byte aligned, 17 bytes); half hf takes the
+// low (0) or high nibbles; value grid[q] * 2^(e - 128), rounded once to f16
+template <> struct WStage<DT_MXFP4> {
+    uint32_t q[4], e;
+    int hf_;
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        const uint8_t *b = row + kt * 17;
+        load_bytes2<4>(b + 1, q);
+        e = byte_at(b);
+        hf_ = hf;
+    }
+    __device__ void decode(int, _Float16 (&o)[16]) const {
+        const float d = e8m0_half(e);
+        const int sh = hf_ * 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t g = fp4_lookup((q[t] >> sh) & 0x0F0F0F0Fu);   // grid + 12 per byte
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                o[4 * t + k] = static_cast<_Float16>(
+                    static_cast<float>(static_cast<int>((g >> (8 * k)) & 0xFF) - 12) * d);
+        }
+    }
+};
 
 // Q2_K: chunk kt = plane j of half h of block kt / 8 (c = 4h + j); half hf
 // takes code bytes 32h + 16hf .. +16 and scale byte 8h + 2j + hf
@@ -635,6 +654,7 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
         KRK_GEMM_CASE(DT_IQ4_XS)
         KRK_GEMM_CASE(DT_Q2_K)
         KRK_GEMM_CASE(DT_Q3_K)
+        KRK_GEMM_CASE(DT_MXFP4)
         default: return hipErrorInvalidValue;
     }
 #undef KRK_GEMM_CASE

@@ -433,6 +433,9 @@ template <> struct XRuns<DT_IQ4_NL> {
 template <> struct XRuns<DT_IQ4_XS> {
     __device__ static int base(int lane) { return 64 * lane; }   // 256 (lane / 4) + 64 (lane % 4)
 };
+template <> struct XRuns<DT_MXFP4> {
+    __device__ static int base(int lane) { return 64 * lane; }
+};
 template <> struct XRuns<DT_Q8_0> {
     __device__ static int base(int lane) { return 64 * lane; }
 };
@@ -684,6 +687,41 @@ template <int RB> struct LdsDot<DT_IQ4_NL, RB> {
                 const float d = h2f(raw[r][5 * u + 4] & 0xFFFF);
                 a = __builtin_fmaf(d * kTwo24, acc[r][u], a);
                 a = __builtin_fmaf(-128.0f * d, xs[u], a);
+            }
+            v[r] = a;
+        }
+    }
+};
+
+template <int RB> struct LdsDot<DT_MXFP4, RB> {
+    using F = WaveFmt<DT_MXFP4>;
+    static constexpr int NS = 2;
+    __device__ static void sums(const float *xl, int b0, float (&xs)[NS]) {
+        LdsDot<DT_Q4_0, RB>::sums(xl, b0, xs);
+    }
+    __device__ static void run(const uint32_t (&raw)[RB][F::NRAW], int, const float *xl, int b0,
+                               const float (&xs)[NS], float (&v)[RB]) {
+        float acc[RB][2];
+#pragma unroll
+        for (int r = 0; r < RB; r++) acc[r][0] = acc[r][1] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const floatx4 lo = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * u + 4 * t));
+                const floatx4 hi = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * u + 16 + 4 * t));
+                const float xl4[4] = {lo.x, lo.y, lo.z, lo.w}, xh4[4] = {hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+                for (int r = 0; r < RB; r++) acc[r][u] = iq4x8<true>(raw[r][5 * u + t], xl4, xh4, acc[r][u]);
+            }
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const float d = e8m0_half(raw[r][5 * u + 4]);
+                a = __builtin_fmaf(d * kTwo24, acc[r][u], a);
+                a = __builtin_fmaf(-12.0f * d, xs[u], a);
             }
             v[r] = a;
         }
@@ -1283,6 +1321,7 @@ static hipError_t dispatch_dt(int dt, const SegTable &t, hipStream_t st) {
         case DT_IQ4_XS: return dispatch_mr<DT_IQ4_XS, XT, OT>(t, st);
         case DT_Q2_K: return dispatch_mr<DT_Q2_K, XT, OT>(t, st);
         case DT_Q3_K: return dispatch_mr<DT_Q3_K, XT, OT>(t, st);
+        case DT_MXFP4: return dispatch_mr<DT_MXFP4, XT, OT>(t, st);
         case DT_Q8_0: return dispatch_mr<DT_Q8_0, XT, OT>(t, st);
         default: return hipErrorInvalidValue;
     }

@@ -122,6 +122,7 @@ bool geometry(uint32_t id, int *bs, int *bb) {
         case KRK_DT_Q5_K: *bs = 256; *bb = 176; return true;
         case KRK_DT_IQ4_XS: *bs = 256; *bb = 136; return true;
         case KRK_DT_Q2_K: *bs = 256; *bb = 84; return true;
+        case KRK_DT_MXFP4: *bs = 32; *bb = 17; return true;
         case KRK_DT_Q3_K: *bs = 256; *bb = 110; return true;
         case KRK_DT_Q6_K: *bs = 256; *bb = 210; return true;
         default: return false;

@@ -23,12 +23,12 @@ __host__ __device__ constexpr int blk_vals(int dt) {
     return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K || dt == DT_IQ4_XS || dt == DT_Q2_K ||
                    dt == DT_Q3_K
                ? 256
-           : (dt == DT_Q4_0 || dt == DT_Q8_0 || dt == DT_IQ4_NL) ? 32
+           : (dt == DT_Q4_0 || dt == DT_Q8_0 || dt == DT_IQ4_NL || dt == DT_MXFP4) ? 32
                                                                   : 1;
 }
 __host__ __device__ constexpr int blk_bytes(int dt) {
     return dt == DT_Q4_K ? 144 : dt == DT_Q5_K ? 176 : dt == DT_Q6_K ? 210 : dt == DT_IQ4_XS ? 136
-         : dt == DT_Q2_K ? 84 : dt == DT_Q3_K ? 110
+         : dt == DT_Q2_K ? 84 : dt == DT_Q3_K ? 110 : dt == DT_MXFP4 ? 17
          : dt == DT_Q4_0 || dt == DT_IQ4_NL ? 18
          : dt == DT_Q8_0 ? 34 : dt == DT_F16 ? 2 : 4;
 }
@@ -183,10 +183,38 @@ __device__ __forceinline__ void dequant_chunk<DT_Q3_K>(const uint8_t *b, int c, 
     }
 }
 
+// MXFP4 half-scale exponent: 2^(e - 128) as f32 bits (e < 2: the denormals
+// 2^-128, 2^-127), quant.cpp:319-330
+__device__ __forceinline__ float e8m0_half(uint32_t e) {
+    const uint32_t bits = e < 2 ? (0x00200000u << e) : ((e - 1) << 23);
+    return __builtin_bit_cast(float, bits);
+}
+__constant__ static const int8_t kFp4Grid[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+// src/quant.cpp:674-686: value grid[q] * d, low nibbles first
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_MXFP4>(const uint8_t *b, int, float *y) {
+    const float d = e8m0_half(b[0]);
+    for (int j = 0; j < 16; j++) {
+        y[j] = static_cast<float>(kFp4Grid[b[1 + j] & 0xF]) * d;
+        y[j + 16] = static_cast<float>(kFp4Grid[b[1 + j] >> 4]) * d;
+    }
+}
+
 // ----------------------------------------------------- aligned raw loads ----
 // NW dwords holding bytes [p, p + 4*NW) of a 2-byte aligned pointer.  Only
 // dwords overlapping that range are read; a 4-aligned dword never crosses a
 // page, so a block's bytes can be fetched without reading past the buffer.
+template <int NW>
+__device__ __forceinline__ void load_bytes2(const uint8_t *p, uint32_t (&o)[NW]);
+
+// the byte at p, from the 4-aligned dword that holds it
+__device__ __forceinline__ uint32_t byte_at(const uint8_t *p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    return (ld32(reinterpret_cast<const uint8_t *>(a & ~uintptr_t(3))) >> (8 * (a & 3))) & 0xFF;
+}
+
+// (any byte alignment works: the window shift is a & 3)
 template <int NW>
 __device__ __forceinline__ void load_bytes2(const uint8_t *p, uint32_t (&o)[NW]) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
@@ -525,10 +553,22 @@ __device__ __forceinline__ uint32_t iq4_lookup(uint32_t idx) {   // idx: four in
     const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
     return (hi & m) | (lo & ~m);
 }
+// the same lookup over the MXFP4 grid biased by 12 (0..24): a small bias
+// keeps the x-sum correction at the grid's own magnitude
+constexpr uint32_t kFp4B0 = 0x0F0E0D0Cu, kFp4B1 = 0x18141210u, kFp4B2 = 0x090A0B0Cu, kFp4B3 = 0x00040608u;
+__device__ __forceinline__ uint32_t fp4_lookup(uint32_t idx) {
+    const uint32_t sel = idx & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(kFp4B1, kFp4B0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(kFp4B3, kFp4B2, sel);
+    const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & m) | (lo & ~m);
+}
 // acc += sum over the 8 indices of a dword (low nibbles with xl[0..3], high
-// nibbles with xh[0..3]) of (grid + 128) * 2^-24 * x, as f16 subnormals
+// nibbles with xh[0..3]) of (grid + bias) * 2^-24 * x, as f16 subnormals
+template <bool FP4 = false>
 __device__ __forceinline__ float iq4x8(uint32_t v, const float *xl, const float *xh, float acc) {
-    const uint32_t a = iq4_lookup(v & 0x0F0F0F0Fu), b = iq4_lookup((v >> 4) & 0x0F0F0F0Fu);
+    const uint32_t a = FP4 ? fp4_lookup(v & 0x0F0F0F0Fu) : iq4_lookup(v & 0x0F0F0F0Fu);
+    const uint32_t b = FP4 ? fp4_lookup((v >> 4) & 0x0F0F0F0Fu) : iq4_lookup((v >> 4) & 0x0F0F0F0Fu);
     acc = mix2(a & 0x00FF00FFu, xl[0], xl[2], acc);
     acc = mix2((a >> 8) & 0x00FF00FFu, xl[1], xl[3], acc);
     acc = mix2(b & 0x00FF00FFu, xh[0], xh[2], acc);
@@ -551,6 +591,28 @@ template <> struct LaneFmt<DT_IQ4_NL> {
 #pragma unroll
         for (int t = 0; t < 4; t++) s = iq4x8(raw[t], &xv[4 * t], &xv[16 + 4 * t], s);
         return __builtin_fmaf(-128.0f * d, xs[0] + xs[1], (d * kTwo24) * s);
+    }
+};
+
+// MXFP4: one lane per 17-byte block (byte aligned): the 16 code bytes by an
+// in-block window, the exponent byte by its aligned dword
+template <> struct LaneFmt<DT_MXFP4> {
+    static constexpr int LPB = 1, NG = 2, RUN = 32, NRUN = 1, NRAW = 5;
+    __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int i) { return i >> 4; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
+        uint32_t q[4];
+        load_bytes2<4>(blk + 1, q);
+        raw[0] = q[0]; raw[1] = q[1]; raw[2] = q[2]; raw[3] = q[3];
+        raw[4] = byte_at(blk);
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[32],
+                                const float (&xs)[NG]) {
+        const float d = e8m0_half(raw[4]);
+        float s = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) s = iq4x8<true>(raw[t], &xv[4 * t], &xv[16 + 4 * t], s);
+        return __builtin_fmaf(-12.0f * d, xs[0] + xs[1], (d * kTwo24) * s);
     }
 };
 
@@ -937,6 +999,40 @@ template <> struct WaveFmt<DT_IQ4_NL> {
             for (int t = 0; t < 4; t++) s = iq4x8(raw[5 * u + t], &xv[32 * u + 4 * t], &xv[32 * u + 16 + 4 * t], s);
             a = __builtin_fmaf(d * kTwo24, s, a);
             a = __builtin_fmaf(-128.0f * d, xs[u], a);
+        }
+        return a;
+    }
+};
+
+template <> struct WaveFmt<DT_MXFP4> {
+    // lane owns blocks 2*lane, 2*lane+1 of the step: 64 contiguous values
+    static constexpr int LPB = 1, BPS = 128, NG = 2, RUN = 64, NRUN = 1, NRAW = 10;
+    __device__ static int blk_of(int lane) { return 2 * lane; }
+    __device__ static int slot_of(int) { return 0; }
+    __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int i) { return i >> 5; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            uint32_t q[4];
+            load_bytes2<4>(blk + 17 * u + 1, q);
+#pragma unroll
+            for (int k = 0; k < 4; k++) raw[5 * u + k] = q[k];
+            raw[5 * u + 4] = byte_at(blk + 17 * u);
+        }
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[64],
+                                const float (&xs)[NG]) {
+        float a = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const float d = e8m0_half(raw[5 * u + 4]);
+            float s = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                s = iq4x8<true>(raw[5 * u + t], &xv[32 * u + 4 * t], &xv[32 * u + 16 + 4 * t], s);
+            a = __builtin_fmaf(d * kTwo24, s, a);
+            a = __builtin_fmaf(-12.0f * d, xs[u], a);
         }
         return a;
     }

@@ -191,6 +191,30 @@ void quant_iq4_nl(const float *v, int64_t n, uint8_t *dst) {
     }
 }
 
+// MXFP4 (17 B / 32 values): the exponent e with 12 * 2^(e - 128) >= amax
+// (the doubled grid's largest magnitude), then each value's nearest grid
+// point of v / 2^(e - 128).
+void quant_mxfp4(const float *v, int64_t n, uint8_t *dst) {
+    static const int grid[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+    for (int64_t b = 0; b < n; b += 32, dst += 17) {
+        double amax = 0.0;
+        for (int l = 0; l < 32; l++) amax = std::max(amax, std::fabs(double(v[b + l])));
+        int e = 0;
+        if (amax > 0) e = clampi(128 + std::ceil(std::log2(amax / 12.0)), 0, 254);
+        dst[0] = static_cast<uint8_t>(e);
+        const double d = std::ldexp(1.0, e - 128);
+        int q[32];
+        for (int l = 0; l < 32; l++) {
+            const double t = double(v[b + l]) / d;
+            int best = 0;
+            for (int k = 1; k < 16; k++)
+                if (std::fabs(t - grid[k]) < std::fabs(t - grid[best])) best = k;
+            q[l] = best;
+        }
+        for (int l = 0; l < 16; l++) dst[1 + l] = static_cast<uint8_t>(q[l] | (q[l + 16] << 4));
+    }
+}
+
 // Q2_K (84 B / 256 values): per 16-value group a 4-bit scale of
 // (max - min) / 3 and a 4-bit min of -min (min clamped to <= 0) on grids of
 // d = max scale / 15 and dmin = max min / 15; codes round((v + m) / s) in 0..3.
@@ -421,6 +445,7 @@ extern "C" int krk_quantize_weights(int wt, const float *v, int64_t n_rows,
         case KRK_DT_IQ4_XS: fn = quant_iq4_xs; break;
         case KRK_DT_Q2_K: fn = quant_q2_k; break;
         case KRK_DT_Q3_K: fn = quant_q3_k; break;
+        case KRK_DT_MXFP4: fn = quant_mxfp4; break;
         case KRK_DT_Q4_K: fn = quant_q4_k; break;
         case KRK_DT_Q5_K: fn = quant_q5_k; break;
         case KRK_DT_Q6_K: fn = quant_q6_k; break;

@@ -88,7 +88,7 @@ static inline float ld_f16(const uint8_t *p) {
 int orc_block_size(int dt) {
     switch (dt) {
         case ORC_F32: case ORC_F16: return 1;
-        case ORC_Q4_0: case ORC_Q8_0: case ORC_IQ4_NL: return 32;
+        case ORC_Q4_0: case ORC_Q8_0: case ORC_IQ4_NL: case ORC_MXFP4: return 32;
         case ORC_Q2_K: case ORC_Q3_K: case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_IQ4_XS: return 256;
         default: return 0;
     }
@@ -99,6 +99,7 @@ int orc_block_bytes(int dt) {
         case ORC_F16: return 2;
         case ORC_Q4_0: case ORC_IQ4_NL: return 18;
         case ORC_Q8_0: return 34;
+        case ORC_MXFP4: return 17;
         case ORC_Q2_K: return 84;
         case ORC_Q3_K: return 110;
         case ORC_Q4_K: return 144;
@@ -205,6 +206,27 @@ static void deq_q3_k(const uint8_t *b, float *y) {
             }
 }
 
+/* src/quant.cpp:83-86, 319-330, 674-686.  17 B / 32: an E8M0 exponent byte
+ * e, then 16 bytes of E2M1 codes (value j the low nibble of byte j, j + 16
+ * the high).  The FP4 grid is doubled (0, 1, 2, 3, 4, 6, 8, 12 and their
+ * negatives), so the exponent decodes at half scale: d = 2^(e - 128)
+ * exactly, e = 0 and 1 being the f32 denormals 2^-128 and 2^-127.  Value
+ * grid[q] * d, one rounding (overflow to inf for the largest e). */
+static const int8_t kFp4[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+static float e8m0_half(uint8_t e) {
+    uint32_t bits = e < 2 ? (0x00200000u << e) : ((uint32_t)(e - 1) << 23);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+static void deq_mxfp4(const uint8_t *b, float *y) {
+    float d = e8m0_half(b[0]);
+    for (int j = 0; j < 16; j++) {
+        y[j] = (float)kFp4[b[1 + j] & 0xF] * d;
+        y[j + 16] = (float)kFp4[b[1 + j] >> 4] * d;
+    }
+}
+
 /* src/quant.cpp:381-387 */
 static void deq_q8_0(const uint8_t *b, float *y) {
     float d = ld_f16(b);
@@ -295,6 +317,7 @@ static void dequant_block(int dt, const uint8_t *p, float *buf) {
         case ORC_F32: memcpy(buf, p, 4); break;
         case ORC_Q4_0: deq_q4_0(p, buf); break;
         case ORC_Q8_0: deq_q8_0(p, buf); break;
+        case ORC_MXFP4: deq_mxfp4(p, buf); break;
         case ORC_IQ4_NL: deq_iq4_nl(p, buf); break;
         case ORC_IQ4_XS: deq_iq4_xs(p, buf); break;
         case ORC_Q2_K: deq_q2_k(p, buf); break;

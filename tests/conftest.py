@@ -32,7 +32,8 @@ def rand_blocks(rng, dt, n_blocks):
     """Random block bytes with finite f16 scale fields (every code pattern)."""
     import oracle
     bb = {oracle.Q4_0: 18, oracle.Q8_0: 34, oracle.Q4_K: 144, oracle.Q5_K: 176, oracle.Q6_K: 210,
-          oracle.IQ4_NL: 18, oracle.IQ4_XS: 136, oracle.Q2_K: 84, oracle.Q3_K: 110}[dt]
+          oracle.IQ4_NL: 18, oracle.IQ4_XS: 136, oracle.Q2_K: 84, oracle.Q3_K: 110,
+          oracle.MXFP4: 17}[dt]
     w = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
 
     def setf16(off, scale):
@@ -50,6 +51,10 @@ def rand_blocks(rng, dt, n_blocks):
         setf16(82, 0.01)
     elif dt == oracle.Q3_K:
         setf16(108, 0.01)
+    elif dt == oracle.MXFP4:
+        # exponent bytes near 2^-7 scale (finite products and sums); every
+        # exponent byte is covered by the dequant tests of their own
+        w[:, 0] = rng.integers(110, 128, size=n_blocks)
     else:
         setf16(208, 0.01)
     return w.reshape(-1)

@@ -16,7 +16,7 @@ from conftest import rand_blocks
 
 pytestmark = pytest.mark.gpu
 
-FMTS = [O.Q4_0, O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS]
+FMTS = [O.Q4_0, O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS, O.MXFP4]
 GEMV_TOL = 1e-5
 GEMM_TOL = 2e-3
 
@@ -79,6 +79,21 @@ def test_quantize_q8_rows_bit_exact(torch_cuda, be32, rng):
         q, d = O.quantize_q8_row(x[r])
         assert np.array_equal(host(xq)[r], q)
         assert np.array_equal(host(dx)[r].view(np.uint32), d.view(np.uint32))
+
+
+def test_mxfp4_dequant_every_exponent(torch_cuda, be32):
+    """Every E8M0 byte (the f32 denormal scales 2^-128, 2^-127 and the
+    overflowing 2^127) and every code, bit for bit against the oracle."""
+    torch = torch_cuda
+    blk = np.zeros((256, 17), np.uint8)
+    blk[:, 0] = np.arange(256)
+    blk[:, 1:] = [(k & 15) | ((15 - k) << 4) for k in range(16)]
+    w = blk.reshape(-1)
+    say("dequant mxfp4 every exponent")
+    out = torch.empty((256, 32), dtype=torch.float32, device="cuda")
+    be32.dequant_rows(out, dev(torch, w), O.MXFP4, 256, 32)
+    be32.sync()
+    assert np.array_equal(host(out).view(np.uint32), O.dequant(O.MXFP4, w, 256, 32).view(np.uint32))
 
 
 # --------------------------------------------------------------------- GEMV --

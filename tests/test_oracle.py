@@ -12,7 +12,7 @@ import oracle as O
 from conftest import rand_blocks
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz")
-FMTS = [O.Q4_0, O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS]
+FMTS = [O.Q4_0, O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS, O.MXFP4]
 
 
 def f16bytes(v):
@@ -277,7 +277,7 @@ def test_oracle_matches_golden_vectors():
     g = np.load(GOLDEN)
     for dt, name in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k"), (O.Q5_K, "q5_k"),
                      (O.Q6_K, "q6_k"), (O.IQ4_NL, "iq4_nl"), (O.IQ4_XS, "iq4_xs"), (O.Q2_K, "q2_k"),
-                     (O.Q3_K, "q3_k")):
+                     (O.Q3_K, "q3_k"), (O.MXFP4, "mxfp4")):
         w, x = g[f"{name}_w"], g[f"{name}_x"]
         n = x.size
         deq = O.dequant(dt, w, 1, n)[0]
@@ -445,3 +445,19 @@ def test_q3_k_closed_form():
                     code = (32 * n + m + j) % 4 - (0 if (m + n + j) % 2 == 0 else 4)
                     want = np.float32(0.5 * (sc[i] - 32)) * np.float32(code)
                     assert y[128 * n + 32 * j + 16 * s + l] == want, (n, j, s, l)
+
+
+def test_mxfp4_closed_form_every_exponent():
+    """MXFP4 (quant.cpp:674-686, e8m0_to_fp32_half 319-330): one block per
+    exponent byte e = 0..255, codes k and 15 - k in byte k; value
+    grid[q] * 2^(e - 128) with the doubled E2M1 grid, exact (ldexp) up to
+    overflow to inf."""
+    grid = [0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12]
+    blk = np.zeros((256, 17), np.uint8)
+    blk[:, 0] = np.arange(256)
+    blk[:, 1:] = [(k & 15) | ((15 - k) << 4) for k in range(16)]
+    y = O.dequant(O.MXFP4, blk.reshape(-1), 256, 32)
+    with np.errstate(over="ignore"):
+        for e in range(256):
+            want = [np.float32(np.ldexp(np.float64(g), e - 128)) for g in grid + grid[::-1]]
+            assert y[e].tolist() == [float(w) for w in want], e
