@@ -28,13 +28,17 @@ extern "C" {
 #endif
 
 /* GGUF type ids; these block formats (plus F16/F32 activations) are on
- * this path.  include/krk/quant.hpp:16-47.  Q2_K, Q3_K, Q5_K, IQ4_NL, IQ4_XS and MXFP4 are served by
+ * this path.  include/krk/quant.hpp:16-47.  Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K, IQ4_NL, IQ4_XS
+ * and MXFP4 are served by
  * the dequant, GEMV (rows 1..8, exact prefill) and MFMA GEMM paths;
  * moe_dispatch banks take Q4_0 / Q8_0 / Q4_K / Q6_K, the int8 rung Q8_0. */
 enum krk_dtype {
     KRK_DT_F32 = 0,
     KRK_DT_F16 = 1,
     KRK_DT_Q4_0 = 2,
+    KRK_DT_Q4_1 = 3,
+    KRK_DT_Q5_0 = 6,
+    KRK_DT_Q5_1 = 7,
     KRK_DT_Q8_0 = 8,
     KRK_DT_Q2_K = 10,
     KRK_DT_Q3_K = 11,

@@ -60,7 +60,8 @@ int hip_fail(krk_backend *b, hipError_t e, const char *what) {
 bool dtype_on_path(int wt) {
     return wt == KRK_DT_Q4_0 || wt == KRK_DT_Q8_0 || wt == KRK_DT_Q4_K || wt == KRK_DT_Q5_K ||
            wt == KRK_DT_Q6_K || wt == KRK_DT_IQ4_NL || wt == KRK_DT_IQ4_XS || wt == KRK_DT_Q2_K ||
-           wt == KRK_DT_Q3_K || wt == KRK_DT_MXFP4;
+           wt == KRK_DT_Q3_K || wt == KRK_DT_MXFP4 || wt == KRK_DT_Q4_1 || wt == KRK_DT_Q5_0 ||
+           wt == KRK_DT_Q5_1;
 }
 
 int make_current(krk_backend *b) {
@@ -153,7 +154,8 @@ const char *krk_status_string(int s) {
 int krk_dtype_block_size(int wt) {
     switch (wt) {
         case KRK_DT_F32: case KRK_DT_F16: return 1;
-        case KRK_DT_Q4_0: case KRK_DT_Q8_0: case KRK_DT_IQ4_NL: case KRK_DT_MXFP4: return 32;
+        case KRK_DT_Q4_0: case KRK_DT_Q8_0: case KRK_DT_IQ4_NL: case KRK_DT_MXFP4:
+        case KRK_DT_Q4_1: case KRK_DT_Q5_0: case KRK_DT_Q5_1: return 32;
         case KRK_DT_Q2_K: case KRK_DT_Q3_K: case KRK_DT_Q4_K: case KRK_DT_Q5_K: case KRK_DT_Q6_K:
         case KRK_DT_IQ4_XS: return 256;
         default: return 0;
@@ -171,6 +173,9 @@ int krk_dtype_block_bytes(int wt) {
         case KRK_DT_IQ4_XS: return 136;
         case KRK_DT_Q2_K: return 84;
         case KRK_DT_MXFP4: return 17;
+        case KRK_DT_Q4_1: return 20;
+        case KRK_DT_Q5_0: return 22;
+        case KRK_DT_Q5_1: return 24;
         case KRK_DT_Q3_K: return 110;
         case KRK_DT_Q6_K: return 210;
         default: return 0;
@@ -405,7 +410,8 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
             for (int m = 0; m < 3; m++) {
                 if (!en.present[m] || !dtype_on_path(en.type[m]) || en.type[m] == KRK_DT_Q5_K ||
                     en.type[m] == KRK_DT_IQ4_NL || en.type[m] == KRK_DT_IQ4_XS || en.type[m] == KRK_DT_Q2_K ||
-                    en.type[m] == KRK_DT_Q3_K || en.type[m] == KRK_DT_MXFP4)
+                    en.type[m] == KRK_DT_Q3_K || en.type[m] == KRK_DT_MXFP4 || en.type[m] == KRK_DT_Q4_1 ||
+                    en.type[m] == KRK_DT_Q5_0 || en.type[m] == KRK_DT_Q5_1)
                     return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: expert %d matrix %d absent or of type %d",
                                 e, m, en.type[m]);
                 if (en.type[m] != e0.type[0])

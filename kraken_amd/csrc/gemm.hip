@@ -272,6 +272,34 @@ template <> struct WStage<DT_IQ4_XS> {
     }
 };
 
+// Q4_1 / Q5_0 / Q5_1: chunk kt is block kt; half hf takes the low (0) or
+// high nibbles and qh bits 16hf + k; value d*q + m or d*(q - 16), to f16
+template <int DT> struct WStageL32 {
+    uint32_t raw[6];
+    int hf_;
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        load_l32<DT>(row + kt * L32<DT>::BB, raw);
+        hf_ = hf;
+    }
+    __device__ void decode(int, _Float16 (&o)[16]) const {
+        const float d = h2f(raw[5] & 0xFFFF), m = h2f(raw[5] >> 16);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t c = l32_codes<DT>(raw, t, hf_);
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int q = static_cast<int>((c >> (8 * k)) & 0xFF);
+                const float v = L32<DT>::M ? __builtin_fmaf(d, static_cast<float>(q), m)
+                                           : d * static_cast<float>(q - L32<DT>::BIAS);
+                o[4 * t + k] = static_cast<_Float16>(v);
+            }
+        }
+    }
+};
+template <> struct WStage<DT_Q4_1> : WStageL32<DT_Q4_1> {};
+template <> struct WStage<DT_Q5_0> : WStageL32<DT_Q5_0> {};
+template <> struct WStage<DT_Q5_1> : WStageL32<DT_Q5_1> {};
+
 // MXFP4: chunk kt is block kt (byte aligned, 17 bytes); half hf takes the
 // low (0) or high nibbles; value grid[q] * 2^(e - 128), rounded once to f16
 template <> struct WStage<DT_MXFP4> {
@@ -655,6 +683,9 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
         KRK_GEMM_CASE(DT_Q2_K)
         KRK_GEMM_CASE(DT_Q3_K)
         KRK_GEMM_CASE(DT_MXFP4)
+        KRK_GEMM_CASE(DT_Q4_1)
+        KRK_GEMM_CASE(DT_Q5_0)
+        KRK_GEMM_CASE(DT_Q5_1)
         default: return hipErrorInvalidValue;
     }
 #undef KRK_GEMM_CASE

@@ -433,6 +433,9 @@ template <> struct XRuns<DT_IQ4_NL> {
 template <> struct XRuns<DT_IQ4_XS> {
     __device__ static int base(int lane) { return 64 * lane; }   // 256 (lane / 4) + 64 (lane % 4)
 };
+template <> struct XRuns<DT_Q4_1> : XRuns<DT_Q4_0> {};
+template <> struct XRuns<DT_Q5_0> : XRuns<DT_Q4_0> {};
+template <> struct XRuns<DT_Q5_1> : XRuns<DT_Q4_0> {};
 template <> struct XRuns<DT_MXFP4> {
     __device__ static int base(int lane) { return 64 * lane; }
 };
@@ -727,6 +730,46 @@ template <int RB> struct LdsDot<DT_MXFP4, RB> {
         }
     }
 };
+
+template <int DT, int RB> struct LdsDotL32 {
+    using F = WaveFmt<DT>;
+    static constexpr int NS = 2;
+    __device__ static void sums(const float *xl, int b0, float (&xs)[NS]) {
+        LdsDot<DT_Q4_0, RB>::sums(xl, b0, xs);
+    }
+    __device__ static void run(const uint32_t (&raw)[RB][F::NRAW], int, const float *xl, int b0,
+                               const float (&xs)[NS], float (&v)[RB]) {
+        float acc[RB][2];
+#pragma unroll
+        for (int r = 0; r < RB; r++) acc[r][0] = acc[r][1] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const floatx4 lo = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * u + 4 * t));
+                const floatx4 hi = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 32 * u + 16 + 4 * t));
+#pragma unroll
+                for (int r = 0; r < RB; r++) {
+                    const uint32_t cl = l32_codes<DT>(&raw[r][6 * u], t, 0), ch = l32_codes<DT>(&raw[r][6 * u], t, 1);
+                    float a = acc[r][u];
+                    a = mix2(cl & 0x001F001Fu, lo.x, lo.z, a);
+                    a = mix2((cl >> 8) & 0x001F001Fu, lo.y, lo.w, a);
+                    a = mix2(ch & 0x001F001Fu, hi.x, hi.z, a);
+                    acc[r][u] = mix2((ch >> 8) & 0x001F001Fu, hi.y, hi.w, a);
+                }
+            }
+#pragma unroll
+        for (int r = 0; r < RB; r++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 2; u++) a = l32_fold<DT>(&raw[r][6 * u], acc[r][u], xs[u], a);
+            v[r] = a;
+        }
+    }
+};
+template <int RB> struct LdsDot<DT_Q4_1, RB> : LdsDotL32<DT_Q4_1, RB> {};
+template <int RB> struct LdsDot<DT_Q5_0, RB> : LdsDotL32<DT_Q5_0, RB> {};
+template <int RB> struct LdsDot<DT_Q5_1, RB> : LdsDotL32<DT_Q5_1, RB> {};
 
 template <int RB> struct LdsDot<DT_IQ4_XS, RB> {
     using F = WaveFmt<DT_IQ4_XS>;
@@ -1322,6 +1365,9 @@ static hipError_t dispatch_dt(int dt, const SegTable &t, hipStream_t st) {
         case DT_Q2_K: return dispatch_mr<DT_Q2_K, XT, OT>(t, st);
         case DT_Q3_K: return dispatch_mr<DT_Q3_K, XT, OT>(t, st);
         case DT_MXFP4: return dispatch_mr<DT_MXFP4, XT, OT>(t, st);
+        case DT_Q4_1: return dispatch_mr<DT_Q4_1, XT, OT>(t, st);
+        case DT_Q5_0: return dispatch_mr<DT_Q5_0, XT, OT>(t, st);
+        case DT_Q5_1: return dispatch_mr<DT_Q5_1, XT, OT>(t, st);
         case DT_Q8_0: return dispatch_mr<DT_Q8_0, XT, OT>(t, st);
         default: return hipErrorInvalidValue;
     }

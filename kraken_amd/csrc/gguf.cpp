@@ -123,6 +123,9 @@ bool geometry(uint32_t id, int *bs, int *bb) {
         case KRK_DT_IQ4_XS: *bs = 256; *bb = 136; return true;
         case KRK_DT_Q2_K: *bs = 256; *bb = 84; return true;
         case KRK_DT_MXFP4: *bs = 32; *bb = 17; return true;
+        case KRK_DT_Q4_1: *bs = 32; *bb = 20; return true;
+        case KRK_DT_Q5_0: *bs = 32; *bb = 22; return true;
+        case KRK_DT_Q5_1: *bs = 32; *bb = 24; return true;
         case KRK_DT_Q3_K: *bs = 256; *bb = 110; return true;
         case KRK_DT_Q6_K: *bs = 256; *bb = 210; return true;
         default: return false;

@@ -23,12 +23,15 @@ __host__ __device__ constexpr int blk_vals(int dt) {
     return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K || dt == DT_IQ4_XS || dt == DT_Q2_K ||
                    dt == DT_Q3_K
                ? 256
-           : (dt == DT_Q4_0 || dt == DT_Q8_0 || dt == DT_IQ4_NL || dt == DT_MXFP4) ? 32
+           : (dt == DT_Q4_0 || dt == DT_Q8_0 || dt == DT_IQ4_NL || dt == DT_MXFP4 || dt == DT_Q4_1 ||
+              dt == DT_Q5_0 || dt == DT_Q5_1)
+               ? 32
                                                                   : 1;
 }
 __host__ __device__ constexpr int blk_bytes(int dt) {
     return dt == DT_Q4_K ? 144 : dt == DT_Q5_K ? 176 : dt == DT_Q6_K ? 210 : dt == DT_IQ4_XS ? 136
-         : dt == DT_Q2_K ? 84 : dt == DT_Q3_K ? 110 : dt == DT_MXFP4 ? 17
+         : dt == DT_Q2_K ? 84 : dt == DT_Q3_K ? 110 : dt == DT_MXFP4 ? 17 : dt == DT_Q4_1 ? 20
+         : dt == DT_Q5_0 ? 22 : dt == DT_Q5_1 ? 24
          : dt == DT_Q4_0 || dt == DT_IQ4_NL ? 18
          : dt == DT_Q8_0 ? 34 : dt == DT_F16 ? 2 : 4;
 }
@@ -228,6 +231,65 @@ __device__ __forceinline__ void load_bytes2(const uint8_t *p, uint32_t (&o)[NW])
     for (int k = 0; k < NW; k++) o[k] = align_bytes(d[k + 1], d[k], s);
 }
 
+// ------------------------------------------------ legacy 32-value formats --
+// Q4_1, Q5_0, Q5_1 (src/quant.cpp:341-378): f16 d at 0, an f16 min m at 2
+// (Q4_1, Q5_1), a 32-bit high-bit plane qh (Q5_0 at 2, Q5_1 at 4; bit k is
+// bit 4 of value k's code), 16 code bytes (value k the low nibble of byte
+// k, k + 16 the high).  Value d*q + m, or d*(q - 16) for Q5_0.
+template <int DT> struct L32;
+template <> struct L32<DT_Q4_1> { static constexpr int BB = 20, QH = -1, QS = 4, BIAS = 0; static constexpr bool M = true; };
+template <> struct L32<DT_Q5_0> { static constexpr int BB = 22, QH = 2, QS = 6, BIAS = 16; static constexpr bool M = false; };
+template <> struct L32<DT_Q5_1> { static constexpr int BB = 24, QH = 4, QS = 8, BIAS = 0; static constexpr bool M = true; };
+
+template <int DT>
+__device__ __forceinline__ void dequant_l32(const uint8_t *b, float *y) {
+    using L = L32<DT>;
+    const float d = ldh(b), m = L::M ? ldh(b + 2) : 0.0f;
+    uint32_t qh = 0;
+    if constexpr (L::QH >= 0)
+        qh = static_cast<uint32_t>(b[L::QH]) | (static_cast<uint32_t>(b[L::QH + 1]) << 8) |
+             (static_cast<uint32_t>(b[L::QH + 2]) << 16) | (static_cast<uint32_t>(b[L::QH + 3]) << 24);
+    for (int k = 0; k < 16; k++) {
+        const int lo = (b[L::QS + k] & 0xF) | static_cast<int>(((qh >> k) & 1u) << 4);
+        const int hi = (b[L::QS + k] >> 4) | static_cast<int>(((qh >> (k + 16)) & 1u) << 4);
+        if constexpr (L::M) {
+            y[k] = __builtin_fmaf(d, static_cast<float>(lo), m);
+            y[k + 16] = __builtin_fmaf(d, static_cast<float>(hi), m);
+        } else {
+            y[k] = d * static_cast<float>(lo - L::BIAS);
+            y[k + 16] = d * static_cast<float>(hi - L::BIAS);
+        }
+    }
+}
+template <> __device__ __forceinline__ void dequant_chunk<DT_Q4_1>(const uint8_t *b, int, float *y) { dequant_l32<DT_Q4_1>(b, y); }
+template <> __device__ __forceinline__ void dequant_chunk<DT_Q5_0>(const uint8_t *b, int, float *y) { dequant_l32<DT_Q5_0>(b, y); }
+template <> __device__ __forceinline__ void dequant_chunk<DT_Q5_1>(const uint8_t *b, int, float *y) { dequant_l32<DT_Q5_1>(b, y); }
+
+// one block's raw words: codes q[0..3], qh, and d (low half) | m (high half)
+template <int DT>
+__device__ __forceinline__ void load_l32(const uint8_t *blk, uint32_t *raw) {
+    using L = L32<DT>;
+    uint32_t q[4], h[1] = {0u}, dm[1];
+    load_bytes2<4>(blk + L::QS, q);
+    if constexpr (L::QH >= 0) load_bytes2<1>(blk + L::QH, h);
+    if constexpr (L::M) {
+        load_bytes2<1>(blk, dm);
+    } else {
+        const uintptr_t da = reinterpret_cast<uintptr_t>(blk);
+        dm[0] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+    }
+    raw[0] = q[0]; raw[1] = q[1]; raw[2] = q[2]; raw[3] = q[3];
+    raw[4] = h[0]; raw[5] = dm[0];
+}
+// four bits b0..b3 of n as bit 4 of four bytes
+__device__ __forceinline__ uint32_t spread4(uint32_t n) { return ((n * 0x00204081u) & 0x01010101u) << 4; }
+// codes of values 4t..4t+3 (hi = 0) or 16+4t.. (hi = 1) as four bytes
+template <int DT>
+__device__ __forceinline__ uint32_t l32_codes(const uint32_t *raw, int t, int hi) {
+    const uint32_t n = (raw[t] >> (4 * hi)) & 0x0F0F0F0Fu;
+    if constexpr (L32<DT>::QH >= 0) return n | spread4((raw[4] >> (16 * hi + 4 * t)) & 0xFu);
+    return n;
+}
 // --------------------------------------------------------------- LaneFmt ----
 // The lane view: LPB lanes per block, each owning 32 values ("a piece").
 // run_start(p, r) is where, inside the block, the r-th run of RUN consecutive
@@ -615,6 +677,43 @@ template <> struct LaneFmt<DT_MXFP4> {
         return __builtin_fmaf(-12.0f * d, xs[0] + xs[1], (d * kTwo24) * s);
     }
 };
+
+// sum_i code_i * 2^-24 * x_i over the block's 32 values (xl: 0..15, xh: 16..31)
+template <int DT>
+__device__ __forceinline__ float l32_sum(const uint32_t *raw, const float *xl, const float *xh, float s) {
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int hi = 0; hi < 2; hi++) {
+            const uint32_t c = l32_codes<DT>(raw, t, hi);
+            const float *x = (hi ? xh : xl) + 4 * t;
+            s = mix2(c & 0x001F001Fu, x[0], x[2], s);
+            s = mix2((c >> 8) & 0x001F001Fu, x[1], x[3], s);
+        }
+    return s;
+}
+// the block's dot from the code sum s and the block's x sum
+template <int DT>
+__device__ __forceinline__ float l32_fold(const uint32_t *raw, float s, float xsum, float acc) {
+    const float d = h2f(raw[5] & 0xFFFF);
+    acc = __builtin_fmaf(d * 16777216.0f, s, acc);
+    const float off = L32<DT>::M ? h2f(raw[5] >> 16) : -static_cast<float>(L32<DT>::BIAS) * d;
+    return __builtin_fmaf(off, xsum, acc);
+}
+
+template <int DT> struct LaneFmtL32 {
+    static constexpr int LPB = 1, NG = 2, RUN = 32, NRUN = 1, NRAW = 6;
+    __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int i) { return i >> 4; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) { load_l32<DT>(blk, raw); }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[32],
+                                const float (&xs)[NG]) {
+        return l32_fold<DT>(raw, l32_sum<DT>(raw, &xv[0], &xv[16], 0.0f), xs[0] + xs[1], 0.0f);
+    }
+};
+template <> struct LaneFmt<DT_Q4_1> : LaneFmtL32<DT_Q4_1> {};
+template <> struct LaneFmt<DT_Q5_0> : LaneFmtL32<DT_Q5_0> {};
+template <> struct LaneFmt<DT_Q5_1> : LaneFmtL32<DT_Q5_1> {};
 
 // IQ4_XS scale of sub-block ib from the header dwords h0 = d | scales_h << 16
 // and h1 = scales_l[0..3]: d * (ls - 32) (quant.cpp:646-650)
@@ -1037,6 +1136,30 @@ template <> struct WaveFmt<DT_MXFP4> {
         return a;
     }
 };
+
+template <int DT> struct WaveFmtL32 {
+    // lane owns blocks 2*lane, 2*lane+1 of the step: 64 contiguous values
+    static constexpr int LPB = 1, BPS = 128, NG = 2, RUN = 64, NRUN = 1, NRAW = 12;
+    __device__ static int blk_of(int lane) { return 2 * lane; }
+    __device__ static int slot_of(int) { return 0; }
+    __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int i) { return i >> 5; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
+        load_l32<DT>(blk, &raw[0]);
+        load_l32<DT>(blk + L32<DT>::BB, &raw[6]);
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[64],
+                                const float (&xs)[NG]) {
+        float a = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+            a = l32_fold<DT>(&raw[6 * u], l32_sum<DT>(&raw[6 * u], &xv[32 * u], &xv[32 * u + 16], 0.0f), xs[u], a);
+        return a;
+    }
+};
+template <> struct WaveFmt<DT_Q4_1> : WaveFmtL32<DT_Q4_1> {};
+template <> struct WaveFmt<DT_Q5_0> : WaveFmtL32<DT_Q5_0> {};
+template <> struct WaveFmt<DT_Q5_1> : WaveFmtL32<DT_Q5_1> {};
 
 template <> struct WaveFmt<DT_IQ4_XS> {
     // lane slot jp = lane % 4 of block lane / 4: sub-blocks 2jp, 2jp+1 (index

@@ -191,6 +191,47 @@ void quant_iq4_nl(const float *v, int64_t n, uint8_t *dst) {
     }
 }
 
+// Q4_1 / Q5_1 (20 / 24 B per 32 values): d = (max - min) / (2^bits - 1),
+// m = min, codes round((v - m) / d); Q5_0 (22 B): ggml's signed-max rule as
+// for Q4_0 (d = max / -16, codes round(v / d + 16) in 0..31).
+template <int BITS, bool MIN>
+void quant_l32(const float *v, int64_t n, uint8_t *dst) {
+    const int bb = MIN ? (BITS == 4 ? 20 : 24) : 22, qs = MIN ? (BITS == 4 ? 4 : 8) : 6;
+    const int qmax = (1 << BITS) - 1;
+    for (int64_t b = 0; b < n; b += 32, dst += bb) {
+        double lo = v[b], hi = v[b], amax = 0.0, smax = 0.0;
+        for (int l = 0; l < 32; l++) {
+            const double t = v[b + l];
+            lo = std::min(lo, t);
+            hi = std::max(hi, t);
+            if (std::fabs(t) > amax) { amax = std::fabs(t); smax = t; }
+        }
+        uint16_t hd, hm = 0;
+        if (MIN) {
+            hd = f64_to_half((hi - lo) / qmax);
+            hm = f64_to_half(lo);
+        } else {
+            hd = f64_to_half(smax / -16.0);
+        }
+        const double d = half_to_f64(hd), m = half_to_f64(hm);
+        put16(dst, hd);
+        if (MIN) put16(dst + 2, hm);
+        uint32_t qh = 0;
+        int q[32];
+        for (int l = 0; l < 32; l++) {
+            const double t = MIN ? (d > 0 ? (double(v[b + l]) - m) / d : 0.0)
+                                 : (d != 0 ? double(v[b + l]) / d + 16.0 : 16.0);
+            q[l] = clampi(std::nearbyint(t), 0, qmax);
+            if (BITS == 5) qh |= static_cast<uint32_t>((q[l] >> 4) & 1) << l;
+        }
+        for (int l = 0; l < 16; l++) dst[qs + l] = static_cast<uint8_t>((q[l] & 15) | ((q[l + 16] & 15) << 4));
+        if (BITS == 5) {
+            uint8_t *h = dst + (MIN ? 4 : 2);
+            for (int k = 0; k < 4; k++) h[k] = static_cast<uint8_t>(qh >> (8 * k));
+        }
+    }
+}
+
 // MXFP4 (17 B / 32 values): the exponent e with 12 * 2^(e - 128) >= amax
 // (the doubled grid's largest magnitude), then each value's nearest grid
 // point of v / 2^(e - 128).
@@ -446,6 +487,9 @@ extern "C" int krk_quantize_weights(int wt, const float *v, int64_t n_rows,
         case KRK_DT_Q2_K: fn = quant_q2_k; break;
         case KRK_DT_Q3_K: fn = quant_q3_k; break;
         case KRK_DT_MXFP4: fn = quant_mxfp4; break;
+        case KRK_DT_Q4_1: fn = quant_l32<4, true>; break;
+        case KRK_DT_Q5_0: fn = quant_l32<5, false>; break;
+        case KRK_DT_Q5_1: fn = quant_l32<5, true>; break;
         case KRK_DT_Q4_K: fn = quant_q4_k; break;
         case KRK_DT_Q5_K: fn = quant_q5_k; break;
         case KRK_DT_Q6_K: fn = quant_q6_k; break;

@@ -88,7 +88,8 @@ static inline float ld_f16(const uint8_t *p) {
 int orc_block_size(int dt) {
     switch (dt) {
         case ORC_F32: case ORC_F16: return 1;
-        case ORC_Q4_0: case ORC_Q8_0: case ORC_IQ4_NL: case ORC_MXFP4: return 32;
+        case ORC_Q4_0: case ORC_Q8_0: case ORC_IQ4_NL: case ORC_MXFP4:
+        case ORC_Q4_1: case ORC_Q5_0: case ORC_Q5_1: return 32;
         case ORC_Q2_K: case ORC_Q3_K: case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_IQ4_XS: return 256;
         default: return 0;
     }
@@ -100,6 +101,9 @@ int orc_block_bytes(int dt) {
         case ORC_Q4_0: case ORC_IQ4_NL: return 18;
         case ORC_Q8_0: return 34;
         case ORC_MXFP4: return 17;
+        case ORC_Q4_1: return 20;
+        case ORC_Q5_0: return 22;
+        case ORC_Q5_1: return 24;
         case ORC_Q2_K: return 84;
         case ORC_Q3_K: return 110;
         case ORC_Q4_K: return 144;
@@ -227,6 +231,30 @@ static void deq_mxfp4(const uint8_t *b, float *y) {
     }
 }
 
+/* src/quant.cpp:341-378: the legacy 32-value formats.  Q4_1 (20 B): f16 d,
+ * f16 m, 16 code bytes, value d*q + m.  Q5_0 (22 B): f16 d, a 32-bit plane
+ * qh (bit k is bit 4 of value k's code), 16 code bytes, value d*(q - 16).
+ * Q5_1 (24 B): d, m, qh, codes, value d*q + m.  Value k is the low nibble
+ * of code byte k, value k + 16 the high nibble.  d*q is exact (<= 16
+ * significant bits), so the one rounding is the add's and an FMA agrees. */
+static void deq_l32(const uint8_t *b, float *y, int has_m, int qh_off, int qs_off, int bias) {
+    float d = ld_f16(b), m = has_m ? ld_f16(b + 2) : 0.0f;
+    uint32_t qh = 0;
+    if (qh_off >= 0) qh = (uint32_t)b[qh_off] | ((uint32_t)b[qh_off + 1] << 8) |
+                          ((uint32_t)b[qh_off + 2] << 16) | ((uint32_t)b[qh_off + 3] << 24);
+    for (int k = 0; k < 16; k++) {
+        int lo = (b[qs_off + k] & 0xF) | (int)(((qh >> k) & 1u) << 4);
+        int hi = (b[qs_off + k] >> 4) | (int)(((qh >> (k + 16)) & 1u) << 4);
+        if (has_m) {
+            y[k] = fmaf(d, (float)lo, m);
+            y[k + 16] = fmaf(d, (float)hi, m);
+        } else {
+            y[k] = d * (float)(lo - bias);
+            y[k + 16] = d * (float)(hi - bias);
+        }
+    }
+}
+
 /* src/quant.cpp:381-387 */
 static void deq_q8_0(const uint8_t *b, float *y) {
     float d = ld_f16(b);
@@ -318,6 +346,9 @@ static void dequant_block(int dt, const uint8_t *p, float *buf) {
         case ORC_Q4_0: deq_q4_0(p, buf); break;
         case ORC_Q8_0: deq_q8_0(p, buf); break;
         case ORC_MXFP4: deq_mxfp4(p, buf); break;
+        case ORC_Q4_1: deq_l32(p, buf, 1, -1, 4, 0); break;
+        case ORC_Q5_0: deq_l32(p, buf, 0, 2, 6, 16); break;
+        case ORC_Q5_1: deq_l32(p, buf, 1, 4, 8, 0); break;
         case ORC_IQ4_NL: deq_iq4_nl(p, buf); break;
         case ORC_IQ4_XS: deq_iq4_xs(p, buf); break;
         case ORC_Q2_K: deq_q2_k(p, buf); break;

@@ -33,7 +33,7 @@ def rand_blocks(rng, dt, n_blocks):
     import oracle
     bb = {oracle.Q4_0: 18, oracle.Q8_0: 34, oracle.Q4_K: 144, oracle.Q5_K: 176, oracle.Q6_K: 210,
           oracle.IQ4_NL: 18, oracle.IQ4_XS: 136, oracle.Q2_K: 84, oracle.Q3_K: 110,
-          oracle.MXFP4: 17}[dt]
+          oracle.MXFP4: 17, oracle.Q4_1: 20, oracle.Q5_0: 22, oracle.Q5_1: 24}[dt]
     w = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
 
     def setf16(off, scale):
@@ -41,9 +41,9 @@ def rand_blocks(rng, dt, n_blocks):
         w[:, off] = v & 0xFF
         w[:, off + 1] = v >> 8
 
-    if dt in (oracle.Q4_0, oracle.Q8_0, oracle.IQ4_NL, oracle.IQ4_XS):
+    if dt in (oracle.Q4_0, oracle.Q8_0, oracle.IQ4_NL, oracle.IQ4_XS, oracle.Q5_0):
         setf16(0, 0.01)
-    elif dt in (oracle.Q4_K, oracle.Q5_K):
+    elif dt in (oracle.Q4_K, oracle.Q5_K, oracle.Q4_1, oracle.Q5_1):
         setf16(0, 0.01)
         setf16(2, 0.01)
     elif dt == oracle.Q2_K:

@@ -3,7 +3,7 @@ code (oracle/_ref/libkrk_ref.so, compiled by oracle/Makefile from
 /root/reference/src/quant.cpp + src/common.cpp).
 
 The fixture is data only: seeded block bytes and activations (inputs) and
-the reference's outputs for them (Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, MXFP4:
+the reference's outputs for them (Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, MXFP4, Q4_1, Q5_0, Q5_1:
 dequant_row f32, dequant_row_f16,
 vec_dot in the strict scalar tier, quantize_q8_row, dot_q8_0_q8_scalar).
 It lets the oracle be checked bit for bit where the reference tree is absent
@@ -112,7 +112,8 @@ def main():
     data.update(iq4_xs_w=w, iq4_xs_x=x, iq4_xs_deq=deq, iq4_xs_deq_f16=h, iq4_xs_dot=dots)
     # Q2_K and Q3_K, each from a stream of its own
     for dt, name, seed in ((oracle.Q2_K, "q2_k", 0x5EED2), (oracle.Q3_K, "q3_k", 0x5EED3),
-                           (oracle.MXFP4, "mxfp4", 0x5EEDF)):
+                           (oracle.MXFP4, "mxfp4", 0x5EEDF), (oracle.Q4_1, "q4_1", 0x5EED1),
+                           (oracle.Q5_0, "q5_0", 0x5EED6), (oracle.Q5_1, "q5_1", 0x5EED7)):
         r = np.random.default_rng(seed)
         bs = ref.ref_block_size(dt)
         w = rand_blocks(r, dt, n // bs)

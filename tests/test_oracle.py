@@ -12,7 +12,8 @@ import oracle as O
 from conftest import rand_blocks
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz")
-FMTS = [O.Q4_0, O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS, O.MXFP4]
+FMTS = [O.Q4_0, O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS, O.MXFP4,
+        O.Q4_1, O.Q5_0, O.Q5_1]
 
 
 def f16bytes(v):
@@ -277,7 +278,8 @@ def test_oracle_matches_golden_vectors():
     g = np.load(GOLDEN)
     for dt, name in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k"), (O.Q5_K, "q5_k"),
                      (O.Q6_K, "q6_k"), (O.IQ4_NL, "iq4_nl"), (O.IQ4_XS, "iq4_xs"), (O.Q2_K, "q2_k"),
-                     (O.Q3_K, "q3_k"), (O.MXFP4, "mxfp4")):
+                     (O.Q3_K, "q3_k"), (O.MXFP4, "mxfp4"), (O.Q4_1, "q4_1"), (O.Q5_0, "q5_0"),
+                     (O.Q5_1, "q5_1")):
         w, x = g[f"{name}_w"], g[f"{name}_x"]
         n = x.size
         deq = O.dequant(dt, w, 1, n)[0]
@@ -461,3 +463,26 @@ def test_mxfp4_closed_form_every_exponent():
         for e in range(256):
             want = [np.float32(np.ldexp(np.float64(g), e - 128)) for g in grid + grid[::-1]]
             assert y[e].tolist() == [float(w) for w in want], e
+
+
+@pytest.mark.parametrize("dt,qh,qs", [(O.Q4_1, None, 4), (O.Q5_0, 2, 6), (O.Q5_1, 4, 8)])
+def test_legacy_32_closed_form(dt, qh, qs):
+    """Q4_1 / Q5_0 / Q5_1 (quant.cpp:341-378): d = 0.5 (and m = -3 where the
+    format has a min); code byte k holds k and 15 - k; the high-bit plane
+    has bit j set for odd j.  Value d q + m, or d (q - 16) for Q5_0, with
+    q the nibble plus 16 times the plane bit."""
+    bb = {O.Q4_1: 20, O.Q5_0: 22, O.Q5_1: 24}[dt]
+    blk = np.zeros(bb, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    has_m = dt != O.Q5_0
+    if has_m:
+        blk[2:4] = np.frombuffer(np.float16(-3.0).tobytes(), np.uint8)
+    if qh is not None:
+        blk[qh:qh + 4] = np.frombuffer(np.uint32(0xAAAAAAAA).tobytes(), np.uint8)
+    blk[qs:qs + 16] = [k | ((15 - k) << 4) for k in range(16)]
+    y = O.dequant(dt, blk, 1, 32)[0]
+    for j in range(32):
+        nib = j if j < 16 else 15 - (j - 16)
+        q = nib + (16 * (j % 2) if qh is not None else 0)
+        want = 0.5 * q - 3.0 if has_m else 0.5 * (q - 16)
+        assert y[j] == np.float32(want), j
