@@ -60,7 +60,7 @@ enum krk_gemm_path {
     KRK_PATH_AUTO = 0,  /* MFMA f16 GEMM for rows > 8                       */
     KRK_PATH_EXACT = 1, /* multi-row GEMV, f32 products (gemv_grid analogue) */
     KRK_PATH_MFMA = 2,  /* W dequantized to f16 LDS tiles, f16 MFMA, f32 acc */
-    KRK_PATH_INT8 = 3   /* Q8_0 x Q8 activations on int8 MFMA (lossy rung)  */
+    KRK_PATH_INT8 = 3   /* Q8_0/Q4_K/Q5_K/Q6_K x Q8 activations (lossy rung) */
 };
 
 enum krk_status {

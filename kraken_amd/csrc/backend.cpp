@@ -260,11 +260,11 @@ int krk_gemm(krk_backend *b, void *out, const void *x, const void *w, int wt, in
     }
     const int64_t rb = krk_dtype_row_bytes(wt, n_in);
     if (b->path == KRK_PATH_INT8) {
-        if (wt != KRK_DT_Q8_0)
-            return fail(b, KRK_ERR_UNSUPPORTED, "the int8 rung serves Q8_0 weights only");
+        if (!krk::gemm_int8_serves(wt))
+            return fail(b, KRK_ERR_UNSUPPORTED, "the int8 rung serves Q8_0, Q4_K, Q5_K and Q6_K weights");
         if (int s = ensure_ws(b, krk::gemm_int8_workspace(rows, n_in))) return s;
-        const hipError_t e = krk::gemm_int8_q8_0(w, rb, x, f16, out, rows, n_out, n_in, b->ws,
-                                                 b->ws_bytes, b->stream);
+        const hipError_t e = krk::gemm_int8(wt, w, rb, x, f16, out, rows, n_out, n_in, b->ws,
+                                            b->ws_bytes, b->stream);
         return e == hipSuccess ? KRK_OK : hip_fail(b, e, "int8 gemm");
     }
     if (int s = ensure_ws(b, krk::gemm_mfma_workspace(wt, rows, n_out, n_in))) return s;

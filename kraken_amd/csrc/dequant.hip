@@ -80,7 +80,8 @@ hipError_t dequant_rows(int dt, const void *w, int64_t row_bytes, int64_t n_rows
 template <typename XT, typename CT>
 __global__ void __launch_bounds__(256) quantize_q8_kernel(const XT *__restrict__ x, int64_t nblk,
                                                           CT *__restrict__ xq,
-                                                          float *__restrict__ dx) {
+                                                          float *__restrict__ dx,
+                                                          float *__restrict__ sx16 = nullptr) {
     const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= nblk) return;
     float v[32];
@@ -108,6 +109,18 @@ __global__ void __launch_bounds__(256) quantize_q8_kernel(const XT *__restrict__
             }
             packed[k] = word;
         }
+    }
+    if (sx16) {  // code sums of the two 16-value halves (the affine int8 fold)
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int c = static_cast<int8_t>(packed[k] >> (8 * j));
+                if (k < 4) s0 += c; else s1 += c;
+            }
+        sx16[2 * b] = static_cast<float>(s0);
+        sx16[2 * b + 1] = static_cast<float>(s1);
     }
     if constexpr (sizeof(CT) == 1) {
         uint32_t *o = reinterpret_cast<uint32_t *>(xq + b * 32);
@@ -140,15 +153,15 @@ hipError_t quantize_q8_rows(const void *x, bool x_f16, int64_t rows, int64_t n, 
 }
 
 hipError_t quantize_q8_rows_f16codes(const void *x, bool x_f16, int64_t rows, int64_t n,
-                                     _Float16 *xq, float *dx, hipStream_t st) {
+                                     _Float16 *xq, float *dx, float *sx16, hipStream_t st) {
     const int64_t nblk = rows * (n / 32);
     const dim3 grid(static_cast<unsigned>((nblk + 255) / 256));
     if (x_f16)
         hipLaunchKernelGGL((quantize_q8_kernel<_Float16, _Float16>), grid, dim3(256), 0, st,
-                           static_cast<const _Float16 *>(x), nblk, xq, dx);
+                           static_cast<const _Float16 *>(x), nblk, xq, dx, sx16);
     else
         hipLaunchKernelGGL((quantize_q8_kernel<float, _Float16>), grid, dim3(256), 0, st,
-                           static_cast<const float *>(x), nblk, xq, dx);
+                           static_cast<const float *>(x), nblk, xq, dx, sx16);
     return hipGetLastError();
 }
 

@@ -84,7 +84,7 @@ hipError_t dequant_rows(int dt, const void *w, int64_t row_bytes, int64_t n_rows
 hipError_t quantize_q8_rows(const void *x, bool x_f16, int64_t rows, int64_t n,
                             int8_t *xq, float *dx, hipStream_t st);
 hipError_t quantize_q8_rows_f16codes(const void *x, bool x_f16, int64_t rows, int64_t n,
-                                     _Float16 *xq, float *dx, hipStream_t st);
+                                     _Float16 *xq, float *dx, float *sx16, hipStream_t st);
 
 // Prefill GEMM (f16 MFMA, f32 accumulate) and the Q8_0 x Q8 int8 MFMA rung.
 // out[M, N] = X[M, K] . deq(W)[N, K]^T.  `ws` is device scratch of ws_bytes.
@@ -93,9 +93,9 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
                      void *out, int64_t M, int64_t N, int64_t K, void *ws, size_t ws_bytes,
                      hipStream_t st);
 size_t gemm_int8_workspace(int64_t M, int64_t K);
-hipError_t gemm_int8_q8_0(const void *w, int64_t row_bytes, const void *x, bool act_f16,
-                          void *out, int64_t M, int64_t N, int64_t K, void *ws,
-                          size_t ws_bytes, hipStream_t st);
+bool gemm_int8_serves(int wt);
+hipError_t gemm_int8(int wt, const void *w, int64_t row_bytes, const void *x, bool act_f16, void *out,
+                     int64_t rows, int64_t n_out, int64_t n_in, void *ws, size_t ws_bytes, hipStream_t st);
 
 // Router and MoE dispatch.
 hipError_t router_softmax(const void *logits, bool act_f16, float *probs, int64_t n_rows,

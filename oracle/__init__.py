@@ -51,6 +51,8 @@ def _load():
         "orc_quantize_q8_row": (None, [_vp, _i64, _vp, _vp]),
         "orc_dot_q8_0_q8": (_f32, [_vp, _vp, _vp, _i64]),
         "orc_gemm_q8_0_q8": (None, [_vp, _vp, _vp, _i64, _i64, _i64, _i32]),
+        "orc_gemm_int8": (None, [_i32, _vp, _vp, _vp, _i64, _i64, _i64, _i32]),
+        "orc_dot_kq_q8": (_f32, [_i32, _vp, _vp, _vp, _i64]),
         "orc_silu_mul": (None, [_vp, _vp, _vp, _i64]),
         "orc_router_softmax": (None, [_vp, _vp, _i64, _i32]),
         "orc_router_topk": (None, [_vp, _i64, _i32, _i32, _vp, _vp, _i32, _f32]),
@@ -95,6 +97,8 @@ def ref():
             "ref_vec_dot": (_f32, [_i32, _vp, _vp, _i64]),
             "ref_quantize_q8_row": (None, [_vp, _i64, _vp, _vp]),
             "ref_dot_q8_0_q8_scalar": (_f32, [_vp, _vp, _vp, _i64]),
+            "ref_dot_q4_K_q8": (_f32, [_vp, _vp, _vp, _i64]),
+            "ref_dot_q6_K_q8": (_f32, [_vp, _vp, _vp, _i64]),
             "ref_fp16_to_fp32": (_f32, [_u16]),
             "ref_fp32_to_fp16": (_u16, [_f32]),
         }
@@ -168,6 +172,16 @@ def gemm_q8_0_q8(w: np.ndarray, x: np.ndarray, n_out: int, nthreads: int = 8
     out = np.empty((rows, n_out), np.float32)
     lib().orc_gemm_q8_0_q8(_p(out), _p(x), _p(np.ascontiguousarray(w)), n_out,
                            n_in, rows, nthreads)
+    return out
+
+
+def gemm_int8(dt: int, w: np.ndarray, x: np.ndarray, n_out: int, nthreads: int = 8
+              ) -> np.ndarray:
+    """The int8 rung for any of its weight types (Q8_0, Q4_K, Q5_K, Q6_K)."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    rows, n_in = x.shape
+    out = np.empty((rows, n_out), np.float32)
+    lib().orc_gemm_int8(dt, _p(out), _p(x), _p(np.ascontiguousarray(w)), n_out, n_in, rows, nthreads)
     return out
 
 

@@ -503,33 +503,120 @@ float orc_dot_q8_0_q8(const void *w, const int8_t *xq, const float *dx,
     return acc;
 }
 
+/* The GPU int8 rung's fold for the affine K-quants (gemm_dp4a.hpp:379-570,
+ * weight staging 197-375): per 32-value block b of the activation row, with
+ * sa = dx[b], the integer dot I and code sum S (exact) of each half, and the
+ * weight half's scale bsc and min bmin:
+ *     acc = fma(sa * bsc, (f32) I, acc);  acc = fma(-(sa * S), bmin, acc)
+ * Q4_K / Q5_K: one half of 32 values; bsc = d*s, bmin = dmin*m of the
+ * sub-block (get_scale_min_k4), S the sum over the 32 codes (the sum of its
+ * two 16-value halves, exact).  Codes are the unsigned Q4_K/Q5_K nibbles
+ * (0..15 / 0..31).  Q6_K: two halves of 16 values with bsc = d*sc of the
+ * 16-value group; the offset 32 is taken in the integer dot as the CPU
+ * twin does (t = I - 32*S in int32, dot_q6_K_q8_d, quant.cpp:2755-2800):
+ *     acc = fma(sa * bsc, (f32)(I - 32*S), acc)
+ * which equals the GPU rung's two-term fold up to its one extra rounding. */
+static void kq_half(int dt, const uint8_t *blk, int b32, int h, int *codes, float *bsc, float *bmin) {
+    /* codes of values 32*b32 + 16*h .. +16 of the 256-value block */
+    int base = 32 * b32 + 16 * h;
+    if (dt == ORC_Q4_K || dt == ORC_Q5_K) {
+        float d = ld_f16(blk), dmin = ld_f16(blk + 2);
+        uint8_t si, mi;
+        scale_min_k4(b32, blk + 4, &si, &mi);
+        *bsc = d * (float)si;
+        *bmin = dmin * (float)mi;
+        const uint8_t *q = blk + (dt == ORC_Q4_K ? 16 : 48) + 32 * (b32 / 2);
+        for (int l = 0; l < 16; l++) {
+            int li = 16 * h + l;
+            int c = (b32 & 1) ? (q[li] >> 4) : (q[li] & 0xF);
+            if (dt == ORC_Q5_K) c |= ((blk[16 + li] >> b32) & 1) << 4;
+            codes[l] = c;
+        }
+    } else { /* Q6_K: value v = 128n + 32qd + l */
+        float d = ld_f16(blk + 208);
+        for (int l = 0; l < 16; l++) {
+            int v = base + l, n = v / 128, qd = (v % 128) / 32, ll = v % 32;
+            const uint8_t *ql = blk + 64 * n, *qh = blk + 128 + 32 * n;
+            int lo = (qd & 1) ? ql[ll + 32] : ql[ll];
+            lo = (qd >> 1) ? (lo >> 4) : (lo & 0xF);
+            codes[l] = lo | (((qh[ll] >> (2 * qd)) & 3) << 4);
+        }
+        int g = (base % 128) / 16 + 8 * (base / 128);
+        *bsc = d * (float)(int8_t)blk[192 + g];
+        *bmin = 32.0f * *bsc;
+    }
+}
+
+float orc_dot_kq_q8(int dt, const void *w, const int8_t *xq, const float *dx, int64_t n) {
+    const uint8_t *p = (const uint8_t *)w;
+    int bb = orc_block_bytes(dt);
+    float acc = 0.0f;
+    for (int64_t b = 0; b < n / 32; b++) {
+        const uint8_t *blk = p + (b / 8) * bb;
+        int b32 = (int)(b % 8);
+        const int8_t *x = xq + 32 * b;
+        float sa = dx[b];
+        if (dt == ORC_Q6_K) {
+            for (int h = 0; h < 2; h++) {
+                int codes[16], I = 0, S = 0;
+                float bsc, bmin;
+                kq_half(dt, blk, b32, h, codes, &bsc, &bmin);
+                for (int l = 0; l < 16; l++) { I += codes[l] * x[16 * h + l]; S += x[16 * h + l]; }
+                (void)bmin;
+                acc = fmaf(sa * bsc, (float)(I - 32 * S), acc);
+            }
+        } else {
+            int I = 0, S0 = 0, S1 = 0;
+            float bsc = 0, bmin = 0;
+            for (int h = 0; h < 2; h++) {
+                int codes[16];
+                kq_half(dt, blk, b32, h, codes, &bsc, &bmin);
+                for (int l = 0; l < 16; l++) {
+                    I += codes[l] * x[16 * h + l];
+                    if (h) S1 += x[16 * h + l]; else S0 += x[16 * h + l];
+                }
+            }
+            acc = fmaf(sa * bsc, (float)I, acc);
+            acc = fmaf(-(sa * ((float)S0 + (float)S1)), bmin, acc);
+        }
+    }
+    return acc;
+}
+
 typedef struct {
     float *out; const int8_t *xq; const float *dx; const uint8_t *w;
     int64_t n_out, n_in, rows, rb;
+    int dt;
 } gq_ctx;
 
 static void gq_body(void *c, int64_t b, int64_t e) {
     gq_ctx *g = (gq_ctx *)c;
     for (int64_t o = b; o < e; o++)
         for (int64_t r = 0; r < g->rows; r++)
-            g->out[r * g->n_out + o] = orc_dot_q8_0_q8(
-                g->w + o * g->rb, g->xq + r * g->n_in, g->dx + r * (g->n_in / 32),
-                g->n_in);
+            g->out[r * g->n_out + o] = g->dt == ORC_Q8_0
+                ? orc_dot_q8_0_q8(g->w + o * g->rb, g->xq + r * g->n_in, g->dx + r * (g->n_in / 32), g->n_in)
+                : orc_dot_kq_q8(g->dt, g->w + o * g->rb, g->xq + r * g->n_in,
+                                g->dx + r * (g->n_in / 32), g->n_in);
 }
 
 /* The CPU backend's Q8_0 x int8 rung (src/backend_cpu.cpp:952-1000): each
  * activation row quantized once, then the scalar integer dot per output. */
-void orc_gemm_q8_0_q8(float *out, const float *x, const void *w,
-                      int64_t n_out, int64_t n_in, int64_t rows, int nthreads) {
+void orc_gemm_int8(int dt, float *out, const float *x, const void *w,
+                   int64_t n_out, int64_t n_in, int64_t rows, int nthreads) {
     int8_t *xq = (int8_t *)malloc((size_t)(rows * n_in));
     float *dx = (float *)malloc((size_t)(rows * (n_in / 32)) * sizeof(float));
     for (int64_t r = 0; r < rows; r++)
         orc_quantize_q8_row(x + r * n_in, n_in, xq + r * n_in, dx + r * (n_in / 32));
     gq_ctx g = {out, xq, dx, (const uint8_t *)w, n_out, n_in, rows,
-                orc_row_bytes(ORC_Q8_0, n_in)};
+                orc_row_bytes(dt, n_in), dt};
     par_for(n_out, nthreads, gq_body, &g);
     free(xq);
     free(dx);
+}
+
+void orc_gemm_q8_0_q8(float *out, const float *x, const void *w,
+                      int64_t n_out, int64_t n_in, int64_t rows, int nthreads) {
+    orc_gemm_int8(ORC_Q8_0, out, x, w, n_out, n_in, rows, nthreads);
 }
 
 /* src/backend_cpu.cpp:2401-2406: o = (g / (1 + exp(-g))) * u, std::exp on a

@@ -43,6 +43,9 @@ void     orc_gemm(float *out, const float *x, const void *w, int dt,
 void     orc_quantize_q8_row(const float *x, int64_t n, int8_t *xq, float *dx);
 float    orc_dot_q8_0_q8(const void *w, const int8_t *xq, const float *dx,
                          int64_t n);
+float    orc_dot_kq_q8(int dt, const void *w, const int8_t *xq, const float *dx, int64_t n);
+void     orc_gemm_int8(int dt, float *out, const float *x, const void *w,
+                       int64_t n_out, int64_t n_in, int64_t rows, int nthreads);
 void     orc_gemm_q8_0_q8(float *out, const float *x, const void *w,
                           int64_t n_out, int64_t n_in, int64_t rows,
                           int nthreads);

@@ -44,6 +44,13 @@ float ref_dot_q8_0_q8_scalar(const void *w, const int8_t *xq, const float *dx,
                              int64_t n) {
     return dot_q8_0_q8_scalar(static_cast<const u8 *>(w), xq, dx, n);
 }
+// the CPU int8 twins of the K-quant rung (quant.cpp:3125-3140, 3193-3200)
+float ref_dot_q4_K_q8(const void *w, const int8_t *xq, const float *dx, int64_t n) {
+    return dot_q4_K_q8(static_cast<const u8 *>(w), xq, dx, n);
+}
+float ref_dot_q6_K_q8(const void *w, const int8_t *xq, const float *dx, int64_t n) {
+    return dot_q6_K_q8(static_cast<const u8 *>(w), xq, dx, n);
+}
 float ref_fp16_to_fp32(uint16_t h) { return fp16_to_fp32(h); }
 uint16_t ref_fp32_to_fp16(float f) { return fp32_to_fp16(f); }
 

@@ -533,16 +533,48 @@ def test_int8_rung_q8_0_bit_exact(krk, torch_cuda, be16, be32, shape):
             be.set_gemm_path(krk.PATH_AUTO)
 
 
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q5_K, O.Q6_K])
+@pytest.mark.parametrize("shape", [(300, 520, 1024), (64, 256, 4096), (17, 40, 256)])
+def test_int8_rung_kquants(krk, torch_cuda, be16, be32, dt, shape):
+    """KRK_PATH_INT8 for the K-quants: the fold the oracle restates
+    (orc_dot_kq_q8: the reference GPU rung's two-term fold for Q4_K / Q5_K,
+    gemm_dp4a.hpp:532-552; the CPU twin's I - 32 S for Q6_K), bit for bit,
+    with edge tiles in M and N."""
+    torch = torch_cuda
+    M, N, K = shape
+    w = make_weights(krk, dt, N, K, seed=74 + dt)
+    x = krk.synth_normal(M * K, seed=75).reshape(M, K)
+    x[0, :32] = 0.0
+    say("int8 rung", dt, M, N, K)
+    ref = O.gemm_int8(dt, w, x, N)
+    for be in (be32, be16):
+        be.set_gemm_path(krk.PATH_INT8)
+    try:
+        out32 = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        be32.gemm(out32, dev(torch, x), dev(torch, w), dt, N, K, M)
+        be32.sync()
+        assert np.array_equal(host(out32).view(np.uint32), ref.view(np.uint32))
+        xh = x.astype(np.float16)
+        ref16 = O.gemm_int8(dt, w, xh.astype(np.float32), N).astype(np.float16)
+        out16 = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        be16.gemm(out16, dev(torch, xh), dev(torch, w), dt, N, K, M)
+        be16.sync()
+        assert np.array_equal(host(out16).view(np.uint16), ref16.view(np.uint16))
+    finally:
+        for be in (be32, be16):
+            be.set_gemm_path(krk.PATH_AUTO)
+
+
 @pytest.mark.gpu
 def test_int8_rung_refuses_other_formats(krk, torch_cuda, be32):
     torch = torch_cuda
     be32.set_gemm_path(krk.PATH_INT8)
     try:
-        w = make_weights(krk, krk.Q4_K, 32, 256, seed=72)
+        w = make_weights(krk, krk.Q4_0, 32, 256, seed=72)
         x = dev(torch, krk.synth_normal(16 * 256, seed=73).reshape(16, 256))
         out = torch.empty((16, 32), dtype=torch.float32, device="cuda")
-        with pytest.raises(krk.KrkError, match="UNSUPPORTED|Q8_0"):
-            be32.gemm(out, x, dev(torch, w), krk.Q4_K, 32, 256, 16)
+        with pytest.raises(krk.KrkError, match="UNSUPPORTED|int8 rung"):
+            be32.gemm(out, x, dev(torch, w), krk.Q4_0, 32, 256, 16)
     finally:
         be32.set_gemm_path(krk.PATH_AUTO)
 

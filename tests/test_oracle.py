@@ -486,3 +486,28 @@ def test_legacy_32_closed_form(dt, qh, qs):
         q = nib + (16 * (j % 2) if qh is not None else 0)
         want = 0.5 * q - 3.0 if has_m else 0.5 * (q - 16)
         assert y[j] == np.float32(want), j
+
+
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q5_K, O.Q6_K])
+def test_kquant_int8_fold(dt):
+    """The int8 rung's affine fold for the K-quants (gemm_dp4a.hpp:532-552):
+    against the exact sum of dequant(w) * xq * dx (the dequant is pinned bit
+    for bit) and, where oracle/_ref is built, against the reference's own CPU
+    int8 twin (dot_q4_K_q8 / dot_q6_K_q8, quant.cpp:3125, 3193), both to f32
+    rounding of the sum of |terms|.  A dropped min term, a sign or a wrong
+    sub-block scale moves the result by O(1) of that sum."""
+    rng = np.random.default_rng(40 + dt)
+    n = 4096
+    ref = O.ref() if O.ref_available() else None
+    for _ in range(10):
+        w = rand_blocks(rng, dt, n // 256)
+        x = rng.standard_normal(n).astype(np.float32)
+        xq, dx = O.quantize_q8_row(x)
+        got = np.float32(O.lib().orc_dot_kq_q8(dt, O._p(w), O._p(xq), O._p(dx), n))
+        terms = O.dequant(dt, w, 1, n)[0].astype(np.float64) * xq * np.repeat(dx.astype(np.float64), 32)
+        scale = float(np.sum(np.abs(terms)))
+        assert abs(float(got) - float(np.sum(terms))) <= 1e-6 * scale
+        if ref is not None and dt != O.Q5_K:
+            fn = ref.ref_dot_q4_K_q8 if dt == O.Q4_K else ref.ref_dot_q6_K_q8
+            r = np.float32(fn(O._p(w), O._p(xq), O._p(dx), n))
+            assert abs(float(got) - float(r)) <= 1e-6 * scale
