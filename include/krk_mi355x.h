@@ -28,8 +28,8 @@ extern "C" {
 #endif
 
 /* GGUF type ids; these block formats (plus F16/F32 activations) are on
- * this path.  include/krk/quant.hpp:16-47.  Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K, IQ4_NL, IQ4_XS
- * and MXFP4 are served by
+ * this path.  include/krk/quant.hpp:16-47.  Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K, IQ4_NL, IQ4_XS,
+ * MXFP4 and unquantized F16 / BF16 weights (16-byte aligned) are served by
  * the dequant, GEMV (rows 1..8, exact prefill) and MFMA GEMM paths;
  * moe_dispatch banks take Q4_0 / Q8_0 / Q4_K / Q6_K, the int8 rung Q8_0. */
 enum krk_dtype {
@@ -47,6 +47,7 @@ enum krk_dtype {
     KRK_DT_Q6_K = 14,
     KRK_DT_IQ4_NL = 20,
     KRK_DT_IQ4_XS = 23,
+    KRK_DT_BF16 = 30,
     KRK_DT_MXFP4 = 39
 };
 

@@ -20,15 +20,16 @@ LIB_PATH = os.path.join(HERE, "libkrk_mi355x.so")
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS = 0, 1, 2, 8, 12, 13, 14, 20, 23
 Q2_K, Q3_K, MXFP4 = 10, 11, 39
 Q4_1, Q5_0, Q5_1 = 3, 6, 7
+BF16 = 30
 ACT_F32, ACT_F16 = 0, 1
 PATH_AUTO, PATH_EXACT, PATH_MFMA, PATH_INT8 = 0, 1, 2, 3
 DTYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K",
                IQ4_NL: "IQ4_NL", IQ4_XS: "IQ4_XS", Q2_K: "Q2_K", Q3_K: "Q3_K", MXFP4: "MXFP4",
-               Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1"}
+               Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1", BF16: "BF16"}
 BLOCK_VALUES = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_NL: 32, IQ4_XS: 256,
-                Q2_K: 256, Q3_K: 256, MXFP4: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32}
+                Q2_K: 256, Q3_K: 256, MXFP4: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, F16: 1, BF16: 1}
 BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136,
-               Q2_K: 84, Q3_K: 110, MXFP4: 17, Q4_1: 20, Q5_0: 22, Q5_1: 24}
+               Q2_K: 84, Q3_K: 110, MXFP4: 17, Q4_1: 20, Q5_0: 22, Q5_1: 24, F16: 2, BF16: 2}
 
 _vp, _i64, _i32, _f32, _u64 = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_uint64
 _P = C.POINTER

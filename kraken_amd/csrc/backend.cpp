@@ -61,7 +61,7 @@ bool dtype_on_path(int wt) {
     return wt == KRK_DT_Q4_0 || wt == KRK_DT_Q8_0 || wt == KRK_DT_Q4_K || wt == KRK_DT_Q5_K ||
            wt == KRK_DT_Q6_K || wt == KRK_DT_IQ4_NL || wt == KRK_DT_IQ4_XS || wt == KRK_DT_Q2_K ||
            wt == KRK_DT_Q3_K || wt == KRK_DT_MXFP4 || wt == KRK_DT_Q4_1 || wt == KRK_DT_Q5_0 ||
-           wt == KRK_DT_Q5_1;
+           wt == KRK_DT_Q5_1 || wt == KRK_DT_F16 || wt == KRK_DT_BF16;
 }
 
 int make_current(krk_backend *b) {
@@ -107,7 +107,8 @@ int check_mm(krk_backend *b, const void *out, const void *x, const void *w, int 
     if (n_in > (int64_t(1) << 30)) return fail(b, KRK_ERR_SHAPE, "n_in=%lld too large", (long long)n_in);
     const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
     if (((wt == KRK_DT_Q4_K || wt == KRK_DT_Q5_K) && (wa & 15)) || (wt == KRK_DT_IQ4_XS && (wa & 7)) ||
-        (wt == KRK_DT_Q2_K && (wa & 3)) || (wt != KRK_DT_MXFP4 && (wa & 1)))
+        (wt == KRK_DT_Q2_K && (wa & 3)) || ((wt == KRK_DT_F16 || wt == KRK_DT_BF16) && (wa & 15)) ||
+        (wt != KRK_DT_MXFP4 && (wa & 1)))
         return fail(b, KRK_ERR_ARG, "weight pointer %p under-aligned for type %d", w, wt);
     if (reinterpret_cast<uintptr_t>(x) & 15)
         return fail(b, KRK_ERR_ARG, "activation pointer %p is not 16-byte aligned", x);
@@ -153,7 +154,7 @@ const char *krk_status_string(int s) {
 
 int krk_dtype_block_size(int wt) {
     switch (wt) {
-        case KRK_DT_F32: case KRK_DT_F16: return 1;
+        case KRK_DT_F32: case KRK_DT_F16: case KRK_DT_BF16: return 1;
         case KRK_DT_Q4_0: case KRK_DT_Q8_0: case KRK_DT_IQ4_NL: case KRK_DT_MXFP4:
         case KRK_DT_Q4_1: case KRK_DT_Q5_0: case KRK_DT_Q5_1: return 32;
         case KRK_DT_Q2_K: case KRK_DT_Q3_K: case KRK_DT_Q4_K: case KRK_DT_Q5_K: case KRK_DT_Q6_K:
@@ -165,7 +166,7 @@ int krk_dtype_block_size(int wt) {
 int krk_dtype_block_bytes(int wt) {
     switch (wt) {
         case KRK_DT_F32: return 4;
-        case KRK_DT_F16: return 2;
+        case KRK_DT_F16: case KRK_DT_BF16: return 2;
         case KRK_DT_Q4_0: case KRK_DT_IQ4_NL: return 18;
         case KRK_DT_Q8_0: return 34;
         case KRK_DT_Q4_K: return 144;
@@ -411,7 +412,8 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
                 if (!en.present[m] || !dtype_on_path(en.type[m]) || en.type[m] == KRK_DT_Q5_K ||
                     en.type[m] == KRK_DT_IQ4_NL || en.type[m] == KRK_DT_IQ4_XS || en.type[m] == KRK_DT_Q2_K ||
                     en.type[m] == KRK_DT_Q3_K || en.type[m] == KRK_DT_MXFP4 || en.type[m] == KRK_DT_Q4_1 ||
-                    en.type[m] == KRK_DT_Q5_0 || en.type[m] == KRK_DT_Q5_1)
+                    en.type[m] == KRK_DT_Q5_0 || en.type[m] == KRK_DT_Q5_1 || en.type[m] == KRK_DT_F16 ||
+                    en.type[m] == KRK_DT_BF16)
                     return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: expert %d matrix %d absent or of type %d",
                                 e, m, en.type[m]);
                 if (en.type[m] != e0.type[0])

@@ -57,6 +57,8 @@ static hipError_t dq(int dt, const void *w, int64_t rb, int64_t n_rows, int64_t 
         case DT_Q4_1: hipLaunchKernelGGL((dequant_kernel<DT_Q4_1, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
         case DT_Q5_0: hipLaunchKernelGGL((dequant_kernel<DT_Q5_0, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
         case DT_Q5_1: hipLaunchKernelGGL((dequant_kernel<DT_Q5_1, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
+        case DT_F16: hipLaunchKernelGGL((dequant_kernel<DT_F16, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
+        case DT_BF16: hipLaunchKernelGGL((dequant_kernel<DT_BF16, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
         case DT_Q8_0: hipLaunchKernelGGL((dequant_kernel<DT_Q8_0, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
         case DT_Q4_K: hipLaunchKernelGGL((dequant_kernel<DT_Q4_K, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
         case DT_Q5_K: hipLaunchKernelGGL((dequant_kernel<DT_Q5_K, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;

@@ -300,6 +300,31 @@ template <> struct WStage<DT_Q4_1> : WStageL32<DT_Q4_1> {};
 template <> struct WStage<DT_Q5_0> : WStageL32<DT_Q5_0> {};
 template <> struct WStage<DT_Q5_1> : WStageL32<DT_Q5_1> {};
 
+// F16 / BF16: chunk kt is pseudo-block kt (64 bytes); half hf its 16 values
+// at 32 hf bytes, F16 as they are, BF16 rounded once to f16
+template <int DT> struct WStageFloat {
+    uint32_t v[8];
+    __device__ void fetch(const uint8_t *row, int kt, int hf) {
+        const u32x4 a = ld128(row + kt * 64 + 32 * hf), b = ld128(row + kt * 64 + 32 * hf + 16);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    __device__ void decode(int, _Float16 (&o)[16]) const {
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            if constexpr (DT == DT_F16) {
+                const half2v h = __builtin_bit_cast(half2v, v[k]);
+                o[2 * k] = h.x;
+                o[2 * k + 1] = h.y;
+            } else {
+                o[2 * k] = static_cast<_Float16>(__builtin_bit_cast(float, v[k] << 16));
+                o[2 * k + 1] = static_cast<_Float16>(__builtin_bit_cast(float, v[k] & 0xFFFF0000u));
+            }
+        }
+    }
+};
+template <> struct WStage<DT_F16> : WStageFloat<DT_F16> {};
+template <> struct WStage<DT_BF16> : WStageFloat<DT_BF16> {};
+
 // MXFP4: chunk kt is block kt (byte aligned, 17 bytes); half hf takes the
 // low (0) or high nibbles; value grid[q] * 2^(e - 128), rounded once to f16
 template <> struct WStage<DT_MXFP4> {
@@ -686,6 +711,8 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
         KRK_GEMM_CASE(DT_Q4_1)
         KRK_GEMM_CASE(DT_Q5_0)
         KRK_GEMM_CASE(DT_Q5_1)
+        KRK_GEMM_CASE(DT_F16)
+        KRK_GEMM_CASE(DT_BF16)
         default: return hipErrorInvalidValue;
     }
 #undef KRK_GEMM_CASE

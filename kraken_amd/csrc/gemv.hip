@@ -434,6 +434,8 @@ template <> struct XRuns<DT_IQ4_XS> {
     __device__ static int base(int lane) { return 64 * lane; }   // 256 (lane / 4) + 64 (lane % 4)
 };
 template <> struct XRuns<DT_Q4_1> : XRuns<DT_Q4_0> {};
+template <> struct XRuns<DT_F16> : XRuns<DT_Q4_0> {};
+template <> struct XRuns<DT_BF16> : XRuns<DT_Q4_0> {};
 template <> struct XRuns<DT_Q5_0> : XRuns<DT_Q4_0> {};
 template <> struct XRuns<DT_Q5_1> : XRuns<DT_Q4_0> {};
 template <> struct XRuns<DT_MXFP4> {
@@ -767,6 +769,30 @@ template <int DT, int RB> struct LdsDotL32 {
         }
     }
 };
+template <int DT, int RB> struct LdsDotFloat {
+    using F = WaveFmt<DT>;
+    static constexpr int NS = 1;
+    __device__ static void sums(const float *, int, float (&xs)[NS]) { xs[0] = 0.0f; }
+    __device__ static void run(const uint32_t (&raw)[RB][F::NRAW], int, const float *xl, int b0,
+                               const float (&)[NS], float (&v)[RB]) {
+        float acc[RB][2];
+#pragma unroll
+        for (int r = 0; r < RB; r++) acc[r][0] = acc[r][1] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            const floatx4 u = *reinterpret_cast<const floatx4 *>(xl + xpad(b0 + 4 * t));
+#pragma unroll
+            for (int r = 0; r < RB; r++) {
+                acc[r][t & 1] = LaneFmtFloat<DT>::pair(raw[r][2 * t], u.x, u.y, acc[r][t & 1]);
+                acc[r][t & 1] = LaneFmtFloat<DT>::pair(raw[r][2 * t + 1], u.z, u.w, acc[r][t & 1]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RB; r++) v[r] = acc[r][0] + acc[r][1];
+    }
+};
+template <int RB> struct LdsDot<DT_F16, RB> : LdsDotFloat<DT_F16, RB> {};
+template <int RB> struct LdsDot<DT_BF16, RB> : LdsDotFloat<DT_BF16, RB> {};
 template <int RB> struct LdsDot<DT_Q4_1, RB> : LdsDotL32<DT_Q4_1, RB> {};
 template <int RB> struct LdsDot<DT_Q5_0, RB> : LdsDotL32<DT_Q5_0, RB> {};
 template <int RB> struct LdsDot<DT_Q5_1, RB> : LdsDotL32<DT_Q5_1, RB> {};
@@ -1368,6 +1394,8 @@ static hipError_t dispatch_dt(int dt, const SegTable &t, hipStream_t st) {
         case DT_Q4_1: return dispatch_mr<DT_Q4_1, XT, OT>(t, st);
         case DT_Q5_0: return dispatch_mr<DT_Q5_0, XT, OT>(t, st);
         case DT_Q5_1: return dispatch_mr<DT_Q5_1, XT, OT>(t, st);
+        case DT_F16: return dispatch_mr<DT_F16, XT, OT>(t, st);
+        case DT_BF16: return dispatch_mr<DT_BF16, XT, OT>(t, st);
         case DT_Q8_0: return dispatch_mr<DT_Q8_0, XT, OT>(t, st);
         default: return hipErrorInvalidValue;
     }

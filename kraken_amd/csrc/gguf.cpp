@@ -115,7 +115,7 @@ bool value(Cursor &c, Value &v) {
 bool geometry(uint32_t id, int *bs, int *bb) {
     switch (id) {
         case KRK_DT_F32: *bs = 1; *bb = 4; return true;
-        case KRK_DT_F16: *bs = 1; *bb = 2; return true;
+        case KRK_DT_F16: case KRK_DT_BF16: *bs = 1; *bb = 2; return true;
         case KRK_DT_Q4_0: case KRK_DT_IQ4_NL: *bs = 32; *bb = 18; return true;
         case KRK_DT_Q8_0: *bs = 32; *bb = 34; return true;
         case KRK_DT_Q4_K: *bs = 256; *bb = 144; return true;

@@ -19,12 +19,14 @@
 namespace krk {
 
 // ---------------------------------------------------------------- geometry --
+// F16 and BF16 weights are handled as 32-value pseudo-blocks of 64 bytes (a
+// row of n values is n / 32 of them), so they ride the same chunk contract.
 __host__ __device__ constexpr int blk_vals(int dt) {
     return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K || dt == DT_IQ4_XS || dt == DT_Q2_K ||
                    dt == DT_Q3_K
                ? 256
            : (dt == DT_Q4_0 || dt == DT_Q8_0 || dt == DT_IQ4_NL || dt == DT_MXFP4 || dt == DT_Q4_1 ||
-              dt == DT_Q5_0 || dt == DT_Q5_1)
+              dt == DT_Q5_0 || dt == DT_Q5_1 || dt == DT_F16 || dt == DT_BF16)
                ? 32
                                                                   : 1;
 }
@@ -33,7 +35,7 @@ __host__ __device__ constexpr int blk_bytes(int dt) {
          : dt == DT_Q2_K ? 84 : dt == DT_Q3_K ? 110 : dt == DT_MXFP4 ? 17 : dt == DT_Q4_1 ? 20
          : dt == DT_Q5_0 ? 22 : dt == DT_Q5_1 ? 24
          : dt == DT_Q4_0 || dt == DT_IQ4_NL ? 18
-         : dt == DT_Q8_0 ? 34 : dt == DT_F16 ? 2 : 4;
+         : dt == DT_Q8_0 ? 34 : dt == DT_F16 || dt == DT_BF16 ? 64 : 4;
 }
 
 __device__ __forceinline__ float ldh(const uint8_t *p) {
@@ -202,6 +204,18 @@ __device__ __forceinline__ void dequant_chunk<DT_MXFP4>(const uint8_t *b, int, f
         y[j] = static_cast<float>(kFp4Grid[b[1 + j] & 0xF]) * d;
         y[j + 16] = static_cast<float>(kFp4Grid[b[1 + j] >> 4]) * d;
     }
+}
+
+// F16 / BF16 weights (dequant.hpp:428-440): widening, exact
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_F16>(const uint8_t *b, int, float *y) {
+    for (int j = 0; j < 32; j++) y[j] = ldh(b + 2 * j);
+}
+__device__ __forceinline__ float bf2f(uint32_t h) { return __builtin_bit_cast(float, h << 16); }
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_BF16>(const uint8_t *b, int, float *y) {
+    for (int j = 0; j < 32; j++)
+        y[j] = bf2f(static_cast<uint32_t>(b[2 * j]) | (static_cast<uint32_t>(b[2 * j + 1]) << 8));
 }
 
 // ----------------------------------------------------- aligned raw loads ----
@@ -715,6 +729,38 @@ template <> struct LaneFmt<DT_Q4_1> : LaneFmtL32<DT_Q4_1> {};
 template <> struct LaneFmt<DT_Q5_0> : LaneFmtL32<DT_Q5_0> {};
 template <> struct LaneFmt<DT_Q5_1> : LaneFmtL32<DT_Q5_1> {};
 
+// F16 / BF16 weights: one lane per 32-value pseudo-block (64 bytes, rows
+// 16-byte aligned); F16 values enter v_fma_mix as f16 operands, BF16 values
+// widen by a shift
+template <int DT> struct LaneFmtFloat {
+    static constexpr int LPB = 1, NG = 1, RUN = 32, NRUN = 1, NRAW = 16;
+    __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int) { return 0; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const u32x4 v = ld128(blk + 16 * k);
+            raw[4 * k] = v.x; raw[4 * k + 1] = v.y; raw[4 * k + 2] = v.z; raw[4 * k + 3] = v.w;
+        }
+    }
+    __device__ static float pair(uint32_t v, float x0, float x1, float acc) {
+        if constexpr (DT == DT_F16) return mix2(v, x0, x1, acc);
+        acc = __builtin_fmaf(__builtin_bit_cast(float, v << 16), x0, acc);
+        return __builtin_fmaf(__builtin_bit_cast(float, v & 0xFFFF0000u), x1, acc);
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[32], const float (&)[NG]) {
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; k += 2) {
+            a = pair(raw[k], xv[2 * k], xv[2 * k + 1], a);
+            b = pair(raw[k + 1], xv[2 * k + 2], xv[2 * k + 3], b);
+        }
+        return a + b;
+    }
+};
+template <> struct LaneFmt<DT_F16> : LaneFmtFloat<DT_F16> {};
+template <> struct LaneFmt<DT_BF16> : LaneFmtFloat<DT_BF16> {};
+
 // IQ4_XS scale of sub-block ib from the header dwords h0 = d | scales_h << 16
 // and h1 = scales_l[0..3]: d * (ls - 32) (quant.cpp:646-650)
 __device__ __forceinline__ float iq4xs_scale(uint32_t h0, uint32_t h1, int ib) {
@@ -1160,6 +1206,33 @@ template <int DT> struct WaveFmtL32 {
 template <> struct WaveFmt<DT_Q4_1> : WaveFmtL32<DT_Q4_1> {};
 template <> struct WaveFmt<DT_Q5_0> : WaveFmtL32<DT_Q5_0> {};
 template <> struct WaveFmt<DT_Q5_1> : WaveFmtL32<DT_Q5_1> {};
+
+template <int DT> struct WaveFmtFloat {
+    // lane owns pseudo-blocks 2*lane, 2*lane+1 of the step: 64 contiguous values
+    static constexpr int LPB = 1, BPS = 128, NG = 1, RUN = 64, NRUN = 1, NRAW = 32;
+    __device__ static int blk_of(int lane) { return 2 * lane; }
+    __device__ static int slot_of(int) { return 0; }
+    __device__ static int run_start(int, int) { return 0; }
+    __device__ static int group_of(int) { return 0; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const u32x4 v = ld128(blk + 16 * k);
+            raw[4 * k] = v.x; raw[4 * k + 1] = v.y; raw[4 * k + 2] = v.z; raw[4 * k + 3] = v.w;
+        }
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[64], const float (&)[NG]) {
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 32; k += 2) {
+            a = LaneFmtFloat<DT>::pair(raw[k], xv[2 * k], xv[2 * k + 1], a);
+            b = LaneFmtFloat<DT>::pair(raw[k + 1], xv[2 * k + 2], xv[2 * k + 3], b);
+        }
+        return a + b;
+    }
+};
+template <> struct WaveFmt<DT_F16> : WaveFmtFloat<DT_F16> {};
+template <> struct WaveFmt<DT_BF16> : WaveFmtFloat<DT_BF16> {};
 
 template <> struct WaveFmt<DT_IQ4_XS> {
     // lane slot jp = lane % 4 of block lane / 4: sub-blocks 2jp, 2jp+1 (index

@@ -232,6 +232,19 @@ void quant_l32(const float *v, int64_t n, uint8_t *dst) {
     }
 }
 
+// F16 / BF16 weights: each value rounded to nearest even
+void quant_f16(const float *v, int64_t n, uint8_t *dst) {
+    for (int64_t i = 0; i < n; i++) put16(dst + 2 * i, f64_to_half(double(v[i])));
+}
+void quant_bf16(const float *v, int64_t n, uint8_t *dst) {
+    for (int64_t i = 0; i < n; i++) {
+        uint32_t b;
+        std::memcpy(&b, &v[i], 4);
+        b += 0x7FFFu + ((b >> 16) & 1u);   // finite inputs only
+        put16(dst + 2 * i, static_cast<uint16_t>(b >> 16));
+    }
+}
+
 // MXFP4 (17 B / 32 values): the exponent e with 12 * 2^(e - 128) >= amax
 // (the doubled grid's largest magnitude), then each value's nearest grid
 // point of v / 2^(e - 128).
@@ -490,6 +503,8 @@ extern "C" int krk_quantize_weights(int wt, const float *v, int64_t n_rows,
         case KRK_DT_Q4_1: fn = quant_l32<4, true>; break;
         case KRK_DT_Q5_0: fn = quant_l32<5, false>; break;
         case KRK_DT_Q5_1: fn = quant_l32<5, true>; break;
+        case KRK_DT_F16: fn = quant_f16; break;
+        case KRK_DT_BF16: fn = quant_bf16; break;
         case KRK_DT_Q4_K: fn = quant_q4_k; break;
         case KRK_DT_Q5_K: fn = quant_q5_k; break;
         case KRK_DT_Q6_K: fn = quant_q6_k; break;

@@ -20,6 +20,7 @@ REF_PATH = os.path.join(HERE, "_ref", "libkrk_ref.so")
 F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS = 0, 1, 2, 8, 12, 13, 14, 20, 23
 Q2_K, Q3_K, MXFP4 = 10, 11, 39
 Q4_1, Q5_0, Q5_1 = 3, 6, 7
+BF16 = 30
 
 _vp, _i64, _i32, _f32, _u16 = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_uint16
 

@@ -87,7 +87,7 @@ static inline float ld_f16(const uint8_t *p) {
 /* Geometry: src/quant.cpp:1805-1900 (block size / bytes), 1891-1895 (row). */
 int orc_block_size(int dt) {
     switch (dt) {
-        case ORC_F32: case ORC_F16: return 1;
+        case ORC_F32: case ORC_F16: case ORC_BF16: return 1;
         case ORC_Q4_0: case ORC_Q8_0: case ORC_IQ4_NL: case ORC_MXFP4:
         case ORC_Q4_1: case ORC_Q5_0: case ORC_Q5_1: return 32;
         case ORC_Q2_K: case ORC_Q3_K: case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_IQ4_XS: return 256;
@@ -97,7 +97,7 @@ int orc_block_size(int dt) {
 int orc_block_bytes(int dt) {
     switch (dt) {
         case ORC_F32: return 4;
-        case ORC_F16: return 2;
+        case ORC_F16: case ORC_BF16: return 2;
         case ORC_Q4_0: case ORC_IQ4_NL: return 18;
         case ORC_Q8_0: return 34;
         case ORC_MXFP4: return 17;
@@ -342,6 +342,11 @@ static void deq_q6_k(const uint8_t *b, float *y) {
 static void dequant_block(int dt, const uint8_t *p, float *buf) {
     switch (dt) {
         case ORC_F16: buf[0] = ld_f16(p); break;
+        case ORC_BF16: { /* src/quant.cpp:1558-1559: the high half of an f32 */
+            uint32_t bits = ((uint32_t)p[0] | ((uint32_t)p[1] << 8)) << 16;
+            memcpy(buf, &bits, 4);
+            break;
+        }
         case ORC_F32: memcpy(buf, p, 4); break;
         case ORC_Q4_0: deq_q4_0(p, buf); break;
         case ORC_Q8_0: deq_q8_0(p, buf); break;
@@ -388,7 +393,29 @@ void orc_dequant_row_f16(int dt, const void *src, uint16_t *out, int64_t n) {
  * product is rounded, then added.  Measured, not assumed: against
  * oracle/_ref/libkrk_ref.so (the reference's quant.cpp built with its own
  * flags) the unfused chain matches bit for bit and the fused one does not. */
+/* src/quant.cpp:5431-5510: the unquantized types are not block-dotted but
+ * summed in four lanes (lane k takes elements i = k mod 4, each step a fused
+ * multiply-add: _mm_fmadd_ps for F32 / F16, the 4-accumulator loop contracted
+ * by the reference build for BF16), combined as (a0 + a1) + (a2 + a3), then a
+ * scalar tail. */
+static float float_dot(int dt, const uint8_t *p, const float *x, int64_t n) {
+    float a[4] = {0, 0, 0, 0}, w[4];
+    int64_t i = 0;
+    for (; i + 4 <= n; i += 4)
+        for (int k = 0; k < 4; k++) {
+            dequant_block(dt, p + (i + k) * orc_block_bytes(dt), &w[k]);
+            a[k] = fmaf(w[k], x[i + k], a[k]);
+        }
+    float s = (a[0] + a[1]) + (a[2] + a[3]);
+    for (; i < n; i++) {
+        dequant_block(dt, p + i * orc_block_bytes(dt), &w[0]);
+        s = fmaf(w[0], x[i], s);
+    }
+    return s;
+}
+
 float orc_vec_dot(int dt, const void *src, const float *x, int64_t n) {
+    if (dt == ORC_F32 || dt == ORC_F16 || dt == ORC_BF16) return float_dot(dt, (const uint8_t *)src, x, n);
     int bs = orc_block_size(dt), bb = orc_block_bytes(dt);
     const uint8_t *p = (const uint8_t *)src;
     float buf[256], sum = 0.0f;

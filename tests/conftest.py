@@ -31,6 +31,11 @@ def krk():
 def rand_blocks(rng, dt, n_blocks):
     """Random block bytes with finite f16 scale fields (every code pattern)."""
     import oracle
+    if dt in (oracle.F16, oracle.BF16):   # finite values of a weight's scale
+        v = (rng.standard_normal(n_blocks) * 0.02).astype(np.float32)
+        if dt == oracle.F16:
+            return v.astype(np.float16).view(np.uint8).copy()
+        return (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).copy()
     bb = {oracle.Q4_0: 18, oracle.Q8_0: 34, oracle.Q4_K: 144, oracle.Q5_K: 176, oracle.Q6_K: 210,
           oracle.IQ4_NL: 18, oracle.IQ4_XS: 136, oracle.Q2_K: 84, oracle.Q3_K: 110,
           oracle.MXFP4: 17, oracle.Q4_1: 20, oracle.Q5_0: 22, oracle.Q5_1: 24}[dt]

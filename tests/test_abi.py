@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(krk):
 def test_geometry_matches_oracle(krk):
     L = krk.lib()
     for dt in (O.Q4_0, O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS, O.MXFP4,
-               O.Q4_1, O.Q5_0, O.Q5_1):
+               O.Q4_1, O.Q5_0, O.Q5_1, O.F16, O.BF16):
         assert L.krk_dtype_block_size(dt) == O.lib().orc_block_size(dt)
         assert L.krk_dtype_block_bytes(dt) == O.lib().orc_block_bytes(dt)
         for n in (32, 256, 4096, 11008, 14336):
@@ -98,7 +98,8 @@ def test_q4_0_quantizer_matches_fixture_generator(krk):
 @pytest.mark.parametrize("dt,bound", [(O.Q4_K, 0.12), (O.Q5_K, 0.06), (O.Q6_K, 0.03), (O.Q8_0, 0.01),
                                       (O.Q4_0, 0.12), (O.IQ4_NL, 0.12), (O.IQ4_XS, 0.12),
                                       (O.Q2_K, 0.45), (O.Q3_K, 0.25), (O.MXFP4, 0.2),
-                                      (O.Q4_1, 0.12), (O.Q5_0, 0.06), (O.Q5_1, 0.06)])
+                                      (O.Q4_1, 0.12), (O.Q5_0, 0.06), (O.Q5_1, 0.06),
+                                      (O.F16, 1e-3), (O.BF16, 4e-3)])
 def test_weight_quantizers_round_trip(krk, dt, bound):
     """The library's own K-quant quantizers (the reference has none): the
     bytes they write decode, through the pinned oracle, to the input within

@@ -22,7 +22,7 @@ REF_DIR = "/root/reference"
 REF_FILES = ["TinyLLama-v0.Q8_0.gguf", "tinystories-gpt-0.1-3m.Q2_K.gguf",
              "tiny-llama3-test-Q3_K_M.gguf"]
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "gguf_q8_0_blocks.npz")
-SERVED = {0, 1, 2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 20, 23, 39}
+SERVED = {0, 1, 2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 20, 23, 30, 39}
 
 
 def _ref_reader():
@@ -101,7 +101,7 @@ def test_reader_reads_every_metadata_type(krk, tmp_path):
     q8 = bytes(rng.integers(0, 256, 2 * 34 * 3, dtype=np.uint8))
     q4k = bytes(rng.integers(0, 256, 144 * 2, dtype=np.uint8))
     f32 = np.arange(5, dtype=np.float32).tobytes()
-    unknown = bytes(range(50))   # type 30 (BF16), not served
+    unknown = bytes(range(50))   # type 24 (I8), not served
     kvs = [("general.architecture", STRING, "llama"), ("general.alignment", U32, 64),
            ("a.u8", U8, 250), ("a.i8", I8, -5), ("a.u16", U16, 65000), ("a.i16", I16, -300),
            ("a.i32", I32, -70000), ("a.f32", F32, 1.5), ("a.bool", BOOL, 1), ("a.u64", U64, 2 ** 40),
@@ -109,7 +109,7 @@ def test_reader_reads_every_metadata_type(krk, tmp_path):
            ("a.arr_i32", ARRAY, [1, -2, 3], I32), ("a.arr_f32", ARRAY, [0.5, 0.25], F32),
            ("a.arr_str", ARRAY, ["x", "yz"], STRING), ("a.arr_u64", ARRAY, [7, 2 ** 33], U64)]
     tensors = [("w.q8", 8, [64, 3], q8), ("w.q4k", 12, [256, 2], q4k), ("v.f32", 0, [5], f32),
-               ("u.bf16", 30, [25], unknown)]
+               ("u.i8", 24, [50], unknown)]
     path = str(tmp_path / "m.gguf")
     data_off = write_gguf(path, kvs, tensors, alignment=64)
     g = krk.Gguf(path)
@@ -133,7 +133,7 @@ def test_reader_reads_every_metadata_type(krk, tmp_path):
     for name, tid, ne, data in tensors:
         t = g.tensor(name)
         assert t.type_id == tid and list(t.ne)[: len(ne)] == ne
-        if tid == 30:
+        if tid == 24:
             assert not t.dtype_known and t.n_bytes == 0
             with pytest.raises(krk.KrkError):
                 g.data(name)

@@ -17,7 +17,7 @@ from conftest import rand_blocks
 pytestmark = pytest.mark.gpu
 
 FMTS = [O.Q4_0, O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS, O.MXFP4,
-        O.Q4_1, O.Q5_0, O.Q5_1]
+        O.Q4_1, O.Q5_0, O.Q5_1, O.F16, O.BF16]
 GEMV_TOL = 1e-5
 GEMM_TOL = 2e-3
 
