@@ -621,7 +621,7 @@ def test_error_paths_write_nothing(krk, torch_cuda, be32):
     out = torch.full((2, n_out), float("nan"), dtype=torch.float32, device="cuda")
     cases = [
         ("not whole blocks", lambda: be32.gemm(out, x, w, O.Q4_0, n_out, 100, 1), "shape"),
-        ("type not served", lambda: be32.gemm(out, x, w, 3, n_out, n_in, 1), "type"),
+        ("type not served", lambda: be32.gemm(out, x, w, 24, n_out, n_in, 1), "type"),
         ("zero rows", lambda: be32.gemm(out, x, w, O.Q4_K, n_out, n_in, 0), "argument"),
         ("zero outputs", lambda: be32.gemm(out, x, w, O.Q4_K, 0, n_in, 1), "argument"),
         ("x under-aligned", lambda: be32.gemm(out, x[1:], w, O.Q4_K, n_out, n_in, 1), "argument"),
