@@ -178,12 +178,22 @@ int krk_router_topk(krk_backend *b, const void *probs, int64_t n_rows,
  *   out[t] = sum over slots s (in ascending expert id) of
  *            wts[t,s] * down_e( silu(gate_e(xn[t])) * up_e(xn[t]) )
  * xn and out are [n_tok, n_embd] in the activation type; ids int32 and wts
- * f32 [n_tok, k] device arrays. */
+ * f32 [n_tok, k] device arrays.
+ * The first call for a (table, layer, n_expert, n_embd, n_ff) reads that
+ * layer's entries back once and validates them (types, geometry, alignment);
+ * later calls with the same key launch without a host round trip, so a
+ * table's layer must not change while the handle remembers it. */
 int krk_moe_dispatch_supported(const krk_backend *b);
 int krk_moe_dispatch(krk_backend *b, const void *table, int layer,
                      int n_expert, const void *ids, const void *wts,
                      const void *xn, void *out, int64_t n_tok, int64_t n_embd,
                      int64_t n_ff, int k);
+
+/* Forget the validations remembered for every layer of `table` (call it
+ * before a dispatched table is rewritten or freed, so that a new table at
+ * the same address is read and checked again).  No counterpart in the
+ * reference, whose dispatch keeps no host-side record of the table. */
+int krk_moe_table_forget(krk_backend *b, const void *table);
 
 /* ------------------------------------------------ dequant / quantize ops -- */
 

@@ -59,6 +59,7 @@ SIGNATURES = {
     "krk_router_topk_supported": (_i32, [_vp]),
     "krk_router_topk": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp, _vp, _i32, _f32]),
     "krk_moe_dispatch_supported": (_i32, [_vp]),
+    "krk_moe_table_forget": (_i32, [_vp, _vp]),
     "krk_moe_dispatch": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64,
                                 _i64, _i32]),
     "krk_dequant_rows_f32": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64]),
@@ -255,6 +256,11 @@ class Backend:
         self._check(lib().krk_moe_dispatch(self._h, _ptr(table), layer, n_expert, _ptr(ids),
                                            _ptr(wts), _ptr(xn), _ptr(out), n_tok, n_embd,
                                            n_ff, k), "moe_dispatch")
+
+    def moe_table_forget(self, table):
+        """Drop the remembered validation of every layer of `table` (before
+        the table is rewritten or freed)."""
+        self._check(lib().krk_moe_table_forget(self._h, _ptr(table)), "moe_table_forget")
 
     # exactness surface
     def dequant_rows(self, out, w, wt: int, n_rows: int, n_in: int, f16: bool = False):

@@ -57,6 +57,17 @@ int hip_fail(krk_backend *b, hipError_t e, const char *what) {
     return fail(b, KRK_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// the byte alignment a weight type's loads need at a row start
+uintptr_t weight_align(int wt) {
+    switch (wt) {
+        case KRK_DT_Q4_K: case KRK_DT_Q5_K: case KRK_DT_F16: case KRK_DT_BF16: return 16;
+        case KRK_DT_IQ4_XS: return 8;
+        case KRK_DT_Q2_K: return 4;
+        case KRK_DT_MXFP4: return 1;
+        default: return 2;
+    }
+}
+
 bool dtype_on_path(int wt) {
     return wt == KRK_DT_Q4_0 || wt == KRK_DT_Q8_0 || wt == KRK_DT_Q4_K || wt == KRK_DT_Q5_K ||
            wt == KRK_DT_Q6_K || wt == KRK_DT_IQ4_NL || wt == KRK_DT_IQ4_XS || wt == KRK_DT_Q2_K ||
@@ -106,9 +117,7 @@ int check_mm(krk_backend *b, const void *out, const void *x, const void *w, int 
                     (long long)n_in, krk_dtype_block_size(wt));
     if (n_in > (int64_t(1) << 30)) return fail(b, KRK_ERR_SHAPE, "n_in=%lld too large", (long long)n_in);
     const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
-    if (((wt == KRK_DT_Q4_K || wt == KRK_DT_Q5_K) && (wa & 15)) || (wt == KRK_DT_IQ4_XS && (wa & 7)) ||
-        (wt == KRK_DT_Q2_K && (wa & 3)) || ((wt == KRK_DT_F16 || wt == KRK_DT_BF16) && (wa & 15)) ||
-        (wt != KRK_DT_MXFP4 && (wa & 1)))
+    if (wa & (weight_align(wt) - 1))
         return fail(b, KRK_ERR_ARG, "weight pointer %p under-aligned for type %d", w, wt);
     if (reinterpret_cast<uintptr_t>(x) & 15)
         return fail(b, KRK_ERR_ARG, "activation pointer %p is not 16-byte aligned", x);
@@ -396,8 +405,8 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
         e0 = b->moe_ok[hit].e0;
         aligned = b->moe_ok[hit].aligned;
     } else {
-        // every bank of the layer: present, of a type the expert kernels
-        // take (Q4_0, Q8_0, Q4_K, Q6_K), one weight type,
+        // every bank of the layer: present, of a served type with its rows
+        // aligned for that type's loads, one weight type,
         // the layer's geometry; and whether all rows start 16-byte aligned
         std::vector<krk_moe_entry> ents(static_cast<size_t>(n_expert));
         hipError_t he = hipMemcpyAsync(ents.data(), tab + static_cast<int64_t>(layer) * n_expert,
@@ -409,12 +418,16 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
         for (int e = 0; e < n_expert; e++) {
             const krk_moe_entry &en = ents[static_cast<size_t>(e)];
             for (int m = 0; m < 3; m++) {
-                if (!en.present[m] || !dtype_on_path(en.type[m]) || en.type[m] == KRK_DT_Q5_K ||
-                    en.type[m] == KRK_DT_IQ4_NL || en.type[m] == KRK_DT_IQ4_XS || en.type[m] == KRK_DT_Q2_K ||
-                    en.type[m] == KRK_DT_Q3_K || en.type[m] == KRK_DT_MXFP4 || en.type[m] == KRK_DT_Q4_1 ||
-                    en.type[m] == KRK_DT_Q5_0 || en.type[m] == KRK_DT_Q5_1 || en.type[m] == KRK_DT_F16 ||
-                    en.type[m] == KRK_DT_BF16)
+                if (!en.present[m] || !dtype_on_path(en.type[m]))
                     return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: expert %d matrix %d absent or of type %d",
+                                e, m, en.type[m]);
+                // the original bank types run unaligned rows on the VALU path;
+                // the others need their loads' alignment at every row start
+                const bool legacy = en.type[m] == KRK_DT_Q4_0 || en.type[m] == KRK_DT_Q8_0 ||
+                                    en.type[m] == KRK_DT_Q4_K || en.type[m] == KRK_DT_Q6_K;
+                if (!legacy && ((reinterpret_cast<uintptr_t>(en.p[m]) | static_cast<uintptr_t>(en.row_bytes[m])) &
+                                (weight_align(en.type[m]) - 1)))
+                    return fail(b, KRK_ERR_ARG, "moe_dispatch: expert %d matrix %d rows under-aligned for type %d",
                                 e, m, en.type[m]);
                 if (en.type[m] != e0.type[0])
                     return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: mixed expert formats");
@@ -439,6 +452,15 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
     if (int s = ensure_ws(b, krk::moe_workspace(n_tok, k, n_expert, n_embd, n_ff))) return s;
     const hipError_t he = krk::moe_dispatch(a, b->ws, b->ws_bytes, b->stream);
     return he == hipSuccess ? KRK_OK : hip_fail(b, he, "moe_dispatch");
+}
+
+int krk_moe_table_forget(krk_backend *b, const void *table) {
+    if (!b) return KRK_ERR_ARG;
+    int n = 0;
+    for (int i = 0; i < b->n_moe_ok; i++)
+        if (b->moe_ok[i].key.table != table) b->moe_ok[n++] = b->moe_ok[i];
+    b->n_moe_ok = n;
+    return KRK_OK;
 }
 
 int krk_dequant_rows_f32(krk_backend *b, float *out, const void *w, int wt, int64_t n_rows,

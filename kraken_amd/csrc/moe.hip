@@ -23,6 +23,16 @@
 #include "gemv_core.hpp"
 #include "krk_mi355x.h"
 
+// every weight type an expert bank may hold (the backend validates the table
+// before any launch; an unknown type never reaches these switches)
+#define KRK_MOE_TYPES(X, T, A)                                                                  \
+    X(DT_Q4_K, T, A) X(DT_Q6_K, T, A) X(DT_Q4_0, T, A) X(DT_Q8_0, T, A) X(DT_Q5_K, T, A)      \
+    X(DT_Q2_K, T, A) X(DT_Q3_K, T, A) X(DT_IQ4_NL, T, A) X(DT_IQ4_XS, T, A) X(DT_MXFP4, T, A) \
+    X(DT_Q4_1, T, A) X(DT_Q5_0, T, A) X(DT_Q5_1, T, A) X(DT_F16, T, A) X(DT_BF16, T, A)
+#define KRK_MOE_UNPAREN(...) __VA_ARGS__
+#define KRK_MOE_ROWS(D, T, A) \
+    case D: gemv_rows<D, KRK_MOE_UNPAREN T>(KRK_MOE_UNPAREN A); break;
+
 namespace krk {
 
 struct MoeWs {
@@ -168,10 +178,8 @@ __global__ void __launch_bounds__(512) moe_gu_kernel(const krk_moe_entry *__rest
         const uint8_t *wg = static_cast<const uint8_t *>(en.p[KRK_MOE_GATE]);
         const uint8_t *wu = static_cast<const uint8_t *>(en.p[KRK_MOE_UP]);
         switch (en.type[KRK_MOE_GATE]) {
-            case DT_Q4_K: gemv_rows<DT_Q4_K, XT, MR, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
-            case DT_Q6_K: gemv_rows<DT_Q6_K, XT, MR, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
-            case DT_Q4_0: gemv_rows<DT_Q4_0, XT, MR, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
-            default:      gemv_rows<DT_Q8_0, XT, MR, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
+            KRK_MOE_TYPES(KRK_MOE_ROWS, (XT, MR, RB), (wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc))
+            default: break;
         }
         float v[MR * RB];
 #pragma unroll
@@ -220,10 +228,8 @@ __global__ void __launch_bounds__(512) moe_down_kernel(const krk_moe_entry *__re
             xr[m] = pass + m < np ? w.mid + static_cast<int64_t>(p0 + pass + m) * n_ff : nullptr;
         float acc[MR][RB];
         switch (en.type[KRK_MOE_DOWN]) {
-            case DT_Q4_K: gemv_rows<DT_Q4_K, float, MR, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, acc); break;
-            case DT_Q6_K: gemv_rows<DT_Q6_K, float, MR, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, acc); break;
-            case DT_Q4_0: gemv_rows<DT_Q4_0, float, MR, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, acc); break;
-            default:      gemv_rows<DT_Q8_0, float, MR, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, acc); break;
+            KRK_MOE_TYPES(KRK_MOE_ROWS, (float, MR, RB), (wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, acc))
+            default: break;
         }
         float v[MR * RB];
 #pragma unroll
@@ -312,10 +318,8 @@ __global__ void __launch_bounds__(512) moe_gu1_kernel(const krk_moe_entry *__res
         const uint8_t *wg = static_cast<const uint8_t *>(en.p[KRK_MOE_GATE]);
         const uint8_t *wu = static_cast<const uint8_t *>(en.p[KRK_MOE_UP]);
         switch (en.type[KRK_MOE_GATE]) {
-            case DT_Q4_K: gemv_rows<DT_Q4_K, XT, 1, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
-            case DT_Q6_K: gemv_rows<DT_Q6_K, XT, 1, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
-            case DT_Q4_0: gemv_rows<DT_Q4_0, XT, 1, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
-            default:      gemv_rows<DT_Q8_0, XT, 1, RB>(wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc); break;
+            KRK_MOE_TYPES(KRK_MOE_ROWS, (XT, 1, RB), (wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc))
+            default: break;
         }
         float v[RB];
 #pragma unroll
@@ -372,10 +376,8 @@ __global__ void __launch_bounds__(512) moe_down1_kernel(const krk_moe_entry *__r
             float a2[1][RB];
             const uint8_t *wd = static_cast<const uint8_t *>(en.p[KRK_MOE_DOWN]);
             switch (en.type[KRK_MOE_DOWN]) {
-                case DT_Q4_K: gemv_rows<DT_Q4_K, float, 1, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, a2, 0, 1); break;
-                case DT_Q6_K: gemv_rows<DT_Q6_K, float, 1, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, a2, 0, 1); break;
-                case DT_Q4_0: gemv_rows<DT_Q4_0, float, 1, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, a2, 0, 1); break;
-                default:      gemv_rows<DT_Q8_0, float, 1, RB>(wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, a2, 0, 1); break;
+                KRK_MOE_TYPES(KRK_MOE_ROWS, (float, 1, RB), (wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, a2, 0, 1))
+                default: break;
             }
             float v[RB];
 #pragma unroll

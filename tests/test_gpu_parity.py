@@ -266,6 +266,23 @@ def test_router_softmax_topk(krk, torch_cuda, be32, rng):
 
 
 # --------------------------------------------------------------------- MoE --
+_TABLES = []   # MoE tables built by the running test
+
+
+@pytest.fixture(autouse=True)
+def _forget_moe_tables(request):
+    """A dispatched table is remembered by its handle (validated once); the
+    test's tables are freed when it ends, so the handles forget them, and a
+    later table at a reused address is validated afresh."""
+    yield
+    for name in ("be32", "be16"):
+        if _TABLES and name in request.fixturenames:
+            be = request.getfixturevalue(name)
+            for t in _TABLES:
+                be.moe_table_forget(t)
+    _TABLES.clear()
+
+
 def build_moe(krk, torch, dt, ne, n_embd, n_ff, seed):
     mats = {}
     entries = []
@@ -284,18 +301,21 @@ def build_moe(krk, torch, dt, ne, n_embd, n_ff, seed):
             ent.present[m] = 1
         entries.append(ent)
     table = dev(torch, np.frombuffer(krk.moe_table_bytes(entries), np.uint8).copy())
+    _TABLES.append(table)
     return mats, table, keep
 
 
+@pytest.mark.parametrize("dt", FMTS)
 @pytest.mark.parametrize("n_tok", [1, 5])
-def test_moe_dispatch_parity(krk, torch_cuda, be32, n_tok):
+def test_moe_dispatch_parity(krk, torch_cuda, be32, n_tok, dt):
+    """Expert banks of every served weight type, one and several tokens."""
     torch = torch_cuda
-    dt, ne, n_embd, n_ff, k = O.Q4_K, 8, 512, 768, 3
+    ne, n_embd, n_ff, k = 8, 512, 768, 3
     mats, table, keep = build_moe(krk, torch, dt, ne, n_embd, n_ff, seed=900)
     logits = krk.synth_normal(n_tok * ne, seed=77).reshape(n_tok, ne)
     ids, wts = O.router_topk(O.router_softmax(logits), k)
     x = krk.synth_normal(n_tok * n_embd, seed=78).reshape(n_tok, n_embd)
-    say("moe", n_tok, ids.tolist())
+    say("moe", dt, n_tok, ids.tolist())
     out = torch.empty((n_tok, n_embd), dtype=torch.float32, device="cuda")
     be32.moe_dispatch(table, 0, ne, dev(torch, ids), dev(torch, wts), dev(torch, x), out, n_tok,
                       n_embd, n_ff, k)
@@ -305,6 +325,30 @@ def test_moe_dispatch_parity(krk, torch_cuda, be32, n_tok):
     e = rel(host(out), ref)
     say("  rel", e)
     assert e <= GEMV_TOL
+
+
+def test_moe_table_rewritten_in_place(krk, torch_cuda, be32):
+    """A dispatched table rewritten in place (same address, another bank
+    type) is read and checked again after krk_moe_table_forget."""
+    torch = torch_cuda
+    ne, n_embd, n_ff, k, n_tok = 8, 512, 768, 2, 2
+    logits = krk.synth_normal(n_tok * ne, seed=97).reshape(n_tok, ne)
+    ids, wts = O.router_topk(O.router_softmax(logits), k)
+    x = krk.synth_normal(n_tok * n_embd, seed=98).reshape(n_tok, n_embd)
+    mats_a, table, keep_a = build_moe(krk, torch, O.Q4_K, ne, n_embd, n_ff, seed=960)
+    mats_b, table_b, keep_b = build_moe(krk, torch, O.IQ4_NL, ne, n_embd, n_ff, seed=970)
+    out = torch.empty((n_tok, n_embd), dtype=torch.float32, device="cuda")
+    for mats, dt in ((mats_a, O.Q4_K), (mats_b, O.IQ4_NL)):
+        if dt == O.IQ4_NL:
+            be32.moe_table_forget(table)
+            table.copy_(table_b)       # the same address now holds the other layer
+        say("moe table", dt)
+        be32.moe_dispatch(table, 0, ne, dev(torch, ids), dev(torch, wts), dev(torch, x), out, n_tok,
+                          n_embd, n_ff, k)
+        be32.sync()
+        ref = O.moe_ffn(x, [mats[0, e] for e in range(ne)], [mats[1, e] for e in range(ne)],
+                        [mats[2, e] for e in range(ne)], dt, ids, wts, n_ff)
+        assert rel(host(out), ref) <= GEMV_TOL
 
 
 @pytest.mark.parametrize("n_tok,k,drop", [(1, 2, False), (1, 8, False), (1, 4, True), (3, 4, True),
