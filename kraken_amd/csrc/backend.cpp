@@ -406,7 +406,7 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
         aligned = b->moe_ok[hit].aligned;
     } else {
         // every bank of the layer: present, of a served type with its rows
-        // aligned for that type's loads, one weight type,
+        // aligned for that type's loads, one type per role (gate = up),
         // the layer's geometry; and whether all rows start 16-byte aligned
         std::vector<krk_moe_entry> ents(static_cast<size_t>(n_expert));
         hipError_t he = hipMemcpyAsync(ents.data(), tab + static_cast<int64_t>(layer) * n_expert,
@@ -429,7 +429,9 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
                                 (weight_align(en.type[m]) - 1)))
                     return fail(b, KRK_ERR_ARG, "moe_dispatch: expert %d matrix %d rows under-aligned for type %d",
                                 e, m, en.type[m]);
-                if (en.type[m] != e0.type[0])
+                // one type per role across the layer, gate and up alike (the
+                // expert kernels decode up with the gate's type)
+                if (en.type[m] != e0.type[m] || en.type[1] != en.type[0])
                     return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: mixed expert formats");
                 if (reinterpret_cast<uintptr_t>(en.p[m]) & 15) aligned = false;
             }
@@ -447,6 +449,7 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
     a.n_tok = n_tok; a.n_embd = n_embd; a.n_ff = n_ff;
     a.act_f16 = b->act == KRK_ACT_F16;
     a.wt = e0.type[0];
+    a.wt_down = e0.type[2];
     a.rb_gate = e0.row_bytes[0]; a.rb_up = e0.row_bytes[1]; a.rb_down = e0.row_bytes[2];
     a.aligned16 = aligned;
     if (int s = ensure_ws(b, krk::moe_workspace(n_tok, k, n_expert, n_embd, n_ff))) return s;

@@ -112,7 +112,8 @@ struct MoeArgs {
     void *out;
     int64_t n_tok, n_embd, n_ff;
     bool act_f16;
-    int wt;              // the (uniform) weight type of the experts
+    int wt;              // the experts' gate / up weight type
+    int wt_down;         // the experts' down weight type
     int64_t rb_gate, rb_up, rb_down;
     bool aligned16;      // every bank's rows start 16-byte aligned
 };

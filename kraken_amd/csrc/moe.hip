@@ -467,7 +467,8 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     // batches (up to kMoeTokenGroups tokens). Larger Q4_K batches take
     // expert-major items, which read each active expert once per item of
     // kItemRows tokens; what the digit kernel cannot take goes to the plan path.
-    const bool on_digits = !a.act_f16 && a.wt == DT_Q4_K && a.aligned16 && a.rb_gate == a.rb_up &&
+    const bool on_digits = !a.act_f16 && a.wt == DT_Q4_K && a.wt_down == DT_Q4_K && a.aligned16 &&
+                           a.rb_gate == a.rb_up &&
                            a.k <= kMaxSegs && a.k * a.n_ff <= (1 << 30);
     const bool groups = on_digits && a.n_tok <= kMoeTokenGroups;
     const bool gu_ok = groups && gemv_digits_ok(DT_Q4_K, gu);

@@ -213,7 +213,9 @@ def router_topk(probs: np.ndarray, k: int, normalize: bool = True,
 
 
 def moe_ffn(x, gate, up, down, wt, ids, wts, n_ff, nthreads: int = 8):
-    """x f32 [n_tok, n_embd]; gate/up/down: lists of per-expert uint8 arrays."""
+    """x f32 [n_tok, n_embd]; gate/up/down: lists of per-expert uint8 arrays;
+    wt one weight type or a (gate, up, down) triple."""
+    wg, wu, wd = (wt, wt, wt) if isinstance(wt, int) else wt
     x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
     n_tok, n_embd = x.shape
     ne = len(gate)
@@ -227,7 +229,7 @@ def moe_ffn(x, gate, up, down, wt, ids, wts, n_ff, nthreads: int = 8):
     d = arr(*[a.ctypes.data for a in keep[2 * ne:]])
     out = np.empty((n_tok, n_embd), np.float32)
     lib().orc_moe_ffn(_p(out), _p(x), C.cast(g, _vp), C.cast(u, _vp),
-                      C.cast(d, _vp), wt, wt, wt, _p(ids), _p(wts), n_tok,
+                      C.cast(d, _vp), wg, wu, wd, _p(ids), _p(wts), n_tok,
                       n_embd, n_ff, ne, k, nthreads)
     return out
 

@@ -290,14 +290,15 @@ def build_moe(krk, torch, dt, ne, n_embd, n_ff, seed):
     for e in range(ne):
         ent = krk.MoeEntry()
         for m, (o, i) in enumerate(((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff))):
-            q = make_weights(krk, dt, o, i, seed=seed + 3 * e + m)
+            dtm = dt if isinstance(dt, int) else dt[m]
+            q = make_weights(krk, dtm, o, i, seed=seed + 3 * e + m)
             mats[m, e] = q
             t = dev(torch, q)
             keep.append(t)
             ent.p[m] = t.data_ptr()
             ent.n_out[m], ent.n_in[m] = o, i
-            ent.row_bytes[m] = krk.row_bytes(dt, i)
-            ent.type[m] = dt
+            ent.row_bytes[m] = krk.row_bytes(dtm, i)
+            ent.type[m] = dtm
             ent.present[m] = 1
         entries.append(ent)
     table = dev(torch, np.frombuffer(krk.moe_table_bytes(entries), np.uint8).copy())
@@ -325,6 +326,26 @@ def test_moe_dispatch_parity(krk, torch_cuda, be32, n_tok, dt):
     e = rel(host(out), ref)
     say("  rel", e)
     assert e <= GEMV_TOL
+
+
+@pytest.mark.parametrize("n_tok", [1, 5, 70])
+def test_moe_mixed_roles(krk, torch_cuda, be32, n_tok):
+    """A Q4_K_M-style layer: Q4_K gate / up with Q6_K down (the VALU expert
+    path; the digit-plane paths take all-Q4_K layers only)."""
+    torch = torch_cuda
+    dt, ne, n_embd, n_ff, k = (O.Q4_K, O.Q4_K, O.Q6_K), 8, 512, 1024, 4
+    mats, table, keep = build_moe(krk, torch, dt, ne, n_embd, n_ff, seed=980)
+    logits = krk.synth_normal(n_tok * ne, seed=99).reshape(n_tok, ne)
+    ids, wts = O.router_topk(O.router_softmax(logits), k)
+    x = krk.synth_normal(n_tok * n_embd, seed=100).reshape(n_tok, n_embd)
+    say("moe mixed", n_tok)
+    out = torch.empty((n_tok, n_embd), dtype=torch.float32, device="cuda")
+    be32.moe_dispatch(table, 0, ne, dev(torch, ids), dev(torch, wts), dev(torch, x), out, n_tok,
+                      n_embd, n_ff, k)
+    be32.sync()
+    ref = O.moe_ffn(x, [mats[0, e] for e in range(ne)], [mats[1, e] for e in range(ne)],
+                    [mats[2, e] for e in range(ne)], dt, ids, wts, n_ff)
+    assert rel(host(out), ref) <= GEMV_TOL
 
 
 def test_moe_table_rewritten_in_place(krk, torch_cuda, be32):
