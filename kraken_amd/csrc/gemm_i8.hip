@@ -54,7 +54,7 @@ typedef float floatx32 __attribute__((ext_vector_type(32)));
 constexpr int TM = 128, TN = 128, LS = 72;  // f16 LDS row: 64 codes + 8 pad
 
 __device__ __forceinline__ int xcd_map(int g, int G) {
-    // consecutive tiles (which share activation rows) land on one XCD's L2
+    // consecutive tiles land on one XCD (and its L2)
     const int per = G / 8;
     if (g >= per * 8) return g;
     return (g & 7) * per + (g >> 3);
@@ -204,7 +204,10 @@ __global__ void __launch_bounds__(256, 2) gemm_i8_kernel(const _Float16 *__restr
 
     const int Gd = static_cast<int>(gridDim.x);
     const int g = xcd_map(static_cast<int>(blockIdx.x), Gd);
-    const int m0 = (g / tiles_n) * TM, n0 = (g % tiles_n) * TN;
+    // M fastest: the tiles an XCD runs together share weight tiles (a few
+    // hundred KB each, kept in its L2) and stream the activations
+    const int tiles_m = Gd / tiles_n;
+    const int m0 = (g % tiles_m) * TM, n0 = (g / tiles_m) * TN;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int wm = (wv >> 1) * 64, wn = (wv & 1) * 64;
     const int nb = K / 32, nst = (nb + 1) / 2;
