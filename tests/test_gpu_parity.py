@@ -348,6 +348,33 @@ def test_moe_mixed_roles(krk, torch_cuda, be32, n_tok):
     assert rel(host(out), ref) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q8_0, O.Q5_K, O.IQ4_XS, O.MXFP4])
+@pytest.mark.parametrize("n_tok", [1, 5])
+def test_moe_dispatch_f16_activations(krk, torch_cuda, be16, n_tok, dt):
+    """f16 activations (the reference GPU backend's own act_type): the
+    dispatch rounds x, mid and the partial sums to f16 along the way, so it
+    is held to the f32 oracle on the same f16-rounded x within 1e-3 (it
+    measures ~2e-4, the f16 rounding of the output).  The
+    bit-level f16 rounding points are not restated by the oracle (parity of
+    their order is unpinned); routing, decode and the fold are."""
+    torch = torch_cuda
+    ne, n_embd, n_ff, k = 8, 512, 768, 3
+    mats, table, keep = build_moe(krk, torch, dt, ne, n_embd, n_ff, seed=1900)
+    logits = krk.synth_normal(n_tok * ne, seed=177).reshape(n_tok, ne)
+    ids, wts = O.router_topk(O.router_softmax(logits), k)
+    x = krk.synth_normal(n_tok * n_embd, seed=178).reshape(n_tok, n_embd).astype(np.float16)
+    say("moe f16", dt, n_tok)
+    out = torch.empty((n_tok, n_embd), dtype=torch.float16, device="cuda")
+    be16.moe_dispatch(table, 0, ne, dev(torch, ids), dev(torch, wts), dev(torch, x), out, n_tok,
+                      n_embd, n_ff, k)
+    be16.sync()
+    ref = O.moe_ffn(x.astype(np.float32), [mats[0, e] for e in range(ne)], [mats[1, e] for e in range(ne)],
+                    [mats[2, e] for e in range(ne)], dt, ids, wts, n_ff)
+    e = rel(host(out).astype(np.float32), ref)
+    say("  rel", e)
+    assert e <= 1e-3
+
+
 def test_moe_table_rewritten_in_place(krk, torch_cuda, be32):
     """A dispatched table rewritten in place (same address, another bank
     type) is read and checked again after krk_moe_table_forget."""
