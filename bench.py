@@ -34,12 +34,15 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--all", action="store_true", help="also run the other BASELINE configs")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list: gemv,gemm,head,layer,moe")
+    ap.add_argument("--only", default="", help="comma list of sections: gemm,int8,layer,head,moe "
+                    "(the headline GEMV always runs); default all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--pmc-pass", action="store_true",
                     help="counter run: 5 plain copies of 256 MiB, then 20 headline GEMVs")
+    ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
+                    help="turn a rocprofv3 --kernel-trace csv into per-(kernel, grid, block) "
+                         "duration rows (markdown, printed)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc counter_collection.csv files of a "
                          "--pmc-pass run into the traffic summary (printed)")
@@ -56,8 +59,9 @@ class Timer:
     then run back to back exactly as a serving loop's graph would run them.
     """
 
-    def __init__(self, torch, stream, backends):
+    def __init__(self, torch, stream, backends, warm_replays=3):
         self.t, self.s, self.backends = torch, stream, backends
+        self.warm_replays = warm_replays
 
     def run(self, fn, iters, warmup, graph=True):
         torch = self.t
@@ -82,7 +86,10 @@ class Timer:
                 fn(i)
         for be in self.backends:
             be.set_stream(self.s)
-        g.replay()  # warm replay
+        # untimed replays until the clocks and caches settle: the first
+        # replays of a fresh graph run up to ~7% slower than later ones
+        for _ in range(self.warm_replays):
+            g.replay()
         torch.cuda.synchronize()
         e0.record(self.s)
         g.replay()
@@ -92,14 +99,31 @@ class Timer:
 
 
 def rotation(torch, w_host, min_bytes=1 << 30):
+    """Distinct copies of a weight matrix filling >= min_bytes, carved out of
+    one allocation (as a model's weights sit in one arena), so every call
+    streams its matrix from HBM rather than from the 256 MB MALL."""
     base = torch.from_numpy(w_host).cuda()
     n = max(2, -(-min_bytes // base.numel()))
-    return [base] + [base.clone() for _ in range(n - 1)]
+    stride = -(-base.numel() // 256) * 256
+    arena = torch.empty(n * stride, dtype=base.dtype, device=base.device)
+    copies = []
+    for i in range(n):
+        c = arena[i * stride:i * stride + base.numel()]
+        c.copy_(base)
+        copies.append(c)
+    return copies
 
 
-def bench_gemv(K, torch, be, timer, args, dt, n_out, n_in, seed, act_f16=False):
+def bench_gemv(K, torch, be, timer, args, dt, n_out, n_in, seed, act_f16=False, tile=1):
+    """tile > 1: n_out / tile seeded rows quantized and repeated, for the
+    vocabulary-sized heads (the host generator would take ~20 s for 525 M
+    values; the bytes stream from HBM either way)."""
     import numpy as np
-    w = K.quantize(dt, K.synth_normal(n_out * n_in, seed=seed, std=0.02), n_out, n_in, 16)
+    part = n_out // tile
+    assert part * tile == n_out
+    w = K.quantize(dt, K.synth_normal(part * n_in, seed=seed, std=0.02), part, n_in, 16)
+    if tile > 1:
+        w = np.tile(w, tile)
     ws = rotation(torch, w)
     x = K.synth_normal(n_in, seed=seed + 1)
     xt = torch.from_numpy(x.astype(np.float16) if act_f16 else x).cuda()
@@ -218,7 +242,10 @@ def bench_layer_grouped(K, torch, be, timer, copies=4):
 def cpu_baseline(O, w, x, n_out, n_in, seconds):
     """The strict scalar oracle (one f32 chain per output row, parallel over
     rows) on this host's cores, on a bounded sample of the same GEMV."""
-    cores = min(16, os.cpu_count() or 1)
+    # the GPU box gives one GPU's job 16 host threads (its CPU share), whatever
+    # nproc shows; the thread count used and nproc are both reported
+    nproc = os.cpu_count() or 1
+    cores = min(16, nproc)
     t0 = time.perf_counter()
     reps = 0
     while True:
@@ -234,7 +261,7 @@ def cpu_baseline(O, w, x, n_out, n_in, seconds):
     O.gemm(O.Q4_K, w[:rows1 * rb], x, rows1, nthreads=1)
     dt_one = (time.perf_counter() - t1) * n_out / rows1
     nbytes = rb * n_out + (n_in + n_out) * 4
-    return {"value": nbytes / dt_all / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+    return {"value": nbytes / dt_all / 1e9, "unit": "GB/s", "cores": cores, "nproc": nproc, "kind": "port",
             "sample": f"Q4_K GEMV {n_in}->{n_out} M=1, {reps} calls over {dt_all * reps:.1f} s",
             "one_core_GBps": nbytes / dt_one / 1e9}
 
@@ -299,6 +326,34 @@ def summarize_pmc(fetch_csv, write_csv):
             "hbm_bytes_per_launch": gf + gw}
 
 
+def summarize_trace(path):
+    """Average device duration per (kernel, grid, workgroup): each bench
+    configuration launches its kernel with its own grid, so every row is one
+    configuration's kernel."""
+    import csv
+    import statistics
+    rows = {}
+    for r in csv.DictReader(open(path)):
+        key = (r["Kernel_Name"], r.get("Grid_Size", r.get("Grid_Size_X", "")),
+               r.get("Workgroup_Size", r.get("Workgroup_Size_X", "")))
+        rows.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    print("| kernel | grid | block | calls | average (us) | median (us) | min (us) | max (us) |")
+    print("|---|---|---|---|---|---|---|---|")
+    for (name, grid, block), d in sorted(rows.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{name}` | {grid} | {block} | {len(d)} | {statistics.mean(d):.2f} | "
+              f"{statistics.median(d):.2f} | {min(d):.2f} | {max(d):.2f} |")
+
+
+def read_profile_field(fname, key):
+    p = os.path.join(ROOT, "profiles", fname)
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith(key + ":"):
+            return line.split(":", 1)[1].strip()
+    return None
+
+
 def read_traffic():
     p = os.path.join(ROOT, "profiles", "q4k_gemv_4096x14336_traffic.txt")
     if not os.path.exists(p):
@@ -316,6 +371,9 @@ def read_traffic():
 
 def main():
     args = parse()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
     if args.summarize_pmc:
         for k, v in summarize_pmc(*args.summarize_pmc).items():
             print(f"{k}: {v:.1f}" if isinstance(v, float) else f"{k}: {v}")
@@ -369,7 +427,7 @@ def main():
             log(f"  {r['ms'] * 1e3:.1f} us  {r['TFLOPs']:.1f} TOP/s  ({100 * r['TFLOPs'] / INT8_PEAK_TOPS:.1f}% of int8 peak)")
         be16.set_gemm_path(K.PATH_AUTO)
 
-    if args.all or want("layer") and only:
+    if want("layer"):
         # config 2: Llama-2-7B Q4_K decode layer, M = 1 -- per matrix, and as
         # the reference's decode issues it (fused.hpp:48-275): q/k/v in one
         # grouped launch, gate/up with the SiLU folded in, then o and down
@@ -378,25 +436,28 @@ def main():
                            ("o", (4096, 4096)), ("gate", (11008, 4096)), ("up", (11008, 4096)),
                            ("down", (4096, 11008))):
             r = bench_gemv(K, torch, be32, timer, args, K.Q4_K, o, i, seed=20)
-            extras[f"layer_{nm}"] = {"us": r["ms"] * 1e3, "GBps": r["GBps"]}
+            extras[f"layer_{nm}"] = {"us": r["ms"] * 1e3, "GBps": r["GBps"], "frac_hbm": r["GBps"] / HBM_PEAK_GBS}
             tot_b += r["bytes"]
             tot_ms += r["ms"]
-        extras["layer_total"] = {"us": tot_ms * 1e3, "GBps": tot_b / tot_ms / 1e6}
+        extras["layer_total"] = {"us": tot_ms * 1e3, "GBps": tot_b / tot_ms / 1e6,
+                                 "frac_hbm": tot_b / tot_ms / 1e6 / HBM_PEAK_GBS}
         log(f"  layer, 7 launches: {tot_ms * 1e3:.1f} us {tot_b / tot_ms / 1e6:.0f} GB/s")
         r = bench_layer_grouped(K, torch, be32, timer)
+        r["frac_hbm"] = r["GBps"] / HBM_PEAK_GBS
         extras["layer_grouped"] = r
         log(f"  layer, 4 grouped launches: {r['us']:.1f} us {r['GBps']:.0f} GB/s")
-    if args.all or want("head") and only:
+    if want("head"):
         for dt, nm in ((K.Q6_K, "q6_k"), (K.Q8_0, "q8_0")):
-            r = bench_gemv(K, torch, be32, timer, args, dt, 128256, 4096, seed=30)
+            r = bench_gemv(K, torch, be32, timer, args, dt, 128256, 4096, seed=30, tile=16)
             extras[f"head_{nm}"] = {"us": r["ms"] * 1e3, "GBps": r["GBps"],
                                     "frac_hbm": r["GBps"] / HBM_PEAK_GBS}
             log(f"  head {nm} {r['ms'] * 1e3:.1f} us {r['GBps']:.0f} GB/s")
 
-    if args.all or want("moe") and only:
+    if want("moe"):
         for T in (1, 16):
             log(f"moe C5 n_tok={T} ...")
             r = bench_moe(K, torch, be32, timer, T)
+            r["frac_hbm"] = r["GBps"] / HBM_PEAK_GBS
             extras[f"moe_c5_t{T}"] = r
             log(f"  {r['us']:.1f} us  {r['GBps']:.0f} GB/s  ({r['distinct_experts']:.1f} experts)")
 
@@ -426,7 +487,7 @@ def main():
                    "rows": 1, "activations": "f32", "weight_copies": g["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(), "kernel": "gemv_digits_kernel<Q4_K, float, float, 28, 2, 2, false, 1, false, false>",
+                     "traffic": read_traffic(), "kernel": read_profile_field("q4k_gemv_4096x14336_kernel_trace.md", "headline_kernel"),
                      "algorithmic_bytes_per_launch": g["bytes"]},
         "cpu_baseline": cpu and {k: v for k, v in cpu.items()},
         "extras": extras,

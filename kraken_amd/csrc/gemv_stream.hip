@@ -1,0 +1,428 @@
+// gemv_stream.hip -- one-row decode GEMV for Q4_K weights with every byte of a
+// workgroup's tile requested in its first instructions.
+//
+// The products run on the int8 matrix cores exactly as in gemv_digits.hip:
+// the weight codes are the B operand, the activations enter as three exact
+// int8 digit planes per 32-value sub-block, and the Q4_K block formula
+// (src/quant.cpp:427-447) is applied once per (row, sub-block) to the exact
+// plane sums.  What differs is the data movement, which sets the time of a
+// decode GEMV far more than the arithmetic does:
+//
+//   * A workgroup owns one tile of up to 32 rows over all of K; its waves
+//     split K into contiguous slices of NBW blocks.  A wave loads its x slice
+//     and then every weight byte of its slice of the tile straight into
+//     registers (three 16-byte loads per 16 rows x 1 block), before any
+//     arithmetic.  With two workgroups per CU the whole matrix of a 33 MB
+//     decode GEMV is in flight from the start of the launch.
+//   * The digit table of a wave covers only its own K slice, so a wave builds
+//     it alone: no barrier and no LDS-shared table stands between the data
+//     arriving and the first MFMA.  Each (16 rows, block) group is decoded
+//     as soon as its three loads have landed (the loads return in order).
+//   * The waves' partial sums meet once, in LDS, at the end of the tile, and
+//     are added in wave order, so the result does not depend on timing.
+//
+// Tiles: plain and residual (SEG_ACC) segments take tiles of TR rows (16 to
+// 32, chosen per launch so that the tiles fill the chip in as few rounds as
+// possible); gate/up (SEG_SILU) segments take 16 gate rows and the same 16
+// up rows and write silu(gate) * up.  The grid is tiles x segments.
+#include <cstdint>
+
+#include "gemv_core.hpp"
+#include "krk_formats.hpp"
+#include "krk_kernels.hpp"
+
+namespace krk {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kTab = 768;   // digit bytes per 256-value block: 8 sub-blocks x 3 planes x 32
+constexpr int kMaxWaves = 16;
+
+__device__ __forceinline__ v4i lds_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
+
+// quad-lane exchanges (lanes l ^ 1 and l ^ 2) through DPP
+__device__ __forceinline__ float quad_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+
+// eight consecutive activations (16-byte aligned) as f32
+__device__ __forceinline__ void load_x8(const float *p, float (&v)[8]) {
+    const floatx4 a = *reinterpret_cast<const floatx4 *>(p);
+    const floatx4 b = *reinterpret_cast<const floatx4 *>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+__device__ __forceinline__ void load_x8(const _Float16 *p, float (&v)[8]) {
+    const half8 h = *reinterpret_cast<const half8 *>(p);
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = static_cast<float>(h[k]);
+}
+
+template <typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWEXACT, int LA = 8>
+__global__ void __launch_bounds__(64 * NWMAX) gemv_stream_q4k(SegTable t) {
+    constexpr int RG = (TR + 15) / 16;     // 16-row groups of a plain tile
+    constexpr int NL = RG * NBW;           // (16 rows, block) groups of a wave
+    constexpr int NPASS = (NBW + 1) / 2;   // x passes: 16 sub-blocks of 8 x 4 lanes each
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // NWEXACT: the launch has exactly NWMAX waves (the common widths 8 and
+    // 16), which lets the LDS offsets and the final sums fold to constants
+    const int nw = NWEXACT ? NWMAX : static_cast<int>(blockDim.x) >> 6;
+    const int c16 = lane & 15, gq = lane >> 4;
+    const int kb0 = wv * NBW;
+
+    // the tile: segment blockIdx.y, tile blockIdx.x of it.  Indexing the
+    // segment by the grid, and reading all of its fields before any test,
+    // keeps them one round of scalar loads away from the first weight
+    // request.  A segment with fewer tiles than the grid's width gives its
+    // extra workgroups the last rows to re-read, and they store nothing.
+    const Seg &sg = t.seg[blockIdx.y];
+    const int kind = sg.kind;
+    const int64_t n_out = sg.n_out;
+    const uint8_t *w = static_cast<const uint8_t *>(sg.w);
+    const uint8_t *w2s = static_cast<const uint8_t *>(sg.w2);
+    const XT *x = static_cast<const XT *>(sg.x);
+    const int64_t rb = t.row_bytes;
+    const int nb = t.n_in >> 8;
+    const bool pair = kind == SEG_SILU;
+    const int rows_t = pair ? 16 : TR;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * rows_t;
+    const uint8_t *w2 = pair ? w2s : w;
+
+    // ---- the wave's activations first: pass p, lane l holds values
+    // 8 (l & 3) .. + 7 of the slice's sub-block 16 p + l / 4
+    // the loads issue at raised wave priority, so a wave that is still
+    // issuing wins the vector-memory port over one that is already decoding
+    __builtin_amdgcn_s_setprio(3);
+    float xv[NPASS][8];
+#pragma unroll
+    for (int p = 0; p < NPASS; p++) {
+        const int sbw = p * 16 + (lane >> 2);
+        const bool in = sbw < 8 * NBW && kb0 + (sbw >> 3) < nb;
+        load_x8(x + (in ? static_cast<int64_t>(kb0) * 256 + sbw * 32 + 8 * (lane & 3) : 0), xv[p]);
+        if (!in) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) xv[p][k] = 0.0f;
+        }
+    }
+    // ---- then every weight byte of the wave's slice of the tile: group i =
+    // (row group rg, block b): lane (c16, gq) takes row rg * 16 + c16's
+    // header and code bytes 16 gq .. + 15 of each 64-byte half
+    u32x4 hd[NL], qa[NL], qb[NL];
+    const uint8_t *src[NL];
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int rg = i / NBW, b = i - (i / NBW) * NBW;
+        int64_t n;
+        const uint8_t *base;
+        if (pair) {
+            n = n0 + c16;
+            base = rg == 0 ? w : w2;
+        } else {
+            const int r = rg * 16 + c16 < rows_t ? rg * 16 + c16 : rows_t - 1;
+            n = n0 + r;
+            base = w;
+        }
+        if (n >= n_out) n = n_out - 1;
+        // a ragged last slice re-reads the matrix's last block (discarded)
+        const int blk = kb0 + b < nb ? kb0 + b : nb - 1;
+        src[i] = base + n * rb + static_cast<int64_t>(blk) * 144;
+    }
+    auto issue = [&](int i) {
+        hd[i] = ld128(src[i]);
+        qa[i] = ld128(src[i] + 16 + 16 * gq);
+        qb[i] = ld128(src[i] + 80 + 16 * gq);
+    };
+#pragma unroll
+    for (int i = 0; i < (LA < NL ? LA : NL); i++) issue(i);
+    __builtin_amdgcn_s_setprio(0);
+
+    // ---- the digit table of the slice (this wave's own LDS), layout
+    // [block][sub-block][plane][32 bytes], and {2^-e, sum x} per sub-block
+    uint8_t *tab = lds + wv * (NBW * kTab);
+    float2 *ex = reinterpret_cast<float2 *>(lds + nw * (NBW * kTab)) + wv * (NBW * 8);
+    float *red = reinterpret_cast<float *>(lds + nw * (NBW * kTab + NBW * 8 * sizeof(float2)));
+#pragma unroll
+    for (int p = 0; p < NPASS; p++) {
+        const int sbw = p * 16 + (lane >> 2);
+        const float *v = xv[p];
+        float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            amax = fmaxf(amax, fabsf(v[k]));
+            sum += v[k];
+        }
+        amax = fmaxf(amax, quad_xor1(amax));
+        amax = fmaxf(amax, quad_xor2(amax));
+        sum += quad_xor1(sum);
+        sum += quad_xor2(sum);
+        // 2^e with |x| 2^e < 2^22: e = 148 - the exponent field of the
+        // sub-block's largest |x|, so the top digit stays within [-64, 64];
+        // zero and non-finite sub-blocks get no digits (a non-finite x makes
+        // the sum, and so the row, non-finite as in the reference)
+        const uint32_t Eb = (__float_as_uint(amax) >> 23) & 255u;
+        const bool live = amax > 0.0f && Eb < 255u;
+        int e = live ? 148 - static_cast<int>(Eb) : 0;
+        e = e > 126 ? 126 : e;
+        const float up = __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
+        const float dn = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+        uint32_t p0[2] = {0u, 0u}, p1[2] = {0u, 0u}, p2[2] = {0u, 0u};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int X = live ? static_cast<int>(__builtin_rintf(v[k] * up)) : 0;
+            const int d0 = ((X + 128) & 255) - 128;
+            const int X1 = (X - d0) >> 8;
+            const int d1 = ((X1 + 128) & 255) - 128;
+            const int d2 = (X1 - d1) >> 8;
+            const int sh = 8 * (k & 3);
+            p0[k >> 2] |= (static_cast<uint32_t>(d0) & 255u) << sh;
+            p1[k >> 2] |= (static_cast<uint32_t>(d1) & 255u) << sh;
+            p2[k >> 2] |= (static_cast<uint32_t>(d2) & 255u) << sh;
+        }
+        if (sbw < 8 * NBW) {
+            uint8_t *o = tab + (sbw >> 3) * kTab + (sbw & 7) * 96 + 8 * (lane & 3);
+            *reinterpret_cast<u32x2 *>(o) = u32x2{p0[0], p0[1]};
+            *reinterpret_cast<u32x2 *>(o + 32) = u32x2{p1[0], p1[1]};
+            *reinterpret_cast<u32x2 *>(o + 64) = u32x2{p2[0], p2[1]};
+            if ((lane & 3) == 0) ex[sbw] = float2{live ? dn : 1.0f, sum};
+        }
+    }
+
+    // ---- per-lane MFMA roles (A row c16 = 4 sub-block' + digit plane)
+    const int ap = c16 & 3, as = c16 >> 2;
+    const int sl = 2 * (gq >> 1);
+    const bool a_lo = ap < 3 && as == sl, a_hi = ap < 3 && as == sl + 1;
+    const int a_off = as * 96 + (ap < 3 ? ap : 0) * 32 + 16 * (gq & 1);
+    const uint32_t M = 0x0F0F0F0Fu;
+    const uint32_t bsh = 8u * static_cast<uint32_t>(gq);
+    const v4i Z = {0, 0, 0, 0};
+    float acc[RG];
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++) acc[rg] = 0.0f;
+    // two-block slices read their A operands once, before the first group
+    // lands (wider slices read them per group: registers)
+    constexpr bool HOLD = NBW == 2;
+    v4i HA[HOLD ? NBW : 1][4];
+    float2 HE[HOLD ? NBW : 1][2];
+    if constexpr (HOLD) {
+#pragma unroll
+        for (int b = 0; b < NBW; b++) {
+            const uint8_t *tb = tab + b * kTab + a_off;
+            HA[b][0] = a_lo ? lds_v4i(tb) : Z;
+            HA[b][1] = a_lo ? lds_v4i(tb + 384) : Z;
+            HA[b][2] = a_hi ? lds_v4i(tb) : Z;
+            HA[b][3] = a_hi ? lds_v4i(tb + 384) : Z;
+            HE[b][0] = ex[b * 8 + gq];
+            HE[b][1] = ex[b * 8 + 4 + gq];
+        }
+    }
+    // group i is decoded after group i + LA is requested (LA: requests in
+    // flight ahead of the decode; measured best with every request issued
+    // before the first decode)
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        if (i + LA < NL) issue(i + LA);
+        __builtin_amdgcn_sched_barrier(0);
+        const int rg = i / NBW, b = i - (i / NBW) * NBW;
+        if (kb0 + b >= nb) continue;   // wave-uniform: the ragged slice's missing blocks
+        const uint8_t *tb = tab + b * kTab + a_off;
+        const int hb = HOLD ? b : 0;
+        const v4i A0l = HOLD ? HA[hb][0] : a_lo ? lds_v4i(tb) : Z;
+        const v4i A1l = HOLD ? HA[hb][1] : a_lo ? lds_v4i(tb + 384) : Z;
+        const v4i A0h = HOLD ? HA[hb][2] : a_hi ? lds_v4i(tb) : Z;
+        const v4i A1h = HOLD ? HA[hb][3] : a_hi ? lds_v4i(tb + 384) : Z;
+        const float2 ex0 = HOLD ? HE[hb][0] : ex[b * 8 + gq], ex1 = HOLD ? HE[hb][1] : ex[b * 8 + 4 + gq];
+        const u32x4 h = hd[i], q0 = qa[i], q1 = qb[i];
+        const v4i B0l = {static_cast<int>(q0.x & M), static_cast<int>(q0.y & M), static_cast<int>(q0.z & M),
+                         static_cast<int>(q0.w & M)};
+        const v4i B0h = {static_cast<int>((q0.x >> 4) & M), static_cast<int>((q0.y >> 4) & M),
+                         static_cast<int>((q0.z >> 4) & M), static_cast<int>((q0.w >> 4) & M)};
+        const v4i B1l = {static_cast<int>(q1.x & M), static_cast<int>(q1.y & M), static_cast<int>(q1.z & M),
+                         static_cast<int>(q1.w & M)};
+        const v4i B1h = {static_cast<int>((q1.x >> 4) & M), static_cast<int>((q1.y >> 4) & M),
+                         static_cast<int>((q1.z >> 4) & M), static_cast<int>((q1.w >> 4) & M)};
+        // scales and mins of sub-blocks gq and 4 + gq (get_scale_min_k4,
+        // src/quant.cpp:427-435): byte gq of scales[0..3], [4..7], [8..11]
+        const uint32_t s1 = h.y >> bsh, s2 = h.z >> bsh, s3 = h.w >> bsh;
+        const float d = h2f(h.x & 0xFFFFu), dmin = h2f(h.x >> 16);
+        const float sc0 = static_cast<float>(s1 & 63u), m0 = static_cast<float>(s2 & 63u);
+        const float sc1 = static_cast<float>((s3 & 15u) | ((s1 >> 2) & 0x30u));
+        const float m1 = static_cast<float>(((s3 >> 4) & 15u) | ((s2 >> 2) & 0x30u));
+        v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0l, B0l, Z, 0, 0, 0);
+        C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0h, B0h, C0, 0, 0, 0);
+        v4i C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1l, B1l, Z, 0, 0, 0);
+        C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1h, B1h, C1, 0, 0, 0);
+        // lane (c16, gq): C rows 4 gq .. 4 gq + 2 are sub-block gq's (C0) and
+        // 4 + gq's (C1) three plane sums for weight row c16
+        const int S0 = C0[0] + (C0[1] << 8) + (C0[2] << 16);
+        const int S1 = C1[0] + (C1[1] << 8) + (C1[2] << 16);
+        float a = acc[rg];
+        a = __builtin_fmaf(d * sc0, ex0.x * static_cast<float>(S0), a);
+        a = __builtin_fmaf(-dmin * m0, ex0.y, a);
+        a = __builtin_fmaf(d * sc1, ex1.x * static_cast<float>(S1), a);
+        a = __builtin_fmaf(-dmin * m1, ex1.y, a);
+        acc[rg] = a;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- the waves' partial sums -> LDS [row][wave]; one thread per output
+    // row adds them in wave order
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++) {
+        // the sum over the four 16-lane rows by the cross-row swaps (VALU,
+        // no LDS): a swap of v with itself leaves rows (0, 0, 2, 2) in one
+        // result and (1, 1, 3, 3) in the other (16-lane swap), or (0, 1, 0,
+        // 1) and (2, 3, 2, 3) (32-lane swap)
+        float v = acc[rg];
+        const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+        const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
+        if (gq == 0) red[(rg * 16 + c16) * nw + wv] = v;
+    }
+    __syncthreads();
+    const int r = static_cast<int>(threadIdx.x);
+    if (r >= rows_t || n0 + r >= n_out) return;
+    auto row_sum = [&](int rr) {
+        float v = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NWMAX; k++)
+            if (k < nw) v += red[rr * nw + k];
+        return v;
+    };
+    OT *o = static_cast<OT *>(sg.out) + n0 + r;
+    if (kind == SEG_SILU) {
+        const float gs = row_sum(r), us = row_sum(16 + r);
+        if constexpr (sizeof(OT) == 2) {
+            // fused_gate_silu_kernel (fused.hpp:161-166): both dots rounded to
+            // f16, activation in f32, saturated
+            const float hg = static_cast<float>(static_cast<_Float16>(gs));
+            const float hu = static_cast<float>(static_cast<_Float16>(us));
+            *o = sat_f16(silu_f(hg) * hu);
+        } else {
+            *o = (gs / (1.0f + expf(-gs))) * us;   // silu_mul, backend_cpu.cpp:2401-2406
+        }
+    } else {
+        const float inv = kind == SEG_ACC && t.rexp ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
+        store_out<OT>(o, row_sum(r), kind, inv);
+    }
+}
+
+int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    return cus;
+}
+
+size_t stream_lds(int nw, int nbw) {
+    return static_cast<size_t>(nw) * nbw * (kTab + 8 * sizeof(float2)) + 32 * static_cast<size_t>(nw) * sizeof(float);
+}
+
+template <typename XT, typename OT, int NBW, int TR>
+hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
+    const size_t l = stream_lds(nw, NBW);
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(t.n));
+    if (nw == 8)
+        hipLaunchKernelGGL((gemv_stream_q4k<XT, OT, NBW, TR, 8, true>), grid, dim3(64 * nw), l, st, t);
+    else if (nw < 8)
+        hipLaunchKernelGGL((gemv_stream_q4k<XT, OT, NBW, TR, 8, false>), grid, dim3(64 * nw), l, st, t);
+    else if (nw == kMaxWaves)
+        hipLaunchKernelGGL((gemv_stream_q4k<XT, OT, NBW, TR, kMaxWaves, true>), grid, dim3(64 * nw), l, st, t);
+    else
+        hipLaunchKernelGGL((gemv_stream_q4k<XT, OT, NBW, TR, kMaxWaves, false>), grid, dim3(64 * nw), l, st, t);
+    return hipGetLastError();
+}
+
+template <typename XT, typename OT, int NBW>
+hipError_t launch_tr(const SegTable &t, int tr, int64_t tiles, int nw, hipStream_t st) {
+    if constexpr (NBW == 2) {
+        switch (tr) {
+            case 20: return launch<XT, OT, NBW, 20>(t, tiles, nw, st);
+            case 24: return launch<XT, OT, NBW, 24>(t, tiles, nw, st);
+            case 28: return launch<XT, OT, NBW, 28>(t, tiles, nw, st);
+            case 32: return launch<XT, OT, NBW, 32>(t, tiles, nw, st);
+            default: break;
+        }
+    }
+    return launch<XT, OT, NBW, 16>(t, tiles, nw, st);
+}
+
+// blocks per wave: two when K has at most 32 blocks (eight waves for 4096),
+// else as few as keep the waves at 16 per workgroup
+int stream_nbw(int nb) { return nb <= 32 ? 2 : (nb + kMaxWaves - 1) / kMaxWaves; }
+
+}  // namespace
+
+bool gemv_stream_ok(int dt, const SegTable &t) {
+    if (dt != DT_Q4_K || t.rows != 1 || t.moe_tab || t.em_items) return false;
+    if (t.n_in % 256 || t.n_in > 256 * 4 * kMaxWaves || t.row_bytes % 16) return false;
+    const int nbw = stream_nbw(t.n_in / 256);
+    for (int i = 0; i < t.n; i++) {
+        const Seg &s = t.seg[i];
+        // gate/up pairs take two row groups, which wider slices cannot afford
+        if (s.kind == SEG_SILU && nbw > 2) return false;
+        if (s.x != t.seg[0].x || (reinterpret_cast<uintptr_t>(s.x) & 15) ||
+            (reinterpret_cast<uintptr_t>(s.w) & 15))
+            return false;
+        if (s.kind == SEG_SILU && (reinterpret_cast<uintptr_t>(s.w2) & 15)) return false;
+    }
+    return true;
+}
+
+hipError_t gemv_stream(bool act_f16, const SegTable &t0, hipStream_t st) {
+    SegTable t = t0;
+    const int nb = t.n_in / 256;
+    const int nbw = stream_nbw(nb);
+    const int nw = (nb + nbw - 1) / nbw;
+    bool has_pair = false;
+    for (int i = 0; i < t.n; i++) has_pair |= t.seg[i].kind == SEG_SILU;
+    // tile height: among 16, 20, .., 32 (32 with gate/up pairs, which need
+    // two row groups; 16 for slices of more than two blocks, whose registers
+    // hold one row group), the one whose tiles fill the resident workgroups
+    // (two per CU at up to eight waves) in the fewest rounds x rows
+    const int64_t cap = static_cast<int64_t>(device_cus()) * (nw <= 8 ? 2 : 1);
+    int tr = 16;
+    int64_t best = INT64_MAX;
+    for (int c = has_pair ? 32 : 16; c <= (nbw > 2 ? 16 : 32); c += 4) {
+        int64_t tiles = 0;
+        for (int i = 0; i < t.n; i++) {
+            const int rows_t = t.seg[i].kind == SEG_SILU ? 16 : c;
+            tiles += (t.seg[i].n_out + rows_t - 1) / rows_t;
+        }
+        const int64_t cost = (tiles + cap - 1) / cap * c;
+        if (cost < best) { best = cost; tr = c; }
+    }
+    // the grid: one row of tiles per segment, as wide as the longest
+    int64_t width = 0;
+    for (int i = 0; i < t.n; i++) {
+        const int64_t rows_t = t.seg[i].kind == SEG_SILU ? 16 : tr;
+        const int64_t n = (t.seg[i].n_out + rows_t - 1) / rows_t;
+        width = n > width ? n : width;
+    }
+    if (width >= (int64_t{1} << 31) || t.n < 1) return hipErrorNotSupported;
+    if (act_f16) {
+        switch (nbw) {
+            case 2: return launch_tr<_Float16, _Float16, 2>(t, tr, width, nw, st);
+            case 3: return launch_tr<_Float16, _Float16, 3>(t, tr, width, nw, st);
+            default: return launch_tr<_Float16, _Float16, 4>(t, tr, width, nw, st);
+        }
+    }
+    switch (nbw) {
+        case 2: return launch_tr<float, float, 2>(t, tr, width, nw, st);
+        case 3: return launch_tr<float, float, 3>(t, tr, width, nw, st);
+        default: return launch_tr<float, float, 4>(t, tr, width, nw, st);
+    }
+}
+
+}  // namespace krk
