@@ -21,6 +21,7 @@
 #ifndef KRK_MI355X_H
 #define KRK_MI355X_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -126,6 +127,22 @@ int krk_dtype_row_aligned(int wt, int64_t n);
  * rows  > 8   : per krk_set_gemm_path. */
 int krk_gemm(krk_backend *b, void *out, const void *x, const void *w, int wt,
              int64_t n_out, int64_t n_in, int64_t rows);
+
+/* krk_gemm without allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Same
+ * arguments, kernels and results as krk_gemm (bit-identical), but the
+ * split-K partials and int8 activation codes that krk_gemm keeps in the
+ * handle's growing workspace live in a fixed device array of
+ * krk_gemm_noalloc_scratch_bytes() (64 MiB) instead: one per device, held
+ * until the process ends, shared by every handle on that device.  A call
+ * whose scratch would exceed it returns KRK_ERR_NOMEM before any launch.
+ * Calls that overlap on one device (several streams or threads) race on
+ * that array; serialise them.  Nothing in the array needs to start at zero:
+ * every call writes the scratch it reads. */
+int krk_gemm_noalloc(krk_backend *b, void *out, const void *x, const void *w, int wt,
+                     int64_t n_out, int64_t n_in, int64_t rows);
+size_t krk_gemm_noalloc_scratch_bytes(void);
 
 /* Backend::gemm_k_ok -- backend.hpp:869.  1 when a contraction of k columns
  * can be addressed (k > 0 and a multiple of 32; the weight type adds its own

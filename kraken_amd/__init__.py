@@ -49,6 +49,8 @@ SIGNATURES = {
     "krk_dtype_row_bytes": (_i64, [_i32, _i64]),
     "krk_dtype_row_aligned": (_i32, [_i32, _i64]),
     "krk_gemm": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64]),
+    "krk_gemm_noalloc": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64]),
+    "krk_gemm_noalloc_scratch_bytes": (C.c_size_t, []),
     "krk_gemm_k_ok": (_i32, [_vp, _i64]),
     "krk_gemm_accumulate": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp,
                                    _P(_i32)]),
@@ -212,6 +214,12 @@ class Backend:
     def gemm(self, out, x, w, wt: int, n_out: int, n_in: int, rows: int):
         self._check(lib().krk_gemm(self._h, _ptr(out), _ptr(x), _ptr(w), wt, n_out, n_in,
                                    rows), "gemm")
+
+    def gemm_noalloc(self, out, x, w, wt: int, n_out: int, n_in: int, rows: int):
+        """gemm with its scratch in the library's fixed per-device array
+        (krk_gemm_noalloc): never allocates; KRK_ERR_NOMEM past its size."""
+        self._check(lib().krk_gemm_noalloc(self._h, _ptr(out), _ptr(x), _ptr(w), wt, n_out, n_in,
+                                           rows), "gemm_noalloc")
 
     def gemm_k_ok(self, k: int) -> bool:
         return bool(lib().krk_gemm_k_ok(self._h, k))

@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -29,6 +30,7 @@ struct MoeKey {
 
 struct krk_backend {
     int device = 0;
+    void *scratch = nullptr;   // this device's address of `scratch` (krk_gemm_noalloc)
     int act = KRK_ACT_F32;
     int path = KRK_PATH_AUTO;
     hipStream_t stream = nullptr;
@@ -41,7 +43,33 @@ struct krk_backend {
     int n_moe_ok = 0;
 };
 
+// Device scratch of krk_gemm_noalloc: split-K partials and int8 activation
+// codes live here instead of in the handle's workspace, so that entry point
+// never allocates.  Every device the library runs on holds one copy until
+// the process ends; calls that overlap on one device share it (and race).
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[kMaxDevices];
+
+// this device's address of `scratch` (the host-side name is only a
+// stand-in); taken once per device, with that device current
+hipError_t scratch_address(int device, void **out) {
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch[device] = p;
+    }
+    *out = g_scratch[device];
+    return hipSuccess;
+}
 
 int fail(krk_backend *b, int code, const char *fmt, ...) {
     char buf[512];
@@ -215,6 +243,9 @@ int krk_backend_create(int device, int act, krk_backend **out) {
     krk_backend *b = new krk_backend();
     b->device = device;
     b->act = act;
+    // krk_gemm_noalloc's scratch address on this device; a failure here
+    // leaves it null, and only that entry point reports it
+    if (scratch_address(device, &b->scratch) != hipSuccess) b->scratch = nullptr;
     *out = b;
     return KRK_OK;
 }
@@ -259,8 +290,14 @@ int krk_gemm_k_ok(const krk_backend *b, int64_t k) {
     return k > 0 && (k % 32) == 0 && k <= (int64_t(1) << 30);
 }
 
-int krk_gemm(krk_backend *b, void *out, const void *x, const void *w, int wt, int64_t n_out,
-             int64_t n_in, int64_t rows) {
+}  // extern "C"
+
+namespace {
+
+// gemm with its scratch either in the handle's workspace (grown on demand,
+// ws == nullptr) or in a caller-fixed buffer of ws_bytes (never allocates)
+int gemm_impl(krk_backend *b, void *out, const void *x, const void *w, int wt, int64_t n_out, int64_t n_in,
+              int64_t rows, void *ws, size_t ws_bytes) {
     if (int s = check_mm(b, out, x, w, wt, n_out, n_in, rows)) return s;
     if (int s = make_current(b)) return s;
     const bool f16 = b->act == KRK_ACT_F16;
@@ -269,19 +306,52 @@ int krk_gemm(krk_backend *b, void *out, const void *x, const void *w, int wt, in
         return run_gemv(b, wt, t);
     }
     const int64_t rb = krk_dtype_row_bytes(wt, n_in);
+    const bool fixed = ws != nullptr;
     if (b->path == KRK_PATH_INT8) {
         if (!krk::gemm_int8_serves(wt))
             return fail(b, KRK_ERR_UNSUPPORTED, "the int8 rung serves Q8_0, Q4_K, Q5_K and Q6_K weights");
-        if (int s = ensure_ws(b, krk::gemm_int8_workspace(rows, n_in))) return s;
-        const hipError_t e = krk::gemm_int8(wt, w, rb, x, f16, out, rows, n_out, n_in, b->ws,
-                                            b->ws_bytes, b->stream);
+        const size_t need = krk::gemm_int8_workspace(rows, n_in);
+        if (fixed && need > ws_bytes)
+            return fail(b, KRK_ERR_NOMEM, "int8 gemm needs %zu bytes of scratch; the fixed scratch holds %zu",
+                        need, ws_bytes);
+        if (!fixed) {
+            if (int s = ensure_ws(b, need)) return s;
+            ws = b->ws;
+            ws_bytes = b->ws_bytes;
+        }
+        const hipError_t e = krk::gemm_int8(wt, w, rb, x, f16, out, rows, n_out, n_in, ws, ws_bytes, b->stream);
         return e == hipSuccess ? KRK_OK : hip_fail(b, e, "int8 gemm");
     }
-    if (int s = ensure_ws(b, krk::gemm_mfma_workspace(wt, rows, n_out, n_in))) return s;
-    const hipError_t e = krk::gemm_mfma(wt, w, rb, x, f16, out, rows, n_out, n_in, b->ws,
-                                        b->ws_bytes, b->stream);
+    const size_t need = krk::gemm_mfma_workspace(wt, rows, n_out, n_in);
+    if (fixed && need > ws_bytes)
+        return fail(b, KRK_ERR_NOMEM, "mfma gemm needs %zu bytes of split-K scratch; the fixed scratch holds %zu",
+                    need, ws_bytes);
+    if (!fixed) {
+        if (int s = ensure_ws(b, need)) return s;
+        ws = b->ws;
+        ws_bytes = b->ws_bytes;
+    }
+    const hipError_t e = krk::gemm_mfma(wt, w, rb, x, f16, out, rows, n_out, n_in, ws, ws_bytes, b->stream);
     return e == hipSuccess ? KRK_OK : hip_fail(b, e, "mfma gemm");
 }
+
+}  // namespace
+
+extern "C" {
+
+int krk_gemm(krk_backend *b, void *out, const void *x, const void *w, int wt, int64_t n_out,
+             int64_t n_in, int64_t rows) {
+    return gemm_impl(b, out, x, w, wt, n_out, n_in, rows, nullptr, 0);
+}
+
+int krk_gemm_noalloc(krk_backend *b, void *out, const void *x, const void *w, int wt, int64_t n_out,
+                     int64_t n_in, int64_t rows) {
+    if (!b) return KRK_ERR_ARG;
+    if (!b->scratch) return fail(b, KRK_ERR_HIP, "gemm_noalloc: no scratch address on device %d", b->device);
+    return gemm_impl(b, out, x, w, wt, n_out, n_in, rows, b->scratch, kScratchBytes);
+}
+
+size_t krk_gemm_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 int krk_gemm_accumulate(krk_backend *b, void *dst, const void *x, const void *w, int wt,
                         int64_t n_out, int64_t n_in, int64_t rows, const int32_t *rexp,
