@@ -31,8 +31,9 @@ extern "C" {
 /* GGUF type ids; these block formats (plus F16/F32 activations) are on
  * this path.  include/krk/quant.hpp:16-47.  Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K, IQ4_NL, IQ4_XS,
  * MXFP4 and unquantized F16 / BF16 weights (16-byte aligned) are served by
- * the dequant, GEMV (rows 1..8, exact prefill) and MFMA GEMM paths;
- * moe_dispatch banks take Q4_0 / Q8_0 / Q4_K / Q6_K, the int8 rung Q8_0. */
+ * the dequant, GEMV (rows 1..8, exact prefill) and MFMA GEMM paths, and by
+ * moe_dispatch as expert banks (one type per role in a layer, gate = up);
+ * the int8 rung takes Q8_0, Q4_K, Q5_K and Q6_K. */
 enum krk_dtype {
     KRK_DT_F32 = 0,
     KRK_DT_F16 = 1,
@@ -197,9 +198,15 @@ int krk_router_topk(krk_backend *b, const void *probs, int64_t n_rows,
  * xn and out are [n_tok, n_embd] in the activation type; ids int32 and wts
  * f32 [n_tok, k] device arrays.
  * The first call for a (table, layer, n_expert, n_embd, n_ff) reads that
- * layer's entries back once and validates them (types, geometry, alignment);
- * later calls with the same key launch without a host round trip, so a
- * table's layer must not change while the handle remembers it. */
+ * layer's entries back once and validates every one: all three matrices
+ * present, of a served type (one type per role across the layer, gate and
+ * up alike), n_out / n_in equal to the layer's geometry, row_bytes equal to
+ * krk_dtype_row_bytes(type, n_in), rows aligned for the type's loads.  Later
+ * calls with the same key launch without a host round trip (and can be
+ * graph-captured), so a table's layer must not change while the handle
+ * remembers it.  The handle remembers up to 256 keys; past that the oldest
+ * is dropped and is read and validated again on its next call (that call
+ * blocks on the read-back and cannot be captured). */
 int krk_moe_dispatch_supported(const krk_backend *b);
 int krk_moe_dispatch(krk_backend *b, const void *table, int layer,
                      int n_expert, const void *ids, const void *wts,

@@ -504,12 +504,28 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
                 if (en.type[m] != e0.type[m] || en.type[1] != en.type[0])
                     return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: mixed expert formats");
                 if (reinterpret_cast<uintptr_t>(en.p[m]) & 15) aligned = false;
+                // the kernels step every bank's rows by its type's row size
+                // (one stride per role for the whole layer)
+                if (en.row_bytes[m] != krk_dtype_row_bytes(en.type[m], en.n_in[m]))
+                    return fail(b, KRK_ERR_ARG,
+                                "moe_dispatch: expert %d matrix %d row_bytes %lld is not the row size %lld of "
+                                "type %d at n_in %lld",
+                                e, m, (long long)en.row_bytes[m],
+                                (long long)krk_dtype_row_bytes(en.type[m], en.n_in[m]), en.type[m],
+                                (long long)en.n_in[m]);
             }
             if (en.n_in[0] != n_embd || en.n_out[0] != n_ff || en.n_in[1] != n_embd || en.n_out[1] != n_ff ||
                 en.n_in[2] != n_ff || en.n_out[2] != n_embd)
                 return fail(b, KRK_ERR_SHAPE, "moe_dispatch: expert %d geometry does not match n_embd/n_ff", e);
         }
-        if (b->n_moe_ok < krk_backend::kMoeCache) b->moe_ok[b->n_moe_ok++] = {key, e0, aligned};
+        // remember it; a full record drops its oldest entry (that layer is
+        // read and checked again on its next dispatch)
+        if (b->n_moe_ok < krk_backend::kMoeCache) {
+            b->moe_ok[b->n_moe_ok++] = {key, e0, aligned};
+        } else {
+            for (int i = 1; i < krk_backend::kMoeCache; i++) b->moe_ok[i - 1] = b->moe_ok[i];
+            b->moe_ok[krk_backend::kMoeCache - 1] = {key, e0, aligned};
+        }
     }
     krk::MoeArgs a{};
     a.table = table; a.layer = layer; a.n_expert = n_expert; a.k = k;

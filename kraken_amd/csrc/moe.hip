@@ -3,9 +3,9 @@
 // reference's moe_table_* kernels, src/hip/kernels/moe_table.hpp:38-551).
 //
 // Q4_K banks with f32 activations take two launches of the digit-plane GEMV
-// for any token count (below).  Otherwise one token takes two VALU launches,
-// and more tokens take four, none of them per expert and none waiting on
-// the host:
+// for up to 64 tokens, and expert-major items above that.  Other f32 cases:
+// one token takes two VALU launches; more tokens take the plan path, none
+// of its launches per expert and none waiting on the host:
 //   1. plan      one workgroup: expert-major plan of the (token, slot) pairs,
 //                the active-expert list in ascending id, and each pair's
 //                plan position;
@@ -18,8 +18,15 @@
 //                fma(w, part, acc) -- the order and the fused add of the host
 //                loop (engine.cpp:12360-12700, scatter_axpy_rows
 //                backend_cpu.cpp:3193-3217).
+// f16 activations (the reference GPU backend's act_type) take the plan path
+// at every token count with the reference GPU's rounding points
+// (moe_table.hpp:250-305, 418-441, 536-551): gate/up dots rounded to f16
+// before silu, a row-scale pass (power of two keeping the row within f16,
+// midf = f16(mid / scale)), down on midf, and a reduce that adds
+// w * (f16(v) * scale) per slot in slot order with an f16 rounding after
+// every add.
 // The weight types and strides are read from the table on the device; every
-// expert of a layer must share one type.
+// expert of a layer must share one type per role.
 #include "gemv_core.hpp"
 #include "krk_mi355x.h"
 
@@ -45,6 +52,8 @@ struct MoeWs {
     float *part;        // [P, n_embd]
     int32_t *items;     // [P][4]         {expert, first plan position, rows <= kItemRows, 0}
     int32_t *n_items;   // [1]
+    _Float16 *midf;     // [P, n_ff]      f16 activations: the row-scaled mid rows
+    float *rscale;      // [P]            f16 activations: each mid row's power-of-two scale
 };
 
 static size_t al(size_t v) { return (v + 255) & ~size_t(255); }
@@ -60,14 +69,16 @@ static MoeWs carve(void *ws, int64_t P, int ne, int64_t n_embd, int64_t n_ff) {
     w.mid = reinterpret_cast<float *>(p); p += al(P * n_ff * 4);
     w.part = reinterpret_cast<float *>(p); p += al(P * n_embd * 4);
     w.items = reinterpret_cast<int32_t *>(p); p += al(P * 16);
-    w.n_items = reinterpret_cast<int32_t *>(p);
+    w.n_items = reinterpret_cast<int32_t *>(p); p += al(4);
+    w.midf = reinterpret_cast<_Float16 *>(p); p += al(P * n_ff * 2);
+    w.rscale = reinterpret_cast<float *>(p);
     return w;
 }
 
 size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t n_ff) {
     const int64_t P = n_tok * k;
     return al((n_expert + 1) * 4) + al(n_expert * 4) + al(4) + 2 * al(P * 4) +
-           al(P * n_ff * 4) + al(P * n_embd * 4) + al(P * 16) + al(4);
+           al(P * n_ff * 4) + al(P * n_embd * 4) + al(P * 16) + al(4) + al(P * n_ff * 2) + al(P * 4);
 }
 
 // ------------------------------------------------------------------ plan ----
@@ -151,6 +162,21 @@ __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict
     }
 }
 
+// The expert's activation row.  f32 activations (the CPU oracle's
+// act_type): silu_mul, backend_cpu.cpp:2401-2406.  f16 activations (the
+// reference GPU backend's): both dots rounded to f16 first and silu with the
+// device exponential (moe_table.hpp:250-253, krk_hip.hpp:130).
+template <typename XT>
+__device__ __forceinline__ float gate_act(float g, float u) {
+    if constexpr (sizeof(XT) == 2) {
+        const float gf = static_cast<float>(static_cast<_Float16>(g));
+        const float uf = static_cast<float>(static_cast<_Float16>(u));
+        return silu_f(gf) * uf;
+    } else {
+        return (g / (1.0f + expf(-g))) * u;
+    }
+}
+
 // -------------------------------------------------------------- gate/up ----
 template <typename XT, int MR, int RB>
 __global__ void __launch_bounds__(512) moe_gu_kernel(const krk_moe_entry *__restrict__ tab,
@@ -199,7 +225,7 @@ __global__ void __launch_bounds__(512) moe_gu_kernel(const krk_moe_entry *__rest
             }
             const int64_t n = n0 + r;
             if (pass + m < np && n < n_ff)
-                w.mid[static_cast<int64_t>(p0 + pass + m) * n_ff + n] = (gs / (1.0f + expf(-gs))) * us;
+                w.mid[static_cast<int64_t>(p0 + pass + m) * n_ff + n] = gate_act<XT>(gs, us);
         }
         __syncthreads();
     }
@@ -207,10 +233,11 @@ __global__ void __launch_bounds__(512) moe_gu_kernel(const krk_moe_entry *__rest
 }
 
 // ----------------------------------------------------------------- down ----
-template <int MR, int RB>
+template <typename MT, int MR, int RB>
 __global__ void __launch_bounds__(512) moe_down_kernel(const krk_moe_entry *__restrict__ tab,
                                                         int64_t n_embd, int64_t n_ff,
                                                         int64_t groups, MoeWs w) {
+    // MT: the activation rows' type -- float mid, or the f16 row-scaled midf
     __shared__ float red[8][MR * RB];
     const int64_t items = static_cast<int64_t>(w.n_act[0]) * groups;
     for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
@@ -222,13 +249,14 @@ __global__ void __launch_bounds__(512) moe_down_kernel(const krk_moe_entry *__re
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint8_t *wd = static_cast<const uint8_t *>(en.p[KRK_MOE_DOWN]);
     for (int pass = 0; pass < np; pass += MR) {
-        const float *xr[MR];
+        const MT *rows = sizeof(MT) == 2 ? reinterpret_cast<const MT *>(w.midf) : reinterpret_cast<const MT *>(w.mid);
+        const MT *xr[MR];
 #pragma unroll
         for (int m = 0; m < MR; m++)
-            xr[m] = pass + m < np ? w.mid + static_cast<int64_t>(p0 + pass + m) * n_ff : nullptr;
+            xr[m] = pass + m < np ? rows + static_cast<int64_t>(p0 + pass + m) * n_ff : nullptr;
         float acc[MR][RB];
         switch (en.type[KRK_MOE_DOWN]) {
-            KRK_MOE_TYPES(KRK_MOE_ROWS, (float, MR, RB), (wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, acc))
+            KRK_MOE_TYPES(KRK_MOE_ROWS, (MT, MR, RB), (wd, en.row_bytes[2], n_embd, (int)n_ff, xr, n0, nullptr, acc))
             default: break;
         }
         float v[MR * RB];
@@ -251,6 +279,53 @@ __global__ void __launch_bounds__(512) moe_down_kernel(const krk_moe_entry *__re
         __syncthreads();
     }
     }
+}
+
+// ---------------------------------------------------- f16 row scale ----
+// f16 activations: each live mid row's power-of-two scale and the f16 row
+// the down dot reads (moe_table_scale_kernel, moe_table.hpp:256-305): the
+// smallest scale >= 1 (at most 2^24) with max |mid| <= 65504 * scale, and
+// midf = f16(mid * (1 / scale)), the reciprocal exact.  One workgroup per
+// plan position; positions past the live pairs leave at once.
+__global__ void __launch_bounds__(256) moe_scale_kernel(int64_t n_ff, int ne, MoeWs w) {
+    __shared__ float red[4];
+    const int64_t p = blockIdx.x;
+    if (p >= w.off[ne]) return;
+    const float *row = w.mid + p * n_ff;
+    float mx = 0.0f;
+    for (int64_t j = threadIdx.x; j < n_ff; j += blockDim.x) mx = fmaxf(mx, fabsf(row[j]));
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float mul = 1.0f;
+    while (m > 65504.0f * mul && mul < 16777216.0f) mul *= 2.0f;
+    if (threadIdx.x == 0) w.rscale[p] = mul;
+    const float inv = 1.0f / mul;
+    for (int64_t j = threadIdx.x; j < n_ff; j += blockDim.x)
+        w.midf[p * n_ff + j] = static_cast<_Float16>(__fmul_rn(row[j], inv));
+}
+
+// f16 activations: the reference GPU's slot-order accumulation
+// (moe_table_reduce_kernel, moe_table.hpp:536-551, with the partial of
+// table_down_batch, 418-441): per slot s in order, part = w * (f16(v) *
+// scale), two round-to-nearest products, and a = f16(a + part); a dropped
+// slot adds nothing (a is already an f16 value).
+__global__ void __launch_bounds__(256) moe_reduce_f16_kernel(const float *__restrict__ wts, int k,
+                                                             int64_t n_embd, MoeWs w,
+                                                             _Float16 *__restrict__ out) {
+    const int64_t t = blockIdx.y;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (j >= n_embd) return;
+    float a = 0.0f;
+    for (int s = 0; s < k; s++) {
+        const int pos = w.plan_pos[t * k + s];
+        if (pos < 0) continue;
+        const float vf = static_cast<float>(static_cast<_Float16>(w.part[static_cast<int64_t>(pos) * n_embd + j]));
+        const float part = __fmul_rn(wts[t * k + s], __fmul_rn(vf, w.rscale[pos]));
+        a = static_cast<float>(static_cast<_Float16>(__fadd_rn(a, part)));
+    }
+    out[t * n_embd + j] = static_cast<_Float16>(a);
 }
 
 // --------------------------------------------------------------- reduce ----
@@ -335,7 +410,7 @@ __global__ void __launch_bounds__(512) moe_gu1_kernel(const krk_moe_entry *__res
                 us += red[kk][H + r];
             }
             const int64_t n = n0 + r;
-            if (n < n_ff) mid[static_cast<int64_t>(s) * n_ff + n] = (gs / (1.0f + expf(-gs))) * us;
+            if (n < n_ff) mid[static_cast<int64_t>(s) * n_ff + n] = gate_act<XT>(gs, us);
         }
         __syncthreads();
     }
@@ -521,45 +596,40 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
         if (e != hipSuccess) return e;
         if (dn_ok) return gemv_digits(DT_Q4_K, false, d, st);
     }
-    if (a.n_tok == 1) {
+    if (a.n_tok == 1 && !a.act_f16) {
         const int64_t ggu = (a.n_ff + 3) / 4, gdn = (a.n_embd + 7) / 8;
-        if (!gu_ok) {
-            if (a.act_f16)
-                hipLaunchKernelGGL((moe_gu1_kernel<_Float16, 8>), cap(a.k * ggu, wgu), dim3(64 * wgu), 0, st,
-                                   tab, a.ids, a.k, a.n_expert, static_cast<const _Float16 *>(a.xn), a.n_embd,
-                                   a.n_ff, ggu, w.mid);
-            else
-                hipLaunchKernelGGL((moe_gu1_kernel<float, 8>), cap(a.k * ggu, wgu), dim3(64 * wgu), 0, st, tab,
-                                   a.ids, a.k, a.n_expert, static_cast<const float *>(a.xn), a.n_embd, a.n_ff,
-                                   ggu, w.mid);
-        }
-        if (a.act_f16)
-            hipLaunchKernelGGL((moe_down1_kernel<_Float16, 8>), cap(gdn, 8), dim3(64 * 8), 0, st, tab, a.ids,
-                               a.wts, a.k, a.n_expert, a.n_embd, a.n_ff, gdn, w.mid,
-                               static_cast<_Float16 *>(a.out));
-        else
-            hipLaunchKernelGGL((moe_down1_kernel<float, 8>), cap(gdn, 8), dim3(64 * 8), 0, st, tab, a.ids,
-                               a.wts, a.k, a.n_expert, a.n_embd, a.n_ff, gdn, w.mid, static_cast<float *>(a.out));
+        if (!gu_ok)
+            hipLaunchKernelGGL((moe_gu1_kernel<float, 8>), cap(a.k * ggu, wgu), dim3(64 * wgu), 0, st, tab,
+                               a.ids, a.k, a.n_expert, static_cast<const float *>(a.xn), a.n_embd, a.n_ff,
+                               ggu, w.mid);
+        hipLaunchKernelGGL((moe_down1_kernel<float, 8>), cap(gdn, 8), dim3(64 * 8), 0, st, tab, a.ids,
+                           a.wts, a.k, a.n_expert, a.n_embd, a.n_ff, gdn, w.mid, static_cast<float *>(a.out));
         return hipGetLastError();
     }
+    // the plan path: every f16 dispatch (the reference GPU's rounding points
+    // need each (token, slot) row whole before its scale), and f32 token
+    // batches the digit kernels do not take
     hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w);
     const int64_t amax = P < a.n_expert ? P : a.n_expert;
     const int64_t ggu = (a.n_ff + 1) / 2, gdn = (a.n_embd + 3) / 4;
-    if (a.act_f16)
+    const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));
+    if (a.act_f16) {
         hipLaunchKernelGGL((moe_gu_kernel<_Float16, 2, 4>), cap(amax * ggu, wgu), dim3(64 * wgu), 0, st,
                            tab, static_cast<const _Float16 *>(a.xn), a.n_embd, a.n_ff, ggu, w);
-    else
-        hipLaunchKernelGGL((moe_gu_kernel<float, 2, 4>), cap(amax * ggu, wgu), dim3(64 * wgu), 0, st,
-                           tab, static_cast<const float *>(a.xn), a.n_embd, a.n_ff, ggu, w);
-    hipLaunchKernelGGL((moe_down_kernel<2, 4>), cap(amax * gdn, wdn), dim3(64 * wdn), 0, st, tab,
+        hipLaunchKernelGGL(moe_scale_kernel, dim3(static_cast<unsigned>(P)), dim3(256), 0, st, a.n_ff,
+                           a.n_expert, w);
+        hipLaunchKernelGGL((moe_down_kernel<_Float16, 2, 4>), cap(amax * gdn, wdn), dim3(64 * wdn), 0, st, tab,
+                           a.n_embd, a.n_ff, gdn, w);
+        hipLaunchKernelGGL(moe_reduce_f16_kernel, rgrid, dim3(256), 0, st, a.wts, a.k, a.n_embd, w,
+                           static_cast<_Float16 *>(a.out));
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((moe_gu_kernel<float, 2, 4>), cap(amax * ggu, wgu), dim3(64 * wgu), 0, st,
+                       tab, static_cast<const float *>(a.xn), a.n_embd, a.n_ff, ggu, w);
+    hipLaunchKernelGGL((moe_down_kernel<float, 2, 4>), cap(amax * gdn, wdn), dim3(64 * wdn), 0, st, tab,
                        a.n_embd, a.n_ff, gdn, w);
-    const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));
-    if (a.act_f16)
-        hipLaunchKernelGGL((moe_reduce_kernel<_Float16>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
-                           a.n_embd, w, static_cast<_Float16 *>(a.out));
-    else
-        hipLaunchKernelGGL((moe_reduce_kernel<float>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
-                           a.n_embd, w, static_cast<float *>(a.out));
+    hipLaunchKernelGGL((moe_reduce_kernel<float>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
+                       a.n_embd, w, static_cast<float *>(a.out));
     return hipGetLastError();
 }
 

@@ -59,6 +59,8 @@ def _load():
         "orc_router_topk": (None, [_vp, _i64, _i32, _i32, _vp, _vp, _i32, _f32]),
         "orc_moe_ffn": (None, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp,
                                _vp, _i64, _i64, _i64, _i32, _i32, _i32]),
+        "orc_moe_ffn_f16": (None, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp,
+                                   _vp, _i64, _i64, _i64, _i32, _i32, _i32]),
         "orc_quantize_q8_0_weights": (None, [_vp, _i64, _vp]),
     }
     for name, (res, args) in sig.items():
@@ -232,6 +234,27 @@ def moe_ffn(x, gate, up, down, wt, ids, wts, n_ff, nthreads: int = 8):
                       C.cast(d, _vp), wg, wu, wd, _p(ids), _p(wts), n_tok,
                       n_embd, n_ff, ne, k, nthreads)
     return out
+
+
+def moe_ffn_f16(x, gate, up, down, wt, ids, wts, n_ff, nthreads: int = 8):
+    """The reference GPU backend's f16 expert FFN (orc_moe_ffn_f16); x holds
+    f16 values; returns float16 [n_tok, n_embd]."""
+    wg, wu, wd = (wt, wt, wt) if isinstance(wt, int) else wt
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    n_tok, n_embd = x.shape
+    ne = len(gate)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    wts = np.ascontiguousarray(wts, dtype=np.float32)
+    k = ids.shape[-1]
+    keep = [np.ascontiguousarray(a) for a in (*gate, *up, *down)]
+    arr = (_vp * ne)
+    g = arr(*[a.ctypes.data for a in keep[:ne]])
+    u = arr(*[a.ctypes.data for a in keep[ne:2 * ne]])
+    d = arr(*[a.ctypes.data for a in keep[2 * ne:]])
+    out = np.empty((n_tok, n_embd), np.uint16)
+    lib().orc_moe_ffn_f16(_p(out), _p(x), C.cast(g, _vp), C.cast(u, _vp), C.cast(d, _vp), wg, wu,
+                          wd, _p(ids), _p(wts), n_tok, n_embd, n_ff, ne, k, nthreads)
+    return out.view(np.float16)
 
 
 def quantize_q8_0_weights(v: np.ndarray) -> np.ndarray:

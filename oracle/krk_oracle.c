@@ -756,6 +756,62 @@ void orc_moe_ffn(float *out, const float *x, const void *const *gate,
     free(rows); free(alpha); free(xg); free(g); free(u); free(mid); free(dn);
 }
 
+/* The reference GPU backend's f16 expert FFN (act_type F16), restated from
+ * src/hip/kernels/moe_table.hpp: gate/up tiles (230-254), the row scale
+ * (256-305), the down partial (418-441) and the slot-order reduce (536-551);
+ * dispatched by backend_hip.hip:2525-2659.  Per token t and slot s in slot
+ * order, expert e = ids[t k + s] (a dropped slot adds nothing):
+ *   mid_j  = silu(f16(gate_e . x_t)_j) * f16(up_e . x_t)_j        (f32)
+ *   scale  = the smallest power of two >= 1 (at most 2^24) with
+ *            max_j |mid_j| <= 65504 * scale
+ *   midf_j = f16(mid_j * (1 / scale))
+ *   part_i = wts[t, s] * (f16(down_e . midf)_i * scale)          (two RN products)
+ *   a_i    = f16(a_i + part_i)                                    (a starts at 0)
+ * out is f16.  x holds f16 values (as f32); the row dots are the strict f32
+ * chain of vec_dot, silu is x / (1 + exp(-x)) in f32.  Output: f16 bits. */
+static float f16r(float v) { return orc_fp16_to_fp32(orc_fp32_to_fp16(v)); }
+
+void orc_moe_ffn_f16(uint16_t *out, const float *x, const void *const *gate,
+                     const void *const *up, const void *const *down, int wt_gate,
+                     int wt_up, int wt_down, const int32_t *ids, const float *wts,
+                     int64_t n_tok, int64_t n_embd, int64_t n_ff, int n_expert,
+                     int k, int nthreads) {
+    float *g = (float *)malloc((size_t)n_ff * sizeof(float));
+    float *u = (float *)malloc((size_t)n_ff * sizeof(float));
+    float *mid = (float *)malloc((size_t)n_ff * sizeof(float));
+    float *v = (float *)malloc((size_t)n_embd * sizeof(float));
+    float *a = (float *)malloc((size_t)n_embd * sizeof(float));
+    for (int64_t t = 0; t < n_tok; t++) {
+        const float *xt = x + t * n_embd;
+        for (int64_t j = 0; j < n_embd; j++) a[j] = 0.0f;
+        for (int s = 0; s < k; s++) {
+            const int e = ids[t * k + s];
+            if (e < 0 || e >= n_expert) continue;
+            orc_gemm(g, xt, gate[e], wt_gate, n_ff, n_embd, 1, nthreads);
+            orc_gemm(u, xt, up[e], wt_up, n_ff, n_embd, 1, nthreads);
+            float mx = 0.0f;
+            for (int64_t j = 0; j < n_ff; j++) {
+                const float gf = f16r(g[j]), uf = f16r(u[j]);
+                mid[j] = (gf / (1.0f + expf(-gf))) * uf;
+                const float m = fabsf(mid[j]);
+                if (m > mx) mx = m;
+            }
+            float mul = 1.0f;
+            while (mx > 65504.0f * mul && mul < 16777216.0f) mul *= 2.0f;
+            const float inv = 1.0f / mul;
+            for (int64_t j = 0; j < n_ff; j++) mid[j] = f16r(mid[j] * inv);
+            orc_gemm(v, mid, down[e], wt_down, n_embd, n_ff, 1, nthreads);
+            const float w = wts[t * k + s];
+            for (int64_t j = 0; j < n_embd; j++) {
+                const float vs = f16r(v[j]) * mul;
+                a[j] = f16r(a[j] + w * vs);
+            }
+        }
+        for (int64_t j = 0; j < n_embd; j++) out[t * n_embd + j] = orc_fp32_to_fp16(a[j]);
+    }
+    free(g); free(u); free(mid); free(v); free(a);
+}
+
 /* ---- tools/make_bench_gguf.py:191-202 (quantize_q8_0), the repo's own q8_0
  * fixture generator.  Python floats are f64: amax = max|v| (1e-8 for an all-
  * zero block), d = amax / 127.0, q = clamp(round_half_even(v / d), +-127),

@@ -67,6 +67,17 @@ void     orc_moe_ffn(float *out, const float *x, const void *const *gate,
                      int64_t n_embd, int64_t n_ff, int n_expert, int k,
                      int nthreads);
 
+/* The reference GPU backend's f16 expert FFN (moe_table.hpp:230-305,
+ * 418-441, 536-551): row-scaled f16 activations into down, f16 partials
+ * added in slot order with an f16 rounding after every add.  x holds f16
+ * values; out receives f16 bits. */
+void     orc_moe_ffn_f16(uint16_t *out, const float *x, const void *const *gate,
+                         const void *const *up, const void *const *down,
+                         int wt_gate, int wt_up, int wt_down,
+                         const int32_t *ids, const float *wts, int64_t n_tok,
+                         int64_t n_embd, int64_t n_ff, int n_expert, int k,
+                         int nthreads);
+
 /* Fixture generator restated from tools/make_bench_gguf.py:191-202 (q8_0). */
 void     orc_quantize_q8_0_weights(const float *v, int64_t n, uint8_t *dst);
 

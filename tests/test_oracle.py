@@ -257,6 +257,71 @@ def test_moe_matches_dense_twin(krk):
         assert np.linalg.norm(out[t] - acc) <= 1e-5 * np.linalg.norm(acc)
 
 
+def _f16_expert(gate_row, up_col, down_col, n=4):
+    """F16 expert banks of n x n: every gate row is gate_row; up row j is
+    [up_col[j], 0, ..]; down row i is [down_col[i], 0, ..] (exact f16 values)."""
+    g = np.tile(np.array(gate_row, np.float16), (n, 1))
+    u = np.zeros((n, n), np.float16)
+    u[:, 0] = up_col
+    d = np.zeros((n, n), np.float16)
+    d[:, 0] = down_col
+    return [m.reshape(-1).view(np.uint8).copy() for m in (g, u, d)]
+
+
+def test_moe_ffn_f16_slot_order_and_row_scale():
+    """The reference GPU's f16 expert FFN (moe_table.hpp:256-305, 418-441,
+    536-551) on F16 banks whose dots are exact, so every value below is fixed
+    by hand: gate rows [32, 0, 0, 0] against x = e0 give g = 32 and silu(32)
+    = 32 in f32; up 2^-5 gives mid = 1; a down entry dd gives v = dd.
+      * slot order with an f16 rounding after every add: parts 1, 2^-11,
+        2^-11 sum to 1 in that order (1 + 2^-11 ties to even) but to
+        1 + 2^-10 in the order 2^-11, 2^-11, 1 -- where the f32 oracle gets
+        1 + 2^-10 in either order;
+      * the row scale: up 2^11 gives mid = 65536 > 65504, so scale 2, midf =
+        32768, and down 2^-15 gives v = 1, part f16(1) * 2 = 2 (no scale: an
+        f16 overflow to inf);
+      * a dropped slot (id -1) adds nothing."""
+    F16 = O.F16
+    x = np.array([[1, 0, 0, 0]], np.float32)
+    big, small = _f16_expert([32, 0, 0, 0], [2.0 ** -5] * 4, [1.0, 0, 0, 0]), \
+        _f16_expert([32, 0, 0, 0], [2.0 ** -5] * 4, [2.0 ** -11, 0, 0, 0])
+    scaled = _f16_expert([32, 0, 0, 0], [2.0 ** 11] * 4, [2.0 ** -15, 0, 0, 0])
+    banks = [big, small, small, scaled]
+    g, u, d = ([b[m] for b in banks] for m in range(3))
+    w1 = np.ones((1, 3), np.float32)
+
+    def run(ids):
+        return O.moe_ffn_f16(x, g, u, d, F16, np.array([ids], np.int32), w1, 4)[0, 0]
+
+    assert run([0, 1, 2]) == np.float16(1.0)
+    assert run([1, 2, 0]) == np.float16(1.0 + 2.0 ** -10)
+    assert run([-1, 1, 0]) == np.float16(1.0)           # 2^-11 then 1: ties to even
+    for ids in ([0, 1, 2], [1, 2, 0]):
+        f32 = O.moe_ffn(x, g, u, d, F16, np.array([ids], np.int32), w1, 4)[0, 0]
+        assert f32 == np.float32(1.0 + 2.0 ** -10)
+    assert run([3, -1, -1]) == np.float16(2.0)
+    assert np.isfinite(run([3, 3, -1]))
+
+
+def test_moe_ffn_f16_tracks_the_f32_oracle(krk):
+    """On quantized banks the f16 form stays within its rounding of the f32
+    oracle (a dropped term or a wrong scale would not)."""
+    rng = np.random.default_rng(23)
+    ne, E, F, T, k = 4, 256, 512, 3, 2
+    mats = {}
+    for e in range(ne):
+        for nm, (o, i) in (("g", (F, E)), ("u", (F, E)), ("d", (E, F))):
+            mats[nm, e] = krk.quantize(O.Q4_K, (rng.standard_normal(o * i) * 0.02).astype(np.float32), o, i)
+    x = rng.standard_normal((T, E)).astype(np.float16).astype(np.float32)
+    g, u, d = ([mats[nm, e] for e in range(ne)] for nm in "gud")
+    ids = np.array([[2, 0], [1, 3], [3, 2]], np.int32)
+    wts = np.array([[0.7, 0.3], [0.5, 0.5], [0.9, 0.1]], np.float32)
+    h = O.moe_ffn_f16(x, g, u, d, O.Q4_K, ids, wts, F).astype(np.float32)
+    f = O.moe_ffn(x, g, u, d, O.Q4_K, ids, wts, F)
+    e = np.linalg.norm(h - f) / np.linalg.norm(f)
+    assert 1e-5 < e < 3e-3
+
+
 def test_q8_0_fixture_quantizer_matches_python_rule():
     """tools/make_bench_gguf.py:191-202 restated with Python's own float
     semantics (f64, round-half-even, struct '<e')."""
