@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                     help="turn a rocprofv3 --kernel-trace csv into per-(kernel, grid, block) "
                          "duration rows (markdown, printed)")
+    ap.add_argument("--summarize-counters", metavar="COUNTER_CSV",
+                    help="turn a rocprofv3 --pmc counter_collection.csv into per-(kernel, grid) "
+                         "medians and derived rates (markdown, printed)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc counter_collection.csv files of a "
                          "--pmc-pass run into the traffic summary (printed)")
@@ -134,7 +137,18 @@ def bench_gemv(K, torch, be, timer, args, dt, n_out, n_in, seed, act_f16=False, 
     nbytes = K.row_bytes(dt, n_in) * n_out
     act_bytes = (n_in + n_out) * (2 if act_f16 else 4)
     return {"ms": ms, "weight_bytes": nbytes, "bytes": nbytes + act_bytes,
-            "GBps": (nbytes + act_bytes) / ms / 1e6, "copies": len(ws), "w": w, "x": x}
+            "GBps": (nbytes + act_bytes) / ms / 1e6, "copies": len(ws), "w": w, "x": x, "ws": ws}
+
+
+def bench_read_ceiling(torch, be, timer, ws, nbytes, blocks=2048):
+    """The same rotation of weight copies read by a plain streaming kernel
+    (krk_probe_read): what one launch of a pure HBM read of these bytes
+    takes on this part, the floor under the decode GEMV."""
+    sink = torch.empty(1024, dtype=torch.int32, device="cuda")
+    n16 = nbytes // 16 * 16
+    ms = timer.run(lambda i: be.probe_read(ws[i % len(ws)], n16, blocks, sink), 400, 4)
+    return {"us": ms * 1e3, "GBps": n16 / ms / 1e6, "frac_hbm": n16 / ms / 1e6 / HBM_PEAK_GBS,
+            "bytes": n16, "blocks": blocks}
 
 
 def bench_gemm(K, torch, be, timer, dt, M, n_out, n_in, seed, iters=20, warmup=3):
@@ -344,6 +358,36 @@ def summarize_trace(path):
               f"{statistics.median(d):.2f} | {min(d):.2f} | {max(d):.2f} |")
 
 
+def summarize_counters(path, cus=256, xcds=8):
+    """Median per dispatch of every counter, per (kernel, grid), plus:
+    clock = GRBM_GUI_ACTIVE / xcds / duration; MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES
+    over (4 SIMDs x cus) x the per-XCD active cycles; wait = SQ_WAIT_ANY /
+    SQ_WAVE_CYCLES."""
+    import csv
+    import statistics
+    groups = {}
+    for r in csv.DictReader(open(path)):
+        key = (r["Kernel_Name"], r["Grid_Size"])
+        g = groups.setdefault(key, {"dur": {}, "c": {}})
+        g["c"].setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+        g["dur"][r["Dispatch_Id"]] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    for (name, grid), g in groups.items():
+        med = {c: statistics.median(v) for c, v in g["c"].items()}
+        dur = statistics.median(g["dur"].values())
+        print(f"### `{name}` grid {grid}")
+        print(f"dispatches: {len(g['dur'])}, median duration under counters: {dur:.1f} us")
+        for c in sorted(med):
+            print(f"- {c}: {med[c]:.0f}")
+        if "GRBM_GUI_ACTIVE" in med:
+            cyc = med["GRBM_GUI_ACTIVE"] / xcds
+            print(f"- clock: {cyc / dur / 1e3:.2f} GHz")
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in med:
+                print(f"- MFMA busy: {100 * med['SQ_VALU_MFMA_BUSY_CYCLES'] / (4 * cus * cyc):.1f}% of SIMD cycles")
+        if "SQ_WAIT_ANY" in med and "SQ_WAVE_CYCLES" in med:
+            print(f"- waiting: {100 * med['SQ_WAIT_ANY'] / med['SQ_WAVE_CYCLES']:.1f}% of wave cycles")
+        print()
+
+
 def read_profile_field(fname, key):
     p = os.path.join(ROOT, "profiles", fname)
     if not os.path.exists(p):
@@ -371,6 +415,9 @@ def read_traffic():
 
 def main():
     args = parse()
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
+        return
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
         return
@@ -403,6 +450,10 @@ def main():
     n_out, n_in = 14336, 4096
     g = bench_gemv(K, torch, be32, timer, args, K.Q4_K, n_out, n_in, seed=1)
     log(f"  {g['ms'] * 1e3:.2f} us/call  {g['GBps']:.0f} GB/s  ({g['copies']} copies)")
+    # the floor: a pure read of the same bytes in one launch
+    rc = bench_read_ceiling(torch, be32, timer, g["ws"], g["weight_bytes"])
+    extras["read_ceiling_q4k_4096x14336"] = rc
+    log(f"  read ceiling: {rc['us']:.2f} us  {rc['GBps']:.0f} GB/s ({100 * rc['frac_hbm']:.1f}% of HBM)")
     # the same call with f16 activations (the reference GPU's activation type)
     g16 = bench_gemv(K, torch, be16, timer, args, K.Q4_K, n_out, n_in, seed=1, act_f16=True)
     extras["gemv_q4k_f16act"] = {"us": g16["ms"] * 1e3, "GBps": g16["GBps"]}

@@ -219,6 +219,14 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer,
  * reference, whose dispatch keeps no host-side record of the table. */
 int krk_moe_table_forget(krk_backend *b, const void *table);
 
+/* ---------------------------------------------------------- measurement -- */
+/* A pure read of `bytes` (a multiple of 16, 16-byte aligned device memory)
+ * by `blocks` workgroups of 256 threads: the HBM stream ceiling of one
+ * launch, which the decode GEMV (every weight byte read once) can
+ * approach but not pass.  `sink`: 4 KiB of device memory the probe may
+ * write.  Measurement only; no counterpart in the reference. */
+int krk_probe_read(krk_backend *b, const void *src, int64_t bytes, int blocks, void *sink);
+
 /* ------------------------------------------------ dequant / quantize ops -- */
 
 /* dequant_row (quant.hpp:203) on the device: out f32 [n_rows, n_in],

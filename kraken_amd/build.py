@@ -19,7 +19,7 @@ LIB = os.path.join(HERE, "libkrk_mi355x.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["backend.cpp", "synth.cpp", "gguf.cpp", "gemv.hip", "gemv_digits.hip", "gemv_stream.hip", "dequant.hip", "gemm.hip",
-           "gemm_i8.hip", "router.hip", "moe.hip"]
+           "gemm_i8.hip", "router.hip", "moe.hip", "probe.hip"]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(ROOT, "include"),
           "-I", CSRC]
