@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list of sections: gemm,int8,layer,head,moe "
+    ap.add_argument("--only", default="", help="comma list of sections: gemm,int8,layer,formats,head,moe "
                     "(the headline GEMV always runs); default all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--pmc-pass", action="store_true",
@@ -497,6 +497,13 @@ def main():
         r["frac_hbm"] = r["GBps"] / HBM_PEAK_GBS
         extras["layer_grouped"] = r
         log(f"  layer, 4 grouped launches: {r['us']:.1f} us {r['GBps']:.0f} GB/s")
+    if want("formats"):
+        # the other north-star formats at the headline's shape and M = 1
+        for dt, nm in ((K.Q6_K, "q6_k"), (K.Q4_0, "q4_0"), (K.Q8_0, "q8_0")):
+            r = bench_gemv(K, torch, be32, timer, args, dt, n_out, n_in, seed=3)
+            extras[f"gemv_{nm}_4096x14336"] = {"us": r["ms"] * 1e3, "GBps": r["GBps"],
+                                                "frac_hbm": r["GBps"] / HBM_PEAK_GBS}
+            log(f"  gemv {nm} 4096->14336: {r['ms'] * 1e3:.2f} us {r['GBps']:.0f} GB/s")
     if want("head"):
         for dt, nm in ((K.Q6_K, "q6_k"), (K.Q8_0, "q8_0")):
             r = bench_gemv(K, torch, be32, timer, args, dt, 128256, 4096, seed=30, tile=16)

@@ -1402,7 +1402,7 @@ static hipError_t dispatch_dt(int dt, const SegTable &t, hipStream_t st) {
 }
 
 hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st) {
-    if (gemv_stream_ok(dt, t)) return gemv_stream(act_f16, t, st);
+    if (gemv_stream_ok(dt, t)) return gemv_stream(dt, act_f16, t, st);
     if (gemv_digits_ok(dt, t)) return gemv_digits(dt, act_f16, t, st);
     if (act_f16) return dispatch_dt<_Float16, _Float16>(dt, t, st);
     return dispatch_dt<float, float>(dt, t, st);

@@ -1,11 +1,12 @@
-// gemv_stream.hip -- one-row decode GEMV for Q4_K weights with every byte of a
-// workgroup's tile requested in its first instructions.
+// gemv_stream.hip -- one-row decode GEMV for Q4_K and Q6_K weights with every
+// byte of a workgroup's tile requested in its first instructions.
 //
 // The products run on the int8 matrix cores exactly as in gemv_digits.hip:
 // the weight codes are the B operand, the activations enter as three exact
-// int8 digit planes per 32-value sub-block, and the Q4_K block formula
-// (src/quant.cpp:427-447) is applied once per (row, sub-block) to the exact
-// plane sums.  What differs is the data movement, which sets the time of a
+// int8 digit planes per 32-value sub-block, and the block formula (Q4_K:
+// src/quant.cpp:427-447; Q6_K: 491-512, the code offset 32 applied through
+// the exact integer sums of x) is applied once per (row, sub-block or scale
+// group) to the exact plane sums.  What differs is the data movement, which sets the time of a
 // decode GEMV far more than the arithmetic does:
 //
 //   * A workgroup owns one tile of up to 32 rows over all of K; its waves
@@ -42,6 +43,25 @@ constexpr int kMaxWaves = 16;
 
 __device__ __forceinline__ v4i lds_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
+// loads from the 2-byte aligned Q6_K blocks (210 bytes): the part runs its
+// global memory with unaligned access allowed, which hipcc's gfx950 target
+// assumes (it emits a single dwordx4 for these)
+__device__ __forceinline__ u32x4 ld128_a2(const uint8_t *p) {
+    u32x4 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 16);
+    return v;
+}
+__device__ __forceinline__ uint2 ld64_a2(const uint8_t *p) {
+    uint2 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 8);
+    return v;
+}
+__device__ __forceinline__ uint32_t ld32_a2(const uint8_t *p) {
+    uint32_t v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 4);
+    return v;
+}
+
 // quad-lane exchanges (lanes l ^ 1 and l ^ 2) through DPP
 __device__ __forceinline__ float quad_xor1(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
@@ -63,8 +83,10 @@ __device__ __forceinline__ void load_x8(const _Float16 *p, float (&v)[8]) {
     for (int k = 0; k < 8; k++) v[k] = static_cast<float>(h[k]);
 }
 
-template <typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWEXACT, int LA = 8>
-__global__ void __launch_bounds__(64 * NWMAX) gemv_stream_q4k(SegTable t) {
+template <int DT, typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWEXACT, int LA = 8>
+__global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
+    constexpr bool Q6 = DT == DT_Q6_K;
+    constexpr int BB = Q6 ? 210 : 144;     // bytes per 256-value block
     constexpr int RG = (TR + 15) / 16;     // 16-row groups of a plain tile
     constexpr int NL = RG * NBW;           // (16 rows, block) groups of a wave
     constexpr int NPASS = (NBW + 1) / 2;   // x passes: 16 sub-blocks of 8 x 4 lanes each
@@ -112,9 +134,17 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_q4k(SegTable t) {
         }
     }
     // ---- then every weight byte of the wave's slice of the tile: group i =
-    // (row group rg, block b): lane (c16, gq) takes row rg * 16 + c16's
-    // header and code bytes 16 gq .. + 15 of each 64-byte half
+    // (row group rg, block b), lane (c16, gq) takes of row rg * 16 + c16:
+    //   Q4_K: the 16-byte header and code bytes 16 gq .. + 15 of each
+    //         64-byte half (hd, qa, qb);
+    //   Q6_K: with h = gq / 2, l = gq % 2: ql bytes 64 h + 16 l and
+    //         64 h + 32 + 16 l (hd, qa), qh bytes 128 + 32 h + 16 l (qb), the
+    //         eight scales 192 + 8 h (sc) and d (the top half of the dword
+    //         at 206, inside the block)
     u32x4 hd[NL], qa[NL], qb[NL];
+    uint2 sc[Q6 ? NL : 1];
+    uint32_t dd[Q6 ? NL : 1];
+    const int h6 = gq >> 1, lh6 = gq & 1;
     const uint8_t *src[NL];
 #pragma unroll
     for (int i = 0; i < NL; i++) {
@@ -132,22 +162,32 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_q4k(SegTable t) {
         if (n >= n_out) n = n_out - 1;
         // a ragged last slice re-reads the matrix's last block (discarded)
         const int blk = kb0 + b < nb ? kb0 + b : nb - 1;
-        src[i] = base + n * rb + static_cast<int64_t>(blk) * 144;
+        src[i] = base + n * rb + static_cast<int64_t>(blk) * BB;
     }
     auto issue = [&](int i) {
-        hd[i] = ld128(src[i]);
-        qa[i] = ld128(src[i] + 16 + 16 * gq);
-        qb[i] = ld128(src[i] + 80 + 16 * gq);
+        if constexpr (Q6) {
+            hd[i] = ld128_a2(src[i] + 64 * h6 + 16 * lh6);
+            qa[i] = ld128_a2(src[i] + 64 * h6 + 32 + 16 * lh6);
+            qb[i] = ld128_a2(src[i] + 128 + 32 * h6 + 16 * lh6);
+            sc[i] = ld64_a2(src[i] + 192 + 8 * h6);
+            dd[i] = ld32_a2(src[i] + 206);
+        } else {
+            hd[i] = ld128(src[i]);
+            qa[i] = ld128(src[i] + 16 + 16 * gq);
+            qb[i] = ld128(src[i] + 80 + 16 * gq);
+        }
     };
 #pragma unroll
     for (int i = 0; i < (LA < NL ? LA : NL); i++) issue(i);
     __builtin_amdgcn_s_setprio(0);
 
     // ---- the digit table of the slice (this wave's own LDS), layout
-    // [block][sub-block][plane][32 bytes], and {2^-e, sum x} per sub-block
+    // [block][sub-block][plane][32 bytes], {2^-e, sum x} per sub-block, and
+    // for Q6_K the exact integer sums of X over each 16-value half (int bits)
     uint8_t *tab = lds + wv * (NBW * kTab);
     float2 *ex = reinterpret_cast<float2 *>(lds + nw * (NBW * kTab)) + wv * (NBW * 8);
-    float *red = reinterpret_cast<float *>(lds + nw * (NBW * kTab + NBW * 8 * sizeof(float2)));
+    float2 *ex16 = reinterpret_cast<float2 *>(lds + nw * (NBW * kTab)) + nw * (NBW * 8) + wv * (NBW * 8);
+    float *red = reinterpret_cast<float *>(lds + nw * (NBW * kTab + 2 * NBW * 8 * sizeof(float2)));
 #pragma unroll
     for (int p = 0; p < NPASS; p++) {
         const int sbw = p * 16 + (lane >> 2);
@@ -173,9 +213,11 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_q4k(SegTable t) {
         const float up = __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
         const float dn = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
         uint32_t p0[2] = {0u, 0u}, p1[2] = {0u, 0u}, p2[2] = {0u, 0u};
+        int xsum = 0;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const int X = live ? static_cast<int>(__builtin_rintf(v[k] * up)) : 0;
+            xsum += X;
             const int d0 = ((X + 128) & 255) - 128;
             const int X1 = (X - d0) >> 8;
             const int d1 = ((X1 + 128) & 255) - 128;
@@ -192,6 +234,13 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_q4k(SegTable t) {
             *reinterpret_cast<u32x2 *>(o + 64) = u32x2{p2[0], p2[1]};
             if ((lane & 3) == 0) ex[sbw] = float2{live ? dn : 1.0f, sum};
         }
+        if constexpr (Q6) {
+            // lanes 4j, 4j + 1 hold values 0..15 of sub-block j, 4j + 2, 4j + 3
+            // values 16..31
+            xsum += __float_as_int(quad_xor1(__int_as_float(xsum)));
+            const int xsum_hi = __float_as_int(quad_xor2(__int_as_float(xsum)));
+            if (sbw < 8 * NBW && (lane & 3) == 0) ex16[sbw] = float2{__int_as_float(xsum), __int_as_float(xsum_hi)};
+        }
     }
 
     // ---- per-lane MFMA roles (A row c16 = 4 sub-block' + digit plane)
@@ -202,12 +251,15 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_q4k(SegTable t) {
     const uint32_t M = 0x0F0F0F0Fu;
     const uint32_t bsh = 8u * static_cast<uint32_t>(gq);
     const v4i Z = {0, 0, 0, 0};
+    // Q6_K: lane group gq's A rows hold sub-block 4 h + qd's half l
+    const bool a6 = ap < 3 && as == gq;
+    const int a6_off = 4 * h6 * 96 + (ap < 3 ? ap : 0) * 32 + 16 * lh6;
     float acc[RG];
 #pragma unroll
     for (int rg = 0; rg < RG; rg++) acc[rg] = 0.0f;
     // two-block slices read their A operands once, before the first group
     // lands (wider slices read them per group: registers)
-    constexpr bool HOLD = NBW == 2;
+    constexpr bool HOLD = NBW == 2 && !Q6;
     v4i HA[HOLD ? NBW : 1][4];
     float2 HE[HOLD ? NBW : 1][2];
     if constexpr (HOLD) {
@@ -231,6 +283,41 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_q4k(SegTable t) {
         __builtin_amdgcn_sched_barrier(0);
         const int rg = i / NBW, b = i - (i / NBW) * NBW;
         if (kb0 + b >= nb) continue;   // wave-uniform: the ragged slice's missing blocks
+        if constexpr (Q6) {
+            // chunk qd of the block: in lane group gq = 2 h + l, the 16 values
+            // 128 h + 32 qd + 16 l + i -- one scale group; code q = 4 low bits
+            // from ql | 2 high bits from qh (dequant_q6_K, quant.cpp:491-512),
+            // 0..63 as int8; the offset 32 through the 16-value sums of X:
+            // S = sum (q - 32) X, |S| <= 16 * 32 * 2^22, exact in wrapping int32
+            const u32x4 l0 = hd[i], l1 = qa[i], qh = qb[i];
+            const float d = h2f(dd[i] >> 16);
+            float a = acc[rg];
+#pragma unroll
+            for (int qd = 0; qd < 4; qd++) {
+                const u32x4 ql = (qd & 1) ? l1 : l0;
+                const uint32_t ns = (qd >> 1) * 4u, hs = 2u * qd;
+                const v4i B = {static_cast<int>(((ql.x >> ns) & M) | (((qh.x >> hs) & 0x03030303u) << 4)),
+                               static_cast<int>(((ql.y >> ns) & M) | (((qh.y >> hs) & 0x03030303u) << 4)),
+                               static_cast<int>(((ql.z >> ns) & M) | (((qh.z >> hs) & 0x03030303u) << 4)),
+                               static_cast<int>(((ql.w >> ns) & M) | (((qh.w >> hs) & 0x03030303u) << 4))};
+                // scale of group 8 h + 2 qd + l: byte 2 qd + l of the lane's eight
+                const int jj = 2 * qd + lh6;
+                const uint32_t sw = jj < 4 ? sc[i].x : sc[i].y;
+                const float ds = d * static_cast<float>(static_cast<int8_t>(sw >> (8 * (jj & 3))));
+                // A rows 4 gq + p: digit plane p of sub-block 4 h + qd, half l
+                const v4i A = a6 ? lds_v4i(tab + b * kTab + a6_off + qd * 96) : Z;
+                const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, Z, 0, 0, 0);
+                const int sbi = b * 8 + 4 * h6 + qd;
+                const float2 h2 = ex16[sbi];
+                const uint32_t xs = static_cast<uint32_t>(__float_as_int(lh6 ? h2.y : h2.x));
+                const int S = static_cast<int>(static_cast<uint32_t>(C[0]) + (static_cast<uint32_t>(C[1]) << 8) +
+                                               (static_cast<uint32_t>(C[2]) << 16) - 32u * xs);
+                a = __builtin_fmaf(ds, ex[sbi].x * static_cast<float>(S), a);
+            }
+            acc[rg] = a;
+            __builtin_amdgcn_sched_barrier(0);
+            continue;
+        }
         const uint8_t *tb = tab + b * kTab + a_off;
         const int hb = HOLD ? b : 0;
         const v4i A0l = HOLD ? HA[hb][0] : a_lo ? lds_v4i(tb) : Z;
@@ -326,36 +413,45 @@ int device_cus() {
 }
 
 size_t stream_lds(int nw, int nbw) {
-    return static_cast<size_t>(nw) * nbw * (kTab + 8 * sizeof(float2)) + 32 * static_cast<size_t>(nw) * sizeof(float);
+    return static_cast<size_t>(nw) * nbw * (kTab + 2 * 8 * sizeof(float2)) + 32 * static_cast<size_t>(nw) * sizeof(float);
 }
 
-template <typename XT, typename OT, int NBW, int TR>
+template <int DT, typename XT, typename OT, int NBW, int TR>
 hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
     const size_t l = stream_lds(nw, NBW);
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(t.n));
     if (nw == 8)
-        hipLaunchKernelGGL((gemv_stream_q4k<XT, OT, NBW, TR, 8, true>), grid, dim3(64 * nw), l, st, t);
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, true>), grid, dim3(64 * nw), l, st, t);
     else if (nw < 8)
-        hipLaunchKernelGGL((gemv_stream_q4k<XT, OT, NBW, TR, 8, false>), grid, dim3(64 * nw), l, st, t);
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, false>), grid, dim3(64 * nw), l, st, t);
     else if (nw == kMaxWaves)
-        hipLaunchKernelGGL((gemv_stream_q4k<XT, OT, NBW, TR, kMaxWaves, true>), grid, dim3(64 * nw), l, st, t);
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, true>), grid, dim3(64 * nw), l, st, t);
     else
-        hipLaunchKernelGGL((gemv_stream_q4k<XT, OT, NBW, TR, kMaxWaves, false>), grid, dim3(64 * nw), l, st, t);
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, false>), grid, dim3(64 * nw), l, st, t);
     return hipGetLastError();
 }
 
-template <typename XT, typename OT, int NBW>
+template <int DT, typename XT, typename OT, int NBW>
 hipError_t launch_tr(const SegTable &t, int tr, int64_t tiles, int nw, hipStream_t st) {
     if constexpr (NBW == 2) {
         switch (tr) {
-            case 20: return launch<XT, OT, NBW, 20>(t, tiles, nw, st);
-            case 24: return launch<XT, OT, NBW, 24>(t, tiles, nw, st);
-            case 28: return launch<XT, OT, NBW, 28>(t, tiles, nw, st);
-            case 32: return launch<XT, OT, NBW, 32>(t, tiles, nw, st);
+            case 20: return launch<DT, XT, OT, NBW, 20>(t, tiles, nw, st);
+            case 24: return launch<DT, XT, OT, NBW, 24>(t, tiles, nw, st);
+            case 28: return launch<DT, XT, OT, NBW, 28>(t, tiles, nw, st);
+            case 32: return launch<DT, XT, OT, NBW, 32>(t, tiles, nw, st);
             default: break;
         }
     }
-    return launch<XT, OT, NBW, 16>(t, tiles, nw, st);
+    return launch<DT, XT, OT, NBW, 16>(t, tiles, nw, st);
+}
+
+template <int DT, typename XT, typename OT>
+hipError_t launch_nbw(int nbw, const SegTable &t, int tr, int64_t tiles, int nw, hipStream_t st) {
+    switch (nbw) {
+        case 2: return launch_tr<DT, XT, OT, 2>(t, tr, tiles, nw, st);
+        case 3: return launch_tr<DT, XT, OT, 3>(t, tr, tiles, nw, st);
+        default: return launch_tr<DT, XT, OT, 4>(t, tr, tiles, nw, st);
+    }
 }
 
 // blocks per wave: two when K has at most 32 blocks (eight waves for 4096),
@@ -365,22 +461,37 @@ int stream_nbw(int nb) { return nb <= 32 ? 2 : (nb + kMaxWaves - 1) / kMaxWaves;
 }  // namespace
 
 bool gemv_stream_ok(int dt, const SegTable &t) {
-    if (dt != DT_Q4_K || t.rows != 1 || t.moe_tab || t.em_items) return false;
-    if (t.n_in % 256 || t.n_in > 256 * 4 * kMaxWaves || t.row_bytes % 16) return false;
+    // (Q8_0 and Q4_0 were tried here: their 32-value blocks cost eight loads
+    // per lane and group, and measured slower than the VALU stream kernel at
+    // one row, 25.6 vs 18.6-20.5 us at 4096 -> 14336)
+    if ((dt != DT_Q4_K && dt != DT_Q6_K) || t.rows != 1 || t.moe_tab || t.em_items) return false;
+    // Q4_K rows are 16-byte multiples and start 16-byte aligned; the others
+    // (210-, 34- and 18-byte blocks) need only the 2-byte alignment of their
+    // f16 fields
+    const uintptr_t wal = dt == DT_Q4_K ? 15 : 1;
+    if (t.n_in % 256 || t.n_in > 256 * 4 * kMaxWaves || (t.row_bytes & static_cast<int64_t>(wal))) return false;
     const int nbw = stream_nbw(t.n_in / 256);
+    // the one-shot tiles serve launches the resident workgroups cover in about
+    // two rounds; a larger matrix (a vocabulary head) streams better through
+    // the persistent row-split digit kernel, whose waves keep a ring of
+    // units in flight from tile to tile
+    int64_t rows = 0;
+    for (int i = 0; i < t.n; i++) rows += t.seg[i].n_out;
+    const int nw = (t.n_in / 256 + nbw - 1) / nbw;
+    if (rows > 2 * 32 * static_cast<int64_t>(device_cus()) * (nw <= 8 ? 2 : 1)) return false;
     for (int i = 0; i < t.n; i++) {
         const Seg &s = t.seg[i];
         // gate/up pairs take two row groups, which wider slices cannot afford
         if (s.kind == SEG_SILU && nbw > 2) return false;
         if (s.x != t.seg[0].x || (reinterpret_cast<uintptr_t>(s.x) & 15) ||
-            (reinterpret_cast<uintptr_t>(s.w) & 15))
+            (reinterpret_cast<uintptr_t>(s.w) & wal))
             return false;
-        if (s.kind == SEG_SILU && (reinterpret_cast<uintptr_t>(s.w2) & 15)) return false;
+        if (s.kind == SEG_SILU && (reinterpret_cast<uintptr_t>(s.w2) & wal)) return false;
     }
     return true;
 }
 
-hipError_t gemv_stream(bool act_f16, const SegTable &t0, hipStream_t st) {
+hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st) {
     SegTable t = t0;
     const int nb = t.n_in / 256;
     const int nbw = stream_nbw(nb);
@@ -411,18 +522,12 @@ hipError_t gemv_stream(bool act_f16, const SegTable &t0, hipStream_t st) {
         width = n > width ? n : width;
     }
     if (width >= (int64_t{1} << 31) || t.n < 1) return hipErrorNotSupported;
-    if (act_f16) {
-        switch (nbw) {
-            case 2: return launch_tr<_Float16, _Float16, 2>(t, tr, width, nw, st);
-            case 3: return launch_tr<_Float16, _Float16, 3>(t, tr, width, nw, st);
-            default: return launch_tr<_Float16, _Float16, 4>(t, tr, width, nw, st);
-        }
-    }
-    switch (nbw) {
-        case 2: return launch_tr<float, float, 2>(t, tr, width, nw, st);
-        case 3: return launch_tr<float, float, 3>(t, tr, width, nw, st);
-        default: return launch_tr<float, float, 4>(t, tr, width, nw, st);
-    }
+    if (dt == DT_Q6_K)
+        return act_f16 ? launch_nbw<DT_Q6_K, _Float16, _Float16>(nbw, t, tr, width, nw, st)
+                       : launch_nbw<DT_Q6_K, float, float>(nbw, t, tr, width, nw, st);
+
+    return act_f16 ? launch_nbw<DT_Q4_K, _Float16, _Float16>(nbw, t, tr, width, nw, st)
+                   : launch_nbw<DT_Q4_K, float, float>(nbw, t, tr, width, nw, st);
 }
 
 }  // namespace krk

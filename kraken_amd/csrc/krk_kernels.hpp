@@ -72,10 +72,10 @@ struct SegTable {
 };
 
 hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st);
-// Q4_K, one activation row: every weight byte of a tile loaded into registers
-// up front, digit planes per wave (gemv_stream.hip)
+// Q4_K and Q6_K, one activation row: every weight byte of a tile loaded into
+// registers up front, digit planes per wave (gemv_stream.hip)
 bool gemv_stream_ok(int dt, const SegTable &t);
-hipError_t gemv_stream(bool act_f16, const SegTable &t, hipStream_t st);
+hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t, hipStream_t st);
 // Q4_K / Q6_K rows 1..8 on the int8 MFMA (activations as exact int8 digit planes)
 bool gemv_digits_ok(int dt, const SegTable &t);
 hipError_t gemv_digits(int dt, bool act_f16, const SegTable &t, hipStream_t st);
