@@ -31,6 +31,7 @@
 #include "gemv_core.hpp"
 #include "krk_formats.hpp"
 #include "krk_kernels.hpp"
+#include "krk_mi355x.h"
 
 namespace krk {
 
@@ -83,7 +84,12 @@ __device__ __forceinline__ void load_x8(const _Float16 *p, float (&v)[8]) {
     for (int k = 0; k < 8; k++) v[k] = static_cast<float>(h[k]);
 }
 
-template <int DT, typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWEXACT, int LA = 8>
+// MOE: 0 plain segments; 1 routed gate/up pairs of one token (grid row s =
+// slot s, its banks read from moe_tab[moe_ids[s]], its output at seg[0].out
+// + s n_out); 2 the routed down projection of one token (K = the k slots'
+// activation rows concatenated; a wave's slice lies in one slot, whose bank
+// it reads and whose routing weight scales its activations)
+template <int DT, typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWEXACT, int MOE = 0, int LA = 8>
 __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr int BB = Q6 ? 210 : 144;     // bytes per 256-value block
@@ -104,17 +110,39 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
     // keeps them one round of scalar loads away from the first weight
     // request.  A segment with fewer tiles than the grid's width gives its
     // extra workgroups the last rows to re-read, and they store nothing.
-    const Seg &sg = t.seg[blockIdx.y];
+    const Seg &sg = t.seg[MOE ? 0 : blockIdx.y];
     const int kind = sg.kind;
     const int64_t n_out = sg.n_out;
     const uint8_t *w = static_cast<const uint8_t *>(sg.w);
     const uint8_t *w2s = static_cast<const uint8_t *>(sg.w2);
+    OT *outp = static_cast<OT *>(sg.out);
     const XT *x = static_cast<const XT *>(sg.x);
     const int64_t rb = t.row_bytes;
     const int nb = t.n_in >> 8;
     const bool pair = kind == SEG_SILU;
     const int rows_t = pair ? 16 : TR;
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * rows_t;
+    // routed banks: one dependent read of the slot's id and table entry
+    // (a dropped slot reads expert 0's bank; its output is never used, or
+    // its routing weight is 0)
+    float wslot = 1.0f;
+    int kblk = kb0;   // first block of this wave's slice within its bank row
+    if constexpr (MOE == 1) {
+        const int e = t.moe_ids[blockIdx.y];
+        const bool live = e >= 0 && e < t.moe_ne;
+        const krk_moe_entry &en = static_cast<const krk_moe_entry *>(t.moe_tab)[live ? e : 0];
+        w = static_cast<const uint8_t *>(en.p[KRK_MOE_GATE]);
+        w2s = static_cast<const uint8_t *>(en.p[KRK_MOE_UP]);
+        outp += static_cast<int64_t>(blockIdx.y) * n_out;
+    } else if constexpr (MOE == 2) {
+        const int bps = static_cast<int>(t.moe_kslot >> 8);   // blocks per slot
+        const int sl = kb0 / bps < t.moe_k ? kb0 / bps : t.moe_k - 1;
+        const int e = t.moe_ids[sl];
+        const bool live = e >= 0 && e < t.moe_ne;
+        w = static_cast<const uint8_t *>(static_cast<const krk_moe_entry *>(t.moe_tab)[live ? e : 0].p[KRK_MOE_DOWN]);
+        wslot = live ? t.moe_wts[sl] : 0.0f;
+        kblk = kb0 - sl * bps;
+    }
     const uint8_t *w2 = pair ? w2s : w;
 
     // ---- the wave's activations first: pass p, lane l holds values
@@ -161,7 +189,7 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
         }
         if (n >= n_out) n = n_out - 1;
         // a ragged last slice re-reads the matrix's last block (discarded)
-        const int blk = kb0 + b < nb ? kb0 + b : nb - 1;
+        const int blk = (kb0 + b < nb ? kb0 + b : nb - 1) - kb0 + kblk;
         src[i] = base + n * rb + static_cast<int64_t>(blk) * BB;
     }
     auto issue = [&](int i) {
@@ -232,7 +260,8 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
             *reinterpret_cast<u32x2 *>(o) = u32x2{p0[0], p0[1]};
             *reinterpret_cast<u32x2 *>(o + 32) = u32x2{p1[0], p1[1]};
             *reinterpret_cast<u32x2 *>(o + 64) = u32x2{p2[0], p2[1]};
-            if ((lane & 3) == 0) ex[sbw] = float2{live ? dn : 1.0f, sum};
+            // (routed down: the slot's weight scales the activations)
+            if ((lane & 3) == 0) ex[sbw] = float2{(live ? dn : 1.0f) * wslot, sum * wslot};
         }
         if constexpr (Q6) {
             // lanes 4j, 4j + 1 hold values 0..15 of sub-block j, 4j + 2, 4j + 3
@@ -383,7 +412,7 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
             if (k < nw) v += red[rr * nw + k];
         return v;
     };
-    OT *o = static_cast<OT *>(sg.out) + n0 + r;
+    OT *o = outp + n0 + r;
     if (kind == SEG_SILU) {
         const float gs = row_sum(r), us = row_sum(16 + r);
         if constexpr (sizeof(OT) == 2) {
@@ -416,18 +445,20 @@ size_t stream_lds(int nw, int nbw) {
     return static_cast<size_t>(nw) * nbw * (kTab + 2 * 8 * sizeof(float2)) + 32 * static_cast<size_t>(nw) * sizeof(float);
 }
 
-template <int DT, typename XT, typename OT, int NBW, int TR>
+template <int DT, typename XT, typename OT, int NBW, int TR, int MOE>
 hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
     const size_t l = stream_lds(nw, NBW);
-    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(t.n));
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(MOE == 2 ? 1 : t.n));
     if (nw == 8)
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, true>), grid, dim3(64 * nw), l, st, t);
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, true, MOE>), grid, dim3(64 * nw), l, st, t);
     else if (nw < 8)
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, false>), grid, dim3(64 * nw), l, st, t);
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, false, MOE>), grid, dim3(64 * nw), l, st, t);
     else if (nw == kMaxWaves)
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, true>), grid, dim3(64 * nw), l, st, t);
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, true, MOE>), grid, dim3(64 * nw), l, st,
+                           t);
     else
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, false>), grid, dim3(64 * nw), l, st, t);
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, false, MOE>), grid, dim3(64 * nw), l,
+                           st, t);
     return hipGetLastError();
 }
 
@@ -435,14 +466,14 @@ template <int DT, typename XT, typename OT, int NBW>
 hipError_t launch_tr(const SegTable &t, int tr, int64_t tiles, int nw, hipStream_t st) {
     if constexpr (NBW == 2) {
         switch (tr) {
-            case 20: return launch<DT, XT, OT, NBW, 20>(t, tiles, nw, st);
-            case 24: return launch<DT, XT, OT, NBW, 24>(t, tiles, nw, st);
-            case 28: return launch<DT, XT, OT, NBW, 28>(t, tiles, nw, st);
-            case 32: return launch<DT, XT, OT, NBW, 32>(t, tiles, nw, st);
+            case 20: return launch<DT, XT, OT, NBW, 20, 0>(t, tiles, nw, st);
+            case 24: return launch<DT, XT, OT, NBW, 24, 0>(t, tiles, nw, st);
+            case 28: return launch<DT, XT, OT, NBW, 28, 0>(t, tiles, nw, st);
+            case 32: return launch<DT, XT, OT, NBW, 32, 0>(t, tiles, nw, st);
             default: break;
         }
     }
-    return launch<DT, XT, OT, NBW, 16>(t, tiles, nw, st);
+    return launch<DT, XT, OT, NBW, 16, 0>(t, tiles, nw, st);
 }
 
 template <int DT, typename XT, typename OT>
@@ -464,7 +495,21 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
     // (Q8_0 and Q4_0 were tried here: their 32-value blocks cost eight loads
     // per lane and group, and measured slower than the VALU stream kernel at
     // one row, 25.6 vs 18.6-20.5 us at 4096 -> 14336)
-    if ((dt != DT_Q4_K && dt != DT_Q6_K) || t.rows != 1 || t.moe_tab || t.em_items) return false;
+    if ((dt != DT_Q4_K && dt != DT_Q6_K) || t.rows != 1 || t.em_items) return false;
+    if (t.moe_tab) {
+        // one routed token, Q4_K banks: gate/up pairs (one per slot, n_in of
+        // at most 32 blocks) or the down projection over the concatenated
+        // slots, each wave's slice inside one slot
+        if (dt != DT_Q4_K || t.moe_tokens > 1 || t.n_in % 256 || t.row_bytes % 16) return false;
+        const int nb = t.n_in / 256, nbw = stream_nbw(nb);
+        if (t.moe_down)
+            return t.n == 1 && t.moe_k >= 1 && t.moe_kslot % 256 == 0 && t.n_in == t.moe_k * t.moe_kslot &&
+                   (t.moe_kslot / 256) % nbw == 0 && nb <= 4 * kMaxWaves && t.seg[0].kind == SEG_PLAIN &&
+                   (reinterpret_cast<uintptr_t>(t.seg[0].x) & 15) == 0;
+        for (int i = 0; i < t.n; i++)
+            if (t.seg[i].kind != SEG_SILU || t.seg[i].x != t.seg[0].x) return false;
+        return nbw == 2 && (reinterpret_cast<uintptr_t>(t.seg[0].x) & 15) == 0;
+    }
     // Q4_K rows are 16-byte multiples and start 16-byte aligned; the others
     // (210-, 34- and 18-byte blocks) need only the 2-byte alignment of their
     // f16 fields
@@ -496,6 +541,38 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
     const int nb = t.n_in / 256;
     const int nbw = stream_nbw(nb);
     const int nw = (nb + nbw - 1) / nbw;
+    if (t.moe_tab) {
+        // routed experts (f32 activations, Q4_K): gate/up pairs take 32-row
+        // tiles (16 + 16), the down projection 16-row tiles when its slices
+        // are wider than two blocks
+        if (act_f16 || dt != DT_Q4_K) return hipErrorNotSupported;
+        if (!t.moe_down) {
+            const int64_t width = (t.seg[0].n_out + 15) / 16;
+            return launch<DT_Q4_K, float, float, 2, 32, 1>(t, width, nw, st);
+        }
+        const int64_t cap = static_cast<int64_t>(device_cus()) * (nw <= 8 ? 2 : 1);
+        int tr = 16;
+        if (nbw == 2) {
+            int64_t best = INT64_MAX;
+            for (int c = 16; c <= 32; c += 4) {
+                const int64_t cost = ((t.seg[0].n_out + c - 1) / c + cap - 1) / cap * c;
+                if (cost < best) { best = cost; tr = c; }
+            }
+        }
+        const int64_t width = (t.seg[0].n_out + tr - 1) / tr;
+        switch (nbw) {
+            case 2:
+                switch (tr) {
+                    case 20: return launch<DT_Q4_K, float, float, 2, 20, 2>(t, width, nw, st);
+                    case 24: return launch<DT_Q4_K, float, float, 2, 24, 2>(t, width, nw, st);
+                    case 28: return launch<DT_Q4_K, float, float, 2, 28, 2>(t, width, nw, st);
+                    case 32: return launch<DT_Q4_K, float, float, 2, 32, 2>(t, width, nw, st);
+                    default: return launch<DT_Q4_K, float, float, 2, 16, 2>(t, width, nw, st);
+                }
+            case 3: return launch<DT_Q4_K, float, float, 3, 16, 2>(t, width, nw, st);
+            default: return launch<DT_Q4_K, float, float, 4, 16, 2>(t, width, nw, st);
+        }
+    }
     bool has_pair = false;
     for (int i = 0; i < t.n; i++) has_pair |= t.seg[i].kind == SEG_SILU;
     // tile height: among 16, 20, .., 32 (32 with gate/up pairs, which need

@@ -592,9 +592,12 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
         }
     }
     if (gu_ok && (dn_ok || a.n_tok == 1)) {
-        const hipError_t e = gemv_digits(DT_Q4_K, false, gu, st);
+        // one token: the register-streaming kernel where it takes the shapes
+        const bool gu_s = a.n_tok == 1 && gemv_stream_ok(DT_Q4_K, gu);
+        const bool dn_s = a.n_tok == 1 && dn_ok && gemv_stream_ok(DT_Q4_K, d);
+        const hipError_t e = gu_s ? gemv_stream(DT_Q4_K, false, gu, st) : gemv_digits(DT_Q4_K, false, gu, st);
         if (e != hipSuccess) return e;
-        if (dn_ok) return gemv_digits(DT_Q4_K, false, d, st);
+        if (dn_ok) return dn_s ? gemv_stream(DT_Q4_K, false, d, st) : gemv_digits(DT_Q4_K, false, d, st);
     }
     if (a.n_tok == 1 && !a.act_f16) {
         const int64_t ggu = (a.n_ff + 3) / 4, gdn = (a.n_embd + 7) / 8;

@@ -480,8 +480,9 @@ def test_moe_table_record_evicts_oldest(krk, torch_cuda):
 @pytest.mark.parametrize("n_tok,k,drop", [(1, 2, False), (1, 8, False), (1, 4, True), (3, 4, True),
                                           (16, 8, False), (70, 2, True), (520, 8, True)])
 def test_moe_dispatch_whole_units(krk, torch_cuda, be32, n_tok, k, drop):
-    """n_ff a multiple of 512: up to 64 tokens, gate/up and down run on the
-    digit-plane kernel (down over each token's concatenated slots), one
+    """n_ff a multiple of 512: one token runs gate/up and down on the
+    register-streaming kernel (down over the concatenated slots, each wave's
+    slice inside one slot); 2..64 tokens on the digit-plane kernel, one
     workgroup group per token; 70 and 520 tokens take expert-major items
     (520 x 8 pairs exceed the plan's LDS copy of the ids).  drop: a slot
     with id -1 contributes nothing, as in the host loop."""
