@@ -44,6 +44,10 @@ constexpr int kMaxWaves = 16;
 
 __device__ __forceinline__ v4i lds_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
+// Q4_0 sub-block s (of the eight in 256 values) -> its digit-table slot:
+// 0 1 4 5 2 3 6 7, so that MFMA m of lane pair p meets block 4 p + m
+__host__ __device__ constexpr int q40_slot(int s) { return s ^ ((((s >> 1) ^ (s >> 2)) & 1) * 6); }
+
 // loads from the 2-byte aligned Q6_K blocks (210 bytes): the part runs its
 // global memory with unaligned access allowed, which hipcc's gfx950 target
 // assumes (it emits a single dwordx4 for these)
@@ -92,7 +96,8 @@ __device__ __forceinline__ void load_x8(const _Float16 *p, float (&v)[8]) {
 template <int DT, typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWEXACT, int MOE = 0, int LA = 8>
 __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
     constexpr bool Q6 = DT == DT_Q6_K;
-    constexpr int BB = Q6 ? 210 : 144;     // bytes per 256-value block
+    constexpr bool Q40 = DT == DT_Q4_0;
+    constexpr int BB = Q6 ? 210 : 144;     // bytes per 256 values (Q4_0: eight 18-byte blocks)
     constexpr int RG = (TR + 15) / 16;     // 16-row groups of a plain tile
     constexpr int NL = RG * NBW;           // (16 rows, block) groups of a wave
     constexpr int NPASS = (NBW + 1) / 2;   // x passes: 16 sub-blocks of 8 x 4 lanes each
@@ -171,7 +176,7 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
     //         at 206, inside the block)
     u32x4 hd[NL], qa[NL], qb[NL];
     uint2 sc[Q6 ? NL : 1];
-    uint32_t dd[Q6 ? NL : 1];
+    uint32_t dd[Q6 || Q40 ? NL : 1];
     const int h6 = gq >> 1, lh6 = gq & 1;
     const uint8_t *src[NL];
 #pragma unroll
@@ -199,6 +204,11 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
             qb[i] = ld128_a2(src[i] + 128 + 32 * h6 + 16 * lh6);
             sc[i] = ld64_a2(src[i] + 192 + 8 * h6);
             dd[i] = ld32_a2(src[i] + 206);
+        } else if constexpr (Q40) {
+            // blocks 2 gq and 2 gq + 1 of the eight: 36 bytes at 36 gq
+            hd[i] = ld128_a2(src[i] + 36 * gq);
+            qa[i] = ld128_a2(src[i] + 36 * gq + 16);
+            dd[i] = ld32_a2(src[i] + 36 * gq + 32);
         } else {
             hd[i] = ld128(src[i]);
             qa[i] = ld128(src[i] + 16 + 16 * gq);
@@ -256,12 +266,17 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
             p2[k >> 2] |= (static_cast<uint32_t>(d2) & 255u) << sh;
         }
         if (sbw < 8 * NBW) {
-            uint8_t *o = tab + (sbw >> 3) * kTab + (sbw & 7) * 96 + 8 * (lane & 3);
+            // Q4_0: sub-block s of the 256 values sits in table slot q40_slot(s),
+            // its values in the order 0..7, 16..23, 8..15, 24..31 (the order
+            // its codes take in the B operand)
+            const int sbt = Q40 ? q40_slot(sbw & 7) : (sbw & 7);
+            const int po = Q40 ? 8 * (((lane & 1) << 1) | ((lane >> 1) & 1)) : 8 * (lane & 3);
+            uint8_t *o = tab + (sbw >> 3) * kTab + sbt * 96 + po;
             *reinterpret_cast<u32x2 *>(o) = u32x2{p0[0], p0[1]};
             *reinterpret_cast<u32x2 *>(o + 32) = u32x2{p1[0], p1[1]};
             *reinterpret_cast<u32x2 *>(o + 64) = u32x2{p2[0], p2[1]};
             // (routed down: the slot's weight scales the activations)
-            if ((lane & 3) == 0) ex[sbw] = float2{(live ? dn : 1.0f) * wslot, sum * wslot};
+            if ((lane & 3) == 0) ex[(sbw & ~7) + sbt] = float2{(live ? dn : 1.0f) * wslot, sum * wslot};
         }
         if constexpr (Q6) {
             // lanes 4j, 4j + 1 hold values 0..15 of sub-block j, 4j + 2, 4j + 3
@@ -349,6 +364,49 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
         }
         const uint8_t *tb = tab + b * kTab + a_off;
         const int hb = HOLD ? b : 0;
+        if constexpr (Q40) {
+            // lane group gq holds blocks 2 gq, 2 gq + 1: {d, 16 code bytes}
+            // twice.  MFMA m of lane pair p = gq / 2 takes block 4 p + m, lane
+            // 2 p its code bytes 0..7 and lane 2 p + 1 bytes 8..15 (low nibbles
+            // = values j .. j + 7, high = j + 16 .. j + 23); the 16-lane swap
+            // trades the halves and the scales between the two lanes
+            const u32x4 L0 = hd[i], L1 = qa[i];
+            const uint32_t L2 = dd[i];
+            uint32_t X[4] = {__builtin_amdgcn_alignbyte(L0.y, L0.x, 2), __builtin_amdgcn_alignbyte(L0.z, L0.y, 2),
+                             L1.y, L1.z};
+            uint32_t Y[4] = {__builtin_amdgcn_alignbyte(L0.w, L0.z, 2), __builtin_amdgcn_alignbyte(L1.x, L0.w, 2),
+                             L1.w, L2};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const auto sw = __builtin_amdgcn_permlane16_swap(X[k], Y[k], false, false);
+                X[k] = sw[0];
+                Y[k] = sw[1];
+            }
+            const auto dsw = __builtin_amdgcn_permlane16_swap(L0.x & 0xFFFFu, L1.x >> 16, false, false);
+            auto codes = [&](uint32_t c0, uint32_t c1) {
+                return v4i{static_cast<int>(c0 & M), static_cast<int>(c1 & M), static_cast<int>((c0 >> 4) & M),
+                           static_cast<int>((c1 >> 4) & M)};
+            };
+            const v4i A0l = HOLD ? HA[hb][0] : a_lo ? lds_v4i(tb) : Z;
+            const v4i A1l = HOLD ? HA[hb][1] : a_lo ? lds_v4i(tb + 384) : Z;
+            const v4i A0h = HOLD ? HA[hb][2] : a_hi ? lds_v4i(tb) : Z;
+            const v4i A1h = HOLD ? HA[hb][3] : a_hi ? lds_v4i(tb + 384) : Z;
+            const float2 ex0 = HOLD ? HE[hb][0] : ex[b * 8 + gq], ex1 = HOLD ? HE[hb][1] : ex[b * 8 + 4 + gq];
+            v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0l, codes(X[0], X[1]), Z, 0, 0, 0);
+            C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0h, codes(X[2], X[3]), C0, 0, 0, 0);
+            v4i C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1l, codes(Y[0], Y[1]), Z, 0, 0, 0);
+            C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1h, codes(Y[2], Y[3]), C1, 0, 0, 0);
+            // table slots gq and 4 + gq: the value d (q - 8) of
+            // dequant_q4_0 (src/quant.cpp:331-339) as d (2^-e S - 8 sum x)
+            const int S0 = C0[0] + (C0[1] << 8) + (C0[2] << 16);
+            const int S1 = C1[0] + (C1[1] << 8) + (C1[2] << 16);
+            float a = acc[rg];
+            a = __builtin_fmaf(h2f(dsw[0]), __builtin_fmaf(ex0.x, static_cast<float>(S0), -8.0f * ex0.y), a);
+            a = __builtin_fmaf(h2f(dsw[1]), __builtin_fmaf(ex1.x, static_cast<float>(S1), -8.0f * ex1.y), a);
+            acc[rg] = a;
+            __builtin_amdgcn_sched_barrier(0);
+            continue;
+        }
         const v4i A0l = HOLD ? HA[hb][0] : a_lo ? lds_v4i(tb) : Z;
         const v4i A1l = HOLD ? HA[hb][1] : a_lo ? lds_v4i(tb + 384) : Z;
         const v4i A0h = HOLD ? HA[hb][2] : a_hi ? lds_v4i(tb) : Z;
@@ -492,10 +550,10 @@ int stream_nbw(int nb) { return nb <= 32 ? 2 : (nb + kMaxWaves - 1) / kMaxWaves;
 }  // namespace
 
 bool gemv_stream_ok(int dt, const SegTable &t) {
-    // (Q8_0 and Q4_0 were tried here: their 32-value blocks cost eight loads
-    // per lane and group, and measured slower than the VALU stream kernel at
-    // one row, 25.6 vs 18.6-20.5 us at 4096 -> 14336)
-    if ((dt != DT_Q4_K && dt != DT_Q6_K) || t.rows != 1 || t.em_items) return false;
+    // (Q8_0 was tried here with eight loads per lane and group, and measured
+    // slower than the VALU stream kernel at one row, 25.6 vs 20.5 us at
+    // 4096 -> 14336)
+    if ((dt != DT_Q4_K && dt != DT_Q6_K && dt != DT_Q4_0) || t.rows != 1 || t.em_items) return false;
     if (t.moe_tab) {
         // one routed token, Q4_K banks: gate/up pairs (one per slot, n_in of
         // at most 32 blocks) or the down projection over the concatenated
@@ -510,10 +568,10 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
             if (t.seg[i].kind != SEG_SILU || t.seg[i].x != t.seg[0].x) return false;
         return nbw == 2 && (reinterpret_cast<uintptr_t>(t.seg[0].x) & 15) == 0;
     }
-    // Q4_K rows are 16-byte multiples and start 16-byte aligned; the others
-    // (210-, 34- and 18-byte blocks) need only the 2-byte alignment of their
-    // f16 fields
-    const uintptr_t wal = dt == DT_Q4_K ? 15 : 1;
+    // Q4_K rows, and Q4_0 rows of whole 256-value groups, are 16-byte
+    // multiples and start 16-byte aligned; Q6_K's 210-byte blocks need only
+    // the 2-byte alignment of their f16 fields
+    const uintptr_t wal = dt == DT_Q6_K ? 1 : 15;
     if (t.n_in % 256 || t.n_in > 256 * 4 * kMaxWaves || (t.row_bytes & static_cast<int64_t>(wal))) return false;
     const int nbw = stream_nbw(t.n_in / 256);
     // the one-shot tiles serve launches the resident workgroups cover in about
@@ -602,6 +660,9 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
     if (dt == DT_Q6_K)
         return act_f16 ? launch_nbw<DT_Q6_K, _Float16, _Float16>(nbw, t, tr, width, nw, st)
                        : launch_nbw<DT_Q6_K, float, float>(nbw, t, tr, width, nw, st);
+    if (dt == DT_Q4_0)
+        return act_f16 ? launch_nbw<DT_Q4_0, _Float16, _Float16>(nbw, t, tr, width, nw, st)
+                       : launch_nbw<DT_Q4_0, float, float>(nbw, t, tr, width, nw, st);
 
     return act_f16 ? launch_nbw<DT_Q4_K, _Float16, _Float16>(nbw, t, tr, width, nw, st)
                    : launch_nbw<DT_Q4_K, float, float>(nbw, t, tr, width, nw, st);

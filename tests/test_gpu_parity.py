@@ -243,6 +243,33 @@ def test_gemm_mfma_parity_many_tiles(krk, torch_cuda, be16, dt):
     assert rel(host(out).astype(np.float32), ref) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q8_0])
+@pytest.mark.parametrize("shape", [(300, 2000, 2304), (700, 1000, 4096), (64, 256, 4096)])
+def test_gemm_splits_repeat(krk, torch_cuda, be16, be32, dt, shape):
+    """Few tiles over the CUs: split-K in two and four (K 4096) and a single
+    split (K 2304), each checked against the oracle in both activation types
+    and bit-equal on a repeated call (the partials leave no state behind)."""
+    torch = torch_cuda
+    M, N, K = shape
+    w = make_weights(krk, dt, N, K, seed=80 + dt)
+    x = krk.synth_normal(M * K, seed=81).reshape(M, K).astype(np.float16)
+    say("gemm splits", dt, M, N, K)
+    ref = O.gemm(dt, w, x.astype(np.float32), N, nthreads=16)
+    wd, xd = dev(torch, w), dev(torch, x)
+    outs = []
+    for _ in range(2):
+        out = torch.full((M, N), float("nan"), dtype=torch.float16, device="cuda")
+        be16.gemm(out, xd, wd, dt, N, K, M)
+        be16.sync()
+        outs.append(host(out))
+    assert rel(outs[0].astype(np.float32), ref) <= GEMM_TOL
+    assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16))
+    out32 = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    be32.gemm(out32, dev(torch, x.astype(np.float32)), wd, dt, N, K, M)
+    be32.sync()
+    assert rel(host(out32), ref) <= GEMM_TOL
+
+
 # ------------------------------------------------------------------ router --
 def test_router_softmax_topk(krk, torch_cuda, be32, rng):
     torch = torch_cuda
