@@ -97,7 +97,9 @@ template <int DT, typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWE
 __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr bool Q40 = DT == DT_Q4_0;
-    constexpr int BB = Q6 ? 210 : 144;     // bytes per 256 values (Q4_0: eight 18-byte blocks)
+    constexpr bool Q80 = DT == DT_Q8_0;
+    constexpr bool QS = Q40 || Q80;        // 32-value blocks, eight per 256 values
+    constexpr int BB = Q6 ? 210 : Q80 ? 272 : 144;   // bytes per 256 values
     constexpr int RG = (TR + 15) / 16;     // 16-row groups of a plain tile
     constexpr int NL = RG * NBW;           // (16 rows, block) groups of a wave
     constexpr int NPASS = (NBW + 1) / 2;   // x passes: 16 sub-blocks of 8 x 4 lanes each
@@ -176,7 +178,8 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
     //         at 206, inside the block)
     u32x4 hd[NL], qa[NL], qb[NL];
     uint2 sc[Q6 ? NL : 1];
-    uint32_t dd[Q6 || Q40 ? NL : 1];
+    uint32_t dd[Q6 || QS ? NL : 1];
+    u32x4 qc[Q80 ? NL : 1];
     const int h6 = gq >> 1, lh6 = gq & 1;
     const uint8_t *src[NL];
 #pragma unroll
@@ -209,6 +212,13 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
             hd[i] = ld128_a2(src[i] + 36 * gq);
             qa[i] = ld128_a2(src[i] + 36 * gq + 16);
             dd[i] = ld32_a2(src[i] + 36 * gq + 32);
+        } else if constexpr (Q80) {
+            // blocks 2 gq and 2 gq + 1 of the eight: 68 bytes at 68 gq
+            hd[i] = ld128_a2(src[i] + 68 * gq);
+            qa[i] = ld128_a2(src[i] + 68 * gq + 16);
+            qb[i] = ld128_a2(src[i] + 68 * gq + 32);
+            qc[i] = ld128_a2(src[i] + 68 * gq + 48);
+            dd[i] = ld32_a2(src[i] + 68 * gq + 64);
         } else {
             hd[i] = ld128(src[i]);
             qa[i] = ld128(src[i] + 16 + 16 * gq);
@@ -266,10 +276,10 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
             p2[k >> 2] |= (static_cast<uint32_t>(d2) & 255u) << sh;
         }
         if (sbw < 8 * NBW) {
-            // Q4_0: sub-block s of the 256 values sits in table slot q40_slot(s),
-            // its values in the order 0..7, 16..23, 8..15, 24..31 (the order
-            // its codes take in the B operand)
-            const int sbt = Q40 ? q40_slot(sbw & 7) : (sbw & 7);
+            // Q4_0 and Q8_0: block s of the eight sits in table slot
+            // q40_slot(s); Q4_0's values in the order 0..7, 16..23, 8..15,
+            // 24..31 (the order its codes take in the B operand)
+            const int sbt = QS ? q40_slot(sbw & 7) : (sbw & 7);
             const int po = Q40 ? 8 * (((lane & 1) << 1) | ((lane >> 1) & 1)) : 8 * (lane & 3);
             uint8_t *o = tab + (sbw >> 3) * kTab + sbt * 96 + po;
             *reinterpret_cast<u32x2 *>(o) = u32x2{p0[0], p0[1]};
@@ -364,6 +374,55 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
         }
         const uint8_t *tb = tab + b * kTab + a_off;
         const int hb = HOLD ? b : 0;
+        if constexpr (Q80) {
+            // lane group gq holds blocks 2 gq, 2 gq + 1: {d, 32 int8 codes}
+            // twice.  MFMA m of lane pair p = gq / 2 takes block 4 p + m, lane
+            // 2 p its codes 0..15 and lane 2 p + 1 codes 16..31; the 16-lane
+            // swap trades the halves and the scales between the two lanes
+            const uint32_t W[17] = {hd[i].x, hd[i].y, hd[i].z, hd[i].w, qa[i].x, qa[i].y, qa[i].z, qa[i].w,
+                                    qb[i].x, qb[i].y, qb[i].z, qb[i].w, qc[i].x, qc[i].y, qc[i].z, qc[i].w, dd[i]};
+            uint32_t X[8], Y[8];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                X[k] = __builtin_amdgcn_alignbyte(W[k + 1], W[k], 2);
+                Y[k] = __builtin_amdgcn_alignbyte(W[k + 5], W[k + 4], 2);
+                X[4 + k] = W[9 + k];
+                Y[4 + k] = W[13 + k];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const auto sw = __builtin_amdgcn_permlane16_swap(X[k], Y[k], false, false);
+                X[k] = sw[0];
+                Y[k] = sw[1];
+            }
+            const auto dsw = __builtin_amdgcn_permlane16_swap(W[0] & 0xFFFFu, W[8] >> 16, false, false);
+            auto codes = [&](const uint32_t *c) {
+                return v4i{static_cast<int>(c[0]), static_cast<int>(c[1]), static_cast<int>(c[2]),
+                           static_cast<int>(c[3])};
+            };
+            const v4i A0l = HOLD ? HA[hb][0] : a_lo ? lds_v4i(tb) : Z;
+            const v4i A1l = HOLD ? HA[hb][1] : a_lo ? lds_v4i(tb + 384) : Z;
+            const v4i A0h = HOLD ? HA[hb][2] : a_hi ? lds_v4i(tb) : Z;
+            const v4i A1h = HOLD ? HA[hb][3] : a_hi ? lds_v4i(tb + 384) : Z;
+            const float2 ex0 = HOLD ? HE[hb][0] : ex[b * 8 + gq], ex1 = HOLD ? HE[hb][1] : ex[b * 8 + 4 + gq];
+            v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0l, codes(X), Z, 0, 0, 0);
+            C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0h, codes(X + 4), C0, 0, 0, 0);
+            v4i C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1l, codes(Y), Z, 0, 0, 0);
+            C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1h, codes(Y + 4), C1, 0, 0, 0);
+            // table slots gq and 4 + gq: d sum q x (dequant_q8_0,
+            // src/quant.cpp:381-387); |sum q X| < 2^34, so the exact plane
+            // sums are combined in f32
+            const float s0 = __builtin_fmaf(65536.0f, static_cast<float>(C0[2]),
+                                            __builtin_fmaf(256.0f, static_cast<float>(C0[1]), static_cast<float>(C0[0])));
+            const float s1 = __builtin_fmaf(65536.0f, static_cast<float>(C1[2]),
+                                            __builtin_fmaf(256.0f, static_cast<float>(C1[1]), static_cast<float>(C1[0])));
+            float a = acc[rg];
+            a = __builtin_fmaf(h2f(dsw[0]), ex0.x * s0, a);
+            a = __builtin_fmaf(h2f(dsw[1]), ex1.x * s1, a);
+            acc[rg] = a;
+            __builtin_amdgcn_sched_barrier(0);
+            continue;
+        }
         if constexpr (Q40) {
             // lane group gq holds blocks 2 gq, 2 gq + 1: {d, 16 code bytes}
             // twice.  MFMA m of lane pair p = gq / 2 takes block 4 p + m, lane
@@ -550,10 +609,8 @@ int stream_nbw(int nb) { return nb <= 32 ? 2 : (nb + kMaxWaves - 1) / kMaxWaves;
 }  // namespace
 
 bool gemv_stream_ok(int dt, const SegTable &t) {
-    // (Q8_0 was tried here with eight loads per lane and group, and measured
-    // slower than the VALU stream kernel at one row, 25.6 vs 20.5 us at
-    // 4096 -> 14336)
-    if ((dt != DT_Q4_K && dt != DT_Q6_K && dt != DT_Q4_0) || t.rows != 1 || t.em_items) return false;
+    if ((dt != DT_Q4_K && dt != DT_Q6_K && dt != DT_Q4_0 && dt != DT_Q8_0) || t.rows != 1 || t.em_items)
+        return false;
     if (t.moe_tab) {
         // one routed token, Q4_K banks: gate/up pairs (one per slot, n_in of
         // at most 32 blocks) or the down projection over the concatenated
@@ -568,7 +625,7 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
             if (t.seg[i].kind != SEG_SILU || t.seg[i].x != t.seg[0].x) return false;
         return nbw == 2 && (reinterpret_cast<uintptr_t>(t.seg[0].x) & 15) == 0;
     }
-    // Q4_K rows, and Q4_0 rows of whole 256-value groups, are 16-byte
+    // Q4_K rows, and Q4_0 / Q8_0 rows of whole 256-value groups, are 16-byte
     // multiples and start 16-byte aligned; Q6_K's 210-byte blocks need only
     // the 2-byte alignment of their f16 fields
     const uintptr_t wal = dt == DT_Q6_K ? 1 : 15;
@@ -663,6 +720,9 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
     if (dt == DT_Q4_0)
         return act_f16 ? launch_nbw<DT_Q4_0, _Float16, _Float16>(nbw, t, tr, width, nw, st)
                        : launch_nbw<DT_Q4_0, float, float>(nbw, t, tr, width, nw, st);
+    if (dt == DT_Q8_0)
+        return act_f16 ? launch_nbw<DT_Q8_0, _Float16, _Float16>(nbw, t, tr, width, nw, st)
+                       : launch_nbw<DT_Q8_0, float, float>(nbw, t, tr, width, nw, st);
 
     return act_f16 ? launch_nbw<DT_Q4_K, _Float16, _Float16>(nbw, t, tr, width, nw, st)
                    : launch_nbw<DT_Q4_K, float, float>(nbw, t, tr, width, nw, st);

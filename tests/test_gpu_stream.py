@@ -1,7 +1,7 @@
-"""GPU parity of the one-row Q4_K / Q6_K / Q4_0 GEMV that loads each tile's weights
+"""GPU parity of the one-row Q4_K / Q6_K / Q4_0 / Q8_0 GEMV that loads each tile's weights
 into registers up front (gemv_stream.hip), against the CPU oracle.
 
-The kernel takes Q4_K, Q6_K and Q4_0 launches with one activation row (plain,
+The kernel takes Q4_K, Q6_K, Q4_0 and Q8_0 launches with one activation row (plain,
 residual and gate/up segments), so these cases walk its shape rules: K slices of two
 to four blocks per wave with a ragged last slice, one to sixteen waves, tile
 heights 16..32 with partial last tiles, several segments per launch, f32
@@ -17,7 +17,7 @@ from test_gpu_parity import GEMV_TOL, dev, digit_edge_x, host, make_weights, rel
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q4_0])
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q4_0, O.Q8_0])
 @pytest.mark.parametrize("n_out,n_in", [(1, 256), (17, 512), (300, 2304), (4096, 4096), (14336, 4096),
                                         (11008, 4096), (4096, 11008), (77, 14336), (1000, 16384),
                                         (33, 8192)])
@@ -34,7 +34,7 @@ def test_stream_shapes(krk, torch_cuda, be32, dt, n_out, n_in):
     assert e <= GEMV_TOL
 
 
-@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q4_0])
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q4_0, O.Q8_0])
 @pytest.mark.parametrize("n_in", [4096, 11008])
 def test_stream_f16(krk, torch_cuda, be16, dt, n_in):
     torch = torch_cuda
@@ -51,7 +51,7 @@ def test_stream_f16(krk, torch_cuda, be16, dt, n_in):
     assert rel(got, ref) <= 2.0 ** -11 + GEMV_TOL
 
 
-@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q4_0])
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q4_0, O.Q8_0])
 def test_stream_groups(krk, torch_cuda, be32, be16, dt):
     """Three plain segments of different heights in one launch; a gate/up
     pair with the SiLU epilogue; the residual epilogue with rexp in f16."""
