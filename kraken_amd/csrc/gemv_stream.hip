@@ -92,9 +92,11 @@ __device__ __forceinline__ void load_x8(const _Float16 *p, float (&v)[8]) {
 // slot s, its banks read from moe_tab[moe_ids[s]], its output at seg[0].out
 // + s n_out); 2 the routed down projection of one token (K = the k slots'
 // activation rows concatenated; a wave's slice lies in one slot, whose bank
-// it reads and whose routing weight scales its activations)
+// it reads and whose routing weight scales its activations); 3 and 4
+// expert-major runs (gate/up pairs, down): grid row a = active expert
+// em_runs[a], its weights loaded once and applied to each of its rows in turn
 template <int DT, typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWEXACT, int MOE = 0, int LA = 8>
-__global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
+__global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kernel(SegTable t) {
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr bool Q40 = DT == DT_Q4_0;
     constexpr bool Q80 = DT == DT_Q8_0;
@@ -150,24 +152,41 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
         wslot = live ? t.moe_wts[sl] : 0.0f;
         kblk = kb0 - sl * bps;
     }
+    int pb = 0, pe = 1;   // the rows served: expert-major runs' plan positions
+    if constexpr (MOE >= 3) {
+        // the run record and the active count in one round of scalar loads
+        const EmRun &run = t.em_runs[blockIdx.y];
+        const int nact = *t.em_n_act;
+        pb = run.pb;
+        pe = run.pe;
+        w = static_cast<const uint8_t *>(run.w[MOE == 3 ? 0 : 2]);
+        w2s = static_cast<const uint8_t *>(run.w[1]);
+        if (static_cast<int>(blockIdx.y) >= nact) return;   // beyond the active experts
+    }
+    auto row_x = [&](int p) {
+        return MOE >= 3 ? x + static_cast<int64_t>(t.em_tok ? t.em_tok[p] : p) * t.em_xrow : x;
+    };
     const uint8_t *w2 = pair ? w2s : w;
 
     // ---- the wave's activations first: pass p, lane l holds values
     // 8 (l & 3) .. + 7 of the slice's sub-block 16 p + l / 4
     // the loads issue at raised wave priority, so a wave that is still
     // issuing wins the vector-memory port over one that is already decoding
-    __builtin_amdgcn_s_setprio(3);
     float xv[NPASS][8];
+    auto load_xrow = [&](const XT *xr) {
 #pragma unroll
-    for (int p = 0; p < NPASS; p++) {
-        const int sbw = p * 16 + (lane >> 2);
-        const bool in = sbw < 8 * NBW && kb0 + (sbw >> 3) < nb;
-        load_x8(x + (in ? static_cast<int64_t>(kb0) * 256 + sbw * 32 + 8 * (lane & 3) : 0), xv[p]);
-        if (!in) {
+        for (int p = 0; p < NPASS; p++) {
+            const int sbw = p * 16 + (lane >> 2);
+            const bool in = sbw < 8 * NBW && kb0 + (sbw >> 3) < nb;
+            load_x8(xr + (in ? static_cast<int64_t>(kb0) * 256 + sbw * 32 + 8 * (lane & 3) : 0), xv[p]);
+            if (!in) {
 #pragma unroll
-            for (int k = 0; k < 8; k++) xv[p][k] = 0.0f;
+                for (int k = 0; k < 8; k++) xv[p][k] = 0.0f;
+            }
         }
-    }
+    };
+    __builtin_amdgcn_s_setprio(3);
+    load_xrow(row_x(pb));
     // ---- then every weight byte of the wave's slice of the tile: group i =
     // (row group rg, block b), lane (c16, gq) takes of row rg * 16 + c16:
     //   Q4_K: the 16-byte header and code bytes 16 gq .. + 15 of each
@@ -229,6 +248,9 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
     for (int i = 0; i < (LA < NL ? LA : NL); i++) issue(i);
     __builtin_amdgcn_s_setprio(0);
 
+    for (int pr = pb; pr < pe; pr++) {
+    // (expert-major runs: every wave has read the previous row's sums)
+    if (MOE >= 3 && pr > pb) __syncthreads();
     // ---- the digit table of the slice (this wave's own LDS), layout
     // [block][sub-block][plane][32 bytes], {2^-e, sum x} per sub-block, and
     // for Q6_K the exact integer sums of X over each 16-value half (int bits)
@@ -297,6 +319,9 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
         }
     }
 
+    // (expert-major runs: the next row's activations load while this one
+    // is multiplied)
+    if (MOE >= 3 && pr + 1 < pe) load_xrow(row_x(pr + 1));
     // ---- per-lane MFMA roles (A row c16 = 4 sub-block' + digit plane)
     const int ap = c16 & 3, as = c16 >> 2;
     const int sl = 2 * (gq >> 1);
@@ -313,7 +338,7 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
     for (int rg = 0; rg < RG; rg++) acc[rg] = 0.0f;
     // two-block slices read their A operands once, before the first group
     // lands (wider slices read them per group: registers)
-    constexpr bool HOLD = NBW == 2 && !Q6;
+    constexpr bool HOLD = NBW == 2 && !Q6 && MOE < 3;   // (expert-major runs keep their weights live across rows: registers)
     v4i HA[HOLD ? NBW : 1][4];
     float2 HE[HOLD ? NBW : 1][2];
     if constexpr (HOLD) {
@@ -333,7 +358,7 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
     // before the first decode)
 #pragma unroll
     for (int i = 0; i < NL; i++) {
-        if (i + LA < NL) issue(i + LA);
+        if (i + LA < NL && pr == pb) issue(i + LA);
         __builtin_amdgcn_sched_barrier(0);
         const int rg = i / NBW, b = i - (i / NBW) * NBW;
         if (kb0 + b >= nb) continue;   // wave-uniform: the ragged slice's missing blocks
@@ -521,7 +546,7 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
     }
     __syncthreads();
     const int r = static_cast<int>(threadIdx.x);
-    if (r >= rows_t || n0 + r >= n_out) return;
+    if (r >= rows_t || n0 + r >= n_out) continue;
     auto row_sum = [&](int rr) {
         float v = 0.0f;
 #pragma unroll
@@ -529,7 +554,7 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
             if (k < nw) v += red[rr * nw + k];
         return v;
     };
-    OT *o = outp + n0 + r;
+    OT *o = outp + (MOE >= 3 ? static_cast<int64_t>(pr) * t.em_orow : 0) + n0 + r;
     if (kind == SEG_SILU) {
         const float gs = row_sum(r), us = row_sum(16 + r);
         if constexpr (sizeof(OT) == 2) {
@@ -544,6 +569,7 @@ __global__ void __launch_bounds__(64 * NWMAX) gemv_stream_kernel(SegTable t) {
     } else {
         const float inv = kind == SEG_ACC && t.rexp ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
         store_out<OT>(o, row_sum(r), kind, inv);
+    }
     }
 }
 
@@ -565,7 +591,8 @@ size_t stream_lds(int nw, int nbw) {
 template <int DT, typename XT, typename OT, int NBW, int TR, int MOE>
 hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
     const size_t l = stream_lds(nw, NBW);
-    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(MOE == 2 ? 1 : t.n));
+    const dim3 grid(static_cast<unsigned>(tiles),
+                    static_cast<unsigned>(MOE == 2 ? 1 : MOE >= 3 ? t.em_max_items : t.n));
     if (nw == 8)
         hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, true, MOE>), grid, dim3(64 * nw), l, st, t);
     else if (nw < 8)
@@ -612,11 +639,20 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
     if ((dt != DT_Q4_K && dt != DT_Q6_K && dt != DT_Q4_0 && dt != DT_Q8_0) || t.rows != 1 || t.em_items)
         return false;
     if (t.moe_tab) {
-        // one routed token, Q4_K banks: gate/up pairs (one per slot, n_in of
-        // at most 32 blocks) or the down projection over the concatenated
-        // slots, each wave's slice inside one slot
-        if (dt != DT_Q4_K || t.moe_tokens > 1 || t.n_in % 256 || t.row_bytes % 16) return false;
+        if (dt != DT_Q4_K || t.n_in % 256 || t.row_bytes % 16) return false;
         const int nb = t.n_in / 256, nbw = stream_nbw(nb);
+        if (t.em_runs) {
+            // expert-major runs, Q4_K banks: gate/up pairs (n_in of at most
+            // 32 blocks) or the down bank; 16-byte aligned activation rows
+            const Seg &s0 = t.seg[0];
+            return t.n == 1 && !t.moe_down && t.em_n_act && t.em_max_items > 0 &&
+                   t.em_xrow % 4 == 0 && nb <= 4 * kMaxWaves && (reinterpret_cast<uintptr_t>(s0.x) & 15) == 0 &&
+                   ((s0.kind == SEG_SILU && nbw == 2) || s0.kind == SEG_PLAIN);
+        }
+        // one routed token: gate/up pairs (one per slot, n_in of at most 32
+        // blocks) or the down projection over the concatenated slots, each
+        // wave's slice inside one slot
+        if (t.moe_tokens > 1) return false;
         if (t.moe_down)
             return t.n == 1 && t.moe_k >= 1 && t.moe_kslot % 256 == 0 && t.n_in == t.moe_k * t.moe_kslot &&
                    (t.moe_kslot / 256) % nbw == 0 && nb <= 4 * kMaxWaves && t.seg[0].kind == SEG_PLAIN &&
@@ -661,6 +697,16 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
         // tiles (16 + 16), the down projection 16-row tiles when its slices
         // are wider than two blocks
         if (act_f16 || dt != DT_Q4_K) return hipErrorNotSupported;
+        if (t.em_runs) {
+            if (t.seg[0].kind == SEG_SILU)
+                return launch<DT_Q4_K, float, float, 2, 32, 3>(t, (t.seg[0].n_out + 15) / 16, nw, st);
+            const int64_t width = (t.seg[0].n_out + 15) / 16;
+            switch (nbw) {
+                case 2: return launch<DT_Q4_K, float, float, 2, 16, 4>(t, width, nw, st);
+                case 3: return launch<DT_Q4_K, float, float, 3, 16, 4>(t, width, nw, st);
+                default: return launch<DT_Q4_K, float, float, 4, 16, 4>(t, width, nw, st);
+            }
+        }
         if (!t.moe_down) {
             const int64_t width = (t.seg[0].n_out + 15) / 16;
             return launch<DT_Q4_K, float, float, 2, 32, 1>(t, width, nw, st);

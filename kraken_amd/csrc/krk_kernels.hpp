@@ -25,6 +25,13 @@ struct Seg {
 
 constexpr int kMaxSegs = 8;
 
+// One active expert of a routed layer: its gate, up and down banks and its
+// plan positions [pb, pe) (written by the MoE plan on the device)
+struct EmRun {
+    const void *w[3];
+    int32_t pb, pe;
+};
+
 struct SegTable {
     Seg seg[kMaxSegs];
     int n;               // segments in use
@@ -69,11 +76,20 @@ struct SegTable {
     int em_wpe;          // set by the launcher
     int em_max_items;    // upper bound on *em_n_items (sizes the grid)
     int64_t em_xrow, em_orow;
+    // Expert-major runs (em_runs nullable; the register-streaming kernel,
+    // with moe_tab and one segment): grid row a serves run em_runs[a] while
+    // a < *em_n_act (em_max_items bounds the rows).  Its weights are the
+    // run's gate/up pair (SEG_SILU) or down bank (SEG_PLAIN), loaded once for
+    // all of its rows: plan positions p = pb .. pe - 1, activations seg[0].x
+    // row em_tok[p] (row p when em_tok is null), outputs seg[0].out row p.
+    const EmRun *em_runs;
+    const int32_t *em_n_act;
 };
 
 hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st);
-// Q4_K and Q6_K, one activation row: every weight byte of a tile loaded into
-// registers up front, digit planes per wave (gemv_stream.hip)
+// Q4_K, Q6_K, Q4_0 and Q8_0, one activation row (or the rows of expert-major
+// runs): every weight byte of a tile loaded into registers up front, digit
+// planes per wave (gemv_stream.hip)
 bool gemv_stream_ok(int dt, const SegTable &t);
 hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t, hipStream_t st);
 // Q4_K / Q6_K rows 1..8 on the int8 MFMA (activations as exact int8 digit planes)

@@ -54,6 +54,7 @@ struct MoeWs {
     int32_t *n_items;   // [1]
     _Float16 *midf;     // [P, n_ff]      f16 activations: the row-scaled mid rows
     float *rscale;      // [P]            f16 activations: each mid row's power-of-two scale
+    EmRun *runs;        // [n_expert]     active experts' banks and plan ranges
 };
 
 static size_t al(size_t v) { return (v + 255) & ~size_t(255); }
@@ -71,14 +72,16 @@ static MoeWs carve(void *ws, int64_t P, int ne, int64_t n_embd, int64_t n_ff) {
     w.items = reinterpret_cast<int32_t *>(p); p += al(P * 16);
     w.n_items = reinterpret_cast<int32_t *>(p); p += al(4);
     w.midf = reinterpret_cast<_Float16 *>(p); p += al(P * n_ff * 2);
-    w.rscale = reinterpret_cast<float *>(p);
+    w.rscale = reinterpret_cast<float *>(p); p += al(P * 4);
+    w.runs = reinterpret_cast<EmRun *>(p);
     return w;
 }
 
 size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t n_ff) {
     const int64_t P = n_tok * k;
     return al((n_expert + 1) * 4) + al(n_expert * 4) + al(4) + 2 * al(P * 4) +
-           al(P * n_ff * 4) + al(P * n_embd * 4) + al(P * 16) + al(4) + al(P * n_ff * 2) + al(P * 4);
+           al(P * n_ff * 4) + al(P * n_embd * 4) + al(P * 16) + al(4) + al(P * n_ff * 2) + al(P * 4) +
+           al(n_expert * sizeof(EmRun));
 }
 
 // ------------------------------------------------------------------ plan ----
@@ -89,7 +92,8 @@ size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t
 constexpr int kPlanLds = 4096;  // (token, slot) pairs whose ids the plan keeps in LDS
 constexpr int kItemRows = 2;    // activation rows of an expert item (the digit kernel's NX)
 __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict__ ids, int64_t P,
-                                                        int k, int ne, MoeWs w) {
+                                                        int k, int ne, MoeWs w,
+                                                        const krk_moe_entry *__restrict__ tab) {
     __shared__ int32_t cnt[1024];
     __shared__ int32_t cur[1024];
     __shared__ int32_t sid[kPlanLds];   // the ids, when they fit
@@ -133,7 +137,16 @@ __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict
         if (e < ne) {
             w.off[e] = base;
             cur[e] = base;
-            if (c[j]) w.act[abase++] = e;
+            if (c[j]) {
+                // the run record: the expert's banks and plan range in one place
+                EmRun &r = w.runs[abase];
+                r.w[0] = tab[e].p[KRK_MOE_GATE];
+                r.w[1] = tab[e].p[KRK_MOE_UP];
+                r.w[2] = tab[e].p[KRK_MOE_DOWN];
+                r.pb = base;
+                r.pe = base + c[j];
+                w.act[abase++] = e;
+            }
             for (int r = 0; r < c[j]; r += kItemRows) {
                 int32_t *it = w.items + 4 * ibase++;
                 it[0] = e;
@@ -334,26 +347,34 @@ __global__ void __launch_bounds__(256) moe_reduce_kernel(const int32_t *__restri
                                                          const float *__restrict__ wts, int k,
                                                          int64_t n_embd, MoeWs w,
                                                          OT *__restrict__ out) {
-    // this token's live pairs in ascending expert id (insertion sort by one
-    // thread, k <= 64), then every thread adds its column in that order
+    // this token's live pairs in ascending expert id (ties, which the router
+    // never makes, in slot order; k <= 64), then every thread adds its
+    // column in that order
     __shared__ int32_t ord_pos[64];
     __shared__ float ord_w[64];
+    __shared__ int32_t s_pos[64], s_id[64];
+    __shared__ float s_w[64];
     __shared__ int nlive;
     const int64_t t = blockIdx.y;
+    if (threadIdx.x < k) {   // the token's pairs, one load round
+        s_pos[threadIdx.x] = w.plan_pos[t * k + threadIdx.x];
+        s_id[threadIdx.x] = ids[t * k + threadIdx.x];
+        s_w[threadIdx.x] = wts[t * k + threadIdx.x];
+    }
+    __syncthreads();
+    // rank of each live pair among the token's live pairs by (expert id,
+    // slot): one thread per slot, no private arrays
+    if (threadIdx.x < k && s_pos[threadIdx.x] >= 0) {
+        const int me = threadIdx.x, e = s_id[me];
+        int q = 0;
+        for (int s = 0; s < k; s++)
+            q += s_pos[s] >= 0 && (s_id[s] < e || (s_id[s] == e && s < me));
+        ord_pos[q] = s_pos[me];
+        ord_w[q] = s_w[me];
+    }
     if (threadIdx.x == 0) {
-        int ord[64];
         int n = 0;
-        for (int s = 0; s < k; s++) {
-            if (w.plan_pos[t * k + s] < 0) continue;
-            const int e = ids[t * k + s];
-            int q = n++;
-            while (q > 0 && ids[t * k + ord[q - 1]] > e) { ord[q] = ord[q - 1]; q--; }
-            ord[q] = s;
-        }
-        for (int q = 0; q < n; q++) {
-            ord_pos[q] = w.plan_pos[t * k + ord[q]];
-            ord_w[q] = wts[t * k + ord[q]];
-        }
+        for (int s = 0; s < k; s++) n += s_pos[s] >= 0;
         nlive = n;
     }
     __syncthreads();
@@ -471,6 +492,7 @@ __global__ void __launch_bounds__(512) moe_down1_kernel(const krk_moe_entry *__r
 }
 
 constexpr int64_t kMoeTokenGroups = 64;
+constexpr int64_t kMoeStreamTokens = 64;   // expert-major streaming runs up to this many tokens
 
 hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t st) {
     const int64_t P = a.n_tok * a.k;
@@ -548,6 +570,48 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     const bool groups = on_digits && a.n_tok <= kMoeTokenGroups;
     const bool gu_ok = groups && gemv_digits_ok(DT_Q4_K, gu);
     const bool dn_ok = groups && gemv_digits_ok(DT_Q4_K, d);
+    if (on_digits && a.n_tok >= 2 && a.n_tok <= kMoeStreamTokens) {
+        // expert-major runs on the register-streaming kernel: one grid row
+        // per active expert, whose weights are loaded once and applied to
+        // each of its tokens in turn; then the ordered per-token reduce
+        SegTable eg{};
+        eg.n = 1;
+        eg.n_in = static_cast<int>(a.n_embd);
+        eg.row_bytes = a.rb_gate;
+        eg.rows = 1;
+        eg.seg[0].x = a.xn;
+        eg.seg[0].out = w.mid;
+        eg.seg[0].n_out = a.n_ff;
+        eg.seg[0].kind = SEG_SILU;
+        eg.moe_tab = tab;
+        eg.moe_ne = a.n_expert;
+        eg.em_runs = w.runs;
+        eg.em_n_act = w.n_act;
+        eg.em_tok = w.plan_tok;
+        eg.em_max_items = static_cast<int>(P < a.n_expert ? P : a.n_expert);
+        eg.em_xrow = a.n_embd;
+        eg.em_orow = a.n_ff;
+        SegTable ed = eg;
+        ed.n_in = static_cast<int>(a.n_ff);
+        ed.row_bytes = a.rb_down;
+        ed.seg[0].x = w.mid;
+        ed.seg[0].out = w.part;
+        ed.seg[0].n_out = a.n_embd;
+        ed.seg[0].kind = SEG_PLAIN;
+        ed.em_tok = nullptr;
+        ed.em_xrow = a.n_ff;
+        ed.em_orow = a.n_embd;
+        if (gemv_stream_ok(DT_Q4_K, eg) && gemv_stream_ok(DT_Q4_K, ed)) {
+            hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab);
+            hipError_t e = gemv_stream(DT_Q4_K, false, eg, st);
+            if (e == hipSuccess) e = gemv_stream(DT_Q4_K, false, ed, st);
+            if (e != hipSuccess) return e;
+            const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));
+            hipLaunchKernelGGL((moe_reduce_kernel<float>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
+                               a.n_embd, w, static_cast<float *>(a.out));
+            return hipGetLastError();
+        }
+    }
     if (on_digits && a.n_tok > kMoeTokenGroups) {
         // expert-major items, each expert's weights read once per run of up
         // to kItemRows of its tokens; then the ordered per-token reduce
@@ -581,7 +645,7 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
         ed.em_xrow = a.n_ff;
         ed.em_orow = a.n_embd;
         if (P <= (1 << 20) && gemv_digits_ok(DT_Q4_K, eg) && gemv_digits_ok(DT_Q4_K, ed)) {
-            hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w);
+            hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab);
             hipError_t e = gemv_digits(DT_Q4_K, false, eg, st);
             if (e == hipSuccess) e = gemv_digits(DT_Q4_K, false, ed, st);
             if (e != hipSuccess) return e;
@@ -612,7 +676,7 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     // the plan path: every f16 dispatch (the reference GPU's rounding points
     // need each (token, slot) row whole before its scale), and f32 token
     // batches the digit kernels do not take
-    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w);
+    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab);
     const int64_t amax = P < a.n_expert ? P : a.n_expert;
     const int64_t ggu = (a.n_ff + 1) / 2, gdn = (a.n_embd + 3) / 4;
     const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));
