@@ -2,13 +2,18 @@
 // device pointer table (Backend::moe_dispatch, backend.hpp:1001-1009; the
 // reference's moe_table_* kernels, src/hip/kernels/moe_table.hpp:38-551).
 //
-// Q4_K banks with f32 activations take two launches of the digit-plane GEMV
-// for up to 64 tokens, and expert-major items above that.  Other f32 cases:
-// one token takes two VALU launches; more tokens take the plan path, none
-// of its launches per expert and none waiting on the host:
+// Q4_K banks with f32 activations run on the int8 matrix cores (digit-plane
+// activations): one token takes two launches of the register-streaming
+// GEMV (gate/up per slot, down over the concatenated slots); more tokens
+// take the plan, then expert-major runs of the same kernel -- one grid row
+// per active expert, whose banks are loaded once and applied to each of its
+// tokens in turn -- for gate/up and for down, then the ordered reduce (step 4
+// below).  Other f32 cases: one token takes two VALU launches; more tokens
+// take the plan path, none of its launches per expert and none waiting on
+// the host:
 //   1. plan      one workgroup: expert-major plan of the (token, slot) pairs,
-//                the active-expert list in ascending id, and each pair's
-//                plan position;
+//                the active-expert list in ascending id (with each expert's
+//                banks and plan range), and each pair's plan position;
 //   2. gate/up   ONE launch over all active experts: workgroup = (expert,
 //                group of ff rows); its pairs' activation rows are gathered
 //                through the plan and share every weight byte read;
@@ -492,7 +497,6 @@ __global__ void __launch_bounds__(512) moe_down1_kernel(const krk_moe_entry *__r
 }
 
 constexpr int64_t kMoeTokenGroups = 64;
-constexpr int64_t kMoeStreamTokens = 64;   // expert-major streaming runs up to this many tokens
 
 hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t st) {
     const int64_t P = a.n_tok * a.k;
@@ -559,18 +563,20 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     d.moe_tokens = static_cast<int>(a.n_tok);
     d.moe_xtok = a.k * a.n_ff;
     d.moe_otok = a.n_embd;
-    // A token group reads its experts for itself, so an expert routed to
-    // several tokens is read several times: token groups serve decode-sized
-    // batches (up to kMoeTokenGroups tokens). Larger Q4_K batches take
-    // expert-major items, which read each active expert once per item of
-    // kItemRows tokens; what the digit kernel cannot take goes to the plan path.
+    // Several tokens take expert-major runs of the streaming kernel (each
+    // active expert's banks read once; measured 280 -> 256 us at 16 tokens and
+    // about twice as fast as the digit kernel's items from 65 tokens up).
+    // Where the streaming kernel cannot take the shapes, token groups of the
+    // digit kernel serve up to kMoeTokenGroups tokens (each token reads its
+    // experts for itself), expert-major items of kItemRows tokens larger
+    // batches, and the plan path whatever the digit kernel cannot take.
     const bool on_digits = !a.act_f16 && a.wt == DT_Q4_K && a.wt_down == DT_Q4_K && a.aligned16 &&
                            a.rb_gate == a.rb_up &&
                            a.k <= kMaxSegs && a.k * a.n_ff <= (1 << 30);
     const bool groups = on_digits && a.n_tok <= kMoeTokenGroups;
     const bool gu_ok = groups && gemv_digits_ok(DT_Q4_K, gu);
     const bool dn_ok = groups && gemv_digits_ok(DT_Q4_K, d);
-    if (on_digits && a.n_tok >= 2 && a.n_tok <= kMoeStreamTokens) {
+    if (on_digits && a.n_tok >= 2) {
         // expert-major runs on the register-streaming kernel: one grid row
         // per active expert, whose weights are loaded once and applied to
         // each of its tokens in turn; then the ordered per-token reduce
