@@ -192,12 +192,13 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     //   Q4_K: the 16-byte header and code bytes 16 gq .. + 15 of each
     //         64-byte half (hd, qa, qb);
     //   Q6_K: with h = gq / 2, l = gq % 2: ql bytes 64 h + 16 l and
-    //         64 h + 32 + 16 l (hd, qa), qh bytes 128 + 32 h + 16 l (qb), the
-    //         eight scales 192 + 8 h (sc) and d (the top half of the dword
-    //         at 206, inside the block)
+    //         64 h + 32 + 16 l (hd, qa), qh bytes 128 + 32 h + 16 l (qb), and
+    //         16 bytes at 192 + 2 h holding the half's eight scales and, for
+    //         h = 1, d (sc)
+    //   Q4_0, Q8_0: blocks 2 gq and 2 gq + 1 of the eight (hd, qa, qb, qc, dd)
     u32x4 hd[NL], qa[NL], qb[NL];
-    uint2 sc[Q6 ? NL : 1];
-    uint32_t dd[Q6 || QS ? NL : 1];
+    u32x4 sc[Q6 ? NL : 1];
+    uint32_t dd[QS ? NL : 1];
     u32x4 qc[Q80 ? NL : 1];
     const int h6 = gq >> 1, lh6 = gq & 1;
     const uint8_t *src[NL];
@@ -224,8 +225,10 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
             hd[i] = ld128_a2(src[i] + 64 * h6 + 16 * lh6);
             qa[i] = ld128_a2(src[i] + 64 * h6 + 32 + 16 * lh6);
             qb[i] = ld128_a2(src[i] + 128 + 32 * h6 + 16 * lh6);
-            sc[i] = ld64_a2(src[i] + 192 + 8 * h6);
-            dd[i] = ld32_a2(src[i] + 206);
+            // the sixteen scales and d: lanes of half h = 0 take bytes
+            // 192..207 (their eight scales first), of h = 1 bytes 194..209
+            // (their eight scales at 6..13, d at 14..15)
+            sc[i] = ld128_a2(src[i] + 192 + 2 * h6);
         } else if constexpr (Q40) {
             // blocks 2 gq and 2 gq + 1 of the eight: 36 bytes at 36 gq
             hd[i] = ld128_a2(src[i] + 36 * gq);
@@ -369,7 +372,10 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
             // 0..63 as int8; the offset 32 through the 16-value sums of X:
             // S = sum (q - 32) X, |S| <= 16 * 32 * 2^22, exact in wrapping int32
             const u32x4 l0 = hd[i], l1 = qa[i], qh = qb[i];
-            const float d = h2f(dd[i] >> 16);
+            // d from a lane of half 1 (lane l ^ 32 or l itself)
+            const float d = h2f(__builtin_amdgcn_permlane32_swap(sc[i].w, sc[i].w, false, false)[1] >> 16);
+            const uint32_t scx = h6 ? __builtin_amdgcn_alignbyte(sc[i].z, sc[i].y, 2) : sc[i].x;
+            const uint32_t scy = h6 ? __builtin_amdgcn_alignbyte(sc[i].w, sc[i].z, 2) : sc[i].y;
             float a = acc[rg];
 #pragma unroll
             for (int qd = 0; qd < 4; qd++) {
@@ -381,7 +387,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
                                static_cast<int>(((ql.w >> ns) & M) | (((qh.w >> hs) & 0x03030303u) << 4))};
                 // scale of group 8 h + 2 qd + l: byte 2 qd + l of the lane's eight
                 const int jj = 2 * qd + lh6;
-                const uint32_t sw = jj < 4 ? sc[i].x : sc[i].y;
+                const uint32_t sw = jj < 4 ? scx : scy;
                 const float ds = d * static_cast<float>(static_cast<int8_t>(sw >> (8 * (jj & 3))));
                 // A rows 4 gq + p: digit plane p of sub-block 4 h + qd, half l
                 const v4i A = a6 ? lds_v4i(tab + b * kTab + a6_off + qd * 96) : Z;
