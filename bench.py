@@ -545,7 +545,7 @@ def main():
                    "rows": 1, "activations": "f32", "weight_copies": g["copies"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(), "kernel": read_profile_field("q4k_gemv_4096x14336_kernel_trace.md", "headline_kernel"),
+                     "traffic": read_traffic(), "kernel": read_profile_field("bench_all_configs_kernel_trace.md", "headline_kernel"),
                      "algorithmic_bytes_per_launch": g["bytes"]},
         "cpu_baseline": cpu and {k: v for k, v in cpu.items()},
         "extras": extras,

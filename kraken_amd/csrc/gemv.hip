@@ -1023,7 +1023,7 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 // lane keeps its 64 activations and their group sums in registers for the
 // kernel's lifetime; otherwise x is staged in LDS and read per unit.
 template <int DT, typename XT, typename OT, int RB, int NSLOT, bool XREG>
-__global__ void __launch_bounds__(512) gemv_stream_kernel(SegTable t, int64_t total, int xfloats) {
+__global__ void __launch_bounds__(512) gemv_valu_kernel(SegTable t, int64_t total, int xfloats) {
     using F = WaveFmt<DT>;
     using D = LdsDot<DT, RB>;
     constexpr int BV = blk_vals(DT), BB = blk_bytes(DT);
@@ -1215,7 +1215,7 @@ static hipError_t launch_stream(SegTable t, hipStream_t st) {
             if (lds + sizeof(Seg) * kMaxSegs > 160u * 1024u) break;
             int blocks = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &blocks, gemv_stream_kernel<DT, XT, OT, RB, NSLOT, XREG>, 64 * cand, lds) != hipSuccess)
+                    &blocks, gemv_valu_kernel<DT, XT, OT, RB, NSLOT, XREG>, 64 * cand, lds) != hipSuccess)
                 blocks = 0;
             if (blocks * cand >= best && blocks > 0) { best = blocks * cand; nw = cand; per_cu = blocks; }
         }
@@ -1232,7 +1232,7 @@ static hipError_t launch_stream(SegTable t, hipStream_t st) {
     }
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
     if (grid * nw > total) grid = (total + nw - 1) / nw;
-    hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, RB, NSLOT, XREG>), dim3(static_cast<unsigned>(grid)),
+    hipLaunchKernelGGL((gemv_valu_kernel<DT, XT, OT, RB, NSLOT, XREG>), dim3(static_cast<unsigned>(grid)),
                        dim3(64 * nw), xbytes + nw * per_wave, st, t, total, xfloats);
     return hipGetLastError();
 }
