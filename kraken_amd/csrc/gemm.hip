@@ -652,10 +652,27 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float *__restr
 static int pick_split(int64_t M, int64_t N, int64_t K, int dt) {
     const int64_t tiles = ((M + GB_M - 1) / GB_M) * ((N + GB_N - 1) / GB_N);
     const int64_t kblk = blk_vals(dt) < GB_K ? GB_K : blk_vals(dt);
-    int s = 1;
-    // fill at least 256 CUs with one workgroup each, keep >= 2048 K per split
-    while (tiles * s < 256 && K / (s * 2) >= 2048 && (K / (s * 2)) % kblk == 0) s *= 2;
-    return s;
+    const int64_t cus = device_cus();
+    // Estimated time of a split (us): rounds of resident workgroups x K per
+    // split at ~0.034 us per K value and round (a 256 x 256 tile, measured),
+    // plus the partials' traffic -- written and read back, 8 s M N bytes --
+    // at ~4 TB/s.  Splits keep at least 1024 K in whole blocks; ties keep
+    // the smaller split.
+    auto cost = [&](int64_t s) {
+        const double rounds = static_cast<double>((tiles * s + cus - 1) / cus);
+        const double part = s > 1 ? 8.0 * static_cast<double>(s) * M * N / 4.0e6 : 0.0;
+        return rounds * static_cast<double>(K / s) * 0.034 + part;
+    };
+    int best = 1;
+    double best_cost = cost(1);
+    for (int s = 2; s <= 64 && K / s >= 1024 && K % s == 0 && (K / s) % kblk == 0; s *= 2) {
+        const double c = cost(s);
+        if (c < best_cost) {
+            best_cost = c;
+            best = s;
+        }
+    }
+    return best;
 }
 
 size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K) {

@@ -579,16 +579,6 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     }
 }
 
-int device_cus() {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            cus = 256;
-    }
-    return cus;
-}
 
 size_t stream_lds(int nw, int nbw) {
     return static_cast<size_t>(nw) * nbw * (kTab + 2 * 8 * sizeof(float2)) + 32 * static_cast<size_t>(nw) * sizeof(float);
@@ -640,6 +630,17 @@ hipError_t launch_nbw(int nbw, const SegTable &t, int tr, int64_t tiles, int nw,
 int stream_nbw(int nb) { return nb <= 32 ? 2 : (nb + kMaxWaves - 1) / kMaxWaves; }
 
 }  // namespace
+
+int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+    }
+    return cus;
+}
 
 bool gemv_stream_ok(int dt, const SegTable &t) {
     if ((dt != DT_Q4_K && dt != DT_Q6_K && dt != DT_Q4_0 && dt != DT_Q8_0) || t.rows != 1 || t.em_items)
