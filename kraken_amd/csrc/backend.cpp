@@ -38,7 +38,7 @@ struct krk_backend {
     size_t ws_bytes = 0;
     std::string err;
     static constexpr int kMoeCache = 256;  // layers of MoE tables checked once
-    struct MoeOk { MoeKey key; krk_moe_entry e0; bool aligned; };
+    struct MoeOk { MoeKey key; krk_moe_entry e0; bool aligned; bool uniform; };
     MoeOk moe_ok[kMoeCache];
     int n_moe_ok = 0;
 };
@@ -472,7 +472,7 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
     // dispatch can be captured in a graph.  A table rewritten in place after
     // its first use is not re-checked.
     krk_moe_entry e0{};
-    bool aligned = false;
+    bool aligned = false, uniform = true;
     const krk_moe_entry *tab = static_cast<const krk_moe_entry *>(table);
     const MoeKey key{table, layer, n_expert, n_embd, n_ff};
     int hit = -1;
@@ -481,10 +481,14 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
     if (hit >= 0) {
         e0 = b->moe_ok[hit].e0;
         aligned = b->moe_ok[hit].aligned;
+        uniform = b->moe_ok[hit].uniform;
     } else {
         // every bank of the layer: present, of a served type with its rows
-        // aligned for that type's loads, one type per role (gate = up),
-        // the layer's geometry; and whether all rows start 16-byte aligned
+        // aligned for that type's loads, gate and up of one type, the
+        // layer's geometry; whether all rows start 16-byte aligned, and
+        // whether every expert has expert 0's types (the matrix-core paths
+        // take uniform Q4_K layers; the VALU kernels read each expert's
+        // types from the table)
         std::vector<krk_moe_entry> ents(static_cast<size_t>(n_expert));
         hipError_t he = hipMemcpyAsync(ents.data(), tab + static_cast<int64_t>(layer) * n_expert,
                                        sizeof(krk_moe_entry) * ents.size(), hipMemcpyDeviceToHost, b->stream);
@@ -506,13 +510,13 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
                                 (weight_align(en.type[m]) - 1)))
                     return fail(b, KRK_ERR_ARG, "moe_dispatch: expert %d matrix %d rows under-aligned for type %d",
                                 e, m, en.type[m]);
-                // one type per role across the layer, gate and up alike (the
-                // expert kernels decode up with the gate's type)
-                if (en.type[m] != e0.type[m] || en.type[1] != en.type[0])
-                    return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: mixed expert formats");
+                // gate and up alike (the expert kernels decode up with the
+                // gate's type); the types may vary from expert to expert
+                if (en.type[1] != en.type[0])
+                    return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: expert %d gate and up of different types", e);
+                if (en.type[m] != e0.type[m]) uniform = false;
                 if (reinterpret_cast<uintptr_t>(en.p[m]) & 15) aligned = false;
                 // the kernels step every bank's rows by its type's row size
-                // (one stride per role for the whole layer)
                 if (en.row_bytes[m] != krk_dtype_row_bytes(en.type[m], en.n_in[m]))
                     return fail(b, KRK_ERR_ARG,
                                 "moe_dispatch: expert %d matrix %d row_bytes %lld is not the row size %lld of "
@@ -528,10 +532,10 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
         // remember it; a full record drops its oldest entry (that layer is
         // read and checked again on its next dispatch)
         if (b->n_moe_ok < krk_backend::kMoeCache) {
-            b->moe_ok[b->n_moe_ok++] = {key, e0, aligned};
+            b->moe_ok[b->n_moe_ok++] = {key, e0, aligned, uniform};
         } else {
             for (int i = 1; i < krk_backend::kMoeCache; i++) b->moe_ok[i - 1] = b->moe_ok[i];
-            b->moe_ok[krk_backend::kMoeCache - 1] = {key, e0, aligned};
+            b->moe_ok[krk_backend::kMoeCache - 1] = {key, e0, aligned, uniform};
         }
     }
     krk::MoeArgs a{};
@@ -541,8 +545,10 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
     a.xn = xn; a.out = out;
     a.n_tok = n_tok; a.n_embd = n_embd; a.n_ff = n_ff;
     a.act_f16 = b->act == KRK_ACT_F16;
-    a.wt = e0.type[0];
-    a.wt_down = e0.type[2];
+    // (a layer whose types vary across experts: no single type, the VALU
+    // kernels' per-expert switch)
+    a.wt = uniform ? e0.type[0] : -1;
+    a.wt_down = uniform ? e0.type[2] : -1;
     a.rb_gate = e0.row_bytes[0]; a.rb_up = e0.row_bytes[1]; a.rb_down = e0.row_bytes[2];
     a.aligned16 = aligned;
     if (int s = ensure_ws(b, krk::moe_workspace(n_tok, k, n_expert, n_embd, n_ff))) return s;

@@ -30,8 +30,9 @@
 // midf = f16(mid / scale)), down on midf, and a reduce that adds
 // w * (f16(v) * scale) per slot in slot order with an f16 rounding after
 // every add.
-// The weight types and strides are read from the table on the device; every
-// expert of a layer must share one type per role.
+// The weight types and strides are read from the table on the device, per
+// expert; gate and up share a type.  Layers whose types vary from expert to
+// expert take the VALU kernels, whose row GEMV switches on each expert's types.
 #include "gemv_core.hpp"
 #include "krk_mi355x.h"
 

@@ -316,8 +316,9 @@ def build_moe(krk, torch, dt, ne, n_embd, n_ff, seed):
     keep = []
     for e in range(ne):
         ent = krk.MoeEntry()
+        dte = dt[e % len(dt)] if isinstance(dt, list) else dt   # a list: types per expert
         for m, (o, i) in enumerate(((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff))):
-            dtm = dt if isinstance(dt, int) else dt[m]
+            dtm = dte if isinstance(dte, int) else dte[m]
             q = make_weights(krk, dtm, o, i, seed=seed + 3 * e + m)
             mats[m, e] = q
             t = dev(torch, q)
@@ -373,6 +374,35 @@ def test_moe_mixed_roles(krk, torch_cuda, be32, n_tok):
     ref = O.moe_ffn(x, [mats[0, e] for e in range(ne)], [mats[1, e] for e in range(ne)],
                     [mats[2, e] for e in range(ne)], dt, ids, wts, n_ff)
     assert rel(host(out), ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("n_tok", [1, 5, 70])
+def test_moe_types_vary_across_experts(krk, torch_cuda, be32, n_tok):
+    """The table carries a type per expert and matrix (moe_table.hpp:47):
+    experts of one layer in different formats, gate = up per expert.  The
+    reference: each routed expert's FFN by the oracle's GEMV in that
+    expert's types, added per token in ascending expert id."""
+    torch = torch_cuda
+    types = [(O.Q4_K, O.Q4_K, O.Q6_K), (O.Q8_0, O.Q8_0, O.Q4_0), (O.Q6_K, O.Q6_K, O.Q4_K),
+             (O.IQ4_NL, O.IQ4_NL, O.Q8_0), (O.Q5_K, O.Q5_K, O.Q5_K)]
+    ne, n_embd, n_ff, k = 8, 512, 768, 3
+    mats, table, keep = build_moe(krk, torch, types, ne, n_embd, n_ff, seed=1300)
+    logits = krk.synth_normal(n_tok * ne, seed=1301).reshape(n_tok, ne)
+    ids, wts = O.router_topk(O.router_softmax(logits), k)
+    x = krk.synth_normal(n_tok * n_embd, seed=1302).reshape(n_tok, n_embd)
+    say("moe types per expert", n_tok)
+    out = torch.empty((n_tok, n_embd), dtype=torch.float32, device="cuda")
+    be32.moe_dispatch(table, 0, ne, dev(torch, ids), dev(torch, wts), dev(torch, x), out, n_tok,
+                      n_embd, n_ff, k)
+    be32.sync()
+    ref = np.zeros((n_tok, n_embd))
+    for t in range(n_tok):
+        for e, s in sorted((int(ids[t, s]), s) for s in range(k)):
+            tg, tu, td = types[e % len(types)]
+            g = O.gemm(tg, mats[0, e], x[t], n_ff)[0]
+            u = O.gemm(tu, mats[1, e], x[t], n_ff)[0]
+            ref[t] += float(wts[t, s]) * O.gemm(td, mats[2, e], O.silu_mul(g, u), n_embd)[0]
+    assert rel(host(out), ref.astype(np.float32)) <= GEMV_TOL
 
 
 def f16_ulps(a, b):
