@@ -32,8 +32,7 @@ extern "C" {
  * this path.  include/krk/quant.hpp:16-47.  Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K, IQ4_NL, IQ4_XS,
  * MXFP4 and unquantized F16 / BF16 weights (16-byte aligned) are served by
  * the dequant, GEMV (rows 1..8, exact prefill) and MFMA GEMM paths, and by
- * moe_dispatch as expert banks (any served type per expert and matrix,
- * gate and up of one type);
+ * moe_dispatch as expert banks (any served type per expert and matrix);
  * the int8 rung takes Q8_0, Q4_K, Q5_K and Q6_K. */
 enum krk_dtype {
     KRK_DT_F32 = 0,
@@ -200,8 +199,8 @@ int krk_router_topk(krk_backend *b, const void *probs, int64_t n_rows,
  * f32 [n_tok, k] device arrays.
  * The first call for a (table, layer, n_expert, n_embd, n_ff) reads that
  * layer's entries back once and validates every one: all three matrices
- * present, of a served type (gate and up alike; types may vary from expert
- * to expert), n_out / n_in equal to the layer's geometry, row_bytes equal to
+ * present, of a served type (types may vary from expert to expert and
+ * between matrices), n_out / n_in equal to the layer's geometry, row_bytes equal to
  * krk_dtype_row_bytes(type, n_in), rows aligned for the type's loads.  Later
  * calls with the same key launch without a host round trip (and can be
  * graph-captured), so a table's layer must not change while the handle

@@ -484,11 +484,10 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
         uniform = b->moe_ok[hit].uniform;
     } else {
         // every bank of the layer: present, of a served type with its rows
-        // aligned for that type's loads, gate and up of one type, the
-        // layer's geometry; whether all rows start 16-byte aligned, and
-        // whether every expert has expert 0's types (the matrix-core paths
-        // take uniform Q4_K layers; the VALU kernels read each expert's
-        // types from the table)
+        // aligned for that type's loads, the layer's geometry; whether all
+        // rows start 16-byte aligned, and whether every expert has expert
+        // 0's types with gate = up (the matrix-core paths take uniform Q4_K
+        // layers; the VALU kernels read each expert's types from the table)
         std::vector<krk_moe_entry> ents(static_cast<size_t>(n_expert));
         hipError_t he = hipMemcpyAsync(ents.data(), tab + static_cast<int64_t>(layer) * n_expert,
                                        sizeof(krk_moe_entry) * ents.size(), hipMemcpyDeviceToHost, b->stream);
@@ -510,11 +509,9 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
                                 (weight_align(en.type[m]) - 1)))
                     return fail(b, KRK_ERR_ARG, "moe_dispatch: expert %d matrix %d rows under-aligned for type %d",
                                 e, m, en.type[m]);
-                // gate and up alike (the expert kernels decode up with the
-                // gate's type); the types may vary from expert to expert
-                if (en.type[1] != en.type[0])
-                    return fail(b, KRK_ERR_UNSUPPORTED, "moe_dispatch: expert %d gate and up of different types", e);
-                if (en.type[m] != e0.type[m]) uniform = false;
+                // the types may vary from expert to expert and between gate
+                // and up
+                if (en.type[m] != e0.type[m] || en.type[1] != en.type[0]) uniform = false;
                 if (reinterpret_cast<uintptr_t>(en.p[m]) & 15) aligned = false;
                 // the kernels step every bank's rows by its type's row size
                 if (en.row_bytes[m] != krk_dtype_row_bytes(en.type[m], en.n_in[m]))

@@ -31,8 +31,9 @@
 // w * (f16(v) * scale) per slot in slot order with an f16 rounding after
 // every add.
 // The weight types and strides are read from the table on the device, per
-// expert; gate and up share a type.  Layers whose types vary from expert to
-// expert take the VALU kernels, whose row GEMV switches on each expert's types.
+// expert and matrix.  Layers whose types vary from expert to expert, or whose
+// gate and up types differ, take the VALU kernels, whose row GEMV switches on
+// each expert's types.
 #include "gemv_core.hpp"
 #include "krk_mi355x.h"
 
@@ -196,6 +197,41 @@ __device__ __forceinline__ float gate_act(float g, float u) {
     }
 }
 
+// Gate rows n0 .. n0 + RB/2 - 1 of an expert into acc[.][0, RB/2) and the
+// same up rows into acc[.][RB/2, RB): one pass when gate and up share a type
+// (each weight unit's activations loaded once for both), two otherwise.
+template <typename XT, int MR, int RB>
+__device__ __forceinline__ void gate_up_rows(const krk_moe_entry &en, int64_t n_ff, int n_embd,
+                                             const XT *const (&xr)[MR], int64_t n0, float (&acc)[MR][RB]) {
+    const uint8_t *wg = static_cast<const uint8_t *>(en.p[KRK_MOE_GATE]);
+    const uint8_t *wu = static_cast<const uint8_t *>(en.p[KRK_MOE_UP]);
+    if (en.type[KRK_MOE_GATE] == en.type[KRK_MOE_UP]) {
+        switch (en.type[KRK_MOE_GATE]) {
+            KRK_MOE_TYPES(KRK_MOE_ROWS, (XT, MR, RB), (wg, en.row_bytes[0], n_ff, n_embd, xr, n0, wu, acc))
+            default: break;
+        }
+        return;
+    }
+    constexpr int H = RB / 2;
+    float h[MR][H];
+    switch (en.type[KRK_MOE_GATE]) {
+        KRK_MOE_TYPES(KRK_MOE_ROWS, (XT, MR, H), (wg, en.row_bytes[0], n_ff, n_embd, xr, n0, nullptr, h))
+        default: break;
+    }
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int r = 0; r < H; r++) acc[m][r] = h[m][r];
+    switch (en.type[KRK_MOE_UP]) {
+        KRK_MOE_TYPES(KRK_MOE_ROWS, (XT, MR, H), (wu, en.row_bytes[1], n_ff, n_embd, xr, n0, nullptr, h))
+        default: break;
+    }
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int r = 0; r < H; r++) acc[m][H + r] = h[m][r];
+}
+
 // -------------------------------------------------------------- gate/up ----
 template <typename XT, int MR, int RB>
 __global__ void __launch_bounds__(512) moe_gu_kernel(const krk_moe_entry *__restrict__ tab,
@@ -220,12 +256,7 @@ __global__ void __launch_bounds__(512) moe_gu_kernel(const krk_moe_entry *__rest
             xr[m] = pass + m < np ? xn + static_cast<int64_t>(w.plan_tok[p0 + pass + m]) * n_embd
                                   : nullptr;
         float acc[MR][RB];
-        const uint8_t *wg = static_cast<const uint8_t *>(en.p[KRK_MOE_GATE]);
-        const uint8_t *wu = static_cast<const uint8_t *>(en.p[KRK_MOE_UP]);
-        switch (en.type[KRK_MOE_GATE]) {
-            KRK_MOE_TYPES(KRK_MOE_ROWS, (XT, MR, RB), (wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc))
-            default: break;
-        }
+        gate_up_rows<XT, MR, RB>(en, n_ff, static_cast<int>(n_embd), xr, n0, acc);
         float v[MR * RB];
 #pragma unroll
         for (int m = 0; m < MR; m++)
@@ -417,12 +448,7 @@ __global__ void __launch_bounds__(512) moe_gu1_kernel(const krk_moe_entry *__res
         const krk_moe_entry &en = tab[e];
         const XT *xr[1] = {xn};
         float acc[1][RB];
-        const uint8_t *wg = static_cast<const uint8_t *>(en.p[KRK_MOE_GATE]);
-        const uint8_t *wu = static_cast<const uint8_t *>(en.p[KRK_MOE_UP]);
-        switch (en.type[KRK_MOE_GATE]) {
-            KRK_MOE_TYPES(KRK_MOE_ROWS, (XT, 1, RB), (wg, en.row_bytes[0], n_ff, (int)n_embd, xr, n0, wu, acc))
-            default: break;
-        }
+        gate_up_rows<XT, 1, RB>(en, n_ff, static_cast<int>(n_embd), xr, n0, acc);
         float v[RB];
 #pragma unroll
         for (int r = 0; r < RB; r++) v[r] = acc[0][r];

@@ -356,12 +356,14 @@ def test_moe_dispatch_parity(krk, torch_cuda, be32, n_tok, dt):
     assert e <= GEMV_TOL
 
 
+@pytest.mark.parametrize("dt", [(O.Q4_K, O.Q4_K, O.Q6_K), (O.Q6_K, O.Q4_K, O.Q8_0)])
 @pytest.mark.parametrize("n_tok", [1, 5, 70])
-def test_moe_mixed_roles(krk, torch_cuda, be32, n_tok):
-    """A Q4_K_M-style layer: Q4_K gate / up with Q6_K down (the VALU expert
-    path; the digit-plane paths take all-Q4_K layers only)."""
+def test_moe_mixed_roles(krk, torch_cuda, be32, n_tok, dt):
+    """A Q4_K_M-style layer (Q4_K gate / up with Q6_K down), and gate and up
+    of different types (two row passes per expert): the VALU expert path;
+    the matrix-core paths take all-Q4_K layers only."""
     torch = torch_cuda
-    dt, ne, n_embd, n_ff, k = (O.Q4_K, O.Q4_K, O.Q6_K), 8, 512, 1024, 4
+    ne, n_embd, n_ff, k = 8, 512, 1024, 4
     mats, table, keep = build_moe(krk, torch, dt, ne, n_embd, n_ff, seed=980)
     logits = krk.synth_normal(n_tok * ne, seed=99).reshape(n_tok, ne)
     ids, wts = O.router_topk(O.router_softmax(logits), k)
@@ -414,7 +416,7 @@ def f16_ulps(a, b):
     return np.abs(ia - ib)
 
 
-@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q8_0, O.Q5_K, O.IQ4_XS, O.MXFP4])
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q8_0, O.Q5_K, O.IQ4_XS, O.MXFP4, (O.Q6_K, O.Q4_K, O.Q8_0)])
 @pytest.mark.parametrize("n_tok", [1, 5, 70])
 def test_moe_dispatch_f16_activations(krk, torch_cuda, be16, n_tok, dt):
     """f16 activations (the reference GPU backend's own act_type) follow its
