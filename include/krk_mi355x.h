@@ -190,6 +190,29 @@ int krk_router_topk(krk_backend *b, const void *probs, int64_t n_rows,
                     int n_expert, int k, void *ids, void *wts, int normalize,
                     float scale);
 
+/* Backend::scan_accum -- backend.hpp:955-972; backend_hip.hip:2455-2471.
+ * Folds one layer's routing into cumulative device histograms (never
+ * cleared here): hits u32 and mass f32, both [n_layer * n_expert];
+ * hits[layer * n_expert + id] += 1 for every routed pair (ids int32
+ * [n_rows, k], ids outside [0, n_expert) skipped) and
+ * mass[layer * n_expert + e] += sum over rows of probs[row, e] (probs f32
+ * [n_rows, n_expert]), one add per expert and call.  n_expert <= 1024. */
+int krk_scan_accum_supported(const krk_backend *b);
+int krk_scan_accum(krk_backend *b, const void *probs, const void *ids,
+                   int64_t n_rows, int n_expert, int k, int layer, void *hits,
+                   void *mass);
+
+/* Backend::moe_plan_build -- backend.hpp:976-980; backend_hip.hip:2473-2485.
+ * The layer's expert plan from device ids int32 [n_rows, k]: off int32
+ * [n_expert + 1] prefix offsets; rows int32 and wt f32 [n_rows * k] in
+ * expert-major order, each expert's pairs in (row, slot) order: rows[at] =
+ * the pair's row, wt[at] = wts[pair] (0 when wts is null).  Entries past
+ * off[n_expert] (dropped pairs) are not written.  n_expert <= 1024 (the
+ * reference fills experts below 256 only). */
+int krk_moe_plan_build(krk_backend *b, const void *ids, int64_t n_rows, int k,
+                       int n_expert, void *off, void *rows, void *wt,
+                       const void *wts);
+
 /* Backend::moe_dispatch -- backend.hpp:1001-1009; backend_hip.hip:2494-2660.
  * The whole routed-expert FFN of one layer from device ids/wts through the
  * device table (table[layer * n_expert + e]):

@@ -61,6 +61,9 @@ SIGNATURES = {
     "krk_router_softmax": (_i32, [_vp, _vp, _vp, _i64, _i32]),
     "krk_router_topk_supported": (_i32, [_vp]),
     "krk_router_topk": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp, _vp, _i32, _f32]),
+    "krk_scan_accum_supported": (_i32, [_vp]),
+    "krk_scan_accum": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _vp]),
+    "krk_moe_plan_build": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp]),
     "krk_moe_dispatch_supported": (_i32, [_vp]),
     "krk_moe_table_forget": (_i32, [_vp, _vp]),
     "krk_moe_dispatch": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _i64, _i64,
@@ -263,6 +266,18 @@ class Backend:
         self._check(lib().krk_router_topk(self._h, _ptr(probs), n_rows, n_expert, k,
                                           _ptr(ids), _ptr(wts), int(normalize), scale),
                     "router_topk")
+
+    def scan_accum(self, probs, ids, n_rows: int, n_expert: int, k: int, layer: int, hits, mass):
+        """Fold one layer's routing into the device histograms hits (u32) and
+        mass (f32), both [n_layer, n_expert] (Backend::scan_accum)."""
+        self._check(lib().krk_scan_accum(self._h, _ptr(probs), _ptr(ids), n_rows, n_expert, k, layer,
+                                         _ptr(hits), _ptr(mass)), "scan_accum")
+
+    def moe_plan_build(self, ids, n_rows: int, k: int, n_expert: int, off, rows, wt, wts=None):
+        """The expert-major plan of the routed pairs (Backend::moe_plan_build)."""
+        self._check(lib().krk_moe_plan_build(self._h, _ptr(ids), n_rows, k, n_expert, _ptr(off),
+                                             _ptr(rows), _ptr(wt), _ptr(wts) if wts is not None else None),
+                    "moe_plan_build")
 
     def moe_dispatch(self, table, layer: int, n_expert: int, ids, wts, xn, out,
                      n_tok: int, n_embd: int, n_ff: int, k: int):

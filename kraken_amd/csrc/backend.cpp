@@ -450,6 +450,34 @@ int krk_router_topk(krk_backend *b, const void *probs, int64_t n_rows, int n_exp
     return e == hipSuccess ? KRK_OK : hip_fail(b, e, "router_topk");
 }
 
+int krk_scan_accum_supported(const krk_backend *b) { return b ? 1 : 0; }
+
+int krk_scan_accum(krk_backend *b, const void *probs, const void *ids, int64_t n_rows, int n_expert, int k,
+                   int layer, void *hits, void *mass) {
+    if (!b) return KRK_ERR_ARG;
+    if (!probs || !ids || !hits || !mass || n_rows <= 0 || n_expert <= 0 || n_expert > 1024 || k <= 0 ||
+        layer < 0 || n_rows > (int64_t(1) << 30))
+        return fail(b, KRK_ERR_ARG, "scan_accum: bad arguments");
+    if (int s = make_current(b)) return s;
+    const hipError_t e = krk::scan_accum(static_cast<const float *>(probs), static_cast<const int32_t *>(ids), n_rows,
+                                         n_expert, k, layer, static_cast<unsigned *>(hits),
+                                         static_cast<float *>(mass), b->stream);
+    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "scan_accum");
+}
+
+int krk_moe_plan_build(krk_backend *b, const void *ids, int64_t n_rows, int k, int n_expert, void *off,
+                       void *rows, void *wt, const void *wts) {
+    if (!b) return KRK_ERR_ARG;
+    if (!ids || !off || !rows || !wt || n_rows <= 0 || k <= 0 || n_expert <= 0 || n_expert > 1024 ||
+        n_rows * k > (int64_t(1) << 30))
+        return fail(b, KRK_ERR_ARG, "moe_plan_build: bad arguments");
+    if (int s = make_current(b)) return s;
+    const hipError_t e = krk::moe_plan_build(static_cast<const int32_t *>(ids), n_rows, k, n_expert,
+                                             static_cast<int32_t *>(off), static_cast<int32_t *>(rows),
+                                             static_cast<float *>(wt), static_cast<const float *>(wts), b->stream);
+    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "moe_plan_build");
+}
+
 int krk_moe_dispatch_supported(const krk_backend *b) { return b ? 1 : 0; }
 
 int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert, const void *ids,

@@ -128,6 +128,10 @@ hipError_t router_softmax(const void *logits, bool act_f16, float *probs, int64_
                           int n_expert, hipStream_t st);
 hipError_t router_topk(const float *probs, int64_t n_rows, int n_expert, int k, int32_t *ids,
                        float *wts, int normalize, float scale, hipStream_t st);
+hipError_t moe_plan_build(const int32_t *ids, int64_t n_rows, int k, int n_expert, int32_t *off,
+                          int32_t *rows, float *wt, const float *wts, hipStream_t st);
+hipError_t scan_accum(const float *probs, const int32_t *ids, int64_t n_rows, int n_expert, int k, int layer,
+                      unsigned *hits, float *mass, hipStream_t st);
 
 struct MoeArgs {
     const void *table;   // krk_moe_entry[n_layer * n_expert]

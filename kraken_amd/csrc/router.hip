@@ -158,4 +158,96 @@ hipError_t router_topk(const float *probs, int64_t n_rows, int n_expert, int k, 
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------ plan ----
+// Backend::moe_plan_build (backend.hpp:976-980; backend_hip.hip:2473-2485,
+// router.hpp:241-275): off[n_expert + 1] prefix offsets of the routed pairs
+// per expert; rows / wt [n_rows * k] in expert-major order, each expert's
+// pairs in (token, slot) order -- rows[at] = the pair's token, wt[at] its
+// weight (0 without wts).  The order is prescribed, so the fill is stable:
+// chunks of 256 pairs in order, a pair's place = its expert's cursor + the
+// number of earlier pairs of the chunk with the same expert.  One workgroup.
+__global__ void __launch_bounds__(256) plan_build_kernel(const int32_t *__restrict__ ids, int64_t P, int k,
+                                                          int ne, int32_t *__restrict__ off,
+                                                          int32_t *__restrict__ rows, float *__restrict__ wt,
+                                                          const float *__restrict__ wts) {
+    __shared__ int32_t cur[1024];
+    __shared__ int32_t ce[256];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < ne; e += 256) cur[e] = 0;
+    __syncthreads();
+    for (int64_t i = tid; i < P; i += 256) {
+        const int e = ids[i];
+        if (e >= 0 && e < ne) atomicAdd(&cur[e], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {   // exclusive scan: off, and each expert's cursor
+        int run = 0;
+        for (int e = 0; e < ne; e++) {
+            const int c = cur[e];
+            off[e] = run;
+            cur[e] = run;
+            run += c;
+        }
+        off[ne] = run;
+    }
+    __syncthreads();
+    for (int64_t c0 = 0; c0 < P; c0 += 256) {
+        const int64_t i = c0 + tid;
+        const int e = i < P ? ids[i] : -1;
+        const bool live = e >= 0 && e < ne;
+        ce[tid] = live ? e : -1;
+        __syncthreads();
+        if (live) {
+            int rank = 0;
+            for (int j = 0; j < tid; j++) rank += ce[j] == e;
+            const int at = cur[e] + rank;
+            rows[at] = static_cast<int32_t>(i / k);
+            wt[at] = wts ? wts[i] : 0.0f;
+        }
+        __syncthreads();
+        if (live) atomicAdd(&cur[e], 1);
+        __syncthreads();
+    }
+}
+
+hipError_t moe_plan_build(const int32_t *ids, int64_t n_rows, int k, int n_expert, int32_t *off,
+                          int32_t *rows, float *wt, const float *wts, hipStream_t st) {
+    if (n_expert > 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(plan_build_kernel, dim3(1), dim3(256), 0, st, ids, n_rows * k, k, n_expert, off, rows,
+                       wt, wts);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------ routing scan ----
+// Backend::scan_accum (backend.hpp:955-972; router.hpp:222-239): fold one
+// layer's routing into the caller's cumulative histograms, hits[layer *
+// n_expert + id] += 1 per routed pair and mass[layer * n_expert + e] += the
+// expert's probability summed over the rows (in row order, then one atomic
+// add per expert and call).  One thread per expert; the pairs are counted
+// by a grid-stride loop.
+__global__ void __launch_bounds__(256) scan_accum_kernel(const float *__restrict__ probs,
+                                                          const int32_t *__restrict__ ids, int64_t n, int ne,
+                                                          int k, int64_t base, unsigned *__restrict__ hits,
+                                                          float *__restrict__ mass) {
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g < ne) {
+        float s = 0.0f;
+        for (int64_t t = 0; t < n; t++) s += probs[t * ne + g];
+        if (s != 0.0f) atomicAdd(&mass[base + g], s);
+    }
+    const int64_t pairs = n * k, stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = g; i < pairs; i += stride) {
+        const int id = ids[i];
+        if (id >= 0 && id < ne) atomicAdd(&hits[base + id], 1u);
+    }
+}
+
+hipError_t scan_accum(const float *probs, const int32_t *ids, int64_t n_rows, int n_expert, int k, int layer,
+                      unsigned *hits, float *mass, hipStream_t st) {
+    const int64_t blocks = (n_expert + 255) / 256;
+    hipLaunchKernelGGL(scan_accum_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, probs, ids,
+                       n_rows, n_expert, k, static_cast<int64_t>(layer) * n_expert, hits, mass);
+    return hipGetLastError();
+}
+
 }  // namespace krk

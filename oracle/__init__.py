@@ -214,6 +214,55 @@ def router_topk(probs: np.ndarray, k: int, normalize: bool = True,
     return ids, wts
 
 
+def moe_plan_build(ids, n_expert: int, wts=None, cursor_experts: int | None = None):
+    """Backend::moe_plan_build's plan (router.hpp:241-275): off [n_expert + 1]
+    prefix counts of the routed pairs per expert; rows / wt [n * k] in
+    expert-major order, each expert's pairs in (row, slot) order, row = pair
+    index // k, wt = the pair's weight (0 without wts).  Entries past
+    off[n_expert] are left as -1 / NaN here (the reference leaves them
+    unwritten).  cursor_experts: the reference's fill keeps cursors for
+    experts below 256 only (router.hpp:263-268); pass 256 to restate that,
+    None to fill every expert.  Pure integer work: numpy loops."""
+    ids = np.ascontiguousarray(np.atleast_2d(ids), dtype=np.int32)
+    n, k = ids.shape
+    flat = ids.reshape(-1)
+    off = np.zeros(n_expert + 1, np.int32)
+    for e in flat:
+        if 0 <= e < n_expert:
+            off[e + 1] += 1
+    off = np.cumsum(off).astype(np.int32)
+    rows = np.full(n * k, -1, np.int32)
+    wt = np.full(n * k, np.nan, np.float32)
+    cursor = off[:-1].copy()
+    w = None if wts is None else np.ascontiguousarray(wts, dtype=np.float32).reshape(-1)
+    for i, e in enumerate(flat):
+        if not (0 <= e < n_expert) or (cursor_experts is not None and e >= cursor_experts):
+            continue
+        at = cursor[e]
+        cursor[e] += 1
+        rows[at] = i // k
+        wt[at] = 0.0 if w is None else w[i]
+    return off, rows, wt
+
+
+def scan_accum(probs, ids, n_expert: int, layer: int, hits, mass):
+    """Backend::scan_accum (router.hpp:222-239), in place on host copies:
+    hits[layer * n_expert + id] += 1 per routed pair; mass[layer * n_expert + e]
+    += the f32 sum over rows, in row order, of probs[row, e] (skipped when
+    that sum is 0)."""
+    probs = np.ascontiguousarray(np.atleast_2d(probs), dtype=np.float32)
+    base = layer * n_expert
+    s = np.zeros(n_expert, np.float32)
+    for t in range(probs.shape[0]):
+        s = (s + probs[t]).astype(np.float32)
+    for e in range(n_expert):
+        if s[e] != 0.0:
+            mass[base + e] = np.float32(mass[base + e] + s[e])
+    for e in np.ascontiguousarray(ids, dtype=np.int32).reshape(-1):
+        if 0 <= e < n_expert:
+            hits[base + e] += 1
+
+
 def moe_ffn(x, gate, up, down, wt, ids, wts, n_ff, nthreads: int = 8):
     """x f32 [n_tok, n_embd]; gate/up/down: lists of per-expert uint8 arrays;
     wt one weight type or a (gate, up, down) triple."""

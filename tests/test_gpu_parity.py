@@ -407,6 +407,56 @@ def test_moe_types_vary_across_experts(krk, torch_cuda, be32, n_tok):
     assert rel(host(out), ref.astype(np.float32)) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("n_rows,k,ne,drop", [(1, 8, 128, 0), (70, 8, 128, 5), (16, 4, 256, 3),
+                                               (300, 6, 300, 0)])
+def test_moe_plan_build(krk, torch_cuda, be32, rng, n_rows, k, ne, drop):
+    """Backend::moe_plan_build against the oracle: offsets, rows and weights
+    in expert-major, then (row, slot) order, bit for bit; dropped pairs (id -1)
+    leave the tail unwritten.  300 experts: every expert is placed (the
+    reference's cursors stop at 256, router.hpp:263-268)."""
+    torch = torch_cuda
+    ids = np.stack([rng.choice(ne, size=k, replace=False) for _ in range(n_rows)]).astype(np.int32)
+    if drop:
+        ids.reshape(-1)[rng.choice(ids.size, size=drop, replace=False)] = -1
+    wts = rng.random((n_rows, k), dtype=np.float32)
+    want_off, want_rows, want_wt = O.moe_plan_build(ids, ne, wts)
+    P = n_rows * k
+    off = torch.full((ne + 1,), -7, dtype=torch.int32, device="cuda")
+    rows = torch.full((P,), -1, dtype=torch.int32, device="cuda")
+    wt = torch.full((P,), float("nan"), dtype=torch.float32, device="cuda")
+    be32.moe_plan_build(dev(torch, ids), n_rows, k, ne, off, rows, wt, dev(torch, wts))
+    be32.sync()
+    n = int(want_off[-1])
+    assert np.array_equal(host(off), want_off)
+    assert np.array_equal(host(rows)[:n], want_rows[:n]) and (host(rows)[n:] == -1).all()
+    assert np.array_equal(host(wt)[:n], want_wt[:n])
+    be32.moe_plan_build(dev(torch, ids), n_rows, k, ne, off, rows, wt, None)
+    be32.sync()
+    assert (host(wt)[:n] == 0.0).all()
+
+
+def test_scan_accum(krk, torch_cuda, be32, rng):
+    """Backend::scan_accum against the oracle: two layers, two calls on one
+    (the histograms accumulate), dropped ids skipped; hits exact and mass
+    bit-equal (each expert's sum runs in row order, one add per call)."""
+    torch = torch_cuda
+    ne, k, n_layer = 128, 8, 3
+    hits_h = np.zeros(n_layer * ne, np.uint32)
+    mass_h = np.zeros(n_layer * ne, np.float32)
+    hits = dev(torch, hits_h.view(np.int32))
+    mass = dev(torch, mass_h)
+    for layer, n_rows, seed in ((1, 16, 1), (1, 5, 2), (2, 70, 3)):
+        logits = krk.synth_normal(n_rows * ne, seed=1400 + seed).reshape(n_rows, ne)
+        probs = O.router_softmax(logits)
+        ids, _ = O.router_topk(probs, k)
+        ids[0, 0] = -1
+        be32.scan_accum(dev(torch, probs), dev(torch, ids), n_rows, ne, k, layer, hits, mass)
+        O.scan_accum(probs, ids, ne, layer, hits_h, mass_h)
+    be32.sync()
+    assert np.array_equal(host(hits).view(np.uint32), hits_h)
+    assert np.array_equal(host(mass), mass_h)
+
+
 def f16_ulps(a, b):
     """Distance in f16 steps between two float16 arrays (same-sign finite)."""
     ia = a.view(np.int16).astype(np.int32)

@@ -579,3 +579,39 @@ def test_kquant_int8_fold(dt):
             fn = ref.ref_dot_q4_K_q8 if dt == O.Q4_K else ref.ref_dot_q6_K_q8
             r = np.float32(fn(O._p(w), O._p(xq), O._p(dx), n))
             assert abs(float(got) - float(r)) <= 1e-6 * scale
+
+
+def test_moe_plan_build_closed_form():
+    """The plan of router.hpp:241-275 worked by hand: three rows of two slots,
+    a dropped id (-1) and an id past n_expert skipped, pairs of one expert in
+    (row, slot) order, and the reference's cursor limit of 256 experts."""
+    ids = np.array([[3, 1], [1, 0], [3, -1], [3, 9]], np.int32)
+    wts = np.array([[0.5, 0.25], [0.125, 1.0], [2.0, 4.0], [8.0, 16.0]], np.float32)
+    off, rows, wt = O.moe_plan_build(ids, 4, wts)
+    assert off.tolist() == [0, 1, 3, 3, 6]
+    assert rows[:6].tolist() == [1, 0, 1, 0, 2, 3]
+    assert wt[:6].tolist() == [1.0, 0.25, 0.125, 0.5, 2.0, 8.0]
+    assert (rows[6:] == -1).all()
+    _, _, wt0 = O.moe_plan_build(ids, 4)
+    assert (wt0[:6] == 0.0).all()
+    # experts from 256 up are counted but, with the reference's cursors, not placed
+    big = np.array([[280, 5], [5, 280]], np.int32)
+    off, rows, _ = O.moe_plan_build(big, 300, cursor_experts=256)
+    assert off[300] == 4 and off[6] == 2 and off[281] == 4
+    assert rows[:2].tolist() == [0, 1] and (rows[2:] == -1).all()
+    _, rows_all, _ = O.moe_plan_build(big, 300)
+    assert rows_all.tolist() == [0, 1, 0, 1]
+
+
+def test_scan_accum_closed_form():
+    """router.hpp:222-239 by hand: hits count routed pairs per (layer,
+    expert), mass adds each expert's probability summed over the rows; both
+    accumulate across calls and layers."""
+    probs = np.array([[0.5, 0.25, 0.25], [0.125, 0.875, 0.0]], np.float32)
+    ids = np.array([[0, 1], [1, -1]], np.int32)
+    hits = np.zeros(2 * 3, np.uint32)
+    mass = np.zeros(2 * 3, np.float32)
+    O.scan_accum(probs, ids, 3, 1, hits, mass)
+    O.scan_accum(probs, ids, 3, 1, hits, mass)
+    assert hits.tolist() == [0, 0, 0, 2, 4, 0]
+    assert mass.tolist() == [0, 0, 0, 1.25, 2.25, 0.5]
