@@ -543,9 +543,10 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
         const int64_t resident = 256LL * (32 / waves_per_wg);
         return dim3(static_cast<unsigned>(want < resident ? want : resident));
     };
-    // Q4_K banks with f32 activations, any token count: both stages on the
-    // digit-plane kernel (int8 matrix cores), the routed banks resolved on
-    // the device, one group of workgroups per token.
+    // The per-token tables (one token on the streaming kernel; token groups
+    // on the digit kernel where the expert-major runs below do not apply),
+    // the routed banks resolved on the device, one group of workgroups per
+    // token:
     //   gate/up: one segment per slot, mid[t * k + s] = silu(g) * u;
     //   down:    one GEMV per token over its k slots concatenated, the
     //            routing weights folded into the activation scales, written
