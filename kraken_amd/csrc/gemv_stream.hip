@@ -41,6 +41,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kTab = 768;   // digit bytes per 256-value block: 8 sub-blocks x 3 planes x 32
 constexpr int kMaxWaves = 16;
+constexpr int kStreamRows = 4;   // dense Q4_K launches of up to this many activation rows
 
 __device__ __forceinline__ v4i lds_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
@@ -95,8 +96,13 @@ __device__ __forceinline__ void load_x8(const _Float16 *p, float (&v)[8]) {
 // it reads and whose routing weight scales its activations); 3 and 4
 // expert-major runs (gate/up pairs, down): grid row a = active expert
 // em_runs[a], its weights loaded once and applied to each of its rows in turn
-template <int DT, typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWEXACT, int MOE = 0, int LA = 8>
+template <int DT, typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWEXACT, int MOE = 0, int LA = 8,
+          int XR = 1>
 __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kernel(SegTable t) {
+    // XR: activation rows (dense Q4_K launches of 2..4 rows): every row's
+    // activations load before the weights, one digit table per row, each
+    // weight group decoded once and multiplied against every row
+    static_assert(XR == 1 || (MOE == 0 && DT == DT_Q4_K), "several rows: dense Q4_K");
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr bool Q40 = DT == DT_Q4_0;
     constexpr bool Q80 = DT == DT_Q8_0;
@@ -172,8 +178,8 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     // 8 (l & 3) .. + 7 of the slice's sub-block 16 p + l / 4
     // the loads issue at raised wave priority, so a wave that is still
     // issuing wins the vector-memory port over one that is already decoding
-    float xv[NPASS][8];
-    auto load_xrow = [&](const XT *xr) {
+    float xvr[XR][NPASS][8];
+    auto load_xrow_to = [&](const XT *xr, float (&xv)[NPASS][8]) {
 #pragma unroll
         for (int p = 0; p < NPASS; p++) {
             const int sbw = p * 16 + (lane >> 2);
@@ -185,8 +191,11 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
             }
         }
     };
+    auto load_xrow = [&](const XT *xr) { load_xrow_to(xr, xvr[0]); };
     __builtin_amdgcn_s_setprio(3);
     load_xrow(row_x(pb));
+#pragma unroll
+    for (int xr = 1; xr < XR; xr++) load_xrow_to(x + xr * t.x_stride, xvr[xr]);
     // ---- then every weight byte of the wave's slice of the tile: group i =
     // (row group rg, block b), lane (c16, gq) takes of row rg * 16 + c16:
     //   Q4_K: the 16-byte header and code bytes 16 gq .. + 15 of each
@@ -257,14 +266,27 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     // ---- the digit table of the slice (this wave's own LDS), layout
     // [block][sub-block][plane][32 bytes], {2^-e, sum x} per sub-block, and
     // for Q6_K the exact integer sums of X over each 16-value half (int bits)
-    uint8_t *tab = lds + wv * (NBW * kTab);
-    float2 *ex = reinterpret_cast<float2 *>(lds + nw * (NBW * kTab)) + wv * (NBW * 8);
+    // (several rows: the LDS holds XR times the tables, {2^-e, sum x}
+    // arrays and partial sums, row by row)
+    const int rstride = nw * (NBW * kTab + 2 * NBW * 8 * static_cast<int>(sizeof(float2))) + 32 * nw * 4;
+    auto tab_of = [&](int xr) { return lds + xr * rstride + wv * (NBW * kTab); };
+    auto ex_of = [&](int xr) {
+        return reinterpret_cast<float2 *>(lds + xr * rstride + nw * (NBW * kTab)) + wv * (NBW * 8);
+    };
+    auto red_of = [&](int xr) {
+        return reinterpret_cast<float *>(lds + xr * rstride + nw * (NBW * kTab + 2 * NBW * 8 * sizeof(float2)));
+    };
+    uint8_t *tab = tab_of(0);
+    float2 *ex = ex_of(0);
     float2 *ex16 = reinterpret_cast<float2 *>(lds + nw * (NBW * kTab)) + nw * (NBW * 8) + wv * (NBW * 8);
-    float *red = reinterpret_cast<float *>(lds + nw * (NBW * kTab + 2 * NBW * 8 * sizeof(float2)));
+#pragma unroll
+    for (int xr = 0; xr < XR; xr++) {
+    uint8_t *tab = tab_of(xr);
+    float2 *ex = ex_of(xr);
 #pragma unroll
     for (int p = 0; p < NPASS; p++) {
         const int sbw = p * 16 + (lane >> 2);
-        const float *v = xv[p];
+        const float *v = xvr[xr][p];
         float amax = 0.0f, sum = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
@@ -321,6 +343,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
             if (sbw < 8 * NBW && (lane & 3) == 0) ex16[sbw] = float2{__int_as_float(xsum), __int_as_float(xsum_hi)};
         }
     }
+    }   // activation rows
 
     // (expert-major runs: the next row's activations load while this one
     // is multiplied)
@@ -339,9 +362,16 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     float acc[RG];
 #pragma unroll
     for (int rg = 0; rg < RG; rg++) acc[rg] = 0.0f;
+    float accx[XR > 1 ? XR - 1 : 1][RG];   // activation rows 1..
+#pragma unroll
+    for (int xr = 0; xr < (XR > 1 ? XR - 1 : 1); xr++)
+#pragma unroll
+        for (int rg = 0; rg < RG; rg++) accx[xr][rg] = 0.0f;
     // two-block slices read their A operands once, before the first group
     // lands (wider slices read them per group: registers)
-    constexpr bool HOLD = NBW == 2 && !Q6 && MOE < 3;   // (expert-major runs keep their weights live across rows: registers)
+    // (expert-major runs keep their weights live across rows, several
+    // activation rows need the registers too)
+    constexpr bool HOLD = NBW == 2 && !Q6 && MOE < 3 && XR == 1;
     v4i HA[HOLD ? NBW : 1][4];
     float2 HE[HOLD ? NBW : 1][2];
     if constexpr (HOLD) {
@@ -518,41 +548,60 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
         const float sc0 = static_cast<float>(s1 & 63u), m0 = static_cast<float>(s2 & 63u);
         const float sc1 = static_cast<float>((s3 & 15u) | ((s1 >> 2) & 0x30u));
         const float m1 = static_cast<float>(((s3 >> 4) & 15u) | ((s2 >> 2) & 0x30u));
-        v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0l, B0l, Z, 0, 0, 0);
-        C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0h, B0h, C0, 0, 0, 0);
-        v4i C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1l, B1l, Z, 0, 0, 0);
-        C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1h, B1h, C1, 0, 0, 0);
-        // lane (c16, gq): C rows 4 gq .. 4 gq + 2 are sub-block gq's (C0) and
-        // 4 + gq's (C1) three plane sums for weight row c16
-        const int S0 = C0[0] + (C0[1] << 8) + (C0[2] << 16);
-        const int S1 = C1[0] + (C1[1] << 8) + (C1[2] << 16);
-        float a = acc[rg];
-        a = __builtin_fmaf(d * sc0, ex0.x * static_cast<float>(S0), a);
-        a = __builtin_fmaf(-dmin * m0, ex0.y, a);
-        a = __builtin_fmaf(d * sc1, ex1.x * static_cast<float>(S1), a);
-        a = __builtin_fmaf(-dmin * m1, ex1.y, a);
-        acc[rg] = a;
+        // one activation row's digit planes against the group's codes
+        auto row_dot = [&](const v4i &a0l, const v4i &a1l, const v4i &a0h, const v4i &a1h, const float2 &e0,
+                           const float2 &e1, float a) {
+            v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0l, B0l, Z, 0, 0, 0);
+            C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0h, B0h, C0, 0, 0, 0);
+            v4i C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1l, B1l, Z, 0, 0, 0);
+            C1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1h, B1h, C1, 0, 0, 0);
+            // lane (c16, gq): C rows 4 gq .. 4 gq + 2 are sub-block gq's (C0)
+            // and 4 + gq's (C1) three plane sums for weight row c16
+            const int S0 = C0[0] + (C0[1] << 8) + (C0[2] << 16);
+            const int S1 = C1[0] + (C1[1] << 8) + (C1[2] << 16);
+            a = __builtin_fmaf(d * sc0, e0.x * static_cast<float>(S0), a);
+            a = __builtin_fmaf(-dmin * m0, e0.y, a);
+            a = __builtin_fmaf(d * sc1, e1.x * static_cast<float>(S1), a);
+            a = __builtin_fmaf(-dmin * m1, e1.y, a);
+            return a;
+        };
+        acc[rg] = row_dot(A0l, A1l, A0h, A1h, ex0, ex1, acc[rg]);
+#pragma unroll
+        for (int xr = 1; xr < XR; xr++) {
+            const uint8_t *tx = tab_of(xr) + b * kTab + a_off;
+            const float2 *ey = ex_of(xr);
+            accx[xr - 1][rg] = row_dot(a_lo ? lds_v4i(tx) : Z, a_lo ? lds_v4i(tx + 384) : Z, a_hi ? lds_v4i(tx) : Z,
+                                       a_hi ? lds_v4i(tx + 384) : Z, ey[b * 8 + gq], ey[b * 8 + 4 + gq],
+                                       accx[xr - 1][rg]);
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
 
     // ---- the waves' partial sums -> LDS [row][wave]; one thread per output
     // row adds them in wave order
 #pragma unroll
+    for (int xr = 0; xr < XR; xr++) {
+    float *red = red_of(xr);
+#pragma unroll
     for (int rg = 0; rg < RG; rg++) {
         // the sum over the four 16-lane rows by the cross-row swaps (VALU,
         // no LDS): a swap of v with itself leaves rows (0, 0, 2, 2) in one
         // result and (1, 1, 3, 3) in the other (16-lane swap), or (0, 1, 0,
         // 1) and (2, 3, 2, 3) (32-lane swap)
-        float v = acc[rg];
+        float v = xr == 0 ? acc[rg] : accx[XR > 1 ? xr - 1 : 0][rg];
         const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
         v = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
         const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
         v = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
         if (gq == 0) red[(rg * 16 + c16) * nw + wv] = v;
     }
+    }
     __syncthreads();
-    const int r = static_cast<int>(threadIdx.x);
-    if (r >= rows_t || n0 + r >= n_out) continue;
+    for (int oi = static_cast<int>(threadIdx.x); oi < rows_t * XR; oi += static_cast<int>(blockDim.x)) {
+    const int xr = XR == 1 ? 0 : oi / rows_t;
+    const int r = oi - xr * rows_t;
+    if (n0 + r >= n_out) continue;
+    const float *red = red_of(xr);
     auto row_sum = [&](int rr) {
         float v = 0.0f;
 #pragma unroll
@@ -560,7 +609,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
             if (k < nw) v += red[rr * nw + k];
         return v;
     };
-    OT *o = outp + (MOE >= 3 ? static_cast<int64_t>(pr) * t.em_orow : 0) + n0 + r;
+    OT *o = outp + (MOE >= 3 ? static_cast<int64_t>(pr) * t.em_orow : 0) + xr * t.out_stride + n0 + r;
     if (kind == SEG_SILU) {
         const float gs = row_sum(r), us = row_sum(16 + r);
         if constexpr (sizeof(OT) == 2) {
@@ -576,6 +625,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
         const float inv = kind == SEG_ACC && t.rexp ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
         store_out<OT>(o, row_sum(r), kind, inv);
     }
+    }   // output rows
     }
 }
 
@@ -584,44 +634,44 @@ size_t stream_lds(int nw, int nbw) {
     return static_cast<size_t>(nw) * nbw * (kTab + 2 * 8 * sizeof(float2)) + 32 * static_cast<size_t>(nw) * sizeof(float);
 }
 
-template <int DT, typename XT, typename OT, int NBW, int TR, int MOE>
+template <int DT, typename XT, typename OT, int NBW, int TR, int MOE, int XR = 1>
 hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
-    const size_t l = stream_lds(nw, NBW);
+    const size_t l = XR * stream_lds(nw, NBW);
     const dim3 grid(static_cast<unsigned>(tiles),
                     static_cast<unsigned>(MOE == 2 ? 1 : MOE >= 3 ? t.em_max_items : t.n));
     if (nw == 8)
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, true, MOE>), grid, dim3(64 * nw), l, st, t);
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, true, MOE, 8, XR>), grid, dim3(64 * nw), l, st, t);
     else if (nw < 8)
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, false, MOE>), grid, dim3(64 * nw), l, st, t);
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, false, MOE, 8, XR>), grid, dim3(64 * nw), l, st, t);
     else if (nw == kMaxWaves)
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, true, MOE>), grid, dim3(64 * nw), l, st,
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, true, MOE, 8, XR>), grid, dim3(64 * nw), l, st,
                            t);
     else
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, false, MOE>), grid, dim3(64 * nw), l,
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, false, MOE, 8, XR>), grid, dim3(64 * nw), l,
                            st, t);
     return hipGetLastError();
 }
 
-template <int DT, typename XT, typename OT, int NBW>
+template <int DT, typename XT, typename OT, int NBW, int XR = 1>
 hipError_t launch_tr(const SegTable &t, int tr, int64_t tiles, int nw, hipStream_t st) {
     if constexpr (NBW == 2) {
         switch (tr) {
-            case 20: return launch<DT, XT, OT, NBW, 20, 0>(t, tiles, nw, st);
-            case 24: return launch<DT, XT, OT, NBW, 24, 0>(t, tiles, nw, st);
-            case 28: return launch<DT, XT, OT, NBW, 28, 0>(t, tiles, nw, st);
-            case 32: return launch<DT, XT, OT, NBW, 32, 0>(t, tiles, nw, st);
+            case 20: return launch<DT, XT, OT, NBW, 20, 0, XR>(t, tiles, nw, st);
+            case 24: return launch<DT, XT, OT, NBW, 24, 0, XR>(t, tiles, nw, st);
+            case 28: return launch<DT, XT, OT, NBW, 28, 0, XR>(t, tiles, nw, st);
+            case 32: return launch<DT, XT, OT, NBW, 32, 0, XR>(t, tiles, nw, st);
             default: break;
         }
     }
-    return launch<DT, XT, OT, NBW, 16, 0>(t, tiles, nw, st);
+    return launch<DT, XT, OT, NBW, 16, 0, XR>(t, tiles, nw, st);
 }
 
-template <int DT, typename XT, typename OT>
+template <int DT, typename XT, typename OT, int XR = 1>
 hipError_t launch_nbw(int nbw, const SegTable &t, int tr, int64_t tiles, int nw, hipStream_t st) {
     switch (nbw) {
-        case 2: return launch_tr<DT, XT, OT, 2>(t, tr, tiles, nw, st);
-        case 3: return launch_tr<DT, XT, OT, 3>(t, tr, tiles, nw, st);
-        default: return launch_tr<DT, XT, OT, 4>(t, tr, tiles, nw, st);
+        case 2: return launch_tr<DT, XT, OT, 2, XR>(t, tr, tiles, nw, st);
+        case 3: return launch_tr<DT, XT, OT, 3, XR>(t, tr, tiles, nw, st);
+        default: return launch_tr<DT, XT, OT, 4, XR>(t, tr, tiles, nw, st);
     }
 }
 
@@ -643,8 +693,10 @@ int device_cus() {
 }
 
 bool gemv_stream_ok(int dt, const SegTable &t) {
-    if ((dt != DT_Q4_K && dt != DT_Q6_K && dt != DT_Q4_0 && dt != DT_Q8_0) || t.rows != 1 || t.em_items)
+    if ((dt != DT_Q4_K && dt != DT_Q6_K && dt != DT_Q4_0 && dt != DT_Q8_0) || t.rows < 1 || t.em_items)
         return false;
+    // several activation rows: dense Q4_K, up to kStreamRows, rows 16-byte aligned
+    if (t.rows > 1 && (dt != DT_Q4_K || t.rows > kStreamRows || t.moe_tab || t.x_stride % 4)) return false;
     if (t.moe_tab) {
         if (dt != DT_Q4_K || t.n_in % 256 || t.row_bytes % 16) return false;
         const int nb = t.n_in / 256, nbw = stream_nbw(nb);
@@ -681,6 +733,8 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
     int64_t rows = 0;
     for (int i = 0; i < t.n; i++) rows += t.seg[i].n_out;
     const int nw = (t.n_in / 256 + nbw - 1) / nbw;
+    // (several rows: their digit tables within the default 64 KB of LDS)
+    if (t.rows > 1 && t.rows * stream_lds(nw, nbw) > 65536) return false;
     if (rows > 2 * 32 * static_cast<int64_t>(device_cus()) * (nw <= 8 ? 2 : 1)) return false;
     for (int i = 0; i < t.n; i++) {
         const Seg &s = t.seg[i];
@@ -777,6 +831,18 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
         return act_f16 ? launch_nbw<DT_Q8_0, _Float16, _Float16>(nbw, t, tr, width, nw, st)
                        : launch_nbw<DT_Q8_0, float, float>(nbw, t, tr, width, nw, st);
 
+    switch (t.rows) {
+        case 2:
+            return act_f16 ? launch_nbw<DT_Q4_K, _Float16, _Float16, 2>(nbw, t, tr, width, nw, st)
+                           : launch_nbw<DT_Q4_K, float, float, 2>(nbw, t, tr, width, nw, st);
+        case 3:
+            return act_f16 ? launch_nbw<DT_Q4_K, _Float16, _Float16, 3>(nbw, t, tr, width, nw, st)
+                           : launch_nbw<DT_Q4_K, float, float, 3>(nbw, t, tr, width, nw, st);
+        case 4:
+            return act_f16 ? launch_nbw<DT_Q4_K, _Float16, _Float16, 4>(nbw, t, tr, width, nw, st)
+                           : launch_nbw<DT_Q4_K, float, float, 4>(nbw, t, tr, width, nw, st);
+        default: break;
+    }
     return act_f16 ? launch_nbw<DT_Q4_K, _Float16, _Float16>(nbw, t, tr, width, nw, st)
                    : launch_nbw<DT_Q4_K, float, float>(nbw, t, tr, width, nw, st);
 }

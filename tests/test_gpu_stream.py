@@ -89,3 +89,28 @@ def test_stream_groups(krk, torch_cuda, be32, be16, dt):
     prod = O.gemm(dt, w, xh.astype(np.float32), n_out)[0]
     want = base.astype(np.float32) + prod.astype(np.float16).astype(np.float32) * 0.5
     assert rel(host(dst)[0].astype(np.float32), want) <= 1e-3
+
+
+@pytest.mark.parametrize("rows", [2, 3, 4])
+@pytest.mark.parametrize("n_out,n_in", [(17, 512), (300, 2304), (14336, 4096), (4096, 11008), (77, 14336)])
+def test_stream_rows(krk, torch_cuda, be32, be16, rows, n_out, n_in):
+    """Dense Q4_K launches of 2..4 activation rows on the streaming kernel:
+    one digit table per row, every weight group multiplied against each
+    row; f32 rows at the 1e-5 bar, f16 rows within their rounding."""
+    torch = torch_cuda
+    w = make_weights(krk, O.Q4_K, n_out, n_in, seed=900 + rows)
+    x = krk.synth_normal(rows * n_in, seed=901 + n_in).reshape(rows, n_in)
+    say("stream rows", rows, n_out, n_in)
+    out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    be32.gemm(out, dev(torch, x), dev(torch, w), O.Q4_K, n_out, n_in, rows)
+    be32.sync()
+    ref = O.gemm(O.Q4_K, w, x, n_out, nthreads=16)
+    for r in range(rows):
+        assert rel(host(out)[r], ref[r]) <= GEMV_TOL, r
+    xh = x.astype(np.float16)
+    out16 = torch.full((rows, n_out), float("nan"), dtype=torch.float16, device="cuda")
+    be16.gemm(out16, dev(torch, xh), dev(torch, w), O.Q4_K, n_out, n_in, rows)
+    be16.sync()
+    ref16 = O.gemm(O.Q4_K, w, xh.astype(np.float32), n_out, nthreads=16)
+    for r in range(rows):
+        assert rel(host(out16)[r].astype(np.float32), ref16[r]) <= 2.0 ** -11 + GEMV_TOL, r
