@@ -1,13 +1,16 @@
-// gemv_stream.hip -- one-row decode GEMV for Q4_K and Q6_K weights with every
-// byte of a workgroup's tile requested in its first instructions.
+// gemv_stream.hip -- decode GEMV (one activation row; dense Q4_K also two to
+// four) for Q4_K, Q6_K, Q4_0 and Q8_0 weights with every byte of a
+// workgroup's tile requested in its first instructions, and the routed
+// expert modes of the MoE dispatch built on it.
 //
 // The products run on the int8 matrix cores exactly as in gemv_digits.hip:
 // the weight codes are the B operand, the activations enter as three exact
 // int8 digit planes per 32-value sub-block, and the block formula (Q4_K:
 // src/quant.cpp:427-447; Q6_K: 491-512, the code offset 32 applied through
-// the exact integer sums of x) is applied once per (row, sub-block or scale
-// group) to the exact plane sums.  What differs is the data movement, which sets the time of a
-// decode GEMV far more than the arithmetic does:
+// the exact integer sums of x; Q4_0: 331-339; Q8_0: 381-387) is applied once
+// per (row, sub-block or scale group) to the exact plane sums.  What differs
+// is the data movement, which sets the time of a decode GEMV far more than
+// the arithmetic does:
 //
 //   * A workgroup owns one tile of up to 32 rows over all of K; its waves
 //     split K into contiguous slices of NBW blocks.  A wave loads its x slice
