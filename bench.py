@@ -340,10 +340,70 @@ def summarize_pmc(fetch_csv, write_csv):
             "hbm_bytes_per_launch": gf + gw}
 
 
+# Labels of the default bench's launches for the trace summary: (substring
+# of the kernel name, grid size, configuration, work per launch, unit of the
+# work: "B" algorithmic bytes, "f16" / "int8" 2 M N K operations, or None).
+_Q4K_ROW, _Q6K_ROW, _Q8_ROW = 2304, 3360, 4352
+_HEAD_BYTES = 14336 * _Q4K_ROW + 4 * (4096 + 14336)
+TRACE_LABELS = [
+    ("gemv_stream_kernel<12, float, float, 2, 28, 8, true, 0, 8>", "262144",
+     "C3 headline: Q4_K GEMV 4096->14336, M=1, f32 activations", _HEAD_BYTES, "B"),
+    ("gemv_stream_kernelILi12EDF16_DF16_Li2ELi28", "262144", "C3 headline shape, f16 activations",
+     14336 * _Q4K_ROW + 2 * (4096 + 14336), "B"),
+    ("gemv_stream_kernel<2, float, float, 2, 28", "262144", "Q4_0 GEMV 4096->14336, M=1", _HEAD_BYTES, "B"),
+    ("gemv_stream_kernel<8, float, float, 2, 28", "262144", "Q8_0 GEMV 4096->14336, M=1",
+     14336 * _Q8_ROW + 4 * (4096 + 14336), "B"),
+    ("gemv_stream_kernel<14, float, float, 2, 28", "262144", "Q6_K GEMV 4096->14336, M=1",
+     14336 * _Q6K_ROW + 4 * (4096 + 14336), "B"),
+    ("probe_read_kernel", "524288", "read ceiling: pure read of the headline's weight bytes",
+     14336 * _Q4K_ROW, "B"),
+    ("gemv_stream_kernel<12, float, float, 2, 16, 8, true, 0, 8>", "131072",
+     "C2 layer: q, k, v, o (Q4_K 4096->4096)", 4096 * _Q4K_ROW + 4 * 8192, "B"),
+    ("gemv_stream_kernel<12, float, float, 2, 24, 8, true, 0, 8>", "235008",
+     "C2 layer: gate, up (Q4_K 4096->11008)", 11008 * _Q4K_ROW + 4 * (4096 + 11008), "B"),
+    ("gemv_stream_kernel<12, float, float, 3, 16, 16, false, 0, 8>", "245760",
+     "C2 layer: down (Q4_K 11008->4096)", 4096 * 6192 + 4 * (4096 + 11008), "B"),
+    ("gemv_stream_kernel<12, float, float, 2, 28, 8, true, 0, 8>", "75264",
+     "C2 grouped: q/k/v in one launch (3 segments)", None, None),
+    ("gemv_stream_kernel<12, float, float, 2, 32, 8, true, 0, 8>", "352256",
+     "C2 grouped: gate+up with the SiLU epilogue", None, None),
+    ("gemv_digits_kernel<14, float, float, 16", "131072", "C4 head: Q6_K 128256x4096, row split",
+     128256 * _Q6K_ROW + 4 * (4096 + 128256), "B"),
+    ("gemv_valu_kernel<8, float, float, 2, 2, true>", "131072", "C4 head: Q8_0 128256x4096, VALU stream kernel",
+     128256 * _Q8_ROW + 4 * (4096 + 128256), "B"),
+    ("gemv_stream_kernel<12, float, float, 2, 32, 8, true, 1, 8>", "49152", "C5 x1: routed gate/up, 8 slots",
+     None, None),
+    ("gemv_stream_kernel<12, float, float, 3, 16, 16, true, 2, 8>", "262144", "C5 x1: routed down over the 8 slots",
+     None, None),
+    ("gemv_stream_kernel<12, float, float, 2, 32, 8, true, 3, 8>", "49152",
+     "C5 x16: expert-major gate/up (about 83 experts x 7.08 MB)", None, None),
+    ("gemv_stream_kernel<12, float, float, 2, 16, 8, false, 4, 8>", "49152",
+     "C5 x16: expert-major down (about 83 experts x 3.54 MB)", None, None),
+    ("moe_plan_kernel", "256", "C5 x16: plan", None, None),
+    ("moe_reduce_kernel<float>", "4096", "C5 x16: ordered reduce", None, None),
+    ("gemm_f16_kernelILi12EDF16", "229376", "C3 prefill up, M=2048 (448 tiles)", 2 * 2048 * 14336 * 4096, "f16"),
+    ("gemm_f16_kernelILi12EDF16", "65536", "C3 prefill down, M=2048 (128 tiles x split 2)",
+     2 * 2048 * 14336 * 4096, "f16"),
+    ("splitk_reduce_kernelIDF16", "8388608", "C3 prefill down, M=2048: split-K reduce", None, None),
+    ("gemm_f16_kernelILi12EDF16", "57344", "C3 prefill up, M=512 (112 tiles x split 2)",
+     2 * 512 * 14336 * 4096, "f16"),
+    ("splitk_reduce_kernelIDF16", "7340032", "C3 prefill up, M=512: split-K reduce", None, None),
+    ("gemm_f16_kernelILi12EDF16", "16384", "C3 prefill down, M=512 (32 tiles x split 4)",
+     2 * 512 * 14336 * 4096, "f16"),
+    ("splitk_reduce_kernelIDF16", "2097152", "C3 prefill down, M=512: split-K reduce", None, None),
+    ("gemm_i8_kernelILi8EDF16", "458752", "int8 rung: Q8_0 4096->14336, M=2048", 2 * 2048 * 14336 * 4096, "int8"),
+    ("quantize_q8_kernelIDF16", "262144", "int8 rung, M=2048: activation quantizer", None, None),
+    ("gemm_i8_kernelILi8EDF16", "114688", "int8 rung: Q8_0 4096->14336, M=512", 2 * 512 * 14336 * 4096, "int8"),
+    ("quantize_q8_kernelIDF16", "65536", "int8 rung, M=512: activation quantizer", None, None),
+]
+
+
 def summarize_trace(path):
-    """Average device duration per (kernel, grid, workgroup): each bench
-    configuration launches its kernel with its own grid, so every row is one
-    configuration's kernel."""
+    """Average device duration per (kernel, grid, workgroup), one row per
+    launch of the default bench (each configuration launches its kernel with
+    its own grid), labelled from TRACE_LABELS with the rate its work implies;
+    this library's launches no label names follow unlabelled.  The last line names the
+    headline's kernel (read back by the bench's roofline)."""
     import csv
     import statistics
     rows = {}
@@ -351,11 +411,34 @@ def summarize_trace(path):
         key = (r["Kernel_Name"], r.get("Grid_Size", r.get("Grid_Size_X", "")),
                r.get("Workgroup_Size", r.get("Workgroup_Size_X", "")))
         rows.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    print("| kernel | grid | block | calls | average (us) | median (us) | min (us) | max (us) |")
+    peaks = {"f16": (2500.0, "TFLOP/s", "f16 peak"), "int8": (5000.0, "TOP/s", "int8 peak")}
+    print("| configuration | kernel | grid | block | calls | average (us) | median (us) | rate from the average |")
     print("|---|---|---|---|---|---|---|---|")
-    for (name, grid, block), d in sorted(rows.items(), key=lambda kv: -sum(kv[1])):
-        print(f"| `{name}` | {grid} | {block} | {len(d)} | {statistics.mean(d):.2f} | "
-              f"{statistics.median(d):.2f} | {min(d):.2f} | {max(d):.2f} |")
+    used, headline = set(), None
+    order = [(lab, [k for k in rows if lab[0] in k[0] and k[1] == lab[1]]) for lab in TRACE_LABELS]
+    for (sub, grid, label, work, unit), hits in order + [((None, None, "", None, None), [k for k in rows if "krk" in k[0]])]:
+        for k in hits:
+            if k in used:
+                continue
+            used.add(k)
+            d = rows[k]
+            avg, med = statistics.mean(d), statistics.median(d)
+            rate = ""
+            if unit == "B":
+                g = work / avg / 1e3
+                rate = f"{g:.0f} GB/s ({100 * g / HBM_PEAK_GBS:.1f}% of HBM)"
+            elif unit in peaks:
+                peak, u, what = peaks[unit]
+                t = work / avg / 1e6
+                rate = f"{t:.0f} {u} ({100 * t / peak:.1f}% of {what})"
+            name = k[0].replace("|", "\\|")
+            print(f"| {label} | `{name}` | {k[1]} | {k[2]} | {len(d)} | {avg:.2f} | {med:.2f} | {rate} |")
+            if headline is None and sub is not None:
+                headline = k[0]
+            if sub is not None:
+                break
+    print()
+    print(f"headline_kernel: {headline}")
 
 
 def summarize_counters(path, cus=256, xcds=8):
