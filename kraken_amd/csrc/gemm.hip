@@ -14,10 +14,12 @@
 //     bank-conflict free;
 //   * the two wave groups run out of phase (ping-pong): one group's MFMAs
 //     overlap the other group's decode and LDS stores, and each thread
-//     fetches the raw bytes of its next step while the other group computes;
+//     fetches the raw bytes of the step after next (two register sets) while
+//     the other group computes;
 //   * tiles are ordered XCD-first: workgroup g runs on XCD g % 8, so the
-//     launch order is remapped to give each XCD a contiguous run of tiles
-//     sharing one activation row-band in its own L2;
+//     launch order is remapped to give each XCD a contiguous run of tiles,
+//     M fastest, so that the workgroups an XCD runs together share a few
+//     weight tiles in its own L2;
 //   * split-K (z dimension) when the tile count cannot fill 256 CUs, with f32
 //     partials summed in a fixed order by a second kernel.
 //
@@ -25,6 +27,8 @@
 // with the host rule (quantize_q8_32_d), v_mfma_i32_32x32x32_i8 per 32-value
 // block, and the block fold acc = fma((f32)isum, d_w * d_x, acc) of
 // dot_q8_0_q8_scalar (src/quant.cpp:3261-3279).
+#include <type_traits>
+
 #include "krk_formats.hpp"
 #include "krk_kernels.hpp"
 
@@ -446,7 +450,7 @@ template <> struct XStage<float> {
 
 // XCD-aware tile order: the hardware hands workgroup g to XCD g % 8.  Give
 // XCD x the contiguous tile range [x*per, (x+1)*per) so its workgroups share
-// activation rows (and weight rows) in that XCD's L2.
+// operand rows in that XCD's L2.
 __device__ __forceinline__ int xcd_remap(int g, int G) {
     const int per = G / 8;
     if (g >= per * 8) return g;  // tail when G is not a multiple of 8
@@ -464,6 +468,17 @@ template <typename XT> struct StepRegs<DT_Q4_K, XT> {
     XStage<XT> x0, x1;
 };
 
+// Whether a (format, activation type) pair keeps two steps of raw bytes in
+// registers without spilling (256 VGPRs at two waves per SIMD; measured on
+// the compiled kernels: the f32-activation staging of the wider formats and
+// the 16-bit-weight and Q3_K stagings do not fit).
+template <int DT, typename XT> constexpr bool deep_prefetch() {
+    if constexpr (std::is_same<XT, float>::value)
+        return !(DT == DT_Q5_K || DT == DT_Q6_K || DT == DT_Q8_0 || DT == DT_Q3_K || DT == DT_F16 ||
+                 DT == DT_BF16);
+    return !(DT == DT_Q3_K || DT == DT_F16);
+}
+
 template <int DT, typename XT, typename OT>
 __global__ void __launch_bounds__(G_THREADS, 1)
     gemm_f16_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const XT *__restrict__ x,
@@ -475,7 +490,8 @@ __global__ void __launch_bounds__(G_THREADS, 1)
 
     const int G = gridDim.x;
     const int g = xcd_remap(static_cast<int>(blockIdx.x), G);
-    const int tm = g / tiles_n, tn = g % tiles_n;
+    const int tiles_m = G / tiles_n;
+    const int tm = g % tiles_m, tn = g / tiles_m;
     const int m0 = tm * GB_M, n0 = tn * GB_N;
     const int kb = static_cast<int>(blockIdx.z) * k_per_split;
     const int ke = min(K, kb + k_per_split);
@@ -590,31 +606,50 @@ __global__ void __launch_bounds__(G_THREADS, 1)
     // of step t into stage t % 2, then fetch step t + 1's raw bytes.  A stage
     // is complete one phase before either group reads it, and rewritten only
     // after both groups have read it.  Both groups pass 2 nk barriers.
-    StepRegs<DT, XT> r;
+    // Raw bytes are double-buffered in registers where the budget allows
+    // (deep_prefetch): group gp keeps step s in set (s + gp) % 2 (ra = 0,
+    // rb = 1), and a step's bytes are requested right after the step two
+    // earlier was staged from the same set, so each load has a full step
+    // (two phases) to land.  In loop iteration t both groups stage from set
+    // (t + 1) % 2, so unrolling the loop by two makes every set choice static
+    // (no register arrays indexed at run time).  Otherwise one set: a step's
+    // bytes are requested after the previous step was staged.
+    constexpr bool DEEP = deep_prefetch<DT, XT>();
+    StepRegs<DT, XT> ra;
+    std::conditional_t<DEEP, StepRegs<DT, XT>, StepRegs<DT, XT> &> rb = ra;
+    constexpr int DIST = DEEP ? 2 : 1;
+    auto stage_fetch = [&](StepRegs<DT, XT> &r, int ms) {
+        stage(r, ms, ms & 1);
+        if (ms + DIST < nk) fetch(r, ms + DIST);
+    };
     if (nk > 0) {
-        fetch(r, 0);
-        stage(r, 0, 0);
-        if (nk > 1) fetch(r, 1);
+        if (DEEP && gp == 1) {
+            fetch(rb, 0);
+            if (nk > 1) fetch(ra, 1);
+            stage_fetch(rb, 0);
+        } else {
+            fetch(ra, 0);
+            if (DEEP && nk > 1) fetch(rb, 1);
+            stage_fetch(ra, 0);
+        }
     }
     __syncthreads();
     if (gp == 1) {
-        if (1 < nk) {
-            stage(r, 1, 1);
-            if (2 < nk) fetch(r, 2);
-        }
+        if (1 < nk) stage_fetch(ra, 1);
         __syncthreads();
     }
-    for (int t = 0; t < nk; t++) {
+    auto iter = [&](StepRegs<DT, XT> &r, int t) {
         __builtin_amdgcn_s_setprio(1);
         mfma_step(t & 1);
         __builtin_amdgcn_s_setprio(0);
         __syncthreads();
         const int ms = t + 1 + gp;
-        if (ms < nk) {
-            stage(r, ms, ms & 1);
-            if (ms + 1 < nk) fetch(r, ms + 1);
-        }
+        if (ms < nk) stage_fetch(r, ms);
         if (t + 1 < nk || gp == 0) __syncthreads();
+    };
+    for (int t = 0; t < nk; t += 2) {
+        iter(rb, t);
+        if (t + 1 < nk) iter(ra, t + 1);
     }
 
     // C fragment: lane holds column j = lane % 32, rows 8*(r/4) + 4*(lane/32) + r%4
