@@ -38,6 +38,7 @@ def parse():
     ap.add_argument("--only", default="", help="comma list of sections: gemm,int8,layer,formats,head,moe "
                     "(the headline GEMV always runs); default all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--moe-tokens", default="1,16", help="comma list of MoE batch sizes to time")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="counter run: 5 plain copies of 256 MiB, then 20 headline GEMVs")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
@@ -161,6 +162,24 @@ def bench_gemm(K, torch, be, timer, dt, M, n_out, n_in, seed, iters=20, warmup=3
     flops = 2.0 * M * n_out * n_in
     return {"ms": ms, "TFLOPs": flops / ms / 1e9, "frac": flops / ms / 1e9 / FP16_PEAK_TFLOPS,
             "M": M, "N": n_out, "K": n_in}
+
+
+def bench_f16_ceiling(torch, be, timer, M, N, K, iters=20, warmup=3):
+    """A plain f16 GEMM at the C3 up shape (krk_probe_gemm) on N(0,1) f16
+    operands -- what dense f16 MFMA work reaches on this part with data like
+    the prefill GEMM's -- and the same kernel with its operands loaded once
+    and re-read from LDS (the matrix cores and LDS alone)."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    x = torch.randn((M, K), dtype=torch.float16, device="cuda", generator=gen)
+    w = torch.randn((N, K), dtype=torch.float16, device="cuda", generator=gen)
+    out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    flops = 2.0 * M * N * K
+    res = {}
+    for loads, nm in ((True, "plain_f16_gemm"), (False, "mfma_lds_skeleton")):
+        ms = timer.run(lambda i: be.probe_gemm(x, w, out, M, N, K, loads), iters, warmup)
+        res[nm] = {"us": ms * 1e3, "TFLOPs": flops / ms / 1e9, "frac_fp16_peak": flops / ms / 1e9 / FP16_PEAK_TFLOPS}
+    return res
 
 
 def q4k_random_rows(torch, n_rows, n_in, gen):
@@ -549,6 +568,11 @@ def main():
                 log(f"  {r['ms'] * 1e3:.1f} us  {r['TFLOPs']:.1f} TFLOP/s  ({100 * r['frac']:.1f}%)")
                 extras[f"prefill_q4k_{name}_m{M}"] = {"us": r["ms"] * 1e3, "TFLOPs": r["TFLOPs"],
                                                       "frac_fp16_peak": r["frac"]}
+        # the f16 ceiling beside it: the same shape with no dequantization
+        log("f16 ceiling at the up shape, M=2048 ...")
+        for nm, r in bench_f16_ceiling(torch, be16, timer, 2048, 14336, 4096).items():
+            extras[f"{nm}_up_m2048"] = r
+            log(f"  {nm}: {r['us']:.1f} us  {r['TFLOPs']:.1f} TFLOP/s  ({100 * r['frac_fp16_peak']:.1f}%)")
 
     if want("int8"):
         # the Q8_0 x Q8 int8 rung at the C3 up shape (KRK_PATH_INT8)
@@ -595,7 +619,7 @@ def main():
             log(f"  head {nm} {r['ms'] * 1e3:.1f} us {r['GBps']:.0f} GB/s")
 
     if want("moe"):
-        for T in (1, 16):
+        for T in (int(v) for v in args.moe_tokens.split(",")):
             log(f"moe C5 n_tok={T} ...")
             r = bench_moe(K, torch, be32, timer, T)
             r["frac_hbm"] = r["GBps"] / HBM_PEAK_GBS
