@@ -375,7 +375,7 @@ def summarize_pmc(fetch_csv, write_csv):
 _Q4K_ROW, _Q6K_ROW, _Q8_ROW = 2304, 3360, 4352
 _HEAD_BYTES = 14336 * _Q4K_ROW + 4 * (4096 + 14336)
 TRACE_LABELS = [
-    ("gemv_stream_kernel<12, float, float, 2, 28, 8, true, 0, 8>", "262144",
+    ("gemv_stream_kernel<12, float, float, 2, 28, 8, true, 0, 8", "262144",
      "C3 headline: Q4_K GEMV 4096->14336, M=1, f32 activations", _HEAD_BYTES, "B"),
     ("gemv_stream_kernelILi12EDF16_DF16_Li2ELi28", "262144", "C3 headline shape, f16 activations",
      14336 * _Q4K_ROW + 2 * (4096 + 14336), "B"),
@@ -386,27 +386,27 @@ TRACE_LABELS = [
      14336 * _Q6K_ROW + 4 * (4096 + 14336), "B"),
     ("probe_read_kernel", "524288", "read ceiling: pure read of the headline's weight bytes",
      14336 * _Q4K_ROW, "B"),
-    ("gemv_stream_kernel<12, float, float, 2, 16, 8, true, 0, 8>", "131072",
+    ("gemv_stream_kernel<12, float, float, 2, 16, 8, true, 0, 8", "131072",
      "C2 layer: q, k, v, o (Q4_K 4096->4096)", 4096 * _Q4K_ROW + 4 * 8192, "B"),
-    ("gemv_stream_kernel<12, float, float, 2, 24, 8, true, 0, 8>", "235008",
+    ("gemv_stream_kernel<12, float, float, 2, 24, 8, true, 0, 8", "235008",
      "C2 layer: gate, up (Q4_K 4096->11008)", 11008 * _Q4K_ROW + 4 * (4096 + 11008), "B"),
-    ("gemv_stream_kernel<12, float, float, 3, 16, 16, false, 0, 8>", "245760",
+    ("gemv_stream_kernel<12, float, float, 3, 16, 16, false, 0, 8", "245760",
      "C2 layer: down (Q4_K 11008->4096)", 4096 * 6192 + 4 * (4096 + 11008), "B"),
-    ("gemv_stream_kernel<12, float, float, 2, 28, 8, true, 0, 8>", "75264",
+    ("gemv_stream_kernel<12, float, float, 2, 28, 8, true, 0, 8", "75264",
      "C2 grouped: q/k/v in one launch (3 segments)", None, None),
-    ("gemv_stream_kernel<12, float, float, 2, 32, 8, true, 0, 8>", "352256",
+    ("gemv_stream_kernel<12, float, float, 2, 32, 8, true, 0, 8", "352256",
      "C2 grouped: gate+up with the SiLU epilogue", None, None),
     ("gemv_digits_kernel<14, float, float, 16", "131072", "C4 head: Q6_K 128256x4096, row split",
      128256 * _Q6K_ROW + 4 * (4096 + 128256), "B"),
     ("gemv_valu_kernel<8, float, float, 2, 2, true>", "131072", "C4 head: Q8_0 128256x4096, VALU stream kernel",
      128256 * _Q8_ROW + 4 * (4096 + 128256), "B"),
-    ("gemv_stream_kernel<12, float, float, 2, 32, 8, true, 1, 8>", "49152", "C5 x1: routed gate/up, 8 slots",
+    ("gemv_stream_kernel<12, float, float, 2, 32, 8, true, 1, 8", "49152", "C5 x1: routed gate/up, 8 slots",
      None, None),
-    ("gemv_stream_kernel<12, float, float, 3, 16, 16, true, 2, 8>", "262144", "C5 x1: routed down over the 8 slots",
+    ("gemv_stream_kernel<12, float, float, 3, 16, 16, true, 2, 8", "262144", "C5 x1: routed down over the 8 slots",
      None, None),
-    ("gemv_stream_kernel<12, float, float, 2, 32, 8, true, 3, 8>", "49152",
+    ("gemv_stream_kernel<12, float, float, 2, 32, 8, true, 3, 8", "49152",
      "C5 x16: expert-major gate/up (about 83 experts x 7.08 MB)", None, None),
-    ("gemv_stream_kernel<12, float, float, 2, 16, 8, false, 4, 8>", "49152",
+    ("gemv_stream_kernel<12, float, float, 2, 16, 8, false, 4, 8", "49152",
      "C5 x16: expert-major down (about 83 experts x 3.54 MB)", None, None),
     ("moe_plan_kernel", "256", "C5 x16: plan", None, None),
     ("moe_reduce_kernel<float>", "4096", "C5 x16: ordered reduce", None, None),
@@ -424,6 +424,14 @@ TRACE_LABELS = [
     ("quantize_q8_kernelIDF16", "262144", "int8 rung, M=2048: activation quantizer", None, None),
     ("gemm_i8_kernelILi8EDF16", "114688", "int8 rung: Q8_0 4096->14336, M=512", 2 * 512 * 14336 * 4096, "int8"),
     ("quantize_q8_kernelIDF16", "65536", "int8 rung, M=512: activation quantizer", None, None),
+    ("probe_gemm_kernelILb1E", "114688", "f16 ceiling: plain f16 GEMM at the up shape, M=2048",
+     2 * 2048 * 14336 * 4096, "f16"),
+    ("probe_gemm_kernel<true>", "114688", "f16 ceiling: plain f16 GEMM at the up shape, M=2048",
+     2 * 2048 * 14336 * 4096, "f16"),
+    ("probe_gemm_kernelILb0E", "114688", "f16 ceiling: its MFMA + LDS skeleton (no global loads)",
+     2 * 2048 * 14336 * 4096, "f16"),
+    ("probe_gemm_kernel<false>", "114688", "f16 ceiling: its MFMA + LDS skeleton (no global loads)",
+     2 * 2048 * 14336 * 4096, "f16"),
 ]
 
 
