@@ -21,6 +21,10 @@ F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS = 0, 1, 2, 8, 12, 13, 14,
 Q2_K, Q3_K, MXFP4 = 10, 11, 39
 Q4_1, Q5_0, Q5_1 = 3, 6, 7
 BF16 = 30
+# formats served through the generic 32-value chunk path
+Q8_1, Q8_K, TQ1_0, TQ2_0, NVFP4 = 9, 15, 34, 35, 40
+ROCMFP4, ROCMFP4_FAST, Q6_0_ROCMFPX, Q3_0_ROCMFPX, Q2_0_ROCMFPX = 100, 101, 102, 104, 107
+CHUNK_FMTS = (Q8_1, Q8_K, TQ1_0, TQ2_0, NVFP4, ROCMFP4, ROCMFP4_FAST, Q6_0_ROCMFPX, Q3_0_ROCMFPX, Q2_0_ROCMFPX)
 
 _vp, _i64, _i32, _f32, _u16 = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_uint16
 

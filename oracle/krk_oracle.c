@@ -90,7 +90,11 @@ int orc_block_size(int dt) {
         case ORC_F32: case ORC_F16: case ORC_BF16: return 1;
         case ORC_Q4_0: case ORC_Q8_0: case ORC_IQ4_NL: case ORC_MXFP4:
         case ORC_Q4_1: case ORC_Q5_0: case ORC_Q5_1: return 32;
+        case ORC_Q8_1: case ORC_ROCMFP4: case ORC_ROCMFP4_FAST: case ORC_Q6_0_ROCMFPX:
+        case ORC_Q3_0_ROCMFPX: case ORC_Q2_0_ROCMFPX: return 32;
+        case ORC_NVFP4: return 64;
         case ORC_Q2_K: case ORC_Q3_K: case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_IQ4_XS: return 256;
+        case ORC_Q8_K: case ORC_TQ1_0: case ORC_TQ2_0: return 256;
         default: return 0;
     }
 }
@@ -110,6 +114,16 @@ int orc_block_bytes(int dt) {
         case ORC_Q5_K: return 176;
         case ORC_IQ4_XS: return 136;
         case ORC_Q6_K: return 210;
+        case ORC_Q8_1: return 36;
+        case ORC_Q8_K: return 292;
+        case ORC_TQ1_0: return 54;
+        case ORC_TQ2_0: return 66;
+        case ORC_NVFP4: return 36;
+        case ORC_ROCMFP4: return 18;
+        case ORC_ROCMFP4_FAST: return 17;
+        case ORC_Q6_0_ROCMFPX: return 26;
+        case ORC_Q3_0_ROCMFPX: return 14;
+        case ORC_Q2_0_ROCMFPX: return 10;
         default: return 0;
     }
 }
@@ -338,6 +352,134 @@ static void deq_q6_k(const uint8_t *b, float *y) {
     }
 }
 
+/* ---- formats served through the generic 32-value chunk path ---------- */
+
+/* src/quant.cpp:389-396: Q8_1 (36 B): f16 d, f16 s, 32 int8 codes; value
+ * d*q + s, the product rounded before the add (unfused in the reference
+ * build, and here: this file is built with -ffp-contract=off). */
+static void deq_q8_1(const uint8_t *b, float *y) {
+    float d = ld_f16(b), s = ld_f16(b + 2);
+    for (int k = 0; k < 32; k++) y[k] = d * (float)(int8_t)b[4 + k] + s;
+}
+
+/* src/quant.cpp:557-564: Q8_K (292 B): f32 d, 256 int8 codes, then 16 int16
+ * block sums the decoder does not read; value d*q. */
+static void deq_q8_k(const uint8_t *b, float *y) {
+    float d;
+    memcpy(&d, b, 4);
+    for (int k = 0; k < 256; k++) y[k] = d * (float)(int8_t)b[4 + k];
+}
+
+/* src/quant.cpp:576-585: a UE4M3 scale byte; 0x00 and 0x7F are 0, bit 7 is
+ * not read; exponent field 0 is man * 2^-9, else (1 + man/8) * 2^(exp-7);
+ * both halved. */
+static float ue4m3(uint8_t x) {
+    if (x == 0 || x == 0x7F) return 0.0f;
+    int e = (x >> 3) & 0xF, m = x & 7;
+    float raw = e == 0 ? ldexpf((float)m, -9) : ldexpf(1.0f + (float)m / 8.0f, e - 7);
+    return raw * 0.5f;
+}
+
+/* src/quant.cpp:661-672: NVFP4 (36 B / 64 values): four UE4M3 scales, then
+ * four 8-byte runs; run s holds values 16s + j (low nibble of byte j) and
+ * 16s + 8 + j (high nibble), on the doubled E2M1 grid. */
+static void deq_nvfp4(const uint8_t *b, float *y) {
+    for (int s = 0; s < 4; s++) {
+        float d = ue4m3(b[s]);
+        const uint8_t *qs = b + 4 + 8 * s;
+        for (int j = 0; j < 8; j++) {
+            y[16 * s + j] = (float)kFp4[qs[j] & 0xF] * d;
+            y[16 * s + j + 8] = (float)kFp4[qs[j] >> 4] * d;
+        }
+    }
+}
+
+/* src/quant.cpp:310-318: the ROCmFP4 code ladder, magnitudes 0, 1, 2, 3, 4,
+ * 6, 8, 10 (the top level is 10, not E2M1's 12), bit 3 the sign. */
+static int rocmfp4_code(int q) {
+    int m = q & 7, mag = m <= 4 ? m : 2 * m - 4;
+    return (q & 8) ? -mag : mag;
+}
+
+/* src/quant.cpp:692-713: ROCmFP4 (18 B): 16 nibble bytes (value j the low
+ * nibble of byte j, j + 16 the high), then the two half scales (UE4M3);
+ * ROCmFP4_FAST (17 B): one scale for all 32. */
+static void deq_rocmfp4(const uint8_t *b, float *y, int two_scales) {
+    float d0 = ue4m3(b[16]), d1 = two_scales ? ue4m3(b[17]) : d0;
+    for (int j = 0; j < 16; j++) {
+        y[j] = (float)rocmfp4_code(b[j] & 0xF) * d0;
+        y[j + 16] = (float)rocmfp4_code(b[j] >> 4) * d1;
+    }
+}
+
+/* src/quant.cpp:740-857: the ROCmFPX 32-value formats, each with two UE4M3
+ * half scales after the codes.  FP2 (10 B): 2-bit codes, four to a byte
+ * from the low bits, on the ladder {-4, -1, 1, 4}.  FP3 (14 B): eight 3-bit
+ * codes per 3 bytes, LSB first; magnitude {0, 1, 2, 4}[c & 3], sign bit 2.
+ * FP6 (26 B): four 6-bit codes per 3 bytes, LSB first; magnitude c & 31,
+ * sign bit 5, and a negative zero is -32. */
+static void deq_rocmfpx2(const uint8_t *b, float *y) {
+    static const int lad[4] = {-4, -1, 1, 4};
+    float d0 = ue4m3(b[8]), d1 = ue4m3(b[9]);
+    for (int j = 0; j < 32; j++) {
+        int c = (b[j / 4] >> (2 * (j % 4))) & 3;
+        y[j] = (float)lad[c] * (j < 16 ? d0 : d1);
+    }
+}
+static void deq_rocmfpx3(const uint8_t *b, float *y) {
+    static const int mag[4] = {0, 1, 2, 4};
+    float d0 = ue4m3(b[12]), d1 = ue4m3(b[13]);
+    for (int j = 0; j < 32; j++) {
+        const uint8_t *g = b + 3 * (j / 8);
+        uint32_t w = (uint32_t)g[0] | ((uint32_t)g[1] << 8) | ((uint32_t)g[2] << 16);
+        int c = (int)((w >> (3 * (j % 8))) & 7);
+        int v = mag[c & 3];
+        y[j] = (float)((c & 4) ? -v : v) * (j < 16 ? d0 : d1);
+    }
+}
+static void deq_rocmfpx6(const uint8_t *b, float *y) {
+    float d0 = ue4m3(b[24]), d1 = ue4m3(b[25]);
+    for (int j = 0; j < 32; j++) {
+        const uint8_t *g = b + 3 * (j / 4);
+        uint32_t w = (uint32_t)g[0] | ((uint32_t)g[1] << 8) | ((uint32_t)g[2] << 16);
+        int c = (int)((w >> (6 * (j % 4))) & 63), m = c & 31;
+        int v = (c & 32) ? -(m == 0 ? 32 : m) : m;
+        y[j] = (float)v * (j < 16 ? d0 : d1);
+    }
+}
+
+/* src/quant.cpp:859-889: TQ1_0 (54 B): base-3 packed trits, five per byte
+ * in qs[0..47] and four per byte in qh[48..51], f16 d at 52.  Trit n of a
+ * byte q is ((uint8)(q * 3^n) * 3) >> 8, minus 1 (the product wraps to a
+ * byte first).  Element v: v < 160 -> byte v % 32, trit v / 32; v < 240 ->
+ * byte 32 + (v - 160) % 16, trit (v - 160) / 16; else byte 48 + (v - 240)
+ * % 4, trit (v - 240) / 4.  Value d * trit. */
+static int tq1_trit(int q, int n) {
+    static const int p3[6] = {1, 3, 9, 27, 81, 243};
+    uint8_t w = (uint8_t)(q * p3[n]);
+    return (int)(((uint16_t)w * 3u) >> 8) - 1;
+}
+static void deq_tq1_0(const uint8_t *b, float *y) {
+    float d = ld_f16(b + 52);
+    for (int v = 0; v < 256; v++) {
+        int t;
+        if (v < 160) t = tq1_trit(b[v % 32], v / 32);
+        else if (v < 240) t = tq1_trit(b[32 + (v - 160) % 16], (v - 160) / 16);
+        else t = tq1_trit(b[48 + (v - 240) % 4], (v - 240) / 4);
+        y[v] = d * (float)t;
+    }
+}
+
+/* src/quant.cpp:907-918: TQ2_0 (66 B): 2-bit codes q in planes, f16 d at
+ * 64; element 128 h + 32 l + m is bits 2l of byte 32 h + m; value d*(q-1). */
+static void deq_tq2_0(const uint8_t *b, float *y) {
+    float d = ld_f16(b + 64);
+    for (int h = 0; h < 2; h++)
+        for (int l = 0; l < 4; l++)
+            for (int m = 0; m < 32; m++)
+                y[128 * h + 32 * l + m] = d * (float)((int)((b[32 * h + m] >> (2 * l)) & 3) - 1);
+}
+
 /* src/quant.cpp:1553-1601 (the formats on this path plus F16). */
 static void dequant_block(int dt, const uint8_t *p, float *buf) {
     switch (dt) {
@@ -361,6 +503,16 @@ static void dequant_block(int dt, const uint8_t *p, float *buf) {
         case ORC_Q4_K: deq_q4_k(p, buf); break;
         case ORC_Q5_K: deq_q5_k(p, buf); break;
         case ORC_Q6_K: deq_q6_k(p, buf); break;
+        case ORC_Q8_1: deq_q8_1(p, buf); break;
+        case ORC_Q8_K: deq_q8_k(p, buf); break;
+        case ORC_NVFP4: deq_nvfp4(p, buf); break;
+        case ORC_ROCMFP4: deq_rocmfp4(p, buf, 1); break;
+        case ORC_ROCMFP4_FAST: deq_rocmfp4(p, buf, 0); break;
+        case ORC_Q2_0_ROCMFPX: deq_rocmfpx2(p, buf); break;
+        case ORC_Q3_0_ROCMFPX: deq_rocmfpx3(p, buf); break;
+        case ORC_Q6_0_ROCMFPX: deq_rocmfpx6(p, buf); break;
+        case ORC_TQ1_0: deq_tq1_0(p, buf); break;
+        case ORC_TQ2_0: deq_tq2_0(p, buf); break;
         default: break;
     }
 }

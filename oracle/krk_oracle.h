@@ -22,7 +22,11 @@ extern "C" {
 enum {
     ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 8,
     ORC_Q2_K = 10, ORC_Q3_K = 11, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_IQ4_NL = 20, ORC_IQ4_XS = 23, ORC_MXFP4 = 39,
-    ORC_Q4_1 = 3, ORC_Q5_0 = 6, ORC_Q5_1 = 7, ORC_BF16 = 30
+    ORC_Q4_1 = 3, ORC_Q5_0 = 6, ORC_Q5_1 = 7, ORC_BF16 = 30,
+    /* include/krk/quant.hpp:25-31, 67-68, 105, 128-129, 166-168 */
+    ORC_Q8_1 = 9, ORC_Q8_K = 15, ORC_TQ1_0 = 34, ORC_TQ2_0 = 35, ORC_NVFP4 = 40,
+    ORC_ROCMFP4 = 100, ORC_ROCMFP4_FAST = 101, ORC_Q6_0_ROCMFPX = 102, ORC_Q3_0_ROCMFPX = 104,
+    ORC_Q2_0_ROCMFPX = 107
 };
 
 float    orc_fp16_to_fp32(uint16_t h);

@@ -38,7 +38,10 @@ def rand_blocks(rng, dt, n_blocks):
         return (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).copy()
     bb = {oracle.Q4_0: 18, oracle.Q8_0: 34, oracle.Q4_K: 144, oracle.Q5_K: 176, oracle.Q6_K: 210,
           oracle.IQ4_NL: 18, oracle.IQ4_XS: 136, oracle.Q2_K: 84, oracle.Q3_K: 110,
-          oracle.MXFP4: 17, oracle.Q4_1: 20, oracle.Q5_0: 22, oracle.Q5_1: 24}[dt]
+          oracle.MXFP4: 17, oracle.Q4_1: 20, oracle.Q5_0: 22, oracle.Q5_1: 24,
+          oracle.Q8_1: 36, oracle.Q8_K: 292, oracle.TQ1_0: 54, oracle.TQ2_0: 66, oracle.NVFP4: 36,
+          oracle.ROCMFP4: 18, oracle.ROCMFP4_FAST: 17, oracle.Q6_0_ROCMFPX: 26, oracle.Q3_0_ROCMFPX: 14,
+          oracle.Q2_0_ROCMFPX: 10}[dt]
     w = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
 
     def setf16(off, scale):
@@ -56,6 +59,18 @@ def rand_blocks(rng, dt, n_blocks):
         setf16(82, 0.01)
     elif dt == oracle.Q3_K:
         setf16(108, 0.01)
+    elif dt == oracle.Q8_1:
+        setf16(0, 0.01)
+        setf16(2, 0.01)
+    elif dt == oracle.Q8_K:
+        d = (rng.standard_normal(n_blocks) * 0.01).astype(np.float32).view(np.uint8).reshape(n_blocks, 4)
+        w[:, 0:4] = d
+    elif dt == oracle.TQ1_0:
+        setf16(52, 0.01)
+    elif dt == oracle.TQ2_0:
+        setf16(64, 0.01)
+    elif dt in oracle.CHUNK_FMTS:
+        pass   # UE4M3 scale bytes: every byte value is finite
     elif dt == oracle.MXFP4:
         # exponent bytes near 2^-7 scale (finite products and sums); every
         # exponent byte is covered by the dequant tests of their own

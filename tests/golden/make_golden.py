@@ -5,7 +5,8 @@ code (oracle/_ref/libkrk_ref.so, compiled by oracle/Makefile from
 The fixture is data only: seeded block bytes and activations (inputs) and
 the reference's outputs for them (Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS, MXFP4, Q4_1, Q5_0, Q5_1:
 dequant_row f32, dequant_row_f16,
-vec_dot in the strict scalar tier, quantize_q8_row, dot_q8_0_q8_scalar).
+vec_dot in the strict scalar tier, quantize_q8_row, dot_q8_0_q8_scalar; and the generic-chunk formats Q8_1, Q8_K, TQ1_0, TQ2_0,
+NVFP4, ROCmFP4, ROCmFP4_FAST and the three ROCmFPX formats).
 It lets the oracle be checked bit for bit where the reference tree is absent
 (the GPU box).  Run:  python tests/golden/make_golden.py
 """
@@ -20,6 +21,10 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 import oracle  # noqa: E402
 from conftest import rand_blocks  # noqa: E402
+
+# the formats served through the generic 32-value chunk path, each from a
+# stream of its own
+CHUNK_GOLDEN = tuple((dt, f"chunk{dt}", 0x5EE000 + dt) for dt in oracle.CHUNK_FMTS)
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "quant_golden.npz")
 
@@ -113,7 +118,8 @@ def main():
     # Q2_K and Q3_K, each from a stream of its own
     for dt, name, seed in ((oracle.Q2_K, "q2_k", 0x5EED2), (oracle.Q3_K, "q3_k", 0x5EED3),
                            (oracle.MXFP4, "mxfp4", 0x5EEDF), (oracle.Q4_1, "q4_1", 0x5EED1),
-                           (oracle.Q5_0, "q5_0", 0x5EED6), (oracle.Q5_1, "q5_1", 0x5EED7)):
+                           (oracle.Q5_0, "q5_0", 0x5EED6), (oracle.Q5_1, "q5_1", 0x5EED7),
+                           *CHUNK_GOLDEN):
         r = np.random.default_rng(seed)
         bs = ref.ref_block_size(dt)
         w = rand_blocks(r, dt, n // bs)

@@ -13,7 +13,7 @@ from conftest import rand_blocks
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_golden.npz")
 FMTS = [O.Q4_0, O.Q8_0, O.Q2_K, O.Q3_K, O.Q4_K, O.Q5_K, O.Q6_K, O.IQ4_NL, O.IQ4_XS, O.MXFP4,
-        O.Q4_1, O.Q5_0, O.Q5_1, O.F16, O.BF16]
+        O.Q4_1, O.Q5_0, O.Q5_1, O.F16, O.BF16, *O.CHUNK_FMTS]
 
 
 def f16bytes(v):
@@ -347,7 +347,7 @@ def test_oracle_matches_golden_vectors():
     for dt, name in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k"), (O.Q5_K, "q5_k"),
                      (O.Q6_K, "q6_k"), (O.IQ4_NL, "iq4_nl"), (O.IQ4_XS, "iq4_xs"), (O.Q2_K, "q2_k"),
                      (O.Q3_K, "q3_k"), (O.MXFP4, "mxfp4"), (O.Q4_1, "q4_1"), (O.Q5_0, "q5_0"),
-                     (O.Q5_1, "q5_1")):
+                     (O.Q5_1, "q5_1"), *((dt, f"chunk{dt}") for dt in O.CHUNK_FMTS)):
         w, x = g[f"{name}_w"], g[f"{name}_x"]
         n = x.size
         deq = O.dequant(dt, w, 1, n)[0]
