@@ -33,7 +33,8 @@ extern "C" {
  * MXFP4 and unquantized F16 / BF16 weights (16-byte aligned) are served by
  * the dequant, GEMV (rows 1..8, exact prefill) and MFMA GEMM paths, and by
  * moe_dispatch as expert banks (any served type per expert and matrix);
- * the int8 rung takes Q8_0, Q4_K, Q5_K and Q6_K. */
+ * the int8 rung takes Q8_0, Q4_K, Q5_K and Q6_K.  The ids after MXFP4 below
+ * take the same operators through a generic 32-value chunk path. */
 enum krk_dtype {
     KRK_DT_F32 = 0,
     KRK_DT_F16 = 1,
@@ -50,7 +51,20 @@ enum krk_dtype {
     KRK_DT_IQ4_NL = 20,
     KRK_DT_IQ4_XS = 23,
     KRK_DT_BF16 = 30,
-    KRK_DT_MXFP4 = 39
+    KRK_DT_MXFP4 = 39,
+    /* served through the generic 32-value chunk path (include/krk/quant.hpp:
+     * 25-31, 67-68, 105, 128-129, 166-168): dequant, GEMV rows 1..8, the MFMA
+     * GEMM and MoE expert banks, at any byte alignment */
+    KRK_DT_Q8_1 = 9,
+    KRK_DT_Q8_K = 15,
+    KRK_DT_TQ1_0 = 34,
+    KRK_DT_TQ2_0 = 35,
+    KRK_DT_NVFP4 = 40,
+    KRK_DT_ROCMFP4 = 100,
+    KRK_DT_ROCMFP4_FAST = 101,
+    KRK_DT_Q6_0_ROCMFPX = 102,
+    KRK_DT_Q3_0_ROCMFPX = 104,
+    KRK_DT_Q2_0_ROCMFPX = 107
 };
 
 /* Activation type of a handle: backend.hpp `act_type()` (F16 on the

@@ -21,15 +21,26 @@ F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_NL, IQ4_XS = 0, 1, 2, 8, 12, 13, 14,
 Q2_K, Q3_K, MXFP4 = 10, 11, 39
 Q4_1, Q5_0, Q5_1 = 3, 6, 7
 BF16 = 30
+# served through the generic 32-value chunk path
+Q8_1, Q8_K, TQ1_0, TQ2_0, NVFP4 = 9, 15, 34, 35, 40
+ROCMFP4, ROCMFP4_FAST, Q6_0_ROCMFPX, Q3_0_ROCMFPX, Q2_0_ROCMFPX = 100, 101, 102, 104, 107
+CHUNK_FMTS = (Q8_1, Q8_K, TQ1_0, TQ2_0, NVFP4, ROCMFP4, ROCMFP4_FAST, Q6_0_ROCMFPX, Q3_0_ROCMFPX, Q2_0_ROCMFPX)
 ACT_F32, ACT_F16 = 0, 1
 PATH_AUTO, PATH_EXACT, PATH_MFMA, PATH_INT8 = 0, 1, 2, 3
 DTYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K",
                IQ4_NL: "IQ4_NL", IQ4_XS: "IQ4_XS", Q2_K: "Q2_K", Q3_K: "Q3_K", MXFP4: "MXFP4",
-               Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1", BF16: "BF16"}
+               Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1", BF16: "BF16", Q8_1: "Q8_1", Q8_K: "Q8_K",
+               TQ1_0: "TQ1_0", TQ2_0: "TQ2_0", NVFP4: "NVFP4", ROCMFP4: "ROCMFP4",
+               ROCMFP4_FAST: "ROCMFP4_FAST", Q6_0_ROCMFPX: "Q6_0_ROCMFPX", Q3_0_ROCMFPX: "Q3_0_ROCMFPX",
+               Q2_0_ROCMFPX: "Q2_0_ROCMFPX"}
 BLOCK_VALUES = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_NL: 32, IQ4_XS: 256,
-                Q2_K: 256, Q3_K: 256, MXFP4: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, F16: 1, BF16: 1}
+                Q2_K: 256, Q3_K: 256, MXFP4: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, F16: 1, BF16: 1,
+                Q8_1: 32, Q8_K: 256, TQ1_0: 256, TQ2_0: 256, NVFP4: 64, ROCMFP4: 32, ROCMFP4_FAST: 32,
+                Q6_0_ROCMFPX: 32, Q3_0_ROCMFPX: 32, Q2_0_ROCMFPX: 32}
 BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136,
-               Q2_K: 84, Q3_K: 110, MXFP4: 17, Q4_1: 20, Q5_0: 22, Q5_1: 24, F16: 2, BF16: 2}
+               Q2_K: 84, Q3_K: 110, MXFP4: 17, Q4_1: 20, Q5_0: 22, Q5_1: 24, F16: 2, BF16: 2,
+               Q8_1: 36, Q8_K: 292, TQ1_0: 54, TQ2_0: 66, NVFP4: 36, ROCMFP4: 18, ROCMFP4_FAST: 17,
+               Q6_0_ROCMFPX: 26, Q3_0_ROCMFPX: 14, Q2_0_ROCMFPX: 10}
 
 _vp, _i64, _i32, _f32, _u64 = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_uint64
 _P = C.POINTER

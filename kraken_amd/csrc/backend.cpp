@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "krk_gguf.h"
+#include "krk_formats.hpp"
 #include "krk_kernels.hpp"
 #include "krk_mi355x.h"
 
@@ -92,6 +93,9 @@ uintptr_t weight_align(int wt) {
         case KRK_DT_IQ4_XS: return 8;
         case KRK_DT_Q2_K: return 4;
         case KRK_DT_MXFP4: return 1;
+        case KRK_DT_Q8_1: case KRK_DT_Q8_K: case KRK_DT_TQ1_0: case KRK_DT_TQ2_0: case KRK_DT_NVFP4:
+        case KRK_DT_ROCMFP4: case KRK_DT_ROCMFP4_FAST: case KRK_DT_Q6_0_ROCMFPX: case KRK_DT_Q3_0_ROCMFPX:
+        case KRK_DT_Q2_0_ROCMFPX: return 1;   // byte loads (the generic chunk path)
         default: return 2;
     }
 }
@@ -100,7 +104,7 @@ bool dtype_on_path(int wt) {
     return wt == KRK_DT_Q4_0 || wt == KRK_DT_Q8_0 || wt == KRK_DT_Q4_K || wt == KRK_DT_Q5_K ||
            wt == KRK_DT_Q6_K || wt == KRK_DT_IQ4_NL || wt == KRK_DT_IQ4_XS || wt == KRK_DT_Q2_K ||
            wt == KRK_DT_Q3_K || wt == KRK_DT_MXFP4 || wt == KRK_DT_Q4_1 || wt == KRK_DT_Q5_0 ||
-           wt == KRK_DT_Q5_1 || wt == KRK_DT_F16 || wt == KRK_DT_BF16;
+           wt == KRK_DT_Q5_1 || wt == KRK_DT_F16 || wt == KRK_DT_BF16 || krk::chunk_fmt(wt);
 }
 
 int make_current(krk_backend *b) {
@@ -196,7 +200,7 @@ int krk_dtype_block_size(int wt) {
         case KRK_DT_Q4_1: case KRK_DT_Q5_0: case KRK_DT_Q5_1: return 32;
         case KRK_DT_Q2_K: case KRK_DT_Q3_K: case KRK_DT_Q4_K: case KRK_DT_Q5_K: case KRK_DT_Q6_K:
         case KRK_DT_IQ4_XS: return 256;
-        default: return 0;
+        default: return krk::chunk_fmt(wt) ? krk::blk_vals(wt) : 0;
     }
 }
 
@@ -216,7 +220,7 @@ int krk_dtype_block_bytes(int wt) {
         case KRK_DT_Q5_1: return 24;
         case KRK_DT_Q3_K: return 110;
         case KRK_DT_Q6_K: return 210;
-        default: return 0;
+        default: return krk::chunk_fmt(wt) ? krk::blk_bytes(wt) : 0;
     }
 }
 

@@ -409,6 +409,35 @@ template <> struct WStage<DT_Q3_K> {
     }
 };
 
+// Generic-chunk formats: the thread keeps its block's address; decode runs
+// the chunk contract and takes its 16-value half.
+template <int DT> struct WStageChunk {
+    const uint8_t *blk;
+    int c, hf;
+    __device__ void fetch(const uint8_t *row, int kt, int h) {
+        constexpr int CPB = blk_vals(DT) / 32;
+        blk = row + static_cast<int64_t>(kt / CPB) * blk_bytes(DT);
+        c = kt % CPB;
+        hf = h;
+    }
+    __device__ void decode(int, _Float16 (&o)[16]) const {
+        float y[32];
+        dequant_chunk<DT>(blk, c, y);
+#pragma unroll
+        for (int i = 0; i < 16; i++) o[i] = static_cast<_Float16>(hf ? y[16 + i] : y[i]);
+    }
+};
+template <> struct WStage<DT_Q8_1> : WStageChunk<DT_Q8_1> {};
+template <> struct WStage<DT_Q8_K> : WStageChunk<DT_Q8_K> {};
+template <> struct WStage<DT_TQ1_0> : WStageChunk<DT_TQ1_0> {};
+template <> struct WStage<DT_TQ2_0> : WStageChunk<DT_TQ2_0> {};
+template <> struct WStage<DT_NVFP4> : WStageChunk<DT_NVFP4> {};
+template <> struct WStage<DT_ROCMFP4> : WStageChunk<DT_ROCMFP4> {};
+template <> struct WStage<DT_ROCMFP4_FAST> : WStageChunk<DT_ROCMFP4_FAST> {};
+template <> struct WStage<DT_Q6_0_ROCMFPX> : WStageChunk<DT_Q6_0_ROCMFPX> {};
+template <> struct WStage<DT_Q3_0_ROCMFPX> : WStageChunk<DT_Q3_0_ROCMFPX> {};
+template <> struct WStage<DT_Q2_0_ROCMFPX> : WStageChunk<DT_Q2_0_ROCMFPX> {};
+
 // ------------------------------------------------------- activation staging
 template <typename XT> struct XStage;
 template <> struct XStage<_Float16> {
@@ -765,6 +794,16 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
         KRK_GEMM_CASE(DT_Q5_1)
         KRK_GEMM_CASE(DT_F16)
         KRK_GEMM_CASE(DT_BF16)
+        KRK_GEMM_CASE(DT_Q8_1)
+        KRK_GEMM_CASE(DT_Q8_K)
+        KRK_GEMM_CASE(DT_TQ1_0)
+        KRK_GEMM_CASE(DT_TQ2_0)
+        KRK_GEMM_CASE(DT_NVFP4)
+        KRK_GEMM_CASE(DT_ROCMFP4)
+        KRK_GEMM_CASE(DT_ROCMFP4_FAST)
+        KRK_GEMM_CASE(DT_Q6_0_ROCMFPX)
+        KRK_GEMM_CASE(DT_Q3_0_ROCMFPX)
+        KRK_GEMM_CASE(DT_Q2_0_ROCMFPX)
         default: return hipErrorInvalidValue;
     }
 #undef KRK_GEMM_CASE

@@ -1379,9 +1379,38 @@ static hipError_t dispatch_mr(SegTable t, hipStream_t st) {
     }
 }
 
+// Generic-chunk formats: the multi-row segment kernel over the chunk lane
+// view, for every row count (no format-specific streaming kernels).
+template <int DT, typename XT, typename OT>
+static hipError_t dispatch_chunk(SegTable t, hipStream_t st) {
+    const int mr = t.rows <= 1 ? 1 : t.rows == 2 ? 2 : 4;
+    const int rb = 8 / mr;
+    int64_t blk = 0;
+    for (int i = 0; i < t.n; i++) {
+        t.seg[i].blk_begin = blk;
+        const int64_t per = t.seg[i].kind == SEG_SILU ? rb / 2 : rb;
+        blk += (t.seg[i].n_out + per - 1) / per;
+    }
+    switch (mr) {
+        case 1: return launch_seg<DT, XT, OT, 1, 8>(t, blk, st);
+        case 2: return launch_seg<DT, XT, OT, 2, 4>(t, blk, st);
+        default: return launch_seg<DT, XT, OT, 4, 2>(t, blk, st);
+    }
+}
+
 template <typename XT, typename OT>
 static hipError_t dispatch_dt(int dt, const SegTable &t, hipStream_t st) {
     switch (dt) {
+        case DT_Q8_1: return dispatch_chunk<DT_Q8_1, XT, OT>(t, st);
+        case DT_Q8_K: return dispatch_chunk<DT_Q8_K, XT, OT>(t, st);
+        case DT_TQ1_0: return dispatch_chunk<DT_TQ1_0, XT, OT>(t, st);
+        case DT_TQ2_0: return dispatch_chunk<DT_TQ2_0, XT, OT>(t, st);
+        case DT_NVFP4: return dispatch_chunk<DT_NVFP4, XT, OT>(t, st);
+        case DT_ROCMFP4: return dispatch_chunk<DT_ROCMFP4, XT, OT>(t, st);
+        case DT_ROCMFP4_FAST: return dispatch_chunk<DT_ROCMFP4_FAST, XT, OT>(t, st);
+        case DT_Q6_0_ROCMFPX: return dispatch_chunk<DT_Q6_0_ROCMFPX, XT, OT>(t, st);
+        case DT_Q3_0_ROCMFPX: return dispatch_chunk<DT_Q3_0_ROCMFPX, XT, OT>(t, st);
+        case DT_Q2_0_ROCMFPX: return dispatch_chunk<DT_Q2_0_ROCMFPX, XT, OT>(t, st);
         case DT_Q4_K: return dispatch_mr<DT_Q4_K, XT, OT>(t, st);
         case DT_Q5_K: return dispatch_mr<DT_Q5_K, XT, OT>(t, st);
         case DT_Q6_K: return dispatch_mr<DT_Q6_K, XT, OT>(t, st);

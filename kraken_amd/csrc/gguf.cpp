@@ -128,6 +128,17 @@ bool geometry(uint32_t id, int *bs, int *bb) {
         case KRK_DT_Q5_1: *bs = 32; *bb = 24; return true;
         case KRK_DT_Q3_K: *bs = 256; *bb = 110; return true;
         case KRK_DT_Q6_K: *bs = 256; *bb = 210; return true;
+        // the generic-chunk formats (include/krk/quant.hpp geometry)
+        case KRK_DT_Q8_1: *bs = 32; *bb = 36; return true;
+        case KRK_DT_Q8_K: *bs = 256; *bb = 292; return true;
+        case KRK_DT_TQ1_0: *bs = 256; *bb = 54; return true;
+        case KRK_DT_TQ2_0: *bs = 256; *bb = 66; return true;
+        case KRK_DT_NVFP4: *bs = 64; *bb = 36; return true;
+        case KRK_DT_ROCMFP4: *bs = 32; *bb = 18; return true;
+        case KRK_DT_ROCMFP4_FAST: *bs = 32; *bb = 17; return true;
+        case KRK_DT_Q6_0_ROCMFPX: *bs = 32; *bb = 26; return true;
+        case KRK_DT_Q3_0_ROCMFPX: *bs = 32; *bb = 14; return true;
+        case KRK_DT_Q2_0_ROCMFPX: *bs = 32; *bb = 10; return true;
         default: return false;
     }
 }

@@ -24,7 +24,11 @@ constexpr int kWave = 64;
 // (include/krk/quant.hpp geometry; src/quant.cpp:1805-1900).
 enum : int { DT_F32 = 0, DT_F16 = 1, DT_Q4_0 = 2, DT_Q8_0 = 8, DT_Q4_K = 12, DT_Q5_K = 13, DT_Q6_K = 14,
              DT_IQ4_NL = 20, DT_IQ4_XS = 23, DT_Q2_K = 10, DT_Q3_K = 11, DT_MXFP4 = 39,
-             DT_Q4_1 = 3, DT_Q5_0 = 6, DT_Q5_1 = 7, DT_BF16 = 30 };
+             DT_Q4_1 = 3, DT_Q5_0 = 6, DT_Q5_1 = 7, DT_BF16 = 30,
+             // served through the generic chunk path (include/krk/quant.hpp:25-31, 67-68, 105,
+             // 128-129, 166-168)
+             DT_Q8_1 = 9, DT_Q8_K = 15, DT_TQ1_0 = 34, DT_TQ2_0 = 35, DT_NVFP4 = 40, DT_ROCMFP4 = 100,
+             DT_ROCMFP4_FAST = 101, DT_Q6_0_ROCMFPX = 102, DT_Q3_0_ROCMFPX = 104, DT_Q2_0_ROCMFPX = 107 };
 
 __device__ __forceinline__ float h2f(uint32_t h16) {
     _Float16 h;

@@ -21,12 +21,22 @@ namespace krk {
 // ---------------------------------------------------------------- geometry --
 // F16 and BF16 weights are handled as 32-value pseudo-blocks of 64 bytes (a
 // row of n values is n / 32 of them), so they ride the same chunk contract.
+// Formats served through the generic chunk path: every kernel reads them
+// through dequant_chunk alone (byte loads, any alignment).
+__host__ __device__ constexpr bool chunk_fmt(int dt) {
+    return dt == DT_Q8_1 || dt == DT_Q8_K || dt == DT_TQ1_0 || dt == DT_TQ2_0 || dt == DT_NVFP4 ||
+           dt == DT_ROCMFP4 || dt == DT_ROCMFP4_FAST || dt == DT_Q6_0_ROCMFPX || dt == DT_Q3_0_ROCMFPX ||
+           dt == DT_Q2_0_ROCMFPX;
+}
 __host__ __device__ constexpr int blk_vals(int dt) {
     return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K || dt == DT_IQ4_XS || dt == DT_Q2_K ||
-                   dt == DT_Q3_K
+                   dt == DT_Q3_K || dt == DT_Q8_K || dt == DT_TQ1_0 || dt == DT_TQ2_0
                ? 256
+           : dt == DT_NVFP4 ? 64
            : (dt == DT_Q4_0 || dt == DT_Q8_0 || dt == DT_IQ4_NL || dt == DT_MXFP4 || dt == DT_Q4_1 ||
-              dt == DT_Q5_0 || dt == DT_Q5_1 || dt == DT_F16 || dt == DT_BF16)
+              dt == DT_Q5_0 || dt == DT_Q5_1 || dt == DT_F16 || dt == DT_BF16 || dt == DT_Q8_1 ||
+              dt == DT_ROCMFP4 || dt == DT_ROCMFP4_FAST || dt == DT_Q6_0_ROCMFPX || dt == DT_Q3_0_ROCMFPX ||
+              dt == DT_Q2_0_ROCMFPX)
                ? 32
                                                                   : 1;
 }
@@ -35,7 +45,10 @@ __host__ __device__ constexpr int blk_bytes(int dt) {
          : dt == DT_Q2_K ? 84 : dt == DT_Q3_K ? 110 : dt == DT_MXFP4 ? 17 : dt == DT_Q4_1 ? 20
          : dt == DT_Q5_0 ? 22 : dt == DT_Q5_1 ? 24
          : dt == DT_Q4_0 || dt == DT_IQ4_NL ? 18
-         : dt == DT_Q8_0 ? 34 : dt == DT_F16 || dt == DT_BF16 ? 64 : 4;
+         : dt == DT_Q8_0 ? 34 : dt == DT_F16 || dt == DT_BF16 ? 64
+         : dt == DT_Q8_1 ? 36 : dt == DT_Q8_K ? 292 : dt == DT_TQ1_0 ? 54 : dt == DT_TQ2_0 ? 66
+         : dt == DT_NVFP4 ? 36 : dt == DT_ROCMFP4 ? 18 : dt == DT_ROCMFP4_FAST ? 17
+         : dt == DT_Q6_0_ROCMFPX ? 26 : dt == DT_Q3_0_ROCMFPX ? 14 : dt == DT_Q2_0_ROCMFPX ? 10 : 4;
 }
 
 __device__ __forceinline__ float ldh(const uint8_t *p) {
@@ -204,6 +217,146 @@ __device__ __forceinline__ void dequant_chunk<DT_MXFP4>(const uint8_t *b, int, f
         y[j] = static_cast<float>(kFp4Grid[b[1 + j] & 0xF]) * d;
         y[j + 16] = static_cast<float>(kFp4Grid[b[1 + j] >> 4]) * d;
     }
+}
+
+// ---------------------------------------------- generic-chunk formats ----
+// Byte loads only: these blocks sit at any byte alignment.
+
+// src/quant.cpp:389-396: Q8_1, value d*q + s with the product rounded before
+// the add (the reference build does not contract it)
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_Q8_1>(const uint8_t *b, int, float *y) {
+    const float d = ldh(b), s = ldh(b + 2);
+    for (int k = 0; k < 32; k++) y[k] = __fadd_rn(__fmul_rn(d, static_cast<float>(static_cast<int8_t>(b[4 + k]))), s);
+}
+
+// src/quant.cpp:557-564: Q8_K, f32 d then 256 int8 codes (the 16 block sums
+// after them are not read)
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_Q8_K>(const uint8_t *b, int c, float *y) {
+    const uint32_t db = static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8) |
+                        (static_cast<uint32_t>(b[2]) << 16) | (static_cast<uint32_t>(b[3]) << 24);
+    const float d = __builtin_bit_cast(float, db);
+    for (int k = 0; k < 32; k++) y[k] = d * static_cast<float>(static_cast<int8_t>(b[4 + 32 * c + k]));
+}
+
+// src/quant.cpp:576-585: UE4M3 scale byte.  0x00 and 0x7F are 0, bit 7 is
+// not read; exponent 0 gives m * 2^-9, else (1 + m/8) * 2^(e-7), both halved
+// -- i.e. m * 2^-10 or (8 + m) * 2^(e-11), each exact in f32.
+__device__ __forceinline__ float ue4m3_f(uint32_t x) {
+    x &= 0xFFu;
+    if (x == 0 || x == 0x7F) return 0.0f;
+    const uint32_t e = (x >> 3) & 0xFu, m = x & 7u;
+    if (e == 0) return static_cast<float>(m) * 0x1p-10f;
+    return static_cast<float>(8u + m) * __builtin_bit_cast(float, (e + 116u) << 23);   // 2^(e - 11)
+}
+
+// src/quant.cpp:661-672: NVFP4, 64-value blocks: four UE4M3 scales, four
+// 8-byte runs; chunk c is runs 2c and 2c + 1 (run s: value 16 s + j the low
+// nibble of byte j, 16 s + 8 + j the high)
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_NVFP4>(const uint8_t *b, int c, float *y) {
+    for (int h = 0; h < 2; h++) {
+        const int s = 2 * c + h;
+        const float d = ue4m3_f(b[s]);
+        const uint8_t *qs = b + 4 + 8 * s;
+        for (int j = 0; j < 8; j++) {
+            y[16 * h + j] = static_cast<float>(kFp4Grid[qs[j] & 0xF]) * d;
+            y[16 * h + 8 + j] = static_cast<float>(kFp4Grid[qs[j] >> 4]) * d;
+        }
+    }
+}
+
+// src/quant.cpp:310-318: ROCmFP4 ladder 0, 1, 2, 3, 4, 6, 8, 10, sign bit 3
+__device__ __forceinline__ int rocmfp4_code(uint32_t q) {
+    const int m = static_cast<int>(q & 7u), mag = m <= 4 ? m : 2 * m - 4;
+    return (q & 8u) ? -mag : mag;
+}
+// src/quant.cpp:692-713: ROCmFP4 (two half scales after 16 nibble bytes)
+// and ROCmFP4_FAST (one scale); value j the low nibble of byte j, j + 16 the
+// high
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_ROCMFP4>(const uint8_t *b, int, float *y) {
+    const float d0 = ue4m3_f(b[16]), d1 = ue4m3_f(b[17]);
+    for (int j = 0; j < 16; j++) {
+        y[j] = static_cast<float>(rocmfp4_code(b[j] & 0xFu)) * d0;
+        y[j + 16] = static_cast<float>(rocmfp4_code(b[j] >> 4)) * d1;
+    }
+}
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_ROCMFP4_FAST>(const uint8_t *b, int, float *y) {
+    const float d = ue4m3_f(b[16]);
+    for (int j = 0; j < 16; j++) {
+        y[j] = static_cast<float>(rocmfp4_code(b[j] & 0xFu)) * d;
+        y[j + 16] = static_cast<float>(rocmfp4_code(b[j] >> 4)) * d;
+    }
+}
+
+// src/quant.cpp:740-857: the ROCmFPX formats, two UE4M3 half scales after
+// the codes.  FP2: four codes a byte from the low bits on {-4, -1, 1, 4};
+// FP3: eight 3-bit codes per 3 bytes, magnitude {0, 1, 2, 4}[c & 3], sign
+// bit 2; FP6: four 6-bit codes per 3 bytes, magnitude c & 31, sign bit 5,
+// negative zero = -32.
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_Q2_0_ROCMFPX>(const uint8_t *b, int, float *y) {
+    const float d0 = ue4m3_f(b[8]), d1 = ue4m3_f(b[9]);
+    for (int j = 0; j < 32; j++) {
+        const uint32_t c = (b[j >> 2] >> (2 * (j & 3))) & 3u;
+        const int v = c == 0 ? -4 : c == 1 ? -1 : c == 2 ? 1 : 4;
+        y[j] = static_cast<float>(v) * (j < 16 ? d0 : d1);
+    }
+}
+__device__ __forceinline__ uint32_t bytes3(const uint8_t *g) {
+    return static_cast<uint32_t>(g[0]) | (static_cast<uint32_t>(g[1]) << 8) | (static_cast<uint32_t>(g[2]) << 16);
+}
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_Q3_0_ROCMFPX>(const uint8_t *b, int, float *y) {
+    const float d0 = ue4m3_f(b[12]), d1 = ue4m3_f(b[13]);
+    for (int j = 0; j < 32; j++) {
+        const uint32_t c = (bytes3(b + 3 * (j >> 3)) >> (3 * (j & 7))) & 7u;
+        const int m = (c & 3u) == 3u ? 4 : static_cast<int>(c & 3u);
+        y[j] = static_cast<float>((c & 4u) ? -m : m) * (j < 16 ? d0 : d1);
+    }
+}
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_Q6_0_ROCMFPX>(const uint8_t *b, int, float *y) {
+    const float d0 = ue4m3_f(b[24]), d1 = ue4m3_f(b[25]);
+    for (int j = 0; j < 32; j++) {
+        const uint32_t c = (bytes3(b + 3 * (j >> 2)) >> (6 * (j & 3))) & 63u;
+        const int m = static_cast<int>(c & 31u);
+        y[j] = static_cast<float>((c & 32u) ? -(m == 0 ? 32 : m) : m) * (j < 16 ? d0 : d1);
+    }
+}
+
+// src/quant.cpp:859-889: TQ1_0 trit n of byte q: ((uint8)(q * 3^n) * 3) >> 8,
+// less 1.  Element v < 160: byte v % 32, trit v / 32; v < 240: byte
+// 32 + (v - 160) % 16, trit (v - 160) / 16; else byte 48 + (v - 240) % 4,
+// trit (v - 240) / 4.  f16 d at byte 52.
+__device__ __forceinline__ int tq1_trit(uint32_t q, int n) {
+    const uint32_t p3 = n == 0 ? 1u : n == 1 ? 3u : n == 2 ? 9u : n == 3 ? 27u : 81u;
+    return static_cast<int>((((q * p3) & 0xFFu) * 3u) >> 8) - 1;
+}
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_TQ1_0>(const uint8_t *b, int c, float *y) {
+    const float d = ldh(b + 52);
+    for (int k = 0; k < 32; k++) {
+        const int v = 32 * c + k;
+        int t;
+        if (v < 160) t = tq1_trit(b[v & 31], v >> 5);
+        else if (v < 240) t = tq1_trit(b[32 + ((v - 160) & 15)], (v - 160) >> 4);
+        else t = tq1_trit(b[48 + ((v - 240) & 3)], (v - 240) >> 2);
+        y[k] = d * static_cast<float>(t);
+    }
+}
+
+// src/quant.cpp:907-918: TQ2_0, element 128 h + 32 l + m is bits 2l of byte
+// 32 h + m, value d (q - 1); f16 d at byte 64.  Chunk c: h = c / 4, l = c % 4.
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_TQ2_0>(const uint8_t *b, int c, float *y) {
+    const float d = ldh(b + 64);
+    const int h = c >> 2, l = c & 3;
+    for (int m = 0; m < 32; m++)
+        y[m] = d * static_cast<float>(static_cast<int>((b[32 * h + m] >> (2 * l)) & 3u) - 1);
 }
 
 // F16 / BF16 weights (dequant.hpp:428-440): widening, exact
@@ -1303,5 +1456,41 @@ template <> struct WaveFmt<DT_Q8_0> {
         return a;
     }
 };
+
+// ---------------------------------------------------- generic chunk lane ----
+// The GEMV view of a generic-chunk format: one lane per 32-value chunk (LPB
+// lanes per block), the lane keeps its block's address and decodes its chunk
+// with dequant_chunk when it is dotted; the dot is one f32 fma chain over the
+// chunk's values in order.
+template <int DT> struct ChunkLane {
+    static constexpr int LPB = blk_vals(DT) / 32, NG = 1, RUN = 32, NRUN = 1, NRAW = 2;
+    __device__ static int run_start(int p, int) { return 32 * p; }
+    __device__ static int group_of(int) { return 0; }
+    __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
+        const uint64_t a = reinterpret_cast<uint64_t>(blk);
+        raw[0] = static_cast<uint32_t>(a);
+        raw[1] = static_cast<uint32_t>(a >> 32);
+    }
+    __device__ static float dot(const uint32_t (&raw)[NRAW], int p, const float (&xv)[32], const float (&)[NG]) {
+        const uint8_t *blk = reinterpret_cast<const uint8_t *>(static_cast<uint64_t>(raw[0]) |
+                                                               (static_cast<uint64_t>(raw[1]) << 32));
+        float y[32];
+        dequant_chunk<DT>(blk, p, y);
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) s = __builtin_fmaf(y[i], xv[i], s);
+        return s;
+    }
+};
+template <> struct LaneFmt<DT_Q8_1> : ChunkLane<DT_Q8_1> {};
+template <> struct LaneFmt<DT_Q8_K> : ChunkLane<DT_Q8_K> {};
+template <> struct LaneFmt<DT_TQ1_0> : ChunkLane<DT_TQ1_0> {};
+template <> struct LaneFmt<DT_TQ2_0> : ChunkLane<DT_TQ2_0> {};
+template <> struct LaneFmt<DT_NVFP4> : ChunkLane<DT_NVFP4> {};
+template <> struct LaneFmt<DT_ROCMFP4> : ChunkLane<DT_ROCMFP4> {};
+template <> struct LaneFmt<DT_ROCMFP4_FAST> : ChunkLane<DT_ROCMFP4_FAST> {};
+template <> struct LaneFmt<DT_Q6_0_ROCMFPX> : ChunkLane<DT_Q6_0_ROCMFPX> {};
+template <> struct LaneFmt<DT_Q3_0_ROCMFPX> : ChunkLane<DT_Q3_0_ROCMFPX> {};
+template <> struct LaneFmt<DT_Q2_0_ROCMFPX> : ChunkLane<DT_Q2_0_ROCMFPX> {};
 
 }  // namespace krk

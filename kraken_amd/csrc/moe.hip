@@ -42,7 +42,10 @@
 #define KRK_MOE_TYPES(X, T, A)                                                                  \
     X(DT_Q4_K, T, A) X(DT_Q6_K, T, A) X(DT_Q4_0, T, A) X(DT_Q8_0, T, A) X(DT_Q5_K, T, A)      \
     X(DT_Q2_K, T, A) X(DT_Q3_K, T, A) X(DT_IQ4_NL, T, A) X(DT_IQ4_XS, T, A) X(DT_MXFP4, T, A) \
-    X(DT_Q4_1, T, A) X(DT_Q5_0, T, A) X(DT_Q5_1, T, A) X(DT_F16, T, A) X(DT_BF16, T, A)
+    X(DT_Q4_1, T, A) X(DT_Q5_0, T, A) X(DT_Q5_1, T, A) X(DT_F16, T, A) X(DT_BF16, T, A)        \
+    X(DT_Q8_1, T, A) X(DT_Q8_K, T, A) X(DT_TQ1_0, T, A) X(DT_TQ2_0, T, A) X(DT_NVFP4, T, A)    \
+    X(DT_ROCMFP4, T, A) X(DT_ROCMFP4_FAST, T, A) X(DT_Q6_0_ROCMFPX, T, A)                     \
+    X(DT_Q3_0_ROCMFPX, T, A) X(DT_Q2_0_ROCMFPX, T, A)
 #define KRK_MOE_UNPAREN(...) __VA_ARGS__
 #define KRK_MOE_ROWS(D, T, A) \
     case D: gemv_rows<D, KRK_MOE_UNPAREN T>(KRK_MOE_UNPAREN A); break;
