@@ -64,7 +64,12 @@ enum krk_dtype {
     KRK_DT_ROCMFP4_FAST = 101,
     KRK_DT_Q6_0_ROCMFPX = 102,
     KRK_DT_Q3_0_ROCMFPX = 104,
-    KRK_DT_Q2_0_ROCMFPX = 107
+    KRK_DT_Q2_0_ROCMFPX = 107,
+    KRK_DT_Q1_0 = 41,      /* include/krk/quant.hpp:120-135 */
+    KRK_DT_Q2_0 = 42,      /* the 128-value / 34-byte layout */
+    KRK_DT_Q2_0_64 = 48,
+    KRK_DT_PQ2_0 = 142,
+    KRK_DT_PTQ1_0 = 143
 };
 
 /* Activation type of a handle: backend.hpp `act_type()` (F16 on the

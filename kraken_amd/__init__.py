@@ -24,7 +24,9 @@ BF16 = 30
 # served through the generic 32-value chunk path
 Q8_1, Q8_K, TQ1_0, TQ2_0, NVFP4 = 9, 15, 34, 35, 40
 ROCMFP4, ROCMFP4_FAST, Q6_0_ROCMFPX, Q3_0_ROCMFPX, Q2_0_ROCMFPX = 100, 101, 102, 104, 107
-CHUNK_FMTS = (Q8_1, Q8_K, TQ1_0, TQ2_0, NVFP4, ROCMFP4, ROCMFP4_FAST, Q6_0_ROCMFPX, Q3_0_ROCMFPX, Q2_0_ROCMFPX)
+Q1_0, Q2_0, Q2_0_64, PQ2_0, PTQ1_0 = 41, 42, 48, 142, 143
+CHUNK_FMTS = (Q8_1, Q8_K, TQ1_0, TQ2_0, NVFP4, ROCMFP4, ROCMFP4_FAST, Q6_0_ROCMFPX, Q3_0_ROCMFPX, Q2_0_ROCMFPX,
+              Q1_0, Q2_0, Q2_0_64, PQ2_0, PTQ1_0)
 ACT_F32, ACT_F16 = 0, 1
 PATH_AUTO, PATH_EXACT, PATH_MFMA, PATH_INT8 = 0, 1, 2, 3
 DTYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K",
@@ -32,15 +34,18 @@ DTYPE_NAMES = {Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6
                Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1", BF16: "BF16", Q8_1: "Q8_1", Q8_K: "Q8_K",
                TQ1_0: "TQ1_0", TQ2_0: "TQ2_0", NVFP4: "NVFP4", ROCMFP4: "ROCMFP4",
                ROCMFP4_FAST: "ROCMFP4_FAST", Q6_0_ROCMFPX: "Q6_0_ROCMFPX", Q3_0_ROCMFPX: "Q3_0_ROCMFPX",
-               Q2_0_ROCMFPX: "Q2_0_ROCMFPX"}
+               Q2_0_ROCMFPX: "Q2_0_ROCMFPX", Q1_0: "Q1_0", Q2_0: "Q2_0", Q2_0_64: "Q2_0_64", PQ2_0: "PQ2_0",
+               PTQ1_0: "PTQ1_0"}
 BLOCK_VALUES = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, IQ4_NL: 32, IQ4_XS: 256,
                 Q2_K: 256, Q3_K: 256, MXFP4: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, F16: 1, BF16: 1,
                 Q8_1: 32, Q8_K: 256, TQ1_0: 256, TQ2_0: 256, NVFP4: 64, ROCMFP4: 32, ROCMFP4_FAST: 32,
-                Q6_0_ROCMFPX: 32, Q3_0_ROCMFPX: 32, Q2_0_ROCMFPX: 32}
+                Q6_0_ROCMFPX: 32, Q3_0_ROCMFPX: 32, Q2_0_ROCMFPX: 32, Q1_0: 128, Q2_0: 128, Q2_0_64: 64,
+                PQ2_0: 128, PTQ1_0: 128}
 BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210, IQ4_NL: 18, IQ4_XS: 136,
                Q2_K: 84, Q3_K: 110, MXFP4: 17, Q4_1: 20, Q5_0: 22, Q5_1: 24, F16: 2, BF16: 2,
                Q8_1: 36, Q8_K: 292, TQ1_0: 54, TQ2_0: 66, NVFP4: 36, ROCMFP4: 18, ROCMFP4_FAST: 17,
-               Q6_0_ROCMFPX: 26, Q3_0_ROCMFPX: 14, Q2_0_ROCMFPX: 10}
+               Q6_0_ROCMFPX: 26, Q3_0_ROCMFPX: 14, Q2_0_ROCMFPX: 10, Q1_0: 18, Q2_0: 34, Q2_0_64: 18,
+               PQ2_0: 34, PTQ1_0: 28}
 
 _vp, _i64, _i32, _f32, _u64 = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_uint64
 _P = C.POINTER

@@ -93,10 +93,7 @@ uintptr_t weight_align(int wt) {
         case KRK_DT_IQ4_XS: return 8;
         case KRK_DT_Q2_K: return 4;
         case KRK_DT_MXFP4: return 1;
-        case KRK_DT_Q8_1: case KRK_DT_Q8_K: case KRK_DT_TQ1_0: case KRK_DT_TQ2_0: case KRK_DT_NVFP4:
-        case KRK_DT_ROCMFP4: case KRK_DT_ROCMFP4_FAST: case KRK_DT_Q6_0_ROCMFPX: case KRK_DT_Q3_0_ROCMFPX:
-        case KRK_DT_Q2_0_ROCMFPX: return 1;   // byte loads (the generic chunk path)
-        default: return 2;
+        default: return krk::chunk_fmt(wt) ? 1 : 2;   // the generic chunk path: byte loads
     }
 }
 

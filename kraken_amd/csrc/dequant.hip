@@ -58,16 +58,10 @@ static hipError_t dq(int dt, const void *w, int64_t rb, int64_t n_rows, int64_t 
         case DT_Q5_0: hipLaunchKernelGGL((dequant_kernel<DT_Q5_0, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
         case DT_Q5_1: hipLaunchKernelGGL((dequant_kernel<DT_Q5_1, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
         case DT_F16: hipLaunchKernelGGL((dequant_kernel<DT_F16, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
-        case DT_Q8_1: hipLaunchKernelGGL((dequant_kernel<DT_Q8_1, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
-        case DT_Q8_K: hipLaunchKernelGGL((dequant_kernel<DT_Q8_K, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
-        case DT_TQ1_0: hipLaunchKernelGGL((dequant_kernel<DT_TQ1_0, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
-        case DT_TQ2_0: hipLaunchKernelGGL((dequant_kernel<DT_TQ2_0, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
-        case DT_NVFP4: hipLaunchKernelGGL((dequant_kernel<DT_NVFP4, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
-        case DT_ROCMFP4: hipLaunchKernelGGL((dequant_kernel<DT_ROCMFP4, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
-        case DT_ROCMFP4_FAST: hipLaunchKernelGGL((dequant_kernel<DT_ROCMFP4_FAST, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
-        case DT_Q6_0_ROCMFPX: hipLaunchKernelGGL((dequant_kernel<DT_Q6_0_ROCMFPX, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
-        case DT_Q3_0_ROCMFPX: hipLaunchKernelGGL((dequant_kernel<DT_Q3_0_ROCMFPX, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
-        case DT_Q2_0_ROCMFPX: hipLaunchKernelGGL((dequant_kernel<DT_Q2_0_ROCMFPX, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
+#define KRK_CHUNK_CASE(D) \
+    case D: hipLaunchKernelGGL((dequant_kernel<D, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
+        KRK_CHUNK_FORMATS(KRK_CHUNK_CASE)
+#undef KRK_CHUNK_CASE
         case DT_BF16: hipLaunchKernelGGL((dequant_kernel<DT_BF16, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
         case DT_Q8_0: hipLaunchKernelGGL((dequant_kernel<DT_Q8_0, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;
         case DT_Q4_K: hipLaunchKernelGGL((dequant_kernel<DT_Q4_K, F16>), grid, dim3(256), 0, st, wb, rb, n_rows, n_in, out); break;

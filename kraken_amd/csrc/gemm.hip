@@ -427,16 +427,9 @@ template <int DT> struct WStageChunk {
         for (int i = 0; i < 16; i++) o[i] = static_cast<_Float16>(hf ? y[16 + i] : y[i]);
     }
 };
-template <> struct WStage<DT_Q8_1> : WStageChunk<DT_Q8_1> {};
-template <> struct WStage<DT_Q8_K> : WStageChunk<DT_Q8_K> {};
-template <> struct WStage<DT_TQ1_0> : WStageChunk<DT_TQ1_0> {};
-template <> struct WStage<DT_TQ2_0> : WStageChunk<DT_TQ2_0> {};
-template <> struct WStage<DT_NVFP4> : WStageChunk<DT_NVFP4> {};
-template <> struct WStage<DT_ROCMFP4> : WStageChunk<DT_ROCMFP4> {};
-template <> struct WStage<DT_ROCMFP4_FAST> : WStageChunk<DT_ROCMFP4_FAST> {};
-template <> struct WStage<DT_Q6_0_ROCMFPX> : WStageChunk<DT_Q6_0_ROCMFPX> {};
-template <> struct WStage<DT_Q3_0_ROCMFPX> : WStageChunk<DT_Q3_0_ROCMFPX> {};
-template <> struct WStage<DT_Q2_0_ROCMFPX> : WStageChunk<DT_Q2_0_ROCMFPX> {};
+#define KRK_CHUNK_WSTAGE(D) template <> struct WStage<D> : WStageChunk<D> {};
+KRK_CHUNK_FORMATS(KRK_CHUNK_WSTAGE)
+#undef KRK_CHUNK_WSTAGE
 
 // ------------------------------------------------------- activation staging
 template <typename XT> struct XStage;
@@ -794,16 +787,7 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
         KRK_GEMM_CASE(DT_Q5_1)
         KRK_GEMM_CASE(DT_F16)
         KRK_GEMM_CASE(DT_BF16)
-        KRK_GEMM_CASE(DT_Q8_1)
-        KRK_GEMM_CASE(DT_Q8_K)
-        KRK_GEMM_CASE(DT_TQ1_0)
-        KRK_GEMM_CASE(DT_TQ2_0)
-        KRK_GEMM_CASE(DT_NVFP4)
-        KRK_GEMM_CASE(DT_ROCMFP4)
-        KRK_GEMM_CASE(DT_ROCMFP4_FAST)
-        KRK_GEMM_CASE(DT_Q6_0_ROCMFPX)
-        KRK_GEMM_CASE(DT_Q3_0_ROCMFPX)
-        KRK_GEMM_CASE(DT_Q2_0_ROCMFPX)
+        KRK_CHUNK_FORMATS(KRK_GEMM_CASE)
         default: return hipErrorInvalidValue;
     }
 #undef KRK_GEMM_CASE

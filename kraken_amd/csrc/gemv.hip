@@ -1401,16 +1401,10 @@ static hipError_t dispatch_chunk(SegTable t, hipStream_t st) {
 template <typename XT, typename OT>
 static hipError_t dispatch_dt(int dt, const SegTable &t, hipStream_t st) {
     switch (dt) {
-        case DT_Q8_1: return dispatch_chunk<DT_Q8_1, XT, OT>(t, st);
-        case DT_Q8_K: return dispatch_chunk<DT_Q8_K, XT, OT>(t, st);
-        case DT_TQ1_0: return dispatch_chunk<DT_TQ1_0, XT, OT>(t, st);
-        case DT_TQ2_0: return dispatch_chunk<DT_TQ2_0, XT, OT>(t, st);
-        case DT_NVFP4: return dispatch_chunk<DT_NVFP4, XT, OT>(t, st);
-        case DT_ROCMFP4: return dispatch_chunk<DT_ROCMFP4, XT, OT>(t, st);
-        case DT_ROCMFP4_FAST: return dispatch_chunk<DT_ROCMFP4_FAST, XT, OT>(t, st);
-        case DT_Q6_0_ROCMFPX: return dispatch_chunk<DT_Q6_0_ROCMFPX, XT, OT>(t, st);
-        case DT_Q3_0_ROCMFPX: return dispatch_chunk<DT_Q3_0_ROCMFPX, XT, OT>(t, st);
-        case DT_Q2_0_ROCMFPX: return dispatch_chunk<DT_Q2_0_ROCMFPX, XT, OT>(t, st);
+#define KRK_CHUNK_CASE(D) \
+    case D: return dispatch_chunk<D, XT, OT>(t, st);
+        KRK_CHUNK_FORMATS(KRK_CHUNK_CASE)
+#undef KRK_CHUNK_CASE
         case DT_Q4_K: return dispatch_mr<DT_Q4_K, XT, OT>(t, st);
         case DT_Q5_K: return dispatch_mr<DT_Q5_K, XT, OT>(t, st);
         case DT_Q6_K: return dispatch_mr<DT_Q6_K, XT, OT>(t, st);

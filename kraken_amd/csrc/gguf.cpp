@@ -139,6 +139,10 @@ bool geometry(uint32_t id, int *bs, int *bb) {
         case KRK_DT_Q6_0_ROCMFPX: *bs = 32; *bb = 26; return true;
         case KRK_DT_Q3_0_ROCMFPX: *bs = 32; *bb = 14; return true;
         case KRK_DT_Q2_0_ROCMFPX: *bs = 32; *bb = 10; return true;
+        case KRK_DT_Q1_0: *bs = 128; *bb = 18; return true;
+        case KRK_DT_Q2_0: case KRK_DT_PQ2_0: *bs = 128; *bb = 34; return true;
+        case KRK_DT_Q2_0_64: *bs = 64; *bb = 18; return true;
+        case KRK_DT_PTQ1_0: *bs = 128; *bb = 28; return true;
         default: return false;
     }
 }

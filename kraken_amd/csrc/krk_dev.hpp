@@ -28,7 +28,8 @@ enum : int { DT_F32 = 0, DT_F16 = 1, DT_Q4_0 = 2, DT_Q8_0 = 8, DT_Q4_K = 12, DT_
              // served through the generic chunk path (include/krk/quant.hpp:25-31, 67-68, 105,
              // 128-129, 166-168)
              DT_Q8_1 = 9, DT_Q8_K = 15, DT_TQ1_0 = 34, DT_TQ2_0 = 35, DT_NVFP4 = 40, DT_ROCMFP4 = 100,
-             DT_ROCMFP4_FAST = 101, DT_Q6_0_ROCMFPX = 102, DT_Q3_0_ROCMFPX = 104, DT_Q2_0_ROCMFPX = 107 };
+             DT_ROCMFP4_FAST = 101, DT_Q6_0_ROCMFPX = 102, DT_Q3_0_ROCMFPX = 104, DT_Q2_0_ROCMFPX = 107,
+             DT_Q1_0 = 41, DT_Q2_0 = 42, DT_Q2_0_64 = 48, DT_PQ2_0 = 142, DT_PTQ1_0 = 143 };
 
 __device__ __forceinline__ float h2f(uint32_t h16) {
     _Float16 h;

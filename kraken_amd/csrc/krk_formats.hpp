@@ -22,17 +22,23 @@ namespace krk {
 // F16 and BF16 weights are handled as 32-value pseudo-blocks of 64 bytes (a
 // row of n values is n / 32 of them), so they ride the same chunk contract.
 // Formats served through the generic chunk path: every kernel reads them
-// through dequant_chunk alone (byte loads, any alignment).
+// through dequant_chunk alone (byte loads, any alignment).  X(type) for each,
+// for the launchers' switches.
+#define KRK_CHUNK_FORMATS(X)                                                                       \
+    X(DT_Q8_1) X(DT_Q8_K) X(DT_TQ1_0) X(DT_TQ2_0) X(DT_NVFP4) X(DT_ROCMFP4) X(DT_ROCMFP4_FAST)      \
+    X(DT_Q6_0_ROCMFPX) X(DT_Q3_0_ROCMFPX) X(DT_Q2_0_ROCMFPX) X(DT_Q1_0) X(DT_Q2_0) X(DT_Q2_0_64)   \
+    X(DT_PQ2_0) X(DT_PTQ1_0)
 __host__ __device__ constexpr bool chunk_fmt(int dt) {
-    return dt == DT_Q8_1 || dt == DT_Q8_K || dt == DT_TQ1_0 || dt == DT_TQ2_0 || dt == DT_NVFP4 ||
-           dt == DT_ROCMFP4 || dt == DT_ROCMFP4_FAST || dt == DT_Q6_0_ROCMFPX || dt == DT_Q3_0_ROCMFPX ||
-           dt == DT_Q2_0_ROCMFPX;
+#define KRK_CHUNK_IS(D) dt == D ||
+    return KRK_CHUNK_FORMATS(KRK_CHUNK_IS) false;
+#undef KRK_CHUNK_IS
 }
 __host__ __device__ constexpr int blk_vals(int dt) {
     return dt == DT_Q4_K || dt == DT_Q5_K || dt == DT_Q6_K || dt == DT_IQ4_XS || dt == DT_Q2_K ||
                    dt == DT_Q3_K || dt == DT_Q8_K || dt == DT_TQ1_0 || dt == DT_TQ2_0
                ? 256
-           : dt == DT_NVFP4 ? 64
+           : dt == DT_NVFP4 || dt == DT_Q2_0_64 ? 64
+           : dt == DT_Q1_0 || dt == DT_Q2_0 || dt == DT_PQ2_0 || dt == DT_PTQ1_0 ? 128
            : (dt == DT_Q4_0 || dt == DT_Q8_0 || dt == DT_IQ4_NL || dt == DT_MXFP4 || dt == DT_Q4_1 ||
               dt == DT_Q5_0 || dt == DT_Q5_1 || dt == DT_F16 || dt == DT_BF16 || dt == DT_Q8_1 ||
               dt == DT_ROCMFP4 || dt == DT_ROCMFP4_FAST || dt == DT_Q6_0_ROCMFPX || dt == DT_Q3_0_ROCMFPX ||
@@ -48,7 +54,9 @@ __host__ __device__ constexpr int blk_bytes(int dt) {
          : dt == DT_Q8_0 ? 34 : dt == DT_F16 || dt == DT_BF16 ? 64
          : dt == DT_Q8_1 ? 36 : dt == DT_Q8_K ? 292 : dt == DT_TQ1_0 ? 54 : dt == DT_TQ2_0 ? 66
          : dt == DT_NVFP4 ? 36 : dt == DT_ROCMFP4 ? 18 : dt == DT_ROCMFP4_FAST ? 17
-         : dt == DT_Q6_0_ROCMFPX ? 26 : dt == DT_Q3_0_ROCMFPX ? 14 : dt == DT_Q2_0_ROCMFPX ? 10 : 4;
+         : dt == DT_Q6_0_ROCMFPX ? 26 : dt == DT_Q3_0_ROCMFPX ? 14 : dt == DT_Q2_0_ROCMFPX ? 10
+         : dt == DT_Q1_0 || dt == DT_Q2_0_64 ? 18 : dt == DT_Q2_0 || dt == DT_PQ2_0 ? 34 : dt == DT_PTQ1_0 ? 28
+         : 4;
 }
 
 __device__ __forceinline__ float ldh(const uint8_t *p) {
@@ -357,6 +365,47 @@ __device__ __forceinline__ void dequant_chunk<DT_TQ2_0>(const uint8_t *b, int c,
     const int h = c >> 2, l = c & 3;
     for (int m = 0; m < 32; m++)
         y[m] = d * static_cast<float>(static_cast<int>((b[32 * h + m] >> (2 * l)) & 3u) - 1);
+}
+
+// src/quant_fmt_a.inc:71-83: Q1_0, one bit per value from the low bit, +d
+// for a 1 and -d for a 0
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_Q1_0>(const uint8_t *b, int c, float *y) {
+    const float d = ldh(b);
+    for (int k = 0; k < 32; k++) {
+        const int j = 32 * c + k;
+        y[k] = ((b[2 + (j >> 3)] >> (j & 7)) & 1u) ? d : -d;
+    }
+}
+// src/quant_fmt_a.inc:85-129: Q2_0 / PQ2_0 (128 values) and Q2_0_64 (64):
+// 2-bit codes four to a byte from the low pair, value (q - 1) * d
+__device__ __forceinline__ void dequant_q2_0n(const uint8_t *b, int c, float *y) {
+    const float d = ldh(b);
+    for (int k = 0; k < 32; k++) {
+        const int j = 32 * c + k;
+        y[k] = static_cast<float>(static_cast<int>((b[2 + (j >> 2)] >> (2 * (j & 3))) & 3u) - 1) * d;
+    }
+}
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_Q2_0>(const uint8_t *b, int c, float *y) { dequant_q2_0n(b, c, y); }
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_PQ2_0>(const uint8_t *b, int c, float *y) { dequant_q2_0n(b, c, y); }
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_Q2_0_64>(const uint8_t *b, int c, float *y) { dequant_q2_0n(b, c, y); }
+// src/quant.cpp:933-950: PTQ1_0, TQ1_0's trits at group 128, f16 d at 26:
+// v < 80 byte v % 16 trit v / 16; v < 120 byte 16 + (v - 80) % 8 trit
+// (v - 80) / 8; else byte 24 + (v - 120) % 2 trit (v - 120) / 2
+template <>
+__device__ __forceinline__ void dequant_chunk<DT_PTQ1_0>(const uint8_t *b, int c, float *y) {
+    const float d = ldh(b + 26);
+    for (int k = 0; k < 32; k++) {
+        const int v = 32 * c + k;
+        int t;
+        if (v < 80) t = tq1_trit(b[v & 15], v >> 4);
+        else if (v < 120) t = tq1_trit(b[16 + ((v - 80) & 7)], (v - 80) >> 3);
+        else t = tq1_trit(b[24 + ((v - 120) & 1)], (v - 120) >> 1);
+        y[k] = d * static_cast<float>(t);
+    }
 }
 
 // F16 / BF16 weights (dequant.hpp:428-440): widening, exact
@@ -1482,15 +1531,8 @@ template <int DT> struct ChunkLane {
         return s;
     }
 };
-template <> struct LaneFmt<DT_Q8_1> : ChunkLane<DT_Q8_1> {};
-template <> struct LaneFmt<DT_Q8_K> : ChunkLane<DT_Q8_K> {};
-template <> struct LaneFmt<DT_TQ1_0> : ChunkLane<DT_TQ1_0> {};
-template <> struct LaneFmt<DT_TQ2_0> : ChunkLane<DT_TQ2_0> {};
-template <> struct LaneFmt<DT_NVFP4> : ChunkLane<DT_NVFP4> {};
-template <> struct LaneFmt<DT_ROCMFP4> : ChunkLane<DT_ROCMFP4> {};
-template <> struct LaneFmt<DT_ROCMFP4_FAST> : ChunkLane<DT_ROCMFP4_FAST> {};
-template <> struct LaneFmt<DT_Q6_0_ROCMFPX> : ChunkLane<DT_Q6_0_ROCMFPX> {};
-template <> struct LaneFmt<DT_Q3_0_ROCMFPX> : ChunkLane<DT_Q3_0_ROCMFPX> {};
-template <> struct LaneFmt<DT_Q2_0_ROCMFPX> : ChunkLane<DT_Q2_0_ROCMFPX> {};
+#define KRK_CHUNK_LANE(D) template <> struct LaneFmt<D> : ChunkLane<D> {};
+KRK_CHUNK_FORMATS(KRK_CHUNK_LANE)
+#undef KRK_CHUNK_LANE
 
 }  // namespace krk

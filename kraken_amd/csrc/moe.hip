@@ -45,7 +45,8 @@
     X(DT_Q4_1, T, A) X(DT_Q5_0, T, A) X(DT_Q5_1, T, A) X(DT_F16, T, A) X(DT_BF16, T, A)        \
     X(DT_Q8_1, T, A) X(DT_Q8_K, T, A) X(DT_TQ1_0, T, A) X(DT_TQ2_0, T, A) X(DT_NVFP4, T, A)    \
     X(DT_ROCMFP4, T, A) X(DT_ROCMFP4_FAST, T, A) X(DT_Q6_0_ROCMFPX, T, A)                     \
-    X(DT_Q3_0_ROCMFPX, T, A) X(DT_Q2_0_ROCMFPX, T, A)
+    X(DT_Q3_0_ROCMFPX, T, A) X(DT_Q2_0_ROCMFPX, T, A) X(DT_Q1_0, T, A) X(DT_Q2_0, T, A)      \
+    X(DT_Q2_0_64, T, A) X(DT_PQ2_0, T, A) X(DT_PTQ1_0, T, A)
 #define KRK_MOE_UNPAREN(...) __VA_ARGS__
 #define KRK_MOE_ROWS(D, T, A) \
     case D: gemv_rows<D, KRK_MOE_UNPAREN T>(KRK_MOE_UNPAREN A); break;

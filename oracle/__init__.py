@@ -24,7 +24,9 @@ BF16 = 30
 # formats served through the generic 32-value chunk path
 Q8_1, Q8_K, TQ1_0, TQ2_0, NVFP4 = 9, 15, 34, 35, 40
 ROCMFP4, ROCMFP4_FAST, Q6_0_ROCMFPX, Q3_0_ROCMFPX, Q2_0_ROCMFPX = 100, 101, 102, 104, 107
-CHUNK_FMTS = (Q8_1, Q8_K, TQ1_0, TQ2_0, NVFP4, ROCMFP4, ROCMFP4_FAST, Q6_0_ROCMFPX, Q3_0_ROCMFPX, Q2_0_ROCMFPX)
+Q1_0, Q2_0, Q2_0_64, PQ2_0, PTQ1_0 = 41, 42, 48, 142, 143
+CHUNK_FMTS = (Q8_1, Q8_K, TQ1_0, TQ2_0, NVFP4, ROCMFP4, ROCMFP4_FAST, Q6_0_ROCMFPX, Q3_0_ROCMFPX, Q2_0_ROCMFPX,
+              Q1_0, Q2_0, Q2_0_64, PQ2_0, PTQ1_0)
 
 _vp, _i64, _i32, _f32, _u16 = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_uint16
 

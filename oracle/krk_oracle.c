@@ -92,7 +92,8 @@ int orc_block_size(int dt) {
         case ORC_Q4_1: case ORC_Q5_0: case ORC_Q5_1: return 32;
         case ORC_Q8_1: case ORC_ROCMFP4: case ORC_ROCMFP4_FAST: case ORC_Q6_0_ROCMFPX:
         case ORC_Q3_0_ROCMFPX: case ORC_Q2_0_ROCMFPX: return 32;
-        case ORC_NVFP4: return 64;
+        case ORC_NVFP4: case ORC_Q2_0_64: return 64;
+        case ORC_Q1_0: case ORC_Q2_0: case ORC_PQ2_0: case ORC_PTQ1_0: return 128;
         case ORC_Q2_K: case ORC_Q3_K: case ORC_Q4_K: case ORC_Q5_K: case ORC_Q6_K: case ORC_IQ4_XS: return 256;
         case ORC_Q8_K: case ORC_TQ1_0: case ORC_TQ2_0: return 256;
         default: return 0;
@@ -124,6 +125,9 @@ int orc_block_bytes(int dt) {
         case ORC_Q6_0_ROCMFPX: return 26;
         case ORC_Q3_0_ROCMFPX: return 14;
         case ORC_Q2_0_ROCMFPX: return 10;
+        case ORC_Q1_0: case ORC_Q2_0_64: return 18;
+        case ORC_Q2_0: case ORC_PQ2_0: return 34;
+        case ORC_PTQ1_0: return 28;
         default: return 0;
     }
 }
@@ -480,6 +484,36 @@ static void deq_tq2_0(const uint8_t *b, float *y) {
                 y[128 * h + 32 * l + m] = d * (float)((int)((b[32 * h + m] >> (2 * l)) & 3) - 1);
 }
 
+/* src/quant_fmt_a.inc:71-83: Q1_0 (18 B / 128): f16 d, one bit per value
+ * (low bit first): +d for a 1, -d for a 0 (no zero). */
+static void deq_q1_0(const uint8_t *b, float *y) {
+    float d = ld_f16(b);
+    for (int j = 0; j < 128; j++) y[j] = ((b[2 + j / 8] >> (j % 8)) & 1) ? d : -d;
+}
+
+/* src/quant_fmt_a.inc:85-129: Q2_0 and PQ2_0 (34 B / 128) and Q2_0_64
+ * (18 B / 64): f16 d, 2-bit codes four to a byte from the low pair, value
+ * (q - 1) * d. */
+static void deq_q2_0n(const uint8_t *b, float *y, int n) {
+    float d = ld_f16(b);
+    for (int j = 0; j < n; j++) y[j] = (float)((int)((b[2 + j / 4] >> (2 * (j % 4))) & 3) - 1) * d;
+}
+
+/* src/quant.cpp:933-950: PTQ1_0 (28 B / 128): TQ1_0's trits at group 128,
+ * f16 d at 26.  Element v < 80: byte v % 16, trit v / 16; v < 120: byte
+ * 16 + (v - 80) % 8, trit (v - 80) / 8; else byte 24 + (v - 120) % 2, trit
+ * (v - 120) / 2. */
+static void deq_ptq1_0(const uint8_t *b, float *y) {
+    float d = ld_f16(b + 26);
+    for (int v = 0; v < 128; v++) {
+        int t;
+        if (v < 80) t = tq1_trit(b[v % 16], v / 16);
+        else if (v < 120) t = tq1_trit(b[16 + (v - 80) % 8], (v - 80) / 8);
+        else t = tq1_trit(b[24 + (v - 120) % 2], (v - 120) / 2);
+        y[v] = d * (float)t;
+    }
+}
+
 /* src/quant.cpp:1553-1601 (the formats on this path plus F16). */
 static void dequant_block(int dt, const uint8_t *p, float *buf) {
     switch (dt) {
@@ -513,6 +547,10 @@ static void dequant_block(int dt, const uint8_t *p, float *buf) {
         case ORC_Q6_0_ROCMFPX: deq_rocmfpx6(p, buf); break;
         case ORC_TQ1_0: deq_tq1_0(p, buf); break;
         case ORC_TQ2_0: deq_tq2_0(p, buf); break;
+        case ORC_Q1_0: deq_q1_0(p, buf); break;
+        case ORC_Q2_0: case ORC_PQ2_0: deq_q2_0n(p, buf, 128); break;
+        case ORC_Q2_0_64: deq_q2_0n(p, buf, 64); break;
+        case ORC_PTQ1_0: deq_ptq1_0(p, buf); break;
         default: break;
     }
 }

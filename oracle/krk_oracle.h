@@ -26,7 +26,7 @@ enum {
     /* include/krk/quant.hpp:25-31, 67-68, 105, 128-129, 166-168 */
     ORC_Q8_1 = 9, ORC_Q8_K = 15, ORC_TQ1_0 = 34, ORC_TQ2_0 = 35, ORC_NVFP4 = 40,
     ORC_ROCMFP4 = 100, ORC_ROCMFP4_FAST = 101, ORC_Q6_0_ROCMFPX = 102, ORC_Q3_0_ROCMFPX = 104,
-    ORC_Q2_0_ROCMFPX = 107
+    ORC_Q2_0_ROCMFPX = 107, ORC_Q1_0 = 41, ORC_Q2_0 = 42, ORC_Q2_0_64 = 48, ORC_PQ2_0 = 142, ORC_PTQ1_0 = 143
 };
 
 float    orc_fp16_to_fp32(uint16_t h);

@@ -41,7 +41,8 @@ def rand_blocks(rng, dt, n_blocks):
           oracle.MXFP4: 17, oracle.Q4_1: 20, oracle.Q5_0: 22, oracle.Q5_1: 24,
           oracle.Q8_1: 36, oracle.Q8_K: 292, oracle.TQ1_0: 54, oracle.TQ2_0: 66, oracle.NVFP4: 36,
           oracle.ROCMFP4: 18, oracle.ROCMFP4_FAST: 17, oracle.Q6_0_ROCMFPX: 26, oracle.Q3_0_ROCMFPX: 14,
-          oracle.Q2_0_ROCMFPX: 10}[dt]
+          oracle.Q2_0_ROCMFPX: 10, oracle.Q1_0: 18, oracle.Q2_0: 34, oracle.Q2_0_64: 18,
+          oracle.PQ2_0: 34, oracle.PTQ1_0: 28}[dt]
     w = rng.integers(0, 256, size=(n_blocks, bb), dtype=np.uint8)
 
     def setf16(off, scale):
@@ -67,6 +68,10 @@ def rand_blocks(rng, dt, n_blocks):
         w[:, 0:4] = d
     elif dt == oracle.TQ1_0:
         setf16(52, 0.01)
+    elif dt == oracle.PTQ1_0:
+        setf16(26, 0.01)
+    elif dt in (oracle.Q1_0, oracle.Q2_0, oracle.Q2_0_64, oracle.PQ2_0):
+        setf16(0, 0.01)
     elif dt == oracle.TQ2_0:
         setf16(64, 0.01)
     elif dt in oracle.CHUNK_FMTS:

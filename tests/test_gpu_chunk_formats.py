@@ -1,6 +1,6 @@
 """GPU parity of the formats served through the generic chunk path (Q8_1,
 Q8_K, TQ1_0, TQ2_0, NVFP4, ROCmFP4, ROCmFP4_FAST and the three ROCmFPX
-formats) against the CPU oracle, whose decoders are pinned bit for bit
+formats, Q1_0, Q2_0, Q2_0_64, PQ2_0, PTQ1_0) against the CPU oracle, whose decoders are pinned bit for bit
 against the reference build and its golden vectors (test_oracle.py).
 
 Every kernel reads these blocks through dequant_chunk alone (byte loads, any
