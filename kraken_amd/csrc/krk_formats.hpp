@@ -228,24 +228,50 @@ __device__ __forceinline__ void dequant_chunk<DT_MXFP4>(const uint8_t *b, int, f
 }
 
 // ---------------------------------------------- generic-chunk formats ----
-// Byte loads only: these blocks sit at any byte alignment.
+// These blocks sit at any byte alignment (17-, 10-, 54-byte blocks ...).
+// The part runs global memory with unaligned access allowed, so a block's
+// bytes come in as whole 16/8/4/2-byte loads at any address; no load reaches
+// past the block's last byte.  Bytes are then taken out of the words with
+// compile-time indices.
+__device__ __forceinline__ u32x4 ldu16(const uint8_t *p) { u32x4 v; __builtin_memcpy(&v, p, 16); return v; }
+__device__ __forceinline__ u32x2 ldu8(const uint8_t *p) { u32x2 v; __builtin_memcpy(&v, p, 8); return v; }
+__device__ __forceinline__ uint32_t ldu4(const uint8_t *p) { uint32_t v; __builtin_memcpy(&v, p, 4); return v; }
+__device__ __forceinline__ uint32_t ldu2(const uint8_t *p) { uint16_t v; __builtin_memcpy(&v, p, 2); return v; }
+// byte k (a constant after unrolling) of a little-endian word array
+template <int NW> __device__ __forceinline__ uint32_t byte_k(const uint32_t (&w)[NW], int k) {
+    return (w[k >> 2] >> (8 * (k & 3))) & 0xFFu;
+}
+__device__ __forceinline__ void put4(uint32_t (&w)[4], u32x4 v, int at = 0) {
+    w[at] = v.x; w[at + 1] = v.y; w[at + 2] = v.z; w[at + 3] = v.w;
+}
+template <int NW> __device__ __forceinline__ void put16(uint32_t (&w)[NW], u32x4 v, int at) {
+    w[at] = v.x; w[at + 1] = v.y; w[at + 2] = v.z; w[at + 3] = v.w;
+}
 
 // src/quant.cpp:389-396: Q8_1, value d*q + s with the product rounded before
 // the add (the reference build does not contract it)
 template <>
 __device__ __forceinline__ void dequant_chunk<DT_Q8_1>(const uint8_t *b, int, float *y) {
-    const float d = ldh(b), s = ldh(b + 2);
-    for (int k = 0; k < 32; k++) y[k] = __fadd_rn(__fmul_rn(d, static_cast<float>(static_cast<int8_t>(b[4 + k]))), s);
+    const uint32_t ds = ldu4(b);
+    const float d = h2f(ds & 0xFFFFu), s = h2f(ds >> 16);
+    uint32_t q[8];
+    put16(q, ldu16(b + 4), 0);
+    put16(q, ldu16(b + 20), 4);
+#pragma unroll
+    for (int k = 0; k < 32; k++)
+        y[k] = __fadd_rn(__fmul_rn(d, static_cast<float>(static_cast<int8_t>(byte_k(q, k)))), s);
 }
 
 // src/quant.cpp:557-564: Q8_K, f32 d then 256 int8 codes (the 16 block sums
 // after them are not read)
 template <>
 __device__ __forceinline__ void dequant_chunk<DT_Q8_K>(const uint8_t *b, int c, float *y) {
-    const uint32_t db = static_cast<uint32_t>(b[0]) | (static_cast<uint32_t>(b[1]) << 8) |
-                        (static_cast<uint32_t>(b[2]) << 16) | (static_cast<uint32_t>(b[3]) << 24);
-    const float d = __builtin_bit_cast(float, db);
-    for (int k = 0; k < 32; k++) y[k] = d * static_cast<float>(static_cast<int8_t>(b[4 + 32 * c + k]));
+    const float d = __builtin_bit_cast(float, ldu4(b));
+    uint32_t q[8];
+    put16(q, ldu16(b + 4 + 32 * c), 0);
+    put16(q, ldu16(b + 20 + 32 * c), 4);
+#pragma unroll
+    for (int k = 0; k < 32; k++) y[k] = d * static_cast<float>(static_cast<int8_t>(byte_k(q, k)));
 }
 
 // src/quant.cpp:576-585: UE4M3 scale byte.  0x00 and 0x7F are 0, bit 7 is
@@ -259,18 +285,30 @@ __device__ __forceinline__ float ue4m3_f(uint32_t x) {
     return static_cast<float>(8u + m) * __builtin_bit_cast(float, (e + 116u) << 23);   // 2^(e - 11)
 }
 
+// the doubled E2M1 grid (kFp4Grid) of one code from two registers (v_perm
+// picks magnitude byte q & 7 of 0, 1, 2, 3, 4, 6, 8, 12), bit 3 the sign: no
+// per-lane constant-memory lookup
+__device__ __forceinline__ int e2m1_grid(uint32_t q) {
+    const int m = static_cast<int>(__builtin_amdgcn_perm(0x0C080604u, 0x03020100u, q & 7u) & 0xFFu);
+    return (q & 8u) ? -m : m;
+}
+
 // src/quant.cpp:661-672: NVFP4, 64-value blocks: four UE4M3 scales, four
 // 8-byte runs; chunk c is runs 2c and 2c + 1 (run s: value 16 s + j the low
 // nibble of byte j, 16 s + 8 + j the high)
 template <>
 __device__ __forceinline__ void dequant_chunk<DT_NVFP4>(const uint8_t *b, int c, float *y) {
+    const uint32_t sc = ldu2(b + 2 * c);
+    uint32_t q[4];
+    put4(q, ldu16(b + 4 + 16 * c));
+#pragma unroll
     for (int h = 0; h < 2; h++) {
-        const int s = 2 * c + h;
-        const float d = ue4m3_f(b[s]);
-        const uint8_t *qs = b + 4 + 8 * s;
+        const float d = ue4m3_f(sc >> (8 * h));
+#pragma unroll
         for (int j = 0; j < 8; j++) {
-            y[16 * h + j] = static_cast<float>(kFp4Grid[qs[j] & 0xF]) * d;
-            y[16 * h + 8 + j] = static_cast<float>(kFp4Grid[qs[j] >> 4]) * d;
+            const uint32_t v = byte_k(q, 8 * h + j);
+            y[16 * h + j] = static_cast<float>(e2m1_grid(v & 0xFu)) * d;
+            y[16 * h + 8 + j] = static_cast<float>(e2m1_grid(v >> 4)) * d;
         }
     }
 }
@@ -283,54 +321,76 @@ __device__ __forceinline__ int rocmfp4_code(uint32_t q) {
 // src/quant.cpp:692-713: ROCmFP4 (two half scales after 16 nibble bytes)
 // and ROCmFP4_FAST (one scale); value j the low nibble of byte j, j + 16 the
 // high
-template <>
-__device__ __forceinline__ void dequant_chunk<DT_ROCMFP4>(const uint8_t *b, int, float *y) {
-    const float d0 = ue4m3_f(b[16]), d1 = ue4m3_f(b[17]);
+template <bool TWO>
+__device__ __forceinline__ void dequant_rocmfp4(const uint8_t *b, float *y) {
+    uint32_t q[4];
+    put4(q, ldu16(b));
+    const uint32_t sc = TWO ? ldu2(b + 16) : b[16];
+    const float d0 = ue4m3_f(sc), d1 = TWO ? ue4m3_f(sc >> 8) : d0;
+#pragma unroll
     for (int j = 0; j < 16; j++) {
-        y[j] = static_cast<float>(rocmfp4_code(b[j] & 0xFu)) * d0;
-        y[j + 16] = static_cast<float>(rocmfp4_code(b[j] >> 4)) * d1;
+        const uint32_t v = byte_k(q, j);
+        y[j] = static_cast<float>(rocmfp4_code(v & 0xFu)) * d0;
+        y[j + 16] = static_cast<float>(rocmfp4_code(v >> 4)) * d1;
     }
 }
 template <>
+__device__ __forceinline__ void dequant_chunk<DT_ROCMFP4>(const uint8_t *b, int, float *y) { dequant_rocmfp4<true>(b, y); }
+template <>
 __device__ __forceinline__ void dequant_chunk<DT_ROCMFP4_FAST>(const uint8_t *b, int, float *y) {
-    const float d = ue4m3_f(b[16]);
-    for (int j = 0; j < 16; j++) {
-        y[j] = static_cast<float>(rocmfp4_code(b[j] & 0xFu)) * d;
-        y[j + 16] = static_cast<float>(rocmfp4_code(b[j] >> 4)) * d;
-    }
+    dequant_rocmfp4<false>(b, y);
 }
 
 // src/quant.cpp:740-857: the ROCmFPX formats, two UE4M3 half scales after
 // the codes.  FP2: four codes a byte from the low bits on {-4, -1, 1, 4};
 // FP3: eight 3-bit codes per 3 bytes, magnitude {0, 1, 2, 4}[c & 3], sign
 // bit 2; FP6: four 6-bit codes per 3 bytes, magnitude c & 31, sign bit 5,
-// negative zero = -32.
+// negative zero = -32.  Code j of a packing of W bits per code, LSB first,
+// is bits [W j, W j + W) of the code bytes (a group never splits a code).
+template <int NW> __device__ __forceinline__ uint32_t bits_at(const uint32_t (&w)[NW], int bit, int n) {
+    const uint32_t lo = w[bit >> 5] >> (bit & 31);
+    const uint32_t hi = (bit & 31) + n > 32 ? w[(bit >> 5) + 1] << (32 - (bit & 31)) : 0u;
+    return (lo | hi) & ((1u << n) - 1u);
+}
 template <>
 __device__ __forceinline__ void dequant_chunk<DT_Q2_0_ROCMFPX>(const uint8_t *b, int, float *y) {
-    const float d0 = ue4m3_f(b[8]), d1 = ue4m3_f(b[9]);
+    const u32x2 qq = ldu8(b);
+    const uint32_t q[2] = {qq.x, qq.y};
+    const uint32_t sc = ldu2(b + 8);
+    const float d0 = ue4m3_f(sc), d1 = ue4m3_f(sc >> 8);
+#pragma unroll
     for (int j = 0; j < 32; j++) {
-        const uint32_t c = (b[j >> 2] >> (2 * (j & 3))) & 3u;
+        const uint32_t c = bits_at(q, 2 * j, 2);
         const int v = c == 0 ? -4 : c == 1 ? -1 : c == 2 ? 1 : 4;
         y[j] = static_cast<float>(v) * (j < 16 ? d0 : d1);
     }
 }
-__device__ __forceinline__ uint32_t bytes3(const uint8_t *g) {
-    return static_cast<uint32_t>(g[0]) | (static_cast<uint32_t>(g[1]) << 8) | (static_cast<uint32_t>(g[2]) << 16);
-}
 template <>
 __device__ __forceinline__ void dequant_chunk<DT_Q3_0_ROCMFPX>(const uint8_t *b, int, float *y) {
-    const float d0 = ue4m3_f(b[12]), d1 = ue4m3_f(b[13]);
+    const u32x2 qq = ldu8(b);
+    const uint32_t q[3] = {qq.x, qq.y, ldu4(b + 8)};
+    const uint32_t sc = ldu2(b + 12);
+    const float d0 = ue4m3_f(sc), d1 = ue4m3_f(sc >> 8);
+#pragma unroll
     for (int j = 0; j < 32; j++) {
-        const uint32_t c = (bytes3(b + 3 * (j >> 3)) >> (3 * (j & 7))) & 7u;
+        // group g = j / 8 is bytes 3g..3g+2, i.e. bits 24 g + 3 (j % 8)
+        const uint32_t c = bits_at(q, 24 * (j >> 3) + 3 * (j & 7), 3);
         const int m = (c & 3u) == 3u ? 4 : static_cast<int>(c & 3u);
         y[j] = static_cast<float>((c & 4u) ? -m : m) * (j < 16 ? d0 : d1);
     }
 }
 template <>
 __device__ __forceinline__ void dequant_chunk<DT_Q6_0_ROCMFPX>(const uint8_t *b, int, float *y) {
-    const float d0 = ue4m3_f(b[24]), d1 = ue4m3_f(b[25]);
+    uint32_t q[6];
+    put16(q, ldu16(b), 0);
+    const u32x2 t = ldu8(b + 16);
+    q[4] = t.x;
+    q[5] = t.y;
+    const uint32_t sc = ldu2(b + 24);
+    const float d0 = ue4m3_f(sc), d1 = ue4m3_f(sc >> 8);
+#pragma unroll
     for (int j = 0; j < 32; j++) {
-        const uint32_t c = (bytes3(b + 3 * (j >> 2)) >> (6 * (j & 3))) & 63u;
+        const uint32_t c = bits_at(q, 24 * (j >> 2) + 6 * (j & 3), 6);
         const int m = static_cast<int>(c & 31u);
         y[j] = static_cast<float>((c & 32u) ? -(m == 0 ? 32 : m) : m) * (j < 16 ? d0 : d1);
     }
@@ -339,20 +399,32 @@ __device__ __forceinline__ void dequant_chunk<DT_Q6_0_ROCMFPX>(const uint8_t *b,
 // src/quant.cpp:859-889: TQ1_0 trit n of byte q: ((uint8)(q * 3^n) * 3) >> 8,
 // less 1.  Element v < 160: byte v % 32, trit v / 32; v < 240: byte
 // 32 + (v - 160) % 16, trit (v - 160) / 16; else byte 48 + (v - 240) % 4,
-// trit (v - 240) / 4.  f16 d at byte 52.
+// trit (v - 240) / 4.  f16 d at byte 52.  In chunk c (v = 32 c + k) the byte
+// index depends on k alone: k (c < 5), 32 + k % 16 (c = 5, 6 and c = 7,
+// k < 16), 48 + (k - 16) % 4 (c = 7, k >= 16).
 __device__ __forceinline__ int tq1_trit(uint32_t q, int n) {
     const uint32_t p3 = n == 0 ? 1u : n == 1 ? 3u : n == 2 ? 9u : n == 3 ? 27u : 81u;
     return static_cast<int>((((q * p3) & 0xFFu) * 3u) >> 8) - 1;
 }
 template <>
 __device__ __forceinline__ void dequant_chunk<DT_TQ1_0>(const uint8_t *b, int c, float *y) {
-    const float d = ldh(b + 52);
+    const float d = h2f(ldu2(b + 52));
+    if (c < 5) {
+        uint32_t q[8];
+        put16(q, ldu16(b), 0);
+        put16(q, ldu16(b + 16), 4);
+#pragma unroll
+        for (int k = 0; k < 32; k++) y[k] = d * static_cast<float>(tq1_trit(byte_k(q, k), c));
+        return;
+    }
+    uint32_t q[5];
+    put16(q, ldu16(b + 32), 0);
+    q[4] = ldu4(b + 48);
+#pragma unroll
     for (int k = 0; k < 32; k++) {
-        const int v = 32 * c + k;
         int t;
-        if (v < 160) t = tq1_trit(b[v & 31], v >> 5);
-        else if (v < 240) t = tq1_trit(b[32 + ((v - 160) & 15)], (v - 160) >> 4);
-        else t = tq1_trit(b[48 + ((v - 240) & 3)], (v - 240) >> 2);
+        if (c < 7 || k < 16) t = tq1_trit(byte_k(q, k & 15), 2 * (c - 5) + (k >> 4));
+        else t = tq1_trit(byte_k(q, 16 + ((k - 16) & 3)), (k - 16) >> 2);
         y[k] = d * static_cast<float>(t);
     }
 }
@@ -361,30 +433,34 @@ __device__ __forceinline__ void dequant_chunk<DT_TQ1_0>(const uint8_t *b, int c,
 // 32 h + m, value d (q - 1); f16 d at byte 64.  Chunk c: h = c / 4, l = c % 4.
 template <>
 __device__ __forceinline__ void dequant_chunk<DT_TQ2_0>(const uint8_t *b, int c, float *y) {
-    const float d = ldh(b + 64);
+    const float d = h2f(ldu2(b + 64));
     const int h = c >> 2, l = c & 3;
+    uint32_t q[8];
+    put16(q, ldu16(b + 32 * h), 0);
+    put16(q, ldu16(b + 32 * h + 16), 4);
+#pragma unroll
     for (int m = 0; m < 32; m++)
-        y[m] = d * static_cast<float>(static_cast<int>((b[32 * h + m] >> (2 * l)) & 3u) - 1);
+        y[m] = d * static_cast<float>(static_cast<int>((byte_k(q, m) >> (2 * l)) & 3u) - 1);
 }
 
 // src/quant_fmt_a.inc:71-83: Q1_0, one bit per value from the low bit, +d
-// for a 1 and -d for a 0
+// for a 1 and -d for a 0; chunk c is bytes 2 + 4c .. 2 + 4c + 3
 template <>
 __device__ __forceinline__ void dequant_chunk<DT_Q1_0>(const uint8_t *b, int c, float *y) {
-    const float d = ldh(b);
-    for (int k = 0; k < 32; k++) {
-        const int j = 32 * c + k;
-        y[k] = ((b[2 + (j >> 3)] >> (j & 7)) & 1u) ? d : -d;
-    }
+    const float d = h2f(ldu2(b));
+    const uint32_t w = ldu4(b + 2 + 4 * c);
+#pragma unroll
+    for (int k = 0; k < 32; k++) y[k] = ((w >> k) & 1u) ? d : -d;
 }
 // src/quant_fmt_a.inc:85-129: Q2_0 / PQ2_0 (128 values) and Q2_0_64 (64):
-// 2-bit codes four to a byte from the low pair, value (q - 1) * d
+// 2-bit codes four to a byte from the low pair, value (q - 1) * d; chunk c is
+// bytes 2 + 8c .. 2 + 8c + 7
 __device__ __forceinline__ void dequant_q2_0n(const uint8_t *b, int c, float *y) {
-    const float d = ldh(b);
-    for (int k = 0; k < 32; k++) {
-        const int j = 32 * c + k;
-        y[k] = static_cast<float>(static_cast<int>((b[2 + (j >> 2)] >> (2 * (j & 3))) & 3u) - 1) * d;
-    }
+    const float d = h2f(ldu2(b));
+    const u32x2 w = ldu8(b + 2 + 8 * c);
+#pragma unroll
+    for (int k = 0; k < 32; k++)
+        y[k] = static_cast<float>(static_cast<int>(((k < 16 ? w.x : w.y) >> (2 * (k & 15))) & 3u) - 1) * d;
 }
 template <>
 __device__ __forceinline__ void dequant_chunk<DT_Q2_0>(const uint8_t *b, int c, float *y) { dequant_q2_0n(b, c, y); }
@@ -394,16 +470,25 @@ template <>
 __device__ __forceinline__ void dequant_chunk<DT_Q2_0_64>(const uint8_t *b, int c, float *y) { dequant_q2_0n(b, c, y); }
 // src/quant.cpp:933-950: PTQ1_0, TQ1_0's trits at group 128, f16 d at 26:
 // v < 80 byte v % 16 trit v / 16; v < 120 byte 16 + (v - 80) % 8 trit
-// (v - 80) / 8; else byte 24 + (v - 120) % 2 trit (v - 120) / 2
+// (v - 80) / 8; else byte 24 + (v - 120) % 2 trit (v - 120) / 2.  The whole
+// 26 code bytes are loaded; each (chunk, k) names its byte and trit.
 template <>
 __device__ __forceinline__ void dequant_chunk<DT_PTQ1_0>(const uint8_t *b, int c, float *y) {
-    const float d = ldh(b + 26);
+    uint32_t q[7];
+    put16(q, ldu16(b), 0);
+    const u32x2 t8 = ldu8(b + 16);
+    q[4] = t8.x;
+    q[5] = t8.y;
+    const uint32_t dq = ldu4(b + 24);
+    q[6] = dq & 0xFFFFu;
+    const float d = h2f(dq >> 16);
+#pragma unroll
     for (int k = 0; k < 32; k++) {
         const int v = 32 * c + k;
         int t;
-        if (v < 80) t = tq1_trit(b[v & 15], v >> 4);
-        else if (v < 120) t = tq1_trit(b[16 + ((v - 80) & 7)], (v - 80) >> 3);
-        else t = tq1_trit(b[24 + ((v - 120) & 1)], (v - 120) >> 1);
+        if (v < 80) t = tq1_trit(byte_k(q, k & 15), v >> 4);
+        else if (v < 120) t = tq1_trit(byte_k(q, 16 + (k & 7)), (v - 80) >> 3);
+        else t = tq1_trit(byte_k(q, 24 + (k & 1)), (v - 120) >> 1);
         y[k] = d * static_cast<float>(t);
     }
 }
