@@ -40,7 +40,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--soak-seconds", type=float, default=3.0,
                     help="untimed back-to-back headline GEMVs before its timed steps")
-    ap.add_argument("--moe-tokens", default="1,16", help="comma list of MoE batch sizes to time")
+    ap.add_argument("--moe-tokens", default="1,16,512", help="comma list of MoE batch sizes to time")
+    ap.add_argument("--moe-exact-tokens", default="512",
+                    help="comma list of MoE batch sizes also timed under KRK_PATH_EXACT")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="counter run: 5 plain copies of 256 MiB, then 20 headline GEMVs")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
@@ -248,8 +250,9 @@ def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, 
         distinct.append(len(set(rid.reshape(-1).tolist())))
     per_expert = 2 * n_ff * K.row_bytes(K.Q4_K, n_embd) + n_embd * K.row_bytes(K.Q4_K, n_ff)
     nbytes = float(np.mean(distinct)) * per_expert + 4 * (2 * n_tok * n_embd + n_tok * n_expert)
+    flops = 2.0 * 3 * n_tok * k * n_embd * n_ff   # gate, up and down of every (token, slot) pair
     return {"us": ms * 1e3, "GBps": nbytes / ms / 1e6, "distinct_experts": float(np.mean(distinct)),
-            "bytes_per_call": nbytes}
+            "bytes_per_call": nbytes, "TFLOPs": flops / ms / 1e9}
 
 
 def bench_layer_grouped(K, torch, be, timer, copies=4):
@@ -642,7 +645,18 @@ def main():
             r = bench_moe(K, torch, be32, timer, T)
             r["frac_hbm"] = r["GBps"] / HBM_PEAK_GBS
             extras[f"moe_c5_t{T}"] = r
-            log(f"  {r['us']:.1f} us  {r['GBps']:.0f} GB/s  ({r['distinct_experts']:.1f} experts)")
+            log(f"  {r['us']:.1f} us  {r['GBps']:.0f} GB/s  {r['TFLOPs']:.1f} TFLOP/s  "
+                f"({r['distinct_experts']:.1f} experts)")
+        for T in (int(v) for v in args.moe_exact_tokens.split(",") if v):
+            log(f"moe C5 n_tok={T}, KRK_PATH_EXACT ...")
+            be32.set_gemm_path(K.PATH_EXACT)
+            try:
+                r = bench_moe(K, torch, be32, timer, T)
+            finally:
+                be32.set_gemm_path(K.PATH_AUTO)
+            r["frac_hbm"] = r["GBps"] / HBM_PEAK_GBS
+            extras[f"moe_c5_t{T}_exact"] = r
+            log(f"  {r['us']:.1f} us  {r['GBps']:.0f} GB/s  {r['TFLOPs']:.1f} TFLOP/s")
 
     # ---- CPU baseline (rank 0, N = 1) ----------------------------------------
     cpu = None

@@ -585,6 +585,7 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer, int n_expert,
     a.wt_down = uniform ? e0.type[2] : -1;
     a.rb_gate = e0.row_bytes[0]; a.rb_up = e0.row_bytes[1]; a.rb_down = e0.row_bytes[2];
     a.aligned16 = aligned;
+    a.mfma = b->path != KRK_PATH_EXACT;
     if (int s = ensure_ws(b, krk::moe_workspace(n_tok, k, n_expert, n_embd, n_ff))) return s;
     const hipError_t he = krk::moe_dispatch(a, b->ws, b->ws_bytes, b->stream);
     return he == hipSuccess ? KRK_OK : hip_fail(b, he, "moe_dispatch");

@@ -31,6 +31,7 @@
 
 #include "krk_formats.hpp"
 #include "krk_kernels.hpp"
+#include "krk_mi355x.h"
 
 namespace krk {
 
@@ -814,6 +815,302 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
         default: return hipErrorInvalidValue;
     }
 #undef KRK_GEMM_CASE
+}
+
+// ------------------------------------------------------ grouped expert GEMM
+// Prefill-sized MoE batches: each plan item (one expert, up to MT = 32 MI of
+// its (token, slot) pairs, activation rows gathered to f16 in plan order)
+// against one N tile of that expert's bank, on v_mfma_f32_16x16x32_f16.
+// The weights go from HBM straight into the MFMA B operand: each wave owns
+// two 16-row column blocks (gate/up: 16 gate rows and the same 16 up rows,
+// so both dots of an output land in one lane), and per 256-value block lane
+// group g = lane / 16 of row j = lane % 16 takes code bytes [16 g, 16 g + 16)
+// and [64 + 16 g, +16): the four groups of a row read its code bytes as two
+// whole 64-byte lines.  Slice s = 4 u + 2 nib + ih of a block (8 MFMAs of 32
+// values) takes, in group g, values 64 (2 u + g / 2) + 32 nib + 16 (g % 2)
+// + 8 ih + e, e < 8 (u: which 64 code bytes, nib: low or high nibbles); the
+// activation fragments are read from LDS at the same positions, so every
+// block's sum is unchanged by the permutation.  Raw weight bytes of the
+// next block are in flight while a block computes; the f16 activation rows
+// are staged a block at a time in two LDS buffers, one barrier per block.
+// An item holds all of an expert's pairs up to MT, so a batch reads each
+// active expert's weights about once.
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+
+// One lane's share of one 256-value block of one weight row.  bf[0], bf[1]:
+// slices 4 u + ih and 4 u + 2 + ih.
+template <int DT> struct LaneBlk {
+    WStage<DT> w[4];   // (u, nib) = chunk 4 u + 2 (g / 2) + nib, half g % 2
+    __device__ void fetch(const uint8_t *row, int blk, int g) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[i].fetch(row, 8 * blk + 4 * (i >> 1) + 2 * (g >> 1) + (i & 1), g & 1);
+    }
+    __device__ void decode(int blk, int g, int u, int ih, half8 (&bf)[2]) const {
+#pragma unroll
+        for (int nib = 0; nib < 2; nib++) {
+            _Float16 o[16];
+            w[2 * u + nib].decode(8 * blk + 4 * u + 2 * (g >> 1) + nib, o);
+#pragma unroll
+            for (int e = 0; e < 8; e++) bf[nib][e] = o[8 * ih + e];
+        }
+    }
+};
+// Q4_K: code byte pairs become the f16 pairs (1024 + q0, 1024 + q1) by one
+// byte permute (0x64 is the high byte of 1024.0 in f16, where the ulp is 1),
+// and each value is one mixed-precision FMA, f16(d1 (1024 + q) - c) with
+// c = 1024 d1 + m1 in f32 (1024 d1 exact).
+template <> struct LaneBlk<DT_Q4_K> {
+    uint32_t hdr[4], q[2][4];
+    __device__ void fetch(const uint8_t *row, int blk, int g) {
+        const uint8_t *b = row + static_cast<int64_t>(blk) * 144;
+        const u32x4 hv = ld128(b);
+        hdr[0] = hv.x; hdr[1] = hv.y; hdr[2] = hv.z; hdr[3] = hv.w;
+        const u32x4 v0 = ld128(b + 16 + 16 * g), v1 = ld128(b + 80 + 16 * g);
+        q[0][0] = v0.x; q[0][1] = v0.y; q[0][2] = v0.z; q[0][3] = v0.w;
+        q[1][0] = v1.x; q[1][1] = v1.y; q[1][2] = v1.z; q[1][3] = v1.w;
+    }
+    __device__ void decode(int, int g, int u, int ih, half8 (&bf)[2]) const {
+        const float d = h2f(hdr[0] & 0xFFFF), dmin = h2f(hdr[0] >> 16);
+        // sub-blocks 2 jp, 2 jp + 1 with jp = 2 u + g / 2 (get_scale_min_k4,
+        // quant.cpp:427-435, as Q4KPair)
+        const uint32_t sh = 16u * static_cast<uint32_t>((g >> 1) & 1);
+        const uint32_t Y = hdr[1] >> sh, Z = hdr[2] >> sh, W = hdr[3] >> sh;
+        const uint32_t A = u ? W : Y, Am = u ? (W >> 4) : Z, s2 = u ? 2u : 0u;
+        const uint32_t sa = (A & 15u) | ((Y >> s2) & 0x30u);
+        const uint32_t sb = ((A >> 8) & 15u) | ((Y >> (8u + s2)) & 0x30u);
+        const uint32_t ma = (Am & 15u) | ((Z >> s2) & 0x30u);
+        const uint32_t mb = ((Am >> 8) & 15u) | ((Z >> (8u + s2)) & 0x30u);
+        const float d1a = d * static_cast<float>(sa), d1b = d * static_cast<float>(sb);
+        const float ca = 1024.0f * d1a + dmin * static_cast<float>(ma);
+        const float cb = 1024.0f * d1b + dmin * static_cast<float>(mb);
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            const uint32_t w = q[u][2 * ih + tt];
+            const uint32_t l = w & 0x0F0F0F0Fu, hn = (w >> 4) & 0x0F0F0F0Fu;
+            const uint32_t pr[4] = {__builtin_amdgcn_perm(0x64646464u, l, 0x04010400u),
+                                    __builtin_amdgcn_perm(0x64646464u, l, 0x04030402u),
+                                    __builtin_amdgcn_perm(0x64646464u, hn, 0x04010400u),
+                                    __builtin_amdgcn_perm(0x64646464u, hn, 0x04030402u)};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const h16x2 hp = __builtin_bit_cast(h16x2, pr[k]);
+                const float dk = k < 2 ? d1a : d1b, ck = k < 2 ? ca : cb;
+                const int o = 4 * tt + 2 * (k & 1);
+                bf[k >> 1][o] = static_cast<_Float16>(__builtin_fmaf(dk, static_cast<float>(hp[0]), -ck));
+                bf[k >> 1][o + 1] = static_cast<_Float16>(__builtin_fmaf(dk, static_cast<float>(hp[1]), -ck));
+            }
+        }
+    }
+};
+
+constexpr int MG_THREADS = 512;
+
+template <int DT, bool GU, int MI>
+__global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K ? 4 : 2)))
+    moe_gemm_kernel(MoeGemmArgs a, int ntiles) {
+    constexpr int MT = 32 * MI;        // item rows
+    constexpr int MB = 2 * MI;         // 16-row M blocks
+    constexpr int LROW = 256 + 8;      // halves per LDS row (16-byte pad)
+    constexpr int SPT = MT * 256 / MG_THREADS;   // staged values per thread: 16 MI
+    constexpr int TPR = 256 / SPT;               // staging threads per row
+    __shared__ _Float16 Xs[2][MT * LROW];
+
+    // blockIdx -> (item, N tile): the hardware gives workgroup g to XCD
+    // g % 8, so every N tile of an item runs on one XCD (its activation rows
+    // stay in that L2) and the items, empty ones included, are dealt evenly
+    // over the XCDs.
+    const int gi = static_cast<int>(blockIdx.x), slot = gi >> 3;
+    const int item = (gi & 7) + 8 * (slot / ntiles), nt = slot % ntiles;
+    if (item >= *a.n_items) return;
+    const int32_t *it = a.items + 4 * item;
+    const int e = it[0], pb = it[1], rows = it[2];
+    const krk_moe_entry *en = static_cast<const krk_moe_entry *>(a.tab) + e;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 15, g = lane >> 4;
+    int row[2];
+    const uint8_t *wrow[2];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const uint8_t *wb;
+        if constexpr (GU) {
+            row[c] = nt * 128 + wave * 16 + j;
+            wb = static_cast<const uint8_t *>(en->p[c == 0 ? KRK_MOE_GATE : KRK_MOE_UP]);
+        } else {
+            row[c] = nt * 256 + wave * 32 + 16 * c + j;
+            wb = static_cast<const uint8_t *>(en->p[KRK_MOE_DOWN]);
+        }
+        wrow[c] = wb + static_cast<int64_t>(row[c] < a.N ? row[c] : a.N - 1) * a.row_bytes;
+    }
+
+    // this thread's staging slice: row sr, values [sc, sc + SPT) of each block
+    const int sr = tid / TPR, sc = (tid % TPR) * SPT;
+    const bool sok = sr < rows;
+    const _Float16 *xs = static_cast<const _Float16 *>(a.x) + static_cast<int64_t>(sok ? pb + sr : 0) * a.K + sc;
+    XStage<_Float16> xr[SPT / 16];
+    auto xfetch = [&](int blk) {
+#pragma unroll
+        for (int i = 0; i < SPT / 16; i++) xr[i].fetch(xs + 256 * blk + 16 * i, sok);
+    };
+    auto xstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < SPT / 16; i++) xr[i].store(&Xs[buf][sr * LROW + sc + 16 * i]);
+    };
+
+    const int nblk = a.K / 256;
+    floatx4 acc[MB][2];
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) acc[i][c] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Q4_K keeps two blocks of raw bytes in registers (the next block's
+    // requests are issued a whole block before it is decoded); the wider
+    // formats keep one (requested right after the block before is decoded).
+    constexpr bool DEEP = DT == DT_Q4_K && MI == 1;
+    struct Set { LaneBlk<DT> r[2]; };
+    auto block = [&](Set &ws, int blk) {
+        LaneBlk<DT>(&wr)[2] = ws.r;
+        const bool next = blk + 1 < nblk;
+        if (next) xfetch(blk + 1);
+        const _Float16 *xb = &Xs[blk & 1][j * LROW + 64 * (g >> 1) + 16 * (g & 1)];
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+#pragma unroll
+            for (int ih = 0; ih < 2; ih++) {
+                half8 bf[2][2];
+                wr[0].decode(blk, g, u, ih, bf[0]);
+                wr[1].decode(blk, g, u, ih, bf[1]);
+                if (!DEEP && u == 1 && ih == 1 && next) {
+                    wr[0].fetch(wrow[0], blk + 1, g);
+                    wr[1].fetch(wrow[1], blk + 1, g);
+                }
+#pragma unroll
+                for (int nib = 0; nib < 2; nib++)
+#pragma unroll
+                    for (int mb = 0; mb < MB; mb++) {
+                        const half8 af = *reinterpret_cast<const half8 *>(
+                            xb + mb * 16 * LROW + 128 * u + 32 * nib + 8 * ih);
+#pragma unroll
+                        for (int c = 0; c < 2; c++)
+                            acc[mb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[c][nib], acc[mb][c], 0, 0, 0);
+                    }
+            }
+        if (DEEP && blk + 2 < nblk) {
+            wr[0].fetch(wrow[0], blk + 2, g);
+            wr[1].fetch(wrow[1], blk + 2, g);
+        }
+        if (next) {
+            xstore((blk + 1) & 1);
+            __syncthreads();
+        }
+    };
+
+    Set ra;
+    std::conditional_t<DEEP, Set, Set &> rb = ra;
+    xfetch(0);
+    ra.r[0].fetch(wrow[0], 0, g);
+    ra.r[1].fetch(wrow[1], 0, g);
+    if (DEEP && nblk > 1) {
+        rb.r[0].fetch(wrow[0], 1, g);
+        rb.r[1].fetch(wrow[1], 1, g);
+    }
+    xstore(0);
+    __syncthreads();
+    for (int blk = 0; blk < nblk; blk += 2) {
+        block(ra, blk);
+        if (blk + 1 < nblk) block(rb, blk + 1);
+    }
+
+    // C fragment (16 x 16): lane holds column j, rows 4 g .. 4 g + 3 of each
+    // M block
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = mb * 16 + 4 * g + r;
+            if (m >= rows) continue;
+            if constexpr (GU) {
+                if (row[0] < a.N) {
+                    const float gt = acc[mb][0][r], up = acc[mb][1][r];
+                    static_cast<_Float16 *>(a.out)[static_cast<int64_t>(pb + m) * a.N + row[0]] =
+                        static_cast<_Float16>((gt / (1.0f + expf(-gt))) * up);
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < 2; c++)
+                    if (row[c] < a.N)
+                        static_cast<float *>(a.out)[static_cast<int64_t>(pb + m) * a.N + row[c]] = acc[mb][c][r];
+            }
+        }
+}
+
+// The items' activation rows in plan order as f16 (the GEMM's operand
+// rounding): row pos = x[plan_tok[pos]] for the live plan positions.
+__global__ void __launch_bounds__(256) moe_gather_f16_kernel(const float *__restrict__ x, int64_t n,
+                                                              const int32_t *__restrict__ plan_tok,
+                                                              const int32_t *__restrict__ n_live,
+                                                              _Float16 *__restrict__ xg) {
+    const int64_t pos = blockIdx.x;
+    if (pos >= *n_live) return;
+    const float *src = x + static_cast<int64_t>(plan_tok[pos]) * n;
+    _Float16 *dst = xg + pos * n;
+    for (int64_t i = 8 * static_cast<int64_t>(threadIdx.x); i < n; i += 8 * 256) {
+        const floatx4 v0 = *reinterpret_cast<const floatx4 *>(src + i);
+        const floatx4 v1 = *reinterpret_cast<const floatx4 *>(src + i + 4);
+        half8 h;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            h[k] = static_cast<_Float16>(v0[k]);
+            h[4 + k] = static_cast<_Float16>(v1[k]);
+        }
+        *reinterpret_cast<half8 *>(dst + i) = h;
+    }
+}
+
+hipError_t moe_gather_f16(const float *x, int64_t n, const int32_t *plan_tok, const int32_t *n_live,
+                          int64_t max_rows, _Float16 *xg, hipStream_t st) {
+    if (n % 8 || max_rows <= 0 || max_rows > (1LL << 31) - 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_gather_f16_kernel, dim3(static_cast<unsigned>(max_rows)), dim3(256), 0, st, x, n,
+                       plan_tok, n_live, xg);
+    return hipGetLastError();
+}
+
+#define KRK_MOE_GEMM_TYPES(X) X(DT_Q4_K) X(DT_Q5_K) X(DT_Q6_K) X(DT_Q8_0) X(DT_Q4_0) X(DT_MXFP4)
+
+bool moe_gemm_ok(int dt) {
+    switch (dt) {
+#define KRK_MG_OK(D) case D:
+        KRK_MOE_GEMM_TYPES(KRK_MG_OK)
+#undef KRK_MG_OK
+        return true;
+        default: return false;
+    }
+}
+
+template <int DT, bool GU>
+static hipError_t launch_moe_gemm(const MoeGemmArgs &a, hipStream_t st) {
+    if (a.K % 256 || a.N <= 0 || a.max_items <= 0) return hipErrorInvalidValue;
+    const int ntiles = (a.N + (GU ? 127 : 255)) / (GU ? 128 : 256);
+    const int64_t blocks = 8LL * ntiles * ((a.max_items + 7) / 8);
+    if (blocks > (1LL << 31) - 1) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>(blocks));
+    switch (a.mi) {
+        case 1: hipLaunchKernelGGL((moe_gemm_kernel<DT, GU, 1>), grid, dim3(MG_THREADS), 0, st, a, ntiles); break;
+        case 2: hipLaunchKernelGGL((moe_gemm_kernel<DT, GU, 2>), grid, dim3(MG_THREADS), 0, st, a, ntiles); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t moe_gemm(int dt, const MoeGemmArgs &a, hipStream_t st) {
+    switch (dt) {
+#define KRK_MG_CASE(D) \
+    case D: return a.gate_up ? launch_moe_gemm<D, true>(a, st) : launch_moe_gemm<D, false>(a, st);
+        KRK_MOE_GEMM_TYPES(KRK_MG_CASE)
+#undef KRK_MG_CASE
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace krk

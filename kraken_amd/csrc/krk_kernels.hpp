@@ -114,6 +114,28 @@ int device_cus();
 hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bool act_f16,
                      void *out, int64_t M, int64_t N, int64_t K, void *ws, size_t ws_bytes,
                      hipStream_t st);
+// Grouped expert GEMM on the f16 MFMA: one launch per projection over the
+// MoE plan's items {expert, first plan position, rows <= 32 mi, 0}; X holds
+// f16 activation rows in plan order [P, K].  Gate/up: out = f16 rows
+// silu(gate) * up per plan position [P, n_ff]; down: out = f32 part rows
+// per plan position [P, n_embd].  moe_gather_f16 writes the gate/up X from
+// the token rows (xg[pos] = f16(x[plan_tok[pos]]) for pos < *n_live).
+struct MoeGemmArgs {
+    const void *tab;           // krk_moe_entry[n_expert] of the layer
+    const int32_t *items;      // 4 per item
+    const int32_t *n_items;    // [1]
+    const void *x;
+    void *out;
+    int64_t row_bytes;         // gate = up row size (gate/up), down row size
+    int K, N;                  // K = n_embd, N = n_ff (gate/up); K = n_ff, N = n_embd (down)
+    int max_items;             // items the grid covers (an upper bound)
+    int mi;                    // item rows = 32 mi, mi in {1, 2}
+    bool gate_up;
+};
+bool moe_gemm_ok(int dt);
+hipError_t moe_gemm(int dt, const MoeGemmArgs &a, hipStream_t st);
+hipError_t moe_gather_f16(const float *x, int64_t n, const int32_t *plan_tok, const int32_t *n_live,
+                          int64_t max_rows, _Float16 *xg, hipStream_t st);
 size_t gemm_int8_workspace(int64_t M, int64_t K);
 bool gemm_int8_serves(int wt);
 hipError_t gemm_int8(int wt, const void *w, int64_t row_bytes, const void *x, bool act_f16, void *out,
@@ -148,6 +170,7 @@ struct MoeArgs {
     int wt_down;         // the experts' down weight type
     int64_t rb_gate, rb_up, rb_down;
     bool aligned16;      // every bank's rows start 16-byte aligned
+    bool mfma;           // the gemm path allows f16 MFMA products (not KRK_PATH_EXACT)
 };
 size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t n_ff);
 hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t st);

@@ -66,6 +66,7 @@ struct MoeWs {
     _Float16 *midf;     // [P, n_ff]      f16 activations: the row-scaled mid rows
     float *rscale;      // [P]            f16 activations: each mid row's power-of-two scale
     EmRun *runs;        // [n_expert]     active experts' banks and plan ranges
+    _Float16 *xg;       // [P, n_embd]    grouped GEMM: activation rows in plan order, f16
 };
 
 static size_t al(size_t v) { return (v + 255) & ~size_t(255); }
@@ -84,7 +85,8 @@ static MoeWs carve(void *ws, int64_t P, int ne, int64_t n_embd, int64_t n_ff) {
     w.n_items = reinterpret_cast<int32_t *>(p); p += al(4);
     w.midf = reinterpret_cast<_Float16 *>(p); p += al(P * n_ff * 2);
     w.rscale = reinterpret_cast<float *>(p); p += al(P * 4);
-    w.runs = reinterpret_cast<EmRun *>(p);
+    w.runs = reinterpret_cast<EmRun *>(p); p += al(ne * sizeof(EmRun));
+    w.xg = reinterpret_cast<_Float16 *>(p);
     return w;
 }
 
@@ -92,7 +94,7 @@ size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t
     const int64_t P = n_tok * k;
     return al((n_expert + 1) * 4) + al(n_expert * 4) + al(4) + 2 * al(P * 4) +
            al(P * n_ff * 4) + al(P * n_embd * 4) + al(P * 16) + al(4) + al(P * n_ff * 2) + al(P * 4) +
-           al(n_expert * sizeof(EmRun));
+           al(n_expert * sizeof(EmRun)) + al(P * n_embd * 2);
 }
 
 // ------------------------------------------------------------------ plan ----
@@ -104,7 +106,8 @@ constexpr int kPlanLds = 4096;  // (token, slot) pairs whose ids the plan keeps 
 constexpr int kItemRows = 2;    // activation rows of an expert item (the digit kernel's NX)
 __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict__ ids, int64_t P,
                                                         int k, int ne, MoeWs w,
-                                                        const krk_moe_entry *__restrict__ tab) {
+                                                        const krk_moe_entry *__restrict__ tab,
+                                                        int item_rows) {
     __shared__ int32_t cnt[1024];
     __shared__ int32_t cur[1024];
     __shared__ int32_t sid[kPlanLds];   // the ids, when they fit
@@ -122,8 +125,8 @@ __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict
     }
     __syncthreads();
     // exclusive scan over experts 4 tid .. 4 tid + 3 (ne <= 1024)
-    // items: each active expert's pairs in runs of up to kItemRows (the rows
-    // one digit-plane pass multiplies against the expert's weights)
+    // items: each active expert's pairs in runs of up to item_rows (the rows
+    // one pass of the digit kernel or the grouped GEMM takes)
     int c[4], run = 0, act = 0, its = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -131,7 +134,7 @@ __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict
         c[j] = e < ne ? cnt[e] : 0;
         run += c[j];
         act += c[j] > 0;
-        its += (c[j] + kItemRows - 1) / kItemRows;
+        its += (c[j] + item_rows - 1) / item_rows;
     }
     int ir = run, ia = act, ii = its;   // inclusive wave scans
     for (int d = 1; d < 64; d <<= 1) {
@@ -158,11 +161,11 @@ __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict
                 r.pe = base + c[j];
                 w.act[abase++] = e;
             }
-            for (int r = 0; r < c[j]; r += kItemRows) {
+            for (int r = 0; r < c[j]; r += item_rows) {
                 int32_t *it = w.items + 4 * ibase++;
                 it[0] = e;
                 it[1] = base + r;
-                it[2] = c[j] - r < kItemRows ? c[j] - r : kItemRows;
+                it[2] = c[j] - r < item_rows ? c[j] - r : item_rows;
                 it[3] = 0;
             }
         }
@@ -528,6 +531,9 @@ __global__ void __launch_bounds__(512) moe_down1_kernel(const krk_moe_entry *__r
 }
 
 constexpr int64_t kMoeTokenGroups = 64;
+// f32 batches from this many tokens take the grouped expert GEMM when the
+// gemm path allows f16 products
+constexpr int64_t kMoeGemmTokens = 32;
 
 hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t st) {
     const int64_t P = a.n_tok * a.k;
@@ -608,6 +614,49 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     const bool groups = on_digits && a.n_tok <= kMoeTokenGroups;
     const bool gu_ok = groups && gemv_digits_ok(DT_Q4_K, gu);
     const bool dn_ok = groups && gemv_digits_ok(DT_Q4_K, d);
+    // Prefill-sized batches under a gemm path that allows f16 products: the
+    // grouped expert GEMM (gemm.hip) over plan items of up to 32 mi pairs,
+    // mi (1 or 2) from the mean pairs per active expert, then the ordered
+    // reduce.
+    // f16 operands and f32 accumulation, as the dense GEMM above 8 rows.
+    if (a.mfma && !a.act_f16 && a.n_tok >= kMoeGemmTokens && a.aligned16 && a.wt >= 0 &&
+        a.rb_gate == a.rb_up && moe_gemm_ok(a.wt) && moe_gemm_ok(a.wt_down) && P <= (1 << 24)) {
+        const int64_t act = P < a.n_expert ? P : a.n_expert;
+        const int64_t per = (P + act - 1) / act;
+        const int mi = per <= 21 ? 1 : 2;
+        hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab,
+                           32 * mi);
+        MoeGemmArgs g{};
+        g.tab = tab;
+        g.items = w.items;
+        g.n_items = w.n_items;
+        const int64_t bound = act + P / (32 * mi);
+        g.max_items = static_cast<int>(bound < P ? bound : P);
+        g.mi = mi;
+        hipError_t e = moe_gather_f16(static_cast<const float *>(a.xn), a.n_embd, w.plan_tok, w.off + a.n_expert,
+                                      P, w.xg, st);
+        if (e != hipSuccess) return e;
+        g.x = w.xg;
+        g.out = w.midf;
+        g.row_bytes = a.rb_gate;
+        g.K = static_cast<int>(a.n_embd);
+        g.N = static_cast<int>(a.n_ff);
+        g.gate_up = true;
+        e = moe_gemm(a.wt, g, st);
+        if (e != hipSuccess) return e;
+        g.x = w.midf;
+        g.out = w.part;
+        g.row_bytes = a.rb_down;
+        g.K = static_cast<int>(a.n_ff);
+        g.N = static_cast<int>(a.n_embd);
+        g.gate_up = false;
+        e = moe_gemm(a.wt_down, g, st);
+        if (e != hipSuccess) return e;
+        const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));
+        hipLaunchKernelGGL((moe_reduce_kernel<float>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
+                           a.n_embd, w, static_cast<float *>(a.out));
+        return hipGetLastError();
+    }
     if (on_digits && a.n_tok >= 2) {
         // expert-major runs on the register-streaming kernel: one grid row
         // per active expert, whose weights are loaded once and applied to
@@ -640,7 +689,8 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
         ed.em_xrow = a.n_ff;
         ed.em_orow = a.n_embd;
         if (gemv_stream_ok(DT_Q4_K, eg) && gemv_stream_ok(DT_Q4_K, ed)) {
-            hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab);
+            hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab,
+                           kItemRows);
             hipError_t e = gemv_stream(DT_Q4_K, false, eg, st);
             if (e == hipSuccess) e = gemv_stream(DT_Q4_K, false, ed, st);
             if (e != hipSuccess) return e;
@@ -683,7 +733,8 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
         ed.em_xrow = a.n_ff;
         ed.em_orow = a.n_embd;
         if (P <= (1 << 20) && gemv_digits_ok(DT_Q4_K, eg) && gemv_digits_ok(DT_Q4_K, ed)) {
-            hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab);
+            hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab,
+                           kItemRows);
             hipError_t e = gemv_digits(DT_Q4_K, false, eg, st);
             if (e == hipSuccess) e = gemv_digits(DT_Q4_K, false, ed, st);
             if (e != hipSuccess) return e;
@@ -714,7 +765,8 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     // the plan path: every f16 dispatch (the reference GPU's rounding points
     // need each (token, slot) row whole before its scale), and f32 token
     // batches the digit kernels do not take
-    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab);
+    hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab,
+                           kItemRows);
     const int64_t amax = P < a.n_expert ? P : a.n_expert;
     const int64_t ggu = (a.n_ff + 1) / 2, gdn = (a.n_embd + 3) / 4;
     const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));

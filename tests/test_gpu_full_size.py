@@ -241,3 +241,46 @@ def test_config5_moe_layer(krk, torch_cuda, be32, c5_layer, n_tok):
     e = rel(host(out), ref)
     say("  rel", e)
     assert e <= GEMV_TOL
+
+
+@pytest.mark.parametrize("path", ["mfma", "exact"])
+def test_config5_moe_prefill_batch(krk, torch_cuda, be32, c5_layer, path):
+    """A prefill-sized batch (512 tokens, every expert active, 32 pairs per
+    expert on average) at the C5 shape.  Under the default gemm path it takes
+    the grouped expert GEMM (f16 products, the MFMA GEMM bar); under
+    KRK_PATH_EXACT the expert-major streaming runs (the GEMV bar).  Tokens
+    are independent of one another, so the oracle checks a sample of 12 of
+    them (first, last and ten spread between) on the device's routing."""
+    torch = torch_cuda
+    banks, table, _ = c5_layer
+    ne, n_embd, n_ff, k, n_tok = 128, 4096, 1536, 8, 512
+    logits = krk.synth_normal(n_tok * ne, seed=390).reshape(n_tok, ne)
+    x = krk.synth_normal(n_tok * n_embd, seed=391).reshape(n_tok, n_embd)
+    probs = torch.empty((n_tok, ne), dtype=torch.float32, device="cuda")
+    ids = torch.empty((n_tok, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((n_tok, k), dtype=torch.float32, device="cuda")
+    out = torch.full((n_tok, n_embd), float("nan"), dtype=torch.float32, device="cuda")
+    say("config 5 prefill", path)
+    be32.set_gemm_path(krk.PATH_EXACT if path == "exact" else krk.PATH_AUTO)
+    try:
+        be32.router_softmax(probs, dev(torch, logits), n_tok, ne)
+        be32.router_topk(probs, n_tok, ne, k, ids, wts, True, 1.0)
+        be32.moe_dispatch(table, 0, ne, ids, wts, dev(torch, x), out, n_tok, n_embd, n_ff, k)
+        be32.sync()
+    finally:
+        be32.set_gemm_path(krk.PATH_AUTO)
+        be32.moe_table_forget(table)
+    rid, rwt = host(ids), host(wts)
+    assert len(set(rid.reshape(-1).tolist())) == ne
+    sel = np.unique(np.r_[0, n_tok - 1, np.linspace(1, n_tok - 2, 10).astype(int)])
+    used = set(rid[sel].reshape(-1).tolist())
+    stand = banks[0, 0]
+    g = [banks[0, e] if e in used else stand for e in range(ne)]
+    u = [banks[1, e] if e in used else stand for e in range(ne)]
+    d = [banks[2, e] if e in used else stand for e in range(ne)]
+    ref = O.moe_ffn(x[sel], g, u, d, O.Q4_K, rid[sel], rwt[sel], n_ff, nthreads=16)
+    got = host(out)
+    assert np.isfinite(got).all()
+    e = rel(got[sel], ref)
+    say("  rel", e)
+    assert e <= (GEMM_TOL if path == "mfma" else GEMV_TOL)

@@ -310,6 +310,15 @@ def _forget_moe_tables(request):
     _TABLES.clear()
 
 
+@pytest.fixture
+def exact_path(krk, be32):
+    """KRK_PATH_EXACT for the test: f32 batches of 32 tokens and more take
+    the GEMV paths (the grouped MFMA GEMM otherwise)."""
+    be32.set_gemm_path(krk.PATH_EXACT)
+    yield
+    be32.set_gemm_path(krk.PATH_AUTO)
+
+
 def build_moe(krk, torch, dt, ne, n_embd, n_ff, seed):
     mats = {}
     entries = []
@@ -356,6 +365,7 @@ def test_moe_dispatch_parity(krk, torch_cuda, be32, n_tok, dt):
     assert e <= GEMV_TOL
 
 
+@pytest.mark.usefixtures("exact_path")
 @pytest.mark.parametrize("dt", [(O.Q4_K, O.Q4_K, O.Q6_K), (O.Q6_K, O.Q4_K, O.Q8_0)])
 @pytest.mark.parametrize("n_tok", [1, 5, 70])
 def test_moe_mixed_roles(krk, torch_cuda, be32, n_tok, dt):
@@ -586,6 +596,7 @@ def test_moe_table_record_evicts_oldest(krk, torch_cuda):
         be.close()
 
 
+@pytest.mark.usefixtures("exact_path")
 @pytest.mark.parametrize("n_tok,k,drop", [(1, 2, False), (1, 8, False), (1, 4, True), (3, 4, True),
                                           (16, 8, False), (70, 2, True), (520, 8, True)])
 def test_moe_dispatch_whole_units(krk, torch_cuda, be32, n_tok, k, drop):
