@@ -863,9 +863,9 @@ template <> struct LaneBlk<DT_Q4_K> {
     uint32_t hdr[4], q[2][4];
     __device__ void fetch(const uint8_t *row, int blk, int g) {
         const uint8_t *b = row + static_cast<int64_t>(blk) * 144;
-        const u32x4 hv = ld128(b);
+        const u32x4 hv = ldg128(b);
         hdr[0] = hv.x; hdr[1] = hv.y; hdr[2] = hv.z; hdr[3] = hv.w;
-        const u32x4 v0 = ld128(b + 16 + 16 * g), v1 = ld128(b + 80 + 16 * g);
+        const u32x4 v0 = ldg128(b + 16 + 16 * g), v1 = ldg128(b + 80 + 16 * g);
         q[0][0] = v0.x; q[0][1] = v0.y; q[0][2] = v0.z; q[0][3] = v0.w;
         q[1][0] = v1.x; q[1][1] = v1.y; q[1][2] = v1.z; q[1][3] = v1.w;
     }
@@ -996,14 +996,14 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
                             acc[mb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[c][nib], acc[mb][c], 0, 0, 0);
                     }
             }
+        // the next block's activations go to LDS before this set's refill is
+        // requested: their wait then covers only loads issued before them
+        if (next) xstore((blk + 1) & 1);
         if (DEEP && blk + 2 < nblk) {
             wr[0].fetch(wrow[0], blk + 2, g);
             wr[1].fetch(wrow[1], blk + 2, g);
         }
-        if (next) {
-            xstore((blk + 1) & 1);
-            __syncthreads();
-        }
+        if (next) __syncthreads();
     };
 
     Set ra;

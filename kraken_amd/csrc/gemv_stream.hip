@@ -70,6 +70,15 @@ __device__ __forceinline__ uint32_t ld32_a2(const uint8_t *p) {
     __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 4);
     return v;
 }
+// the same through global-space pointers (the weight requests)
+typedef u32x4 u32x4_a2 __attribute__((aligned(2)));
+typedef uint32_t u32_a2 __attribute__((aligned(2)));
+__device__ __forceinline__ u32x4 ld128_a2(gbyte *p) {
+    return *(const __attribute__((address_space(1))) u32x4_a2 *)p;
+}
+__device__ __forceinline__ uint32_t ld32_a2(gbyte *p) {
+    return *(const __attribute__((address_space(1))) u32_a2 *)p;
+}
 
 // quad-lane exchanges (lanes l ^ 1 and l ^ 2) through DPP
 __device__ __forceinline__ float quad_xor1(float v) {
@@ -213,7 +222,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     uint32_t dd[QS ? NL : 1];
     u32x4 qc[Q80 ? NL : 1];
     const int h6 = gq >> 1, lh6 = gq & 1;
-    const uint8_t *src[NL];
+    gbyte *src[NL];
 #pragma unroll
     for (int i = 0; i < NL; i++) {
         const int rg = i / NBW, b = i - (i / NBW) * NBW;
@@ -230,7 +239,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
         if (n >= n_out) n = n_out - 1;
         // a ragged last slice re-reads the matrix's last block (discarded)
         const int blk = (kb0 + b < nb ? kb0 + b : nb - 1) - kb0 + kblk;
-        src[i] = base + n * rb + static_cast<int64_t>(blk) * BB;
+        src[i] = to_global(base + n * rb + static_cast<int64_t>(blk) * BB);
     }
     auto issue = [&](int i) {
         if constexpr (Q6) {

@@ -48,6 +48,18 @@ __device__ __forceinline__ u32x4 ld128(const uint8_t *p) {
 __device__ __forceinline__ u32x2 ld64(const uint8_t *p) {
     return *reinterpret_cast<const u32x2 *>(p);
 }
+// Device (global) memory through a pointer the compiler cannot place: one
+// read from memory (a table entry, a run record) is generic to it, and loads
+// through a generic pointer are FLAT instructions, which also count against
+// lgkmcnt, so every wait for an LDS read would wait for them too and
+// prefetched weights would stop being in flight across LDS work.  gbyte
+// pointers load with global instructions.
+typedef const __attribute__((address_space(1))) uint8_t gbyte;
+__device__ __forceinline__ gbyte *to_global(const uint8_t *p) { return (gbyte *)p; }
+__device__ __forceinline__ u32x4 ld128(gbyte *p) {
+    return *(const __attribute__((address_space(1))) u32x4 *)p;
+}
+__device__ __forceinline__ u32x4 ldg128(const uint8_t *p) { return ld128(to_global(p)); }
 
 // ({hi,lo} >> 8*s)[31:0], s in 0..3 (v_alignbyte_b32).
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
