@@ -129,10 +129,9 @@ template <> struct WStage<DT_Q6_K> {
         load_bytes2<4>(b + 64 * h + 32 * (qd & 1) + 16 * hf, ql);
         load_bytes2<4>(b + 128 + 32 * h + 16 * hf, qh);
         // scale byte sc[8h + 2qd + hf] and d (bytes 208..209)
-        const uintptr_t sa = reinterpret_cast<uintptr_t>(b + 192 + 8 * h + 2 * qd + hf);
-        sw = ld32(reinterpret_cast<const uint8_t *>(sa & ~uintptr_t(3))) >> (8 * (sa & 3));
+        sw = ld32_at(b + 192 + 8 * h + 2 * qd + hf);
         const uintptr_t da = reinterpret_cast<uintptr_t>(b + 208);
-        dw = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        dw = ld32_at(b + 208);
     }
     __device__ void decode(int kt, _Float16 (&o)[16]) const {
         const int c = kt & 7, qd = c & 3;
@@ -187,8 +186,7 @@ template <> struct WStage<DT_Q8_0> {
     __device__ void fetch(const uint8_t *row, int kt, int hf) {
         const uint8_t *b = row + kt * 34;
         load_bytes2<4>(b + 2 + 16 * hf, q);
-        const uintptr_t da = reinterpret_cast<uintptr_t>(b);
-        dw = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        dw = ld32_at(b);
     }
     __device__ void decode(int, _Float16 (&o)[16]) const {
         const float d = h2f(dw & 0xFFFF);
@@ -208,7 +206,7 @@ template <> struct WStage<DT_Q4_0> {
         const uint8_t *b = row + kt * 18;
         load_bytes2<4>(b + 2, q);
         const uintptr_t da = reinterpret_cast<uintptr_t>(b);
-        dw = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        dw = ld32_at(b);
         hf_ = hf;
     }
     __device__ void decode(int, _Float16 (&o)[16]) const {
@@ -232,7 +230,7 @@ template <> struct WStage<DT_IQ4_NL> {
         const uint8_t *b = row + kt * 18;
         load_bytes2<4>(b + 2, q);
         const uintptr_t da = reinterpret_cast<uintptr_t>(b);
-        dw = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        dw = ld32_at(b);
         hf_ = hf;
     }
     __device__ void decode(int, _Float16 (&o)[16]) const {

@@ -171,8 +171,7 @@ template <> struct I8W<DT_Q6_K> {
         const int ns = 4 * (qd >> 1), hs = 2 * qd;
 #pragma unroll
         for (int k = 0; k < 8; k++) q[k] = ((ql[k] >> ns) & 0x0F0F0F0Fu) | (((qh[k] >> hs) & 0x03030303u) << 4);
-        const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
-        const float d = h2f((ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3))) & 0xFFFF);
+        const float d = h2f((ld32_at(blk + 208)) & 0xFFFF);
 #pragma unroll
         for (int g = 0; g < 2; g++)
             bsc[g] = d * static_cast<float>(static_cast<int8_t>(byte_at(blk + 192 + 8 * n + 2 * qd + g)));

@@ -42,6 +42,14 @@ __device__ __forceinline__ float h2f(uint32_t h16) {
 __device__ __forceinline__ uint32_t ld32(const uint8_t *p) {
     return *reinterpret_cast<const uint32_t *>(p);
 }
+// The bytes from p to the end of the 4-aligned dword that holds p, in the
+// low bits (zeros above).  The aligned address comes from pointer
+// arithmetic, which keeps p's address space (an integer round trip would
+// make the load a FLAT one).
+__device__ __forceinline__ uint32_t ld32_at(const uint8_t *p) {
+    const uint32_t o = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3);
+    return ld32(p - o) >> (8 * o);
+}
 __device__ __forceinline__ u32x4 ld128(const uint8_t *p) {
     return *reinterpret_cast<const u32x4 *>(p);
 }

@@ -514,16 +514,14 @@ __device__ __forceinline__ void load_bytes2(const uint8_t *p, uint32_t (&o)[NW])
 
 // the byte at p, from the 4-aligned dword that holds it
 __device__ __forceinline__ uint32_t byte_at(const uint8_t *p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    return (ld32(reinterpret_cast<const uint8_t *>(a & ~uintptr_t(3))) >> (8 * (a & 3))) & 0xFF;
+    return ld32_at(p) & 0xFF;
 }
 
 // (any byte alignment works: the window shift is a & 3)
 template <int NW>
 __device__ __forceinline__ void load_bytes2(const uint8_t *p, uint32_t (&o)[NW]) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint8_t *base = reinterpret_cast<const uint8_t *>(a & ~uintptr_t(3));
-    const uint32_t s = static_cast<uint32_t>(a & 3);
+    const uint32_t s = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3);
+    const uint8_t *base = p - s;   // pointer arithmetic keeps p's address space
     uint32_t d[NW + 1];
 #pragma unroll
     for (int k = 0; k < NW; k++) d[k] = ld32(base + 4 * k);
@@ -577,7 +575,7 @@ __device__ __forceinline__ void load_l32(const uint8_t *blk, uint32_t *raw) {
         load_bytes2<1>(blk, dm);
     } else {
         const uintptr_t da = reinterpret_cast<uintptr_t>(blk);
-        dm[0] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        dm[0] = ld32_at(blk);
     }
     raw[0] = q[0]; raw[1] = q[1]; raw[2] = q[2]; raw[3] = q[3];
     raw[4] = h[0]; raw[5] = dm[0];
@@ -742,7 +740,7 @@ template <> struct LaneFmt<DT_Q6_K> {
         // d is the last two bytes of the block; read the dword that holds them
         // without touching anything past the block.
         const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
-        raw[8] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        raw[8] = ld32_at(blk + 208);
         raw[0] = a[0]; raw[1] = a[1]; raw[2] = b[0]; raw[3] = b[1];
         raw[4] = q[0]; raw[5] = q[1]; raw[6] = s[0]; raw[7] = s[1];
     }
@@ -804,7 +802,7 @@ __device__ __forceinline__ int q3k_scale_w(uint32_t R0, uint32_t R1, uint32_t R2
 // 4-aligned dword that holds them, which never leaves the block's page
 __device__ __forceinline__ uint32_t q3k_d_word(const uint8_t *blk) {
     const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 108);
-    return ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+    return ld32_at(blk + 108);
 }
 
 // Q2_K lane view: piece p, half h = p / 4, bytes o = 8 (p % 4) .. +7 of the
@@ -890,7 +888,7 @@ template <> struct LaneFmt<DT_Q4_0> {
         uint32_t q[4];
         load_bytes2<4>(blk + 2, q);
         const uintptr_t da = reinterpret_cast<uintptr_t>(blk);
-        raw[4] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        raw[4] = ld32_at(blk);
         raw[0] = q[0]; raw[1] = q[1]; raw[2] = q[2]; raw[3] = q[3];
     }
     __device__ static float dot(const uint32_t (&raw)[NRAW], int, const float (&xv)[32],
@@ -1087,7 +1085,7 @@ template <> struct LaneFmt<DT_Q8_0> {
         uint32_t q[8];
         load_bytes2<8>(blk + 2, q);
         const uintptr_t da = reinterpret_cast<uintptr_t>(blk);
-        raw[8] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        raw[8] = ld32_at(blk);
 #pragma unroll
         for (int k = 0; k < 8; k++) raw[k] = q[k];
     }
@@ -1233,7 +1231,7 @@ template <> struct WaveFmt<DT_Q6_K> {
         load_bytes2<4>(blk + 128 + 32 * h + l0, q);
         load_bytes2<2>(blk + 192 + 8 * h, s);
         const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
-        raw[14] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+        raw[14] = ld32_at(blk + 208);
 #pragma unroll
         for (int k = 0; k < 4; k++) { raw[k] = a[k]; raw[4 + k] = b[k]; raw[8 + k] = q[k]; }
         raw[12] = s[0]; raw[13] = s[1];
@@ -1386,8 +1384,7 @@ template <> struct WaveFmt<DT_Q4_0> {
             const uint8_t *b = blk + 18 * u;
             uint32_t q[4];
             load_bytes2<4>(b + 2, q);
-            const uintptr_t da = reinterpret_cast<uintptr_t>(b);
-            raw[5 * u + 4] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+            raw[5 * u + 4] = ld32_at(b);
 #pragma unroll
             for (int k = 0; k < 4; k++) raw[5 * u + k] = q[k];
         }
@@ -1565,7 +1562,7 @@ template <> struct WaveFmt<DT_Q8_0> {
             uint32_t q[8];
             load_bytes2<8>(b + 2, q);
             const uintptr_t da = reinterpret_cast<uintptr_t>(b);
-            raw[9 * u + 8] = ld32(reinterpret_cast<const uint8_t *>(da & ~uintptr_t(3))) >> (8 * (da & 3));
+            raw[9 * u + 8] = ld32_at(b);
 #pragma unroll
             for (int k = 0; k < 8; k++) raw[9 * u + k] = q[k];
         }
