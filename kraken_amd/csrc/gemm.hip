@@ -130,7 +130,6 @@ template <> struct WStage<DT_Q6_K> {
         load_bytes2<4>(b + 128 + 32 * h + 16 * hf, qh);
         // scale byte sc[8h + 2qd + hf] and d (bytes 208..209)
         sw = ld32_at(b + 192 + 8 * h + 2 * qd + hf);
-        const uintptr_t da = reinterpret_cast<uintptr_t>(b + 208);
         dw = ld32_at(b + 208);
     }
     __device__ void decode(int kt, _Float16 (&o)[16]) const {
@@ -205,7 +204,6 @@ template <> struct WStage<DT_Q4_0> {
     __device__ void fetch(const uint8_t *row, int kt, int hf) {
         const uint8_t *b = row + kt * 18;
         load_bytes2<4>(b + 2, q);
-        const uintptr_t da = reinterpret_cast<uintptr_t>(b);
         dw = ld32_at(b);
         hf_ = hf;
     }
@@ -229,7 +227,6 @@ template <> struct WStage<DT_IQ4_NL> {
     __device__ void fetch(const uint8_t *row, int kt, int hf) {
         const uint8_t *b = row + kt * 18;
         load_bytes2<4>(b + 2, q);
-        const uintptr_t da = reinterpret_cast<uintptr_t>(b);
         dw = ld32_at(b);
         hf_ = hf;
     }

@@ -574,7 +574,6 @@ __device__ __forceinline__ void load_l32(const uint8_t *blk, uint32_t *raw) {
     if constexpr (L::M) {
         load_bytes2<1>(blk, dm);
     } else {
-        const uintptr_t da = reinterpret_cast<uintptr_t>(blk);
         dm[0] = ld32_at(blk);
     }
     raw[0] = q[0]; raw[1] = q[1]; raw[2] = q[2]; raw[3] = q[3];
@@ -739,7 +738,6 @@ template <> struct LaneFmt<DT_Q6_K> {
         load_bytes2<2>(blk + 192 + 8 * h, s);
         // d is the last two bytes of the block; read the dword that holds them
         // without touching anything past the block.
-        const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
         raw[8] = ld32_at(blk + 208);
         raw[0] = a[0]; raw[1] = a[1]; raw[2] = b[0]; raw[3] = b[1];
         raw[4] = q[0]; raw[5] = q[1]; raw[6] = s[0]; raw[7] = s[1];
@@ -801,7 +799,6 @@ __device__ __forceinline__ int q3k_scale_w(uint32_t R0, uint32_t R1, uint32_t R2
 // Q3_K's d (bytes 108..109) in the low half of a dword, read from the
 // 4-aligned dword that holds them, which never leaves the block's page
 __device__ __forceinline__ uint32_t q3k_d_word(const uint8_t *blk) {
-    const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 108);
     return ld32_at(blk + 108);
 }
 
@@ -887,7 +884,6 @@ template <> struct LaneFmt<DT_Q4_0> {
     __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
         uint32_t q[4];
         load_bytes2<4>(blk + 2, q);
-        const uintptr_t da = reinterpret_cast<uintptr_t>(blk);
         raw[4] = ld32_at(blk);
         raw[0] = q[0]; raw[1] = q[1]; raw[2] = q[2]; raw[3] = q[3];
     }
@@ -1084,7 +1080,6 @@ template <> struct LaneFmt<DT_Q8_0> {
     __device__ static void load(uint32_t (&raw)[NRAW], const uint8_t *blk, int) {
         uint32_t q[8];
         load_bytes2<8>(blk + 2, q);
-        const uintptr_t da = reinterpret_cast<uintptr_t>(blk);
         raw[8] = ld32_at(blk);
 #pragma unroll
         for (int k = 0; k < 8; k++) raw[k] = q[k];
@@ -1230,7 +1225,6 @@ template <> struct WaveFmt<DT_Q6_K> {
         load_bytes2<4>(blk + 64 * h + 32 + l0, b);
         load_bytes2<4>(blk + 128 + 32 * h + l0, q);
         load_bytes2<2>(blk + 192 + 8 * h, s);
-        const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
         raw[14] = ld32_at(blk + 208);
 #pragma unroll
         for (int k = 0; k < 4; k++) { raw[k] = a[k]; raw[4 + k] = b[k]; raw[8 + k] = q[k]; }
@@ -1561,7 +1555,6 @@ template <> struct WaveFmt<DT_Q8_0> {
             const uint8_t *b = blk + 34 * u;
             uint32_t q[8];
             load_bytes2<8>(b + 2, q);
-            const uintptr_t da = reinterpret_cast<uintptr_t>(b);
             raw[9 * u + 8] = ld32_at(b);
 #pragma unroll
             for (int k = 0; k < 8; k++) raw[9 * u + k] = q[k];
