@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--soak-seconds", type=float, default=3.0,
                     help="untimed back-to-back headline GEMVs before its timed steps")
     ap.add_argument("--moe-tokens", default="1,16,512", help="comma list of MoE batch sizes to time")
+    ap.add_argument("--moe-q4km-tokens", default="16,512",
+                    help="comma list of MoE batch sizes also timed with Q6_K down banks (Q4_K_M)")
     ap.add_argument("--moe-exact-tokens", default="512",
                     help="comma list of MoE batch sizes also timed under KRK_PATH_EXACT")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -206,11 +208,22 @@ def q4k_random_rows(torch, n_rows, n_in, gen):
     return w.reshape(n_rows, nb * 144)
 
 
-def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, k=8, calls=64):
+def q6k_random_rows(torch, n_rows, n_in, gen):
+    """Q6_K rows of random codes and scales with d = 2^-10 (bytes 208..209)."""
+    nb = n_in // 256
+    w = torch.randint(0, 256, (n_rows, nb, 210), dtype=torch.uint8, device="cuda", generator=gen)
+    w[:, :, 208] = 0x00
+    w[:, :, 209] = 0x14
+    return w.reshape(n_rows, nb * 210)
+
+
+def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, k=8, calls=64, down=None):
     """qwen3moe-shaped experts (Q4_K gate/up [1536, 4096],
     down [4096, 1536]), router softmax -> top-8 -> normalize -> dispatch.
     Each timed call routes a different seeded logits block, so the experts
-    read vary and the 1.36 GB bank streams from HBM."""
+    read vary and the 1.36 GB bank streams from HBM.  down = K.Q6_K: the
+    Q4_K_M layout (Q6_K down banks)."""
+    down = K.Q4_K if down is None else down
     import numpy as np
     gen = torch.Generator(device="cuda")
     gen.manual_seed(5)
@@ -218,12 +231,13 @@ def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, 
     for e in range(n_expert):
         ent = K.MoeEntry()
         for m, (o, i) in enumerate(((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff))):
-            t = q4k_random_rows(torch, o, i, gen)
+            dt = down if m == 2 else K.Q4_K
+            t = (q6k_random_rows if dt == K.Q6_K else q4k_random_rows)(torch, o, i, gen)
             mats.append(t)
             ent.p[m] = t.data_ptr()
             ent.n_out[m], ent.n_in[m] = o, i
-            ent.row_bytes[m] = K.row_bytes(K.Q4_K, i)
-            ent.type[m] = K.Q4_K
+            ent.row_bytes[m] = K.row_bytes(dt, i)
+            ent.type[m] = dt
             ent.present[m] = 1
         entries.append(ent)
     table = torch.from_numpy(np.frombuffer(K.moe_table_bytes(entries), np.uint8).copy()).cuda()
@@ -248,7 +262,7 @@ def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, 
     for i in range(calls):
         rid, _ = O.router_topk(O.router_softmax(lg[i]), k)
         distinct.append(len(set(rid.reshape(-1).tolist())))
-    per_expert = 2 * n_ff * K.row_bytes(K.Q4_K, n_embd) + n_embd * K.row_bytes(K.Q4_K, n_ff)
+    per_expert = 2 * n_ff * K.row_bytes(K.Q4_K, n_embd) + n_embd * K.row_bytes(down, n_ff)
     nbytes = float(np.mean(distinct)) * per_expert + 4 * (2 * n_tok * n_embd + n_tok * n_expert)
     flops = 2.0 * 3 * n_tok * k * n_embd * n_ff   # gate, up and down of every (token, slot) pair
     return {"us": ms * 1e3, "GBps": nbytes / ms / 1e6, "distinct_experts": float(np.mean(distinct)),
@@ -640,13 +654,19 @@ def main():
             log(f"  head {nm} {r['ms'] * 1e3:.1f} us {r['GBps']:.0f} GB/s")
 
     if want("moe"):
-        for T in (int(v) for v in args.moe_tokens.split(",")):
+        for T in (int(v) for v in args.moe_tokens.split(",") if v):
             log(f"moe C5 n_tok={T} ...")
             r = bench_moe(K, torch, be32, timer, T)
             r["frac_hbm"] = r["GBps"] / HBM_PEAK_GBS
             extras[f"moe_c5_t{T}"] = r
             log(f"  {r['us']:.1f} us  {r['GBps']:.0f} GB/s  {r['TFLOPs']:.1f} TFLOP/s  "
                 f"({r['distinct_experts']:.1f} experts)")
+        for T in (int(v) for v in args.moe_q4km_tokens.split(",") if v):
+            log(f"moe C5 n_tok={T}, Q6_K down banks ...")
+            r = bench_moe(K, torch, be32, timer, T, down=K.Q6_K)
+            r["frac_hbm"] = r["GBps"] / HBM_PEAK_GBS
+            extras[f"moe_c5_q4km_t{T}"] = r
+            log(f"  {r['us']:.1f} us  {r['GBps']:.0f} GB/s  {r['TFLOPs']:.1f} TFLOP/s")
         for T in (int(v) for v in args.moe_exact_tokens.split(",") if v):
             log(f"moe C5 n_tok={T}, KRK_PATH_EXACT ...")
             be32.set_gemm_path(K.PATH_EXACT)

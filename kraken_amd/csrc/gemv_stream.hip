@@ -695,7 +695,11 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
     // several activation rows: dense Q4_K, up to kStreamRows, rows 16-byte aligned
     if (t.rows > 1 && (dt != DT_Q4_K || t.rows > kStreamRows || t.moe_tab || t.x_stride % 4)) return false;
     if (t.moe_tab) {
-        if (dt != DT_Q4_K || t.n_in % 256 || t.row_bytes % 16) return false;
+        // Q4_K banks; the down bank may also be Q6_K (Q4_K_M layers: its
+        // 210-byte blocks need only 2-byte aligned rows)
+        const bool down = t.moe_down || (t.em_runs && t.seg[0].kind == SEG_PLAIN);
+        if (!(dt == DT_Q4_K || (dt == DT_Q6_K && down)) || t.n_in % 256 || t.row_bytes % (dt == DT_Q6_K ? 2 : 16))
+            return false;
         const int nb = t.n_in / 256, nbw = stream_nbw(nb);
         if (t.em_runs) {
             // expert-major runs, Q4_K banks: gate/up pairs (n_in of at most
@@ -754,7 +758,25 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
         // routed experts (f32 activations, Q4_K): gate/up pairs take 32-row
         // tiles (16 + 16), the down projection 16-row tiles when its slices
         // are wider than two blocks
-        if (act_f16 || dt != DT_Q4_K) return hipErrorNotSupported;
+        if (act_f16 || !(dt == DT_Q4_K || dt == DT_Q6_K)) return hipErrorNotSupported;
+        if (dt == DT_Q6_K) {   // the down bank of a Q4_K_M layer
+            if (t.em_runs) {
+                if (t.seg[0].kind == SEG_SILU) return hipErrorNotSupported;
+                const int64_t width = (t.seg[0].n_out + 15) / 16;
+                switch (nbw) {
+                    case 2: return launch<DT_Q6_K, float, float, 2, 16, 4>(t, width, nw, st);
+                    case 3: return launch<DT_Q6_K, float, float, 3, 16, 4>(t, width, nw, st);
+                    default: return launch<DT_Q6_K, float, float, 4, 16, 4>(t, width, nw, st);
+                }
+            }
+            if (!t.moe_down) return hipErrorNotSupported;
+            const int64_t width = (t.seg[0].n_out + 15) / 16;
+            switch (nbw) {
+                case 2: return launch<DT_Q6_K, float, float, 2, 16, 2>(t, width, nw, st);
+                case 3: return launch<DT_Q6_K, float, float, 3, 16, 2>(t, width, nw, st);
+                default: return launch<DT_Q6_K, float, float, 4, 16, 2>(t, width, nw, st);
+            }
+        }
         if (t.em_runs) {
             if (t.seg[0].kind == SEG_SILU)
                 return launch<DT_Q4_K, float, float, 2, 32, 3>(t, (t.seg[0].n_out + 15) / 16, nw, st);

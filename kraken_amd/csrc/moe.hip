@@ -608,9 +608,12 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     // digit kernel serve up to kMoeTokenGroups tokens (each token reads its
     // experts for itself), expert-major items of kItemRows tokens larger
     // batches, and the plan path whatever the digit kernel cannot take.
-    const bool on_digits = !a.act_f16 && a.wt == DT_Q4_K && a.wt_down == DT_Q4_K && a.aligned16 &&
-                           a.rb_gate == a.rb_up &&
-                           a.k <= kMaxSegs && a.k * a.n_ff <= (1 << 30);
+    // Q4_K gate/up; the streaming kernel also takes a Q6_K down bank (Q4_K_M
+    // layers), the digit kernel only Q4_K
+    const bool q4k_gu = !a.act_f16 && a.wt == DT_Q4_K && a.aligned16 && a.rb_gate == a.rb_up &&
+                        a.k <= kMaxSegs && a.k * a.n_ff <= (1 << 30);
+    const bool on_digits = q4k_gu && a.wt_down == DT_Q4_K;
+    const bool on_stream = q4k_gu && (a.wt_down == DT_Q4_K || a.wt_down == DT_Q6_K);
     const bool groups = on_digits && a.n_tok <= kMoeTokenGroups;
     const bool gu_ok = groups && gemv_digits_ok(DT_Q4_K, gu);
     const bool dn_ok = groups && gemv_digits_ok(DT_Q4_K, d);
@@ -657,7 +660,7 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
                            a.n_embd, w, static_cast<float *>(a.out));
         return hipGetLastError();
     }
-    if (on_digits && a.n_tok >= 2) {
+    if (on_stream && a.n_tok >= 2) {
         // expert-major runs on the register-streaming kernel: one grid row
         // per active expert, whose weights are loaded once and applied to
         // each of its tokens in turn; then the ordered per-token reduce
@@ -688,11 +691,11 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
         ed.em_tok = nullptr;
         ed.em_xrow = a.n_ff;
         ed.em_orow = a.n_embd;
-        if (gemv_stream_ok(DT_Q4_K, eg) && gemv_stream_ok(DT_Q4_K, ed)) {
+        if (gemv_stream_ok(DT_Q4_K, eg) && gemv_stream_ok(a.wt_down, ed)) {
             hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab,
                            kItemRows);
             hipError_t e = gemv_stream(DT_Q4_K, false, eg, st);
-            if (e == hipSuccess) e = gemv_stream(DT_Q4_K, false, ed, st);
+            if (e == hipSuccess) e = gemv_stream(a.wt_down, false, ed, st);
             if (e != hipSuccess) return e;
             const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));
             hipLaunchKernelGGL((moe_reduce_kernel<float>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
@@ -743,6 +746,12 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
                                a.n_embd, w, static_cast<float *>(a.out));
             return hipGetLastError();
         }
+    }
+    if (on_stream && !on_digits && a.n_tok == 1 && gemv_stream_ok(DT_Q4_K, gu) && gemv_stream_ok(a.wt_down, d)) {
+        // one token of a Q4_K_M layer: both launches on the streaming kernel
+        const hipError_t e = gemv_stream(DT_Q4_K, false, gu, st);
+        if (e != hipSuccess) return e;
+        return gemv_stream(a.wt_down, false, d, st);
     }
     if (gu_ok && (dn_ok || a.n_tok == 1)) {
         // one token: the register-streaming kernel where it takes the shapes

@@ -284,3 +284,59 @@ def test_config5_moe_prefill_batch(krk, torch_cuda, be32, c5_layer, path):
     e = rel(got[sel], ref)
     say("  rel", e)
     assert e <= (GEMM_TOL if path == "mfma" else GEMV_TOL)
+
+
+def q6k_random_bank(rng, n_rows, n_in):
+    """Q6_K rows of random codes and scales with d = 2^-10."""
+    nb = n_in // 256
+    w = rng.integers(0, 256, size=(n_rows, nb, 210), dtype=np.uint8)
+    w[:, :, 208:210] = [0x00, 0x14]
+    return w.reshape(-1)
+
+
+@pytest.mark.parametrize("n_tok", [1, 16])
+def test_config5_q4_k_m_layer(krk, torch_cuda, be32, c5_layer, n_tok):
+    """The C5 shape with Q6_K down banks (the Q4_K_M layout): gate/up on the
+    streaming kernel's routed modes for Q4_K, down on its Q6_K modes (one
+    token: over the concatenated slots; several: expert-major runs), against
+    the oracle on the device's routing (the GEMV bar)."""
+    torch = torch_cuda
+    banks, _, _ = c5_layer
+    ne, n_embd, n_ff, k = 128, 4096, 1536, 8
+    rng = np.random.default_rng(380)
+    down, entries, keep = {}, [], []
+    for e in range(ne):
+        ent = krk.MoeEntry()
+        for m, (o, i) in enumerate(((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff))):
+            q = banks[m, e] if m < 2 else q6k_random_bank(rng, o, i)
+            if m == 2:
+                down[e] = q
+            t = dev(torch, q)
+            keep.append(t)
+            dt = O.Q6_K if m == 2 else O.Q4_K
+            ent.p[m] = t.data_ptr()
+            ent.n_out[m], ent.n_in[m] = o, i
+            ent.row_bytes[m] = krk.row_bytes(dt, i)
+            ent.type[m] = dt
+            ent.present[m] = 1
+        entries.append(ent)
+    table = dev(torch, np.frombuffer(krk.moe_table_bytes(entries), np.uint8).copy())
+    logits = krk.synth_normal(n_tok * ne, seed=385 + n_tok).reshape(n_tok, ne)
+    x = krk.synth_normal(n_tok * n_embd, seed=386 + n_tok).reshape(n_tok, n_embd)
+    ids, wts = O.router_topk(O.router_softmax(logits), k)
+    out = torch.full((n_tok, n_embd), float("nan"), dtype=torch.float32, device="cuda")
+    say("config 5 q4_k_m", n_tok)
+    try:
+        be32.moe_dispatch(table, 0, ne, dev(torch, ids), dev(torch, wts), dev(torch, x), out, n_tok,
+                          n_embd, n_ff, k)
+        be32.sync()
+    finally:
+        be32.moe_table_forget(table)
+    used = set(ids.reshape(-1).tolist())
+    g = [banks[0, e] if e in used else banks[0, 0] for e in range(ne)]
+    u = [banks[1, e] if e in used else banks[0, 0] for e in range(ne)]
+    d = [down[e] if e in used else down[0] for e in range(ne)]
+    ref = O.moe_ffn(x, g, u, d, (O.Q4_K, O.Q4_K, O.Q6_K), ids, wts, n_ff, nthreads=16)
+    e = rel(host(out), ref)
+    say("  rel", e)
+    assert e <= GEMV_TOL
