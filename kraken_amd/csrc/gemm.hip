@@ -835,6 +835,10 @@ typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
 // One lane's share of one 256-value block of one weight row.  bf[0], bf[1]:
 // slices 4 u + ih and 4 u + 2 + ih.
 template <int DT> struct LaneBlk {
+    // value 128 u + NIB nib + gofs(g) + 8 ih + e of the block in slice
+    // 4 u + 2 nib + ih of lane group g (the activation side reads the same)
+    static constexpr int NIB = 32;
+    __device__ static int gofs(int g) { return 64 * (g >> 1) + 16 * (g & 1); }
     WStage<DT> w[4];   // (u, nib) = chunk 4 u + 2 (g / 2) + nib, half g % 2
     __device__ void fetch(const uint8_t *row, int blk, int g) {
 #pragma unroll
@@ -855,6 +859,8 @@ template <int DT> struct LaneBlk {
 // and each value is one mixed-precision FMA, f16(d1 (1024 + q) - c) with
 // c = 1024 d1 + m1 in f32 (1024 d1 exact).
 template <> struct LaneBlk<DT_Q4_K> {
+    static constexpr int NIB = 32;
+    __device__ static int gofs(int g) { return 64 * (g >> 1) + 16 * (g & 1); }
     uint32_t hdr[4], q[2][4];
     __device__ void fetch(const uint8_t *row, int blk, int g) {
         const uint8_t *b = row + static_cast<int64_t>(blk) * 144;
@@ -898,10 +904,62 @@ template <> struct LaneBlk<DT_Q4_K> {
     }
 };
 
+// Q6_K (210-byte blocks, 2-byte aligned rows): in half u of the block,
+// lane group g takes ql bytes [64 u + 16 g, +16) -- the four groups read
+// the half's 64 ql bytes as one line -- and the qh bytes of the same
+// positions l = 16 (g % 2) + i: low nibbles are quadrant g / 2 (values
+// 128 u + 16 g + i), high nibbles quadrant 2 + g / 2 (values + 64), with
+// scales sc[8 u + g] and sc[8 u + 4 + g].  Values are
+// f16(ds (1024 + q) - 1056 ds), ds = d sc (the host's (d sc) (q - 32)).
+template <> struct LaneBlk<DT_Q6_K> {
+    static constexpr int NIB = 64;
+    __device__ static int gofs(int g) { return 16 * g; }
+    uint32_t ql[2][4], qh[2][4], sc[4], dw;
+    __device__ void fetch(const uint8_t *row, int blk, int g) {
+        gbyte *b = to_global(row + static_cast<int64_t>(blk) * 210);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const u32x4 l = ld128_a2(b + 64 * u + 16 * g), h = ld128_a2(b + 128 + 32 * u + 16 * (g & 1));
+            ql[u][0] = l.x; ql[u][1] = l.y; ql[u][2] = l.z; ql[u][3] = l.w;
+            qh[u][0] = h.x; qh[u][1] = h.y; qh[u][2] = h.z; qh[u][3] = h.w;
+        }
+        const u32x4 s = ld128_a2(b + 192);
+        sc[0] = s.x; sc[1] = s.y; sc[2] = s.z; sc[3] = s.w;
+        dw = ld16g(b + 208);
+    }
+    __device__ void decode(int, int g, int u, int ih, half8 (&bf)[2]) const {
+        const float d = h2f(dw);
+        // scale bytes 8 u + g and 8 u + 4 + g: dwords 2 u and 2 u + 1, byte g
+        const int sa = static_cast<int8_t>((sc[2 * u] >> (8 * g)) & 0xFFu);
+        const int sb = static_cast<int8_t>((sc[2 * u + 1] >> (8 * g)) & 0xFFu);
+        const float da = d * static_cast<float>(sa), db = d * static_cast<float>(sb);
+        const float ca = 1056.0f * da, cb = 1056.0f * db;
+        const uint32_t s0 = 2u * static_cast<uint32_t>(g >> 1);
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            const uint32_t lw = ql[u][2 * ih + tt], hw = qh[u][2 * ih + tt];
+            const uint32_t lo = (lw & 0x0F0F0F0Fu) | (((hw >> s0) & 0x03030303u) << 4);
+            const uint32_t hi = ((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> (s0 + 4u)) & 0x03030303u) << 4);
+            const uint32_t pr[4] = {__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u),
+                                    __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u),
+                                    __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u),
+                                    __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const h16x2 hp = __builtin_bit_cast(h16x2, pr[k]);
+                const float dk = k < 2 ? da : db, ck = k < 2 ? ca : cb;
+                const int o = 4 * tt + 2 * (k & 1);
+                bf[k >> 1][o] = static_cast<_Float16>(__builtin_fmaf(dk, static_cast<float>(hp[0]), -ck));
+                bf[k >> 1][o + 1] = static_cast<_Float16>(__builtin_fmaf(dk, static_cast<float>(hp[1]), -ck));
+            }
+        }
+    }
+};
+
 constexpr int MG_THREADS = 512;
 
 template <int DT, bool GU, int MI>
-__global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K ? 4 : 2)))
+__global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K || (DT == DT_Q6_K && MI == 1) ? 4 : 2)))
     moe_gemm_kernel(MoeGemmArgs a, int ntiles) {
     constexpr int MT = 32 * MI;        // item rows
     constexpr int MB = 2 * MI;         // 16-row M blocks
@@ -968,7 +1026,7 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
         LaneBlk<DT>(&wr)[2] = ws.r;
         const bool next = blk + 1 < nblk;
         if (next) xfetch(blk + 1);
-        const _Float16 *xb = &Xs[blk & 1][j * LROW + 64 * (g >> 1) + 16 * (g & 1)];
+        const _Float16 *xb = &Xs[blk & 1][j * LROW + LaneBlk<DT>::gofs(g)];
 #pragma unroll
         for (int u = 0; u < 2; u++)
 #pragma unroll
@@ -985,7 +1043,7 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
                     for (int mb = 0; mb < MB; mb++) {
                         const half8 af = *reinterpret_cast<const half8 *>(
-                            xb + mb * 16 * LROW + 128 * u + 32 * nib + 8 * ih);
+                            xb + mb * 16 * LROW + 128 * u + LaneBlk<DT>::NIB * nib + 8 * ih);
 #pragma unroll
                         for (int c = 0; c < 2; c++)
                             acc[mb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[c][nib], acc[mb][c], 0, 0, 0);

@@ -52,19 +52,6 @@ __device__ __forceinline__ v4i lds_v4i(const uint8_t *p) { return *reinterpret_c
 // 0 1 4 5 2 3 6 7, so that MFMA m of lane pair p meets block 4 p + m
 __host__ __device__ constexpr int q40_slot(int s) { return s ^ ((((s >> 1) ^ (s >> 2)) & 1) * 6); }
 
-// loads from the 2-byte aligned Q6_K blocks (210 bytes), through global-space
-// pointers (the weight requests): the part runs its global memory with
-// unaligned access allowed, which hipcc's gfx950 target assumes (it emits a
-// single dwordx4 for these)
-typedef u32x4 u32x4_a2 __attribute__((aligned(2)));
-typedef uint32_t u32_a2 __attribute__((aligned(2)));
-__device__ __forceinline__ u32x4 ld128_a2(gbyte *p) {
-    return *(const __attribute__((address_space(1))) u32x4_a2 *)p;
-}
-__device__ __forceinline__ uint32_t ld32_a2(gbyte *p) {
-    return *(const __attribute__((address_space(1))) u32_a2 *)p;
-}
-
 // quad-lane exchanges (lanes l ^ 1 and l ^ 2) through DPP
 __device__ __forceinline__ float quad_xor1(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));

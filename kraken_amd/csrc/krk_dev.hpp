@@ -68,6 +68,20 @@ __device__ __forceinline__ u32x4 ld128(gbyte *p) {
     return *(const __attribute__((address_space(1))) u32x4 *)p;
 }
 __device__ __forceinline__ u32x4 ldg128(const uint8_t *p) { return ld128(to_global(p)); }
+// 2-byte aligned reads (Q6_K's 210-byte blocks): the part runs its global
+// memory with unaligned access allowed, which hipcc's gfx950 target assumes
+// (one dwordx4 / dword / ushort load each)
+typedef u32x4 u32x4_a2 __attribute__((aligned(2)));
+typedef uint32_t u32_a2 __attribute__((aligned(2)));
+__device__ __forceinline__ u32x4 ld128_a2(gbyte *p) {
+    return *(const __attribute__((address_space(1))) u32x4_a2 *)p;
+}
+__device__ __forceinline__ uint32_t ld32_a2(gbyte *p) {
+    return *(const __attribute__((address_space(1))) u32_a2 *)p;
+}
+__device__ __forceinline__ uint32_t ld16g(gbyte *p) {
+    return *(const __attribute__((address_space(1))) uint16_t *)p;
+}
 
 // ({hi,lo} >> 8*s)[31:0], s in 0..3 (v_alignbyte_b32).
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
