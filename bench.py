@@ -255,6 +255,9 @@ def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, 
         be.moe_dispatch(table, 0, n_expert, ids, wts, x, out, n_tok, n_embd, n_ff, k)
 
     ms = timer.run(step, calls, 4)
+    # the handle remembers a dispatched table by its address; the next call's
+    # table may be allocated at the same address
+    be.moe_table_forget(table)
     # distinct experts per call, from the same routing on the host
     import oracle as O
     distinct = []
@@ -425,8 +428,19 @@ TRACE_LABELS = [
      "C5 x16: expert-major gate/up (about 83 experts x 7.08 MB)", None, None),
     ("gemv_stream_kernel<12, float, float, 2, 16, 8, false, 4, 8", "49152",
      "C5 x16: expert-major down (about 83 experts x 3.54 MB)", None, None),
-    ("moe_plan_kernel", "256", "C5 x16: plan", None, None),
-    ("moe_reduce_kernel<float>", "4096", "C5 x16: ordered reduce", None, None),
+    ("gemv_stream_kernel<14, float, float, 2, 16, 8, false, 4, 8", "49152",
+     "C5 x16, Q6_K down banks: expert-major down", None, None),
+    ("gemv_stream_kernel<14, float, float, 2, 16, 16, true, 2, 8", "262144",
+     "C5 x1, Q6_K down banks: routed down over the 8 slots", None, None),
+    ("moe_gemm_kernel<12, true, 2>", "1179648", "C5 x512: grouped expert GEMM, gate/up (64-row items)",
+     2 * 4096 * 4096 * 3072, "f16"),
+    ("moe_gemm_kernel<12, false, 2>", "1572864", "C5 x512: grouped expert GEMM, down (Q4_K)",
+     2 * 4096 * 1536 * 4096, "f16"),
+    ("moe_gemm_kernel<14, false, 2>", "1572864", "C5 x512: grouped expert GEMM, down (Q6_K banks)",
+     2 * 4096 * 1536 * 4096, "f16"),
+    ("moe_gather_f16_kernel", "1048576", "C5 x512: activation rows gathered to f16 in plan order", None, None),
+    ("moe_plan_kernel", "256", "C5 x16 and x512: plan", None, None),
+    ("moe_reduce_kernel<float>", "4096", "C5 x16 and x512: ordered reduce", None, None),
     ("gemm_f16_kernelILi12EDF16", "229376", "C3 prefill up, M=2048 (448 tiles)", 2 * 2048 * 14336 * 4096, "f16"),
     ("gemm_f16_kernelILi12EDF16", "65536", "C3 prefill down, M=2048 (128 tiles x split 2)",
      2 * 2048 * 14336 * 4096, "f16"),
