@@ -838,6 +838,7 @@ template <int DT> struct LaneBlk {
     // value 128 u + NIB nib + gofs(g) + 8 ih + e of the block in slice
     // 4 u + 2 nib + ih of lane group g (the activation side reads the same)
     static constexpr int NIB = 32;
+    static constexpr int LOADS = -1;   // vector loads per fetch: not counted
     __device__ static int gofs(int g) { return 64 * (g >> 1) + 16 * (g & 1); }
     WStage<DT> w[4];   // (u, nib) = chunk 4 u + 2 (g / 2) + nib, half g % 2
     __device__ void fetch(const uint8_t *row, int blk, int g) {
@@ -860,6 +861,7 @@ template <int DT> struct LaneBlk {
 // c = 1024 d1 + m1 in f32 (1024 d1 exact).
 template <> struct LaneBlk<DT_Q4_K> {
     static constexpr int NIB = 32;
+    static constexpr int LOADS = 3;
     __device__ static int gofs(int g) { return 64 * (g >> 1) + 16 * (g & 1); }
     uint32_t hdr[4], q[2][4];
     __device__ void fetch(const uint8_t *row, int blk, int g) {
@@ -913,6 +915,7 @@ template <> struct LaneBlk<DT_Q4_K> {
 // f16(ds (1024 + q) - 1056 ds), ds = d sc (the host's (d sc) (q - 32)).
 template <> struct LaneBlk<DT_Q6_K> {
     static constexpr int NIB = 64;
+    static constexpr int LOADS = 6;
     __device__ static int gofs(int g) { return 16 * g; }
     uint32_t ql[2][4], qh[2][4], sc[4], dw;
     __device__ void fetch(const uint8_t *row, int blk, int g) {
@@ -958,15 +961,23 @@ template <> struct LaneBlk<DT_Q6_K> {
 
 constexpr int MG_THREADS = 512;
 
+// s_waitcnt vmcnt(N) alone (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] |
+// lgkmcnt[11:8] | vmcnt[5:4] << 14)
+template <int N> __device__ __forceinline__ void mg_wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 template <int DT, bool GU, int MI>
 __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K || (DT == DT_Q6_K && MI == 1) ? 4 : 2)))
     moe_gemm_kernel(MoeGemmArgs a, int ntiles) {
     constexpr int MT = 32 * MI;        // item rows
     constexpr int MB = 2 * MI;         // 16-row M blocks
-    constexpr int LROW = 256 + 8;      // halves per LDS row (16-byte pad)
-    constexpr int SPT = MT * 256 / MG_THREADS;   // staged values per thread: 16 MI
-    constexpr int TPR = 256 / SPT;               // staging threads per row
-    __shared__ _Float16 Xs[2][MT * LROW];
+    constexpr int NI = MT / 16;        // activation DMA instructions per wave and block
+    // two buffers of MT rows x 256 halves; 16-byte chunk c of row r at slot
+    // c ^ (r % 16), so the 16 rows a fragment read touches at one chunk hit
+    // distinct bank groups
+    __shared__ __attribute__((aligned(1024))) _Float16 Xs[2][MT * 256];
 
     // blockIdx -> (item, N tile): the hardware gives workgroup g to XCD
     // g % 8, so every N tile of an item runs on one XCD (its activation rows
@@ -996,18 +1007,40 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
         wrow[c] = wb + static_cast<int64_t>(row[c] < a.N ? row[c] : a.N - 1) * a.row_bytes;
     }
 
-    // this thread's staging slice: row sr, values [sc, sc + SPT) of each block
-    const int sr = tid / TPR, sc = (tid % TPR) * SPT;
-    const bool sok = sr < rows;
-    const _Float16 *xs = static_cast<const _Float16 *>(a.x) + static_cast<int64_t>(sok ? pb + sr : 0) * a.K + sc;
-    XStage<_Float16> xr[SPT / 16];
-    auto xfetch = [&](int blk) {
+    // activation rows by LDS DMA (global_load_lds, 16 bytes a lane): wave
+    // w's instruction i fills rows 2 (NI w + i) + lane / 32, slots lane % 32
+    // (rows past the item re-read its first row; their outputs are dropped)
+    gbyte *dsrc[NI];
 #pragma unroll
-        for (int i = 0; i < SPT / 16; i++) xr[i].fetch(xs + 256 * blk + 16 * i, sok);
+    for (int i = 0; i < NI; i++) {
+        const int r = 2 * (NI * wave + i) + (lane >> 5);
+        const int c = (lane & 31) ^ (r & 15);
+        dsrc[i] = to_global(reinterpret_cast<const uint8_t *>(static_cast<const _Float16 *>(a.x) +
+                                                              static_cast<int64_t>(pb + (r < rows ? r : 0)) * a.K +
+                                                              8 * c));
+    }
+    auto xdma = [&](int blk, int buf) {
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(dsrc[i] + 512 * static_cast<int64_t>(blk)),
+                (__attribute__((address_space(3))) void *)(&Xs[buf][(2 * (NI * wave + i)) * 256]), 16, 0, 0);
     };
-    auto xstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < SPT / 16; i++) xr[i].store(&Xs[buf][sr * LROW + sc + 16 * i]);
+    // this wave's DMA of a block has landed once at most the `later` vector
+    // loads issued after it are outstanding (in-order completion); then a
+    // bare barrier (__syncthreads would also wait for the weight prefetch)
+    auto publish = [&](bool fetched) {
+        constexpr int L = LaneBlk<DT>::LOADS;
+        if (L > 0 && fetched) mg_wait_vm<2 * (L > 0 ? L : 0)>();
+        else mg_wait_vm<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    // A fragment of (u, nib, ih) for lane (j, g): row j of an M block, chunk
+    // 16 u + (NIB / 8) nib + ih + gofs(g) / 8 (disjoint bits), swizzled
+    const int cd = LaneBlk<DT>::gofs(g) >> 3;
+    auto a_off = [&](int u, int nib, int ih) {
+        const int c = 16 * u + (LaneBlk<DT>::NIB / 8) * nib + ih + cd;
+        return j * 256 + ((c ^ j) << 3);
     };
 
     const int nblk = a.K / 256;
@@ -1025,8 +1058,8 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
     auto block = [&](Set &ws, int blk) {
         LaneBlk<DT>(&wr)[2] = ws.r;
         const bool next = blk + 1 < nblk;
-        if (next) xfetch(blk + 1);
-        const _Float16 *xb = &Xs[blk & 1][j * LROW + LaneBlk<DT>::gofs(g)];
+        if (next) xdma(blk + 1, (blk + 1) & 1);
+        const _Float16 *xb = Xs[blk & 1];
 #pragma unroll
         for (int u = 0; u < 2; u++)
 #pragma unroll
@@ -1042,34 +1075,30 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
                 for (int nib = 0; nib < 2; nib++)
 #pragma unroll
                     for (int mb = 0; mb < MB; mb++) {
-                        const half8 af = *reinterpret_cast<const half8 *>(
-                            xb + mb * 16 * LROW + 128 * u + LaneBlk<DT>::NIB * nib + 8 * ih);
+                        const half8 af = *reinterpret_cast<const half8 *>(xb + mb * 16 * 256 + a_off(u, nib, ih));
 #pragma unroll
                         for (int c = 0; c < 2; c++)
                             acc[mb][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[c][nib], acc[mb][c], 0, 0, 0);
                     }
             }
-        // the next block's activations go to LDS before this set's refill is
-        // requested: their wait then covers only loads issued before them
-        if (next) xstore((blk + 1) & 1);
-        if (DEEP && blk + 2 < nblk) {
+        const bool deep_fetch = DEEP && blk + 2 < nblk;
+        if (deep_fetch) {
             wr[0].fetch(wrow[0], blk + 2, g);
             wr[1].fetch(wrow[1], blk + 2, g);
         }
-        if (next) __syncthreads();
+        if (next) publish(deep_fetch || !DEEP);
     };
 
     Set ra;
     std::conditional_t<DEEP, Set, Set &> rb = ra;
-    xfetch(0);
+    xdma(0, 0);
     ra.r[0].fetch(wrow[0], 0, g);
     ra.r[1].fetch(wrow[1], 0, g);
     if (DEEP && nblk > 1) {
         rb.r[0].fetch(wrow[0], 1, g);
         rb.r[1].fetch(wrow[1], 1, g);
     }
-    xstore(0);
-    __syncthreads();
+    publish(true);
     for (int blk = 0; blk < nblk; blk += 2) {
         block(ra, blk);
         if (blk + 1 < nblk) block(rb, blk + 1);
