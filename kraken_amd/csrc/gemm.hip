@@ -969,7 +969,7 @@ template <int N> __device__ __forceinline__ void mg_wait_vm() {
 }
 
 template <int DT, bool GU, int MI>
-__global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K || (DT == DT_Q6_K && MI == 1) ? 4 : 2)))
+__global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K || DT == DT_Q6_K ? 4 : 2)))
     moe_gemm_kernel(MoeGemmArgs a, int ntiles) {
     constexpr int MT = 32 * MI;        // item rows
     constexpr int MB = 2 * MI;         // 16-row M blocks
@@ -1075,6 +1075,7 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
                 for (int nib = 0; nib < 2; nib++)
 #pragma unroll
                     for (int mb = 0; mb < MB; mb++) {
+                        if (mb > 0 && 16 * mb >= rows) break;   // M blocks past the item: no work
                         const half8 af = *reinterpret_cast<const half8 *>(xb + mb * 16 * 256 + a_off(u, nib, ih));
 #pragma unroll
                         for (int c = 0; c < 2; c++)
