@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list of sections: gemm,int8,layer,formats,head,moe "
+    ap.add_argument("--only", default="", help="comma list of sections: gemm,rows,int8,layer,formats,head,moe "
                     "(the headline GEMV always runs); default all")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--soak-seconds", type=float, default=3.0,
@@ -622,6 +622,16 @@ def main():
         for nm, r in bench_f16_ceiling(torch, be16, timer, 2048, 14336, 4096).items():
             extras[f"{nm}_up_m2048"] = r
             log(f"  {nm}: {r['us']:.1f} us  {r['TFLOPs']:.1f} TFLOP/s  ({100 * r['frac_fp16_peak']:.1f}%)")
+
+    if want("rows"):
+        # batched rows between the decode GEMV (<= 8) and prefill: 16..128
+        # activation rows of the C3 up shape on the MFMA path
+        for M in (16, 32, 64, 128):
+            log(f"gemm q4_k up M={M} ...")
+            r = bench_gemm(K, torch, be16, timer, K.Q4_K, M, 14336, 4096, seed=11)
+            gbs = 14336 * K.row_bytes(K.Q4_K, 4096) / r["ms"] / 1e6
+            log(f"  {r['ms'] * 1e3:.1f} us  {r['TFLOPs']:.1f} TFLOP/s  {gbs:.0f} GB/s of weights")
+            extras[f"gemm_q4k_up_m{M}"] = {"us": r["ms"] * 1e3, "TFLOPs": r["TFLOPs"], "weight_GBps": gbs}
 
     if want("int8"):
         # the Q8_0 x Q8 int8 rung at the C3 up shape (KRK_PATH_INT8)

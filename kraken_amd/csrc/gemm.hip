@@ -751,7 +751,34 @@ static int pick_split(int64_t M, int64_t N, int64_t K, int dt) {
     return best;
 }
 
+// Batches of up to kStreamGemmRows rows take the weight-streaming kernel of
+// the grouped expert GEMM in its dense mode: the 256 x 256 tiles would be
+// mostly padding, and the weights, not the MFMAs, bound these.
+constexpr int64_t kStreamGemmRows = 128;
+static bool stream_gemm(int dt, int64_t M, int64_t N, int64_t K) {
+    return M <= kStreamGemmRows && K % 256 == 0 && N < (1LL << 31) && K < (1LL << 31) && moe_gemm_ok(dt);
+}
+
+// K ranges of a dense streaming launch: the largest divisor of the block
+// count up to what brings the workgroups to two per CU
+static int stream_split(int64_t M, int64_t N, int64_t K) {
+    const int64_t mt = M <= 32 ? 32 : 64;
+    const int64_t wgs = ((M + mt - 1) / mt) * ((N + 255) / 256);
+    const int64_t want = (device_cus() + wgs - 1) / wgs;
+    const int64_t nb = K / 256;
+    int best = 1;
+    for (int s = 1; s <= nb && s <= want; s++)
+        if (nb % s == 0) best = s;
+    return best;
+}
+static size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
+
 size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K) {
+    if (stream_gemm(dt, M, N, K)) {   // f32 rows as f16, and the split partials
+        const int s = stream_split(M, N, K);
+        return al256(static_cast<size_t>(M * K) * sizeof(_Float16)) +
+               (s > 1 ? static_cast<size_t>(s) * M * N * sizeof(float) : 0);
+    }
     const int s = pick_split(M, N, K, dt);
     return s > 1 ? static_cast<size_t>(s) * M * N * sizeof(float) : 0;
 }
@@ -784,6 +811,39 @@ static hipError_t launch_f16(const void *w, int64_t rb, const void *x, void *out
 hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bool act_f16,
                      void *out, int64_t M, int64_t N, int64_t K, void *ws, size_t ws_bytes,
                      hipStream_t st) {
+    if (stream_gemm(dt, M, N, K)) {
+        if (ws_bytes < gemm_mfma_workspace(dt, M, N, K)) return hipErrorInvalidValue;
+        const int split = stream_split(M, N, K);
+        float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
+                                                al256(static_cast<size_t>(M * K) * sizeof(_Float16)));
+        MoeGemmArgs g{};
+        g.x = x;
+        if (!act_f16) {   // the rows as f16 (the operand rounding of every MFMA path)
+            const hipError_t e = moe_gather_f16(static_cast<const float *>(x), K, nullptr, nullptr, M,
+                                                static_cast<_Float16 *>(ws), st);
+            if (e != hipSuccess) return e;
+            g.x = ws;
+        }
+        g.w = w;
+        g.ksplit = split;
+        g.out = split > 1 ? static_cast<void *>(part) : out;
+        g.out_f16 = act_f16;
+        g.row_bytes = row_bytes;
+        g.K = static_cast<int>(K);
+        g.N = static_cast<int>(N);
+        g.M = static_cast<int>(M);
+        g.mi = M <= 32 ? 1 : 2;
+        hipError_t e = moe_gemm(dt, g, st);
+        if (e != hipSuccess || split == 1) return e;
+        const int64_t MN = M * N;
+        if (act_f16)
+            hipLaunchKernelGGL((splitk_reduce_kernel<_Float16>), dim3(static_cast<unsigned>((MN + 2047) / 2048)),
+                               dim3(256), 0, st, part, static_cast<_Float16 *>(out), MN, split);
+        else
+            hipLaunchKernelGGL((splitk_reduce_kernel<float>), dim3(static_cast<unsigned>((MN + 2047) / 2048)),
+                               dim3(256), 0, st, part, static_cast<float *>(out), MN, split);
+        return hipGetLastError();
+    }
 #define KRK_GEMM_CASE(D)                                                                       \
     case D:                                                                                   \
         return act_f16 ? launch_f16<D, _Float16, _Float16>(w, row_bytes, x, out, M, N, K, ws,  \
@@ -983,12 +1043,30 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
     // g % 8, so every N tile of an item runs on one XCD (its activation rows
     // stay in that L2) and the items, empty ones included, are dealt evenly
     // over the XCDs.
+    // Dense mode: every N tile's row items run on one XCD (they share its
+    // weights in that L2).
     const int gi = static_cast<int>(blockIdx.x), slot = gi >> 3;
-    const int item = (gi & 7) + 8 * (slot / ntiles), nt = slot % ntiles;
-    if (item >= *a.n_items) return;
-    const int32_t *it = a.items + 4 * item;
-    const int e = it[0], pb = it[1], rows = it[2];
-    const krk_moe_entry *en = static_cast<const krk_moe_entry *>(a.tab) + e;
+    const bool dense = !GU && a.w != nullptr;
+    int item, nt, pb, rows, ks = 0;
+    const krk_moe_entry *en = nullptr;
+    if (dense) {
+        // slot -> (item fastest, N tile group, K range)
+        const int nit = (a.M + MT - 1) / MT, ntg = (ntiles + 7) / 8;
+        item = slot % nit;
+        nt = (gi & 7) + 8 * ((slot / nit) % ntg);
+        ks = (slot / nit) / ntg;
+        if (nt >= ntiles) return;
+        pb = item * MT;
+        rows = a.M - pb < MT ? a.M - pb : MT;
+    } else {
+        item = (gi & 7) + 8 * (slot / ntiles);
+        nt = slot % ntiles;
+        if (item >= *a.n_items) return;
+        const int32_t *it = a.items + 4 * item;
+        pb = it[1];
+        rows = it[2];
+        en = static_cast<const krk_moe_entry *>(a.tab) + it[0];
+    }
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 15, g = lane >> 4;
@@ -1002,9 +1080,17 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
             wb = static_cast<const uint8_t *>(en->p[c == 0 ? KRK_MOE_GATE : KRK_MOE_UP]);
         } else {
             row[c] = nt * 256 + wave * 32 + 16 * c + j;
-            wb = static_cast<const uint8_t *>(en->p[KRK_MOE_DOWN]);
+            wb = dense ? static_cast<const uint8_t *>(a.w) : static_cast<const uint8_t *>(en->p[KRK_MOE_DOWN]);
         }
         wrow[c] = wb + static_cast<int64_t>(row[c] < a.N ? row[c] : a.N - 1) * a.row_bytes;
+    }
+    // a dense launch's K range: its blocks start kb0 blocks into every row
+    const int nblk = a.K / 256 / (dense ? a.ksplit : 1);
+    const int64_t kb0 = static_cast<int64_t>(ks) * nblk;
+    if (ks) {
+        const int64_t bb = a.row_bytes / (a.K / 256);   // bytes per 256 values
+#pragma unroll
+        for (int c = 0; c < 2; c++) wrow[c] += kb0 * bb;
     }
 
     // activation rows by LDS DMA (global_load_lds, 16 bytes a lane): wave
@@ -1017,7 +1103,7 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
         const int c = (lane & 31) ^ (r & 15);
         dsrc[i] = to_global(reinterpret_cast<const uint8_t *>(static_cast<const _Float16 *>(a.x) +
                                                               static_cast<int64_t>(pb + (r < rows ? r : 0)) * a.K +
-                                                              8 * c));
+                                                              256 * kb0 + 8 * c));
     }
     auto xdma = [&](int blk, int buf) {
 #pragma unroll
@@ -1043,7 +1129,6 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
         return j * 256 + ((c ^ j) << 3);
     };
 
-    const int nblk = a.K / 256;
     floatx4 acc[MB][2];
 #pragma unroll
     for (int i = 0; i < MB; i++)
@@ -1122,8 +1207,15 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
             } else {
 #pragma unroll
                 for (int c = 0; c < 2; c++)
-                    if (row[c] < a.N)
-                        static_cast<float *>(a.out)[static_cast<int64_t>(pb + m) * a.N + row[c]] = acc[mb][c][r];
+                    if (row[c] < a.N) {
+                        const int64_t o = static_cast<int64_t>(pb + m) * a.N + row[c];
+                        if (a.ksplit > 1)   // (dense) this K range's f32 partial
+                            static_cast<float *>(a.out)[static_cast<int64_t>(ks) * a.M * a.N + o] = acc[mb][c][r];
+                        else if (a.out_f16)
+                            static_cast<_Float16 *>(a.out)[o] = static_cast<_Float16>(acc[mb][c][r]);
+                        else
+                            static_cast<float *>(a.out)[o] = acc[mb][c][r];
+                    }
             }
         }
 }
@@ -1135,8 +1227,8 @@ __global__ void __launch_bounds__(256) moe_gather_f16_kernel(const float *__rest
                                                               const int32_t *__restrict__ n_live,
                                                               _Float16 *__restrict__ xg) {
     const int64_t pos = blockIdx.x;
-    if (pos >= *n_live) return;
-    const float *src = x + static_cast<int64_t>(plan_tok[pos]) * n;
+    if (n_live && pos >= *n_live) return;
+    const float *src = x + (plan_tok ? static_cast<int64_t>(plan_tok[pos]) : pos) * n;
     _Float16 *dst = xg + pos * n;
     for (int64_t i = 8 * static_cast<int64_t>(threadIdx.x); i < n; i += 8 * 256) {
         const floatx4 v0 = *reinterpret_cast<const floatx4 *>(src + i);
@@ -1173,9 +1265,12 @@ bool moe_gemm_ok(int dt) {
 
 template <int DT, bool GU>
 static hipError_t launch_moe_gemm(const MoeGemmArgs &a, hipStream_t st) {
-    if (a.K % 256 || a.N <= 0 || a.max_items <= 0) return hipErrorInvalidValue;
+    if (a.K % 256 || a.N <= 0 ||
+        (a.w ? (GU || a.M <= 0 || a.ksplit < 1 || (a.K / 256) % a.ksplit) : a.max_items <= 0))
+        return hipErrorInvalidValue;
     const int ntiles = (a.N + (GU ? 127 : 255)) / (GU ? 128 : 256);
-    const int64_t blocks = 8LL * ntiles * ((a.max_items + 7) / 8);
+    const int64_t blocks = a.w ? 8LL * ((a.M + 32 * a.mi - 1) / (32 * a.mi)) * ((ntiles + 7) / 8) * a.ksplit
+                               : 8LL * ntiles * ((a.max_items + 7) / 8);
     if (blocks > (1LL << 31) - 1) return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>(blocks));
     switch (a.mi) {

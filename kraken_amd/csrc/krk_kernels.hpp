@@ -131,6 +131,12 @@ struct MoeGemmArgs {
     int max_items;             // items the grid covers (an upper bound)
     int mi;                    // item rows = 32 mi, mi in {1, 2}
     bool gate_up;
+    // dense mode (w non-null, items unused, not gate/up): one weight matrix,
+    // items of 32 mi of the M rows of X, out [M, N] in f32 or f16
+    const void *w;
+    int M;
+    bool out_f16;
+    int ksplit;                // dense: K in ksplit whole-block ranges, f32 partials [ksplit][M][N] at out
 };
 bool moe_gemm_ok(int dt);
 hipError_t moe_gemm(int dt, const MoeGemmArgs &a, hipStream_t st);
