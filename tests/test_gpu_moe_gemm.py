@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from test_gpu_parity import GEMM_TOL, GEMV_TOL, build_moe, dev, host, rel, say
+from test_gpu_parity import GEMM_TOL, GEMV_TOL, build_moe, dev, host, make_weights, rel, say
 
 pytestmark = pytest.mark.gpu
 
@@ -69,3 +69,27 @@ def test_moe_gemm_repeat_smaller(krk, torch_cuda, be32):
     e1 = run(krk, torch_cuda, be32, O.Q4_K, 8, 512, 768, 8, 200, seed=2300)
     e2 = run(krk, torch_cuda, be32, O.Q4_K, 8, 512, 768, 2, 40, seed=2400)
     assert e1 <= GEMM_TOL and e2 <= GEMM_TOL
+
+
+@pytest.mark.parametrize("rows", [9, 16, 33, 64, 100, 128])
+@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q8_0, O.Q5_K, O.Q4_0, O.MXFP4])
+@pytest.mark.parametrize("n_in", [1024, 4096])
+def test_dense_streaming_gemm(krk, torch_cuda, be32, be16, rows, dt, n_in):
+    """Dense GEMMs of 9..128 rows take the grouped kernel's dense mode (items
+    of 32 or 64 rows, K split over whole blocks, f32 partials summed in a
+    fixed order): f32 and f16 activations against the oracle, MFMA bar."""
+    torch = torch_cuda
+    n_out = 520   # a partial 256-row tile
+    w = make_weights(krk, dt, n_out, n_in, seed=2500 + rows)
+    x = krk.synth_normal(rows * n_in, seed=2600 + rows).reshape(rows, n_in)
+    ref = O.gemm(dt, w, x, n_out)
+    say("dense streaming gemm", dt, rows, n_in)
+    out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    be32.gemm(out, dev(torch, x), dev(torch, w), dt, n_out, n_in, rows)
+    be32.sync()
+    assert rel(host(out), ref) <= GEMM_TOL
+    x16 = x.astype(np.float16)
+    out16 = torch.full((rows, n_out), float("nan"), dtype=torch.float16, device="cuda")
+    be16.gemm(out16, dev(torch, x16), dev(torch, w), dt, n_out, n_in, rows)
+    be16.sync()
+    assert rel(host(out16).astype(np.float32), O.gemm(dt, w, x16.astype(np.float32), n_out)) <= GEMM_TOL
