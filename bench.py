@@ -439,6 +439,9 @@ TRACE_LABELS = [
     ("moe_gemm_kernel<14, false, 2>", "1572864", "C5 x512: grouped expert GEMM, down (Q6_K banks)",
      2 * 4096 * 1536 * 4096, "f16"),
     ("moe_gather_f16_kernel", "1048576", "C5 x512: activation rows gathered to f16 in plan order", None, None),
+    ("moe_gemm_kernel<12, false, 1>", "114688", "rows 16 and 32: Q4_K 4096->14336, streaming dense mode (split-K 4)",
+     None, None),
+    ("moe_gemm_kernel<12, false, 2>", "114688", "rows 64 and 128: Q4_K 4096->14336, streaming dense mode", None, None),
     ("moe_plan_kernel", "256", "C5 x16 and x512: plan", None, None),
     ("moe_reduce_kernel<float>", "4096", "C5 x16 and x512: ordered reduce", None, None),
     ("gemm_f16_kernelILi12EDF16", "229376", "C3 prefill up, M=2048 (448 tiles)", 2 * 2048 * 14336 * 4096, "f16"),
