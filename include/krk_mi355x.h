@@ -238,7 +238,11 @@ int krk_moe_plan_build(krk_backend *b, const void *ids, int64_t n_rows, int k,
  *   out[t] = sum over slots s (in ascending expert id) of
  *            wts[t,s] * down_e( silu(gate_e(xn[t])) * up_e(xn[t]) )
  * xn and out are [n_tok, n_embd] in the activation type; ids int32 and wts
- * f32 [n_tok, k] device arrays.
+ * f32 [n_tok, k] device arrays.  With f32 activations, batches of 32 tokens
+ * or more whose banks are uniform Q4_K/Q5_K/Q6_K/Q8_0/Q4_0/MXFP4 (gate and
+ * up of one type) form their products from f16 operands on the matrix
+ * cores, as a gemm of more than 8 rows does, unless krk_set_gemm_path
+ * selected KRK_PATH_EXACT.
  * The first call for a (table, layer, n_expert, n_embd, n_ff) reads that
  * layer's entries back once and validates every one: all three matrices
  * present, of a served type (types may vary from expert to expert and
