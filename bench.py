@@ -629,7 +629,7 @@ def main():
     if want("rows"):
         # batched rows between the decode GEMV (<= 8) and prefill: 16..128
         # activation rows of the C3 up shape on the MFMA path
-        for M in (16, 32, 64, 128):
+        for M in (4, 5, 8, 16, 32, 64, 128):
             log(f"gemm q4_k up M={M} ...")
             r = bench_gemm(K, torch, be16, timer, K.Q4_K, M, 14336, 4096, seed=11)
             gbs = 14336 * K.row_bytes(K.Q4_K, 4096) / r["ms"] / 1e6
