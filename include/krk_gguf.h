@@ -1,6 +1,6 @@
 /*
  * krk_gguf.h -- C ABI of the GGUF container reader and the verbatim weight
- * upload (SURVEY's next item 2): real checkpoints' blocks go to the kernels
+ * upload: real checkpoints' blocks go to the kernels
  * byte for byte, as the reference's model loader uploads them.
  *
  * Replaces krk::Gguf (include/krk/gguf.hpp:86-160, src/gguf.cpp:130-470)
