@@ -23,6 +23,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 INT8_PEAK_TOPS = 5000.0
+ROTATE_BYTES = 2 << 30   # distinct weight copies per GEMV configuration: 8x the MALL
 
 
 def log(*a):
@@ -37,6 +38,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="", help="comma list of sections: gemm,rows,int8,layer,formats,head,moe "
                     "(the headline GEMV always runs); default all")
+    ap.add_argument("--rotate-gib", type=float, default=2.0,
+                    help="GiB of distinct weight copies each GEMV configuration rotates through")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--soak-seconds", type=float, default=3.0,
                     help="untimed back-to-back headline GEMVs before its timed steps")
@@ -60,66 +63,95 @@ def parse():
 
 
 class Timer:
-    """HIP events on the stream the kernels are launched on.
+    """HIP events on the stream the kernels are launched on, marginal time
+    per call as the reference's kraken-bench measures it
+    (tools/bench_ops.cpp:269-285: (t_many - t_one) / (iters - 1)).
 
     A Python call through ctypes costs ~13 us of host time, longer than a
     decode GEMV kernel, so timing a loop of eager calls measures the host.
-    ``run`` therefore captures the calls into a HIP graph (on a side stream,
-    with the backends switched to it) and times graph replays: the kernels
-    then run back to back exactly as a serving loop's graph would run them.
+    ``run`` therefore captures the calls into HIP graphs (on a side stream,
+    with the backends switched to it): graphs of ``iters`` back-to-back
+    calls and graphs of a single call, each replay timed alone.  The median
+    single-call replay is subtracted from the median ``iters``-call replay,
+    so the graph's launch latency and the first call's ramp cancel and what
+    remains is the steady-state time per call, independent of ``iters``.
+
+    ``distinct``: fn(i) reads weight copy i % distinct.  The calls are then
+    split over windows of ``iters`` consecutive copies, one graph each, and
+    the windows (and the single-call graphs, one per copy) are replayed in
+    turn, so successive replays read distinct copies and no replay finds
+    its weights in the 256 MB MALL left there by the one before.
     """
 
-    def __init__(self, torch, stream, backends, warm_replays=3):
+    def __init__(self, torch, stream, backends, warm_replays=2, reps=3):
         self.t, self.s, self.backends = torch, stream, backends
-        self.warm_replays = warm_replays
+        self.warm_replays, self.reps = warm_replays, reps
 
-    def run(self, fn, iters, warmup, graph=True, soak_s=0.0):
-        """ms per call of fn over `iters` calls; soak_s: untimed replays of
-        the captured graph for that many seconds first (the headline, so
-        the GPU is busy long enough for an outside sampler to see it)."""
+    def _capture(self, fn, first, count):
         torch = self.t
-        for i in range(warmup):
-            fn(i)
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        if not graph:
-            e0.record(self.s)
-            for i in range(iters):
-                fn(i)
-            e1.record(self.s)
-            torch.cuda.synchronize()
-            return e0.elapsed_time(e1) / iters  # ms per call
         g = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
         with torch.cuda.graph(g, stream=side):
             for be in self.backends:
                 be.set_stream(side)
-            for i in range(iters):
+            for i in range(first, first + count):
                 fn(i)
         for be in self.backends:
             be.set_stream(self.s)
+        return g
+
+    def _time(self, graphs, reps):
+        """Median over reps rounds of each graph's replay, the graphs taken
+        in turn."""
+        torch = self.t
+        ts = []
+        for _ in range(reps):
+            for g in graphs:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(self.s)
+                g.replay()
+                e1.record(self.s)
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1))
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    def run(self, fn, iters, warmup, soak_s=0.0, distinct=1):
+        """Marginal ms per call of fn over `iters` back-to-back calls;
+        soak_s: untimed replays for that many seconds first (the headline,
+        so the GPU is busy long enough for an outside sampler to see it)."""
+        torch = self.t
+        iters = max(1, iters)
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        nwin = max(1, -(-distinct // iters))
+        many = [self._capture(fn, j * iters, iters) for j in range(nwin)]
+        ones = [self._capture(fn, j, 1) for j in range(max(1, distinct))] if iters > 1 else []
         # untimed replays until the clocks and caches settle: the first
         # replays of a fresh graph run up to ~7% slower than later ones
         for _ in range(self.warm_replays):
-            g.replay()
+            for g in many + ones:
+                g.replay()
         torch.cuda.synchronize()
         t_end = time.perf_counter() + soak_s
         while time.perf_counter() < t_end:
-            for _ in range(16):
+            for g in many:
                 g.replay()
             torch.cuda.synchronize()
-        e0.record(self.s)
-        g.replay()
-        e1.record(self.s)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / iters
+        t_many = self._time(many, max(self.reps, -(-5 // nwin)))
+        if not ones:
+            return t_many
+        t_one = self._time(ones, max(1, -(-5 // len(ones))))
+        return (t_many - t_one) / (iters - 1)
 
 
-def rotation(torch, w_host, min_bytes=1 << 30):
+def rotation(torch, w_host, min_bytes=None):
     """Distinct copies of a weight matrix filling >= min_bytes, carved out of
     one allocation (as a model's weights sit in one arena), so every call
     streams its matrix from HBM rather than from the 256 MB MALL."""
+    min_bytes = ROTATE_BYTES if min_bytes is None else min_bytes
     base = torch.from_numpy(w_host).cuda()
     n = max(2, -(-min_bytes // base.numel()))
     stride = -(-base.numel() // 256) * 256
@@ -148,22 +180,11 @@ def bench_gemv(K, torch, be, timer, args, dt, n_out, n_in, seed, act_f16=False, 
     out = torch.empty((1, n_out), dtype=torch.float16 if act_f16 else torch.float32,
                       device="cuda")
     ms = timer.run(lambda i: be.gemm(out, xt, ws[i % len(ws)], dt, n_out, n_in, 1),
-                   args.steps, args.warmup, soak_s=soak_s)
+                   args.steps, args.warmup, soak_s=soak_s, distinct=len(ws))
     nbytes = K.row_bytes(dt, n_in) * n_out
     act_bytes = (n_in + n_out) * (2 if act_f16 else 4)
     return {"ms": ms, "weight_bytes": nbytes, "bytes": nbytes + act_bytes,
             "GBps": (nbytes + act_bytes) / ms / 1e6, "copies": len(ws), "w": w, "x": x, "ws": ws}
-
-
-def bench_read_ceiling(torch, be, timer, ws, nbytes, blocks=2048):
-    """The same rotation of weight copies read by a plain streaming kernel
-    (krk_probe_read): what one launch of a pure HBM read of these bytes
-    takes on this part, the floor under the decode GEMV."""
-    sink = torch.empty(1024, dtype=torch.int32, device="cuda")
-    n16 = nbytes // 16 * 16
-    ms = timer.run(lambda i: be.probe_read(ws[i % len(ws)], n16, blocks, sink), 400, 4)
-    return {"us": ms * 1e3, "GBps": n16 / ms / 1e6, "frac_hbm": n16 / ms / 1e6 / HBM_PEAK_GBS,
-            "bytes": n16, "blocks": blocks}
 
 
 def bench_gemm(K, torch, be, timer, dt, M, n_out, n_in, seed, iters=20, warmup=3):
@@ -176,24 +197,6 @@ def bench_gemm(K, torch, be, timer, dt, M, n_out, n_in, seed, iters=20, warmup=3
     flops = 2.0 * M * n_out * n_in
     return {"ms": ms, "TFLOPs": flops / ms / 1e9, "frac": flops / ms / 1e9 / FP16_PEAK_TFLOPS,
             "M": M, "N": n_out, "K": n_in}
-
-
-def bench_f16_ceiling(torch, be, timer, M, N, K, iters=20, warmup=3):
-    """A plain f16 GEMM at the C3 up shape (krk_probe_gemm) on N(0,1) f16
-    operands -- what dense f16 MFMA work reaches on this part with data like
-    the prefill GEMM's -- and the same kernel with its operands loaded once
-    and re-read from LDS (the matrix cores and LDS alone)."""
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(7)
-    x = torch.randn((M, K), dtype=torch.float16, device="cuda", generator=gen)
-    w = torch.randn((N, K), dtype=torch.float16, device="cuda", generator=gen)
-    out = torch.empty((M, N), dtype=torch.float16, device="cuda")
-    flops = 2.0 * M * N * K
-    res = {}
-    for loads, nm in ((True, "plain_f16_gemm"), (False, "mfma_lds_skeleton")):
-        ms = timer.run(lambda i: be.probe_gemm(x, w, out, M, N, K, loads), iters, warmup)
-        res[nm] = {"us": ms * 1e3, "TFLOPs": flops / ms / 1e9, "frac_fp16_peak": flops / ms / 1e9 / FP16_PEAK_TFLOPS}
-    return res
 
 
 def q4k_random_rows(torch, n_rows, n_in, gen):
@@ -254,7 +257,7 @@ def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, 
         be.router_topk(probs, n_tok, n_expert, k, ids, wts, True, 1.0)
         be.moe_dispatch(table, 0, n_expert, ids, wts, x, out, n_tok, n_embd, n_ff, k)
 
-    ms = timer.run(step, calls, 4)
+    ms = timer.run(step, calls, 4, distinct=calls)
     # the handle remembers a dispatched table by its address; the next call's
     # table may be allocated at the same address
     be.moe_table_forget(table)
@@ -272,11 +275,13 @@ def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, 
             "bytes_per_call": nbytes, "TFLOPs": flops / ms / 1e9}
 
 
-def bench_layer_grouped(K, torch, be, timer, copies=4):
+def bench_layer_grouped(K, torch, be, timer, copies=None):
     """One Llama-2-7B decode layer's weight math the way the engine issues it:
     gemm_group(q, k, v), gemm(o), gemm_group(gate, up, silu), gemm(down).
-    The layer's 113.8 MB rotate through `copies` distinct layers."""
+    The layer's 113.8 MB rotate through `copies` distinct layers (default:
+    as many as fill the rotation bytes)."""
     import numpy as np
+    copies = copies or -(-ROTATE_BYTES // 113_836_032)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(7)
     shapes = {"q": (4096, 4096), "k": (4096, 4096), "v": (4096, 4096), "o": (4096, 4096),
@@ -296,23 +301,35 @@ def bench_layer_grouped(K, torch, be, timer, copies=4):
         be.gemm_group([ffn, up], x, [L["gate"], L["up"]], K.Q4_K, [11008, 11008], 4096, 1, silu=True)
         be.gemm(y, ffn, L["down"], K.Q4_K, 4096, 11008, 1)
 
-    ms = timer.run(step, 64, 4)
+    ms = timer.run(step, 64, 4, distinct=copies)
     nbytes = sum(K.row_bytes(K.Q4_K, i) * o for o, i in shapes.values())
     nbytes += 4 * (4 * 4096 + 4 * 4096 + 11008 * 2 + 4096)
     return {"us": ms * 1e3, "GBps": nbytes / ms / 1e6, "bytes": nbytes, "launches": 4}
 
 
 def cpu_baseline(O, w, x, n_out, n_in, seconds):
-    """The strict scalar oracle (one f32 chain per output row, parallel over
-    rows) on this host's cores, on a bounded sample of the same GEMV."""
+    """The reference's strict scalar CPU path (one f32 vec_dot chain per
+    output row, rows split over threads) on this host's cores, on a bounded
+    sample of the same GEMV: the reference's own quant code built from its
+    sources (oracle/_ref, kind "reference") where that build travelled with
+    the tree, else the C restatement (kind "port"), which equals it bit for
+    bit."""
     # the GPU box gives one GPU's job 16 host threads (its CPU share), whatever
     # nproc shows; the thread count used and nproc are both reported
     nproc = os.cpu_count() or 1
     cores = min(16, nproc)
+    kind = "reference" if O.ref_available() else "port"
+
+    def run(wb, rows, threads):
+        if kind == "reference":
+            O.ref_gemv(O.Q4_K, wb, x, rows, nthreads=threads)
+        else:
+            O.gemm(O.Q4_K, wb, x, rows, nthreads=threads)
+
     t0 = time.perf_counter()
     reps = 0
     while True:
-        O.gemm(O.Q4_K, w, x, n_out, nthreads=cores)
+        run(w, n_out, cores)
         reps += 1
         if time.perf_counter() - t0 >= seconds:
             break
@@ -321,10 +338,10 @@ def cpu_baseline(O, w, x, n_out, n_in, seconds):
     rows1 = max(1, n_out // 16)
     rb = O.row_bytes(O.Q4_K, n_in)
     t1 = time.perf_counter()
-    O.gemm(O.Q4_K, w[:rows1 * rb], x, rows1, nthreads=1)
+    run(w[:rows1 * rb], rows1, 1)
     dt_one = (time.perf_counter() - t1) * n_out / rows1
     nbytes = rb * n_out + (n_in + n_out) * 4
-    return {"value": nbytes / dt_all / 1e9, "unit": "GB/s", "cores": cores, "nproc": nproc, "kind": "port",
+    return {"value": nbytes / dt_all / 1e9, "unit": "GB/s", "cores": cores, "nproc": nproc, "kind": kind,
             "sample": f"Q4_K GEMV {n_in}->{n_out} M=1, {reps} calls over {dt_all * reps:.1f} s",
             "one_core_GBps": nbytes / dt_one / 1e9}
 
@@ -396,16 +413,14 @@ _Q4K_ROW, _Q6K_ROW, _Q8_ROW = 2304, 3360, 4352
 _HEAD_BYTES = 14336 * _Q4K_ROW + 4 * (4096 + 14336)
 TRACE_LABELS = [
     ("gemv_stream_kernel<12, float, float, 2, 28, 8, true, 0, 8", "262144",
-     "C3 headline: Q4_K GEMV 4096->14336, M=1, f32 activations", _HEAD_BYTES, "B"),
-    ("gemv_stream_kernelILi12EDF16_DF16_Li2ELi28", "262144", "C3 headline shape, f16 activations",
+     "headline: Q4_K GEMV 4096->14336, M=1, f32 activations", _HEAD_BYTES, "B"),
+    ("gemv_stream_kernelILi12EDF16_DF16_Li2ELi28", "262144", "headline shape, f16 activations",
      14336 * _Q4K_ROW + 2 * (4096 + 14336), "B"),
     ("gemv_stream_kernel<2, float, float, 2, 28", "262144", "Q4_0 GEMV 4096->14336, M=1", _HEAD_BYTES, "B"),
     ("gemv_stream_kernel<8, float, float, 2, 28", "262144", "Q8_0 GEMV 4096->14336, M=1",
      14336 * _Q8_ROW + 4 * (4096 + 14336), "B"),
     ("gemv_stream_kernel<14, float, float, 2, 28", "262144", "Q6_K GEMV 4096->14336, M=1",
      14336 * _Q6K_ROW + 4 * (4096 + 14336), "B"),
-    ("probe_read_kernel", "524288", "read ceiling: pure read of the headline's weight bytes",
-     14336 * _Q4K_ROW, "B"),
     ("gemv_stream_kernel<12, float, float, 2, 16, 8, true, 0, 8", "131072",
      "C2 layer: q, k, v, o (Q4_K 4096->4096)", 4096 * _Q4K_ROW + 4 * 8192, "B"),
     ("gemv_stream_kernel<12, float, float, 2, 24, 8, true, 0, 8", "235008",
@@ -458,14 +473,6 @@ TRACE_LABELS = [
     ("quantize_q8_kernelIDF16", "262144", "int8 rung, M=2048: activation quantizer", None, None),
     ("gemm_i8_kernelILi8EDF16", "114688", "int8 rung: Q8_0 4096->14336, M=512", 2 * 512 * 14336 * 4096, "int8"),
     ("quantize_q8_kernelIDF16", "65536", "int8 rung, M=512: activation quantizer", None, None),
-    ("probe_gemm_kernelILb1E", "114688", "f16 ceiling: plain f16 GEMM at the up shape, M=2048",
-     2 * 2048 * 14336 * 4096, "f16"),
-    ("probe_gemm_kernel<true>", "114688", "f16 ceiling: plain f16 GEMM at the up shape, M=2048",
-     2 * 2048 * 14336 * 4096, "f16"),
-    ("probe_gemm_kernelILb0E", "114688", "f16 ceiling: its MFMA + LDS skeleton (no global loads)",
-     2 * 2048 * 14336 * 4096, "f16"),
-    ("probe_gemm_kernel<false>", "114688", "f16 ceiling: its MFMA + LDS skeleton (no global loads)",
-     2 * 2048 * 14336 * 4096, "f16"),
 ]
 
 
@@ -591,6 +598,8 @@ def main():
 
     import kraken_amd as K
 
+    global ROTATE_BYTES
+    ROTATE_BYTES = int(args.rotate_gib * (1 << 30))
     only = set(filter(None, args.only.split(",")))
     want = (lambda k: k in only) if only else (lambda k: True)
     stream = torch.cuda.current_stream()
@@ -604,10 +613,6 @@ def main():
     n_out, n_in = 14336, 4096
     g = bench_gemv(K, torch, be32, timer, args, K.Q4_K, n_out, n_in, seed=1, soak_s=args.soak_seconds)
     log(f"  {g['ms'] * 1e3:.2f} us/call  {g['GBps']:.0f} GB/s  ({g['copies']} copies)")
-    # the floor: a pure read of the same bytes in one launch
-    rc = bench_read_ceiling(torch, be32, timer, g["ws"], g["weight_bytes"])
-    extras["read_ceiling_q4k_4096x14336"] = rc
-    log(f"  read ceiling: {rc['us']:.2f} us  {rc['GBps']:.0f} GB/s ({100 * rc['frac_hbm']:.1f}% of HBM)")
     # the same call with f16 activations (the reference GPU's activation type)
     g16 = bench_gemv(K, torch, be16, timer, args, K.Q4_K, n_out, n_in, seed=1, act_f16=True)
     extras["gemv_q4k_f16act"] = {"us": g16["ms"] * 1e3, "GBps": g16["GBps"]}
@@ -620,11 +625,6 @@ def main():
                 log(f"  {r['ms'] * 1e3:.1f} us  {r['TFLOPs']:.1f} TFLOP/s  ({100 * r['frac']:.1f}%)")
                 extras[f"prefill_q4k_{name}_m{M}"] = {"us": r["ms"] * 1e3, "TFLOPs": r["TFLOPs"],
                                                       "frac_fp16_peak": r["frac"]}
-        # the f16 ceiling beside it: the same shape with no dequantization
-        log("f16 ceiling at the up shape, M=2048 ...")
-        for nm, r in bench_f16_ceiling(torch, be16, timer, 2048, 14336, 4096).items():
-            extras[f"{nm}_up_m2048"] = r
-            log(f"  {nm}: {r['us']:.1f} us  {r['TFLOPs']:.1f} TFLOP/s  ({100 * r['frac_fp16_peak']:.1f}%)")
 
     if want("rows"):
         # batched rows between the decode GEMV (<= 8) and prefill: 16..128

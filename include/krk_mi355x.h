@@ -265,25 +265,6 @@ int krk_moe_dispatch(krk_backend *b, const void *table, int layer,
  * reference, whose dispatch keeps no host-side record of the table. */
 int krk_moe_table_forget(krk_backend *b, const void *table);
 
-/* ---------------------------------------------------------- measurement -- */
-/* A pure read of `bytes` (a multiple of 16, 16-byte aligned device memory)
- * by `blocks` workgroups of 256 threads: the HBM stream ceiling of one
- * launch, which the decode GEMV (every weight byte read once) can
- * approach but not pass.  `sink`: 4 KiB of device memory the probe may
- * write.  Measurement only; no counterpart in the reference. */
-int krk_probe_read(krk_backend *b, const void *src, int64_t bytes, int blocks, void *sink);
-
-/* A plain f16 GEMM, out[M, N] = x[M, K] . w[N, K]^T (f16 rows, 16-byte
- * aligned, K a multiple of 32, f32 accumulate, f16 out), on the matrix cores
- * with both operands moved global -> LDS by DMA: what dense f16 MFMA work
- * reaches on this part with the given operands, beside the prefill GEMM
- * (which adds the dequantization).  loads = 0 runs the same kernel with its
- * operands loaded once and re-read from LDS at every K step (the matrix-core
- * and LDS work alone; `out` is then not the product).  Measurement only; no
- * counterpart in the reference. */
-int krk_probe_gemm(krk_backend *b, const void *x, const void *w, void *out, int64_t M, int64_t N, int64_t K,
-                   int loads);
-
 /* ------------------------------------------------ dequant / quantize ops -- */
 
 /* dequant_row (quant.hpp:203) on the device: out f32 [n_rows, n_in],

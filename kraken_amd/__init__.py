@@ -68,8 +68,6 @@ SIGNATURES = {
     "krk_gemm_noalloc": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64]),
     "krk_gemm_noalloc_scratch_bytes": (C.c_size_t, []),
     "krk_gemm_k_ok": (_i32, [_vp, _i64]),
-    "krk_probe_read": (_i32, [_vp, _vp, _i64, _i32, _vp]),
-    "krk_probe_gemm": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32]),
     "krk_gemm_accumulate": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp,
                                    _P(_i32)]),
     "krk_gemm_group": (_i32, [_vp, _P(_vp), _vp, _P(_vp), _i32, _P(_i64), _i64, _i32,
@@ -241,14 +239,6 @@ class Backend:
         (krk_gemm_noalloc): never allocates; KRK_ERR_NOMEM past its size."""
         self._check(lib().krk_gemm_noalloc(self._h, _ptr(out), _ptr(x), _ptr(w), wt, n_out, n_in,
                                            rows), "gemm_noalloc")
-
-    def probe_read(self, src, nbytes: int, blocks: int, sink):
-        """Measurement: a pure read of nbytes of src (krk_probe_read)."""
-        self._check(lib().krk_probe_read(self._h, _ptr(src), nbytes, blocks, _ptr(sink)), "probe_read")
-
-    def probe_gemm(self, x, w, out, M: int, N: int, K: int, loads: bool = True):
-        """Measurement: a plain f16 GEMM out = x . w^T (krk_probe_gemm)."""
-        self._check(lib().krk_probe_gemm(self._h, _ptr(x), _ptr(w), _ptr(out), M, N, K, int(loads)), "probe_gemm")
 
     def gemm_k_ok(self, k: int) -> bool:
         return bool(lib().krk_gemm_k_ok(self._h, k))

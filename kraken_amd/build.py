@@ -19,7 +19,7 @@ LIB = os.path.join(HERE, "libkrk_mi355x.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["backend.cpp", "synth.cpp", "gguf.cpp", "gemv.hip", "gemv_digits.hip", "gemv_stream.hip", "dequant.hip", "gemm.hip",
-           "gemm_i8.hip", "router.hip", "moe.hip", "probe.hip"]
+           "gemm_i8.hip", "router.hip", "moe.hip"]
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(ROOT, "include"),
           "-I", CSRC]
@@ -27,9 +27,21 @@ DEVICE = ["--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
           "-packed-fp32-ops", "-munsafe-fp-atomics"]
 
 
-def _compile(src: str) -> str:
+def _stale(path: str, obj: str) -> bool:
+    """The object is older than its source or than any header it may include."""
+    if not os.path.exists(obj):
+        return True
+    deps = [path] + [os.path.join(d, f) for d in (CSRC, os.path.join(ROOT, "include"))
+                     for f in os.listdir(d) if f.endswith((".h", ".hpp"))]
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def _compile(src: str, force: bool = True) -> str:
     path = os.path.join(CSRC, src)
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+    if not force and not _stale(path, obj):
+        return obj
     if src.endswith(".hip") or src == "backend.cpp":
         cmd = [HIPCC, *COMMON, *DEVICE, "-x", "hip", "-c", path, "-o", obj]
     else:
@@ -45,11 +57,13 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int | None = None) -> str:
+def build(jobs: int | None = None, force: bool = True) -> str:
+    """Compile every source (force=False: only those whose object is stale)
+    and link the library."""
     os.makedirs(BUILD, exist_ok=True)
     jobs = jobs or min(8, len(SOURCES))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(lambda s: _compile(s, force), SOURCES))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-lpthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -60,4 +74,4 @@ def build(jobs: int | None = None) -> str:
 
 
 if __name__ == "__main__":
-    print(build())
+    print(build(force="--changed" not in sys.argv))

@@ -354,21 +354,6 @@ int krk_gemm_noalloc(krk_backend *b, void *out, const void *x, const void *w, in
 
 size_t krk_gemm_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
-int krk_probe_read(krk_backend *b, const void *src, int64_t bytes, int blocks, void *sink) {
-    if (!b || !src || !sink) return KRK_ERR_ARG;
-    if (int s = make_current(b)) return s;
-    const hipError_t e = krk::probe_read(src, bytes, blocks, sink, b->stream);
-    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "probe_read");
-}
-
-int krk_probe_gemm(krk_backend *b, const void *x, const void *w, void *out, int64_t M, int64_t N, int64_t K,
-                   int loads) {
-    if (!b || !x || !w || !out) return KRK_ERR_ARG;
-    if (int s = make_current(b)) return s;
-    const hipError_t e = krk::probe_gemm(x, w, out, M, N, K, loads != 0, b->stream);
-    return e == hipSuccess ? KRK_OK : hip_fail(b, e, "probe_gemm");
-}
-
 int krk_gemm_accumulate(krk_backend *b, void *dst, const void *x, const void *w, int wt,
                         int64_t n_out, int64_t n_in, int64_t rows, const int32_t *rexp,
                         int *fused) {

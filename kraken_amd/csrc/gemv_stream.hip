@@ -48,6 +48,20 @@ constexpr int kStreamRows = 4;   // dense Q4_K launches of up to this many activ
 
 __device__ __forceinline__ v4i lds_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
+// Load-transpose geometry of a Q4_K tile of TR rows and a wave slice of NBW
+// blocks: P 16-byte pieces per row, NJ load instructions per lane, and a
+// ring of SR row slots (rows 16.. of a two-group tile reuse the slots of
+// rows 0.. once the first group is consumed; the rows that reuse them
+// arrive only in instructions after the last one the first group needs)
+template <int NBW, int TR> struct LtGeom {
+    static constexpr int P = 9 * NBW, SLB = 144 * NBW;
+    static constexpr int NJ = (TR * P + 63) / 64;
+    static constexpr int J0 = (16 * P + 63) / 64 - 1;
+    static constexpr int SR0 = (64 * (J0 + 1) + P - 1) / P;
+    static constexpr int SR = TR <= 16 ? TR : (SR0 < 16 ? 16 : SR0);
+    static_assert(TR <= 32 && (TR <= 16 || SR + 16 >= TR), "two row groups at most");
+};
+
 // Q4_0 sub-block s (of the eight in 256 values) -> its digit-table slot:
 // 0 1 4 5 2 3 6 7, so that MFMA m of lane pair p meets block 4 p + m
 __host__ __device__ constexpr int q40_slot(int s) { return s ^ ((((s >> 1) ^ (s >> 2)) & 1) * 6); }
@@ -81,12 +95,16 @@ __device__ __forceinline__ void load_x8(const _Float16 *p, float (&v)[8]) {
 // expert-major runs (gate/up pairs, down): grid row a = active expert
 // em_runs[a], its weights loaded once and applied to each of its rows in turn
 template <int DT, typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWEXACT, int MOE = 0, int LA = 8,
-          int XR = 1>
+          int XR = 1, bool LT = false>
 __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kernel(SegTable t) {
     // XR: activation rows (dense Q4_K launches of 2..4 rows): every row's
     // activations load before the weights, one digit table per row, each
     // weight group decoded once and multiplied against every row
     static_assert(XR == 1 || (MOE == 0 && DT == DT_Q4_K), "several rows: dense Q4_K");
+    // LT: the weights move as lane-contiguous 16-byte pieces (full cache
+    // lines, nontemporal) and are transposed through the wave's LDS
+    static_assert(!LT || (DT == DT_Q4_K && MOE < 3), "load-transpose: Q4_K, dense or routed");
+    using LTG = LtGeom<NBW, TR>;
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr bool Q40 = DT == DT_Q4_0;
     constexpr bool Q80 = DT == DT_Q8_0;
@@ -240,8 +258,25 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
             qb[i] = ld128(src[i] + 80 + 16 * gq);
         }
     };
+    // LT: piece q = 64 j + lane of the tile is row q / P, bytes 16 (q % P)
+    // of the wave's slice (P pieces per row), all requested at once
+    u32x4 lv[LT ? LTG::NJ : 1];
+    if constexpr (LT) {
 #pragma unroll
-    for (int i = 0; i < (LA < NL ? LA : NL); i++) issue(i);
+        for (int j = 0; j < LTG::NJ; j++) {
+            int q = 64 * j + lane;
+            q = q < TR * LTG::P ? q : TR * LTG::P - 1;
+            const int r = q / LTG::P, o = (q - r * LTG::P) * 16, b = o / 144;
+            int64_t n = pair ? n0 + (r & 15) : n0 + r;
+            if (n >= n_out) n = n_out - 1;
+            const uint8_t *base = pair && r >= 16 ? w2 : w;
+            const int blk = (kb0 + b < nb ? kb0 + b : nb - 1) - kb0 + kblk;
+            lv[j] = ld128_nt(to_global(base + n * rb + static_cast<int64_t>(blk) * 144 + (o - 144 * b)));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < (LA < NL ? LA : NL); i++) issue(i);
+    }
     __builtin_amdgcn_s_setprio(0);
 
     for (int pr = pb; pr < pe; pr++) {
@@ -291,20 +326,33 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
         e = e > 126 ? 126 : e;
         const float up = __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
         const float dn = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
-        uint32_t p0[2] = {0u, 0u}, p1[2] = {0u, 0u}, p2[2] = {0u, 0u};
-        int xsum = 0;
+        // X = rint(x 2^e) by one fma with 1.5 2^23 (x 2^e is exact and
+        // |x 2^e| < 2^22, so the sum rounds to the nearest integer, ties to
+        // even); Y = X + 0x808080 holds the balanced digits as biased bytes:
+        // d_i = byte_i(Y) ^ 0x80 with X = d0 + 2^8 d1 + 2^16 d2
+        uint32_t Y[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int X = live ? static_cast<int>(__builtin_rintf(v[k] * up)) : 0;
-            xsum += X;
-            const int d0 = ((X + 128) & 255) - 128;
-            const int X1 = (X - d0) >> 8;
-            const int d1 = ((X1 + 128) & 255) - 128;
-            const int d2 = (X1 - d1) >> 8;
-            const int sh = 8 * (k & 3);
-            p0[k >> 2] |= (static_cast<uint32_t>(d0) & 255u) << sh;
-            p1[k >> 2] |= (static_cast<uint32_t>(d1) & 255u) << sh;
-            p2[k >> 2] |= (static_cast<uint32_t>(d2) & 255u) << sh;
+        for (int k = 0; k < 8; k++)
+            Y[k] = __float_as_uint(__builtin_fmaf(v[k], up, 12582912.0f)) + (0x808080u - 0x4B400000u);
+        uint32_t p0[2], p1[2], p2[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const uint32_t *y = Y + 4 * hh;
+            // bytes 0 and 1 of a value pair, and byte 2 of it
+            const uint32_t A01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);
+            const uint32_t A23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
+            const uint32_t B01 = __builtin_amdgcn_perm(y[1], y[0], 0x06020602u);
+            const uint32_t B23 = __builtin_amdgcn_perm(y[3], y[2], 0x06020602u);
+            p0[hh] = live ? __builtin_amdgcn_perm(A23, A01, 0x05040100u) ^ 0x80808080u : 0u;
+            p1[hh] = live ? __builtin_amdgcn_perm(A23, A01, 0x07060302u) ^ 0x80808080u : 0u;
+            p2[hh] = live ? __builtin_amdgcn_perm(B23, B01, 0x05040100u) ^ 0x80808080u : 0u;
+        }
+        int xsum = 0;
+        if constexpr (Q6) {
+            uint32_t ys = 0u;
+#pragma unroll
+            for (int k = 0; k < 8; k++) ys += Y[k];
+            xsum = live ? static_cast<int>(ys - 8u * 0x808080u) : 0;
         }
         if (sbw < 8 * NBW) {
             // Q4_0 and Q8_0: block s of the eight sits in table slot
@@ -373,11 +421,37 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     // group i is decoded after group i + LA is requested (LA: requests in
     // flight ahead of the decode; measured best with every request issued
     // before the first decode)
+    // LT: the wave's slice buffer (rows in a ring of LTG::SR slots, so rows
+    // 16.. may reuse the slots of rows 0.. once those are consumed)
+    uint8_t *wbuf = lds + XR * rstride + wv * (LTG::SR * LTG::SLB);
+    auto lt_slot = [&](int r) { return r < LTG::SR ? r : r - LTG::SR; };
+    int lt_put = 0;   // instructions written to the buffer so far
 #pragma unroll
     for (int i = 0; i < NL; i++) {
-        if (i + LA < NL && pr == pb) issue(i + LA);
+        if (!LT && i + LA < NL && pr == pb) issue(i + LA);
         __builtin_amdgcn_sched_barrier(0);
         const int rg = i / NBW, b = i - (i / NBW) * NBW;
+        if constexpr (LT) {
+            // the pieces of every row of row group rg into the buffer (one
+            // wave's LDS operations complete in order)
+            const int jend = ((16 * (rg + 1) < TR ? 16 * (rg + 1) : TR) * LTG::P + 63) / 64;
+#pragma unroll
+            for (int j = 0; j < LTG::NJ; j++) {
+                if (j < lt_put || j >= jend) continue;
+                const int q = 64 * j + lane;
+                if (q < TR * LTG::P) {
+                    const int r = q / LTG::P;
+                    *reinterpret_cast<u32x4 *>(wbuf + lt_slot(r) * LTG::SLB + (q - r * LTG::P) * 16) = lv[j];
+                }
+            }
+            lt_put = jend > lt_put ? jend : lt_put;
+            int r = rg * 16 + c16;
+            r = r < TR ? r : TR - 1;
+            const uint8_t *sb = wbuf + lt_slot(r) * LTG::SLB + 144 * b;
+            hd[i] = *reinterpret_cast<const u32x4 *>(sb);
+            qa[i] = *reinterpret_cast<const u32x4 *>(sb + 16 + 16 * gq);
+            qb[i] = *reinterpret_cast<const u32x4 *>(sb + 80 + 16 * gq);
+        }
         if (kb0 + b >= nb) continue;   // wave-uniform: the ragged slice's missing blocks
         if constexpr (Q6) {
             // chunk qd of the block: in lane group gq = 2 h + l, the 16 values
@@ -617,22 +691,34 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
 size_t stream_lds(int nw, int nbw) {
     return static_cast<size_t>(nw) * nbw * (kTab + 2 * 8 * sizeof(float2)) + 32 * static_cast<size_t>(nw) * sizeof(float);
 }
+// the load-transpose slice buffers of a launch
+size_t stream_lt_lds(int nw, int nbw, int tr) {
+    const int p = 9 * nbw, j0 = (16 * p + 63) / 64 - 1;
+    const int sr0 = (64 * (j0 + 1) + p - 1) / p;
+    const int sr = tr <= 16 ? tr : (sr0 < 16 ? 16 : sr0);
+    return static_cast<size_t>(nw) * sr * 144 * nbw;
+}
 
 template <int DT, typename XT, typename OT, int NBW, int TR, int MOE, int XR = 1>
 hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
-    const size_t l = XR * stream_lds(nw, NBW);
+    // Q4_K one-row launches of two-block slices (K <= 8192) load their
+    // weights by load-transpose; the slice buffers fit the 64 KB of LDS
+    constexpr bool LT = DT == DT_Q4_K && MOE < 3 && XR == 1 && NBW == 2;
+    const size_t l = XR * stream_lds(nw, NBW) + (LT ? stream_lt_lds(nw, NBW, TR) : 0);
     const dim3 grid(static_cast<unsigned>(tiles),
                     static_cast<unsigned>(MOE == 2 ? 1 : MOE >= 3 ? t.em_max_items : t.n));
     if (nw == 8)
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, true, MOE, 8, XR>), grid, dim3(64 * nw), l, st, t);
-    else if (nw < 8)
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, false, MOE, 8, XR>), grid, dim3(64 * nw), l, st, t);
-    else if (nw == kMaxWaves)
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, true, MOE, 8, XR>), grid, dim3(64 * nw), l, st,
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, true, MOE, 8, XR, LT>), grid, dim3(64 * nw), l, st,
                            t);
+    else if (nw < 8)
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, false, MOE, 8, XR, LT>), grid, dim3(64 * nw), l, st,
+                           t);
+    else if (nw == kMaxWaves)
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, true, MOE, 8, XR, LT>), grid, dim3(64 * nw),
+                           l, st, t);
     else
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, false, MOE, 8, XR>), grid, dim3(64 * nw), l,
-                           st, t);
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, false, MOE, 8, XR, LT>), grid,
+                           dim3(64 * nw), l, st, t);
     return hipGetLastError();
 }
 

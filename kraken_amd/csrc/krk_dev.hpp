@@ -68,6 +68,14 @@ __device__ __forceinline__ u32x4 ld128(gbyte *p) {
     return *(const __attribute__((address_space(1))) u32x4 *)p;
 }
 __device__ __forceinline__ u32x4 ldg128(const uint8_t *p) { return ld128(to_global(p)); }
+// A weight read whose whole cache line is consumed by the same instruction
+// (lane-contiguous pieces) and never again: the nontemporal policy ("nt")
+// streams it.  (Reads that use half a line, the other half coming from
+// another instruction, must not take it: the second half is then fetched
+// again.)
+__device__ __forceinline__ u32x4 ld128_nt(gbyte *p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4 *)p);
+}
 // 2-byte aligned reads (Q6_K's 210-byte blocks): the part runs its global
 // memory with unaligned access allowed, which hipcc's gfx950 target assumes
 // (one dwordx4 / dword / ushort load each)

@@ -147,12 +147,6 @@ bool gemm_int8_serves(int wt);
 hipError_t gemm_int8(int wt, const void *w, int64_t row_bytes, const void *x, bool act_f16, void *out,
                      int64_t rows, int64_t n_out, int64_t n_in, void *ws, size_t ws_bytes, hipStream_t st);
 
-// Measurement: a pure read of `bytes` (16-byte aligned) by `blocks`
-// workgroups; `sink` is 4 KiB of device memory it may write.
-hipError_t probe_read(const void *src, int64_t bytes, int blocks, void *sink, hipStream_t st);
-hipError_t probe_gemm(const void *x, const void *w, void *out, int64_t M, int64_t N, int64_t K, bool loads,
-                      hipStream_t st);
-
 // Router and MoE dispatch.
 hipError_t router_softmax(const void *logits, bool act_f16, float *probs, int64_t n_rows,
                           int n_expert, hipStream_t st);

@@ -110,12 +110,28 @@ def ref():
             "ref_dot_q6_K_q8": (_f32, [_vp, _vp, _vp, _i64]),
             "ref_fp16_to_fp32": (_f32, [_u16]),
             "ref_fp32_to_fp16": (_u16, [_f32]),
+            "ref_gemv_strict": (None, [_i32, _vp, _i64, _vp, _i64, _i64, _vp, _i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(r, name)
             fn.restype, fn.argtypes = res, args
         _ref = r
     return _ref
+
+
+def ref_gemv(dt: int, w: np.ndarray, x: np.ndarray, n_out: int, nthreads: int = 8) -> np.ndarray:
+    """The reference's own strict vec_dot per output row (oracle/_ref),
+    rows over nthreads threads; None when oracle/_ref was not built."""
+    r = ref()
+    if r is None:
+        return None
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    rb = int(r.ref_row_bytes(dt, x.size))
+    assert w.size >= n_out * rb
+    out = np.empty(n_out, np.float32)
+    r.ref_gemv_strict(dt, _p(w), rb, _p(x), n_out, x.size, _p(out), nthreads)
+    return out
 
 
 # ---------------------------------------------------------------- numpy API --

@@ -8,6 +8,8 @@
 // (include/krk/quant.hpp:245-273): fast, avx2 and int8 tiers off.
 #include <cstring>
 #include <string>
+#include <thread>
+#include <vector>
 
 #include "krk/gguf.hpp"
 #include "krk/quant.hpp"
@@ -36,6 +38,26 @@ void ref_dequant_row_f16(int dt, const void *src, uint16_t *out, int64_t n) {
 float ref_vec_dot(int dt, const void *src, const float *x, int64_t n) {
     strict_tier();
     return vec_dot(static_cast<DType>(dt), src, x, n);
+}
+// The strict scalar GEMV out[r] = vec_dot(W row r, x), one reference
+// vec_dot call per output row, rows split over nthreads std::threads (the
+// reference CPU backend's split: src/backend_cpu.cpp:1-8, 914-1320; each row
+// is one f32 chain, so the result does not depend on the thread count).
+void ref_gemv_strict(int dt, const void *w, int64_t row_bytes, const float *x, int64_t n_out, int64_t n_in,
+                     float *out, int nthreads) {
+    strict_tier();
+    if (nthreads < 1) nthreads = 1;
+    std::vector<std::thread> th;
+    const int64_t per = (n_out + nthreads - 1) / nthreads;
+    for (int t = 0; t < nthreads; t++) {
+        const int64_t r0 = t * per, r1 = r0 + per < n_out ? r0 + per : n_out;
+        if (r0 >= r1) break;
+        th.emplace_back([=] {
+            for (int64_t r = r0; r < r1; r++)
+                out[r] = vec_dot(static_cast<DType>(dt), static_cast<const u8 *>(w) + r * row_bytes, x, n_in);
+        });
+    }
+    for (auto &t : th) t.join();
 }
 void ref_quantize_q8_row(const float *x, int64_t n, int8_t *xq, float *dx) {
     quantize_q8_row(x, n, xq, dx);

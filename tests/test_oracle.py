@@ -365,6 +365,20 @@ def test_oracle_matches_golden_vectors():
 
 
 @pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (no reference tree)")
+def test_reference_strict_gemv_equals_oracle():
+    """The bench's CPU baseline (the reference's own vec_dot per row over
+    threads) gives the oracle's GEMV bit for bit, for any thread count."""
+    rng = np.random.default_rng(41)
+    for dt in (O.Q4_K, O.Q6_K, O.Q8_0, O.Q4_0):
+        n_out, n_in = 37, 1024
+        w = rand_blocks(rng, dt, n_out * n_in // O.lib().orc_block_size(dt))
+        x = rng.standard_normal(n_in).astype(np.float32)
+        want = O.gemm(dt, w, x, n_out)[0]
+        for th in (1, 3, 8):
+            assert np.array_equal(O.ref_gemv(dt, w, x, n_out, nthreads=th).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (no reference tree)")
 def test_oracle_matches_reference_build():
     ref = O.ref()
     rng = np.random.default_rng(29)
