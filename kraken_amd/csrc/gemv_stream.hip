@@ -262,22 +262,40 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     // of the wave's slice (P pieces per row), all requested at once
     u32x4 lv[LT ? LTG::NJ : 1];
     if constexpr (LT) {
+        // wave-uniform bases and limits; per lane a 32-bit offset (rows are
+        // shorter than 2^26 bytes): the row is clamped to the matrix's last,
+        // the offset to the last 16 bytes of the slice's last block
+        const int64_t slice = static_cast<int64_t>(kblk) * 144;
+        const uint8_t *wb0 = w + n0 * rb + slice;
+        const uint8_t *wb1 = w2 + n0 * rb + slice;
+        const int64_t left = n_out - n0;
+        const int rlim = pair ? 16 : TR;
+        const int rmax = static_cast<int>(left < rlim ? left : rlim) - 1;
+        const int omax = ((nb - kb0 < NBW ? nb - kb0 : NBW) * 144) - 16;
+        const uint32_t rb32 = static_cast<uint32_t>(rb);
 #pragma unroll
         for (int j = 0; j < LTG::NJ; j++) {
-            int q = 64 * j + lane;
-            q = q < TR * LTG::P ? q : TR * LTG::P - 1;
-            const int r = q / LTG::P, o = (q - r * LTG::P) * 16, b = o / 144;
-            int64_t n = pair ? n0 + (r & 15) : n0 + r;
-            if (n >= n_out) n = n_out - 1;
-            const uint8_t *base = pair && r >= 16 ? w2 : w;
-            const int blk = (kb0 + b < nb ? kb0 + b : nb - 1) - kb0 + kblk;
-            lv[j] = ld128_nt(to_global(base + n * rb + static_cast<int64_t>(blk) * 144 + (o - 144 * b)));
+            const int q = 64 * j + lane;
+            const int r = q / LTG::P;
+            int o = (q - r * LTG::P) * 16;
+            o = o < omax ? o : omax;
+            if (pair) {
+                const int rr = (r & 15) < rmax ? (r & 15) : rmax;
+                const uint8_t *bj = r >= 16 ? wb1 : wb0;
+                lv[j] = ld128_nt(to_global(bj + (static_cast<uint32_t>(rr) * rb32 + static_cast<uint32_t>(o))));
+            } else {
+                const int rr = r < rmax ? r : rmax;
+                lv[j] = ld128_nt(to_global(wb0 + (static_cast<uint32_t>(rr) * rb32 + static_cast<uint32_t>(o))));
+            }
         }
     } else {
 #pragma unroll
         for (int i = 0; i < (LA < NL ? LA : NL); i++) issue(i);
     }
     __builtin_amdgcn_s_setprio(0);
+    // the residual scale 2^-rexp of SEG_ACC segments, read while the weights
+    // are in flight rather than after the final barrier
+    const float acc_inv = kind == SEG_ACC && t.rexp ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
 
     for (int pr = pb; pr < pe; pr++) {
     // (expert-major runs: every wave has read the previous row's sums)
@@ -407,13 +425,17 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     v4i HA[HOLD ? NBW : 1][4];
     float2 HE[HOLD ? NBW : 1][2];
     if constexpr (HOLD) {
+        // every lane reads, and the lanes whose A rows are zero mask the
+        // words (no branch around the reads)
+        const int mlo = a_lo ? -1 : 0, mhi = a_hi ? -1 : 0;
 #pragma unroll
         for (int b = 0; b < NBW; b++) {
             const uint8_t *tb = tab + b * kTab + a_off;
-            HA[b][0] = a_lo ? lds_v4i(tb) : Z;
-            HA[b][1] = a_lo ? lds_v4i(tb + 384) : Z;
-            HA[b][2] = a_hi ? lds_v4i(tb) : Z;
-            HA[b][3] = a_hi ? lds_v4i(tb + 384) : Z;
+            const v4i r0 = lds_v4i(tb), r1 = lds_v4i(tb + 384);
+            HA[b][0] = r0 & mlo;
+            HA[b][1] = r1 & mlo;
+            HA[b][2] = r0 & mhi;
+            HA[b][3] = r1 & mhi;
             HE[b][0] = ex[b * 8 + gq];
             HE[b][1] = ex[b * 8 + 4 + gq];
         }
@@ -451,8 +473,11 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
             hd[i] = *reinterpret_cast<const u32x4 *>(sb);
             qa[i] = *reinterpret_cast<const u32x4 *>(sb + 16 + 16 * gq);
             qb[i] = *reinterpret_cast<const u32x4 *>(sb + 80 + 16 * gq);
+            // a ragged slice's missing block: d = dmin = 0 against zero
+            // activations adds exactly zero (no branch between the groups)
+            if (kb0 + b >= nb) hd[i] = u32x4{0u, 0u, 0u, 0u};
         }
-        if (kb0 + b >= nb) continue;   // wave-uniform: the ragged slice's missing blocks
+        if (!LT && kb0 + b >= nb) continue;   // wave-uniform: the ragged slice's missing blocks
         if constexpr (Q6) {
             // chunk qd of the block: in lane group gq = 2 h + l, the 16 values
             // 128 h + 32 qd + 16 l + i -- one scale group; code q = 4 low bits
@@ -655,7 +680,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     }
     }
     __syncthreads();
-    for (int oi = static_cast<int>(threadIdx.x); oi < rows_t * XR; oi += static_cast<int>(blockDim.x)) {
+    for (int oi = static_cast<int>(threadIdx.x); oi < rows_t * XR; oi += 64 * nw) {
     const int xr = XR == 1 ? 0 : oi / rows_t;
     const int r = oi - xr * rows_t;
     if (n0 + r >= n_out) continue;
@@ -680,8 +705,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
             *o = (gs / (1.0f + expf(-gs))) * us;   // silu_mul, backend_cpu.cpp:2401-2406
         }
     } else {
-        const float inv = kind == SEG_ACC && t.rexp ? exp2f(-static_cast<float>(t.rexp[0])) : 1.0f;
-        store_out<OT>(o, row_sum(r), kind, inv);
+        store_out<OT>(o, row_sum(r), kind, acc_inv);
     }
     }   // output rows
     }
@@ -765,6 +789,8 @@ int device_cus() {
 bool gemv_stream_ok(int dt, const SegTable &t) {
     if ((dt != DT_Q4_K && dt != DT_Q6_K && dt != DT_Q4_0 && dt != DT_Q8_0) || t.rows < 1 || t.em_items)
         return false;
+    // (the load-transpose tiles address 32 rows within 32-bit offsets)
+    if (t.row_bytes >= (int64_t{1} << 26)) return false;
     // several activation rows: dense Q4_K, up to kStreamRows, rows 16-byte aligned
     if (t.rows > 1 && (dt != DT_Q4_K || t.rows > kStreamRows || t.moe_tab || t.x_stride % 4)) return false;
     if (t.moe_tab) {
