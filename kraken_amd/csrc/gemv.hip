@@ -1426,23 +1426,6 @@ static hipError_t dispatch_dt(int dt, const SegTable &t, hipStream_t st) {
 
 hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st) {
     if (gemv_stream_ok(dt, t)) return gemv_stream(dt, act_f16, t, st);
-    // Q4_K rows 5..8: the streaming kernel's four-row launch and one for the
-    // rest (each reads the weights once; measured faster than the digit
-    // kernel's single pass over the eight)
-    if (dt == DT_Q4_K && t.rows > 4 && t.rows <= 8 && !t.moe_tab && !t.rexp) {
-        SegTable lo = t, hi = t;
-        lo.rows = 4;
-        hi.rows = t.rows - 4;
-        const int64_t es = act_f16 ? 2 : 4;   // activations and outputs share the type
-        for (int i = 0; i < t.n; i++) {
-            hi.seg[i].x = static_cast<const uint8_t *>(t.seg[i].x) + 4 * t.x_stride * es;
-            hi.seg[i].out = static_cast<uint8_t *>(t.seg[i].out) + 4 * t.out_stride * es;
-        }
-        if (gemv_stream_ok(dt, lo) && gemv_stream_ok(dt, hi)) {
-            const hipError_t e = gemv_stream(dt, act_f16, lo, st);
-            return e != hipSuccess ? e : gemv_stream(dt, act_f16, hi, st);
-        }
-    }
     if (gemv_digits_ok(dt, t)) return gemv_digits(dt, act_f16, t, st);
     if (act_f16) return dispatch_dt<_Float16, _Float16>(dt, t, st);
     return dispatch_dt<float, float>(dt, t, st);

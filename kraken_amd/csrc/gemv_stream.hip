@@ -29,6 +29,7 @@
 // 32, chosen per launch so that the tiles fill the chip in as few rounds as
 // possible); gate/up (SEG_SILU) segments take 16 gate rows and the same 16
 // up rows and write silu(gate) * up.  The grid is tiles x segments.
+#include <algorithm>
 #include <cstdint>
 
 #include "gemv_core.hpp"
@@ -44,7 +45,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kTab = 768;   // digit bytes per 256-value block: 8 sub-blocks x 3 planes x 32
 constexpr int kMaxWaves = 16;
-constexpr int kStreamRows = 4;   // dense Q4_K launches of up to this many activation rows
+constexpr int kStreamRows = 8;   // dense Q4_K launches of up to this many activation rows
+constexpr int kStreamRowsWide = 4;   // ... of slices wider than two blocks
+constexpr size_t kLdsMax = 163840;   // LDS per workgroup on gfx950 (160 KB)
 
 __device__ __forceinline__ v4i lds_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
@@ -96,7 +99,10 @@ __device__ __forceinline__ void load_x8(const _Float16 *p, float (&v)[8]) {
 // em_runs[a], its weights loaded once and applied to each of its rows in turn
 template <int DT, typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWEXACT, int MOE = 0, int LA = 8,
           int XR = 1, bool LT = false>
-__global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kernel(SegTable t) {
+// (the second bound is waves per SIMD: four for the expert-major runs and
+// for six to eight rows, whose registers would otherwise leave one
+// workgroup per CU)
+__global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8) ? 4 : 1) gemv_stream_kernel(SegTable t) {
     // XR: activation rows (dense Q4_K launches of 2..4 rows): every row's
     // activations load before the weights, one digit table per row, each
     // weight group decoded once and multiplied against every row
@@ -180,7 +186,11 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     // 8 (l & 3) .. + 7 of the slice's sub-block 16 p + l / 4
     // the loads issue at raised wave priority, so a wave that is still
     // issuing wins the vector-memory port over one that is already decoding
-    float xvr[XR][NPASS][8];
+    // rows per pass: six to eight rows run in passes of four, their digit
+    // tables rebuilt in the same (wave-private) LDS while the weights stay
+    // in registers, so two workgroups still fit a CU
+    constexpr int XP = XR > 5 ? 4 : XR;
+    float xvr[XP][NPASS][8];
     auto load_xrow_to = [&](const XT *xr, float (&xv)[NPASS][8]) {
 #pragma unroll
         for (int p = 0; p < NPASS; p++) {
@@ -197,7 +207,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     __builtin_amdgcn_s_setprio(3);
     load_xrow(row_x(pb));
 #pragma unroll
-    for (int xr = 1; xr < XR; xr++) load_xrow_to(x + xr * t.x_stride, xvr[xr]);
+    for (int xr = 1; xr < XP; xr++) load_xrow_to(x + xr * t.x_stride, xvr[xr]);
     // ---- then every weight byte of the wave's slice of the tile: group i =
     // (row group rg, block b), lane (c16, gq) takes of row rg * 16 + c16:
     //   Q4_K: the 16-byte header and code bytes 16 gq .. + 15 of each
@@ -265,10 +275,15 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
         // wave-uniform bases and limits; per lane a 32-bit offset (rows are
         // shorter than 2^26 bytes): the row is clamped to the matrix's last,
         // the offset to the last 16 bytes of the slice's last block
+        // (a segment shorter than the grid's width gives its extra tiles
+        // n0 >= n_out: they re-read the matrix's last row, as the plain
+        // path does, and store nothing; rmax is never negative, so the
+        // unsigned offsets below stay inside the matrix)
         const int64_t slice = static_cast<int64_t>(kblk) * 144;
-        const uint8_t *wb0 = w + n0 * rb + slice;
-        const uint8_t *wb1 = w2 + n0 * rb + slice;
-        const int64_t left = n_out - n0;
+        const int64_t nbase = n0 < n_out ? n0 : n_out - 1;
+        const uint8_t *wb0 = w + nbase * rb + slice;
+        const uint8_t *wb1 = w2 + nbase * rb + slice;
+        const int64_t left = n_out - nbase;
         const int rlim = pair ? 16 : TR;
         const int rmax = static_cast<int>(left < rlim ? left : rlim) - 1;
         const int omax = ((nb - kb0 < NBW ? nb - kb0 : NBW) * 144) - 16;
@@ -305,25 +320,54 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     // for Q6_K the exact integer sums of X over each 16-value half (int bits)
     // (several rows: the LDS holds XR times the tables, {2^-e, sum x}
     // arrays and partial sums, row by row)
-    const int rstride = nw * (NBW * kTab + 2 * NBW * 8 * static_cast<int>(sizeof(float2))) + 32 * nw * 4;
-    auto tab_of = [&](int xr) { return lds + xr * rstride + wv * (NBW * kTab); };
-    auto ex_of = [&](int xr) {
-        return reinterpret_cast<float2 *>(lds + xr * rstride + nw * (NBW * kTab)) + wv * (NBW * 8);
+    // layout: XP table slots, then the XR rows' partial sums, then (LT) the
+    // slice buffers
+    const int tstride = nw * (NBW * kTab + 2 * NBW * 8 * static_cast<int>(sizeof(float2)));
+    const int rstride = XP * tstride + XR * 32 * nw * 4;
+    auto tab_of = [&](int sl) { return lds + sl * tstride + wv * (NBW * kTab); };
+    auto ex_of = [&](int sl) {
+        return reinterpret_cast<float2 *>(lds + sl * tstride + nw * (NBW * kTab)) + wv * (NBW * 8);
     };
-    auto red_of = [&](int xr) {
-        return reinterpret_cast<float *>(lds + xr * rstride + nw * (NBW * kTab + 2 * NBW * 8 * sizeof(float2)));
-    };
+    auto red_of = [&](int xr) { return reinterpret_cast<float *>(lds + XP * tstride + xr * 32 * nw * 4); };
     uint8_t *tab = tab_of(0);
     float2 *ex = ex_of(0);
     float2 *ex16 = reinterpret_cast<float2 *>(lds + nw * (NBW * kTab)) + nw * (NBW * 8) + wv * (NBW * 8);
+    // ---- per-lane MFMA roles (A row c16 = 4 sub-block' + digit plane)
+    const int ap = c16 & 3, as = c16 >> 2;
+    const int sl = 2 * (gq >> 1);
+    const bool a_lo = ap < 3 && as == sl, a_hi = ap < 3 && as == sl + 1;
+    const int a_off = as * 96 + (ap < 3 ? ap : 0) * 32 + 16 * (gq & 1);
+    const uint32_t M = 0x0F0F0F0Fu;
+    const uint32_t bsh = 8u * static_cast<uint32_t>(gq);
+    const v4i Z = {0, 0, 0, 0};
+    // Q6_K: lane group gq's A rows hold sub-block 4 h + qd's half l
+    const bool a6 = ap < 3 && as == gq;
+    const int a6_off = 4 * h6 * 96 + (ap < 3 ? ap : 0) * 32 + 16 * lh6;
+    float acc[RG];
 #pragma unroll
-    for (int xr = 0; xr < XR; xr++) {
-    uint8_t *tab = tab_of(xr);
-    float2 *ex = ex_of(xr);
+    for (int rg = 0; rg < RG; rg++) acc[rg] = 0.0f;
+    float accx[XR > 1 ? XR - 1 : 1][RG];   // activation rows 1..
+#pragma unroll
+    for (int xr = 0; xr < (XR > 1 ? XR - 1 : 1); xr++)
+#pragma unroll
+        for (int rg = 0; rg < RG; rg++) accx[xr][rg] = 0.0f;
+#pragma unroll
+    for (int p0 = 0; p0 < XR; p0 += XP) {
+    const int pend = p0 + XP < XR ? p0 + XP : XR;
+    // (a later pass's activations: L2-resident rows, loaded once the
+    // previous pass has released their registers)
+    if (p0 > 0) {
+#pragma unroll
+        for (int xr = p0; xr < pend; xr++) load_xrow_to(x + xr * t.x_stride, xvr[xr - p0]);
+    }
+#pragma unroll
+    for (int xr = p0; xr < pend; xr++) {
+    uint8_t *tab = tab_of(xr - p0);
+    float2 *ex = ex_of(xr - p0);
 #pragma unroll
     for (int p = 0; p < NPASS; p++) {
         const int sbw = p * 16 + (lane >> 2);
-        const float *v = xvr[xr][p];
+        const float *v = xvr[xr - p0][p];
         float amax = 0.0f, sum = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
@@ -398,25 +442,6 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     // (expert-major runs: the next row's activations load while this one
     // is multiplied)
     if (MOE >= 3 && pr + 1 < pe) load_xrow(row_x(pr + 1));
-    // ---- per-lane MFMA roles (A row c16 = 4 sub-block' + digit plane)
-    const int ap = c16 & 3, as = c16 >> 2;
-    const int sl = 2 * (gq >> 1);
-    const bool a_lo = ap < 3 && as == sl, a_hi = ap < 3 && as == sl + 1;
-    const int a_off = as * 96 + (ap < 3 ? ap : 0) * 32 + 16 * (gq & 1);
-    const uint32_t M = 0x0F0F0F0Fu;
-    const uint32_t bsh = 8u * static_cast<uint32_t>(gq);
-    const v4i Z = {0, 0, 0, 0};
-    // Q6_K: lane group gq's A rows hold sub-block 4 h + qd's half l
-    const bool a6 = ap < 3 && as == gq;
-    const int a6_off = 4 * h6 * 96 + (ap < 3 ? ap : 0) * 32 + 16 * lh6;
-    float acc[RG];
-#pragma unroll
-    for (int rg = 0; rg < RG; rg++) acc[rg] = 0.0f;
-    float accx[XR > 1 ? XR - 1 : 1][RG];   // activation rows 1..
-#pragma unroll
-    for (int xr = 0; xr < (XR > 1 ? XR - 1 : 1); xr++)
-#pragma unroll
-        for (int rg = 0; rg < RG; rg++) accx[xr][rg] = 0.0f;
     // two-block slices read their A operands once, before the first group
     // lands (wider slices read them per group: registers)
     // (expert-major runs keep their weights live across rows, several
@@ -445,12 +470,12 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
     // before the first decode)
     // LT: the wave's slice buffer (rows in a ring of LTG::SR slots, so rows
     // 16.. may reuse the slots of rows 0.. once those are consumed)
-    uint8_t *wbuf = lds + XR * rstride + wv * (LTG::SR * LTG::SLB);
+    uint8_t *wbuf = lds + rstride + wv * (LTG::SR * LTG::SLB);
     auto lt_slot = [&](int r) { return r < LTG::SR ? r : r - LTG::SR; };
     int lt_put = 0;   // instructions written to the buffer so far
 #pragma unroll
     for (int i = 0; i < NL; i++) {
-        if (!LT && i + LA < NL && pr == pb) issue(i + LA);
+        if (!LT && i + LA < NL && pr == pb && p0 == 0) issue(i + LA);
         __builtin_amdgcn_sched_barrier(0);
         const int rg = i / NBW, b = i - (i / NBW) * NBW;
         if constexpr (LT) {
@@ -648,17 +673,18 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
             a = __builtin_fmaf(-dmin * m1, e1.y, a);
             return a;
         };
-        acc[rg] = row_dot(A0l, A1l, A0h, A1h, ex0, ex1, acc[rg]);
+        if (p0 == 0) acc[rg] = row_dot(A0l, A1l, A0h, A1h, ex0, ex1, acc[rg]);
 #pragma unroll
-        for (int xr = 1; xr < XR; xr++) {
-            const uint8_t *tx = tab_of(xr) + b * kTab + a_off;
-            const float2 *ey = ex_of(xr);
+        for (int xr = p0 > 1 ? p0 : 1; xr < pend; xr++) {
+            const uint8_t *tx = tab_of(xr - p0) + b * kTab + a_off;
+            const float2 *ey = ex_of(xr - p0);
             accx[xr - 1][rg] = row_dot(a_lo ? lds_v4i(tx) : Z, a_lo ? lds_v4i(tx + 384) : Z, a_hi ? lds_v4i(tx) : Z,
                                        a_hi ? lds_v4i(tx + 384) : Z, ey[b * 8 + gq], ey[b * 8 + 4 + gq],
                                        accx[xr - 1][rg]);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
+    }   // passes of activation rows
 
     // ---- the waves' partial sums -> LDS [row][wave]; one thread per output
     // row adds them in wave order
@@ -712,8 +738,9 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 ? 4 : 1) gemv_stream_kern
 }
 
 
-size_t stream_lds(int nw, int nbw) {
-    return static_cast<size_t>(nw) * nbw * (kTab + 2 * 8 * sizeof(float2)) + 32 * static_cast<size_t>(nw) * sizeof(float);
+size_t stream_lds(int nw, int nbw, int xr = 1) {
+    const size_t xp = xr > 5 ? 4 : xr;   // table slots: rows per pass
+    return xp * nw * nbw * (kTab + 2 * 8 * sizeof(float2)) + xr * 32 * static_cast<size_t>(nw) * sizeof(float);
 }
 // the load-transpose slice buffers of a launch
 size_t stream_lt_lds(int nw, int nbw, int tr) {
@@ -728,7 +755,7 @@ hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
     // Q4_K one-row launches of two-block slices (K <= 8192) load their
     // weights by load-transpose; the slice buffers fit the 64 KB of LDS
     constexpr bool LT = DT == DT_Q4_K && MOE < 3 && XR == 1 && NBW == 2;
-    const size_t l = XR * stream_lds(nw, NBW) + (LT ? stream_lt_lds(nw, NBW, TR) : 0);
+    const size_t l = stream_lds(nw, NBW, XR) + (LT ? stream_lt_lds(nw, NBW, TR) : 0);
     const dim3 grid(static_cast<unsigned>(tiles),
                     static_cast<unsigned>(MOE == 2 ? 1 : MOE >= 3 ? t.em_max_items : t.n));
     if (nw == 8)
@@ -834,7 +861,10 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
     for (int i = 0; i < t.n; i++) rows += t.seg[i].n_out;
     const int nw = (t.n_in / 256 + nbw - 1) / nbw;
     // (several rows: their digit tables within the default 64 KB of LDS)
-    if (t.rows > 1 && t.rows * stream_lds(nw, nbw) > 65536) return false;
+    // (several rows: their digit tables within the 160 KB of LDS; five and
+    // more rows on two-block slices)
+    if (t.rows > 1 && (stream_lds(nw, nbw, static_cast<int>(t.rows)) > kLdsMax || (t.rows > kStreamRowsWide && nbw != 2)))
+        return false;
     if (rows > 2 * 32 * static_cast<int64_t>(device_cus()) * (nw <= 8 ? 2 : 1)) return false;
     for (int i = 0; i < t.n; i++) {
         const Seg &s = t.seg[i];
@@ -919,10 +949,16 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
     // two row groups; 16 for slices of more than two blocks, whose registers
     // hold one row group), the one whose tiles fill the resident workgroups
     // (two per CU at up to eight waves) in the fewest rounds x rows
-    const int64_t cap = static_cast<int64_t>(device_cus()) * (nw <= 8 ? 2 : 1);
+    // (workgroups per CU: two at up to eight waves, fewer when several rows'
+    // tables fill the LDS)
+    const size_t lds1 = stream_lds(nw, nbw, static_cast<int>(t.rows)) + (t.rows == 1 ? stream_lt_lds(nw, nbw, 32) : 0);
+    const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(nw <= 8 ? 2 : 1, static_cast<int64_t>(kLdsMax / lds1)));
+    const int64_t cap = static_cast<int64_t>(device_cus()) * per_cu;
     int tr = 16;
     int64_t best = INT64_MAX;
-    for (int c = has_pair ? 32 : 16; c <= (nbw > 2 ? 16 : 32); c += 4) {
+    // (six to eight rows: one row group, whose registers hold the weights
+    // beside four rows' operands without spilling)
+    for (int c = has_pair ? 32 : 16; c <= (nbw > 2 || t.rows > 5 ? 16 : 32); c += 4) {
         int64_t tiles = 0;
         for (int i = 0; i < t.n; i++) {
             const int rows_t = t.seg[i].kind == SEG_SILU ? 16 : c;
@@ -959,6 +995,19 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
         case 4:
             return act_f16 ? launch_nbw<DT_Q4_K, _Float16, _Float16, 4>(nbw, t, tr, width, nw, st)
                            : launch_nbw<DT_Q4_K, float, float, 4>(nbw, t, tr, width, nw, st);
+        // five to eight rows: two-block slices only (gemv_stream_ok)
+        case 5:
+            return act_f16 ? launch_tr<DT_Q4_K, _Float16, _Float16, 2, 5>(t, tr, width, nw, st)
+                           : launch_tr<DT_Q4_K, float, float, 2, 5>(t, tr, width, nw, st);
+        case 6:
+            return act_f16 ? launch_tr<DT_Q4_K, _Float16, _Float16, 2, 6>(t, tr, width, nw, st)
+                           : launch_tr<DT_Q4_K, float, float, 2, 6>(t, tr, width, nw, st);
+        case 7:
+            return act_f16 ? launch_tr<DT_Q4_K, _Float16, _Float16, 2, 7>(t, tr, width, nw, st)
+                           : launch_tr<DT_Q4_K, float, float, 2, 7>(t, tr, width, nw, st);
+        case 8:
+            return act_f16 ? launch_tr<DT_Q4_K, _Float16, _Float16, 2, 8>(t, tr, width, nw, st)
+                           : launch_tr<DT_Q4_K, float, float, 2, 8>(t, tr, width, nw, st);
         default: break;
     }
     return act_f16 ? launch_nbw<DT_Q4_K, _Float16, _Float16>(nbw, t, tr, width, nw, st)

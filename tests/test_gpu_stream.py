@@ -91,10 +91,11 @@ def test_stream_groups(krk, torch_cuda, be32, be16, dt):
     assert rel(host(dst)[0].astype(np.float32), want) <= 1e-3
 
 
-@pytest.mark.parametrize("rows", [2, 3, 4])
+@pytest.mark.parametrize("rows", [2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("n_out,n_in", [(17, 512), (300, 2304), (14336, 4096), (4096, 11008), (77, 14336)])
 def test_stream_rows(krk, torch_cuda, be32, be16, rows, n_out, n_in):
-    """Dense Q4_K launches of 2..4 activation rows on the streaming kernel:
+    """Dense Q4_K launches of 2..8 activation rows on the streaming kernel
+    (five and more on two-block slices; wider ones go to the digit kernel):
     one digit table per row, every weight group multiplied against each
     row; f32 rows at the 1e-5 bar, f16 rows within their rounding."""
     torch = torch_cuda
