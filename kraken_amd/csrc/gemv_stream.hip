@@ -752,9 +752,12 @@ size_t stream_lt_lds(int nw, int nbw, int tr) {
 
 template <int DT, typename XT, typename OT, int NBW, int TR, int MOE, int XR = 1>
 hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
-    // Q4_K one-row launches of two-block slices (K <= 8192) load their
-    // weights by load-transpose; the slice buffers fit the 64 KB of LDS
-    constexpr bool LT = DT == DT_Q4_K && MOE < 3 && XR == 1 && NBW == 2;
+    // Q4_K one-row launches of two-block slices (K <= 8192), and of
+    // three-block slices in 16-row tiles (K <= 12288: the routed down
+    // projection, 11008-wide rows), load their weights by load-transpose;
+    // at sixteen waves the three-block buffers and tables take 156 KB of the
+    // 160 KB of LDS
+    constexpr bool LT = DT == DT_Q4_K && MOE < 3 && XR == 1 && (NBW == 2 || (NBW == 3 && TR == 16));
     const size_t l = stream_lds(nw, NBW, XR) + (LT ? stream_lt_lds(nw, NBW, TR) : 0);
     const dim3 grid(static_cast<unsigned>(tiles),
                     static_cast<unsigned>(MOE == 2 ? 1 : MOE >= 3 ? t.em_max_items : t.n));
