@@ -51,13 +51,15 @@ constexpr size_t kLdsMax = 163840;   // LDS per workgroup on gfx950 (160 KB)
 
 __device__ __forceinline__ v4i lds_v4i(const uint8_t *p) { return *reinterpret_cast<const v4i *>(p); }
 
-// Load-transpose geometry of a Q4_K tile of TR rows and a wave slice of NBW
-// blocks: P 16-byte pieces per row, NJ load instructions per lane, and a
-// ring of SR row slots (rows 16.. of a two-group tile reuse the slots of
-// rows 0.. once the first group is consumed; the rows that reuse them
+// Load-transpose geometry of a tile of TR rows and a wave slice of NBW
+// blocks of PB 16-byte pieces each (Q4_K: 9 pieces = its 144 bytes; Q6_K:
+// 14 pieces over its 210 bytes, the last one its bytes 194..209) on LDS
+// strides of 16 PB bytes: P pieces per row, NJ load instructions per lane,
+// and a ring of SR row slots (rows 16.. of a two-group tile reuse the slots
+// of rows 0.. once the first group is consumed; the rows that reuse them
 // arrive only in instructions after the last one the first group needs)
-template <int NBW, int TR> struct LtGeom {
-    static constexpr int P = 9 * NBW, SLB = 144 * NBW;
+template <int NBW, int TR, int PB = 9> struct LtGeom {
+    static constexpr int P = PB * NBW, SLB = 16 * PB * NBW;
     static constexpr int NJ = (TR * P + 63) / 64;
     static constexpr int J0 = (16 * P + 63) / 64 - 1;
     static constexpr int SR0 = (64 * (J0 + 1) + P - 1) / P;
@@ -109,8 +111,8 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
     static_assert(XR == 1 || (MOE == 0 && DT == DT_Q4_K), "several rows: dense Q4_K");
     // LT: the weights move as lane-contiguous 16-byte pieces (full cache
     // lines, nontemporal) and are transposed through the wave's LDS
-    static_assert(!LT || (DT == DT_Q4_K && MOE < 3), "load-transpose: Q4_K, dense or routed");
-    using LTG = LtGeom<NBW, TR>;
+    static_assert(!LT || ((DT == DT_Q4_K || DT == DT_Q6_K) && MOE < 3), "load-transpose: Q4_K or Q6_K, dense or routed");
+    using LTG = LtGeom<NBW, TR, DT == DT_Q6_K ? 14 : 9>;
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr bool Q40 = DT == DT_Q4_0;
     constexpr bool Q80 = DT == DT_Q8_0;
@@ -219,6 +221,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
     //   Q4_0, Q8_0: blocks 2 gq and 2 gq + 1 of the eight (hd, qa, qb, qc, dd)
     u32x4 hd[NL], qa[NL], qb[NL];
     u32x4 sc[Q6 ? NL : 1];
+    uint32_t dd6[Q6 && LT ? NL : 1];   // (LT) Q6_K's d, read from the LDS copy
     uint32_t dd[QS ? NL : 1];
     u32x4 qc[Q80 ? NL : 1];
     const int h6 = gq >> 1, lh6 = gq & 1;
@@ -279,7 +282,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
         // n0 >= n_out: they re-read the matrix's last row, as the plain
         // path does, and store nothing; rmax is never negative, so the
         // unsigned offsets below stay inside the matrix)
-        const int64_t slice = static_cast<int64_t>(kblk) * 144;
+        const int64_t slice = static_cast<int64_t>(kblk) * BB;
         const int64_t nbase = n0 < n_out ? n0 : n_out - 1;
         const uint8_t *wb0 = w + nbase * rb + slice;
         const uint8_t *wb1 = w2 + nbase * rb + slice;
@@ -287,13 +290,20 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
         const int rlim = pair ? 16 : TR;
         const int rmax = static_cast<int>(left < rlim ? left : rlim) - 1;
         const int omax = ((nb - kb0 < NBW ? nb - kb0 : NBW) * 144) - 16;
+        const int bmax = (nb - kb0 < NBW ? nb - kb0 : NBW) - 1;   // the slice's last block
         const uint32_t rb32 = static_cast<uint32_t>(rb);
 #pragma unroll
         for (int j = 0; j < LTG::NJ; j++) {
             const int q = 64 * j + lane;
             const int r = q / LTG::P;
             int o = (q - r * LTG::P) * 16;
-            o = o < omax ? o : omax;
+            if constexpr (Q6) {
+                // piece kk of block b: bytes 16 kk, the last one bytes 194..209
+                const int k = q - r * LTG::P, bq = k / 14, kk = k - 14 * bq;
+                o = (bq < bmax ? bq : bmax) * 210 + (kk < 13 ? 16 * kk : 194);
+            } else {
+                o = o < omax ? o : omax;
+            }
             if (pair) {
                 const int rr = (r & 15) < rmax ? (r & 15) : rmax;
                 const uint8_t *bj = r >= 16 ? wb1 : wb0;
@@ -494,13 +504,29 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
             lt_put = jend > lt_put ? jend : lt_put;
             int r = rg * 16 + c16;
             r = r < TR ? r : TR - 1;
-            const uint8_t *sb = wbuf + lt_slot(r) * LTG::SLB + 144 * b;
-            hd[i] = *reinterpret_cast<const u32x4 *>(sb);
-            qa[i] = *reinterpret_cast<const u32x4 *>(sb + 16 + 16 * gq);
-            qb[i] = *reinterpret_cast<const u32x4 *>(sb + 80 + 16 * gq);
-            // a ragged slice's missing block: d = dmin = 0 against zero
-            // activations adds exactly zero (no branch between the groups)
-            if (kb0 + b >= nb) hd[i] = u32x4{0u, 0u, 0u, 0u};
+            const uint8_t *sb = wbuf + lt_slot(r) * LTG::SLB + 16 * (LTG::P / NBW) * b;
+            if constexpr (Q6) {
+                // LDS block: bytes 0..207 in place, bytes 194..209 at 208..223:
+                // the sixteen scales at 192 (this half's eight at 8 h), d at 222
+                hd[i] = *reinterpret_cast<const u32x4 *>(sb + 64 * h6 + 16 * lh6);
+                qa[i] = *reinterpret_cast<const u32x4 *>(sb + 64 * h6 + 32 + 16 * lh6);
+                qb[i] = *reinterpret_cast<const u32x4 *>(sb + 128 + 32 * h6 + 16 * lh6);
+                sc[i] = *reinterpret_cast<const u32x4 *>(sb + 192);
+                dd6[i] = *reinterpret_cast<const uint32_t *>(sb + 220) >> 16;
+                // a ragged slice's missing block: d = 0 and zero scales add
+                // exactly zero
+                if (kb0 + b >= nb) {
+                    sc[i] = u32x4{0u, 0u, 0u, 0u};
+                    dd6[i] = 0u;
+                }
+            } else {
+                hd[i] = *reinterpret_cast<const u32x4 *>(sb);
+                qa[i] = *reinterpret_cast<const u32x4 *>(sb + 16 + 16 * gq);
+                qb[i] = *reinterpret_cast<const u32x4 *>(sb + 80 + 16 * gq);
+                // a ragged slice's missing block: d = dmin = 0 against zero
+                // activations adds exactly zero (no branch between the groups)
+                if (kb0 + b >= nb) hd[i] = u32x4{0u, 0u, 0u, 0u};
+            }
         }
         if (!LT && kb0 + b >= nb) continue;   // wave-uniform: the ragged slice's missing blocks
         if constexpr (Q6) {
@@ -511,9 +537,18 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
             // S = sum (q - 32) X, |S| <= 16 * 32 * 2^22, exact in wrapping int32
             const u32x4 l0 = hd[i], l1 = qa[i], qh = qb[i];
             // d from a lane of half 1 (lane l ^ 32 or l itself)
-            const float d = h2f(__builtin_amdgcn_permlane32_swap(sc[i].w, sc[i].w, false, false)[1] >> 16);
-            const uint32_t scx = h6 ? __builtin_amdgcn_alignbyte(sc[i].z, sc[i].y, 2) : sc[i].x;
-            const uint32_t scy = h6 ? __builtin_amdgcn_alignbyte(sc[i].w, sc[i].z, 2) : sc[i].y;
+            float d;
+            uint32_t scx, scy;
+            if constexpr (LT) {
+                // (LDS copy: all sixteen scales from byte 192, d beside)
+                d = h2f(dd6[i]);
+                scx = h6 ? sc[i].z : sc[i].x;
+                scy = h6 ? sc[i].w : sc[i].y;
+            } else {
+                d = h2f(__builtin_amdgcn_permlane32_swap(sc[i].w, sc[i].w, false, false)[1] >> 16);
+                scx = h6 ? __builtin_amdgcn_alignbyte(sc[i].z, sc[i].y, 2) : sc[i].x;
+                scy = h6 ? __builtin_amdgcn_alignbyte(sc[i].w, sc[i].z, 2) : sc[i].y;
+            }
             float a = acc[rg];
 #pragma unroll
             for (int qd = 0; qd < 4; qd++) {
@@ -743,11 +778,11 @@ size_t stream_lds(int nw, int nbw, int xr = 1) {
     return xp * nw * nbw * (kTab + 2 * 8 * sizeof(float2)) + xr * 32 * static_cast<size_t>(nw) * sizeof(float);
 }
 // the load-transpose slice buffers of a launch
-size_t stream_lt_lds(int nw, int nbw, int tr) {
-    const int p = 9 * nbw, j0 = (16 * p + 63) / 64 - 1;
+size_t stream_lt_lds(int nw, int nbw, int tr, int pb = 9) {
+    const int p = pb * nbw, j0 = (16 * p + 63) / 64 - 1;
     const int sr0 = (64 * (j0 + 1) + p - 1) / p;
     const int sr = tr <= 16 ? tr : (sr0 < 16 ? 16 : sr0);
-    return static_cast<size_t>(nw) * sr * 144 * nbw;
+    return static_cast<size_t>(nw) * sr * 16 * pb * nbw;
 }
 
 template <int DT, typename XT, typename OT, int NBW, int TR, int MOE, int XR = 1>
@@ -757,8 +792,10 @@ hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
     // projection, 11008-wide rows), load their weights by load-transpose;
     // at sixteen waves the three-block buffers and tables take 156 KB of the
     // 160 KB of LDS
-    constexpr bool LT = DT == DT_Q4_K && MOE < 3 && XR == 1 && (NBW == 2 || (NBW == 3 && TR == 16));
-    const size_t l = stream_lds(nw, NBW, XR) + (LT ? stream_lt_lds(nw, NBW, TR) : 0);
+    // (Q6_K: two-block slices)
+    constexpr bool LT = MOE < 3 && XR == 1 &&
+                        ((DT == DT_Q4_K && (NBW == 2 || (NBW == 3 && TR == 16))) || (DT == DT_Q6_K && NBW == 2));
+    const size_t l = stream_lds(nw, NBW, XR) + (LT ? stream_lt_lds(nw, NBW, TR, DT == DT_Q6_K ? 14 : 9) : 0);
     const dim3 grid(static_cast<unsigned>(tiles),
                     static_cast<unsigned>(MOE == 2 ? 1 : MOE >= 3 ? t.em_max_items : t.n));
     if (nw == 8)
@@ -954,7 +991,8 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
     // (two per CU at up to eight waves) in the fewest rounds x rows
     // (workgroups per CU: two at up to eight waves, fewer when several rows'
     // tables fill the LDS)
-    const size_t lds1 = stream_lds(nw, nbw, static_cast<int>(t.rows)) + (t.rows == 1 ? stream_lt_lds(nw, nbw, 32) : 0);
+    const size_t lds1 = stream_lds(nw, nbw, static_cast<int>(t.rows)) +
+                        (t.rows == 1 ? stream_lt_lds(nw, nbw, 32, dt == DT_Q6_K ? 14 : 9) : 0);
     const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(nw <= 8 ? 2 : 1, static_cast<int64_t>(kLdsMax / lds1)));
     const int64_t cap = static_cast<int64_t>(device_cus()) * per_cu;
     int tr = 16;
