@@ -104,7 +104,8 @@ template <int DT, typename XT, typename OT, int NBW, int TR, int NWMAX, bool NWE
 // (the second bound is waves per SIMD: four for the expert-major runs and
 // for six to eight rows, whose registers would otherwise leave one
 // workgroup per CU)
-__global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8) ? 4 : 1) gemv_stream_kernel(SegTable t) {
+__global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8) ? 4 : 1)
+    gemv_stream_kernel(SegTable t) {
     // XR: activation rows (dense Q4_K launches of 2..4 rows): every row's
     // activations load before the weights, one digit table per row, each
     // weight group decoded once and multiplied against every row
@@ -900,12 +901,16 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
     int64_t rows = 0;
     for (int i = 0; i < t.n; i++) rows += t.seg[i].n_out;
     const int nw = (t.n_in / 256 + nbw - 1) / nbw;
-    // (several rows: their digit tables within the default 64 KB of LDS)
     // (several rows: their digit tables within the 160 KB of LDS; five and
     // more rows on two-block slices)
     if (t.rows > 1 && (stream_lds(nw, nbw, static_cast<int>(t.rows)) > kLdsMax || (t.rows > kStreamRowsWide && nbw != 2)))
         return false;
-    if (rows > 2 * 32 * static_cast<int64_t>(device_cus()) * (nw <= 8 ? 2 : 1)) return false;
+    // (one-row Q4_K launches of two-block slices stream any height: with
+    // load-transpose a 128256-row head took 57.8 us here against 66.6 us on
+    // the digit kernel; Q6_K's head stays there, 92 us against 95-110)
+    if (rows > 2 * 32 * static_cast<int64_t>(device_cus()) * (nw <= 8 ? 2 : 1) &&
+        !(dt == DT_Q4_K && nbw == 2 && t.rows == 1))
+        return false;
     for (int i = 0; i < t.n; i++) {
         const Seg &s = t.seg[i];
         // gate/up pairs take two row groups, which wider slices cannot afford

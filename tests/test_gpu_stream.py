@@ -115,3 +115,20 @@ def test_stream_rows(krk, torch_cuda, be32, be16, rows, n_out, n_in):
     ref16 = O.gemm(O.Q4_K, w, xh.astype(np.float32), n_out, nthreads=16)
     for r in range(rows):
         assert rel(host(out16)[r].astype(np.float32), ref16[r]) <= 2.0 ** -11 + GEMV_TOL, r
+
+
+def test_stream_q4_k_vocab_head(krk, torch_cuda, be32):
+    """A vocabulary-sized Q4_K matrix (128256 x 4096, one row) streams in many
+    rounds of load-transpose tiles: every row against the oracle at 1e-5."""
+    torch = torch_cuda
+    n_out, n_in, rep = 128256, 4096, 16
+    part = make_weights(krk, O.Q4_K, n_out // rep, n_in, seed=77)
+    w = np.tile(part, rep)
+    x = krk.synth_normal(n_in, seed=78)
+    say("stream q4_k head", n_out, n_in)
+    out = torch.full((1, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    be32.gemm(out, dev(torch, x), dev(torch, w), O.Q4_K, n_out, n_in, 1)
+    be32.sync()
+    ref = O.gemm(O.Q4_K, part, x, n_out // rep, nthreads=16)[0]
+    got = host(out)[0]
+    assert rel(got, np.tile(ref, rep)) <= GEMV_TOL
