@@ -484,14 +484,26 @@ def summarize_trace(path):
     headline's kernel (read back by the bench's roofline)."""
     import csv
     import statistics
-    rows = {}
+    rows, seq = {}, []
     for r in csv.DictReader(open(path)):
         key = (r["Kernel_Name"], r.get("Grid_Size", r.get("Grid_Size_X", "")),
                r.get("Workgroup_Size", r.get("Workgroup_Size_X", "")))
-        rows.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        rows.setdefault(key, []).append((t1 - t0) / 1e3)
+        seq.append((t1, key))
+    # end-to-end spacing: the interval between the ends of two consecutive
+    # dispatches of the same launch with nothing between them (back to back
+    # in a graph replay): the time per call the bench's marginal method
+    # measures.  A dispatch's own start stamp can precede the end of the one
+    # before it, so its duration overstates back-to-back launches.
+    seq.sort()
+    spacing = {}
+    for (ta, ka), (tb, kb) in zip(seq, seq[1:]):
+        if ka == kb:
+            spacing.setdefault(kb, []).append((tb - ta) / 1e3)
     peaks = {"f16": (2500.0, "TFLOP/s", "f16 peak"), "int8": (5000.0, "TOP/s", "int8 peak")}
-    print("| configuration | kernel | grid | block | calls | average (us) | median (us) | rate from the average |")
-    print("|---|---|---|---|---|---|---|---|")
+    print("| configuration | kernel | grid | block | calls | average (us) | median (us) | median spacing (us) | rate from the spacing |")
+    print("|---|---|---|---|---|---|---|---|---|")
     used, headline = set(), None
     order = [(lab, [k for k in rows if lab[0] in k[0] and k[1] == lab[1]]) for lab in TRACE_LABELS]
     for (sub, grid, label, work, unit), hits in order + [((None, None, "", None, None), [k for k in rows if "krk" in k[0]])]:
@@ -501,16 +513,19 @@ def summarize_trace(path):
             used.add(k)
             d = rows[k]
             avg, med = statistics.mean(d), statistics.median(d)
+            sp = statistics.median(spacing[k]) if len(spacing.get(k, [])) >= 3 else None
+            per = sp if sp is not None else avg
             rate = ""
             if unit == "B":
-                g = work / avg / 1e3
+                g = work / per / 1e3
                 rate = f"{g:.0f} GB/s ({100 * g / HBM_PEAK_GBS:.1f}% of HBM)"
             elif unit in peaks:
                 peak, u, what = peaks[unit]
-                t = work / avg / 1e6
+                t = work / per / 1e6
                 rate = f"{t:.0f} {u} ({100 * t / peak:.1f}% of {what})"
             name = k[0].replace("|", "\\|")
-            print(f"| {label} | `{name}` | {k[1]} | {k[2]} | {len(d)} | {avg:.2f} | {med:.2f} | {rate} |")
+            sps = f"{sp:.2f}" if sp is not None else "-"
+            print(f"| {label} | `{name}` | {k[1]} | {k[2]} | {len(d)} | {avg:.2f} | {med:.2f} | {sps} | {rate} |")
             if headline is None and sub is not None:
                 headline = k[0]
             if sub is not None:
