@@ -199,44 +199,30 @@ def bench_gemm(K, torch, be, timer, dt, M, n_out, n_in, seed, iters=20, warmup=3
             "M": M, "N": n_out, "K": n_in}
 
 
-def q4k_random_rows(torch, n_rows, n_in, gen):
-    """Q4_K rows of random codes and scales with fixed d = dmin = 2^-10 (f16
-    0x1400): valid blocks, made on the device (the MoE bank is 1.36 GB)."""
-    nb = n_in // 256
-    w = torch.randint(0, 256, (n_rows, nb, 144), dtype=torch.uint8, device="cuda", generator=gen)
-    w[:, :, 0] = 0x00
-    w[:, :, 1] = 0x14
-    w[:, :, 2] = 0x00
-    w[:, :, 3] = 0x14
-    return w.reshape(n_rows, nb * 144)
-
-
-def q6k_random_rows(torch, n_rows, n_in, gen):
-    """Q6_K rows of random codes and scales with d = 2^-10 (bytes 208..209)."""
-    nb = n_in // 256
-    w = torch.randint(0, 256, (n_rows, nb, 210), dtype=torch.uint8, device="cuda", generator=gen)
-    w[:, :, 208] = 0x00
-    w[:, :, 209] = 0x14
-    return w.reshape(n_rows, nb * 210)
-
-
-def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, k=8, calls=64, down=None):
-    """qwen3moe-shaped experts (Q4_K gate/up [1536, 4096],
-    down [4096, 1536]), router softmax -> top-8 -> normalize -> dispatch.
-    Each timed call routes a different seeded logits block, so the experts
-    read vary and the 1.36 GB bank streams from HBM.  down = K.Q6_K: the
-    Q4_K_M layout (Q6_K down banks)."""
-    down = K.Q4_K if down is None else down
+def moe_banks(K, torch, down, n_expert=128, n_embd=4096, n_ff=1536, distinct=8):
+    """BASELINE config 5's expert banks: Q4_K gate/up [1536, 4096] and down
+    [4096, 1536] (down = K.Q6_K: the Q4_K_M layout), quantized by the
+    library's quantizer from seeded N(0, 0.02) weights.  `distinct` experts
+    are generated (2.4 G values for all 128 would take the host ~40 s) and
+    the 128 banks are separate device copies of them: every bank is its own
+    memory, so the bytes a call streams are those of 128 distinct experts."""
     import numpy as np
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(5)
-    mats, entries = [], []
+    shapes = ((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff))
+    proto = []
+    for d in range(distinct):
+        mats = []
+        for m, (o, i) in enumerate(shapes):
+            dt = down if m == 2 else K.Q4_K
+            v = K.synth_normal(o * i, seed=500 + 3 * d + m, std=0.02, nthreads=16)
+            mats.append(K.quantize(dt, v, o, i, 16))
+        proto.append(mats)
+    keep, entries = [], []
     for e in range(n_expert):
         ent = K.MoeEntry()
-        for m, (o, i) in enumerate(((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff))):
+        for m, (o, i) in enumerate(shapes):
             dt = down if m == 2 else K.Q4_K
-            t = (q6k_random_rows if dt == K.Q6_K else q4k_random_rows)(torch, o, i, gen)
-            mats.append(t)
+            t = torch.from_numpy(proto[e % distinct][m]).cuda()
+            keep.append(t)
             ent.p[m] = t.data_ptr()
             ent.n_out[m], ent.n_in[m] = o, i
             ent.row_bytes[m] = K.row_bytes(dt, i)
@@ -244,6 +230,17 @@ def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, 
             ent.present[m] = 1
         entries.append(ent)
     table = torch.from_numpy(np.frombuffer(K.moe_table_bytes(entries), np.uint8).copy()).cuda()
+    return keep, table
+
+
+def bench_moe(K, torch, be, timer, n_tok, banks, n_expert=128, n_embd=4096, n_ff=1536, k=8, calls=64, down=None):
+    """qwen3moe-shaped experts (moe_banks), router softmax
+    -> top-8 -> normalize -> dispatch.  Each timed call routes a different
+    seeded logits block, so the experts read vary and the 1.36 GB of banks
+    stream from HBM."""
+    down = K.Q4_K if down is None else down
+    import numpy as np
+    _, table = banks
     logits = torch.from_numpy(K.synth_normal(calls * n_tok * n_expert, seed=31)).cuda()
     logits = logits.reshape(calls, n_tok, n_expert)
     x = torch.from_numpy(K.synth_normal(n_tok * n_embd, seed=32)).cuda().reshape(n_tok, n_embd)
@@ -258,9 +255,6 @@ def bench_moe(K, torch, be, timer, n_tok, n_expert=128, n_embd=4096, n_ff=1536, 
         be.moe_dispatch(table, 0, n_expert, ids, wts, x, out, n_tok, n_embd, n_ff, k)
 
     ms = timer.run(step, calls, 4, distinct=calls)
-    # the handle remembers a dispatched table by its address; the next call's
-    # table may be allocated at the same address
-    be.moe_table_forget(table)
     # distinct experts per call, from the same routing on the host
     import oracle as O
     distinct = []
@@ -282,12 +276,12 @@ def bench_layer_grouped(K, torch, be, timer, copies=None):
     as many as fill the rotation bytes)."""
     import numpy as np
     copies = copies or -(-ROTATE_BYTES // 113_836_032)
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(7)
     shapes = {"q": (4096, 4096), "k": (4096, 4096), "v": (4096, 4096), "o": (4096, 4096),
               "gate": (11008, 4096), "up": (11008, 4096), "down": (4096, 11008)}
-    layers = [{nm: q4k_random_rows(torch, o, i, gen) for nm, (o, i) in shapes.items()}
-              for _ in range(copies)]
+    # one layer quantized from seeded N(0, 0.02), `copies` device copies of it
+    host = {nm: K.quantize(K.Q4_K, K.synth_normal(o * i, seed=40 + j, std=0.02, nthreads=16), o, i, 16)
+            for j, (nm, (o, i)) in enumerate(shapes.items())}
+    layers = [{nm: torch.from_numpy(h).cuda() for nm, h in host.items()} for _ in range(copies)]
     x = torch.from_numpy(K.synth_normal(4096, seed=40)).cuda().reshape(1, 4096)
     q, kk, v, o = (torch.empty((1, 4096), device="cuda") for _ in range(4))
     ffn = torch.empty((1, 11008), device="cuda")
@@ -696,16 +690,20 @@ def main():
             log(f"  head {nm} {r['ms'] * 1e3:.1f} us {r['GBps']:.0f} GB/s")
 
     if want("moe"):
+        log("moe banks ...")
+        banks = moe_banks(K, torch, K.Q4_K)
         for T in (int(v) for v in args.moe_tokens.split(",") if v):
             log(f"moe C5 n_tok={T} ...")
-            r = bench_moe(K, torch, be32, timer, T)
+            r = bench_moe(K, torch, be32, timer, T, banks)
             r["frac_hbm"] = r["GBps"] / HBM_PEAK_GBS
             extras[f"moe_c5_t{T}"] = r
             log(f"  {r['us']:.1f} us  {r['GBps']:.0f} GB/s  {r['TFLOPs']:.1f} TFLOP/s  "
                 f"({r['distinct_experts']:.1f} experts)")
+        banks6 = None
         for T in (int(v) for v in args.moe_q4km_tokens.split(",") if v):
             log(f"moe C5 n_tok={T}, Q6_K down banks ...")
-            r = bench_moe(K, torch, be32, timer, T, down=K.Q6_K)
+            banks6 = banks6 or moe_banks(K, torch, K.Q6_K)
+            r = bench_moe(K, torch, be32, timer, T, banks6, down=K.Q6_K)
             r["frac_hbm"] = r["GBps"] / HBM_PEAK_GBS
             extras[f"moe_c5_q4km_t{T}"] = r
             log(f"  {r['us']:.1f} us  {r['GBps']:.0f} GB/s  {r['TFLOPs']:.1f} TFLOP/s")
@@ -713,12 +711,17 @@ def main():
             log(f"moe C5 n_tok={T}, KRK_PATH_EXACT ...")
             be32.set_gemm_path(K.PATH_EXACT)
             try:
-                r = bench_moe(K, torch, be32, timer, T)
+                r = bench_moe(K, torch, be32, timer, T, banks)
             finally:
                 be32.set_gemm_path(K.PATH_AUTO)
             r["frac_hbm"] = r["GBps"] / HBM_PEAK_GBS
             extras[f"moe_c5_t{T}_exact"] = r
             log(f"  {r['us']:.1f} us  {r['GBps']:.0f} GB/s  {r['TFLOPs']:.1f} TFLOP/s")
+        # the handle remembers a dispatched table by its address, which a
+        # later allocation may reuse
+        be32.moe_table_forget(banks[1])
+        if banks6 is not None:
+            be32.moe_table_forget(banks6[1])
 
     # ---- CPU baseline (rank 0, N = 1) ----------------------------------------
     cpu = None

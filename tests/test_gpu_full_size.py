@@ -166,27 +166,24 @@ def test_config4_q8_0_head(krk, torch_cuda, be32, be16):
 
 
 # ---------------------------------------------------------------- config 5 --
-def q4k_random_bank(rng, n_rows, n_in):
-    """Q4_K rows of random codes and scales with d = dmin = 2^-10: valid
-    blocks at the config's size without quantizing 1.36 GB on the host."""
-    nb = n_in // 256
-    w = rng.integers(0, 256, size=(n_rows, nb, 144), dtype=np.uint8)
-    w[:, :, 0:4] = [0x00, 0x14, 0x00, 0x14]
-    return w.reshape(-1)
-
-
 @pytest.fixture(scope="module")
 def c5_layer(krk, torch_cuda):
+    """The C5 banks as the config states them: Q4_K gate/up [1536, 4096] and
+    down [4096, 1536] quantized from seeded N(0, 0.02) weights.  Eight
+    distinct experts are generated (all 128 would take the host ~40 s) and
+    the 128 banks are separate device copies of them."""
     torch = torch_cuda
-    ne, n_embd, n_ff = 128, 4096, 1536
-    rng = np.random.default_rng(350)
+    ne, n_embd, n_ff, distinct = 128, 4096, 1536, 8
+    shapes = ((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff))
+    proto = [[krk.quantize(O.Q4_K, krk.synth_normal(o * i, seed=350 + 3 * d + m, std=0.02, nthreads=16), o, i, 16)
+              for m, (o, i) in enumerate(shapes)] for d in range(distinct)]
     banks = {}
     entries = []
     keep = []
     for e in range(ne):
         ent = krk.MoeEntry()
-        for m, (o, i) in enumerate(((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff))):
-            q = q4k_random_bank(rng, o, i)
+        for m, (o, i) in enumerate(shapes):
+            q = proto[e % distinct][m]
             banks[m, e] = q
             t = dev(torch, q)
             keep.append(t)
@@ -286,14 +283,6 @@ def test_config5_moe_prefill_batch(krk, torch_cuda, be32, c5_layer, path):
     assert e <= (GEMM_TOL if path == "mfma" else GEMV_TOL)
 
 
-def q6k_random_bank(rng, n_rows, n_in):
-    """Q6_K rows of random codes and scales with d = 2^-10."""
-    nb = n_in // 256
-    w = rng.integers(0, 256, size=(n_rows, nb, 210), dtype=np.uint8)
-    w[:, :, 208:210] = [0x00, 0x14]
-    return w.reshape(-1)
-
-
 @pytest.mark.parametrize("n_tok", [1, 16])
 def test_config5_q4_k_m_layer(krk, torch_cuda, be32, c5_layer, n_tok):
     """The C5 shape with Q6_K down banks (the Q4_K_M layout): gate/up on the
@@ -303,12 +292,14 @@ def test_config5_q4_k_m_layer(krk, torch_cuda, be32, c5_layer, n_tok):
     torch = torch_cuda
     banks, _, _ = c5_layer
     ne, n_embd, n_ff, k = 128, 4096, 1536, 8
-    rng = np.random.default_rng(380)
+    # Q6_K down banks quantized from N(0, 0.02): eight distinct, 128 copies
+    d6 = [krk.quantize(O.Q6_K, krk.synth_normal(n_embd * n_ff, seed=380 + d, std=0.02, nthreads=16), n_embd,
+                       n_ff, 16) for d in range(8)]
     down, entries, keep = {}, [], []
     for e in range(ne):
         ent = krk.MoeEntry()
         for m, (o, i) in enumerate(((n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff))):
-            q = banks[m, e] if m < 2 else q6k_random_bank(rng, o, i)
+            q = banks[m, e] if m < 2 else d6[e % 8]
             if m == 2:
                 down[e] = q
             t = dev(torch, q)
