@@ -155,7 +155,10 @@ int krk_gemm(krk_backend *b, void *out, const void *x, const void *w, int wt,
  * split-K partials and int8 activation codes that krk_gemm keeps in the
  * handle's growing workspace live in a fixed device array of
  * krk_gemm_noalloc_scratch_bytes() (64 MiB) instead: one per device, held
- * until the process ends, shared by every handle on that device.  A call
+ * until the process ends, shared by every handle on that device.  The array
+ * is part of the library's code object, so loading the library reserves
+ * those 64 MiB on every device it runs on, whether or not this entry point
+ * is ever called.  A call
  * whose scratch would exceed it returns KRK_ERR_NOMEM before any launch.
  * Calls that overlap on one device (several streams or threads) race on
  * that array; serialise them.  Nothing in the array needs to start at zero:

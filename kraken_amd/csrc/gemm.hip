@@ -692,14 +692,19 @@ __global__ void __launch_bounds__(G_THREADS, 1)
 
 // Fixed-order sum of the split-K partials: 8 consecutive outputs per thread
 // (two 16-byte loads per split, one 16- or 32-byte store), the tail of MN
-// not a multiple of 8 one by one.
+// not a multiple of 8 (and every output of a shape or output pointer the
+// 16-byte accesses do not fit) one by one.
 template <typename OT>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float *__restrict__ part,
                                                             OT *__restrict__ out, int64_t MN,
                                                             int splits) {
     const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
     if (i >= MN) return;
-    if (i + 8 <= MN) {
+    // 16-byte accesses need every slice (z MN floats into the 256-byte
+    // aligned workspace) and the output 16-byte aligned; other shapes and
+    // outputs are summed value by value
+    const bool vec = (MN & 3) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    if (vec && i + 8 <= MN) {
         floatx4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
         for (int z = 0; z < splits; z++) {
             const floatx4 u = *reinterpret_cast<const floatx4 *>(part + z * MN + i);
@@ -718,7 +723,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float *__restr
         }
         return;
     }
-    for (int64_t j = i; j < MN; j++) {
+    for (int64_t j = i; j < (i + 8 < MN ? i + 8 : MN); j++) {
         float s = 0.0f;
         for (int z = 0; z < splits; z++) s += part[z * MN + j];
         out[j] = static_cast<OT>(s);

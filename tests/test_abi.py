@@ -133,3 +133,17 @@ def test_bench_refuses_multi_gpu():
                        capture_output=True, text=True, timeout=300)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr)
+
+
+def test_dma_wait_check_catches_a_short_count():
+    """kraken_amd/build.py's check of the grouped expert GEMM's DMA publish
+    waits (run on every build): a vmcnt(N) before a barrier is accepted only
+    after at least N vector loads issued after the last DMA."""
+    from kraken_amd.build import check_dma_waits
+    ok = "\n".join(["_ZN3krk15moe_gemm_kernelX: ; @k", "\tglobal_load_lds_dwordx4 v[0:1], off",
+                    "\tglobal_load_dwordx4 v[2:5], v[6:7], off", "\tglobal_load_dwordx4 v[8:11], v[6:7], off",
+                    "\ts_waitcnt vmcnt(2)", "\ts_barrier", "\ts_endpgm"])
+    assert check_dma_waits(ok) == (1, [])
+    short = ok.replace("vmcnt(2)", "vmcnt(3)")
+    sites, bad = check_dma_waits(short)
+    assert sites == 1 and bad and bad[0][2:] == (2, 3)

@@ -93,3 +93,25 @@ def test_dense_streaming_gemm(krk, torch_cuda, be32, be16, rows, dt, n_in):
     be16.gemm(out16, dev(torch, x16), dev(torch, w), dt, n_out, n_in, rows)
     be16.sync()
     assert rel(host(out16).astype(np.float32), O.gemm(dt, w, x16.astype(np.float32), n_out)) <= GEMM_TOL
+
+
+@pytest.mark.parametrize("rows,n_out", [(9, 1001), (17, 1001), (33, 333)])
+def test_dense_streaming_gemm_odd_outputs(krk, torch_cuda, be32, be16, rows, n_out):
+    """Split-K partials of an M N that is not a multiple of four (every slice
+    after the first starts off 16-byte alignment), and an output that starts
+    2 bytes off alignment: the fixed-order reduce sums them value by value."""
+    torch = torch_cuda
+    n_in = 4096
+    w = make_weights(krk, O.Q4_K, n_out, n_in, seed=2700 + rows)
+    x = krk.synth_normal(rows * n_in, seed=2800 + rows).reshape(rows, n_in)
+    say("dense streaming gemm, odd outputs", rows, n_out)
+    out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
+    be32.gemm(out, dev(torch, x), dev(torch, w), O.Q4_K, n_out, n_in, rows)
+    be32.sync()
+    assert rel(host(out), O.gemm(O.Q4_K, w, x, n_out)) <= GEMM_TOL
+    x16 = x.astype(np.float16)
+    buf = torch.full((rows * n_out + 1,), float("nan"), dtype=torch.float16, device="cuda")
+    out16 = buf[1:].view(rows, n_out)   # 2 bytes past the allocation's alignment
+    be16.gemm(out16, dev(torch, x16), dev(torch, w), O.Q4_K, n_out, n_in, rows)
+    be16.sync()
+    assert rel(host(out16).astype(np.float32), O.gemm(O.Q4_K, w, x16.astype(np.float32), n_out)) <= GEMM_TOL
