@@ -112,7 +112,8 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
     static_assert(XR == 1 || (MOE == 0 && DT == DT_Q4_K), "several rows: dense Q4_K");
     // LT: the weights move as lane-contiguous 16-byte pieces (full cache
     // lines, nontemporal) and are transposed through the wave's LDS
-    static_assert(!LT || ((DT == DT_Q4_K || DT == DT_Q6_K) && MOE < 3), "load-transpose: Q4_K or Q6_K, dense or routed");
+    static_assert(!LT || ((DT == DT_Q4_K || DT == DT_Q6_K || DT == DT_Q4_0) && MOE < 3),
+                  "load-transpose: Q4_K, Q6_K or Q4_0, dense or routed");
     using LTG = LtGeom<NBW, TR, DT == DT_Q6_K ? 14 : 9>;
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr bool Q40 = DT == DT_Q4_0;
@@ -520,6 +521,21 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
                     sc[i] = u32x4{0u, 0u, 0u, 0u};
                     dd6[i] = 0u;
                 }
+            } else if constexpr (Q40) {
+                // lane group gq's blocks 2 gq, 2 gq + 1 at 36 gq of the
+                // 144-byte group (4-byte aligned reads)
+                u32x4 a, c;
+                __builtin_memcpy(&a, __builtin_assume_aligned(sb + 36 * gq, 4), 16);
+                __builtin_memcpy(&c, __builtin_assume_aligned(sb + 36 * gq + 16, 4), 16);
+                hd[i] = a;
+                qa[i] = c;
+                dd[i] = *reinterpret_cast<const uint32_t *>(sb + 36 * gq + 32);
+                // a ragged slice's missing block: d = 0 (and zero codes)
+                if (kb0 + b >= nb) {
+                    hd[i] = u32x4{0u, 0u, 0u, 0u};
+                    qa[i] = u32x4{0u, 0u, 0u, 0u};
+                    dd[i] = 0u;
+                }
             } else {
                 hd[i] = *reinterpret_cast<const u32x4 *>(sb);
                 qa[i] = *reinterpret_cast<const u32x4 *>(sb + 16 + 16 * gq);
@@ -797,8 +813,11 @@ hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
     // (expert-major runs keep their weights in registers across rows: the
     // gate/up pairs would spill beside the pieces in flight, and the down
     // projection measured 4% slower with it)
+    // (Q4_0: its 256-value groups are 144 bytes like Q4_K's blocks; Q8_0's
+    // 272-byte groups would need 85 KB a workgroup and halve the occupancy)
     constexpr bool LT = XR == 1 && MOE < 3 &&
-                        ((DT == DT_Q4_K && (NBW == 2 || (NBW == 3 && TR == 16))) || (DT == DT_Q6_K && NBW == 2));
+                        ((DT == DT_Q4_K && (NBW == 2 || (NBW == 3 && TR == 16))) ||
+                         ((DT == DT_Q6_K || DT == DT_Q4_0) && NBW == 2));
     const size_t l = stream_lds(nw, NBW, XR) + (LT ? stream_lt_lds(nw, NBW, TR, DT == DT_Q6_K ? 14 : 9) : 0);
     const dim3 grid(static_cast<unsigned>(tiles),
                     static_cast<unsigned>(MOE == 2 ? 1 : MOE >= 3 ? t.em_max_items : t.n));
@@ -908,11 +927,13 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
     // more rows on two-block slices)
     if (t.rows > 1 && (stream_lds(nw, nbw, static_cast<int>(t.rows)) > kLdsMax || (t.rows > kStreamRowsWide && nbw != 2)))
         return false;
-    // (one-row Q4_K launches of two-block slices stream any height: with
-    // load-transpose a 128256-row head took 57.8 us here against 66.6 us on
-    // the digit kernel; Q6_K's head stays there, 92 us against 95-110)
+    // (one-row Q4_K and Q4_0 launches of two-block slices stream any
+    // height: a 128256-row Q4_K head took 57.8 us here against 66.6 us on
+    // the digit kernel, Q4_0 70.3 us against 82.3 on the VALU kernel; the
+    // Q6_K head stays on the digit kernel (92 us against 95-110), Q8_0's on
+    // the VALU kernel (106 us against 113))
     if (rows > 2 * 32 * static_cast<int64_t>(device_cus()) * (nw <= 8 ? 2 : 1) &&
-        !(dt == DT_Q4_K && nbw == 2 && t.rows == 1))
+        !((dt == DT_Q4_K || dt == DT_Q4_0) && nbw == 2 && t.rows == 1))
         return false;
     for (int i = 0; i < t.n; i++) {
         const Seg &s = t.seg[i];
