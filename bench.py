@@ -448,6 +448,12 @@ TRACE_LABELS = [
     ("moe_gemm_kernel<14, false, 2>", "1572864", "C5 x512: grouped expert GEMM, down (Q6_K banks)",
      2 * 4096 * 1536 * 4096, "f16"),
     ("moe_gather_f16_kernel", "1048576", "C5 x512: activation rows gathered to f16 in plan order", None, None),
+    ("gemv_stream_kernelILi12EDF16_DF16_Li2ELi28ELi8ELb1ELi0ELi8ELi4ELb0E", "262144",
+     "rows 4: Q4_K 4096->14336, f16 activations, one pass (weights only in the rate)", 14336 * _Q4K_ROW, "B"),
+    ("gemv_stream_kernelILi12EDF16_DF16_Li2ELi28ELi8ELb1ELi0ELi8ELi5ELb0E", "262144",
+     "rows 5: the same, one pass", 14336 * _Q4K_ROW, "B"),
+    ("gemv_stream_kernelILi12EDF16_DF16_Li2ELi16ELi8ELb1ELi0ELi8ELi8ELb0E", "458752",
+     "rows 8: the same, one pass in two passes of four rows' tables", 14336 * _Q4K_ROW, "B"),
     ("moe_gemm_kernel<12, false, 1>", "114688", "rows 16 and 32: Q4_K 4096->14336, streaming dense mode (split-K 4)",
      None, None),
     ("moe_gemm_kernel<12, false, 2>", "114688", "rows 64 and 128: Q4_K 4096->14336, streaming dense mode", None, None),
@@ -456,13 +462,13 @@ TRACE_LABELS = [
     ("gemm_f16_kernelILi12EDF16", "229376", "C3 prefill up, M=2048 (448 tiles)", 2 * 2048 * 14336 * 4096, "f16"),
     ("gemm_f16_kernelILi12EDF16", "65536", "C3 prefill down, M=2048 (128 tiles x split 2)",
      2 * 2048 * 14336 * 4096, "f16"),
-    ("splitk_reduce_kernelIDF16", "8388608", "C3 prefill down, M=2048: split-K reduce", None, None),
+    ("splitk_reduce_kernelIDF16", "1048576", "C3 prefill down, M=2048: split-K reduce", None, None),
     ("gemm_f16_kernelILi12EDF16", "57344", "C3 prefill up, M=512 (112 tiles x split 2)",
      2 * 512 * 14336 * 4096, "f16"),
-    ("splitk_reduce_kernelIDF16", "7340032", "C3 prefill up, M=512: split-K reduce", None, None),
-    ("gemm_f16_kernelILi12EDF16", "16384", "C3 prefill down, M=512 (32 tiles x split 4)",
+    ("splitk_reduce_kernelIDF16", "917504", "C3 prefill up, M=512: split-K reduce", None, None),
+    ("gemm_f16_kernelILi12EDF16", "16384", "C3 prefill down, M=512 (32 tiles x split 8)",
      2 * 512 * 14336 * 4096, "f16"),
-    ("splitk_reduce_kernelIDF16", "2097152", "C3 prefill down, M=512: split-K reduce", None, None),
+    ("splitk_reduce_kernelIDF16", "262144", "C3 prefill down, M=512: split-K reduce", None, None),
     ("gemm_i8_kernelILi8EDF16", "458752", "int8 rung: Q8_0 4096->14336, M=2048", 2 * 2048 * 14336 * 4096, "int8"),
     ("quantize_q8_kernelIDF16", "262144", "int8 rung, M=2048: activation quantizer", None, None),
     ("gemm_i8_kernelILi8EDF16", "114688", "int8 rung: Q8_0 4096->14336, M=512", 2 * 512 * 14336 * 4096, "int8"),

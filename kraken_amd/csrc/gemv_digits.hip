@@ -70,8 +70,7 @@ template <> __device__ __forceinline__ void dma_lds<16>(const void *src, uint8_t
     __builtin_amdgcn_global_load_lds(src, (lds_void_t *)dst, 16, 0, 0);
 }
 
-template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT, bool RSPLIT,
-          bool EM>
+template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT, bool RSPLIT>
 __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t total, int nks, int nwc) {
     constexpr bool Q6 = DT == DT_Q6_K;
     // 32-value formats: 8 blocks per 256 values, each in an LDS slot of
@@ -97,20 +96,8 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     constexpr int CH = (U + CHB - 1) / CHB;
     constexpr int SLOT = ((U + 1023) / 1024) * 1024;
     static_assert(NSLOT * CH < 64, "vmcnt is 6 bits");
-    static_assert(!(Q6 || QS) || (!DOWN && !MT && !EM), "Q6_K, Q8_0, Q4_0: plain segments");
-    static_assert(!EM || (!DOWN && !MT && !RSPLIT), "expert items: one mode");
-    // expert-major item of this workgroup group; groups past the last item
-    // leave at once (before any barrier or LDS use)
-    int em_e = 0, em_rows = 0;
-    int64_t em_first = 0;
-    if constexpr (EM) {
-        const int item = static_cast<int>(blockIdx.x) / t.em_wpe;
-        if (item >= *t.em_n_items) return;
-        em_e = t.em_items[4 * item];
-        em_first = t.em_items[4 * item + 1];
-        em_rows = t.em_items[4 * item + 2];
-    }
-    const int64_t nrows = EM ? em_rows : t.rows;   // activation rows of this launch
+    static_assert(!(Q6 || QS) || (!DOWN && !MT), "Q6_K, Q8_0, Q4_0: plain segments");
+    const int64_t nrows = t.rows;   // activation rows of this launch
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ Seg segl[kMaxSegs];
     // down mode uses segl[0] only; the bank and the weight of each slot live
@@ -141,8 +128,8 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     // A workgroup owns tiles of ROWS rows (tiles lb, lb + nlb, ...); its
     // waves split K: wave wv takes the units ks = wv, wv + nwc, ...  With
     // several routed tokens, workgroup group tok serves token tok.
-    constexpr bool multi = MT || EM;   // several routed tokens / expert items
-    const int nlb = MT ? t.moe_wpt : EM ? t.em_wpe : static_cast<int>(gridDim.x);
+    constexpr bool multi = MT;   // several routed tokens
+    const int nlb = MT ? t.moe_wpt : static_cast<int>(gridDim.x);
     const int tok = multi ? static_cast<int>(blockIdx.x) / nlb : 0;
     const int lb = multi ? static_cast<int>(blockIdx.x) - tok * nlb : static_cast<int>(blockIdx.x);
     // Row split (chosen when there are many tiles): each wave owns whole
@@ -245,15 +232,8 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     // ---- x loads (four threads per 32-value sub-block, kXPasses passes over
     // the NX rows' sub-blocks; rows past nrows read as zero)
     const XT *x = static_cast<const XT *>(t.seg[0].x) + (MT ? tok * t.moe_xtok : 0);
-    // activation row r of this launch (expert items gather their rows)
-    auto xrow_off = [&](int r) -> int64_t {
-        if constexpr (EM) {
-            const int64_t p = em_first + r;
-            return (t.em_tok ? static_cast<int64_t>(t.em_tok[p]) : p) * t.em_xrow;
-        } else {
-            return static_cast<int64_t>(r) * t.x_stride;
-        }
-    };
+    // activation row r of this launch
+    auto xrow_off = [&](int r) -> int64_t { return static_cast<int64_t>(r) * t.x_stride; };
     const int q = threadIdx.x & 3;
     const int nsb = nb * 8;
     const int nxs = NX * nsb;
@@ -282,18 +262,7 @@ __global__ void __launch_bounds__(512) gemv_digits_kernel(SegTable t, int64_t to
     // ---- routed experts: resolve the segments on the device first (one
     // dependent read of the ids and the table entries per workgroup)
     const bool moe = t.moe_tab != nullptr;
-    if (EM) {
-        if (threadIdx.x == 0) {
-            const krk_moe_entry &en = static_cast<const krk_moe_entry *>(t.moe_tab)[em_e];
-            Seg sg = t.seg[0];
-            const bool pair = sg.kind == SEG_SILU;
-            sg.w = en.p[pair ? KRK_MOE_GATE : KRK_MOE_DOWN];
-            sg.w2 = pair ? en.p[KRK_MOE_UP] : nullptr;
-            sg.out = static_cast<float *>(sg.out) + em_first * t.em_orow;
-            segl[0] = sg;
-        }
-        __syncthreads();
-    } else if (DOWN) {
+    if (DOWN) {
         if (threadIdx.x < t.moe_k) {
             const krk_moe_entry *mt = static_cast<const krk_moe_entry *>(t.moe_tab);
             const int64_t pi = static_cast<int64_t>(tok) * t.moe_k + threadIdx.x;
@@ -756,7 +725,7 @@ constexpr size_t slot_bytes(int rows, int dt = DT_Q4_K) {
 }
 
 template <int DT, typename XT, typename OT, int ROWS, int KB, int NSLOT, bool DOWN, int NX, bool MT,
-          bool RSPLIT = false, bool EM = false>
+          bool RSPLIT = false>
 hipError_t launch(SegTable t, hipStream_t st) {
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr int RS = 16 * ((ROWS + 15) / 16);
@@ -786,7 +755,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
             if (l > kLdsBudget) break;
             int blocks = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                    &blocks, gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, RSPLIT, EM>, 64 * cand, l) !=
+                    &blocks, gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, RSPLIT>, 64 * cand, l) !=
                 hipSuccess)
                 blocks = 0;
             // waves doing useful work per CU: with K split over the waves a
@@ -808,19 +777,10 @@ hipError_t launch(SegTable t, hipStream_t st) {
     }
     int64_t grid = static_cast<int64_t>(cus) * per_cu;
     // row split when every wave of a full grid gets at least two tiles
-    if constexpr (!RSPLIT && NX == 1 && !DOWN && !MT && !EM) {
+    if constexpr (!RSPLIT && NX == 1 && !DOWN && !MT) {
         if (total >= 2 * grid * nw) return launch<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, true>(t, st);
     }
-    if (EM) {
-        // a group of workgroups per expert item; about three workgroups per
-        // CU over the items a call can have, so the groups of the items that
-        // exist fill the chip (the others leave at once)
-        int64_t wpe = (grid * 3 + t.em_max_items - 1) / t.em_max_items;
-        if (wpe > total) wpe = total;
-        if (wpe < 1) wpe = 1;
-        t.em_wpe = static_cast<int>(wpe);
-        grid = wpe * t.em_max_items;
-    } else if (MT) {
+    if (MT) {
         // a group of workgroups per token, the groups filling the chip together
         int64_t wpt = grid / t.moe_tokens;
         if (wpt > total) wpt = total;
@@ -830,7 +790,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
     } else if (grid > total) {
         grid = total;
     }
-    hipLaunchKernelGGL((gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, RSPLIT, EM>),
+    hipLaunchKernelGGL((gemv_digits_kernel<DT, XT, OT, ROWS, KB, NSLOT, DOWN, NX, MT, RSPLIT>),
                        dim3(static_cast<unsigned>(grid)), dim3(64 * nw), fixed + nw * per_wave, st, t, total,
                        nks, nw);
     return hipGetLastError();
@@ -930,16 +890,6 @@ hipError_t dispatch_nx(int dt, const SegTable &t, hipStream_t st) {
 // rows 2..8: passes of up to nx_cap activation rows, each reading W once
 template <typename XT, typename OT>
 hipError_t dispatch(int dt, const SegTable &t, hipStream_t st) {
-    if (t.em_items) {
-        // expert items of up to t.rows (2) activation rows: gate/up pairs or down
-        if constexpr (sizeof(XT) == 4) {
-            if (t.rows != 2) return hipErrorNotSupported;
-            return t.seg[0].kind == SEG_SILU ? launch<DT_Q4_K, XT, OT, 32, 2, 2, false, 2, false, false, true>(t, st)
-                                             : launch<DT_Q4_K, XT, OT, 16, 2, 2, false, 2, false, false, true>(t, st);
-        } else {
-            return hipErrorNotSupported;   // f32 activations
-        }
-    }
     if (t.rows == 1) return dispatch_nx<XT, OT, 1>(dt, t, st);
     const int cap = nx_cap(t.n_in, dt);
     for (int64_t r0 = 0; r0 < t.rows; r0 += cap) {
@@ -977,11 +927,7 @@ bool gemv_digits_ok(int dt, const SegTable &t) {
         return true;
     }
     if (dt != DT_Q4_K || t.n_in % 256 || t.row_bytes % 16) return false;
-    if (t.em_items) {
-        // expert items: one segment, f32 rows of up to 2, Q4_K banks
-        return t.n == 1 && t.rows == 2 && !t.moe_down && t.em_max_items > 0 && t.em_xrow % 4 == 0 &&
-               (t.seg[0].kind == SEG_PLAIN || (t.seg[0].kind == SEG_SILU && t.n_in <= 8192));
-    }
+    if (t.em_runs) return false;   // expert-major runs are the streaming kernel's
     if (t.moe_tab && t.rows != 1) return false;
     if (t.moe_tab && t.moe_down &&
         (t.n != 1 || t.moe_k < 1 || t.moe_k > kMaxDownSlots || t.moe_kslot % 512 ||

@@ -877,7 +877,7 @@ int device_cus() {
 }
 
 bool gemv_stream_ok(int dt, const SegTable &t) {
-    if ((dt != DT_Q4_K && dt != DT_Q6_K && dt != DT_Q4_0 && dt != DT_Q8_0) || t.rows < 1 || t.em_items)
+    if ((dt != DT_Q4_K && dt != DT_Q6_K && dt != DT_Q4_0 && dt != DT_Q8_0) || t.rows < 1)
         return false;
     // (the load-transpose tiles address 32 rows within 32-bit offsets)
     if (t.row_bytes >= (int64_t{1} << 26)) return false;

@@ -63,18 +63,11 @@ struct SegTable {
     int moe_tokens;
     int moe_wpt;
     int64_t moe_xtok, moe_otok;
-    // Expert-major items (em_items nullable; with moe_tab): workgroup group
-    // i (of em_wpe workgroups) serves item i = {expert, first, rows, -} while
-    // i < *em_n_items.  Its weights are moe_tab[expert]'s gate/up pair (seg
-    // kind SEG_SILU) or down bank (SEG_PLAIN); its activation rows are
-    // seg[0].x rows em_tok[p] (rows p when em_tok is null) and its outputs
-    // seg[0].out rows p, for p = first .. first + rows - 1; row lengths
-    // em_xrow / em_orow elements.
-    const int32_t *em_items;
-    const int32_t *em_n_items;
+    // Expert-major rows (with em_runs below): activation rows seg[0].x row
+    // em_tok[p] (row p when em_tok is null) of em_xrow elements, outputs
+    // seg[0].out row p of em_orow elements; em_max_items bounds the runs.
     const int32_t *em_tok;
-    int em_wpe;          // set by the launcher
-    int em_max_items;    // upper bound on *em_n_items (sizes the grid)
+    int em_max_items;
     int64_t em_xrow, em_orow;
     // Expert-major runs (em_runs nullable; the register-streaming kernel,
     // with moe_tab and one segment): grid row a serves run em_runs[a] while

@@ -103,7 +103,7 @@ size_t moe_workspace(int64_t n_tok, int k, int n_expert, int64_t n_embd, int64_t
 // takes a per-expert atomic cursor.  The expert offsets and the active list
 // come from a block-wide exclusive scan (4 experts per thread).
 constexpr int kPlanLds = 4096;  // (token, slot) pairs whose ids the plan keeps in LDS
-constexpr int kItemRows = 2;    // activation rows of an expert item (the digit kernel's NX)
+constexpr int kItemRows = 2;    // plan item rows of the VALU expert kernels
 __global__ void __launch_bounds__(256) moe_plan_kernel(const int32_t *__restrict__ ids, int64_t P,
                                                         int k, int ne, MoeWs w,
                                                         const krk_moe_entry *__restrict__ tab,
@@ -606,8 +606,10 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
     // about twice as fast as the digit kernel's items from 65 tokens up).
     // Where the streaming kernel cannot take the shapes, token groups of the
     // digit kernel serve up to kMoeTokenGroups tokens (each token reads its
-    // experts for itself), expert-major items of kItemRows tokens larger
-    // batches, and the plan path whatever the digit kernel cannot take.
+    // experts for itself), and the plan path whatever the digit kernel
+    // cannot take.  (The digit kernel's expert-major items, once the path
+    // above 64 tokens, took exactly the shapes the streaming kernel takes
+    // and were removed.)
     // Q4_K gate/up; the streaming kernel also takes a Q6_K down bank (Q4_K_M
     // layers), the digit kernel only Q4_K
     const bool q4k_gu = !a.act_f16 && a.wt == DT_Q4_K && a.aligned16 && a.rb_gate == a.rb_up &&
@@ -696,50 +698,6 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
                            kItemRows);
             hipError_t e = gemv_stream(DT_Q4_K, false, eg, st);
             if (e == hipSuccess) e = gemv_stream(a.wt_down, false, ed, st);
-            if (e != hipSuccess) return e;
-            const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));
-            hipLaunchKernelGGL((moe_reduce_kernel<float>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
-                               a.n_embd, w, static_cast<float *>(a.out));
-            return hipGetLastError();
-        }
-    }
-    if (on_digits && a.n_tok > kMoeTokenGroups) {
-        // expert-major items, each expert's weights read once per run of up
-        // to kItemRows of its tokens; then the ordered per-token reduce
-        SegTable eg{};
-        eg.n = 1;
-        eg.n_in = static_cast<int>(a.n_embd);
-        eg.row_bytes = a.rb_gate;
-        eg.rows = kItemRows;
-        eg.out_stride = a.n_ff;
-        eg.seg[0].x = a.xn;
-        eg.seg[0].out = w.mid;
-        eg.seg[0].n_out = a.n_ff;
-        eg.seg[0].kind = SEG_SILU;
-        eg.moe_tab = tab;
-        eg.moe_ne = a.n_expert;
-        eg.em_items = w.items;
-        eg.em_n_items = w.n_items;
-        eg.em_tok = w.plan_tok;
-        eg.em_max_items = static_cast<int>(P);
-        eg.em_xrow = a.n_embd;
-        eg.em_orow = a.n_ff;
-        SegTable ed = eg;
-        ed.n_in = static_cast<int>(a.n_ff);
-        ed.row_bytes = a.rb_down;
-        ed.out_stride = a.n_embd;
-        ed.seg[0].x = w.mid;
-        ed.seg[0].out = w.part;
-        ed.seg[0].n_out = a.n_embd;
-        ed.seg[0].kind = SEG_PLAIN;
-        ed.em_tok = nullptr;
-        ed.em_xrow = a.n_ff;
-        ed.em_orow = a.n_embd;
-        if (P <= (1 << 20) && gemv_digits_ok(DT_Q4_K, eg) && gemv_digits_ok(DT_Q4_K, ed)) {
-            hipLaunchKernelGGL(moe_plan_kernel, dim3(1), dim3(256), 0, st, a.ids, P, a.k, a.n_expert, w, tab,
-                           kItemRows);
-            hipError_t e = gemv_digits(DT_Q4_K, false, eg, st);
-            if (e == hipSuccess) e = gemv_digits(DT_Q4_K, false, ed, st);
             if (e != hipSuccess) return e;
             const dim3 rgrid(static_cast<unsigned>((a.n_embd + 255) / 256), static_cast<unsigned>(a.n_tok));
             hipLaunchKernelGGL((moe_reduce_kernel<float>), rgrid, dim3(256), 0, st, a.ids, a.wts, a.k,
