@@ -112,9 +112,9 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
     static_assert(XR == 1 || (MOE == 0 && DT == DT_Q4_K), "several rows: dense Q4_K");
     // LT: the weights move as lane-contiguous 16-byte pieces (full cache
     // lines, nontemporal) and are transposed through the wave's LDS
-    static_assert(!LT || ((DT == DT_Q4_K || DT == DT_Q6_K || DT == DT_Q4_0) && MOE < 3),
-                  "load-transpose: Q4_K, Q6_K or Q4_0, dense or routed");
-    using LTG = LtGeom<NBW, TR, DT == DT_Q6_K ? 14 : 9>;
+    static_assert(!LT || ((DT == DT_Q4_K || DT == DT_Q6_K || DT == DT_Q4_0 || DT == DT_Q8_0) && MOE < 3),
+                  "load-transpose: Q4_K, Q6_K, Q4_0 or Q8_0, dense or routed");
+    using LTG = LtGeom<NBW, TR, DT == DT_Q6_K ? 14 : DT == DT_Q8_0 ? 17 : 9>;
     constexpr bool Q6 = DT == DT_Q6_K;
     constexpr bool Q40 = DT == DT_Q4_0;
     constexpr bool Q80 = DT == DT_Q8_0;
@@ -291,7 +291,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
         const int64_t left = n_out - nbase;
         const int rlim = pair ? 16 : TR;
         const int rmax = static_cast<int>(left < rlim ? left : rlim) - 1;
-        const int omax = ((nb - kb0 < NBW ? nb - kb0 : NBW) * 144) - 16;
+        const int omax = ((nb - kb0 < NBW ? nb - kb0 : NBW) * BB) - 16;
         const int bmax = (nb - kb0 < NBW ? nb - kb0 : NBW) - 1;   // the slice's last block
         const uint32_t rb32 = static_cast<uint32_t>(rb);
 #pragma unroll
@@ -520,6 +520,26 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
                 if (kb0 + b >= nb) {
                     sc[i] = u32x4{0u, 0u, 0u, 0u};
                     dd6[i] = 0u;
+                }
+            } else if constexpr (Q80) {
+                // lane group gq's blocks 2 gq, 2 gq + 1 at 68 gq of the
+                // 272-byte group (4-byte aligned reads)
+                u32x4 v0, v1, v2, v3;
+                __builtin_memcpy(&v0, __builtin_assume_aligned(sb + 68 * gq, 4), 16);
+                __builtin_memcpy(&v1, __builtin_assume_aligned(sb + 68 * gq + 16, 4), 16);
+                __builtin_memcpy(&v2, __builtin_assume_aligned(sb + 68 * gq + 32, 4), 16);
+                __builtin_memcpy(&v3, __builtin_assume_aligned(sb + 68 * gq + 48, 4), 16);
+                hd[i] = v0;
+                qa[i] = v1;
+                qb[i] = v2;
+                qc[i] = v3;
+                dd[i] = *reinterpret_cast<const uint32_t *>(sb + 68 * gq + 64);
+                if (kb0 + b >= nb) {
+                    hd[i] = u32x4{0u, 0u, 0u, 0u};
+                    qa[i] = hd[i];
+                    qb[i] = hd[i];
+                    qc[i] = hd[i];
+                    dd[i] = 0u;
                 }
             } else if constexpr (Q40) {
                 // lane group gq's blocks 2 gq, 2 gq + 1 at 36 gq of the
@@ -814,11 +834,14 @@ hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
     // gate/up pairs would spill beside the pieces in flight, and the down
     // projection measured 4% slower with it)
     // (Q4_0: its 256-value groups are 144 bytes like Q4_K's blocks; Q8_0's
-    // 272-byte groups would need 85 KB a workgroup and halve the occupancy)
+    // 272-byte groups fit the LDS up to eight waves (K <= 4096), and sixteen
+    // waves keep register loads)
     constexpr bool LT = XR == 1 && MOE < 3 &&
                         ((DT == DT_Q4_K && (NBW == 2 || (NBW == 3 && TR == 16))) ||
-                         ((DT == DT_Q6_K || DT == DT_Q4_0) && NBW == 2));
-    const size_t l = stream_lds(nw, NBW, XR) + (LT ? stream_lt_lds(nw, NBW, TR, DT == DT_Q6_K ? 14 : 9) : 0);
+                         ((DT == DT_Q6_K || DT == DT_Q4_0 || DT == DT_Q8_0) && NBW == 2));
+    constexpr bool LTW = LT && DT != DT_Q8_0;   // (over eight waves)
+    const size_t l = stream_lds(nw, NBW, XR) +
+                     ((nw <= 8 ? LT : LTW) ? stream_lt_lds(nw, NBW, TR, DT == DT_Q6_K ? 14 : DT == DT_Q8_0 ? 17 : 9) : 0);
     const dim3 grid(static_cast<unsigned>(tiles),
                     static_cast<unsigned>(MOE == 2 ? 1 : MOE >= 3 ? t.em_max_items : t.n));
     if (nw == 8)
@@ -828,10 +851,10 @@ hipError_t launch(const SegTable &t, int64_t tiles, int nw, hipStream_t st) {
         hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, 8, false, MOE, 8, XR, LT>), grid, dim3(64 * nw), l, st,
                            t);
     else if (nw == kMaxWaves)
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, true, MOE, 8, XR, LT>), grid, dim3(64 * nw),
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, true, MOE, 8, XR, LTW>), grid, dim3(64 * nw),
                            l, st, t);
     else
-        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, false, MOE, 8, XR, LT>), grid,
+        hipLaunchKernelGGL((gemv_stream_kernel<DT, XT, OT, NBW, TR, kMaxWaves, false, MOE, 8, XR, LTW>), grid,
                            dim3(64 * nw), l, st, t);
     return hipGetLastError();
 }
@@ -1020,8 +1043,11 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
     // (two per CU at up to eight waves) in the fewest rounds x rows
     // (workgroups per CU: two at up to eight waves, fewer when several rows'
     // tables fill the LDS)
+    // (load-transpose buffers: one-row launches of two-block slices, and
+    // Q4_K's three-block slices, whose tiles are 16 rows)
+    const bool lt = t.rows == 1 && ((nbw == 2 && (dt != DT_Q8_0 || nw <= 8)) || (dt == DT_Q4_K && nbw == 3));
     const size_t lds1 = stream_lds(nw, nbw, static_cast<int>(t.rows)) +
-                        (t.rows == 1 ? stream_lt_lds(nw, nbw, 32, dt == DT_Q6_K ? 14 : 9) : 0);
+                        (lt ? stream_lt_lds(nw, nbw, 32, dt == DT_Q6_K ? 14 : dt == DT_Q8_0 ? 17 : 9) : 0);
     const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(nw <= 8 ? 2 : 1, static_cast<int64_t>(kLdsMax / lds1)));
     const int64_t cap = static_cast<int64_t>(device_cus()) * per_cu;
     int tr = 16;
