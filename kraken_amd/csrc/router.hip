@@ -7,6 +7,8 @@
 #include "krk_dev.hpp"
 #include "krk_kernels.hpp"
 
+#include <type_traits>
+
 // wave-wide reductions of the device library (DPP/permlane based)
 extern "C" __device__ __attribute__((const)) float __ockl_wfred_max_f32(float);
 extern "C" __device__ __attribute__((const)) int __ockl_wfred_min_i32(int);
@@ -15,11 +17,23 @@ namespace krk {
 
 constexpr int kMaxExpertsPerLane = 16;   // n_expert <= 1024 over 64 lanes
 
+// f(std::integral_constant<int, EPL>) with the fewest experts per lane, of
+// 1, 2, 4, 8 and 16, that covers n_expert
+template <typename F> void with_epl(int ne, F &&f) {
+    if (ne <= 64) f(std::integral_constant<int, 1>{});
+    else if (ne <= 128) f(std::integral_constant<int, 2>{});
+    else if (ne <= 256) f(std::integral_constant<int, 4>{});
+    else if (ne <= 512) f(std::integral_constant<int, 8>{});
+    else f(std::integral_constant<int, kMaxExpertsPerLane>{});
+}
+
 // One wave per token row.  The exponentials are computed in parallel (the
 // same expf per element as a serial loop); the sum runs serially in
 // ascending expert id in lane 0, as the host does, so only expf itself can
 // differ from the host.
-template <typename T>
+// EPL: experts per lane (64 EPL >= ne), so a 128-expert router unrolls two
+// slots instead of walking the sixteen a 1024-expert one needs
+template <typename T, int EPL>
 __global__ void __launch_bounds__(64) router_softmax_kernel(const T *__restrict__ logits,
                                                            float *__restrict__ probs,
                                                            int64_t n_rows, int ne) {
@@ -29,12 +43,10 @@ __global__ void __launch_bounds__(64) router_softmax_kernel(const T *__restrict_
     const int lane = threadIdx.x;
     const T *l = logits + r * ne;
     float *p = probs + r * ne;
-    float v[kMaxExpertsPerLane];
+    float v[EPL];
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; i++) {
-        v[i] = -INFINITY;
-        if (64 * i >= ne) break;   // uniform
+    for (int i = 0; i < EPL; i++) {
         const int e = lane + 64 * i;
         v[i] = e < ne ? static_cast<float>(l[e]) : -INFINITY;
         mx = fmaxf(mx, v[i]);
@@ -43,8 +55,7 @@ __global__ void __launch_bounds__(64) router_softmax_kernel(const T *__restrict_
     // NaN, which fmax (and the wave reduction) skip as the host's > does
     mx = __ockl_wfred_max_f32(mx);
 #pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; i++) {
-        if (64 * i >= ne) break;
+    for (int i = 0; i < EPL; i++) {
         const int e = lane + 64 * i;
         if (e < ne) ex[e] = expf(v[i] - mx);
     }
@@ -78,12 +89,16 @@ hipError_t router_softmax(const void *logits, bool act_f16, float *probs, int64_
                           int n_expert, hipStream_t st) {
     if (n_expert > 64 * kMaxExpertsPerLane) return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>(n_rows));
-    if (act_f16)
-        hipLaunchKernelGGL((router_softmax_kernel<_Float16>), grid, dim3(64), 0, st,
-                           static_cast<const _Float16 *>(logits), probs, n_rows, n_expert);
-    else
-        hipLaunchKernelGGL((router_softmax_kernel<float>), grid, dim3(64), 0, st,
-                           static_cast<const float *>(logits), probs, n_rows, n_expert);
+    auto go = [&](auto epl) {
+        constexpr int E = decltype(epl)::value;
+        if (act_f16)
+            hipLaunchKernelGGL((router_softmax_kernel<_Float16, E>), grid, dim3(64), 0, st,
+                               static_cast<const _Float16 *>(logits), probs, n_rows, n_expert);
+        else
+            hipLaunchKernelGGL((router_softmax_kernel<float, E>), grid, dim3(64), 0, st,
+                               static_cast<const float *>(logits), probs, n_rows, n_expert);
+    };
+    with_epl(n_expert, go);
     return hipGetLastError();
 }
 
@@ -91,6 +106,7 @@ hipError_t router_softmax(const void *logits, bool act_f16, float *probs, int64_
 // taken.  The winner of a round is the largest probability and, among equal
 // ones, the lowest id -- what the host's ascending strict-> scan picks.  The
 // normalisation sum runs serially over the k picks in pick order.
+template <int EPL>
 __global__ void __launch_bounds__(64) router_topk_kernel(const float *__restrict__ probs,
                                                         int64_t n_rows, int ne, int k,
                                                         int32_t *__restrict__ ids,
@@ -101,11 +117,9 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float *__restrict
     const int64_t r = blockIdx.x;
     const int lane = threadIdx.x;
     const float *p = probs + r * ne;
-    float v[kMaxExpertsPerLane];
+    float v[EPL];
 #pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; i++) {
-        v[i] = -INFINITY;
-        if (64 * i >= ne) break;   // uniform
+    for (int i = 0; i < EPL; i++) {
         const int e = lane + 64 * i;
         v[i] = e < ne ? p[e] : -INFINITY;
     }
@@ -115,8 +129,7 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float *__restrict
         float bp = -1.0f;
         int be = -1;
 #pragma unroll
-        for (int i = 0; i < kMaxExpertsPerLane; i++) {
-            if (64 * i >= ne) break;
+        for (int i = 0; i < EPL; i++) {
             const int e = lane + 64 * i;
             if (e < ne && !(taken & (1u << i)) && v[i] > bp) { bp = v[i]; be = e; }
         }
@@ -125,11 +138,13 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float *__restrict
         const float gp = __ockl_wfred_max_f32(bp);
         be = __ockl_wfred_min_i32(be >= 0 && bp == gp ? be : 0x7fffffff);
         if (be == 0x7fffffff) be = -1;
-        bp = gp;
+        // the weight is p[be] from its own lane (the wave maximum may carry
+        // the other zero's sign when +0 and -0 tie)
+        const float pw = __shfl(bp, be & 63);
         if (be >= 0 && (be & 63) == lane) taken |= 1u << (be >> 6);
         if (lane == 0) {
             isel[s] = be;
-            wsel[s] = be >= 0 ? bp : 0.0f;   // bp is p[be] itself
+            wsel[s] = be >= 0 ? pw : 0.0f;
         }
     }
     __syncthreads();
@@ -149,12 +164,81 @@ __global__ void __launch_bounds__(64) router_topk_kernel(const float *__restrict
     }
 }
 
+// Up to 256 experts: one thread per expert, each computing its own rank in
+// one pass instead of k dependent rounds of wave reductions.  Expert e's key
+// is (the order-preserving bits of p[e], ~e) as one 64-bit integer -- larger
+// p first, and among equal p (-0 taken as +0, as == does) the lower id -- and
+// its rank is the number of larger keys.  Candidates are what the rounds
+// above can pick: p > -1 and not NaN; the others hold key 0 and count for
+// nothing.  A candidate of rank < k writes itself to pick slot rank; slots
+// no candidate fills stay id -1, weight 0, as above.
+template <int NW>
+__global__ void __launch_bounds__(64 * NW) router_topk_rank_kernel(const float *__restrict__ probs,
+                                                                  int64_t n_rows, int ne, int k,
+                                                                  int32_t *__restrict__ ids,
+                                                                  float *__restrict__ wts, int normalize,
+                                                                  float scale) {
+    __shared__ __align__(16) uint64_t key[64 * NW];
+    __shared__ float wsel[64];
+    __shared__ int32_t isel[64];
+    const int64_t r = blockIdx.x;
+    const int t = threadIdx.x;
+    const float v = t < ne ? probs[r * ne + t] : -INFINITY;
+    const bool cand = v > -1.0f;
+    const uint32_t b = __float_as_uint(v + 0.0f);
+    const uint32_t ob = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    const uint64_t my = cand ? (static_cast<uint64_t>(ob) << 32) | static_cast<uint32_t>(~t) : 0;
+    key[t] = my;
+    if (t < k) {
+        isel[t] = -1;
+        wsel[t] = 0.0f;
+    }
+    __syncthreads();
+    if (cand) {
+        int rank = 0;
+#pragma unroll 16
+        for (int j = 0; j < 64 * NW; j++) rank += key[j] > my;
+        if (rank < k) {
+            isel[rank] = t;
+            wsel[rank] = v;
+        }
+    }
+    __syncthreads();
+    if (t == 0 && normalize) {
+        float ksum = 0.0f;
+        for (int s = 0; s < k; s++) ksum += wsel[s];
+        const float kinv = ksum > 0.0f ? 1.0f / ksum : 0.0f;
+        for (int s = 0; s < k; s++) wsel[s] *= kinv;
+    }
+    __syncthreads();
+    const bool sc = scale != 0.0f && scale != 1.0f;
+    if (t < k) {
+        ids[r * k + t] = isel[t];
+        wts[r * k + t] = sc ? wsel[t] * scale : wsel[t];
+    }
+}
+
 hipError_t router_topk(const float *probs, int64_t n_rows, int n_expert, int k, int32_t *ids,
                        float *wts, int normalize, float scale, hipStream_t st) {
     if (n_expert > 64 * kMaxExpertsPerLane || k > 64) return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>(n_rows));
-    hipLaunchKernelGGL(router_topk_kernel, grid, dim3(64), 0, st, probs, n_rows, n_expert, k, ids,
-                       wts, normalize, scale);
+    if (n_expert <= 256) {
+        const int nw = (n_expert + 63) / 64;
+        if (nw <= 1)
+            hipLaunchKernelGGL(router_topk_rank_kernel<1>, grid, dim3(64), 0, st, probs, n_rows, n_expert, k, ids,
+                               wts, normalize, scale);
+        else if (nw == 2)
+            hipLaunchKernelGGL(router_topk_rank_kernel<2>, grid, dim3(128), 0, st, probs, n_rows, n_expert, k, ids,
+                               wts, normalize, scale);
+        else
+            hipLaunchKernelGGL(router_topk_rank_kernel<4>, grid, dim3(256), 0, st, probs, n_rows, n_expert, k, ids,
+                               wts, normalize, scale);
+        return hipGetLastError();
+    }
+    with_epl(n_expert, [&](auto epl) {
+        hipLaunchKernelGGL((router_topk_kernel<decltype(epl)::value>), grid, dim3(64), 0, st, probs, n_rows,
+                           n_expert, k, ids, wts, normalize, scale);
+    });
     return hipGetLastError();
 }
 

@@ -271,25 +271,59 @@ def test_gemm_splits_repeat(krk, torch_cuda, be16, be32, dt, shape):
 
 
 # ------------------------------------------------------------------ router --
-def test_router_softmax_topk(krk, torch_cuda, be32, rng):
+# expert counts: each experts-per-lane instantiation (1, 2, 4, 8, 16 of the
+# 64 lanes) at and past its boundary
+@pytest.mark.parametrize("ne,k", [(8, 2), (64, 8), (65, 8), (128, 8), (129, 6), (256, 8), (300, 8),
+                                  (512, 16), (1000, 8), (1024, 64)])
+def test_router_softmax_topk(krk, torch_cuda, be32, ne, k):
     torch = torch_cuda
-    logits = rng.standard_normal((16, 128)).astype(np.float32)
-    logits[3, 7] = logits[3, 100] = 6.0
-    probs = torch.empty((16, 128), dtype=torch.float32, device="cuda")
-    be32.router_softmax(probs, dev(torch, logits), 16, 128)
+    rng = np.random.default_rng(ne)
+    logits = rng.standard_normal((16, ne)).astype(np.float32)
+    logits[3, 1] = logits[3, ne - 1] = 6.0
+    probs = torch.empty((16, ne), dtype=torch.float32, device="cuda")
+    be32.router_softmax(probs, dev(torch, logits), 16, ne)
     be32.sync()
     ref = O.router_softmax(logits)
     assert np.allclose(host(probs), ref, rtol=2e-6, atol=1e-12)
     # selection on identical probabilities is exact, ties to the lower id
     p = dev(torch, ref)
-    ids = torch.empty((16, 8), dtype=torch.int32, device="cuda")
-    wts = torch.empty((16, 8), dtype=torch.float32, device="cuda")
-    be32.router_topk(p, 16, 128, 8, ids, wts, True, 1.0)
+    ids = torch.empty((16, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((16, k), dtype=torch.float32, device="cuda")
+    be32.router_topk(p, 16, ne, k, ids, wts, True, 1.0)
     be32.sync()
-    rid, rwt = O.router_topk(ref, 8)
+    rid, rwt = O.router_topk(ref, k)
     assert np.array_equal(host(ids), rid)
     assert np.array_equal(host(wts).view(np.uint32), rwt.view(np.uint32))
-    assert host(ids)[3, 0] == 7 and host(ids)[3, 1] == 100
+    assert host(ids)[3, 0] == 1 and host(ids)[3, 1] == ne - 1
+
+
+@pytest.mark.parametrize("ne", [40, 128, 200, 300])
+def test_router_topk_edge_rows(krk, torch_cuda, be32, ne):
+    """top-k on arbitrary inputs: values at or below -1 and NaN are never
+    picked, equal values (-0 and +0 among them) go to the lower id, rows with
+    fewer candidates than k fill the rest with id -1 and weight 0."""
+    torch = torch_cuda
+    k = 8
+    rng = np.random.default_rng(7 + ne)
+    p = rng.random((6, ne)).astype(np.float32)
+    p[0, :] = 0.25                                  # all equal
+    p[1, :] = -1.0                                  # no candidate
+    p[1, [5, ne - 3]] = [0.5, -0.999]               # two candidates
+    p[2, ::3] = np.nan
+    p[2, 1::3] = -2.0
+    p[3, :] = 0.0
+    p[3, 1::2] = -0.0                               # +0 / -0 ties
+    p[4, :] = rng.integers(0, 3, ne) * 0.125        # many ties
+    p[5, :] = -rng.random(ne).astype(np.float32)    # all in (-1, 0]
+    ids = torch.empty((6, k), dtype=torch.int32, device="cuda")
+    wts = torch.empty((6, k), dtype=torch.float32, device="cuda")
+    for norm, scale in ((True, 1.0), (False, 2.5)):
+        be32.router_topk(dev(torch, p), 6, ne, k, ids, wts, norm, scale)
+        be32.sync()
+        rid, rwt = O.router_topk(p, k, norm, scale)
+        assert np.array_equal(host(ids), rid)
+        assert np.array_equal(host(wts).view(np.uint32), rwt.view(np.uint32))
+    assert list(host(ids)[1, 2:]) == [-1] * (k - 2)
 
 
 # --------------------------------------------------------------------- MoE --
