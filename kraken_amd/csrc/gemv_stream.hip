@@ -954,7 +954,8 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
     // height: a 128256-row Q4_K head took 57.8 us here against 66.6 us on
     // the digit kernel, Q4_0 70.3 us against 82.3 on the VALU kernel; the
     // Q6_K head stays on the digit kernel (92 us against 95-110), Q8_0's on
-    // the VALU kernel (106 us against 113))
+    // the VALU kernel (106 us against 113; with load-transpose 101.2 against
+    // 103.7 on one box))
     if (rows > 2 * 32 * static_cast<int64_t>(device_cus()) * (nw <= 8 ? 2 : 1) &&
         !((dt == DT_Q4_K || dt == DT_Q4_0) && nbw == 2 && t.rows == 1))
         return false;
