@@ -76,11 +76,10 @@ enum krk_dtype {
  * reference GPU backend, F32 on its CPU oracle, backend_cpu.cpp:584). */
 enum krk_act { KRK_ACT_F32 = 0, KRK_ACT_F16 = 1 };
 
-/* Kernel family for rows > 8, and for 6..8 under AUTO (krk_gemm)
- * (backend_hip.hip:2712-2893 `gemm_rung` and the KRK_GEMM_EXACT /
- * KRK_GEMM_PATH / KRK_GEMM_INT8 switches). */
+/* Kernel family for rows > 8 (backend_hip.hip:2712-2893 `gemm_rung` and the
+ * KRK_GEMM_EXACT / KRK_GEMM_PATH / KRK_GEMM_INT8 switches). */
 enum krk_gemm_path {
-    KRK_PATH_AUTO = 0,  /* MFMA f16 GEMM for rows > 8 (and 6..8, krk_gemm)  */
+    KRK_PATH_AUTO = 0,  /* MFMA f16 GEMM for rows > 8                       */
     KRK_PATH_EXACT = 1, /* multi-row GEMV, f32 products (gemv_grid analogue) */
     KRK_PATH_MFMA = 2,  /* W dequantized to f16 LDS tiles, f16 MFMA, f32 acc */
     KRK_PATH_INT8 = 3   /* Q8_0/Q4_K/Q5_K/Q6_K x Q8 activations (lossy rung) */
@@ -144,12 +143,7 @@ int krk_dtype_row_aligned(int wt, int64_t n);
  * rows == 1..8: fused dequant+dot GEMV with exact products and f32
  *               accumulation; Q4_K at rows == 1 forms the products on the
  *               int8 matrix cores from exact digit planes of x (rounded at
- *               2^-23 of each 32-value sub-block's maximum).  Under
- *               KRK_PATH_AUTO, 6..8 rows of a shape the MFMA GEMM's
- *               weight-streaming kernel takes (Q4_K/Q5_K/Q6_K/Q8_0/Q4_0/
- *               MXFP4, n_in a multiple of 256) run there instead, as the
- *               reference's KRK_GEMV_M=0 arm puts rows 2..8 on its matrix
- *               tile (backend_hip.hip:2719-2722).
+ *               2^-23 of each 32-value sub-block's maximum).
  * rows  > 8   : per krk_set_gemm_path. */
 int krk_gemm(krk_backend *b, void *out, const void *x, const void *w, int wt,
              int64_t n_out, int64_t n_in, int64_t rows);

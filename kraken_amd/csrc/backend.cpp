@@ -302,14 +302,7 @@ int gemm_impl(krk_backend *b, void *out, const void *x, const void *w, int wt, i
     if (int s = check_mm(b, out, x, w, wt, n_out, n_in, rows)) return s;
     if (int s = make_current(b)) return s;
     const bool f16 = b->act == KRK_ACT_F16;
-    // GEMV rows: up to 8 (all of them under KRK_PATH_EXACT); under
-    // KRK_PATH_AUTO six to eight rows go to the f16 MFMA GEMM where its
-    // weight-streaming kernel takes the shape (Q4_K 4096 -> 14336: 8 rows
-    // 17.9 us there against 25.5 us as GEMV rows; 5 rows 16.4 us as GEMV
-    // rows against 17.6 us there)
-    const bool gemv_rows = rows <= 5 || (rows <= 8 && (b->path != KRK_PATH_AUTO ||
-                                                       !krk::gemm_mfma_streams(wt, rows, n_out, n_in)));
-    if (gemv_rows || b->path == KRK_PATH_EXACT) {
+    if (rows <= 8 || b->path == KRK_PATH_EXACT) {
         krk::SegTable t = one_seg(w, x, out, wt, n_out, n_in, rows, krk::SEG_PLAIN, nullptr);
         return run_gemv(b, wt, t);
     }

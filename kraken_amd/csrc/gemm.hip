@@ -779,8 +779,6 @@ static int stream_split(int64_t M, int64_t N, int64_t K) {
 }
 static size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
-bool gemm_mfma_streams(int dt, int64_t M, int64_t N, int64_t K) { return stream_gemm(dt, M, N, K); }
-
 size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K) {
     if (stream_gemm(dt, M, N, K)) {   // f32 rows as f16, and the split partials
         const int s = stream_split(M, N, K);

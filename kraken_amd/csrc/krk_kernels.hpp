@@ -102,8 +102,6 @@ hipError_t quantize_q8_rows_f16codes(const void *x, bool x_f16, int64_t rows, in
 // Prefill GEMM (f16 MFMA, f32 accumulate) and the Q8_0 x Q8 int8 MFMA rung.
 // out[M, N] = X[M, K] . deq(W)[N, K]^T.  `ws` is device scratch of ws_bytes.
 size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K);
-// gemm_mfma takes M rows by its weight-streaming kernel (the small batches)
-bool gemm_mfma_streams(int dt, int64_t M, int64_t N, int64_t K);
 // compute units of the current device (cached on first use)
 int device_cus();
 hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bool act_f16,

@@ -14,7 +14,7 @@ import pytest
 
 import oracle as O
 from conftest import rand_blocks
-from test_gpu_parity import GEMM_TOL, GEMV_TOL, _TABLES, dev, gemv_rows, host, rel, say
+from test_gpu_parity import GEMM_TOL, GEMV_TOL, _TABLES, dev, host, rel, say
 
 pytestmark = pytest.mark.gpu
 
@@ -67,8 +67,7 @@ def test_chunk_gemv_parity(torch_cuda, be32, dt, rows):
     x = np.random.default_rng(rows).standard_normal((rows, n_in)).astype(np.float32)
     say("gemv chunk fmt", dt, rows)
     out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
-    with gemv_rows(rows, be32):
-        be32.gemm(out, dev(torch, x), dev(torch, w), dt, n_out, n_in, rows)
+    be32.gemm(out, dev(torch, x), dev(torch, w), dt, n_out, n_in, rows)
     be32.sync()
     assert rel(host(out), O.gemm(dt, w, x, n_out)) <= GEMV_TOL
 

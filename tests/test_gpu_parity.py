@@ -6,7 +6,6 @@ Bars: dequantized values bit-exact; GEMV within
 own gate uses a norm for the same cancellation reason,
 tools/bench_ops.cpp:255-262); f16-staged MFMA GEMM within 2e-3 relative
 Frobenius error."""
-import contextlib
 import sys
 
 import numpy as np
@@ -98,22 +97,6 @@ def test_mxfp4_dequant_every_exponent(torch_cuda, be32):
     assert np.array_equal(host(out).view(np.uint32), O.dequant(O.MXFP4, w, 256, 32).view(np.uint32))
 
 
-@contextlib.contextmanager
-def gemv_rows(rows, *backends):
-    """Six to eight rows take the f16 MFMA GEMM under KRK_PATH_AUTO where its
-    weight-streaming kernel serves the shape; KRK_PATH_EXACT keeps them on
-    the GEMV kernels, which the tests using this hold to the 1e-5 bar."""
-    import kraken_amd
-    pin = rows > 5
-    for b in backends if pin else ():
-        b.set_gemm_path(kraken_amd.PATH_EXACT)
-    try:
-        yield
-    finally:
-        for b in backends if pin else ():
-            b.set_gemm_path(kraken_amd.PATH_AUTO)
-
-
 # --------------------------------------------------------------------- GEMV --
 @pytest.mark.parametrize("dt", FMTS)
 @pytest.mark.parametrize("rows", [1, 2, 3, 5, 8])
@@ -124,8 +107,7 @@ def test_gemv_f32_parity(krk, torch_cuda, be32, dt, rows):
     x = krk.synth_normal(rows * n_in, seed=200 + rows).reshape(rows, n_in)
     say("gemv", dt, rows, n_out, n_in)
     out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
-    with gemv_rows(rows, be32):
-        be32.gemm(out, dev(torch, x), dev(torch, w), dt, n_out, n_in, rows)
+    be32.gemm(out, dev(torch, x), dev(torch, w), dt, n_out, n_in, rows)
     be32.sync()
     ref = O.gemm(dt, w, x, n_out)
     e = rel(host(out), ref)
@@ -689,8 +671,7 @@ def test_q4_k_digits_rows(krk, torch_cuda, be32, rows, n_out, n_in):
     x = krk.synth_normal(rows * n_in, seed=801 + rows).reshape(rows, n_in)
     say("digits rows", rows, n_out, n_in)
     out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
-    with gemv_rows(rows, be32):
-        be32.gemm(out, dev(torch, x), dev(torch, w), O.Q4_K, n_out, n_in, rows)
+    be32.gemm(out, dev(torch, x), dev(torch, w), O.Q4_K, n_out, n_in, rows)
     be32.sync()
     ref = O.gemm(O.Q4_K, w, x, n_out)
     for r in range(rows):
@@ -759,8 +740,7 @@ def test_q6_k_digits(krk, torch_cuda, be32, rows, n_out, n_in):
     x = krk.synth_normal(rows * n_in, seed=841 + rows).reshape(rows, n_in)
     say("q6_k digits", rows, n_out, n_in)
     out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
-    with gemv_rows(rows, be32):
-        be32.gemm(out, dev(torch, x), dev(torch, w), O.Q6_K, n_out, n_in, rows)
+    be32.gemm(out, dev(torch, x), dev(torch, w), O.Q6_K, n_out, n_in, rows)
     be32.sync()
     ref = O.gemm(O.Q6_K, w, x, n_out)
     for r in range(rows):

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from test_gpu_parity import GEMM_TOL, GEMV_TOL, dev, digit_edge_x, gemv_rows, host, make_weights, rel, say
+from test_gpu_parity import GEMV_TOL, dev, digit_edge_x, host, make_weights, rel, say
 
 pytestmark = pytest.mark.gpu
 
@@ -103,46 +103,18 @@ def test_stream_rows(krk, torch_cuda, be32, be16, rows, n_out, n_in):
     x = krk.synth_normal(rows * n_in, seed=901 + n_in).reshape(rows, n_in)
     say("stream rows", rows, n_out, n_in)
     out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
-    with gemv_rows(rows, be32):
-        be32.gemm(out, dev(torch, x), dev(torch, w), O.Q4_K, n_out, n_in, rows)
+    be32.gemm(out, dev(torch, x), dev(torch, w), O.Q4_K, n_out, n_in, rows)
     be32.sync()
     ref = O.gemm(O.Q4_K, w, x, n_out, nthreads=16)
     for r in range(rows):
         assert rel(host(out)[r], ref[r]) <= GEMV_TOL, r
     xh = x.astype(np.float16)
     out16 = torch.full((rows, n_out), float("nan"), dtype=torch.float16, device="cuda")
-    with gemv_rows(rows, be16):
-        be16.gemm(out16, dev(torch, xh), dev(torch, w), O.Q4_K, n_out, n_in, rows)
+    be16.gemm(out16, dev(torch, xh), dev(torch, w), O.Q4_K, n_out, n_in, rows)
     be16.sync()
     ref16 = O.gemm(O.Q4_K, w, xh.astype(np.float32), n_out, nthreads=16)
     for r in range(rows):
         assert rel(host(out16)[r].astype(np.float32), ref16[r]) <= 2.0 ** -11 + GEMV_TOL, r
-
-
-@pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q8_0, O.Q4_0])
-@pytest.mark.parametrize("rows", [6, 7, 8])
-@pytest.mark.parametrize("n_out,n_in", [(17, 512), (300, 2304), (14336, 4096), (4096, 11008)])
-def test_auto_rows_6_to_8_take_mfma(krk, torch_cuda, be32, be16, dt, rows, n_out, n_in):
-    """Under KRK_PATH_AUTO six to eight rows of the streaming GEMM's shapes
-    take the f16 MFMA GEMM: f16 operands, f32 accumulation, the dense GEMM's
-    bar, row by row; f32 and f16 activations."""
-    torch = torch_cuda
-    w = make_weights(krk, dt, n_out, n_in, seed=950 + rows + dt)
-    x = krk.synth_normal(rows * n_in, seed=951 + n_in).reshape(rows, n_in)
-    say("auto rows", dt, rows, n_out, n_in)
-    ref = O.gemm(dt, w, x, n_out, nthreads=16)
-    out = torch.full((rows, n_out), float("nan"), dtype=torch.float32, device="cuda")
-    be32.gemm(out, dev(torch, x), dev(torch, w), dt, n_out, n_in, rows)
-    be32.sync()
-    for r in range(rows):
-        assert rel(host(out)[r], ref[r]) <= GEMM_TOL, r
-    xh = x.astype(np.float16)
-    ref16 = O.gemm(dt, w, xh.astype(np.float32), n_out, nthreads=16)
-    out16 = torch.full((rows, n_out), float("nan"), dtype=torch.float16, device="cuda")
-    be16.gemm(out16, dev(torch, xh), dev(torch, w), dt, n_out, n_in, rows)
-    be16.sync()
-    for r in range(rows):
-        assert rel(host(out16)[r].astype(np.float32), ref16[r]) <= GEMM_TOL, r
 
 
 def test_stream_q4_k_vocab_head(krk, torch_cuda, be32):
