@@ -953,7 +953,8 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
     // (one-row Q4_K and Q4_0 launches of two-block slices stream any
     // height: a 128256-row Q4_K head took 57.8 us here against 66.6 us on
     // the digit kernel, Q4_0 70.3 us against 82.3 on the VALU kernel; the
-    // Q6_K head stays on the digit kernel (92 us against 95-110), Q8_0's on
+    // Q6_K head stays on the digit kernel (92 us against 95-110; 85.2
+    // against 90.5 with 16-row tiles at two workgroups per CU), Q8_0's on
     // the VALU kernel (106 us against 113; with load-transpose 101.2 against
     // 103.7 on one box))
     if (rows > 2 * 32 * static_cast<int64_t>(device_cus()) * (nw <= 8 ? 2 : 1) &&
@@ -1061,7 +1062,10 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
             const int rows_t = t.seg[i].kind == SEG_SILU ? 16 : c;
             tiles += (t.seg[i].n_out + rows_t - 1) / rows_t;
         }
-        const int64_t cost = (tiles + cap - 1) / cap * c;
+        // (Q6_K's one-row load-transpose tiles above 16 rows hold 135
+        // registers a lane: one workgroup per CU)
+        const int64_t capc = dt == DT_Q6_K && lt && c > 16 ? static_cast<int64_t>(device_cus()) : cap;
+        const int64_t cost = (tiles + capc - 1) / capc * c;
         if (cost < best) { best = cost; tr = c; }
     }
     // the grid: one row of tiles per segment, as wide as the longest
