@@ -1035,7 +1035,7 @@ template <int N> __device__ __forceinline__ void mg_wait_vm() {
 }
 
 template <int DT, bool GU, int MI>
-__global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K || DT == DT_Q6_K ? 4 : 2)))
+__global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K || (DT == DT_Q6_K && MI == 1) ? 4 : 2)))
     moe_gemm_kernel(MoeGemmArgs a, int ntiles) {
     constexpr int MT = 32 * MI;        // item rows
     constexpr int MB = 2 * MI;         // 16-row M blocks
