@@ -413,7 +413,7 @@ TRACE_LABELS = [
     ("gemv_stream_kernel<2, float, float, 2, 28", "262144", "Q4_0 GEMV 4096->14336, M=1", _HEAD_BYTES, "B"),
     ("gemv_stream_kernel<8, float, float, 2, 28", "262144", "Q8_0 GEMV 4096->14336, M=1",
      14336 * _Q8_ROW + 4 * (4096 + 14336), "B"),
-    ("gemv_stream_kernel<14, float, float, 2, 28", "262144", "Q6_K GEMV 4096->14336, M=1",
+    ("gemv_stream_kernel<14, float, float, 2, 16, 8, true, 0, 8", "458752", "Q6_K GEMV 4096->14336, M=1 (16-row tiles)",
      14336 * _Q6K_ROW + 4 * (4096 + 14336), "B"),
     ("gemv_stream_kernel<12, float, float, 2, 16, 8, true, 0, 8", "131072",
      "C2 layer: q, k, v, o (Q4_K 4096->4096)", 4096 * _Q4K_ROW + 4 * 8192, "B"),
@@ -448,6 +448,12 @@ TRACE_LABELS = [
     ("moe_gemm_kernel<14, false, 2>", "1572864", "C5 x512: grouped expert GEMM, down (Q6_K banks)",
      2 * 4096 * 1536 * 4096, "f16"),
     ("moe_gather_f16_kernel", "1048576", "C5 x512: activation rows gathered to f16 in plan order", None, None),
+    ("router_softmax_kernel<float, 2>", "64", "C5 x1: router softmax (128 experts)", None, None),
+    ("router_topk_rank_kernel<2>", "128", "C5 x1: router top-8 (rank per expert)", None, None),
+    ("router_softmax_kernel<float, 2>", "1024", "C5 x16: router softmax", None, None),
+    ("router_topk_rank_kernel<2>", "2048", "C5 x16: router top-8", None, None),
+    ("router_softmax_kernel<float, 2>", "32768", "C5 x512: router softmax", None, None),
+    ("router_topk_rank_kernel<2>", "65536", "C5 x512: router top-8", None, None),
     ("gemv_stream_kernelILi12EDF16_DF16_Li2ELi28ELi8ELb1ELi0ELi8ELi4ELb0E", "262144",
      "rows 4: Q4_K 4096->14336, f16 activations, one pass (weights only in the rate)", 14336 * _Q4K_ROW, "B"),
     ("gemv_stream_kernelILi12EDF16_DF16_Li2ELi28ELi8ELb1ELi0ELi8ELi5ELb0E", "262144",
