@@ -48,6 +48,8 @@ def parse():
                     help="comma list of MoE batch sizes also timed with Q6_K down banks (Q4_K_M)")
     ap.add_argument("--moe-exact-tokens", default="512",
                     help="comma list of MoE batch sizes also timed under KRK_PATH_EXACT")
+    ap.add_argument("--pmc-rows", default="", metavar="ROWS",
+                    help="run the rows GEMV (comma list of row counts) for a counter pass and exit")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="counter run: 5 plain copies of 256 MiB, then 20 headline GEMVs")
     ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
@@ -366,6 +368,26 @@ def pmc_pass():
     be.close()
 
 
+def pmc_rows(rows):
+    """The program the rows counters are read on: the Q4_K GEMV of each
+    activation-row count (4096 -> 14336, f16 activations, as the bench's
+    rows section), ten eager calls each."""
+    import torch
+
+    import kraken_amd as K
+    be = K.Backend(0, K.ACT_F16)
+    n_out, n_in = 14336, 4096
+    w = torch.from_numpy(K.quantize(K.Q4_K, K.synth_normal(n_out * n_in, seed=1, std=0.02, nthreads=16),
+                                    n_out, n_in, 16)).cuda()
+    for m in rows:
+        x = torch.from_numpy(K.synth_normal(m * n_in, seed=2)).cuda().reshape(m, n_in).half()
+        out = torch.empty((m, n_out), dtype=torch.float16, device="cuda")
+        for _ in range(10):
+            be.gemm(out, x, w, K.Q4_K, n_out, n_in, m)
+    torch.cuda.synchronize()
+    be.close()
+
+
 def summarize_pmc(fetch_csv, write_csv):
     """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the copy and the GEMV,
     the copy's counter/true-bytes factor, and the GEMV's HBM bytes."""
@@ -611,6 +633,9 @@ def main():
         print("bench.py: this build runs on one GPU only (no sharding, no collectives); "
               "run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_rows:
+        pmc_rows([int(v) for v in args.pmc_rows.split(",")])
+        return
     if args.pmc_pass:
         pmc_pass()
         return
