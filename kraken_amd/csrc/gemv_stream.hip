@@ -44,6 +44,10 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kTab = 768;   // digit bytes per 256-value block: 8 sub-blocks x 3 planes x 32
+// (several rows: each block's table is followed by a 16-byte zero pad, which
+// the lanes whose A rows are zero read instead of selecting zeros)
+constexpr int kTabPad = 768, kTabRows = 784;
+__host__ __device__ constexpr int tab_stride(int xr) { return xr > 1 ? kTabRows : kTab; }
 constexpr int kMaxWaves = 16;
 constexpr int kStreamRows = 8;   // dense Q4_K launches of up to this many activation rows
 constexpr int kStreamRowsWide = 4;   // ... of slices wider than two blocks
@@ -123,6 +127,8 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
     constexpr int RG = (TR + 15) / 16;     // 16-row groups of a plain tile
     constexpr int NL = RG * NBW;           // (16 rows, block) groups of a wave
     constexpr int NPASS = (NBW + 1) / 2;   // x passes: 16 sub-blocks of 8 x 4 lanes each
+    constexpr bool PAD = XR > 1;           // zero-padded tables, A operands read without selects
+    constexpr int KT = tab_stride(XR);
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -334,16 +340,16 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
     // arrays and partial sums, row by row)
     // layout: XP table slots, then the XR rows' partial sums, then (LT) the
     // slice buffers
-    const int tstride = nw * (NBW * kTab + 2 * NBW * 8 * static_cast<int>(sizeof(float2)));
+    const int tstride = nw * (NBW * KT + 2 * NBW * 8 * static_cast<int>(sizeof(float2)));
     const int rstride = XP * tstride + XR * 32 * nw * 4;
-    auto tab_of = [&](int sl) { return lds + sl * tstride + wv * (NBW * kTab); };
+    auto tab_of = [&](int sl) { return lds + sl * tstride + wv * (NBW * KT); };
     auto ex_of = [&](int sl) {
-        return reinterpret_cast<float2 *>(lds + sl * tstride + nw * (NBW * kTab)) + wv * (NBW * 8);
+        return reinterpret_cast<float2 *>(lds + sl * tstride + nw * (NBW * KT)) + wv * (NBW * 8);
     };
     auto red_of = [&](int xr) { return reinterpret_cast<float *>(lds + XP * tstride + xr * 32 * nw * 4); };
     uint8_t *tab = tab_of(0);
     float2 *ex = ex_of(0);
-    float2 *ex16 = reinterpret_cast<float2 *>(lds + nw * (NBW * kTab)) + nw * (NBW * 8) + wv * (NBW * 8);
+    float2 *ex16 = reinterpret_cast<float2 *>(lds + nw * (NBW * KT)) + nw * (NBW * 8) + wv * (NBW * 8);
     // ---- per-lane MFMA roles (A row c16 = 4 sub-block' + digit plane)
     const int ap = c16 & 3, as = c16 >> 2;
     const int sl = 2 * (gq >> 1);
@@ -355,6 +361,10 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
     // Q6_K: lane group gq's A rows hold sub-block 4 h + qd's half l
     const bool a6 = ap < 3 && as == gq;
     const int a6_off = 4 * h6 * 96 + (ap < 3 ? ap : 0) * 32 + 16 * lh6;
+    // the lanes' A-operand offsets within a block's table: lanes whose A
+    // rows are zero read the block's zero pad (no select, no branch)
+    const int o_lo0 = a_lo ? a_off : kTabPad, o_lo1 = a_lo ? a_off + 384 : kTabPad;
+    const int o_hi0 = a_hi ? a_off : kTabPad, o_hi1 = a_hi ? a_off + 384 : kTabPad;
     float acc[RG];
 #pragma unroll
     for (int rg = 0; rg < RG; rg++) acc[rg] = 0.0f;
@@ -434,7 +444,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
             // 24..31 (the order its codes take in the B operand)
             const int sbt = QS ? q40_slot(sbw & 7) : (sbw & 7);
             const int po = Q40 ? 8 * (((lane & 1) << 1) | ((lane >> 1) & 1)) : 8 * (lane & 3);
-            uint8_t *o = tab + (sbw >> 3) * kTab + sbt * 96 + po;
+            uint8_t *o = tab + (sbw >> 3) * KT + sbt * 96 + po;
             *reinterpret_cast<u32x2 *>(o) = u32x2{p0[0], p0[1]};
             *reinterpret_cast<u32x2 *>(o + 32) = u32x2{p1[0], p1[1]};
             *reinterpret_cast<u32x2 *>(o + 64) = u32x2{p2[0], p2[1]};
@@ -449,6 +459,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
             if (sbw < 8 * NBW && (lane & 3) == 0) ex16[sbw] = float2{__int_as_float(xsum), __int_as_float(xsum_hi)};
         }
     }
+    if (PAD && lane < NBW) *reinterpret_cast<u32x4 *>(tab + lane * KT + kTabPad) = u32x4{0u, 0u, 0u, 0u};
     }   // activation rows
 
     // (expert-major runs: the next row's activations load while this one
@@ -467,7 +478,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
         const int mlo = a_lo ? -1 : 0, mhi = a_hi ? -1 : 0;
 #pragma unroll
         for (int b = 0; b < NBW; b++) {
-            const uint8_t *tb = tab + b * kTab + a_off;
+            const uint8_t *tb = tab + b * KT + a_off;
             const v4i r0 = lds_v4i(tb), r1 = lds_v4i(tb + 384);
             HA[b][0] = r0 & mlo;
             HA[b][1] = r1 & mlo;
@@ -600,7 +611,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
                 const uint32_t sw = jj < 4 ? scx : scy;
                 const float ds = d * static_cast<float>(static_cast<int8_t>(sw >> (8 * (jj & 3))));
                 // A rows 4 gq + p: digit plane p of sub-block 4 h + qd, half l
-                const v4i A = a6 ? lds_v4i(tab + b * kTab + a6_off + qd * 96) : Z;
+                const v4i A = a6 ? lds_v4i(tab + b * KT + a6_off + qd * 96) : Z;
                 const v4i C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, Z, 0, 0, 0);
                 const int sbi = b * 8 + 4 * h6 + qd;
                 const float2 h2 = ex16[sbi];
@@ -613,8 +624,23 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
             __builtin_amdgcn_sched_barrier(0);
             continue;
         }
-        const uint8_t *tb = tab + b * kTab + a_off;
+        const uint8_t *tb = tab + b * KT;
         const int hb = HOLD ? b : 0;
+        // A operands of one row's table at tbb: padded tables read every
+        // lane's offset, plain ones select zeros for the lanes outside
+        auto a_ops = [&](const uint8_t *tbb, v4i &a0l, v4i &a1l, v4i &a0h, v4i &a1h) {
+            if constexpr (PAD) {
+                a0l = lds_v4i(tbb + o_lo0);
+                a1l = lds_v4i(tbb + o_lo1);
+                a0h = lds_v4i(tbb + o_hi0);
+                a1h = lds_v4i(tbb + o_hi1);
+            } else {
+                a0l = a_lo ? lds_v4i(tbb + a_off) : Z;
+                a1l = a_lo ? lds_v4i(tbb + a_off + 384) : Z;
+                a0h = a_hi ? lds_v4i(tbb + a_off) : Z;
+                a1h = a_hi ? lds_v4i(tbb + a_off + 384) : Z;
+            }
+        };
         if constexpr (Q80) {
             // lane group gq holds blocks 2 gq, 2 gq + 1: {d, 32 int8 codes}
             // twice.  MFMA m of lane pair p = gq / 2 takes block 4 p + m, lane
@@ -641,10 +667,15 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
                 return v4i{static_cast<int>(c[0]), static_cast<int>(c[1]), static_cast<int>(c[2]),
                            static_cast<int>(c[3])};
             };
-            const v4i A0l = HOLD ? HA[hb][0] : a_lo ? lds_v4i(tb) : Z;
-            const v4i A1l = HOLD ? HA[hb][1] : a_lo ? lds_v4i(tb + 384) : Z;
-            const v4i A0h = HOLD ? HA[hb][2] : a_hi ? lds_v4i(tb) : Z;
-            const v4i A1h = HOLD ? HA[hb][3] : a_hi ? lds_v4i(tb + 384) : Z;
+            v4i A0l, A1l, A0h, A1h;
+            if constexpr (HOLD) {
+                A0l = HA[hb][0];
+                A1l = HA[hb][1];
+                A0h = HA[hb][2];
+                A1h = HA[hb][3];
+            } else {
+                a_ops(tb, A0l, A1l, A0h, A1h);
+            }
             const float2 ex0 = HOLD ? HE[hb][0] : ex[b * 8 + gq], ex1 = HOLD ? HE[hb][1] : ex[b * 8 + 4 + gq];
             v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0l, codes(X), Z, 0, 0, 0);
             C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0h, codes(X + 4), C0, 0, 0, 0);
@@ -687,10 +718,15 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
                 return v4i{static_cast<int>(c0 & M), static_cast<int>(c1 & M), static_cast<int>((c0 >> 4) & M),
                            static_cast<int>((c1 >> 4) & M)};
             };
-            const v4i A0l = HOLD ? HA[hb][0] : a_lo ? lds_v4i(tb) : Z;
-            const v4i A1l = HOLD ? HA[hb][1] : a_lo ? lds_v4i(tb + 384) : Z;
-            const v4i A0h = HOLD ? HA[hb][2] : a_hi ? lds_v4i(tb) : Z;
-            const v4i A1h = HOLD ? HA[hb][3] : a_hi ? lds_v4i(tb + 384) : Z;
+            v4i A0l, A1l, A0h, A1h;
+            if constexpr (HOLD) {
+                A0l = HA[hb][0];
+                A1l = HA[hb][1];
+                A0h = HA[hb][2];
+                A1h = HA[hb][3];
+            } else {
+                a_ops(tb, A0l, A1l, A0h, A1h);
+            }
             const float2 ex0 = HOLD ? HE[hb][0] : ex[b * 8 + gq], ex1 = HOLD ? HE[hb][1] : ex[b * 8 + 4 + gq];
             v4i C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0l, codes(X[0], X[1]), Z, 0, 0, 0);
             C0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0h, codes(X[2], X[3]), C0, 0, 0, 0);
@@ -707,10 +743,15 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
             __builtin_amdgcn_sched_barrier(0);
             continue;
         }
-        const v4i A0l = HOLD ? HA[hb][0] : a_lo ? lds_v4i(tb) : Z;
-        const v4i A1l = HOLD ? HA[hb][1] : a_lo ? lds_v4i(tb + 384) : Z;
-        const v4i A0h = HOLD ? HA[hb][2] : a_hi ? lds_v4i(tb) : Z;
-        const v4i A1h = HOLD ? HA[hb][3] : a_hi ? lds_v4i(tb + 384) : Z;
+        v4i A0l, A1l, A0h, A1h;
+        if constexpr (HOLD) {
+            A0l = HA[hb][0];
+            A1l = HA[hb][1];
+            A0h = HA[hb][2];
+            A1h = HA[hb][3];
+        } else {
+            a_ops(tb, A0l, A1l, A0h, A1h);
+        }
         const float2 ex0 = HOLD ? HE[hb][0] : ex[b * 8 + gq], ex1 = HOLD ? HE[hb][1] : ex[b * 8 + 4 + gq];
         const u32x4 h = hd[i], q0 = qa[i], q1 = qb[i];
         const v4i B0l = {static_cast<int>(q0.x & M), static_cast<int>(q0.y & M), static_cast<int>(q0.z & M),
@@ -748,11 +789,10 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
         if (p0 == 0) acc[rg] = row_dot(A0l, A1l, A0h, A1h, ex0, ex1, acc[rg]);
 #pragma unroll
         for (int xr = p0 > 1 ? p0 : 1; xr < pend; xr++) {
-            const uint8_t *tx = tab_of(xr - p0) + b * kTab + a_off;
             const float2 *ey = ex_of(xr - p0);
-            accx[xr - 1][rg] = row_dot(a_lo ? lds_v4i(tx) : Z, a_lo ? lds_v4i(tx + 384) : Z, a_hi ? lds_v4i(tx) : Z,
-                                       a_hi ? lds_v4i(tx + 384) : Z, ey[b * 8 + gq], ey[b * 8 + 4 + gq],
-                                       accx[xr - 1][rg]);
+            v4i a0l, a1l, a0h, a1h;
+            a_ops(tab_of(xr - p0) + b * KT, a0l, a1l, a0h, a1h);
+            accx[xr - 1][rg] = row_dot(a0l, a1l, a0h, a1h, ey[b * 8 + gq], ey[b * 8 + 4 + gq], accx[xr - 1][rg]);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -812,7 +852,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
 
 size_t stream_lds(int nw, int nbw, int xr = 1) {
     const size_t xp = xr > 5 ? 4 : xr;   // table slots: rows per pass
-    return xp * nw * nbw * (kTab + 2 * 8 * sizeof(float2)) + xr * 32 * static_cast<size_t>(nw) * sizeof(float);
+    return xp * nw * nbw * (tab_stride(xr) + 2 * 8 * sizeof(float2)) + xr * 32 * static_cast<size_t>(nw) * sizeof(float);
 }
 // the load-transpose slice buffers of a launch
 size_t stream_lt_lds(int nw, int nbw, int tr, int pb = 9) {
