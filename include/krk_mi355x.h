@@ -143,7 +143,9 @@ int krk_dtype_row_aligned(int wt, int64_t n);
  * rows == 1..8: fused dequant+dot GEMV with exact products and f32
  *               accumulation; Q4_K at rows == 1 forms the products on the
  *               int8 matrix cores from exact digit planes of x (rounded at
- *               2^-23 of each 32-value sub-block's maximum).
+ *               2^-23 of each 32-value sub-block's maximum), and Q4_K at
+ *               rows == 2..8 the same, the rows' digit tables built once per
+ *               call in the handle's workspace (grown on the first such call).
  * rows  > 8   : per krk_set_gemm_path. */
 int krk_gemm(krk_backend *b, void *out, const void *x, const void *w, int wt,
              int64_t n_out, int64_t n_in, int64_t rows);
@@ -152,8 +154,8 @@ int krk_gemm(krk_backend *b, void *out, const void *x, const void *w, int wt,
  * callers that cannot allocate device memory -- code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc.  Same
  * arguments, kernels and results as krk_gemm (bit-identical), but the
- * split-K partials and int8 activation codes that krk_gemm keeps in the
- * handle's growing workspace live in a fixed device array of
+ * split-K partials, int8 activation codes and several-row digit tables that
+ * krk_gemm keeps in the handle's growing workspace live in a fixed device array of
  * krk_gemm_noalloc_scratch_bytes() (64 MiB) instead: one per device, held
  * until the process ends, shared by every handle on that device.  The array
  * is part of the library's code object, so loading the library reserves

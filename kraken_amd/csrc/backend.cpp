@@ -302,12 +302,25 @@ int gemm_impl(krk_backend *b, void *out, const void *x, const void *w, int wt, i
     if (int s = check_mm(b, out, x, w, wt, n_out, n_in, rows)) return s;
     if (int s = make_current(b)) return s;
     const bool f16 = b->act == KRK_ACT_F16;
+    const bool fixed = ws != nullptr;
     if (rows <= 8 || b->path == KRK_PATH_EXACT) {
         krk::SegTable t = one_seg(w, x, out, wt, n_out, n_in, rows, krk::SEG_PLAIN, nullptr);
+        if (rows > 1 && rows <= 8) {
+            // the streaming kernel's digit tables of the rows, built once per call
+            const size_t need = krk::gemv_stream_xtab_bytes(rows, n_in);
+            if (fixed) {
+                if (need > ws_bytes)
+                    return fail(b, KRK_ERR_NOMEM, "gemv rows need %zu bytes of scratch; the fixed scratch holds %zu",
+                                need, ws_bytes);
+            } else {
+                if (int s = ensure_ws(b, need)) return s;
+                ws = b->ws;
+            }
+            t.xtab = static_cast<uint8_t *>(ws);
+        }
         return run_gemv(b, wt, t);
     }
     const int64_t rb = krk_dtype_row_bytes(wt, n_in);
-    const bool fixed = ws != nullptr;
     if (b->path == KRK_PATH_INT8) {
         if (!krk::gemm_int8_serves(wt))
             return fail(b, KRK_ERR_UNSUPPORTED, "the int8 rung serves Q8_0, Q4_K, Q5_K and Q6_K weights");

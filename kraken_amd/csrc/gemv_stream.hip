@@ -44,10 +44,13 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kTab = 768;   // digit bytes per 256-value block: 8 sub-blocks x 3 planes x 32
-// (several rows: each block's table is followed by a 16-byte zero pad, which
-// the lanes whose A rows are zero read instead of selecting zeros)
-constexpr int kTabPad = 768, kTabRows = 784;
+// Several rows: the tables are built once per call (stream_xtab_kernel) and
+// each block's entry is 848 bytes: the 768 digit bytes, a 16-byte zero pad
+// (which the lanes whose A rows are zero read instead of selecting zeros)
+// and the eight sub-blocks' {2^-e, sum x}; a wave copies its slice whole.
+constexpr int kTabPad = 768, kTabEx = 784, kTabRows = 848;
 __host__ __device__ constexpr int tab_stride(int xr) { return xr > 1 ? kTabRows : kTab; }
+
 constexpr int kMaxWaves = 16;
 constexpr int kStreamRows = 8;   // dense Q4_K launches of up to this many activation rows
 constexpr int kStreamRowsWide = 4;   // ... of slices wider than two blocks
@@ -94,6 +97,75 @@ __device__ __forceinline__ void load_x8(const _Float16 *p, float (&v)[8]) {
     const half8 h = *reinterpret_cast<const half8 *>(p);
 #pragma unroll
     for (int k = 0; k < 8; k++) v[k] = static_cast<float>(h[k]);
+}
+
+// The digit planes of eight activations, values 8 (lane & 3) .. + 7 of one
+// 32-value sub-block (the quad of lanes 4j .. 4j + 3 holds the sub-block):
+// the three planes' bytes for these values into the sub-block's 96 table
+// bytes (natural value order) and, from lane 4j, {2^-e, sum x}.  The same
+// arithmetic as the one-row kernel's in-place build.
+__device__ __forceinline__ void q4k_sub_digits(const float (&v)[8], int lane, uint8_t *sub, float2 *exs) {
+    float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        amax = fmaxf(amax, fabsf(v[k]));
+        sum += v[k];
+    }
+    amax = fmaxf(amax, quad_xor1(amax));
+    amax = fmaxf(amax, quad_xor2(amax));
+    sum += quad_xor1(sum);
+    sum += quad_xor2(sum);
+    const uint32_t Eb = (__float_as_uint(amax) >> 23) & 255u;
+    const bool live = amax > 0.0f && Eb < 255u;
+    int e = live ? 148 - static_cast<int>(Eb) : 0;
+    e = e > 126 ? 126 : e;
+    const float up = __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
+    const float dn = __uint_as_float(static_cast<uint32_t>(127 - e) << 23);
+    uint32_t Y[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+        Y[k] = __float_as_uint(__builtin_fmaf(v[k], up, 12582912.0f)) + (0x808080u - 0x4B400000u);
+    uint32_t p0[2], p1[2], p2[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const uint32_t *y = Y + 4 * hh;
+        const uint32_t A01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);
+        const uint32_t A23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
+        const uint32_t B01 = __builtin_amdgcn_perm(y[1], y[0], 0x06020602u);
+        const uint32_t B23 = __builtin_amdgcn_perm(y[3], y[2], 0x06020602u);
+        p0[hh] = live ? __builtin_amdgcn_perm(A23, A01, 0x05040100u) ^ 0x80808080u : 0u;
+        p1[hh] = live ? __builtin_amdgcn_perm(A23, A01, 0x07060302u) ^ 0x80808080u : 0u;
+        p2[hh] = live ? __builtin_amdgcn_perm(B23, B01, 0x05040100u) ^ 0x80808080u : 0u;
+    }
+    uint8_t *o = sub + 8 * (lane & 3);
+    *reinterpret_cast<u32x2 *>(o) = u32x2{p0[0], p0[1]};
+    *reinterpret_cast<u32x2 *>(o + 32) = u32x2{p1[0], p1[1]};
+    *reinterpret_cast<u32x2 *>(o + 64) = u32x2{p2[0], p2[1]};
+    if ((lane & 3) == 0) *exs = float2{live ? dn : 1.0f, sum};
+}
+
+// The activation rows' digit tables of a several-row launch, once per call:
+// row r's blocks 0 .. nbp - 1 at out + (r nbp + b) 848 (blocks from nb on,
+// a ragged last slice's, as zero activations: no digits, {1, 0}).  One wave
+// per (two blocks, row).
+template <typename XT>
+__global__ void __launch_bounds__(64) stream_xtab_kernel(const XT *__restrict__ x, int64_t x_stride, int nb, int nbp,
+                                                         uint8_t *__restrict__ out) {
+    const int lane = threadIdx.x;
+    const int sbw = lane >> 2, blk = 2 * static_cast<int>(blockIdx.x) + (sbw >> 3), s = sbw & 7;
+    const bool in = blk < nb;
+    float v[8];
+    load_x8(x + static_cast<int64_t>(blockIdx.y) * x_stride + (in ? static_cast<int64_t>(blk) * 256 + s * 32 + 8 * (lane & 3) : 0),
+            v);
+    if (!in) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = 0.0f;
+    }
+    uint8_t *base = out + (static_cast<int64_t>(blockIdx.y) * nbp + (blk < nbp ? blk : nbp - 1)) * kTabRows;
+    if (blk < nbp) {
+        q4k_sub_digits(v, lane, base + s * 96, reinterpret_cast<float2 *>(base + kTabEx) + s);
+        if (s == 0 && (lane & 3) == 0) *reinterpret_cast<u32x4 *>(base + kTabPad) = u32x4{0u, 0u, 0u, 0u};
+    }
 }
 
 // MOE: 0 plain segments; 1 routed gate/up pairs of one token (grid row s =
@@ -200,7 +272,24 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
     // tables rebuilt in the same (wave-private) LDS while the weights stay
     // in registers, so two workgroups still fit a CU
     constexpr int XP = XR > 5 ? 4 : XR;
-    float xvr[XP][NPASS][8];
+    float xvr[PAD ? 1 : XP][NPASS][8];
+    // (several rows: the pass's table slices, NBW 848-byte blocks per row,
+    // 16 bytes a lane per piece; copied from the call's precomputed tables)
+    constexpr int PQ = PAD ? (NBW * (kTabRows / 16) + 63) / 64 : 1;
+    u32x4 tv[PAD ? XP : 1][PQ];
+    const int nbp = PAD ? nw * NBW : 0;
+    auto load_tabs = [&](int r0, int r1) {
+#pragma unroll
+        for (int r = 0; r < XP; r++) {
+            if (r0 + r >= r1) break;
+            const uint8_t *src = t.xtab + (static_cast<int64_t>(r0 + r) * nbp + kb0) * kTabRows;
+#pragma unroll
+            for (int j = 0; j < PQ; j++) {
+                const int q = 64 * j + lane;
+                tv[r][j] = q < NBW * (kTabRows / 16) ? ldg128(src + 16 * q) : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
     auto load_xrow_to = [&](const XT *xr, float (&xv)[NPASS][8]) {
 #pragma unroll
         for (int p = 0; p < NPASS; p++) {
@@ -215,9 +304,13 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
     };
     auto load_xrow = [&](const XT *xr) { load_xrow_to(xr, xvr[0]); };
     __builtin_amdgcn_s_setprio(3);
-    load_xrow(row_x(pb));
+    if constexpr (PAD) {
+        load_tabs(0, XP);
+    } else {
+        load_xrow(row_x(pb));
 #pragma unroll
-    for (int xr = 1; xr < XP; xr++) load_xrow_to(x + xr * t.x_stride, xvr[xr]);
+        for (int xr = 1; xr < XP; xr++) load_xrow_to(x + xr * t.x_stride, xvr[xr]);
+    }
     // ---- then every weight byte of the wave's slice of the tile: group i =
     // (row group rg, block b), lane (c16, gq) takes of row rg * 16 + c16:
     //   Q4_K: the 16-byte header and code bytes 16 gq .. + 15 of each
@@ -340,13 +433,18 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
     // arrays and partial sums, row by row)
     // layout: XP table slots, then the XR rows' partial sums, then (LT) the
     // slice buffers
-    const int tstride = nw * (NBW * KT + 2 * NBW * 8 * static_cast<int>(sizeof(float2)));
+    const int tstride = PAD ? nw * NBW * KT : nw * (NBW * KT + 2 * NBW * 8 * static_cast<int>(sizeof(float2)));
     const int rstride = XP * tstride + XR * 32 * nw * 4;
     auto tab_of = [&](int sl) { return lds + sl * tstride + wv * (NBW * KT); };
     auto ex_of = [&](int sl) {
         return reinterpret_cast<float2 *>(lds + sl * tstride + nw * (NBW * KT)) + wv * (NBW * 8);
     };
     auto red_of = [&](int xr) { return reinterpret_cast<float *>(lds + XP * tstride + xr * 32 * nw * 4); };
+    // {2^-e, sum x} of block b of table slot sl
+    auto ex_blk = [&](int sl, int b) -> const float2 * {
+        if constexpr (PAD) return reinterpret_cast<const float2 *>(tab_of(sl) + b * KT + kTabEx);
+        else return ex_of(sl) + b * 8;
+    };
     uint8_t *tab = tab_of(0);
     float2 *ex = ex_of(0);
     float2 *ex16 = reinterpret_cast<float2 *>(lds + nw * (NBW * KT)) + nw * (NBW * 8) + wv * (NBW * 8);
@@ -379,9 +477,27 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
     // (a later pass's activations: L2-resident rows, loaded once the
     // previous pass has released their registers)
     if (p0 > 0) {
+        if constexpr (PAD) {
+            load_tabs(p0, pend);
+        } else {
 #pragma unroll
-        for (int xr = p0; xr < pend; xr++) load_xrow_to(x + xr * t.x_stride, xvr[xr - p0]);
+            for (int xr = p0; xr < pend; xr++) load_xrow_to(x + xr * t.x_stride, xvr[xr - p0]);
+        }
     }
+    if constexpr (PAD) {
+        // the pass's rows: their slices into the wave's table slots (this
+        // wave's reads of the previous pass completed in order before these
+        // writes)
+#pragma unroll
+        for (int r = 0; r < XP; r++) {
+            if (p0 + r >= pend) break;
+#pragma unroll
+            for (int j = 0; j < PQ; j++) {
+                const int q = 64 * j + lane;
+                if (q < NBW * (kTabRows / 16)) *reinterpret_cast<u32x4 *>(tab_of(r) + 16 * q) = tv[r][j];
+            }
+        }
+    } else {
 #pragma unroll
     for (int xr = p0; xr < pend; xr++) {
     uint8_t *tab = tab_of(xr - p0);
@@ -459,8 +575,8 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
             if (sbw < 8 * NBW && (lane & 3) == 0) ex16[sbw] = float2{__int_as_float(xsum), __int_as_float(xsum_hi)};
         }
     }
-    if (PAD && lane < NBW) *reinterpret_cast<u32x4 *>(tab + lane * KT + kTabPad) = u32x4{0u, 0u, 0u, 0u};
     }   // activation rows
+    }   // tables built in place
 
     // (expert-major runs: the next row's activations load while this one
     // is multiplied)
@@ -752,7 +868,7 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
         } else {
             a_ops(tb, A0l, A1l, A0h, A1h);
         }
-        const float2 ex0 = HOLD ? HE[hb][0] : ex[b * 8 + gq], ex1 = HOLD ? HE[hb][1] : ex[b * 8 + 4 + gq];
+        const float2 ex0 = HOLD ? HE[hb][0] : ex_blk(0, b)[gq], ex1 = HOLD ? HE[hb][1] : ex_blk(0, b)[4 + gq];
         const u32x4 h = hd[i], q0 = qa[i], q1 = qb[i];
         const v4i B0l = {static_cast<int>(q0.x & M), static_cast<int>(q0.y & M), static_cast<int>(q0.z & M),
                          static_cast<int>(q0.w & M)};
@@ -789,10 +905,10 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
         if (p0 == 0) acc[rg] = row_dot(A0l, A1l, A0h, A1h, ex0, ex1, acc[rg]);
 #pragma unroll
         for (int xr = p0 > 1 ? p0 : 1; xr < pend; xr++) {
-            const float2 *ey = ex_of(xr - p0);
+            const float2 *ey = ex_blk(xr - p0, b);
             v4i a0l, a1l, a0h, a1h;
             a_ops(tab_of(xr - p0) + b * KT, a0l, a1l, a0h, a1h);
-            accx[xr - 1][rg] = row_dot(a0l, a1l, a0h, a1h, ey[b * 8 + gq], ey[b * 8 + 4 + gq], accx[xr - 1][rg]);
+            accx[xr - 1][rg] = row_dot(a0l, a1l, a0h, a1h, ey[gq], ey[4 + gq], accx[xr - 1][rg]);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -852,7 +968,8 @@ __global__ void __launch_bounds__(64 * NWMAX, MOE >= 3 || (XR > 4 && NWMAX == 8)
 
 size_t stream_lds(int nw, int nbw, int xr = 1) {
     const size_t xp = xr > 5 ? 4 : xr;   // table slots: rows per pass
-    return xp * nw * nbw * (tab_stride(xr) + 2 * 8 * sizeof(float2)) + xr * 32 * static_cast<size_t>(nw) * sizeof(float);
+    const size_t per = xr > 1 ? kTabRows : kTab + 2 * 8 * sizeof(float2);
+    return xp * nw * nbw * per + xr * 32 * static_cast<size_t>(nw) * sizeof(float);
 }
 // the load-transpose slice buffers of a launch
 size_t stream_lt_lds(int nw, int nbw, int tr, int pb = 9) {
@@ -988,7 +1105,8 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
     const int nw = (t.n_in / 256 + nbw - 1) / nbw;
     // (several rows: their digit tables within the 160 KB of LDS; five and
     // more rows on two-block slices)
-    if (t.rows > 1 && (stream_lds(nw, nbw, static_cast<int>(t.rows)) > kLdsMax || (t.rows > kStreamRowsWide && nbw != 2)))
+    if (t.rows > 1 && (!t.xtab || stream_lds(nw, nbw, static_cast<int>(t.rows)) > kLdsMax ||
+                       (t.rows > kStreamRowsWide && nbw != 2)))
         return false;
     // (one-row Q4_K and Q4_0 launches of two-block slices stream any
     // height: a 128256-row Q4_K head took 57.8 us here against 66.6 us on
@@ -1010,6 +1128,14 @@ bool gemv_stream_ok(int dt, const SegTable &t) {
         if (s.kind == SEG_SILU && (reinterpret_cast<uintptr_t>(s.w2) & wal)) return false;
     }
     return true;
+}
+
+size_t gemv_stream_xtab_bytes(int64_t rows, int64_t n_in) {
+    const int nb = static_cast<int>(n_in / 256);
+    if (rows < 2 || nb < 1) return 0;
+    const int nbw = stream_nbw(nb);
+    const int nw = (nb + nbw - 1) / nbw;
+    return static_cast<size_t>(rows) * nw * nbw * kTabRows;
 }
 
 hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st) {
@@ -1094,8 +1220,7 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
     const int64_t cap = static_cast<int64_t>(device_cus()) * per_cu;
     int tr = 16;
     int64_t best = INT64_MAX;
-    // (six to eight rows: one row group, whose registers hold the weights
-    // beside four rows' operands without spilling)
+    // (six to eight rows: 16-row tiles, measured faster than taller ones)
     for (int c = has_pair ? 32 : 16; c <= (nbw > 2 || t.rows > 5 ? 16 : 32); c += 4) {
         int64_t tiles = 0;
         for (int i = 0; i < t.n; i++) {
@@ -1126,6 +1251,18 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
         return act_f16 ? launch_nbw<DT_Q8_0, _Float16, _Float16>(nbw, t, tr, width, nw, st)
                        : launch_nbw<DT_Q8_0, float, float>(nbw, t, tr, width, nw, st);
 
+    if (t.rows > 1) {
+        // the rows' digit tables, once for every workgroup of the launch
+        const int nbp = nw * nbw;
+        const dim3 xg(static_cast<unsigned>((nbp + 1) / 2), static_cast<unsigned>(t.rows));
+        if (act_f16)
+            hipLaunchKernelGGL(stream_xtab_kernel<_Float16>, xg, dim3(64), 0, st,
+                               static_cast<const _Float16 *>(t.seg[0].x), t.x_stride, nb, nbp, t.xtab);
+        else
+            hipLaunchKernelGGL(stream_xtab_kernel<float>, xg, dim3(64), 0, st, static_cast<const float *>(t.seg[0].x),
+                               t.x_stride, nb, nbp, t.xtab);
+        if (const hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+    }
     switch (t.rows) {
         case 2:
             return act_f16 ? launch_nbw<DT_Q4_K, _Float16, _Float16, 2>(nbw, t, tr, width, nw, st)

@@ -77,6 +77,11 @@ struct SegTable {
     // row em_tok[p] (row p when em_tok is null), outputs seg[0].out row p.
     const EmRun *em_runs;
     const int32_t *em_n_act;
+    // Dense launches of 2..8 activation rows on the streaming kernel: device
+    // scratch of gemv_stream_xtab_bytes(rows, n_in) for the rows' digit
+    // tables, built once per call (nullable: then those launches take the
+    // other kernels)
+    uint8_t *xtab;
 };
 
 hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st);
@@ -84,6 +89,8 @@ hipError_t gemv_segments(int dt, bool act_f16, const SegTable &t, hipStream_t st
 // runs): every weight byte of a tile loaded into registers up front, digit
 // planes per wave (gemv_stream.hip)
 bool gemv_stream_ok(int dt, const SegTable &t);
+// scratch bytes of the several-row streaming launches' digit tables
+size_t gemv_stream_xtab_bytes(int64_t rows, int64_t n_in);
 hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t, hipStream_t st);
 // Q4_K / Q6_K rows 1..8 on the int8 MFMA (activations as exact int8 digit planes)
 bool gemv_digits_ok(int dt, const SegTable &t);
