@@ -470,6 +470,8 @@ TRACE_LABELS = [
     ("moe_gemm_kernel<14, false, 2>", "1572864", "C5 x512: grouped expert GEMM, down (Q6_K banks)",
      2 * 4096 * 1536 * 4096, "f16"),
     ("moe_gather_f16_kernel", "1048576", "C5 x512: activation rows gathered to f16 in plan order", None, None),
+    ("stream_xtab_kernelIDF16", "512", "rows 4, 5 and 8: the rows' digit tables, built once per call (rows in grid y)",
+     None, None),
     ("router_softmax_kernel<float, 2>", "64", "C5 x1: router softmax (128 experts)", None, None),
     ("router_topk_rank_kernel<2>", "128", "C5 x1: router top-8 (rank per expert)", None, None),
     ("router_softmax_kernel<float, 2>", "1024", "C5 x16: router softmax", None, None),
@@ -481,7 +483,7 @@ TRACE_LABELS = [
     ("gemv_stream_kernelILi12EDF16_DF16_Li2ELi28ELi8ELb1ELi0ELi8ELi5ELb0E", "262144",
      "rows 5: the same, one pass", 14336 * _Q4K_ROW, "B"),
     ("gemv_stream_kernelILi12EDF16_DF16_Li2ELi16ELi8ELb1ELi0ELi8ELi8ELb0E", "458752",
-     "rows 8: the same, one pass in two passes of four rows' tables", 14336 * _Q4K_ROW, "B"),
+     "rows 8: the same, one pass, two passes of four rows' tables", 14336 * _Q4K_ROW, "B"),
     ("moe_gemm_kernel<12, false, 1>", "114688", "rows 16 and 32: Q4_K 4096->14336, streaming dense mode (split-K 4)",
      None, None),
     ("moe_gemm_kernel<12, false, 2>", "114688", "rows 64 and 128: Q4_K 4096->14336, streaming dense mode", None, None),
