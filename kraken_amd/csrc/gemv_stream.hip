@@ -1220,7 +1220,8 @@ hipError_t gemv_stream(int dt, bool act_f16, const SegTable &t0, hipStream_t st)
     const int64_t cap = static_cast<int64_t>(device_cus()) * per_cu;
     int tr = 16;
     int64_t best = INT64_MAX;
-    // (six to eight rows: 16-row tiles, measured faster than taller ones)
+    // (six to eight rows: 16-row tiles; taller ones spill 25-27 registers at
+    // the four waves per SIMD these rows run at, 27-40 us against 20 at 8 rows)
     for (int c = has_pair ? 32 : 16; c <= (nbw > 2 || t.rows > 5 ? 16 : 32); c += 4) {
         int64_t tiles = 0;
         for (int i = 0; i < t.n; i++) {
