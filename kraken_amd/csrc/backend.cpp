@@ -37,6 +37,9 @@ struct krk_backend {
     hipStream_t stream = nullptr;
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    // per-tile counters of the MFMA GEMM's in-kernel split-K sum, zeroed at
+    // creation and left zero by every call (null: the reduce kernel instead)
+    unsigned *tile_cnt = nullptr;
     std::string err;
     static constexpr int kMoeCache = 256;  // layers of MoE tables checked once
     struct MoeOk { MoeKey key; krk_moe_entry e0; bool aligned; bool uniform; };
@@ -247,16 +250,24 @@ int krk_backend_create(int device, int act, krk_backend **out) {
     // krk_gemm_noalloc's scratch address on this device; a failure here
     // leaves it null, and only that entry point reports it
     if (scratch_address(device, &b->scratch) != hipSuccess) b->scratch = nullptr;
+    const size_t cb = sizeof(unsigned) * krk::kTileCounters;
+    if (hipMalloc(&b->tile_cnt, cb) != hipSuccess) {
+        b->tile_cnt = nullptr;
+    } else if (hipMemset(b->tile_cnt, 0, cb) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        (void)hipFree(b->tile_cnt);
+        b->tile_cnt = nullptr;
+    }
     *out = b;
     return KRK_OK;
 }
 
 int krk_backend_destroy(krk_backend *b) {
     if (!b) return KRK_ERR_ARG;
-    if (b->ws) {
+    if (b->ws || b->tile_cnt) {
         (void)hipSetDevice(b->device);
         (void)hipStreamSynchronize(b->stream);
-        (void)hipFree(b->ws);
+        if (b->ws) (void)hipFree(b->ws);
+        if (b->tile_cnt) (void)hipFree(b->tile_cnt);
     }
     delete b;
     return KRK_OK;
@@ -345,7 +356,8 @@ int gemm_impl(krk_backend *b, void *out, const void *x, const void *w, int wt, i
         ws = b->ws;
         ws_bytes = b->ws_bytes;
     }
-    const hipError_t e = krk::gemm_mfma(wt, w, rb, x, f16, out, rows, n_out, n_in, ws, ws_bytes, b->stream);
+    const hipError_t e = krk::gemm_mfma(wt, w, rb, x, f16, out, rows, n_out, n_in, ws, ws_bytes,
+                                           b->tile_cnt, b->stream);
     return e == hipSuccess ? KRK_OK : hip_fail(b, e, "mfma gemm");
 }
 

@@ -500,8 +500,8 @@ template <int DT, typename XT> constexpr bool deep_prefetch() {
 template <int DT, typename XT, typename OT>
 __global__ void __launch_bounds__(G_THREADS, 1)
     gemm_f16_kernel(const uint8_t *__restrict__ w, int64_t row_bytes, const XT *__restrict__ x,
-                    OT *__restrict__ out, float *__restrict__ part, int M, int N, int K,
-                    int k_per_split, int tiles_n) {
+                    OT *__restrict__ out, float *__restrict__ part, unsigned *__restrict__ cnt,
+                    int M, int N, int K, int k_per_split, int tiles_n) {
     // two LDS stages of a 256 x 64 activation tile and a 256 x 64 weight tile
     __shared__ _Float16 Xs[2][GB_M * LDS_ROW];
     __shared__ _Float16 Ws[2][GB_N * LDS_ROW];
@@ -670,6 +670,46 @@ __global__ void __launch_bounds__(G_THREADS, 1)
         if (t + 1 < nk) iter(ra, t + 1);
     }
 
+    // Split-K fix-up (cnt set, two splits): each split stores its
+    // accumulators as a fragment image (register-major, 256 B per wave and
+    // register), waits for the stores to complete, and counts itself in the
+    // tile's counter; the split that arrives second adds the other's image
+    // to its registers (a + b = b + a: the result does not depend on which
+    // split arrives first), writes the output and clears the counter for the
+    // next call.  Images and counter go through agent-scope atomics, which
+    // are coherent across the XCDs' L2s without a cache write-back or
+    // invalidate.
+    if (cnt) {
+        __shared__ int is_last;
+        const int z = static_cast<int>(blockIdx.z);
+        float *img = part + static_cast<int64_t>(g) * (2 * 65536) + tid;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    __hip_atomic_store(img + (z * 128 + (i * 2 + j) * 16 + r) * 512, acc[i][j][r],
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0)
+            is_last = __hip_atomic_fetch_add(cnt + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1u;
+        __syncthreads();
+        if (!is_last) return;
+        const float *other = img + (1 - z) * 128 * 512;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    acc[i][j][r] += __hip_atomic_load(other + ((i * 2 + j) * 16 + r) * 512, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) __hip_atomic_store(cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        part = nullptr;
+    }
+
     // C fragment: lane holds column j = lane % 32, rows 8*(r/4) + 4*(lane/32) + r%4
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -786,27 +826,37 @@ size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K) {
                (s > 1 ? static_cast<size_t>(s) * M * N * sizeof(float) : 0);
     }
     const int s = pick_split(M, N, K, dt);
-    return s > 1 ? static_cast<size_t>(s) * M * N * sizeof(float) : 0;
+    if (s == 1) return 0;
+    // the larger of the reduce kernel's slices and the two-split fix-up's
+    // fragment images (one 256 x 256 image per tile and split)
+    const size_t tiles = static_cast<size_t>((M + GB_M - 1) / GB_M) * ((N + GB_N - 1) / GB_N);
+    const size_t flat = static_cast<size_t>(s) * M * N, imgs = tiles * s * GB_M * GB_N;
+    return (flat > imgs ? flat : imgs) * sizeof(float);
 }
 
 template <int DT, typename XT, typename OT>
 static hipError_t launch_f16(const void *w, int64_t rb, const void *x, void *out, int64_t M,
-                             int64_t N, int64_t K, void *ws, size_t ws_bytes, hipStream_t st) {
+                             int64_t N, int64_t K, void *ws, size_t ws_bytes, unsigned *cnt,
+                             hipStream_t st) {
     const int tiles_m = static_cast<int>((M + GB_M - 1) / GB_M);
     const int tiles_n = static_cast<int>((N + GB_N - 1) / GB_N);
     const int s = pick_split(M, N, K, DT);
     const int kps = static_cast<int>(K / s);
     float *part = nullptr;
     if (s > 1) {
-        if (ws_bytes < static_cast<size_t>(s) * M * N * sizeof(float)) return hipErrorInvalidValue;
+        if (ws_bytes < gemm_mfma_workspace(DT, M, N, K)) return hipErrorInvalidValue;
         part = static_cast<float *>(ws);
     }
+    // two splits sum inside the GEMM when the caller brings tile counters
+    // (zero between calls); more splits would leave the serial sum of the
+    // last to arrive long, and take the reduce kernel
+    const bool fix = s == 2 && cnt && tiles_m * tiles_n <= kTileCounters;
     dim3 grid(static_cast<unsigned>(tiles_m * tiles_n), 1, static_cast<unsigned>(s));
     hipLaunchKernelGGL((gemm_f16_kernel<DT, XT, OT>), grid, dim3(G_THREADS), 0, st,
                        static_cast<const uint8_t *>(w), rb, static_cast<const XT *>(x),
-                       static_cast<OT *>(out), part, static_cast<int>(M), static_cast<int>(N),
-                       static_cast<int>(K), kps, tiles_n);
-    if (s > 1) {
+                       static_cast<OT *>(out), part, fix ? cnt : nullptr, static_cast<int>(M),
+                       static_cast<int>(N), static_cast<int>(K), kps, tiles_n);
+    if (s > 1 && !fix) {
         const int64_t MN = M * N;
         hipLaunchKernelGGL((splitk_reduce_kernel<OT>), dim3(static_cast<unsigned>((MN + 2047) / 2048)),
                            dim3(256), 0, st, part, static_cast<OT *>(out), MN, s);
@@ -816,7 +866,7 @@ static hipError_t launch_f16(const void *w, int64_t rb, const void *x, void *out
 
 hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bool act_f16,
                      void *out, int64_t M, int64_t N, int64_t K, void *ws, size_t ws_bytes,
-                     hipStream_t st) {
+                     unsigned *cnt, hipStream_t st) {
     if (stream_gemm(dt, M, N, K)) {
         if (ws_bytes < gemm_mfma_workspace(dt, M, N, K)) return hipErrorInvalidValue;
         const int split = stream_split(M, N, K);
@@ -853,9 +903,9 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
 #define KRK_GEMM_CASE(D)                                                                       \
     case D:                                                                                   \
         return act_f16 ? launch_f16<D, _Float16, _Float16>(w, row_bytes, x, out, M, N, K, ws,  \
-                                                           ws_bytes, st)                       \
+                                                           ws_bytes, cnt, st)                  \
                        : launch_f16<D, float, float>(w, row_bytes, x, out, M, N, K, ws,        \
-                                                     ws_bytes, st);
+                                                     ws_bytes, cnt, st);
     switch (dt) {
         KRK_GEMM_CASE(DT_Q4_K)
         KRK_GEMM_CASE(DT_Q5_K)

@@ -111,9 +111,14 @@ hipError_t quantize_q8_rows_f16codes(const void *x, bool x_f16, int64_t rows, in
 size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K);
 // compute units of the current device (cached on first use)
 int device_cus();
+// cnt: kTileCounters zeroed counters owned by the caller (left zero after
+// every call), which let a two-way split-K launch sum its splits inside the
+// GEMM; null keeps the separate reduce kernel.  Calls sharing counters must
+// not overlap.
+constexpr int kTileCounters = 4096;
 hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bool act_f16,
                      void *out, int64_t M, int64_t N, int64_t K, void *ws, size_t ws_bytes,
-                     hipStream_t st);
+                     unsigned *cnt, hipStream_t st);
 // Grouped expert GEMM on the f16 MFMA: one launch per projection over the
 // MoE plan's items {expert, first plan position, rows <= 32 mi, 0}; X holds
 // f16 activation rows in plan order [P, K].  Gate/up: out = f16 rows

@@ -244,11 +244,15 @@ def test_gemm_mfma_parity_many_tiles(krk, torch_cuda, be16, dt):
 
 
 @pytest.mark.parametrize("dt", [O.Q4_K, O.Q6_K, O.Q8_0])
-@pytest.mark.parametrize("shape", [(300, 2000, 2304), (700, 1000, 4096), (64, 256, 4096)])
+@pytest.mark.parametrize("shape", [(300, 2000, 2304), (700, 1000, 4096), (64, 256, 4096),
+                                   (300, 10277, 2048)])
 def test_gemm_splits_repeat(krk, torch_cuda, be16, be32, dt, shape):
-    """Few tiles over the CUs: split-K in two and four (K 4096) and a single
-    split (K 2304), each checked against the oracle in both activation types
-    and bit-equal on a repeated call (the partials leave no state behind)."""
+    """Few tiles over the CUs: split-K in four (700 x 1000, K 4096: the reduce
+    kernel), in two (82 tiles, K 2048: the splits summed inside the GEMM by
+    the last to arrive, ragged M and N edge tiles) and a single split (K
+    2304), each checked against the oracle in both activation types and
+    bit-equal on a repeated call (partials and tile counters leave no state
+    behind)."""
     torch = torch_cuda
     M, N, K = shape
     w = make_weights(krk, dt, N, K, seed=80 + dt)
