@@ -510,12 +510,10 @@ TRACE_LABELS = [
     ("moe_plan_kernel", "256", "C5 x16 and x512: plan", None, None),
     ("moe_reduce_kernel<float>", "4096", "C5 x16 and x512: ordered reduce", None, None),
     ("gemm_f16_kernelILi12EDF16", "229376", "C3 prefill up, M=2048 (448 tiles)", 2 * 2048 * 14336 * 4096, "f16"),
-    ("gemm_f16_kernelILi12EDF16", "65536", "C3 prefill down, M=2048 (128 tiles x split 2)",
+    ("gemm_f16_kernelILi12EDF16", "65536", "C3 prefill down, M=2048 (128 tiles x split 2, summed in the kernel)",
      2 * 2048 * 14336 * 4096, "f16"),
-    ("splitk_reduce_kernelIDF16", "1048576", "C3 prefill down, M=2048: split-K reduce", None, None),
-    ("gemm_f16_kernelILi12EDF16", "57344", "C3 prefill up, M=512 (112 tiles x split 2)",
+    ("gemm_f16_kernelILi12EDF16", "57344", "C3 prefill up, M=512 (112 tiles x split 2, summed in the kernel)",
      2 * 512 * 14336 * 4096, "f16"),
-    ("splitk_reduce_kernelIDF16", "917504", "C3 prefill up, M=512: split-K reduce", None, None),
     ("gemm_f16_kernelILi12EDF16", "16384", "C3 prefill down, M=512 (32 tiles x split 8)",
      2 * 512 * 14336 * 4096, "f16"),
     ("splitk_reduce_kernelIDF16", "262144", "C3 prefill down, M=512: split-K reduce", None, None),
