@@ -938,6 +938,41 @@ def test_moe_dispatch_graph_replay(krk, torch_cuda, be32):
         assert np.array_equal(host(out).view(np.uint32), want.view(np.uint32)), rep
 
 
+@pytest.mark.parametrize("shape", [(300, 10277, 2048), (700, 1000, 4096)])
+def test_gemm_graph_replay(krk, torch_cuda, be16, shape):
+    """The MFMA GEMM captured in a HIP graph: two splits summed in the GEMM
+    through per-tile counters (300 x 10277, K 2048), four splits through the
+    reduce kernel (700 x 1000, K 4096).  Every replay, with eager GEMMs of
+    the same shape on other operands between the replays, equals the eager
+    result bit for bit (the counters are back at zero after every call)."""
+    torch = torch_cuda
+    M, N, K = shape
+    w = dev(torch, make_weights(krk, O.Q4_K, N, K, seed=970))
+    w2 = dev(torch, make_weights(krk, O.Q4_K, N, K, seed=971))
+    x = dev(torch, krk.synth_normal(M * K, seed=972).reshape(M, K).astype(np.float16))
+    eager = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    be16.gemm(eager, x, w, O.Q4_K, N, K, M)
+    be16.sync()
+    want = host(eager)
+    other = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    main = be16.stream
+    with torch.cuda.graph(g, stream=side):
+        be16.set_stream(side)
+        be16.gemm(out, x, w, O.Q4_K, N, K, M)
+    be16.set_stream(main)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        be16.gemm(other, x, w2, O.Q4_K, N, K, M)
+        be16.sync()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(out).view(np.uint16), want.view(np.uint16)), rep
+
+
 def test_error_paths_write_nothing(krk, torch_cuda, be32):
     """Arguments the reference aborts on (a K that is not whole blocks,
     backend_hip.hip:3186-3191; geometry moe_dispatch cannot express,
