@@ -113,7 +113,10 @@ typedef struct krk_moe_entry {
 /* ---------------------------------------------------------------- handle -- */
 
 /* make_hip_backend(device_index, err) -- backend.hpp:1886,
- * backend_hip.hip:5036.  act is a krk_act. */
+ * backend_hip.hip:5036.  act is a krk_act.  The handle allocates 16 KB of
+ * device memory here (zeroed tile counters through which a two-way split-K
+ * GEMM sums its splits inside the kernel; every call leaves them zero), so
+ * calls on one handle must not overlap: the handle has one stream. */
 int krk_backend_create(int device, int act, krk_backend **out);
 int krk_backend_destroy(krk_backend *b);
 /* Launch stream (a hipStream_t); NULL selects the null stream. */
