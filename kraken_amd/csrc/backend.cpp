@@ -347,7 +347,9 @@ int gemm_impl(krk_backend *b, void *out, const void *x, const void *w, int wt, i
         const hipError_t e = krk::gemm_int8(wt, w, rb, x, f16, out, rows, n_out, n_in, ws, ws_bytes, b->stream);
         return e == hipSuccess ? KRK_OK : hip_fail(b, e, "int8 gemm");
     }
-    const size_t need = krk::gemm_mfma_workspace(wt, rows, n_out, n_in);
+    // a fixed scratch needs the least the GEMM runs with; the growing
+    // workspace takes what its fastest form needs
+    const size_t need = krk::gemm_mfma_workspace(wt, rows, n_out, n_in, fixed);
     if (fixed && need > ws_bytes)
         return fail(b, KRK_ERR_NOMEM, "mfma gemm needs %zu bytes of split-K scratch; the fixed scratch holds %zu",
                     need, ws_bytes);

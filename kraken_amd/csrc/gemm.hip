@@ -819,19 +819,26 @@ static int stream_split(int64_t M, int64_t N, int64_t K) {
 }
 static size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
 
-size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K) {
+// Split-K scratch of the tile GEMM: the reduce kernel's slices (flat,
+// s M N floats) and the two-split fix-up's fragment images (one 256 x 256
+// image per tile and split; more than flat when M or N ends in a partial
+// tile)
+static size_t splitk_floats(int64_t M, int64_t N, int s, bool images) {
+    if (s == 1) return 0;
+    if (!images) return static_cast<size_t>(s) * M * N;
+    const size_t tiles = static_cast<size_t>((M + GB_M - 1) / GB_M) * ((N + GB_N - 1) / GB_N);
+    return tiles * s * GB_M * GB_N;
+}
+
+size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K, bool minimal) {
     if (stream_gemm(dt, M, N, K)) {   // f32 rows as f16, and the split partials
         const int s = stream_split(M, N, K);
         return al256(static_cast<size_t>(M * K) * sizeof(_Float16)) +
                (s > 1 ? static_cast<size_t>(s) * M * N * sizeof(float) : 0);
     }
     const int s = pick_split(M, N, K, dt);
-    if (s == 1) return 0;
-    // the larger of the reduce kernel's slices and the two-split fix-up's
-    // fragment images (one 256 x 256 image per tile and split)
-    const size_t tiles = static_cast<size_t>((M + GB_M - 1) / GB_M) * ((N + GB_N - 1) / GB_N);
-    const size_t flat = static_cast<size_t>(s) * M * N, imgs = tiles * s * GB_M * GB_N;
-    return (flat > imgs ? flat : imgs) * sizeof(float);
+    const size_t flat = splitk_floats(M, N, s, false), imgs = splitk_floats(M, N, s, true);
+    return (minimal || flat > imgs ? flat : imgs) * sizeof(float);
 }
 
 template <int DT, typename XT, typename OT>
@@ -844,13 +851,15 @@ static hipError_t launch_f16(const void *w, int64_t rb, const void *x, void *out
     const int kps = static_cast<int>(K / s);
     float *part = nullptr;
     if (s > 1) {
-        if (ws_bytes < gemm_mfma_workspace(DT, M, N, K)) return hipErrorInvalidValue;
+        if (ws_bytes < splitk_floats(M, N, s, false) * sizeof(float)) return hipErrorInvalidValue;
         part = static_cast<float *>(ws);
     }
     // two splits sum inside the GEMM when the caller brings tile counters
-    // (zero between calls); more splits would leave the serial sum of the
-    // last to arrive long, and take the reduce kernel
-    const bool fix = s == 2 && cnt && tiles_m * tiles_n <= kTileCounters;
+    // (zero between calls) and scratch for the images; more splits would
+    // leave the serial sum of the last to arrive long, and take the reduce
+    // kernel
+    const bool fix = s == 2 && cnt && tiles_m * tiles_n <= kTileCounters &&
+                     ws_bytes >= splitk_floats(M, N, s, true) * sizeof(float);
     dim3 grid(static_cast<unsigned>(tiles_m * tiles_n), 1, static_cast<unsigned>(s));
     hipLaunchKernelGGL((gemm_f16_kernel<DT, XT, OT>), grid, dim3(G_THREADS), 0, st,
                        static_cast<const uint8_t *>(w), rb, static_cast<const XT *>(x),
@@ -868,7 +877,7 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
                      void *out, int64_t M, int64_t N, int64_t K, void *ws, size_t ws_bytes,
                      unsigned *cnt, hipStream_t st) {
     if (stream_gemm(dt, M, N, K)) {
-        if (ws_bytes < gemm_mfma_workspace(dt, M, N, K)) return hipErrorInvalidValue;
+        if (ws_bytes < gemm_mfma_workspace(dt, M, N, K, false)) return hipErrorInvalidValue;
         const int split = stream_split(M, N, K);
         float *part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
                                                 al256(static_cast<size_t>(M * K) * sizeof(_Float16)));

@@ -108,7 +108,9 @@ hipError_t quantize_q8_rows_f16codes(const void *x, bool x_f16, int64_t rows, in
 
 // Prefill GEMM (f16 MFMA, f32 accumulate) and the Q8_0 x Q8 int8 MFMA rung.
 // out[M, N] = X[M, K] . deq(W)[N, K]^T.  `ws` is device scratch of ws_bytes.
-size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K);
+// scratch of gemm_mfma: what its fastest form needs, or (minimal) the
+// least it runs with
+size_t gemm_mfma_workspace(int dt, int64_t M, int64_t N, int64_t K, bool minimal);
 // compute units of the current device (cached on first use)
 int device_cus();
 // cnt: kTileCounters zeroed counters owned by the caller (left zero after
