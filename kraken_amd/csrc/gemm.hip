@@ -20,8 +20,10 @@
 //     launch order is remapped to give each XCD a contiguous run of tiles,
 //     M fastest, so that the workgroups an XCD runs together share a few
 //     weight tiles in its own L2;
-//   * split-K (z dimension) when the tile count cannot fill 256 CUs, with f32
-//     partials summed in a fixed order by a second kernel.
+//   * split-K (z dimension) when the tile count cannot fill 256 CUs: two
+//     splits summed inside the GEMM by the one that arrives second (per-tile
+//     counters), more splits as f32 partials summed in a fixed order by a
+//     second kernel.
 //
 // int8 path (KRK_PATH_INT8, Q8_0 weights only): activations quantized per 32
 // with the host rule (quantize_q8_32_d), v_mfma_i32_32x32x32_i8 per 32-value
@@ -691,6 +693,9 @@ __global__ void __launch_bounds__(G_THREADS, 1)
                 for (int r = 0; r < 16; r++)
                     __hip_atomic_store(img + (z * 128 + (i * 2 + j) * 16 + r) * 512, acc[i][j][r],
                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the image stores stay above the wait (a compiler barrier), and the
+        // wait holds the count back until every store has completed
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0)
