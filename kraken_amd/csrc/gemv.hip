@@ -374,14 +374,14 @@ static hipError_t launch_wave(SegTable t, hipStream_t st) {
         const int64_t per = t.seg[i].kind == SEG_SILU ? RB / 2 : RB;
         total += (t.seg[i].n_out + per - 1) / per;
     }
-    static int cus = 0;
+    static thread_local int cus = 0;
     if (!cus) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             cus = 256;
     }
-    static int per_cu = 0;
+    static thread_local int per_cu = 0;
     if (!per_cu &&
         (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_wave_kernel<DT, XT, OT, RB>, 256, 0) !=
              hipSuccess || per_cu < 1))
@@ -1204,7 +1204,7 @@ static hipError_t launch_stream(SegTable t, hipStream_t st) {
     // waves per workgroup: the most resident waves per CU, ties to the
     // larger workgroup (fewer x stagings); occupancy per shape is cached
     struct Pick { int n_in, nw, per_cu; };
-    static Pick cache[8] = {};
+    static thread_local Pick cache[8] = {};
     int nw = 0, per_cu = 0;
     for (const Pick &c : cache)
         if (c.nw && c.n_in == (XREG ? 0 : t.n_in)) { nw = c.nw; per_cu = c.per_cu; break; }
@@ -1223,7 +1223,7 @@ static hipError_t launch_stream(SegTable t, hipStream_t st) {
         for (Pick &c : cache)
             if (!c.nw) { c = Pick{XREG ? 0 : t.n_in, nw, per_cu}; break; }
     }
-    static int cus = 0;
+    static thread_local int cus = 0;
     if (!cus) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -1274,7 +1274,7 @@ static hipError_t launch_lds(SegTable t, hipStream_t st) {
         total += (t.seg[i].n_out + per - 1) / per;
     }
     const size_t lds = static_cast<size_t>(t.n_in + 4 * (t.n_in / 64) + 4) * sizeof(float);
-    static int cus = 0;
+    static thread_local int cus = 0;
     if (!cus) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -1282,8 +1282,8 @@ static hipError_t launch_lds(SegTable t, hipStream_t st) {
             cus = 256;
     }
     // resident workgroups per CU, queried once per distinct LDS size
-    static size_t cached_lds[8] = {};
-    static int cached_occ[8] = {};
+    static thread_local size_t cached_lds[8] = {};
+    static thread_local int cached_occ[8] = {};
     int per_cu = 0;
     for (int i = 0; i < 8 && cached_lds[i]; i++)
         if (cached_lds[i] == lds) { per_cu = cached_occ[i]; break; }
@@ -1326,14 +1326,14 @@ static hipError_t launch_persist(SegTable t, hipStream_t st) {
     const int nsteps = (t.n_in / blk_vals(DT) + kWave / LaneFmt<DT>::LPB - 1) / (kWave / LaneFmt<DT>::LPB);
     const int threads = 64 * nsteps;
     // resident workgroups per CU for this instantiation and block size
-    static int cus = 0;
+    static thread_local int cus = 0;
     if (!cus) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             cus = 256;
     }
-    static int per_cu = 0;
+    static thread_local int per_cu = 0;
     if (!per_cu && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_persist_kernel<DT, XT, OT, RB>,
                                                                  threads, 0) != hipSuccess || per_cu < 1))
         per_cu = 1;

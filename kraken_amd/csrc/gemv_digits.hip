@@ -744,7 +744,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
     // kXPasses sub-blocks per thread (4 threads each) must cover NX * nb * 8
     const int min_nw = (NX * nb * 8 * 4 + 64 * kXPasses - 1) / (64 * kXPasses);
     struct Pick { int nb, nw, per_cu; };
-    static Pick cache[16] = {};
+    static thread_local Pick cache[16] = {};
     int nw = 0, per_cu = 0;
     for (const Pick &c : cache)
         if (c.nw && c.nb == nb) { nw = c.nw; per_cu = c.per_cu; break; }
@@ -768,7 +768,7 @@ hipError_t launch(SegTable t, hipStream_t st) {
         for (Pick &c : cache)
             if (!c.nw) { c = Pick{nb, nw, per_cu}; break; }
     }
-    static int cus = 0;
+    static thread_local int cus = 0;
     if (!cus) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -817,7 +817,7 @@ hipError_t launch_rows(int rows, const SegTable &t, hipStream_t st) {
 }
 
 int device_cus() {
-    static int cus = 0;
+    static thread_local int cus = 0;
     if (!cus) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||

@@ -1046,7 +1046,7 @@ int stream_nbw(int nb) { return nb <= 32 ? 2 : (nb + kMaxWaves - 1) / kMaxWaves;
 }  // namespace
 
 int device_cus() {
-    static int cus = 0;
+    static thread_local int cus = 0;
     if (!cus) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
