@@ -973,6 +973,62 @@ def test_gemm_graph_replay(krk, torch_cuda, be16, shape):
         assert np.array_equal(host(out).view(np.uint16), want.view(np.uint16)), rep
 
 
+def test_handles_on_host_threads(krk, torch_cuda):
+    """Four host threads, each with its own handle and stream, run GEMVs and
+    GEMMs of several types and shapes at the same time (the launchers' shape
+    caches are per thread; a handle's calls stay on its thread): every result
+    equals a one-thread run of the same calls bit for bit."""
+    import threading
+
+    torch = torch_cuda
+    cases = [(O.Q4_K, 1, 3072, 4096), (O.Q8_0, 1, 2048, 2048), (O.Q6_K, 1, 1536, 4096),
+             (O.Q5_K, 3, 1000, 2048), (O.Q4_0, 1, 4096, 1024), (O.Q4_K, 300, 520, 2048)]
+    ops = []
+    for i, (dt, rows, n_out, n_in) in enumerate(cases):
+        w = dev(torch, make_weights(krk, dt, n_out, n_in, seed=1100 + i))
+        x = dev(torch, krk.synth_normal(rows * n_in, seed=1110 + i).reshape(rows, n_in))
+        ops.append((dt, rows, n_out, n_in, w, x))
+
+    def run(be, stream):
+        outs = []
+        with torch.cuda.stream(stream):
+            for dt, rows, n_out, n_in, w, x in ops:
+                o = torch.empty((rows, n_out), dtype=torch.float32, device="cuda")
+                be.gemm(o, x, w, dt, n_out, n_in, rows)
+                outs.append(o)
+        be.sync()
+        return [host(o) for o in outs]
+
+    be0 = krk.Backend(0, krk.ACT_F32, stream=torch.cuda.Stream())
+    try:
+        want = run(be0, be0.stream)
+    finally:
+        be0.close()
+    got, errs = [None] * 4, []
+
+    def worker(k):
+        try:
+            st = torch.cuda.Stream()
+            be = krk.Backend(0, krk.ACT_F32, stream=st)
+            try:
+                for _ in range(3):
+                    got[k] = run(be, st)
+            finally:
+                be.close()
+        except Exception as e:   # reported in the main thread
+            errs.append(e)
+
+    ts = [threading.Thread(target=worker, args=(k,)) for k in range(4)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errs, errs
+    for k in range(4):
+        for a, b in zip(got[k], want):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_error_paths_write_nothing(krk, torch_cuda, be32):
     """Arguments the reference aborts on (a K that is not whole blocks,
     backend_hip.hip:3186-3191; geometry moe_dispatch cannot express,
