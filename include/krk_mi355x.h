@@ -16,7 +16,9 @@
  *     x, w, out, ids, wts and the MoE table are device pointers).
  *   - Launches are asynchronous on the handle's stream (the null stream until
  *     krk_set_stream); krk_sync waits for them.
- *   - Not thread-safe: one host thread drives one handle, as in the reference.
+ *   - A handle is not thread-safe: one host thread drives one handle, as in
+ *     the reference.  Several threads may each drive their own handle at the
+ *     same time (the library's launch-shape caches are per thread).
  */
 #ifndef KRK_MI355X_H
 #define KRK_MI355X_H
