@@ -28,6 +28,7 @@ def free_bytes():
 @pytest.mark.parametrize("path,dt,shapes", [
     ("auto", O.Q4_K, [(512, 4096, 14336), (64, 4096, 4096)]),     # split-K 8 (64 MiB of partials), then 4
     ("auto", O.Q6_K, [(300, 2048, 8192), (24, 512, 4096)]),
+    ("auto", O.Q4_K, [(512, 14336, 4096), (300, 10277, 2048)]),    # two splits summed in the GEMM
     ("auto", O.Q4_K, [(1, 14336, 4096), (3, 1000, 2048)]),         # GEMV rows
     ("int8", O.Q8_0, [(256, 2048, 4096), (40, 300, 1024)]),
 ])
