@@ -1171,8 +1171,9 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
     for (int i = 0; i < NI; i++) {
         const int r = 2 * (NI * wave + i) + (lane >> 5);
         const int c = (lane & 31) ^ (r & 15);
-        dsrc[i] = to_global(reinterpret_cast<const uint8_t *>(static_cast<const _Float16 *>(a.x) +
-                                                              static_cast<int64_t>(pb + (r < rows ? r : 0)) * a.K +
+        const int pr = pb + (r < rows ? r : 0);
+        const int64_t xr = a.xtok ? static_cast<int64_t>(a.xtok[pr]) : pr;
+        dsrc[i] = to_global(reinterpret_cast<const uint8_t *>(static_cast<const _Float16 *>(a.x) + xr * a.K +
                                                               256 * kb0 + 8 * c));
     }
     auto xdma = [&](int blk, int buf) {
@@ -1290,8 +1291,9 @@ __global__ void __launch_bounds__(MG_THREADS) __attribute__((amdgpu_waves_per_eu
         }
 }
 
-// The items' activation rows in plan order as f16 (the GEMM's operand
-// rounding): row pos = x[plan_tok[pos]] for the live plan positions.
+// Activation rows as f16 (the GEMM's operand rounding): row pos =
+// x[plan_tok[pos]] for the live plan positions, or without plan_tok row pos
+// = x[pos] (the tokens' rows, or a dense GEMM's).
 __global__ void __launch_bounds__(256) moe_gather_f16_kernel(const float *__restrict__ x, int64_t n,
                                                               const int32_t *__restrict__ plan_tok,
                                                               const int32_t *__restrict__ n_live,

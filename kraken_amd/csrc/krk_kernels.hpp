@@ -125,8 +125,9 @@ hipError_t gemm_mfma(int dt, const void *w, int64_t row_bytes, const void *x, bo
 // MoE plan's items {expert, first plan position, rows <= 32 mi, 0}; X holds
 // f16 activation rows in plan order [P, K].  Gate/up: out = f16 rows
 // silu(gate) * up per plan position [P, n_ff]; down: out = f32 part rows
-// per plan position [P, n_embd].  moe_gather_f16 writes the gate/up X from
-// the token rows (xg[pos] = f16(x[plan_tok[pos]]) for pos < *n_live).
+// per plan position [P, n_embd].  moe_gather_f16 writes f16 rows: with
+// plan_tok, xg[pos] = f16(x[plan_tok[pos]]) for pos < *n_live; without,
+// xg[pos] = f16(x[pos]).
 struct MoeGemmArgs {
     const void *tab;           // krk_moe_entry[n_expert] of the layer
     const int32_t *items;      // 4 per item
@@ -144,6 +145,8 @@ struct MoeGemmArgs {
     int M;
     bool out_f16;
     int ksplit;                // dense: K in ksplit whole-block ranges, f32 partials [ksplit][M][N] at out
+    const int32_t *xtok;       // non-null: plan position p's activation row is x row xtok[p] (gate/up on
+                               // the tokens' rows); null: x rows in plan order
 };
 bool moe_gemm_ok(int dt);
 hipError_t moe_gemm(int dt, const MoeGemmArgs &a, hipStream_t st);

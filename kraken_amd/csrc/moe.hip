@@ -66,7 +66,7 @@ struct MoeWs {
     _Float16 *midf;     // [P, n_ff]      f16 activations: the row-scaled mid rows
     float *rscale;      // [P]            f16 activations: each mid row's power-of-two scale
     EmRun *runs;        // [n_expert]     active experts' banks and plan ranges
-    _Float16 *xg;       // [P, n_embd]    grouped GEMM: activation rows in plan order, f16
+    _Float16 *xg;       // [P, n_embd]    grouped GEMM: the tokens' activation rows, f16
 };
 
 static size_t al(size_t v) { return (v + 255) & ~size_t(255); }
@@ -638,10 +638,13 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
         const int64_t bound = act + P / (32 * mi);
         g.max_items = static_cast<int>(bound < P ? bound : P);
         g.mi = mi;
-        hipError_t e = moe_gather_f16(static_cast<const float *>(a.xn), a.n_embd, w.plan_tok, w.off + a.n_expert,
-                                      P, w.xg, st);
+        // the tokens' rows as f16 once; gate/up reads each plan position's
+        // row through plan_tok
+        hipError_t e = moe_gather_f16(static_cast<const float *>(a.xn), a.n_embd, nullptr, nullptr, a.n_tok,
+                                      w.xg, st);
         if (e != hipSuccess) return e;
         g.x = w.xg;
+        g.xtok = w.plan_tok;
         g.out = w.midf;
         g.row_bytes = a.rb_gate;
         g.K = static_cast<int>(a.n_embd);
@@ -650,6 +653,7 @@ hipError_t moe_dispatch(const MoeArgs &a, void *ws, size_t ws_bytes, hipStream_t
         e = moe_gemm(a.wt, g, st);
         if (e != hipSuccess) return e;
         g.x = w.midf;
+        g.xtok = nullptr;
         g.out = w.part;
         g.row_bytes = a.rb_down;
         g.K = static_cast<int>(a.n_ff);
