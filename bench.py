@@ -489,7 +489,7 @@ TRACE_LABELS = [
      2 * 4096 * 1536 * 4096, "f16"),
     ("moe_gemm_kernel<14, false, 2>", "1572864", "C5 x512: grouped expert GEMM, down (Q6_K banks)",
      2 * 4096 * 1536 * 4096, "f16"),
-    ("moe_gather_f16_kernel", "1048576", "C5 x512: activation rows gathered to f16 in plan order", None, None),
+    ("moe_gather_f16_kernel", "131072", "C5 x512: the tokens' activation rows to f16, once per token", None, None),
     ("stream_xtab_kernelIDF16", "512", "rows 4, 5 and 8: the rows' digit tables, built once per call (rows in grid y)",
      None, None),
     ("router_softmax_kernel<float, 2>", "64", "C5 x1: router softmax (128 experts)", None, None),
